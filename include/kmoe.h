@@ -1,0 +1,200 @@
+/*
+ * kmoe.h — C ABI of the MI355X (gfx950) MoE FFN hot path.
+ *
+ * This is the seam a Rust FFI crate binds. It replaces,
+ * behind kestrel's unchanged InferenceSession trait
+ * (crates/kestrel-backends/src/lib.rs:60-74):
+ *   - quant::matmul                (crates/kestrel-engine/src/quant.rs:229)
+ *   - Q8Row / Q8KRow::quantize     (crates/kestrel-engine/src/qdot.rs:30, :347)
+ *   - Transformer::route           (crates/kestrel-engine/src/transformer.rs:472)
+ *   - the dispatch of moe_ffn      (transformer.rs:525-531)
+ *   - Transformer::moe_ffn         (transformer.rs:513), without the shared expert
+ *   - ExpertStore's resident tier  (crates/kestrel-memory/src/expert.rs:223-641),
+ *     as an HBM-resident expert tier with Tier::Vram accounting
+ *     (crates/kestrel-memory/src/ledger.rs:10-14, :75)
+ *
+ * Conventions
+ *   - Every entry point returns a kmoe_status (0 = ok). On error the context
+ *     keeps a message, kmoe_last_error(). Sizes that the reference asserts on
+ *     (quant.rs:231-234) return KMOE_E_INVALID instead of aborting.
+ *   - Pointers named *_dev are device (HBM) pointers. Calls that take them are
+ *     asynchronous on the context's stream; kmoe_synchronize() waits.
+ *   - Weights are GGUF bytes verbatim (ggml order: a [rows, cols] matrix is
+ *     row-major, cols contiguous; kestrel-gguf lib.rs:151, quant.rs:226-228).
+ *   - A context is one device and one stream. It is not thread-safe: callers
+ *     serialise, as Transformer::forward(&mut self) does. Several contexts may
+ *     coexist.
+ */
+#ifndef KMOE_H
+#define KMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KMOE_ABI_VERSION 1
+
+/* Status codes; the mapping to EngineError (transformer.rs:15-27) is
+ * INVALID/UNSUPPORTED -> Unsupported or Other, BUDGET -> Budget,
+ * NOT_LOADED -> Store, HIP -> Other. */
+typedef enum {
+  KMOE_OK = 0,
+  KMOE_E_INVALID = -1,     /* bad argument or size mismatch */
+  KMOE_E_UNSUPPORTED = -2, /* ggml type or shape without a kernel */
+  KMOE_E_BUDGET = -3,      /* Tier::Vram reservation past the limit */
+  KMOE_E_HIP = -4,         /* HIP runtime error */
+  KMOE_E_NOT_LOADED = -5   /* layer, router or expert not uploaded */
+} kmoe_status;
+
+/* ggml type ids, kestrel-gguf types.rs:67-107. Kernels exist for F32
+ * (router), Q8_0 and Q4_K. */
+enum { KMOE_F32 = 0, KMOE_Q8_0 = 8, KMOE_Q4_K = 12 };
+
+/* Arithmetic regime of the quantized matmuls (quant.rs:229-328).
+ * KMOE_REGIME_AVX2 (default): the reference on an AVX2+FMA host. A matmul
+ *   (one expert) with s_rows >= 4 dequantizes weights to f32 and multiplies
+ *   f32 activations (quant.rs:242-260); with s_rows < 4 it quantizes
+ *   activations to int8 (Q8_K per 256 for Q4_K, quant.rs:262-281; Q8 per 32
+ *   for Q8_0, quant.rs:282-310) and takes integer dots.
+ * KMOE_REGIME_INT8: int8 activations for every row count: the per-row integer
+ *   kernels of the reference applied to every row (batched/prefill regime).
+ * KMOE_REGIME_EXACT: KESTREL_EXACT=1 (quant.rs:29-46): f32 for every row. */
+enum { KMOE_REGIME_AVX2 = 0, KMOE_REGIME_INT8 = 1, KMOE_REGIME_EXACT = 2 };
+
+typedef struct kmoe_ctx kmoe_ctx;
+
+/* ------------------------------------------------------------------ context */
+/* Replaces nothing one-to-one: NativeSession::load builds the engine
+ * (backends/src/lib.rs:125-187); this creates the device side of it. */
+int kmoe_create(int device, kmoe_ctx **out);
+int kmoe_destroy(kmoe_ctx *ctx);
+/* Message of the last failed call on ctx ("" if none). Valid until the next call. */
+const char *kmoe_last_error(const kmoe_ctx *ctx);
+int kmoe_abi_version(void);
+/* Use an external hipStream_t (e.g. the caller's) instead of the context's own.
+ * NULL restores the context's stream. */
+int kmoe_set_stream(kmoe_ctx *ctx, void *hip_stream);
+void *kmoe_get_stream(kmoe_ctx *ctx);
+int kmoe_synchronize(kmoe_ctx *ctx);
+int kmoe_set_regime(kmoe_ctx *ctx, int regime);
+int kmoe_get_regime(const kmoe_ctx *ctx);
+
+/* ------------------------------------------------- Tier::Vram accounting */
+/* Ledger::reserve for Tier::Vram (ledger.rs:75): every device byte the context
+ * owns (expert tier, routers, workspace, kmoe_device_alloc) is reserved
+ * against `limit` first; past it, calls fail with KMOE_E_BUDGET.
+ * limit 0 = the device's total memory. */
+int kmoe_vram_set_limit(kmoe_ctx *ctx, uint64_t limit_bytes);
+int kmoe_vram_usage(const kmoe_ctx *ctx, uint64_t *reserved, uint64_t *limit);
+
+/* Device buffers for callers without their own allocator (counted in Tier::Vram). */
+int kmoe_device_alloc(kmoe_ctx *ctx, size_t bytes, void **dev);
+int kmoe_device_free(kmoe_ctx *ctx, void *dev);
+int kmoe_copy_h2d(kmoe_ctx *ctx, void *dst_dev, const void *src, size_t bytes);  /* stream-ordered, synchronous */
+int kmoe_copy_d2h(kmoe_ctx *ctx, void *dst, const void *src_dev, size_t bytes);  /* stream-ordered, synchronous */
+
+/* -------------------------------------------------------------- kernel seam */
+/* quant::matmul (quant.rs:229): out[s*rows + r] = W[r] . x[s] for W of
+ * ggml_type with shape [rows, cols], x [s_rows, cols] f32, out [s_rows, rows] f32.
+ * w_len must be >= rows * bytes_for(cols) (quant.rs:233-234). The regime of
+ * the context picks the arithmetic as the reference does for s_rows. */
+int kmoe_matmul(kmoe_ctx *ctx, int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols,
+                const float *x_dev, int64_t s_rows, float *out_dev);
+
+/* Q8KRow::quantize (qdot.rs:347-367) per row of x [s_rows, cols], cols % 256 == 0:
+ * q [s_rows, cols] i8, d [s_rows, cols/256] f32, bsums [s_rows, cols/16] i32. */
+int kmoe_quantize_q8k(kmoe_ctx *ctx, const float *x_dev, int64_t s_rows, int64_t cols, int8_t *q_dev, float *d_dev,
+                      int32_t *bsums_dev);
+/* Q8Row::quantize (qdot.rs:30-49) per row, cols % 32 == 0:
+ * q [s_rows, cols] i8, d [s_rows, cols/32] f32, s16 [s_rows, cols/16] i32. */
+int kmoe_quantize_q8(kmoe_ctx *ctx, const float *x_dev, int64_t s_rows, int64_t cols, int8_t *q_dev, float *d_dev,
+                     int32_t *s16_dev);
+
+/* Integer accumulators of the Q4_K x Q8_K dot (avx2.rs:361-374), per
+ * (token s, row r, superblock b): sumi = sum_j sc_j * sum(q . x) and
+ * mins = sum_j m_j * (bsum pair), both int32, written at [(s*rows + r)*nsb + b],
+ * nsb = cols/256. Computed by the same device code as the matvec. */
+int kmoe_q4k_block_sums(kmoe_ctx *ctx, const void *w_dev, int64_t rows, int64_t cols, const int8_t *q_dev,
+                        const int32_t *bsums_dev, int64_t s_rows, int32_t *sumi_dev, int32_t *mins_dev);
+/* Per-block int32 dot of Q8_0 x Q8 (avx2.rs:51-56), at [(s*rows + r)*nb + b], nb = cols/32. */
+int kmoe_q8_0_block_sums(kmoe_ctx *ctx, const void *w_dev, int64_t rows, int64_t cols, const int8_t *q_dev,
+                         int64_t s_rows, int32_t *p_dev);
+/* Matvec on pre-quantized activations: the int8 path of kmoe_matmul with the
+ * caller's Q8_K (Q4_K weights) or Q8 (Q8_0 weights, bsums unused) rows. */
+int kmoe_matvec_q8(kmoe_ctx *ctx, int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols,
+                   const int8_t *q_dev, const float *d_dev, const int32_t *bsums_dev, int64_t s_rows, float *out_dev);
+
+/* ------------------------------------------------------ routing + dispatch */
+/* Transformer::route (transformer.rs:472-496) on a router given by pointer:
+ * logits = matmul(F32 router [n_expert, d], h [s_rows, d]) in the reference's
+ * summation order for s_rows, softmax, top-k (descending p, ties to the lower
+ * index), optional renormalisation (floor 2^-14) and weights_scale.
+ * idx [s_rows, k] u32 and w [s_rows, k] f32 in selection order;
+ * logits_dev (optional, may be NULL) receives [s_rows, n_expert]. */
+int kmoe_route(kmoe_ctx *ctx, const float *router_dev, int32_t n_expert, int64_t d, const float *h_dev,
+               int64_t s_rows, int32_t k, int32_t norm_topk, float weights_scale, uint32_t *idx_dev, float *w_dev,
+               float *logits_dev);
+/* The dispatch of moe_ffn (transformer.rs:525-531): a stable counting sort of
+ * the s_rows*k (token, slot) pairs by expert id. perm [s_rows*k] holds flat
+ * indices s*k + j; offsets [n_expert+1] is the exclusive scan of the counts. */
+int kmoe_dispatch(kmoe_ctx *ctx, const uint32_t *idx_dev, int64_t s_rows, int32_t k, int32_t n_expert,
+                  uint32_t *perm_dev, uint32_t *offsets_dev);
+
+/* ------------------------------------------------------ HBM expert tier */
+/* One MoE layer (MoeInfo, kestrel-model lib.rs:103-117, and the stacked
+ * ffn_{gate,up,down}_exps geometry). */
+typedef struct {
+  uint32_t n_expert;
+  uint32_t n_expert_used;
+  int32_t norm_topk;   /* renormalise selected weights (default: all but qwen2moe) */
+  float weights_scale; /* 0 or 1 = none */
+  int64_t n_embd;      /* d */
+  int64_t n_ff;        /* expert FFN width */
+  int32_t gate_type, up_type, down_type;
+} kmoe_moe_desc;
+
+/* Reserve the layer's expert tier: n_expert * (gate + up + down) bytes, one
+ * contiguous extent per expert (the prepared-container layout,
+ * docs/prepared-format.md), plus the f32 router. Fails with KMOE_E_BUDGET past
+ * the Tier::Vram limit. */
+int kmoe_layer_create(kmoe_ctx *ctx, uint32_t layer, const kmoe_moe_desc *desc);
+int kmoe_layer_destroy(kmoe_ctx *ctx, uint32_t layer);
+/* Router tensor blk.L.ffn_gate_inp.weight, F32 [n_expert, n_embd], host bytes. */
+int kmoe_router_upload(kmoe_ctx *ctx, uint32_t layer, const float *router, size_t bytes);
+/* ExpertStore::load/preload_all (expert.rs:251-303, :620-641): copy expert e's
+ * part (0 gate, 1 up, 2 down) GGUF bytes verbatim from host memory. */
+int kmoe_expert_upload(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes, size_t len);
+/* Same from device memory (device-to-device copy). */
+int kmoe_expert_upload_dev(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes_dev,
+                           size_t len);
+/* ExpertStore::is_ready (expert.rs:445): 1 when all three parts are resident, else 0. */
+int kmoe_expert_is_ready(kmoe_ctx *ctx, uint32_t layer, uint32_t expert);
+/* ExpertBuf::part (expert.rs:72-76): device pointer and length of a resident part. */
+int kmoe_expert_part(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void **dev, size_t *len);
+/* ExpertStore::bytes_per_expert (expert.rs:269). */
+int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
+
+/* ------------------------------------------------------------ layer seam */
+/* Transformer::moe_ffn (transformer.rs:513-570) for one layer: route, dispatch
+ * (batch union: each routed expert's weights are read once for all its rows),
+ * per-expert SwiGLU FFN in the context's regime, and the combine
+ * out[s] = sum over the token's experts in ascending id of w * y.
+ * h [s_rows, n_embd] f32 in, out [s_rows, n_embd] f32 out (device). */
+int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev);
+/* Routing state of the last kmoe_moe_ffn on ctx (device copies; any may be NULL):
+ * idx/w [s_rows*k], perm [s_rows*k], offsets [n_expert+1]. */
+int kmoe_moe_last_routing(kmoe_ctx *ctx, uint32_t *idx_dev, float *w_dev, uint32_t *perm_dev,
+                          uint32_t *offsets_dev);
+
+/* Per-kernel timing with HIP events on the context's stream (0 = off). */
+int kmoe_profile_enable(kmoe_ctx *ctx, int on);
+/* Accumulated time and launch count of the kernel named `kernel` since enable. */
+int kmoe_profile_read(kmoe_ctx *ctx, const char *kernel, double *total_ms, int64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KMOE_H */

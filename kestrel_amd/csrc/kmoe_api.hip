@@ -1,0 +1,761 @@
+// kmoe_api.hip — the C ABI of include/kmoe.h: context, Tier::Vram ledger,
+// HBM-resident expert tier, workspace, and the moe_ffn pipeline.
+//
+// One context = one device + one stream. Calls that take device pointers
+// enqueue work and return; errors from argument checks are reported before
+// anything is enqueued.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/kmoe.h"
+#include "kmoe_launch.h"
+
+using namespace kmoe;
+
+namespace {
+
+int64_t block_size(int t) {
+  switch (t) {
+    case KMOE_F32: return 1;
+    case KMOE_Q8_0: return 32;
+    case KMOE_Q4_K: return 256;
+    default: return -1;
+  }
+}
+int64_t type_size(int t) {
+  switch (t) {
+    case KMOE_F32: return 4;
+    case KMOE_Q8_0: return 34;
+    case KMOE_Q4_K: return 144;
+    default: return -1;
+  }
+}
+// GgmlType::bytes_for (types.rs:184-191); -1 when cols is not a block multiple.
+int64_t bytes_for(int t, int64_t n) {
+  const int64_t bs = block_size(t);
+  if (bs <= 0 || n < 0 || n % bs != 0) return -1;
+  return n / bs * type_size(t);
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Layer {
+  kmoe_moe_desc desc{};
+  uint8_t *arena = nullptr;  // n_expert contiguous experts: [gate | up | down]
+  float *router = nullptr;
+  size_t part_len[3] = {0, 0, 0};
+  size_t part_off[3] = {0, 0, 0};
+  size_t expert_stride = 0;
+  size_t reserved = 0;
+  bool router_ok = false;
+  std::vector<uint8_t> loaded;  // bit p set when part p of expert e is resident
+};
+
+struct Event2 {
+  std::string name;
+  hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct kmoe_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  std::string err;
+  int regime = KMOE_REGIME_AVX2;
+  uint64_t vram_limit = 0;
+  uint64_t vram_reserved = 0;
+  std::map<uint32_t, Layer> layers;
+  std::map<void *, size_t> user_allocs;
+  // workspace
+  uint8_t *ws = nullptr;
+  size_t ws_size = 0;
+  // last moe_ffn routing (pointers into ws) and its sizes
+  uint32_t *last_idx = nullptr, *last_perm = nullptr, *last_off = nullptr;
+  float *last_w = nullptr;
+  int64_t last_slots = 0;
+  int32_t last_E = 0;
+  // profiling
+  bool prof = false;
+  std::vector<Event2> pending;
+  std::map<std::string, std::pair<double, int64_t>> prof_acc;
+};
+
+namespace {
+
+int fail(kmoe_ctx *c, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  return code;
+}
+
+#define HIP_OK(ctx, expr)                                                                                   \
+  do {                                                                                                      \
+    hipError_t e_ = (expr);                                                                                 \
+    if (e_ != hipSuccess) return fail((ctx), KMOE_E_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                                  \
+  } while (0)
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+// Ledger::reserve (ledger.rs:75-102): an error value, never an OOM.
+int reserve(kmoe_ctx *c, uint64_t bytes, const char *purpose) {
+  if (c->vram_reserved + bytes > c->vram_limit)
+    return fail(c, KMOE_E_BUDGET,
+                "VRAM budget exhausted: requested %llu bytes for %s, %llu/%llu reserved",
+                (unsigned long long)bytes, purpose, (unsigned long long)c->vram_reserved,
+                (unsigned long long)c->vram_limit);
+  c->vram_reserved += bytes;
+  return KMOE_OK;
+}
+void release(kmoe_ctx *c, uint64_t bytes) { c->vram_reserved -= bytes < c->vram_reserved ? bytes : c->vram_reserved; }
+
+int dev_alloc(kmoe_ctx *c, size_t bytes, void **p, const char *purpose) {
+  int rc = reserve(c, bytes, purpose);
+  if (rc) return rc;
+  hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    release(c, bytes);
+    return fail(c, KMOE_E_HIP, "hipMalloc(%zu) for %s: %s", bytes, purpose, hipGetErrorString(e));
+  }
+  return KMOE_OK;
+}
+
+// Accumulate finished profiling events.
+void prof_drain(kmoe_ctx *c) {
+  for (auto &ev : c->pending) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(ev.b) == hipSuccess && hipEventElapsedTime(&ms, ev.a, ev.b) == hipSuccess) {
+      auto &acc = c->prof_acc[ev.name];
+      acc.first += ms;
+      acc.second += 1;
+    }
+    (void)hipEventDestroy(ev.a);
+    (void)hipEventDestroy(ev.b);
+  }
+  c->pending.clear();
+}
+
+// Run one launch, bracketed by events when profiling.
+template <class F>
+hipError_t timed(kmoe_ctx *c, const char *name, F &&launch) {
+  if (!c->prof) return launch();
+  Event2 ev{name, nullptr, nullptr};
+  hipError_t e = hipEventCreate(&ev.a);
+  if (e == hipSuccess) e = hipEventCreate(&ev.b);
+  if (e == hipSuccess) e = hipEventRecord(ev.a, c->stream);
+  if (e != hipSuccess) return e;
+  e = launch();
+  if (e != hipSuccess) return e;
+  e = hipEventRecord(ev.b, c->stream);
+  c->pending.push_back(ev);
+  if (c->pending.size() > 4096) prof_drain(c);
+  return e;
+}
+
+#define LAUNCH(ctx, name, expr) HIP_OK(ctx, timed((ctx), (name), [&]() -> hipError_t { return (expr); }))
+
+// Workspace carving.
+struct Carver {
+  uint8_t *base;
+  size_t off = 0;
+  template <class T>
+  T *take(size_t n) {
+    T *p = reinterpret_cast<T *>(base ? base + off : nullptr);
+    off = align_up(off + n * sizeof(T));
+    return p;
+  }
+};
+
+struct MoeWs {
+  int8_t *xq;
+  float *xd;
+  int32_t *xs;
+  float *logits;
+  uint32_t *idx;
+  float *wsel;
+  uint32_t *perm, *offsets, *inv, *rank;
+  int32_t *n_active, *active;
+  float *h;
+  int8_t *hq;
+  float *hd;
+  int32_t *hs;
+  float *y;
+};
+
+MoeWs carve_moe(uint8_t *base, int64_t S, int64_t E, int64_t k, int64_t d, int64_t F, size_t *total) {
+  Carver cv{base};
+  MoeWs w{};
+  const int64_t slots = S * k;
+  w.xq = cv.take<int8_t>(S * d);
+  w.xd = cv.take<float>(S * (d / 32));
+  w.xs = cv.take<int32_t>(S * (d / 16));
+  w.logits = cv.take<float>(S * E);
+  w.idx = cv.take<uint32_t>(slots);
+  w.wsel = cv.take<float>(slots);
+  w.perm = cv.take<uint32_t>(slots);
+  w.offsets = cv.take<uint32_t>(E + 1);
+  w.inv = cv.take<uint32_t>(slots);
+  w.rank = cv.take<uint32_t>(slots);
+  w.n_active = cv.take<int32_t>(1);
+  w.active = cv.take<int32_t>(E);
+  w.h = cv.take<float>(slots * F);
+  w.hq = cv.take<int8_t>(slots * F);
+  w.hd = cv.take<float>(slots * (F / 32));
+  w.hs = cv.take<int32_t>(slots * (F / 16));
+  w.y = cv.take<float>(slots * d);
+  *total = cv.off;
+  return w;
+}
+
+int ensure_ws(kmoe_ctx *c, size_t need) {
+  if (need <= c->ws_size) return KMOE_OK;
+  size_t sz = align_up(need + need / 4);
+  if (c->ws) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    HIP_OK(c, hipFree(c->ws));
+    release(c, c->ws_size);
+    c->ws = nullptr;
+    c->ws_size = 0;
+    c->last_idx = c->last_perm = c->last_off = nullptr;
+    c->last_w = nullptr;
+  }
+  void *p = nullptr;
+  int rc = dev_alloc(c, sz, &p, "workspace");
+  if (rc) return rc;
+  c->ws = (uint8_t *)p;
+  c->ws_size = sz;
+  return KMOE_OK;
+}
+
+bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q8_0; }
+
+// Row-shape checks shared by the quantized kernels.
+int check_quant_shape(kmoe_ctx *c, int t, int64_t cols) {
+  if (!supported_weight(t)) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel (Q8_0=8, Q4_K=12)", t);
+  if (bytes_for(t, cols) < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
+  if (t == KMOE_Q8_0 && cols % 64 != 0)
+    return fail(c, KMOE_E_UNSUPPORTED, "Q8_0 rows need cols %% 64 == 0 (dword-aligned row starts), got %lld",
+                (long long)cols);
+  if (cols % 64 != 0) return fail(c, KMOE_E_UNSUPPORTED, "cols %% 64 != 0");
+  const int64_t per = cols + cols / 4 + cols / 8 + 48;
+  if (3 * per > 65536) return fail(c, KMOE_E_UNSUPPORTED, "cols %lld too wide for the LDS-staged kernels", (long long)cols);
+  return KMOE_OK;
+}
+
+bool int_path(int regime, int64_t s_rows) {
+  return regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2 && s_rows < 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+int kmoe_abi_version(void) { return KMOE_ABI_VERSION; }
+
+int kmoe_create(int device, kmoe_ctx **out) {
+  if (!out) return KMOE_E_INVALID;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return KMOE_E_INVALID;
+  DeviceGuard g(device);
+  kmoe_ctx *c = new kmoe_ctx();
+  c->device = device;
+  if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return KMOE_E_HIP;
+  }
+  c->stream = c->own;
+  size_t fr = 0, tot = 0;
+  if (hipMemGetInfo(&fr, &tot) == hipSuccess) c->vram_limit = tot;
+  *out = c;
+  return KMOE_OK;
+}
+
+int kmoe_destroy(kmoe_ctx *c) {
+  if (!c) return KMOE_OK;
+  DeviceGuard g(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  prof_drain(c);
+  for (auto &kv : c->layers) {
+    (void)hipFree(kv.second.arena);
+    (void)hipFree(kv.second.router);
+  }
+  for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return KMOE_OK;
+}
+
+const char *kmoe_last_error(const kmoe_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+int kmoe_set_stream(kmoe_ctx *c, void *s) {
+  if (!c) return KMOE_E_INVALID;
+  c->stream = s ? (hipStream_t)s : c->own;
+  return KMOE_OK;
+}
+void *kmoe_get_stream(kmoe_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int kmoe_synchronize(kmoe_ctx *c) {
+  if (!c) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return KMOE_OK;
+}
+
+int kmoe_set_regime(kmoe_ctx *c, int regime) {
+  if (!c) return KMOE_E_INVALID;
+  if (regime < KMOE_REGIME_AVX2 || regime > KMOE_REGIME_EXACT) return fail(c, KMOE_E_INVALID, "bad regime %d", regime);
+  c->regime = regime;
+  return KMOE_OK;
+}
+int kmoe_get_regime(const kmoe_ctx *c) { return c ? c->regime : -1; }
+
+int kmoe_vram_set_limit(kmoe_ctx *c, uint64_t limit) {
+  if (!c) return KMOE_E_INVALID;
+  if (limit == 0) {
+    DeviceGuard g(c->device);
+    size_t fr = 0, tot = 0;
+    HIP_OK(c, hipMemGetInfo(&fr, &tot));
+    limit = tot;
+  }
+  if (limit < c->vram_reserved)
+    return fail(c, KMOE_E_BUDGET, "limit %llu below the %llu bytes already reserved", (unsigned long long)limit,
+                (unsigned long long)c->vram_reserved);
+  c->vram_limit = limit;
+  return KMOE_OK;
+}
+
+int kmoe_vram_usage(const kmoe_ctx *c, uint64_t *reserved, uint64_t *limit) {
+  if (!c) return KMOE_E_INVALID;
+  if (reserved) *reserved = c->vram_reserved;
+  if (limit) *limit = c->vram_limit;
+  return KMOE_OK;
+}
+
+int kmoe_device_alloc(kmoe_ctx *c, size_t bytes, void **dev) {
+  if (!c || !dev) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  int rc = dev_alloc(c, bytes, dev, "caller buffer");
+  if (rc) return rc;
+  c->user_allocs[*dev] = bytes;
+  return KMOE_OK;
+}
+
+int kmoe_device_free(kmoe_ctx *c, void *dev) {
+  if (!c) return KMOE_E_INVALID;
+  auto it = c->user_allocs.find(dev);
+  if (it == c->user_allocs.end()) return fail(c, KMOE_E_INVALID, "pointer not allocated by kmoe_device_alloc");
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipFree(dev));
+  release(c, it->second);
+  c->user_allocs.erase(it);
+  return KMOE_OK;
+}
+
+int kmoe_copy_h2d(kmoe_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return KMOE_OK;
+}
+
+int kmoe_copy_d2h(kmoe_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return KMOE_OK;
+}
+
+// ------------------------------------------------------------------ kernels
+
+int kmoe_quantize_q8k(kmoe_ctx *c, const float *x, int64_t s_rows, int64_t cols, int8_t *q, float *d, int32_t *bs) {
+  if (!c) return KMOE_E_INVALID;
+  if (s_rows < 0 || cols <= 0 || cols % 256 != 0) return fail(c, KMOE_E_INVALID, "Q8_K needs cols %% 256 == 0");
+  if (s_rows == 0) return KMOE_OK;
+  if (!x || !q || !d || !bs) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, q, d, bs));
+  return KMOE_OK;
+}
+
+int kmoe_quantize_q8(kmoe_ctx *c, const float *x, int64_t s_rows, int64_t cols, int8_t *q, float *d, int32_t *s16) {
+  if (!c) return KMOE_E_INVALID;
+  if (s_rows < 0 || cols <= 0 || cols % 32 != 0) return fail(c, KMOE_E_INVALID, "Q8 needs cols %% 32 == 0");
+  if (s_rows == 0) return KMOE_OK;
+  if (!x || !q || !d || !s16) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, q, d, s16));
+  return KMOE_OK;
+}
+
+int kmoe_matvec_q8(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const int8_t *q,
+                   const float *d, const int32_t *bs, int64_t s_rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  int rc = check_quant_shape(c, t, cols);
+  if (rc) return rc;
+  if (rows < 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "negative size");
+  if ((uint64_t)w_len < (uint64_t)bytes_for(t, cols) * (uint64_t)rows)
+    return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows,
+                (long long)bytes_for(t, cols));
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !q || !d || !out || (t == KMOE_Q4_K && !bs)) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q8_0",
+         launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, bs, s_rows, out));
+  return KMOE_OK;
+}
+
+int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, const int32_t *bs,
+                        int64_t s_rows, int32_t *sumi, int32_t *mins) {
+  if (!c) return KMOE_E_INVALID;
+  int rc = check_quant_shape(c, KMOE_Q4_K, cols);
+  if (rc) return rc;
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !q || !bs || !sumi || !mins) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "block_sums_q4k",
+         launch_block_sums(c->stream, KMOE_Q4_K, (const uint8_t *)w, rows, cols, q, bs, s_rows, sumi, mins));
+  return KMOE_OK;
+}
+
+int kmoe_q8_0_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, int64_t s_rows,
+                         int32_t *p) {
+  if (!c) return KMOE_E_INVALID;
+  int rc = check_quant_shape(c, KMOE_Q8_0, cols);
+  if (rc) return rc;
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !q || !p) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "block_sums_q8_0",
+         launch_block_sums(c->stream, KMOE_Q8_0, (const uint8_t *)w, rows, cols, q, nullptr, s_rows, p, nullptr));
+  return KMOE_OK;
+}
+
+int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const float *x,
+                int64_t s_rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (rows < 0 || cols <= 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  const int64_t rb = bytes_for(t, cols);
+  if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
+  if (rb < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
+  if ((uint64_t)w_len < (uint64_t)rb * (uint64_t)rows)
+    return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows, (long long)rb);
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !x || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  if (t == KMOE_F32) {  // quant.rs:242 (s_rows >= 4) or :311-327 (dequant + quant::dot): summation order kept
+    if (rows > (int64_t)INT32_MAX) return fail(c, KMOE_E_INVALID, "too many rows");
+    LAUNCH(c, "matmul_f32_ordered",
+           launch_router_logits(c->stream, (const float *)w, (int32_t)rows, cols, x, s_rows, out));
+    return KMOE_OK;
+  }
+  int rc = check_quant_shape(c, t, cols);
+  if (rc) return rc;
+  if (!int_path(c->regime, s_rows)) {
+    LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, (const uint8_t *)w, rows, cols, x, s_rows, out));
+    return KMOE_OK;
+  }
+  // int8 activations, quantized into the workspace
+  size_t need = align_up((size_t)s_rows * cols) + align_up((size_t)s_rows * (cols / 32) * 4) +
+                align_up((size_t)s_rows * (cols / 16) * 4);
+  rc = ensure_ws(c, need);
+  if (rc) return rc;
+  Carver cv{c->ws};
+  int8_t *q = cv.take<int8_t>(s_rows * cols);
+  float *d = cv.take<float>(s_rows * (cols / 32));
+  int32_t *s = cv.take<int32_t>(s_rows * (cols / 16));
+  if (t == KMOE_Q4_K) {
+    LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, q, d, s));
+    LAUNCH(c, "matvec_q4k", launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out));
+  } else {
+    LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, q, d, s));
+    LAUNCH(c, "matvec_q8_0", launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out));
+  }
+  return KMOE_OK;
+}
+
+int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const float *h, int64_t S, int32_t k,
+               int32_t norm_topk, float weights_scale, uint32_t *idx, float *w, float *logits) {
+  if (!c) return KMOE_E_INVALID;
+  if (E <= 0 || E > 512 || k <= 0 || k > 16 || k > E || d <= 0 || S < 0)
+    return fail(c, KMOE_E_INVALID, "route: need 0 < k <= min(E, 16), E <= 512");
+  if (S == 0) return KMOE_OK;
+  if (!router || !h || !idx || !w) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  float *lg = logits;
+  if (!lg) {
+    int rc = ensure_ws(c, align_up((size_t)S * E * 4));
+    if (rc) return rc;
+    lg = (float *)c->ws;
+  }
+  LAUNCH(c, "router_logits", launch_router_logits(c->stream, router, E, d, h, S, lg));
+  LAUNCH(c, "route_topk", launch_route_topk(c->stream, lg, S, E, k, norm_topk, weights_scale, idx, w));
+  return KMOE_OK;
+}
+
+int kmoe_dispatch(kmoe_ctx *c, const uint32_t *idx, int64_t S, int32_t k, int32_t E, uint32_t *perm, uint32_t *off) {
+  if (!c) return KMOE_E_INVALID;
+  if (E <= 0 || E > 512 || k <= 0 || S < 0) return fail(c, KMOE_E_INVALID, "dispatch: bad sizes");
+  if (!idx || !perm || !off) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  int rc = ensure_ws(c, align_up((size_t)S * k * 4));
+  if (rc) return rc;
+  LAUNCH(c, "dispatch",
+         launch_dispatch(c->stream, idx, S * k, E, perm, off, nullptr, nullptr, nullptr, (uint32_t *)c->ws));
+  return KMOE_OK;
+}
+
+// ------------------------------------------------------------ expert tier
+
+int kmoe_layer_create(kmoe_ctx *c, uint32_t layer, const kmoe_moe_desc *desc) {
+  if (!c || !desc) return KMOE_E_INVALID;
+  const kmoe_moe_desc &D = *desc;
+  if (c->layers.count(layer)) return fail(c, KMOE_E_INVALID, "layer %u already exists", layer);
+  if (D.n_expert == 0 || D.n_expert > 512 || D.n_expert_used == 0 || D.n_expert_used > 16 ||
+      D.n_expert_used > D.n_expert)
+    return fail(c, KMOE_E_INVALID, "need 0 < n_expert_used <= min(n_expert, 16), n_expert <= 512");
+  if (D.gate_type != D.up_type) return fail(c, KMOE_E_UNSUPPORTED, "gate and up must share a ggml type");
+  int rc = check_quant_shape(c, D.gate_type, D.n_embd);
+  if (!rc) rc = check_quant_shape(c, D.down_type, D.n_ff);
+  if (rc) return rc;
+  if (D.n_ff % 64 != 0) return fail(c, KMOE_E_UNSUPPORTED, "n_ff %% 64 != 0");
+  Layer L;
+  L.desc = D;
+  L.part_len[0] = (size_t)bytes_for(D.gate_type, D.n_embd) * D.n_ff;
+  L.part_len[1] = (size_t)bytes_for(D.up_type, D.n_embd) * D.n_ff;
+  L.part_len[2] = (size_t)bytes_for(D.down_type, D.n_ff) * D.n_embd;
+  L.part_off[0] = 0;
+  L.part_off[1] = align_up(L.part_len[0]);
+  L.part_off[2] = L.part_off[1] + align_up(L.part_len[1]);
+  L.expert_stride = L.part_off[2] + align_up(L.part_len[2]);
+  const size_t arena = L.expert_stride * D.n_expert;
+  const size_t router = align_up((size_t)D.n_expert * D.n_embd * 4);
+  DeviceGuard g(c->device);
+  void *p = nullptr;
+  rc = dev_alloc(c, arena, &p, "expert tier");
+  if (rc) return rc;
+  L.arena = (uint8_t *)p;
+  rc = dev_alloc(c, router, &p, "router");
+  if (rc) {
+    (void)hipFree(L.arena);
+    release(c, arena);
+    return rc;
+  }
+  L.router = (float *)p;
+  L.reserved = arena + router;
+  L.loaded.assign(D.n_expert, 0);
+  c->layers[layer] = L;
+  return KMOE_OK;
+}
+
+int kmoe_layer_destroy(kmoe_ctx *c, uint32_t layer) {
+  if (!c) return KMOE_E_INVALID;
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  (void)hipFree(it->second.arena);
+  (void)hipFree(it->second.router);
+  release(c, it->second.reserved);
+  c->layers.erase(it);
+  return KMOE_OK;
+}
+
+static Layer *find_layer(kmoe_ctx *c, uint32_t layer) {
+  auto it = c->layers.find(layer);
+  return it == c->layers.end() ? nullptr : &it->second;
+}
+
+int kmoe_router_upload(kmoe_ctx *c, uint32_t layer, const float *router, size_t bytes) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  const size_t need = (size_t)L->desc.n_expert * L->desc.n_embd * 4;
+  if (bytes != need || !router) return fail(c, KMOE_E_INVALID, "router bytes %zu != %zu", bytes, need);
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(L->router, router, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  L->router_ok = true;
+  return KMOE_OK;
+}
+
+static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len,
+                         hipMemcpyKind kind) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (e >= L->desc.n_expert || part < 0 || part > 2) return fail(c, KMOE_E_INVALID, "expert %u part %d", e, part);
+  if (len != L->part_len[part] || !bytes)
+    return fail(c, KMOE_E_INVALID, "expert part bytes %zu != %zu", len, L->part_len[part]);
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(L->arena + e * L->expert_stride + L->part_off[part], bytes, len, kind, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  L->loaded[e] |= (uint8_t)(1u << part);
+  return KMOE_OK;
+}
+
+int kmoe_expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len) {
+  return expert_upload(c, layer, e, part, bytes, len, hipMemcpyHostToDevice);
+}
+int kmoe_expert_upload_dev(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len) {
+  return expert_upload(c, layer, e, part, bytes, len, hipMemcpyDeviceToDevice);
+}
+
+int kmoe_expert_is_ready(kmoe_ctx *c, uint32_t layer, uint32_t e) {
+  if (!c) return 0;
+  Layer *L = find_layer(c, layer);
+  if (!L || e >= L->desc.n_expert) return 0;
+  return L->loaded[e] == 7 ? 1 : 0;
+}
+
+int kmoe_expert_part(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void **dev, size_t *len) {
+  if (!c || !dev || !len) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (e >= L->desc.n_expert || part < 0 || part > 2) return fail(c, KMOE_E_INVALID, "expert %u part %d", e, part);
+  if (!(L->loaded[e] & (1u << part))) return fail(c, KMOE_E_NOT_LOADED, "expert %u part %d not resident", e, part);
+  *dev = L->arena + e * L->expert_stride + L->part_off[part];
+  *len = L->part_len[part];
+  return KMOE_OK;
+}
+
+int kmoe_bytes_per_expert(kmoe_ctx *c, uint32_t layer, uint64_t *bytes) {
+  if (!c || !bytes) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  *bytes = L->part_len[0] + L->part_len[1] + L->part_len[2];
+  return KMOE_OK;
+}
+
+// --------------------------------------------------------------- moe_ffn
+
+int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (S < 0) return fail(c, KMOE_E_INVALID, "negative s_rows");
+  if (S == 0) return KMOE_OK;
+  if (!h || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  if (!L->router_ok) return fail(c, KMOE_E_NOT_LOADED, "layer %u router not uploaded", layer);
+  for (uint32_t e = 0; e < L->desc.n_expert; ++e)
+    if (L->loaded[e] != 7) return fail(c, KMOE_E_NOT_LOADED, "layer %u expert %u not resident", layer, e);
+  const kmoe_moe_desc &D = L->desc;
+  const int64_t E = D.n_expert, k = D.n_expert_used, d = D.n_embd, F = D.n_ff;
+  const int64_t slots = S * k;
+  if (slots > (int64_t)UINT32_MAX / 2) return fail(c, KMOE_E_INVALID, "too many tokens");
+  size_t need = 0;
+  carve_moe(nullptr, S, E, k, d, F, &need);
+  DeviceGuard g(c->device);
+  int rc = ensure_ws(c, need);
+  if (rc) return rc;
+  size_t tmp;
+  MoeWs w = carve_moe(c->ws, S, E, k, d, F, &tmp);
+  const int regime = c->regime;
+  hipStream_t st = c->stream;
+
+  // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531)
+  LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
+  LAUNCH(c, "route_topk",
+         launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk, D.weights_scale, w.idx, w.wsel));
+  LAUNCH(c, "dispatch", launch_dispatch(st, w.idx, slots, (int32_t)E, w.perm, w.offsets, w.inv, w.n_active,
+                                        w.active, w.rank));
+  Routing rt{w.n_active, w.active, w.offsets, w.perm, w.inv, w.wsel, (int32_t)k};
+  ExpertTier tier{L->arena, (int64_t)L->expert_stride,
+                  {(int64_t)L->part_off[0], (int64_t)L->part_off[1], (int64_t)L->part_off[2]}};
+  const int max_active = (int)(slots < E ? slots : E);
+  // Which regimes can occur: an expert has at most S rows.
+  const bool any_int = regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2);
+  const bool any_f32 = regime == KMOE_REGIME_EXACT || (regime == KMOE_REGIME_AVX2 && S >= 4);
+  const int gt = D.gate_type, dt = D.down_type;
+
+  // expert gate/up + SwiGLU (transformer.rs:551-558)
+  if (any_int) {
+    if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
+    else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
+    LAUNCH(c, "moe_gate_up_int",
+           launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
+  }
+  if (any_f32) {
+    LAUNCH(c, "moe_gate_f32", launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, h, w.h));
+    LAUNCH(c, "moe_up_f32", launch_moe_f32(st, 1, gt, tier, F, d, rt, regime, max_active, S, h, w.h));
+  }
+  // down (transformer.rs:559-560)
+  if (any_int) {
+    LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
+           launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
+    LAUNCH(c, "moe_down_int",
+           launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
+  }
+  if (any_f32) LAUNCH(c, "moe_down_f32", launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, w.h, w.y));
+  // combine (transformer.rs:566-570)
+  LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
+
+  c->last_idx = w.idx;
+  c->last_w = w.wsel;
+  c->last_perm = w.perm;
+  c->last_off = w.offsets;
+  c->last_slots = slots;
+  c->last_E = (int32_t)E;
+  return KMOE_OK;
+}
+
+int kmoe_moe_last_routing(kmoe_ctx *c, uint32_t *idx, float *wv, uint32_t *perm, uint32_t *off) {
+  if (!c) return KMOE_E_INVALID;
+  if (!c->last_idx) return fail(c, KMOE_E_NOT_LOADED, "no kmoe_moe_ffn call yet");
+  DeviceGuard g(c->device);
+  const size_t n = (size_t)c->last_slots;
+  if (idx) HIP_OK(c, hipMemcpyAsync(idx, c->last_idx, n * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (wv) HIP_OK(c, hipMemcpyAsync(wv, c->last_w, n * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (perm) HIP_OK(c, hipMemcpyAsync(perm, c->last_perm, n * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (off) HIP_OK(c, hipMemcpyAsync(off, c->last_off, (size_t)(c->last_E + 1) * 4, hipMemcpyDeviceToDevice, c->stream));
+  return KMOE_OK;
+}
+
+// ------------------------------------------------------------- profiling
+
+int kmoe_profile_enable(kmoe_ctx *c, int on) {
+  if (!c) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  prof_drain(c);
+  c->prof_acc.clear();
+  c->prof = on != 0;
+  return KMOE_OK;
+}
+
+int kmoe_profile_read(kmoe_ctx *c, const char *kernel, double *total_ms, int64_t *launches) {
+  if (!c || !kernel) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  prof_drain(c);
+  auto it = c->prof_acc.find(kernel);
+  if (total_ms) *total_ms = it == c->prof_acc.end() ? 0.0 : it->second.first;
+  if (launches) *launches = it == c->prof_acc.end() ? 0 : it->second.second;
+  return KMOE_OK;
+}
+
+}  // extern "C"

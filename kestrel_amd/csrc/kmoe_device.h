@@ -1,0 +1,151 @@
+// kmoe_device.h — device helpers shared by the gfx950 kernels.
+//
+// Wave64 throughout. Cross-lane sums use DPP inside a 16-lane row
+// (quad_perm xor1/xor2, row_half_mirror, row_mirror) and ds_swizzle/bpermute
+// shuffles across rows. All float code is compiled with -ffp-contract=off:
+// an FMA appears only where fmaf() is written.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kmoe {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// DPP controls (gfx9): quad_perm [1,0,3,2] = lane^1, [2,3,0,1] = lane^2,
+// row_half_mirror (lane i <- 7-i within 8), row_mirror (lane i <- 15-i within 16).
+constexpr int kDppXor1 = 0xb1;
+constexpr int kDppXor2 = 0x4e;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// Sum over aligned groups of W lanes (W in 1..64, power of two); every lane of
+// the group receives the group sum.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (W >= 2) v += dpp_f<kDppXor1>(v);
+  if constexpr (W >= 4) v += dpp_f<kDppXor2>(v);
+  if constexpr (W >= 8) v += dpp_f<kDppHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_f<kDppMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v) {
+  if constexpr (W >= 2) v += dpp_i<kDppXor1>(v);
+  if constexpr (W >= 4) v += dpp_i<kDppXor2>(v);
+  if constexpr (W >= 8) v += dpp_i<kDppHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_i<kDppMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+// Max over groups of W lanes (exact in any order).
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (W >= 2) v = fmaxf(v, dpp_f<kDppXor1>(v));
+  if constexpr (W >= 4) v = fmaxf(v, dpp_f<kDppXor2>(v));
+  if constexpr (W >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  if constexpr (W >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
+  if constexpr (W >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (W >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+// scale_min_k4 (quant.rs:54-61) for sub-blocks j = 2k and 2k+1 of a Q4_K
+// superblock whose 12 scale bytes are the little-endian words s03, s47, s811.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s03, uint32_t s47, uint32_t s811, int k, int &sA,
+                                                   int &mA, int &sB, int &mB) {
+  if (k < 2) {
+    const int j = 2 * k;
+    sA = (int)(byte_of(s03, j) & 63u);
+    mA = (int)(byte_of(s47, j) & 63u);
+    sB = (int)(byte_of(s03, j + 1) & 63u);
+    mB = (int)(byte_of(s47, j + 1) & 63u);
+  } else {
+    const int i = 2 * k - 4;  // j - 4 for j = 2k
+    sA = (int)((byte_of(s811, i) & 0xfu) | ((byte_of(s03, i) >> 6) << 4));
+    mA = (int)((byte_of(s811, i) >> 4) | ((byte_of(s47, i) >> 6) << 4));
+    sB = (int)((byte_of(s811, i + 1) & 0xfu) | ((byte_of(s03, i + 1) >> 6) << 4));
+    mB = (int)((byte_of(s811, i + 1) >> 4) | ((byte_of(s47, i + 1) >> 6) << 4));
+  }
+}
+
+// Dword-aligned 16-byte load (global_load_dwordx4 accepts 4-byte alignment).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ uint4 load_u4_a4(const void *p) {
+  u32x4a4 v = *(const u32x4a4 *)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Correctly rounded expf via double exp. glibc's expf (what the reference's
+// f32::exp calls) is within 0.502 ulp, so the two agree except on inputs
+// whose exact value lies within ~0.002 ulp of a rounding midpoint.
+__device__ __forceinline__ float expf_cr(float x) { return (float)exp((double)x); }
+
+// Rust `(v).round() as i32` clamped to [-127, 127] (qdot.rs:43, :360).
+__device__ __forceinline__ int8_t q8_round(float v) {
+  float r = roundf(v);  // half away from zero, like f32::round
+  if (isnan(r)) return 0;
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8_t d) {
+  return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) | ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
+}
+
+// Q8KRow::quantize of one 256-element block by one full wave (qdot.rs:353-365).
+// Lane l owns elements 4l..4l+3. Writes q[0..256), *d, bsums[0..16).
+__device__ __forceinline__ void wave_quant_q8k_block(const float *x, int8_t *q, float *d, int32_t *bsums, int lane) {
+  const float4 v = *(const float4 *)(x + 4 * lane);
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = group_max<64>(amax);
+  const float scale = amax / 127.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  const int8_t a = q8_round(v.x * inv), b = q8_round(v.y * inv), c = q8_round(v.z * inv), e = q8_round(v.w * inv);
+  *(uint32_t *)(q + 4 * lane) = pack_i8x4(a, b, c, e);
+  int s = (int)a + (int)b + (int)c + (int)e;
+  s = group_sum_i<4>(s);
+  if ((lane & 3) == 0) bsums[lane >> 2] = s;
+  if (lane == 0) *d = scale;
+}
+
+// Q8Row::quantize of one 32-element block by an aligned group of 8 lanes
+// (qdot.rs:36-47). g = lane & 7 owns elements 4g..4g+3.
+__device__ __forceinline__ void group8_quant_q8_block(const float *x, int8_t *q, float *d, int32_t *s16, int g) {
+  const float4 v = *(const float4 *)(x + 4 * g);
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  amax = group_max<8>(amax);
+  const float scale = amax / 127.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  const int8_t a = q8_round(v.x * inv), b = q8_round(v.y * inv), c = q8_round(v.z * inv), e = q8_round(v.w * inv);
+  *(uint32_t *)(q + 4 * g) = pack_i8x4(a, b, c, e);
+  int s = (int)a + (int)b + (int)c + (int)e;
+  s = group_sum_i<4>(s);
+  if ((g & 3) == 0) s16[g >> 2] = s;
+  if (g == 0) *d = scale;
+}
+
+}  // namespace kmoe

@@ -1,0 +1,74 @@
+// kmoe_launch.h — host-side launchers of the gfx950 kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kmoe {
+
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12 };
+enum { REGIME_AVX2 = 0, REGIME_INT8 = 1, REGIME_EXACT = 2 };
+
+// ---- activation quantizers (kmoe_quant.hip)
+hipError_t launch_quant_q8k(hipStream_t st, const float *x, int64_t rows, int64_t cols, int8_t *q, float *d,
+                            int32_t *bsums);
+hipError_t launch_quant_q8(hipStream_t st, const float *x, int64_t rows, int64_t cols, int8_t *q, float *d,
+                           int32_t *s16);
+
+// ---- routing on-device state produced by dispatch, read by the grouped kernels
+struct Routing {
+  const int32_t *n_active;  // [1] number of experts with rows
+  const int32_t *active;    // [n_expert] their ids, ascending
+  const uint32_t *offsets;  // [n_expert+1]
+  const uint32_t *perm;     // [S*k] flat (token*k + slot), sorted by expert then token
+  const uint32_t *inv;      // [S*k] position of flat index in perm
+  const float *wsel;        // [S*k] routing weights, flat
+  int32_t topk;
+};
+
+// Expert tier addressing: expert e's part p starts at base + e*stride + off[p].
+struct ExpertTier {
+  const uint8_t *base;
+  int64_t stride;
+  int64_t off[3];
+};
+
+// ---- int8 matvecs (kmoe_matvec.hip)
+// Plain: out[s*rows + r] for s < s_rows; activations pre-quantized.
+hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+                             const float *xd, const int32_t *xbs, int64_t s_rows, float *out);
+// Block sums (debug path of the same device code).
+hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                             const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins);
+// Grouped MoE, int path: gate+up+SwiGLU -> h [slots, F] f32 (mode 0) or down -> y [slots, d] f32 (mode 1).
+// Experts handled: those whose row count the regime sends to the int path.
+hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                          const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
+                          const float *xd, const int32_t *xbs, float *out);
+
+// ---- f32 path (kmoe_gemm_f32.hip): dequantized weights x f32 activations
+// Plain: out[s*rows + r].
+hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const float *x,
+                             int64_t s_rows, float *out);
+// Grouped: mode 0 = gate (store g into h), 1 = up (h = silu(h) * u), 2 = down (store y).
+hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                          const Routing &rt, int regime, int max_active, int64_t max_rows_per_expert,
+                          const float *x, float *out);
+
+// ---- routing (kmoe_route.hip)
+// logits [S, E] = router [E, d] . x [S, d] in the reference's summation order.
+hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
+                                int64_t s_rows, float *logits);
+hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
+                             int32_t norm_topk, float weights_scale, uint32_t *idx, float *w);
+// Stable counting sort by expert. inv/n_active/active may be null.
+hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
+                           uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp);
+// Q8_K / Q8 quantization of the slot rows of h that go to the int path.
+hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t n_slots, int64_t cols,
+                              const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
+                              int32_t *sums);
+// out[s] = sum over the token's experts in ascending id of w * y[slot].
+hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out);
+
+}  // namespace kmoe

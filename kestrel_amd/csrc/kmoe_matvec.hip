@@ -1,0 +1,434 @@
+// kmoe_matvec.hip — int8-activation matvecs over GGUF blocks (the decode path).
+//
+// Arithmetic (per weight row r, activation row s):
+//   Q4_K x Q8_K (avx2.rs:351-379): per superblock b,
+//     sumi_b = sum_j sc_j * sum_{32 elems of j} q*x,  mins_b = sum_j m_j * (bsum pair of j)
+//     y += (d_b * xd_b) * sumi_b - (dmin_b * xd_b) * mins_b
+//   Q8_0 x Q8 (avx2.rs:49-58): per block b, p_b = sum q*x, y += (d_b * xd_b) * p_b
+// The integers are exact (int32, no saturation: max |pair| is 2*15*127 for
+// Q4_K and 2*128*127 for Q8_0), so sumi_b, mins_b and p_b equal the
+// reference's bit for bit; the fp32 epilogue sums in a different order, which
+// moves the result by a few ulp (checked against a 1e-3 relative L2 bound).
+//
+// Layout and mapping. Weights stay in GGUF bytes. A Q4_K "task" is one
+// quarter of a 144-byte superblock: the 16-byte header (d, dmin, 12 scale
+// bytes) plus 32 bytes of nibbles (64 weights of sub-blocks 2k and 2k+1).
+// Four consecutive lanes read one superblock, so a wave's loads cover whole
+// superblocks contiguously. A Q8_0 task is one 34-byte block, read as nine
+// dwords from the dword-aligned address below it. LPR lanes share a row
+// (LPR = 64 for 4096-wide Q4_K rows: one row per wave per step); they reduce
+// with DPP and cross-row shuffles. Activations (int8 rows, their scales and
+// 16-sums) are staged once per work-group in LDS; each lane reads its 64
+// activation bytes with ds_read_b128.
+#include "kmoe_device.h"
+#include "kmoe_launch.h"
+
+namespace kmoe {
+
+namespace {
+
+struct MvArgs {
+  const uint8_t *w0;
+  int64_t rows, cols;
+  const int8_t *xq;
+  const float *xd;
+  const int32_t *xbs;
+  int64_t s_rows;
+  float *out;
+  int32_t *isumi, *imins;
+  ExpertTier tier;
+  Routing rt;
+  int regime;
+  int rows_per_block;
+};
+
+enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
+
+__device__ __forceinline__ bool int_regime(int regime, int n) {
+  return regime == REGIME_INT8 || (regime == REGIME_AVX2 && n < 4);
+}
+
+// Bytes per activation row in LDS, 16-byte aligned pieces: q, sums, scales.
+template <int TYPE>
+struct ActLayout {
+  int64_t q, s, d, total;
+  __host__ __device__ ActLayout(int64_t cols) {
+    q = (cols + 15) & ~15ll;
+    s = TYPE == T_Q4_K ? ((cols / 16 * 4 + 15) & ~15ll) : 0;  // Q8_0 never reads the 16-sums
+    const int64_t nd = TYPE == T_Q4_K ? cols / 256 : cols / 32;
+    d = (nd * 4 + 15) & ~15ll;
+    total = q + s + d;
+  }
+};
+
+struct Q4kW {
+  uint4 hdr, qa, qb;
+};
+
+__device__ __forceinline__ Q4kW q4k_load(const uint8_t *row, int t) {
+  const uint8_t *sb = row + (int64_t)(t >> 2) * 144;
+  const int k = t & 3;
+  Q4kW w;
+  w.hdr = *(const uint4 *)sb;
+  w.qa = *(const uint4 *)(sb + 16 + 32 * k);
+  w.qb = *(const uint4 *)(sb + 32 + 32 * k);
+  return w;
+}
+
+// Integer part of one Q4_K task against one Q8_K row (xq/xbs at the superblock).
+__device__ __forceinline__ void q4k_ints(const Q4kW &w, int k, const int8_t *xq_sb, const int32_t *xbs_sb, int &sumi,
+                                         int &mins) {
+  int sA, mA, sB, mB;
+  q4k_scale_min_pair(w.hdr.y, w.hdr.z, w.hdr.w, k, sA, mA, sB, mB);
+  const int4 *xv = (const int4 *)(xq_sb + 64 * k);
+  const int4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+  const uint32_t m = 0x0f0f0f0fu;
+  int lo = 0, hi = 0;
+  lo = sdot4(w.qa.x & m, (uint32_t)x0.x, lo);
+  lo = sdot4(w.qa.y & m, (uint32_t)x0.y, lo);
+  lo = sdot4(w.qa.z & m, (uint32_t)x0.z, lo);
+  lo = sdot4(w.qa.w & m, (uint32_t)x0.w, lo);
+  lo = sdot4(w.qb.x & m, (uint32_t)x1.x, lo);
+  lo = sdot4(w.qb.y & m, (uint32_t)x1.y, lo);
+  lo = sdot4(w.qb.z & m, (uint32_t)x1.z, lo);
+  lo = sdot4(w.qb.w & m, (uint32_t)x1.w, lo);
+  hi = sdot4((w.qa.x >> 4) & m, (uint32_t)x2.x, hi);
+  hi = sdot4((w.qa.y >> 4) & m, (uint32_t)x2.y, hi);
+  hi = sdot4((w.qa.z >> 4) & m, (uint32_t)x2.z, hi);
+  hi = sdot4((w.qa.w >> 4) & m, (uint32_t)x2.w, hi);
+  hi = sdot4((w.qb.x >> 4) & m, (uint32_t)x3.x, hi);
+  hi = sdot4((w.qb.y >> 4) & m, (uint32_t)x3.y, hi);
+  hi = sdot4((w.qb.z >> 4) & m, (uint32_t)x3.z, hi);
+  hi = sdot4((w.qb.w >> 4) & m, (uint32_t)x3.w, hi);
+  sumi = sA * lo + sB * hi;
+  const int4 bs = *(const int4 *)(xbs_sb + 4 * k);
+  mins = mA * (bs.x + bs.y) + mB * (bs.z + bs.w);
+}
+
+struct Q80W {
+  uint4 a, b;
+  uint32_t c;
+  int sh;  // 0: block starts on a dword, 2: two bytes past one
+};
+
+__device__ __forceinline__ Q80W q80_load(const uint8_t *row, int t) {
+  const uintptr_t addr = (uintptr_t)(row + (int64_t)t * 34);
+  const uint8_t *base = (const uint8_t *)(addr & ~(uintptr_t)3);
+  Q80W w;
+  w.sh = (int)(addr & 3);
+  w.a = load_u4_a4(base);
+  w.b = load_u4_a4(base + 16);
+  w.c = *(const uint32_t *)(base + 32);
+  return w;
+}
+
+__device__ __forceinline__ int q80_int(const Q80W &w, const int8_t *xq_b, float &dw) {
+  const uint32_t v[9] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w, w.c};
+  uint32_t q[8];
+  if (w.sh == 0) {
+    dw = f16_bits_to_f32(v[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+  } else {
+    dw = f16_bits_to_f32(v[0] >> 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = v[i + 1];
+  }
+  const int4 *xv = (const int4 *)xq_b;
+  const int4 x0 = xv[0], x1 = xv[1];
+  int p = 0;
+  p = sdot4(q[0], (uint32_t)x0.x, p);
+  p = sdot4(q[1], (uint32_t)x0.y, p);
+  p = sdot4(q[2], (uint32_t)x0.z, p);
+  p = sdot4(q[3], (uint32_t)x0.w, p);
+  p = sdot4(q[4], (uint32_t)x1.x, p);
+  p = sdot4(q[5], (uint32_t)x1.y, p);
+  p = sdot4(q[6], (uint32_t)x1.z, p);
+  p = sdot4(q[7], (uint32_t)x1.w, p);
+  return p;
+}
+
+template <int TYPE, int LPR, int NT, int MODE>
+__global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int RPW = 64 / LPR;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row_in_wave = lane / LPR, lr = lane % LPR;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
+  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t xs_stride = cols / 16, xd_stride = nblk;
+  const ActLayout<TYPE> L(cols);
+
+  int n;
+  int64_t p0 = 0;
+  const uint8_t *W0 = a.w0, *W1 = nullptr;
+  if constexpr (MODE == M_PLAIN || MODE == M_SUMS) {
+    n = (int)a.s_rows;
+  } else {
+    const int i = blockIdx.y;
+    if (i >= *a.rt.n_active) return;
+    const int e = a.rt.active[i];
+    p0 = a.rt.offsets[e];
+    n = (int)(a.rt.offsets[e + 1] - p0);
+    if (!int_regime(a.regime, n)) return;
+    const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
+    if constexpr (MODE == M_GATE_UP) {
+      W0 = eb + a.tier.off[0];
+      W1 = eb + a.tier.off[1];
+    } else {
+      W0 = eb + a.tier.off[2];
+    }
+  }
+  const int64_t r_begin = (int64_t)blockIdx.x * a.rows_per_block;
+  const int64_t r_end = r_begin + a.rows_per_block < rows ? r_begin + a.rows_per_block : rows;
+
+  for (int c0 = 0; c0 < n; c0 += NT) {
+    const int nt = n - c0 < NT ? n - c0 : NT;
+    // ---- stage the activation rows of tokens c0..c0+nt in LDS
+    for (int t = 0; t < nt; ++t) {
+      int64_t src;
+      if constexpr (MODE == M_GATE_UP) src = a.rt.perm[p0 + c0 + t] / a.rt.topk;
+      else if constexpr (MODE == M_DOWN) src = p0 + c0 + t;
+      else src = c0 + t;
+      char *dst = smem + t * L.total;
+      const uint32_t *sq = (const uint32_t *)(a.xq + src * cols);
+      for (int64_t i = threadIdx.x; i < cols / 4; i += 256) ((uint32_t *)dst)[i] = sq[i];
+      if constexpr (TYPE == T_Q4_K) {
+        const int32_t *ss = a.xbs + src * xs_stride;
+        for (int64_t i = threadIdx.x; i < xs_stride; i += 256) ((int32_t *)(dst + L.q))[i] = ss[i];
+      }
+      const float *sd = a.xd + src * xd_stride;
+      for (int64_t i = threadIdx.x; i < xd_stride; i += 256) ((float *)(dst + L.q + L.s))[i] = sd[i];
+    }
+    __syncthreads();
+
+    for (int64_t rb = r_begin + (int64_t)wave * RPW; rb < r_end; rb += 4 * RPW) {
+      const int64_t r = rb + row_in_wave;
+      const bool valid = r < r_end;
+      float acc0[NT], acc1[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc0[t] = acc1[t] = 0.0f;
+      if (valid) {
+        const uint8_t *row0 = W0 + r * row_bytes;
+        const uint8_t *row1 = MODE == M_GATE_UP ? W1 + r * row_bytes : nullptr;
+        for (int t = lr; t < ntasks; t += LPR) {
+          if constexpr (TYPE == T_Q4_K) {
+            const int sb = t >> 2, k = t & 3;
+            const Q4kW w0 = q4k_load(row0, t);
+            Q4kW w1;
+            if constexpr (MODE == M_GATE_UP) w1 = q4k_load(row1, t);
+            const float d0 = f16_bits_to_f32(w0.hdr.x), m0 = f16_bits_to_f32(w0.hdr.x >> 16);
+#pragma unroll
+            for (int tk = 0; tk < NT; ++tk) {
+              if (tk < nt) {
+                const char *act = smem + tk * L.total;
+                const int8_t *xq_sb = (const int8_t *)act + sb * 256;
+                const int32_t *xbs_sb = (const int32_t *)(act + L.q) + sb * 16;
+                const float xd = ((const float *)(act + L.q + L.s))[sb];
+                int si, mi;
+                q4k_ints(w0, k, xq_sb, xbs_sb, si, mi);
+                if constexpr (MODE == M_SUMS) {
+                  const int ss = group_sum_i<4>(si), ms = group_sum_i<4>(mi);
+                  if (k == 0) {
+                    const int64_t o = ((int64_t)(c0 + tk) * rows + r) * nblk + sb;
+                    a.isumi[o] = ss;
+                    a.imins[o] = ms;
+                  }
+                } else {
+                  acc0[tk] = fmaf(d0 * xd, (float)si, acc0[tk]);
+                  acc0[tk] = fmaf(-(m0 * xd), (float)mi, acc0[tk]);
+                  if constexpr (MODE == M_GATE_UP) {
+                    const float d1 = f16_bits_to_f32(w1.hdr.x), m1 = f16_bits_to_f32(w1.hdr.x >> 16);
+                    q4k_ints(w1, k, xq_sb, xbs_sb, si, mi);
+                    acc1[tk] = fmaf(d1 * xd, (float)si, acc1[tk]);
+                    acc1[tk] = fmaf(-(m1 * xd), (float)mi, acc1[tk]);
+                  }
+                }
+              }
+            }
+          } else {
+            const Q80W w0 = q80_load(row0, t);
+            Q80W w1;
+            if constexpr (MODE == M_GATE_UP) w1 = q80_load(row1, t);
+#pragma unroll
+            for (int tk = 0; tk < NT; ++tk) {
+              if (tk < nt) {
+                const char *act = smem + tk * L.total;
+                const int8_t *xq_b = (const int8_t *)act + t * 32;
+                const float xd = ((const float *)(act + L.q + L.s))[t];
+                float dw;
+                const int p = q80_int(w0, xq_b, dw);
+                if constexpr (MODE == M_SUMS) {
+                  a.isumi[((int64_t)(c0 + tk) * rows + r) * nblk + t] = p;
+                } else {
+                  acc0[tk] = fmaf(dw * xd, (float)p, acc0[tk]);
+                  if constexpr (MODE == M_GATE_UP) {
+                    float dw1;
+                    const int p1 = q80_int(w1, xq_b, dw1);
+                    acc1[tk] = fmaf(dw1 * xd, (float)p1, acc1[tk]);
+                  }
+                }
+              }
+            }
+          }
+        }
+      }
+      if constexpr (MODE != M_SUMS) {
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) {
+          acc0[tk] = group_sum<LPR>(acc0[tk]);
+          if constexpr (MODE == M_GATE_UP) acc1[tk] = group_sum<LPR>(acc1[tk]);
+        }
+        if (valid && lr == 0) {
+#pragma unroll
+          for (int tk = 0; tk < NT; ++tk) {
+            if (tk < nt) {
+              if constexpr (MODE == M_PLAIN) {
+                a.out[(int64_t)(c0 + tk) * rows + r] = acc0[tk];
+              } else if constexpr (MODE == M_DOWN) {
+                a.out[(p0 + c0 + tk) * rows + r] = acc0[tk];
+              } else {  // SwiGLU (transformer.rs:558): g / (1 + exp(-g)) * u
+                const float g = acc0[tk];
+                const float den = 1.0f + expf_cr(-g);
+                const float q = g / den;
+                a.out[(p0 + c0 + tk) * rows + r] = q * acc1[tk];
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int TYPE, int LPR, int NT, int MODE>
+hipError_t launch_one(hipStream_t st, const MvArgs &a, dim3 grid) {
+  const ActLayout<TYPE> L(a.cols);
+  const size_t shmem = (size_t)NT * L.total;
+  hipLaunchKernelGGL((k_matvec_int<TYPE, LPR, NT, MODE>), grid, dim3(256), shmem, st, a);
+  return hipGetLastError();
+}
+
+// Lanes per row: the widest of 64/32/16/4 that keeps >= 85% of lanes busy.
+int pick_lpr(int ntasks) {
+  const int opts[4] = {64, 32, 16, 4};
+  int best = 4;
+  double best_eff = -1.0;
+  for (int o : opts) {
+    const int iters = (ntasks + o - 1) / o;
+    const double eff = (double)ntasks / (double)(iters * o);
+    if (eff >= 0.85) return o;
+    if (eff > best_eff) {
+      best_eff = eff;
+      best = o;
+    }
+  }
+  return best;
+}
+
+template <int TYPE, int MODE>
+hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_max) {
+  const int64_t nblk = TYPE == T_Q4_K ? a.cols / 256 : a.cols / 32;
+  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int lpr = pick_lpr(ntasks);
+#define KMOE_LPR_CASE(LPRV)                                                                          \
+  case LPRV:                                                                                         \
+    if constexpr (MODE == M_SUMS) return launch_one<TYPE, LPRV, 1, MODE>(st, a, grid);               \
+    else return nt_max == 1 ? launch_one<TYPE, LPRV, 1, MODE>(st, a, grid)                           \
+                            : launch_one<TYPE, LPRV, 3, MODE>(st, a, grid);
+  switch (lpr) {
+    KMOE_LPR_CASE(64)
+    KMOE_LPR_CASE(32)
+    KMOE_LPR_CASE(16)
+    KMOE_LPR_CASE(4)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef KMOE_LPR_CASE
+}
+
+constexpr int kRowsPerBlock = 64;
+
+bool act_fits(int type, int64_t cols) {
+  const int64_t per = type == T_Q4_K ? ActLayout<T_Q4_K>(cols).total : ActLayout<T_Q8_0>(cols).total;
+  return 3 * per <= 65536;
+}
+
+}  // namespace
+
+hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+                             const float *xd, const int32_t *xbs, int64_t s_rows, float *out) {
+  if (rows == 0 || s_rows == 0) return hipSuccess;
+  if (!act_fits(type, cols)) return hipErrorInvalidValue;
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.s_rows = s_rows;
+  a.out = out;
+  a.rows_per_block = kRowsPerBlock;
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  const int nt = s_rows == 1 ? 1 : 3;
+  if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_PLAIN>(st, a, grid, nt);
+  if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_PLAIN>(st, a, grid, nt);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                             const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins) {
+  if (rows == 0 || s_rows == 0) return hipSuccess;
+  if (!act_fits(type, cols)) return hipErrorInvalidValue;
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xbs = xbs;
+  a.s_rows = s_rows;
+  a.isumi = sumi;
+  a.imins = mins;
+  a.rows_per_block = kRowsPerBlock;
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  // The Q8_0 scales are not read by the sums; Q4_K's dw/xd are not either, but
+  // the staging copies xd: give it a valid dummy of the right length.
+  a.xd = (const float *)xq;  // nblk*4 bytes <= cols bytes are readable there
+  if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_SUMS>(st, a, grid, 1);
+  if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_SUMS>(st, a, grid, 1);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                          const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
+                          const float *xd, const int32_t *xbs, float *out) {
+  if (rows == 0 || max_active == 0) return hipSuccess;
+  if (!act_fits(type, cols)) return hipErrorInvalidValue;
+  MvArgs a{};
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.out = out;
+  a.tier = tier;
+  a.rt = rt;
+  a.regime = regime;
+  a.rows_per_block = kRowsPerBlock;
+  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)max_active);
+  // A single token routes at most one row to each expert: the NT=1 kernel.
+  const int nt = s_rows == 1 ? 1 : 3;
+  if (type == T_Q4_K)
+    return mode == 0 ? dispatch_lpr_nt<T_Q4_K, M_GATE_UP>(st, a, grid, nt)
+                     : dispatch_lpr_nt<T_Q4_K, M_DOWN>(st, a, grid, nt);
+  if (type == T_Q8_0)
+    return mode == 0 ? dispatch_lpr_nt<T_Q8_0, M_GATE_UP>(st, a, grid, nt)
+                     : dispatch_lpr_nt<T_Q8_0, M_DOWN>(st, a, grid, nt);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace kmoe

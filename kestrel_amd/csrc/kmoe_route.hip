@@ -1,0 +1,365 @@
+// kmoe_route.hip — router logits, softmax/top-k, dispatch, slot quantization
+// and the combine of Transformer::moe_ffn (transformer.rs:472-570).
+//
+// Router logits must be bit-identical to the reference's for the routing
+// indices to be, so each logit is summed in the exact order quant::matmul
+// (quant.rs:229) uses for an F32 [E, d] router at this s_rows:
+//   s_rows < 4 (or d % 8 != 0): quant::dot (quant.rs:208-224): eight chains
+//     acc_l += w*x (multiply, then add) over elements 8c+l, summed
+//     acc_0..acc_7 in order, then the tail.
+//   s_rows >= 4: gemm_f32 over 48-row tiles (quant.rs:243-257). In each tile
+//     the first rows/3*3 rows of each group of 4 activation rows use the
+//     3x4 register kernel (avx2.rs:238-273): eight FMA chains over 8c+l and
+//     hsum; the other rows and the last s_rows % 4 activation rows use
+//     dot_f32 (avx2.rs:289-308): two interleaved sets of eight FMA chains,
+//     added lane-wise, hsum, then the tail.
+// hsum (avx2.rs:20-27) = ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)).
+// One lane per chain (16 lanes per logit); lane 0 of the 16 combines them.
+#include "kmoe_device.h"
+#include "kmoe_launch.h"
+
+namespace kmoe {
+
+namespace {
+
+enum { ORD_GEMM = 0, ORD_DOTF32 = 1, ORD_QDOT = 2 };
+
+__device__ __forceinline__ float hsum8(const float *v) {
+  const float a = v[0] + v[4], b = v[2] + v[6], c = v[1] + v[5], d = v[3] + v[7];
+  return (a + b) + (c + d);
+}
+
+__global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__ W, int32_t E, int64_t d,
+                                                       const float *__restrict__ X, int64_t S,
+                                                       float *__restrict__ logits) {
+  const int l16 = threadIdx.x & 15;
+  const int64_t pair = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool valid = pair < S * E;
+  const int64_t s = valid ? pair / E : 0;
+  const int e = valid ? (int)(pair % E) : 0;
+  int ord;
+  if (S < 4 || (d % 8) != 0) {
+    ord = ORD_QDOT;
+  } else {
+    const int64_t s4 = S / 4 * 4;
+    const int r0 = e / 48 * 48;
+    const int trows = (E - r0 < 48 ? E - r0 : 48);
+    const int rows3 = trows / 3 * 3;
+    ord = (s < s4 && (e - r0) < rows3) ? ORD_GEMM : ORD_DOTF32;
+  }
+  const float *w = W + (int64_t)e * d;
+  const float *x = X + s * d;
+  const int64_t n8 = d / 8;
+  float acc = 0.0f;
+  if (valid) {
+    if (ord == ORD_GEMM) {
+      if (l16 < 8) {
+#pragma unroll 8
+        for (int64_t c = 0; c < n8; ++c) acc = fmaf(w[8 * c + l16], x[8 * c + l16], acc);
+      }
+    } else if (ord == ORD_QDOT) {
+      if (l16 < 8) {
+#pragma unroll 8
+        for (int64_t c = 0; c < n8; ++c) {
+          const float p = w[8 * c + l16] * x[8 * c + l16];
+          acc = acc + p;
+        }
+      }
+    } else {
+      const int64_t n16 = d / 16;
+      const int l = l16 & 7;
+      const int64_t off = l16 < 8 ? 0 : 8;
+#pragma unroll 8
+      for (int64_t c = 0; c < n16; ++c) acc = fmaf(w[16 * c + off + l], x[16 * c + off + l], acc);
+      if (l16 < 8 && (d - 16 * n16) >= 8) acc = fmaf(w[16 * n16 + l], x[16 * n16 + l], acc);
+    }
+  }
+  // Gather the 16 chains of this logit in lane 0 of the group.
+  float v[16];
+  const int base = threadIdx.x & 63 & ~15;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = __shfl(acc, base + i);
+  if (!valid || l16 != 0) return;
+  float r;
+  if (ord == ORD_GEMM) {
+    r = hsum8(v);
+  } else if (ord == ORD_DOTF32) {
+    float u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = v[i] + v[i + 8];
+    r = hsum8(u);
+    for (int64_t c = d / 8 * 8; c < d; ++c) {
+      const float p = w[c] * x[c];
+      r = r + p;
+    }
+  } else {
+    r = -0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r = r + v[i];
+    for (int64_t c = n8 * 8; c < d; ++c) {
+      const float p = w[c] * x[c];
+      r = r + p;
+    }
+  }
+  logits[s * E + e] = r;
+}
+
+// One wave per token: softmax, top-k, renormalisation (transformer.rs:479-495).
+constexpr int kMaxExperts = 512;
+
+__global__ void __launch_bounds__(256) k_route_topk(const float *__restrict__ logits, int64_t S, int32_t E, int32_t k,
+                                                    int32_t norm_topk, float weights_scale, uint32_t *__restrict__ idx,
+                                                    float *__restrict__ wout) {
+  __shared__ float P[4][kMaxExperts];
+  __shared__ int taken[4][kMaxExperts];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t s = (int64_t)blockIdx.x * 4 + wave;
+  const bool valid = s < S;  // no early return: the block barriers below stay uniform
+  const float *row = logits + (valid ? s : 0) * E;
+  float m = -INFINITY;
+  for (int e = lane; e < E; e += 64) m = fmaxf(m, row[e]);
+  m = group_max<64>(m);
+  for (int e = lane; e < E; e += 64) {
+    P[wave][e] = expf_cr(row[e] - m);
+    taken[wave][e] = 0;
+  }
+  __syncthreads();
+  float sum = 0.0f;
+  if (lane == 0) {
+    sum = -0.0f;
+    for (int e = 0; e < E; ++e) sum = sum + P[wave][e];
+  }
+  sum = __shfl(sum, 0);
+  for (int e = lane; e < E; e += 64) P[wave][e] = P[wave][e] / sum;
+  __syncthreads();
+  float wsel[16];
+  uint32_t isel[16];
+  for (int j = 0; j < k; ++j) {
+    // Largest p, ties to the lower index: key = (bits(p) << 32) | ~index.
+    uint64_t best = 0;
+    for (int e = lane; e < E; e += 64) {
+      if (taken[wave][e]) continue;
+      const uint64_t key = ((uint64_t)__float_as_uint(P[wave][e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+      best = key > best ? key : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t hi = __shfl_xor((unsigned)(best >> 32), off), lo = __shfl_xor((unsigned)best, off);
+      const uint64_t o = ((uint64_t)hi << 32) | lo;
+      best = o > best ? o : best;
+    }
+    const uint32_t e = 0xffffffffu - (uint32_t)best;
+    if (lane == 0) taken[wave][e] = 1;
+    isel[j] = e;
+    wsel[j] = P[wave][e];
+    __syncthreads();
+  }
+  if (lane != 0 || !valid) return;
+  if (norm_topk) {
+    float ss = -0.0f;
+    for (int j = 0; j < k; ++j) ss = ss + wsel[j];
+    ss = fmaxf(ss, 6.103515625e-05f);
+    for (int j = 0; j < k; ++j) wsel[j] = wsel[j] / ss;
+  }
+  if (weights_scale != 0.0f && weights_scale != 1.0f)
+    for (int j = 0; j < k; ++j) wsel[j] = wsel[j] * weights_scale;
+  for (int j = 0; j < k; ++j) {
+    idx[s * k + j] = isel[j];
+    wout[s * k + j] = wsel[j];
+  }
+}
+
+// Stable counting sort of n flat (token, slot) entries by expert id, in one
+// work-group of 1024 threads. Per chunk of 1024 entries, each wave finds the
+// lanes that share its expert with log2(E) ballots, ranks within the wave by
+// popcount, and a per-expert prefix over the 16 waves (plus a running base
+// from earlier chunks) gives every entry its rank among its expert's entries
+// in flat order — the order BTreeMap<expert, Vec<(token, w)>> fills in.
+__global__ void __launch_bounds__(1024) k_dispatch(const uint32_t *__restrict__ idx, int64_t n, int32_t E,
+                                                   uint32_t *__restrict__ perm, uint32_t *__restrict__ offsets,
+                                                   uint32_t *__restrict__ inv, int32_t *__restrict__ n_active,
+                                                   int32_t *__restrict__ active, uint32_t *__restrict__ rank) {
+  __shared__ uint32_t hist[16][kMaxExperts];
+  __shared__ uint32_t base[kMaxExperts];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  for (int e = tid; e < E; e += 1024) base[e] = 0;
+  for (int w = 0; w < 16; ++w)
+    for (int e = tid; e < E; e += 1024) hist[w][e] = 0;
+  __syncthreads();
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
+    const int64_t i = c0 + tid;
+    const uint32_t ev = i < n ? idx[i] : 0u;
+    const bool valid = i < n && ev < (uint32_t)E;  // ids >= E are dropped, never indexed
+    const uint32_t e = valid ? ev : 0u;
+    uint64_t same = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1u;
+      const uint64_t m = __ballot(valid && bit);
+      same &= bit ? m : ~m;
+    }
+    const uint32_t wrank = (uint32_t)__popcll(same & lt);
+    if (valid && wrank == 0) hist[wave][e] = (uint32_t)__popcll(same);
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += 1024) {
+      uint32_t run = base[ee];
+      for (int w = 0; w < 16; ++w) {
+        const uint32_t c = hist[w][ee];
+        hist[w][ee] = run;
+        run += c;
+      }
+      base[ee] = run;
+    }
+    __syncthreads();
+    if (valid) rank[i] = hist[wave][e] + wrank;
+    __syncthreads();
+    for (int w = 0; w < 16; ++w)
+      for (int ee = tid; ee < E; ee += 1024) hist[w][ee] = 0;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    uint32_t run = 0;
+    int na = 0;
+    for (int ee = 0; ee < E; ++ee) {
+      offsets[ee] = run;
+      if (base[ee] > 0 && active) active[na++] = ee;
+      run += base[ee];
+      base[ee] = offsets[ee];
+    }
+    offsets[E] = run;
+    if (n_active) *n_active = na;
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += 1024) {
+    if (idx[i] >= (uint32_t)E) continue;
+    const uint32_t p = base[idx[i]] + rank[i];
+    perm[p] = (uint32_t)i;
+    if (inv) inv[i] = p;
+  }
+}
+
+__device__ __forceinline__ bool slot_is_int(const Routing &rt, const uint32_t *idx_flat, int64_t p, int regime) {
+  if (regime == REGIME_INT8) return true;
+  if (regime == REGIME_EXACT) return false;
+  const uint32_t e = idx_flat[rt.perm[p]];
+  return rt.offsets[e + 1] - rt.offsets[e] < 4;
+}
+
+__global__ void __launch_bounds__(256) k_quant_slots_q8k(const float *__restrict__ h, int64_t n_slots, int64_t cols,
+                                                         Routing rt, const uint32_t *__restrict__ idx_flat, int regime,
+                                                         int8_t *__restrict__ q, float *__restrict__ d,
+                                                         int32_t *__restrict__ bs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = cols / 256;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= n_slots * nb) return;
+  const int64_t p = blk / nb;
+  if (!slot_is_int(rt, idx_flat, p, regime)) return;
+  wave_quant_q8k_block(h + blk * 256, q + blk * 256, d + blk, bs + blk * 16, lane);
+}
+
+__global__ void __launch_bounds__(256) k_quant_slots_q8(const float *__restrict__ h, int64_t n_slots, int64_t cols,
+                                                        Routing rt, const uint32_t *__restrict__ idx_flat, int regime,
+                                                        int8_t *__restrict__ q, float *__restrict__ d,
+                                                        int32_t *__restrict__ s16) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = cols / 32;
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+  if (blk >= n_slots * nb) return;
+  const int64_t p = blk / nb;
+  if (!slot_is_int(rt, idx_flat, p, regime)) return;
+  group8_quant_q8_block(h + blk * 32, q + blk * 32, d + blk, s16 + blk * 2, lane & 7);
+}
+
+// out[s, c] = sum over the token's slots in ascending expert id of w * y[slot, c]
+// (multiply, then add; transformer.rs:566-570).
+__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ y, Routing rt, int64_t S, int64_t d,
+                                                 float *__restrict__ out) {
+  const int64_t s = blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s >= S || c >= d) return;
+  const int k = rt.topk;
+  uint32_t p[16];
+  float w[16];
+  for (int j = 0; j < k; ++j) {
+    p[j] = rt.inv[s * k + j];
+    w[j] = rt.wsel[s * k + j];
+  }
+  for (int j = 1; j < k; ++j) {  // ascending slot position == ascending expert id
+    const uint32_t pj = p[j];
+    const float wj = w[j];
+    int i = j - 1;
+    while (i >= 0 && p[i] > pj) {
+      p[i + 1] = p[i];
+      w[i + 1] = w[i];
+      --i;
+    }
+    p[i + 1] = pj;
+    w[i + 1] = wj;
+  }
+  float o = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const float t = w[j] * y[(int64_t)p[j] * d + c];
+    o = o + t;
+  }
+  out[s * d + c] = o;
+}
+
+}  // namespace
+
+hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
+                                int64_t s_rows, float *logits) {
+  const int64_t pairs = s_rows * n_expert;
+  if (pairs == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_router_logits, dim3((unsigned)((pairs + 15) / 16)), dim3(256), 0, st, router, n_expert, d, x,
+                     s_rows, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
+                             int32_t norm_topk, float weights_scale, uint32_t *idx, float *w) {
+  if (s_rows == 0) return hipSuccess;
+  if (n_expert > kMaxExperts || k > 16 || k > n_expert || k <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_route_topk, dim3((unsigned)((s_rows + 3) / 4)), dim3(256), 0, st, logits, s_rows, n_expert, k,
+                     norm_topk, weights_scale, idx, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
+                           uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp) {
+  if (n_expert > kMaxExperts || n_expert <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, idx, n_slots, n_expert, perm, offsets, inv, n_active,
+                     active, rank_tmp);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t n_slots, int64_t cols,
+                              const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
+                              int32_t *sums) {
+  if (n_slots == 0) return hipSuccess;
+  if (type == T_Q4_K) {
+    const int64_t nb = n_slots * (cols / 256);
+    hipLaunchKernelGGL(k_quant_slots_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
+                       idx_flat, regime, q, d, sums);
+  } else if (type == T_Q8_0) {
+    const int64_t nb = n_slots * (cols / 32);
+    const int64_t waves = (nb + 7) / 8;
+    hipLaunchKernelGGL(k_quant_slots_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
+                       idx_flat, regime, q, d, sums);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out) {
+  if (s_rows == 0) return hipSuccess;
+  if (rt.topk > 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)((d + 255) / 256), (unsigned)s_rows), dim3(256), 0, st, y, rt, s_rows,
+                     d, out);
+  return hipGetLastError();
+}
+
+}  // namespace kmoe

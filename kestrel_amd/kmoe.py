@@ -1,0 +1,298 @@
+"""ctypes binding of libkmoe.so (include/kmoe.h) with torch tensors as device buffers.
+
+The library is the product: if it is missing this module raises on import of
+the binding; there is no CPU fallback. PyTorch only provides device memory and
+the stream the calls are ordered on.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkmoe.so")
+
+F32, Q8_0, Q4_K = 0, 8, 12
+REGIME_AVX2, REGIME_INT8, REGIME_EXACT = 0, 1, 2
+BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144)}
+
+STATUS = {0: "OK", -1: "INVALID", -2: "UNSUPPORTED", -3: "BUDGET", -4: "HIP", -5: "NOT_LOADED"}
+
+# Every symbol include/kmoe.h declares, with (restype, argtypes).
+_P, _i32, _i64, _u32, _u64, _sz, _f = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float
+SIGNATURES = {
+    "kmoe_create": (C.c_int, [C.c_int, C.POINTER(_P)]),
+    "kmoe_destroy": (C.c_int, [_P]),
+    "kmoe_last_error": (C.c_char_p, [_P]),
+    "kmoe_abi_version": (C.c_int, []),
+    "kmoe_set_stream": (C.c_int, [_P, _P]),
+    "kmoe_get_stream": (_P, [_P]),
+    "kmoe_synchronize": (C.c_int, [_P]),
+    "kmoe_set_regime": (C.c_int, [_P, C.c_int]),
+    "kmoe_get_regime": (C.c_int, [_P]),
+    "kmoe_vram_set_limit": (C.c_int, [_P, _u64]),
+    "kmoe_vram_usage": (C.c_int, [_P, C.POINTER(_u64), C.POINTER(_u64)]),
+    "kmoe_device_alloc": (C.c_int, [_P, _sz, C.POINTER(_P)]),
+    "kmoe_device_free": (C.c_int, [_P, _P]),
+    "kmoe_copy_h2d": (C.c_int, [_P, _P, _P, _sz]),
+    "kmoe_copy_d2h": (C.c_int, [_P, _P, _P, _sz]),
+    "kmoe_matmul": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _i64, _P]),
+    "kmoe_quantize_q8k": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _P]),
+    "kmoe_quantize_q8": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _P]),
+    "kmoe_q4k_block_sums": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _i64, _P, _P]),
+    "kmoe_q8_0_block_sums": (C.c_int, [_P, _P, _i64, _i64, _P, _i64, _P]),
+    "kmoe_matvec_q8": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _P, _P, _i64, _P]),
+    "kmoe_route": (C.c_int, [_P, _P, _i32, _i64, _P, _i64, _i32, _i32, _f, _P, _P, _P]),
+    "kmoe_dispatch": (C.c_int, [_P, _P, _i64, _i32, _i32, _P, _P]),
+    "kmoe_layer_create": (C.c_int, [_P, _u32, _P]),
+    "kmoe_layer_destroy": (C.c_int, [_P, _u32]),
+    "kmoe_router_upload": (C.c_int, [_P, _u32, _P, _sz]),
+    "kmoe_expert_upload": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
+    "kmoe_expert_upload_dev": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
+    "kmoe_expert_is_ready": (C.c_int, [_P, _u32, _u32]),
+    "kmoe_expert_part": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_P), C.POINTER(_sz)]),
+    "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
+    "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
+    "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
+    "kmoe_profile_enable": (C.c_int, [_P, C.c_int]),
+    "kmoe_profile_read": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(_i64)]),
+}
+
+
+class MoeDesc(C.Structure):
+    """kmoe_moe_desc (include/kmoe.h)."""
+
+    _fields_ = [
+        ("n_expert", _u32),
+        ("n_expert_used", _u32),
+        ("norm_topk", _i32),
+        ("weights_scale", _f),
+        ("n_embd", _i64),
+        ("n_ff", _i64),
+        ("gate_type", _i32),
+        ("up_type", _i32),
+        ("down_type", _i32),
+    ]
+
+
+class KmoeError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"kmoe {STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libkmoe.so; raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing: run `python -m kestrel_amd.build` (or __graft_entry__.build())")
+        L = C.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def bytes_for(t: int, n: int) -> int:
+    bs, ts = BLOCK[t]
+    if n % bs:
+        raise ValueError(f"{n} not a multiple of block size {bs}")
+    return n // bs * ts
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+class Context:
+    """One device and one stream (torch's current stream unless `stream` is given)."""
+
+    def __init__(self, device: int = 0, stream=None):
+        import torch
+
+        self.torch = torch
+        self.lib = load_library()
+        self.device = device
+        h = _P()
+        rc = self.lib.kmoe_create(device, C.byref(h))
+        if rc != 0:
+            raise KmoeError(rc, "kmoe_create failed")
+        self.h = h
+        s = stream if stream is not None else torch.cuda.current_stream(device)
+        self.set_stream(s)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.kmoe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc: int):
+        if rc != 0:
+            raise KmoeError(rc, self.lib.kmoe_last_error(self.h).decode())
+
+    def set_stream(self, stream):
+        self.stream = stream
+        self.check(self.lib.kmoe_set_stream(self.h, stream.cuda_stream))
+
+    def sync(self):
+        self.check(self.lib.kmoe_synchronize(self.h))
+
+    def set_regime(self, regime: int):
+        self.check(self.lib.kmoe_set_regime(self.h, regime))
+
+    def vram_set_limit(self, limit: int):
+        self.check(self.lib.kmoe_vram_set_limit(self.h, limit))
+
+    def vram_usage(self):
+        r, l = _u64(), _u64()
+        self.check(self.lib.kmoe_vram_usage(self.h, C.byref(r), C.byref(l)))
+        return r.value, l.value
+
+    # ------------------------------------------------------------ kernel seam
+    def _empty(self, shape, dtype):
+        return self.torch.empty(shape, dtype=dtype, device=f"cuda:{self.device}")
+
+    def matmul(self, t: int, w, rows: int, cols: int, x):
+        """quant::matmul (quant.rs:229): x [S, cols] f32 -> [S, rows] f32."""
+        x = x.reshape(-1, cols)
+        out = self._empty((x.shape[0], rows), self.torch.float32)
+        self.check(self.lib.kmoe_matmul(self.h, t, _ptr(w), w.numel() * w.element_size(), rows, cols, _ptr(x),
+                                        x.shape[0], _ptr(out)))
+        return out
+
+    def quantize_q8k(self, x):
+        S, n = x.shape
+        q = self._empty((S, n), self.torch.int8)
+        d = self._empty((S, n // 256), self.torch.float32)
+        bs = self._empty((S, n // 16), self.torch.int32)
+        self.check(self.lib.kmoe_quantize_q8k(self.h, _ptr(x), S, n, _ptr(q), _ptr(d), _ptr(bs)))
+        return q, d, bs
+
+    def quantize_q8(self, x):
+        S, n = x.shape
+        q = self._empty((S, n), self.torch.int8)
+        d = self._empty((S, n // 32), self.torch.float32)
+        s16 = self._empty((S, n // 16), self.torch.int32)
+        self.check(self.lib.kmoe_quantize_q8(self.h, _ptr(x), S, n, _ptr(q), _ptr(d), _ptr(s16)))
+        return q, d, s16
+
+    def matvec_q8(self, t, w, rows, cols, q, d, bs):
+        S = q.shape[0]
+        out = self._empty((S, rows), self.torch.float32)
+        self.check(self.lib.kmoe_matvec_q8(self.h, t, _ptr(w), w.numel(), rows, cols, _ptr(q), _ptr(d), _ptr(bs), S,
+                                           _ptr(out)))
+        return out
+
+    def q4k_block_sums(self, w, rows, cols, q, bs):
+        S = q.shape[0]
+        nb = cols // 256
+        sumi = self._empty((S, rows, nb), self.torch.int32)
+        mins = self._empty((S, rows, nb), self.torch.int32)
+        self.check(self.lib.kmoe_q4k_block_sums(self.h, _ptr(w), rows, cols, _ptr(q), _ptr(bs), S, _ptr(sumi),
+                                                _ptr(mins)))
+        return sumi, mins
+
+    def q8_0_block_sums(self, w, rows, cols, q):
+        S = q.shape[0]
+        p = self._empty((S, rows, cols // 32), self.torch.int32)
+        self.check(self.lib.kmoe_q8_0_block_sums(self.h, _ptr(w), rows, cols, _ptr(q), S, _ptr(p)))
+        return p
+
+    def route(self, router, h, k: int, norm_topk=True, weights_scale=0.0):
+        E, d = router.shape
+        S = h.shape[0]
+        idx = self._empty((S, k), self.torch.int32)
+        w = self._empty((S, k), self.torch.float32)
+        logits = self._empty((S, E), self.torch.float32)
+        self.check(self.lib.kmoe_route(self.h, _ptr(router), E, d, _ptr(h), S, k, int(norm_topk), weights_scale,
+                                       _ptr(idx), _ptr(w), _ptr(logits)))
+        return idx, w, logits
+
+    def dispatch(self, idx, n_expert: int):
+        S, k = idx.shape
+        perm = self._empty((S * k,), self.torch.int32)
+        off = self._empty((n_expert + 1,), self.torch.int32)
+        self.check(self.lib.kmoe_dispatch(self.h, _ptr(idx), S, k, n_expert, _ptr(perm), _ptr(off)))
+        return perm, off
+
+    # ------------------------------------------------------------ expert tier
+    def layer_create(self, layer: int, n_expert, n_used, d, ff, gate_type, up_type, down_type, norm_topk=True,
+                     weights_scale=0.0):
+        desc = MoeDesc(n_expert, n_used, int(norm_topk), weights_scale, d, ff, gate_type, up_type, down_type)
+        self.check(self.lib.kmoe_layer_create(self.h, layer, C.byref(desc)))
+
+    def layer_destroy(self, layer: int):
+        self.check(self.lib.kmoe_layer_destroy(self.h, layer))
+
+    def router_upload(self, layer: int, router: np.ndarray):
+        r = np.ascontiguousarray(router, dtype=np.float32)
+        self.check(self.lib.kmoe_router_upload(self.h, layer, r.ctypes.data, r.nbytes))
+
+    def expert_upload(self, layer: int, e: int, part: int, data):
+        if isinstance(data, np.ndarray):
+            b = np.ascontiguousarray(data).view(np.uint8)
+            self.check(self.lib.kmoe_expert_upload(self.h, layer, e, part, b.ctypes.data, b.nbytes))
+        else:  # torch device tensor
+            self.check(self.lib.kmoe_expert_upload_dev(self.h, layer, e, part, _ptr(data),
+                                                       data.numel() * data.element_size()))
+
+    def expert_is_ready(self, layer: int, e: int) -> bool:
+        return self.lib.kmoe_expert_is_ready(self.h, layer, e) == 1
+
+    def expert_part(self, layer: int, e: int, part: int):
+        p, n = _P(), _sz()
+        self.check(self.lib.kmoe_expert_part(self.h, layer, e, part, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def bytes_per_expert(self, layer: int) -> int:
+        v = _u64()
+        self.check(self.lib.kmoe_bytes_per_expert(self.h, layer, C.byref(v)))
+        return v.value
+
+    def moe_ffn(self, layer: int, h, out=None):
+        S, d = h.shape
+        if out is None:
+            out = self._empty((S, d), self.torch.float32)
+        self.check(self.lib.kmoe_moe_ffn(self.h, layer, _ptr(h), S, _ptr(out)))
+        return out
+
+    def last_routing(self, S: int, k: int, n_expert: int):
+        idx = self._empty((S, k), self.torch.int32)
+        w = self._empty((S, k), self.torch.float32)
+        perm = self._empty((S * k,), self.torch.int32)
+        off = self._empty((n_expert + 1,), self.torch.int32)
+        self.check(self.lib.kmoe_moe_last_routing(self.h, _ptr(idx), _ptr(w), _ptr(perm), _ptr(off)))
+        return idx, w, perm, off
+
+    # ------------------------------------------------------------ profiling
+    def profile_enable(self, on: bool = True):
+        self.check(self.lib.kmoe_profile_enable(self.h, int(on)))
+
+    def profile_read(self, kernel: str):
+        ms, n = C.c_double(), _i64()
+        self.check(self.lib.kmoe_profile_read(self.h, kernel.encode(), C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
+
+@dataclass
+class Shape:
+    n_expert: int
+    k: int
+    d: int
+    ff: int
+    wtype: int

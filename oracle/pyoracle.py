@@ -1,0 +1,281 @@
+"""ctypes binding of the CPU oracle (test infrastructure only; see __init__.py)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkmoe_oracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
+REGIME_AVX2, REGIME_INT8, REGIME_EXACT = 0, 1, 2
+
+_P = C.c_void_p
+_i64 = C.c_int64
+_sz = C.c_size_t
+
+
+def build() -> str:
+    """Compile the oracle in place (make); returns the library path."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+class MoeLayer(C.Structure):
+    """orc_moe_layer (kmoe_oracle.h)."""
+
+    _fields_ = [
+        ("n_expert", C.c_int32),
+        ("n_expert_used", C.c_int32),
+        ("norm_topk", C.c_int32),
+        ("weights_scale", C.c_float),
+        ("n_embd", C.c_int64),
+        ("n_ff", C.c_int64),
+        ("gate_type", C.c_int32),
+        ("up_type", C.c_int32),
+        ("down_type", C.c_int32),
+        ("router", _P),
+        ("gate", C.POINTER(_P)),
+        ("up", C.POINTER(_P)),
+        ("down", C.POINTER(_P)),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        sig = {
+            "orc_block_size": (_i64, [C.c_int]),
+            "orc_type_size": (_i64, [C.c_int]),
+            "orc_bytes_for": (_i64, [C.c_int, _i64]),
+            "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "orc_fill_normal": (None, [C.c_uint64, C.c_float, C.c_float, _P, _sz]),
+            "orc_fill_xorshift_bytes": (None, [C.c_uint32, _P, _sz, C.c_uint8]),
+            "orc_quantize_q8_0": (None, [_P, _sz, _P]),
+            "orc_quantize_q4_k": (None, [_P, _sz, _P]),
+            "orc_quantize_rows": (None, [C.c_int, _P, _sz, _sz, _P, C.c_int]),
+            "orc_dequant_row": (C.c_int, [C.c_int, _P, _P, _sz]),
+            "orc_q8row_quantize": (None, [_P, _sz, _P, _P, _P]),
+            "orc_q8krow_quantize": (None, [_P, _sz, _P, _P, _P]),
+            "orc_unpack": (C.c_int, [C.c_int, _P, _sz, _P, _P, _P]),
+            "orc_dot_unpacked_scalar": (C.c_float, [_P, _P, _P, _sz, _P, _P, _P]),
+            "orc_dot_unpacked_avx2": (C.c_float, [_P, _P, _P, _sz, _P, _P, _P]),
+            "orc_dot_q8_0": (C.c_float, [_P, _sz, _P, _P]),
+            "orc_dot_q4_0": (C.c_float, [_P, _sz, _P, _P]),
+            "orc_dot_q4_k": (C.c_float, [_P, _sz, _P, _P, _P]),
+            "orc_dot_q4_k_8k": (C.c_float, [_P, _sz, _P, _P, _P]),
+            "orc_q4k_block_acc": (None, [_P, _sz, _P, _P, _P, _P]),
+            "orc_q4k_block_acc_bruteforce": (None, [_P, _sz, _P, _P, _P, _P]),
+            "orc_q8_0_block_acc": (None, [_P, _sz, _P, _P]),
+            "orc_quant_dot": (C.c_float, [_P, _P, _sz]),
+            "orc_dot_f32": (C.c_float, [_P, _P, _sz]),
+            "orc_gemm_f32": (None, [_P, _sz, _P, _sz, _sz, _P]),
+            "orc_matmul": (C.c_int, [C.c_int, _P, _sz, _sz, _sz, _P, _sz, _P, C.c_int, C.c_int]),
+            "orc_route": (C.c_int, [C.POINTER(MoeLayer), _P, _sz, _P, _P, C.c_int, C.c_int]),
+            "orc_route_from_logits": (None, [_P, _sz, C.c_int, C.c_int, C.c_int, C.c_float, _P, _P]),
+            "orc_dispatch": (None, [_P, _sz, C.c_int, C.c_int, _P, _P]),
+            "orc_moe_ffn": (C.c_int, [C.POINTER(MoeLayer), _P, _sz, _P, C.c_int, C.c_int]),
+            "orc_bench_gemv": (C.c_double, [C.c_int, _sz, _sz, _sz, C.c_int]),
+            "orc_hw_threads": (C.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_P)
+
+
+# ---------------------------------------------------------------- geometry
+def block_size(t: int) -> int:
+    return lib().orc_block_size(t)
+
+
+def type_size(t: int) -> int:
+    return lib().orc_type_size(t)
+
+
+def bytes_for(t: int, n: int):
+    v = lib().orc_bytes_for(t, n)
+    return None if v < 0 else v
+
+
+# ---------------------------------------------------------------- generators
+def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_fill_normal(seed, mean, std, _p(out), n)
+    return out
+
+
+def xorshift_bytes(seed: int, n: int, mask: int = 0xFF) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint8)
+    lib().orc_fill_xorshift_bytes(seed, _p(out), n, mask)
+    return out
+
+
+def f16_bits(v: float) -> int:
+    return lib().orc_f32_to_f16(v)
+
+
+# ---------------------------------------------------------------- quantizers
+def quantize(t: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    """Quantize a [rows, cols] f32 matrix into GGUF row bytes of type t."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape if x.ndim == 2 else (1, x.shape[0])
+    rb = bytes_for(t, cols)
+    out = np.empty(rows * rb, dtype=np.uint8)
+    lib().orc_quantize_rows(t, _p(x), rows, cols, _p(out), threads)
+    return out
+
+
+def dequant(t: int, w: np.ndarray, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    rc = lib().orc_dequant_row(t, _p(np.ascontiguousarray(w, dtype=np.uint8)), _p(out), n)
+    assert rc == 0
+    return out
+
+
+def q8k_quantize(x: np.ndarray):
+    """Q8KRow::quantize per row of x [S, n] -> (q int8 [S,n], d f32 [S,n/256], bsums i32 [S,n/16])."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    S, n = x.shape
+    q = np.empty((S, n), np.int8)
+    d = np.empty((S, n // 256), np.float32)
+    bs = np.empty((S, n // 16), np.int32)
+    for s in range(S):
+        lib().orc_q8krow_quantize(_p(x[s]), n, _p(q[s]), _p(d[s]), _p(bs[s]))
+    return q, d, bs
+
+
+def q8_quantize(x: np.ndarray):
+    """Q8Row::quantize per row -> (q int8 [S,n], d f32 [S,n/32], s16 i32 [S,n/16])."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    S, n = x.shape
+    q = np.empty((S, n), np.int8)
+    d = np.empty((S, n // 32), np.float32)
+    s16 = np.empty((S, n // 16), np.int32)
+    for s in range(S):
+        lib().orc_q8row_quantize(_p(x[s]), n, _p(q[s]), _p(d[s]), _p(s16[s]))
+    return q, d, s16
+
+
+def unpack(t: int, w: np.ndarray, n: int):
+    q = np.empty(n, np.int8)
+    sc = np.empty(n // 16, np.float32)
+    mn = np.empty(n // 16, np.float32)
+    rc = lib().orc_unpack(t, _p(np.ascontiguousarray(w, dtype=np.uint8)), n, _p(q), _p(sc), _p(mn))
+    assert rc == 0
+    return q, sc, mn
+
+
+def q4k_block_acc(w_row: np.ndarray, n: int, q: np.ndarray, bsums: np.ndarray):
+    nb = n // 256
+    sumi = np.empty(nb, np.int32)
+    mins = np.empty(nb, np.int32)
+    lib().orc_q4k_block_acc(_p(w_row), n, _p(q), _p(bsums), _p(sumi), _p(mins))
+    return sumi, mins
+
+
+def q4k_block_acc_bruteforce(w_row: np.ndarray, n: int, q: np.ndarray, bsums: np.ndarray):
+    nb = n // 256
+    sumi = np.empty(nb, np.int64)
+    mins = np.empty(nb, np.int64)
+    lib().orc_q4k_block_acc_bruteforce(_p(w_row), n, _p(q), _p(bsums), _p(sumi), _p(mins))
+    return sumi, mins
+
+
+def q8_0_block_acc(w_row: np.ndarray, n: int, q: np.ndarray):
+    p = np.empty(n // 32, np.int32)
+    lib().orc_q8_0_block_acc(_p(w_row), n, _p(q), _p(p))
+    return p
+
+
+# ---------------------------------------------------------------- matmul / MoE
+def matmul(t: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, regime: int = REGIME_AVX2,
+           threads: int = 0) -> np.ndarray:
+    """quant::matmul (quant.rs:229): x [S, cols] f32 -> out [S, rows] f32."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    S = x.shape[0]
+    out = np.empty((S, rows), np.float32)
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    rc = lib().orc_matmul(t, _p(w), w.nbytes, rows, cols, _p(x), S, _p(out), regime, threads)
+    if rc != 0:
+        raise ValueError(f"orc_matmul failed rc={rc}")
+    return out
+
+
+class Layer:
+    """Owns the numpy buffers behind an orc_moe_layer."""
+
+    def __init__(self, n_expert, n_used, d, ff, gate_type, up_type, down_type, router, gate, up, down,
+                 norm_topk=True, weights_scale=0.0):
+        self.router = np.ascontiguousarray(router, dtype=np.float32)
+        self.gate = [np.ascontiguousarray(g, dtype=np.uint8) for g in gate]
+        self.up = [np.ascontiguousarray(g, dtype=np.uint8) for g in up]
+        self.down = [np.ascontiguousarray(g, dtype=np.uint8) for g in down]
+        arr = _P * n_expert
+        self._gp = arr(*[g.ctypes.data for g in self.gate])
+        self._up = arr(*[g.ctypes.data for g in self.up])
+        self._dp = arr(*[g.ctypes.data for g in self.down])
+        self.c = MoeLayer(n_expert, n_used, int(norm_topk), weights_scale, d, ff, gate_type, up_type, down_type,
+                          self.router.ctypes.data, self._gp, self._up, self._dp)
+        self.n_expert, self.k, self.d, self.ff = n_expert, n_used, d, ff
+
+    def route(self, h: np.ndarray, regime: int = REGIME_AVX2, threads: int = 0):
+        h = np.ascontiguousarray(np.atleast_2d(h), dtype=np.float32)
+        S = h.shape[0]
+        idx = np.empty((S, self.k), np.uint32)
+        w = np.empty((S, self.k), np.float32)
+        rc = lib().orc_route(C.byref(self.c), _p(h), S, _p(idx), _p(w), regime, threads)
+        assert rc == 0
+        return idx, w
+
+    def moe_ffn(self, h: np.ndarray, regime: int = REGIME_AVX2, threads: int = 0) -> np.ndarray:
+        h = np.ascontiguousarray(np.atleast_2d(h), dtype=np.float32)
+        S = h.shape[0]
+        out = np.empty((S, self.d), np.float32)
+        rc = lib().orc_moe_ffn(C.byref(self.c), _p(h), S, _p(out), regime, threads)
+        if rc != 0:
+            raise ValueError(f"orc_moe_ffn failed rc={rc}")
+        return out
+
+
+def route_from_logits(logits: np.ndarray, k: int, norm_topk=True, weights_scale=0.0):
+    logits = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
+    S, E = logits.shape
+    idx = np.empty((S, k), np.uint32)
+    w = np.empty((S, k), np.float32)
+    lib().orc_route_from_logits(_p(logits), S, E, k, int(norm_topk), weights_scale, _p(idx), _p(w))
+    return idx, w
+
+
+def dispatch(idx: np.ndarray, n_expert: int):
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    S, k = idx.shape
+    perm = np.empty(S * k, np.uint32)
+    offsets = np.empty(n_expert + 1, np.uint32)
+    lib().orc_dispatch(_p(idx), S, k, n_expert, _p(perm), _p(offsets))
+    return perm, offsets
+
+
+def bench_gemv(t: int, rows: int, cols: int, iters: int, threads: int = 0) -> float:
+    return lib().orc_bench_gemv(t, rows, cols, iters, threads)
+
+
+def hw_threads() -> int:
+    return lib().orc_hw_threads()

@@ -1,0 +1,91 @@
+"""Shared input builders for the parity tests (seeded; identical bytes go to
+the oracle and to the GPU)."""
+from __future__ import annotations
+
+import numpy as np
+
+F32, Q8_0, Q4_K = 0, 8, 12
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144)}
+
+
+def row_bytes(t: int, cols: int) -> int:
+    bs, ts = BLOCK[t]
+    return cols // bs * ts
+
+
+def f16_bytes(v: float) -> np.ndarray:
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def random_blocks(t: int, rows: int, cols: int, seed: int, d: float | None = None,
+                  dmin: float | None = None) -> np.ndarray:
+    """Well-formed blocks of random bytes with f16 scales overwritten, the way
+    the reference's kernel tests build them (avx2.rs:198-208, qdot.rs:275-299).
+    Defaults give weights of std ~0.02 (Q4_K: dmin = 7.5 d centres them)."""
+    rng = np.random.default_rng(seed)
+    bs, ts = BLOCK[t]
+    nb = rows * cols // bs
+    raw = rng.integers(0, 256, size=(nb, ts), dtype=np.uint8)
+    if t == Q4_K:
+        d = 1.4e-4 if d is None else d
+        dmin = 7.5 * d if dmin is None else dmin
+        raw[:, 0:2] = f16_bytes(d)
+        raw[:, 2:4] = f16_bytes(dmin)
+    else:
+        d = 0.02 / 74.0 if d is None else d
+        raw[:, 0:2] = f16_bytes(d)
+    return raw.reshape(-1)
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+class LayerSpec:
+    """One MoE layer's host-side tensors (GGUF bytes per expert, f32 router)."""
+
+    def __init__(self, n_expert, k, d, ff, wtype, seed=0, quantized=True, norm_topk=True, weights_scale=0.0,
+                 down_type=None, zipf=None):
+        from oracle import pyoracle as orc
+
+        self.n_expert, self.k, self.d, self.ff = n_expert, k, d, ff
+        self.gate_type = self.up_type = wtype
+        self.down_type = wtype if down_type is None else down_type
+        self.norm_topk, self.weights_scale = norm_topk, weights_scale
+        s = seed * 7919
+        self.router = orc.normal(s + 1, n_expert * d, 0.0, 0.02).reshape(n_expert, d)
+        if zipf is not None:
+            # Zipf(s) load imbalance through the unchanged routing function: a
+            # rank-1 term along the all-ones direction of the router rows; with
+            # activations offset by +1 it adds log(zipf weight) to the logits.
+            rng = np.random.default_rng(seed + 17)
+            rank = rng.permutation(n_expert) + 1
+            bias = -zipf * np.log(rank.astype(np.float64))
+            self.router = (self.router + (bias / d)[:, None]).astype(np.float32)
+
+        def mk(sd, t, r, c):
+            if quantized:
+                return orc.quantize(t, orc.normal(sd, r * c, 0.0, 0.02).reshape(r, c))
+            return random_blocks(t, r, c, sd)
+
+        self.gate = [mk(s + 100 + e, self.gate_type, ff, d) for e in range(n_expert)]
+        self.up = [mk(s + 200 + e, self.up_type, ff, d) for e in range(n_expert)]
+        self.down = [mk(s + 300 + e, self.down_type, d, ff) for e in range(n_expert)]
+
+    def oracle_layer(self):
+        from oracle import pyoracle as orc
+
+        return orc.Layer(self.n_expert, self.k, self.d, self.ff, self.gate_type, self.up_type, self.down_type,
+                         self.router, self.gate, self.up, self.down, self.norm_topk, self.weights_scale)
+
+    def upload(self, ctx, layer: int = 0):
+        ctx.layer_create(layer, self.n_expert, self.k, self.d, self.ff, self.gate_type, self.up_type,
+                         self.down_type, self.norm_topk, self.weights_scale)
+        ctx.router_upload(layer, self.router)
+        for e in range(self.n_expert):
+            ctx.expert_upload(layer, e, 0, self.gate[e])
+            ctx.expert_upload(layer, e, 1, self.up[e])
+            ctx.expert_upload(layer, e, 2, self.down[e])

@@ -1,0 +1,172 @@
+"""Kernel-level parity of the HIP path against the oracle, through the C ABI.
+
+Bar: bit-exact for integers (quantized activations, per-block integer
+accumulators, routing indices, dispatch permutation); fp32 results within
+1e-3 relative L2 of the oracle (the reference's AVX2 arithmetic).
+"""
+import numpy as np
+import pytest
+
+from tests.helpers import Q4_K, Q8_0, F32, random_blocks, rel_l2, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # fp32 relative L2 bound from the parity contract
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+
+    from kestrel_amd.kmoe import Context
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    c = Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (3, 4096), (7, 14336), (2, 2048), (5, 768)])
+def test_quantize_q8k_bit_exact(ctx, orc, rows, cols):
+    x = orc.normal(rows * 31 + cols, rows * cols).reshape(rows, cols) * np.float32(3.0)
+    x[0, :256] = 0.0  # zero block: scale 0, inv 0, q 0
+    if cols >= 512:
+        x[0, 300] = np.float32(1e30)  # huge value; the rest of the block quantizes to 0
+    q, d, bs = ctx.quantize_q8k(dev(x))
+    rq, rd, rbs = orc.q8k_quantize(x)
+    assert np.array_equal(host(q), rq)
+    assert np.array_equal(host(d).view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(host(bs), rbs)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (3, 1024), (2, 512), (4, 96)])
+def test_quantize_q8_bit_exact(ctx, orc, rows, cols):
+    x = orc.normal(rows * 17 + cols, rows * cols).reshape(rows, cols)
+    x[-1, :32] = 0.0
+    q, d, s16 = ctx.quantize_q8(dev(x))
+    rq, rd, rs = orc.q8_quantize(x)
+    assert np.array_equal(host(q), rq)
+    assert np.array_equal(host(d).view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(host(s16), rs)
+
+
+@pytest.mark.parametrize("rows,cols,S", [(64, 4096, 1), (37, 14336, 2), (16, 2048, 3), (9, 768, 1), (130, 4096, 3)])
+def test_q4k_block_sums_bit_exact(ctx, orc, rows, cols, S):
+    w = random_blocks(Q4_K, rows, cols, seed=rows + cols)
+    w[:: 144 * 5 + 7] = 0xFF  # every scale/min/nibble pattern, including the 6-bit high bits
+    x = orc.normal(cols + S, S * cols).reshape(S, cols)
+    q, d, bs = orc.q8k_quantize(x)
+    sumi, mins = ctx.q4k_block_sums(dev(w), rows, cols, dev(q), dev(bs))
+    sumi, mins = host(sumi), host(mins)
+    rb = row_bytes(Q4_K, cols)
+    for s in range(S):
+        for r in range(rows):
+            es, em = orc.q4k_block_acc(w[r * rb:(r + 1) * rb], cols, q[s], bs[s])
+            assert np.array_equal(sumi[s, r], es), (s, r)
+            assert np.array_equal(mins[s, r], em), (s, r)
+
+
+@pytest.mark.parametrize("rows,cols,S", [(40, 1024, 1), (33, 512, 3)])
+def test_q8_0_block_sums_bit_exact(ctx, orc, rows, cols, S):
+    w = random_blocks(Q8_0, rows, cols, seed=rows * 3 + cols)  # raw bytes include -128
+    x = orc.normal(cols + 5 * S, S * cols).reshape(S, cols)
+    q, d, s16 = orc.q8_quantize(x)
+    p = host(ctx.q8_0_block_sums(dev(w), rows, cols, dev(q)))
+    rb = row_bytes(Q8_0, cols)
+    for s in range(S):
+        for r in range(rows):
+            assert np.array_equal(p[s, r], orc.q8_0_block_acc(w[r * rb:(r + 1) * rb], cols, q[s])), (s, r)
+
+
+@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 14336, 4096), (Q4_K, 4096, 14336),
+                                         (Q8_0, 512, 1024), (Q8_0, 1024, 512)])
+def test_matvec_decode_matches_oracle(ctx, orc, t, rows, cols):
+    """Dense quantized matvec at decode batch 1 (the C2 shapes for Q4_K)."""
+    w = random_blocks(t, rows, cols, seed=rows ^ cols)
+    x = orc.normal(rows + cols, cols).reshape(1, cols)
+    out = host(ctx.matmul(t, dev(w), rows, cols, dev(x)))
+    ref = orc.matmul(t, w, rows, cols, x)
+    assert rel_l2(out, ref) < TOL, rel_l2(out, ref)
+    # and on the oracle's own Q8_K/Q8 bytes: same integers -> fp32 within a few ulp
+    qf = orc.q8k_quantize if t == Q4_K else orc.q8_quantize
+    q, d, s = qf(x)
+    out2 = host(ctx.matvec_q8(t, dev(w), rows, cols, dev(q), dev(d), dev(s)))
+    assert rel_l2(out2, ref) < 1e-5
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q8_0])
+@pytest.mark.parametrize("S", [1, 2, 3, 4, 5, 8, 17])
+@pytest.mark.parametrize("regime", [0, 1, 2])
+def test_matmul_regimes_match_oracle(ctx, orc, t, S, regime):
+    rows, cols = (192, 1024) if t == Q4_K else (160, 512)
+    w = orc.quantize(t, orc.normal(S * 13 + t, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    x = orc.normal(S * 101 + regime, S * cols).reshape(S, cols)
+    ctx.set_regime(regime)
+    try:
+        out = host(ctx.matmul(t, dev(w), rows, cols, dev(x)))
+    finally:
+        ctx.set_regime(0)
+    ref = orc.matmul(t, w, rows, cols, x, regime)
+    assert rel_l2(out, ref) < TOL, (S, regime, rel_l2(out, ref))
+
+
+@pytest.mark.parametrize("E,d,S", [(8, 4096, 1), (8, 4096, 3), (8, 4096, 4), (8, 1024, 16), (128, 2048, 1),
+                                   (128, 2048, 7), (64, 2048, 9), (50, 1024, 6), (8, 1000, 5), (8, 1000, 2),
+                                   (8, 1004, 5), (8, 1004, 1)])
+def test_router_logits_bit_exact(ctx, orc, E, d, S):
+    """F32 router matmul in the reference's summation order for this S."""
+    wr = orc.normal(E * d, E * d, 0.0, 0.02).reshape(E, d)
+    h = orc.normal(S * 7 + E, S * d).reshape(S, d)
+    out = host(ctx.matmul(F32, dev(wr), E, d, dev(h)))
+    ref = orc.matmul(F32, wr.view(np.uint8), E, d, h)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("E,k,d,S,norm,scale", [(8, 2, 4096, 1, True, 0.0), (8, 2, 1024, 16, True, 0.0),
+                                                (128, 8, 2048, 33, True, 0.0), (64, 6, 2048, 5, False, 2.5),
+                                                (60, 4, 1024, 3, True, 1.0)])
+def test_route_matches_oracle(ctx, orc, E, k, d, S, norm, scale):
+    wr = orc.normal(E + d, E * d, 0.0, 0.02).reshape(E, d)
+    h = orc.normal(S + d, S * d).reshape(S, d)
+    idx, w, logits = ctx.route(dev(wr), dev(h), k, norm, scale)
+    from oracle.pyoracle import Layer
+
+    L = Layer(E, k, d, 256, Q4_K, Q4_K, Q4_K, wr, [np.zeros(1, np.uint8)] * E, [np.zeros(1, np.uint8)] * E,
+              [np.zeros(1, np.uint8)] * E, norm, scale)
+    ridx, rw = L.route(h)
+    assert np.array_equal(host(idx).astype(np.uint32), ridx)
+    # p = expf(v - m): the device uses a correctly rounded expf, glibc's is
+    # within 0.502 ulp, so weights agree to a few ulp.
+    assert np.allclose(host(w), rw, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("S,k,E", [(1, 2, 8), (16, 2, 8), (7, 6, 64), (512, 2, 8), (700, 8, 128), (2048, 8, 128),
+                                   (3, 1, 1), (100, 4, 512)])
+def test_dispatch_bit_exact(ctx, orc, S, k, E):
+    rng = np.random.default_rng(S * 31 + E)
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(S)]).astype(np.uint32)
+    perm, off = ctx.dispatch(dev(idx.view(np.int32)), E)
+    rp, ro = orc.dispatch(idx, E)
+    assert np.array_equal(host(perm).view(np.uint32), rp)
+    assert np.array_equal(host(off).view(np.uint32), ro)
+
+
+def test_dispatch_all_to_one_expert(ctx, orc):
+    idx = np.zeros((3000, 1), np.uint32)
+    perm, off = ctx.dispatch(dev(idx.view(np.int32)), 4)
+    assert np.array_equal(host(perm).view(np.uint32), np.arange(3000, dtype=np.uint32))
+    assert host(off).tolist() == [0, 3000, 3000, 3000, 3000]

@@ -1,0 +1,166 @@
+"""Layer-level parity: kmoe_moe_ffn (Transformer::moe_ffn, transformer.rs:513-570)
+against the oracle, and the HBM expert tier's API behaviour."""
+import numpy as np
+import pytest
+
+from tests.helpers import Q4_K, Q8_0, LayerSpec, random_blocks, rel_l2, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+
+    from kestrel_amd.kmoe import Context
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    c = Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+_layer_id = [100]
+
+
+def run_layer(ctx, orc, spec: LayerSpec, S: int, regime: int, seed: int, h=None):
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    try:
+        if h is None:
+            h = orc.normal(seed, S * spec.d).reshape(S, spec.d)
+        ctx.set_regime(regime)
+        out = host(ctx.moe_ffn(lid, dev(h)))
+        idx, w, perm, off = (host(t) for t in ctx.last_routing(S, spec.k, spec.n_expert))
+    finally:
+        ctx.set_regime(0)
+        ctx.layer_destroy(lid)
+    L = spec.oracle_layer()
+    ridx, rw = L.route(h, regime)
+    rperm, roff = orc.dispatch(ridx, spec.n_expert)
+    ref = L.moe_ffn(h, regime)
+    return dict(out=out, ref=ref, idx=idx.view(np.uint32), ridx=ridx, w=w, rw=rw, perm=perm.view(np.uint32),
+                rperm=rperm, off=off.view(np.uint32), roff=roff)
+
+
+def check(r, tol=TOL):
+    assert np.array_equal(r["idx"], r["ridx"]), "routing indices differ"
+    assert np.allclose(r["w"], r["rw"], rtol=1e-6, atol=0), "routing weights differ"
+    assert np.array_equal(r["perm"], r["rperm"]), "dispatch permutation differs"
+    assert np.array_equal(r["off"], r["roff"]), "dispatch offsets differ"
+    e = rel_l2(r["out"], r["ref"])
+    assert e < tol, f"rel L2 {e:.3e}"
+    return e
+
+
+@pytest.mark.parametrize("regime", [0, 1, 2])
+def test_c1_q8_0_moe_16_tokens(ctx, orc, regime):
+    """Config 1: hidden 1024, FFN 512, 8 experts, top-2, Q8_0 from N(0, 0.02),
+    16 tokens N(0, 1), seed 0. Under the AVX2 regime experts with >= 4 rows
+    take the f32 path and the rest the int8 path, as on the reference host."""
+    spec = LayerSpec(8, 2, 1024, 512, Q8_0, seed=0)
+    check(run_layer(ctx, orc, spec, 16, regime, seed=0))
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 5, 8, 32])
+def test_q4k_moe_small_all_regimes(ctx, orc, S):
+    spec = LayerSpec(8, 2, 1024, 768, Q4_K, seed=S)
+    for regime in (0, 1, 2):
+        check(run_layer(ctx, orc, spec, S, regime, seed=1000 + S))
+
+
+def test_qwen3_like_zipf_routing(ctx, orc):
+    """Config 4 geometry (hidden 2048, FFN 768, 128 experts, top-8, Q4_K) with
+    Zipf(1.1) load imbalance; activations offset by +1 carry the bias."""
+    spec = LayerSpec(128, 8, 2048, 768, Q4_K, seed=4, quantized=False, zipf=1.1)
+    for S, regime in [(1, 0), (16, 0), (64, 1)]:
+        h = orc.normal(40 + S, S * 2048, 1.0, 1.0).reshape(S, 2048)
+        r = check(run_layer(ctx, orc, spec, S, regime, seed=0, h=h))
+        assert r < TOL
+
+
+def test_mixtral_shape_decode_b1(ctx, orc):
+    """Config 3 at decode batch 1: hidden 4096, FFN 14336, 8 experts, top-2,
+    Q4_K random blocks (793 MB of experts), router N(0, 0.02)."""
+    spec = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=3, quantized=False)
+    check(run_layer(ctx, orc, spec, 1, 0, seed=11))
+
+
+def test_norm_topk_off_and_weights_scale(ctx, orc):
+    spec = LayerSpec(16, 4, 1024, 512, Q8_0, seed=9, norm_topk=False, weights_scale=2.5)
+    check(run_layer(ctx, orc, spec, 6, 0, seed=3))
+
+
+# ----------------------------------------------------------------- expert tier
+def test_expert_tier_serves_correct_slices(ctx):
+    """memory/src/expert.rs:731-751: every expert slice holds l*1000 + e*10 + k;
+    the tier must hand back exactly those bytes for (layer, expert, part)."""
+    import ctypes
+
+    d, ff, E = 256, 256, 8
+    for l in range(2):
+        ctx.layer_create(l, E, 2, d, ff, Q8_0, Q8_0, Q8_0)
+        assert not ctx.expert_is_ready(l, 0)
+        for e in range(E):
+            for k in range(3):
+                n = row_bytes(Q8_0, d if k < 2 else ff) * (ff if k < 2 else d)
+                v = np.full(n // 4, l * 1000 + e * 10 + k, np.float32)
+                ctx.expert_upload(l, e, k, v.view(np.uint8))
+        for e in range(E):
+            assert ctx.expert_is_ready(l, e)
+            for k in range(3):
+                p, n = ctx.expert_part(l, e, k)
+                buf = np.empty(n // 4, np.float32)
+                ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(p), n))
+                assert np.all(buf == l * 1000 + e * 10 + k)
+        assert ctx.bytes_per_expert(l) == 3 * 256 * 8 * 34
+    ctx.layer_destroy(0)
+    ctx.layer_destroy(1)
+
+
+def test_errors_map_to_status_codes(ctx):
+    from kestrel_amd.kmoe import KmoeError
+
+    import torch
+
+    w = torch.zeros(10, dtype=torch.uint8, device="cuda")
+    x = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
+    with pytest.raises(KmoeError) as e:  # weight buffer smaller than rows x row_bytes (quant.rs:233-234)
+        ctx.matmul(Q4_K, w, 4, 256, x)
+    assert e.value.status == -1
+    with pytest.raises(KmoeError) as e:  # type without a kernel
+        ctx.matmul(14, w, 4, 256, x)
+    assert e.value.status == -2
+    with pytest.raises(KmoeError) as e:  # layer never created
+        ctx.moe_ffn(77, x)
+    assert e.value.status == -5
+    ctx.layer_create(78, 8, 2, 256, 256, Q4_K, Q4_K, Q4_K)
+    with pytest.raises(KmoeError) as e:  # experts not resident
+        ctx.moe_ffn(78, x)
+    assert e.value.status == -5
+    ctx.layer_destroy(78)
+    reserved, limit = ctx.vram_usage()
+    ctx.vram_set_limit(reserved + 1024)
+    try:
+        with pytest.raises(KmoeError) as e:  # Tier::Vram budget (ledger.rs:75-102)
+            ctx.layer_create(79, 8, 2, 4096, 14336, Q4_K, Q4_K, Q4_K)
+        assert e.value.status == -3
+    finally:
+        ctx.vram_set_limit(0)

@@ -1,0 +1,317 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Each test replays one of the reference's own unit tests (same generators,
+same sizes, same tolerances; file:line cited), or checks the oracle against
+something the mathematics fixes: brute-force integer sums, float64 dequantized
+products, a stable sort, an argsort of the logits. None of them retypes the
+oracle's formula.
+"""
+import numpy as np
+import pytest
+
+from oracle.pyoracle import F32, Q4_0, Q4_K, Q6_K, Q8_0, REGIME_AVX2, REGIME_EXACT, REGIME_INT8
+
+
+def _blocks(orc, t, n, seed, scale):
+    """qdot.rs:275-299 / avx2.rs:198-208: xorshift32 bytes, f16 scales overwritten."""
+    w = orc.xorshift_bytes(seed, orc.bytes_for(t, n)).copy()
+    bs = orc.type_size(t)
+    offs = {Q8_0: [0], Q4_0: [0], Q4_K: [0, 2], Q6_K: [208]}[t]
+    h = orc.f16_bits(scale)
+    blk = w.reshape(-1, bs)
+    for o in offs:
+        blk[:, o] = h & 0xFF
+        blk[:, o + 1] = h >> 8
+    return w
+
+
+def test_q8_0_and_q4_0_known_values(orc):
+    # quant.rs:375-394
+    b = np.zeros(34, np.uint8)
+    h = orc.f16_bits(0.5)
+    b[0], b[1] = h & 0xFF, h >> 8
+    b[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    y = orc.dequant(Q8_0, b, 32)
+    assert y[0] == -8.0 and y[31] == 7.5
+    b = np.zeros(18, np.uint8)
+    h = orc.f16_bits(2.0)
+    b[0], b[1] = h & 0xFF, h >> 8
+    b[2] = 0x9F
+    y = orc.dequant(Q4_0, b, 32)
+    assert y[0] == 14.0 and y[16] == 2.0 and y[1] == -16.0
+
+
+def test_known_bpw(orc):
+    # kestrel-gguf types.rs:300-307
+    for t, bpw in [(Q4_0, 4.5), (Q8_0, 8.5), (Q4_K, 4.5), (Q6_K, 6.5625)]:
+        assert orc.type_size(t) * 8 / orc.block_size(t) == bpw
+    assert orc.bytes_for(Q4_K, 512) == 288
+    assert orc.bytes_for(Q4_K, 100) is None
+    # Row bytes of the shapes this build runs (types.rs:184-191).
+    assert orc.bytes_for(Q4_K, 4096) == 2304 and orc.bytes_for(Q4_K, 14336) == 8064
+    assert orc.bytes_for(Q8_0, 1024) == 1088 and orc.bytes_for(Q8_0, 512) == 544
+
+
+def test_f16_conversion_is_exact(orc):
+    # half 2.7.1 to_f32 is the IEEE conversion: check every finite f16 against numpy.
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    lib = orc.lib()
+    got = np.array([lib.orc_f16_to_f32(int(b)) for b in bits[::97]], np.float32)
+    r = ref[::97]
+    fin = np.isfinite(r)
+    assert np.array_equal(got[fin].view(np.uint32), r[fin].view(np.uint32))
+    # f32 -> f16 round-to-nearest-even agrees with numpy on random values.
+    v = orc.normal(5, 4000, 0.0, 3.0) * np.float32(10.0) ** orc.normal(6, 4000, 0.0, 2.0).clip(-6, 3.5)
+    mine = np.array([orc.f16_bits(float(x)) for x in v], np.uint16)
+    assert np.array_equal(mine, v.astype(np.float16).view(np.uint16))
+
+
+def test_matmul_matches_naive(orc):
+    # quant.rs:397-411 (F32, S=3 < 4: dequant + quant::dot)
+    rows, cols, s = 37, 64, 3
+    i = np.arange(rows * cols)
+    wf = (((i * 31) % 17).astype(np.float32) - 8.0) * np.float32(0.1)
+    x = ((np.arange(s * cols) % 5).astype(np.float32) - 2.0)
+    out = orc.matmul(F32, wf.view(np.uint8), rows, cols, x.reshape(s, cols))
+    e = x.reshape(s, cols).astype(np.float64) @ wf.reshape(rows, cols).astype(np.float64).T
+    assert np.abs(out - e).max() < 1e-3
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K])
+def test_unpack_matches_dequantization_exactly(orc, t):
+    # qdot.rs:301-315
+    n = 1024
+    w = _blocks(orc, t, n, 7, 0.01)
+    wf = orc.dequant(t, w, n)
+    q, sc, mn = orc.unpack(t, w, n)
+    i = np.arange(n)
+    v = sc[i // 16] * q.astype(np.float32) - mn[i // 16]
+    assert np.all(np.abs(v - wf) <= 1e-5 * np.maximum(np.abs(wf), 1.0))
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
+def test_dot_close_to_float(orc, t):
+    # qdot.rs:317-333
+    n = 1024
+    i = np.arange(n)
+    x = (((i * 37) % 101).astype(np.float32) - 50.0) / np.float32(25.0)
+    q, d, s16 = orc.q8_quantize(x)
+    w = _blocks(orc, t, n, 3, 0.01)
+    wf = orc.dequant(t, w, n)
+    exact = orc.lib().orc_quant_dot(wf.ctypes.data, x.ctypes.data, n)
+    uq, usc, umn = orc.unpack(t, w, n)
+    fast = orc.lib().orc_dot_unpacked_avx2(uq.ctypes.data, usc.ctypes.data, umn.ctypes.data, n, q.ctypes.data,
+                                           d.ctypes.data, s16.ctypes.data)
+    tol = float(np.abs(wf).sum()) * 2.0 / 127.0 * 0.6
+    assert abs(exact - fast) <= max(tol, 1e-3)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K])
+def test_fused_kernels_match_unpacked_reference(orc, t):
+    # avx2.rs:184-223
+    n = 2048
+    i = np.arange(n)
+    x = (((i * 53) % 211).astype(np.float32) - 105.0) / np.float32(40.0)
+    q, d, s16 = orc.q8_quantize(x)
+    q, d, s16 = q[0], d[0], s16[0]
+    w = _blocks(orc, t, n, 9, 0.02)
+    uq, usc, umn = orc.unpack(t, w, n)
+    r = np.float32(0.0)
+    for k in range(n // 16):  # scalar reference over the unpacked representation
+        p = int(np.dot(uq[16 * k:16 * k + 16].astype(np.int32), q[16 * k:16 * k + 16].astype(np.int32)))
+        r = np.float32(r + d[k // 2] * (usc[k] * np.float32(p) - umn[k] * np.float32(s16[k])))
+    L = orc.lib()
+    f = {Q8_0: lambda: L.orc_dot_q8_0(w.ctypes.data, n, q.ctypes.data, d.ctypes.data),
+         Q4_0: lambda: L.orc_dot_q4_0(w.ctypes.data, n, q.ctypes.data, d.ctypes.data),
+         Q4_K: lambda: L.orc_dot_q4_k(w.ctypes.data, n, q.ctypes.data, d.ctypes.data, s16.ctypes.data)}[t]
+    fused = f()
+    generic = L.orc_dot_unpacked_avx2(uq.ctypes.data, usc.ctypes.data, umn.ctypes.data, n, q.ctypes.data,
+                                      d.ctypes.data, s16.ctypes.data)
+    tol = 1e-4 * max(abs(float(r)), 1.0)
+    assert abs(fused - r) <= tol
+    assert abs(generic - r) <= tol
+
+
+def test_gemm_matches_naive(orc):
+    # avx2.rs:312-330
+    for rows, s_rows, cols in [(7, 9, 64), (3, 4, 8), (1, 1, 24), (10, 3, 256)]:
+        w = (((np.arange(rows * cols) * 7) % 13).astype(np.float32) - 6.0) * np.float32(0.1)
+        x = (((np.arange(s_rows * cols) * 5) % 11).astype(np.float32) - 5.0) * np.float32(0.2)
+        res = np.empty(rows * s_rows, np.float32)
+        orc.lib().orc_gemm_f32(w.ctypes.data, rows, x.ctypes.data, s_rows, cols, res.ctypes.data)
+        e = w.reshape(rows, cols).astype(np.float64) @ x.reshape(s_rows, cols).astype(np.float64).T
+        assert np.abs(res.reshape(rows, s_rows) - e).max() < 1e-3
+
+
+def test_q8k_kernels_match_dequantized_math(orc):
+    # avx2.rs:425-460 (Q4_K)
+    n = 2048
+    i = np.arange(n)
+    x = (((i * 53) % 211).astype(np.float32) - 105.0) / np.float32(40.0)
+    q, d, bs = orc.q8k_quantize(x)
+    w = _blocks(orc, Q4_K, n, 7, 0.02)
+    uq, usc, umn = orc.unpack(Q4_K, w, n)
+    wv = (usc[i // 16] * uq.astype(np.float32) - umn[i // 16]).astype(np.float64)
+    r = float(np.sum(wv * q[0].astype(np.float64) * d[0][i // 256].astype(np.float64)))
+    got = orc.lib().orc_dot_q4_k_8k(w.ctypes.data, n, q.ctypes.data, d.ctypes.data, bs.ctypes.data)
+    assert abs(got - r) <= 1e-3 * max(abs(r), 1.0)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_q4k_block_accumulators_match_bruteforce(orc, seed):
+    n = 4096
+    x = orc.normal(seed, n)
+    q, d, bs = orc.q8k_quantize(x)
+    w = orc.quantize(Q4_K, orc.normal(seed + 100, n, 0.0, 0.02).reshape(1, n))
+    wr = orc.xorshift_bytes(seed, w.size)  # raw bytes: every scale/min/nibble pattern
+    for ww in (w, wr):
+        s, m = orc.q4k_block_acc(ww, n, q[0], bs[0])
+        s2, m2 = orc.q4k_block_acc_bruteforce(ww, n, q[0], bs[0])
+        assert np.array_equal(s.astype(np.int64), s2) and np.array_equal(m.astype(np.int64), m2)
+
+
+def test_q8_0_block_accumulators_match_bruteforce(orc):
+    n = 1024
+    q, d, s16 = orc.q8_quantize(orc.normal(4, n))
+    w = orc.xorshift_bytes(11, orc.bytes_for(Q8_0, n))  # includes -128 weights
+    p = orc.q8_0_block_acc(w, n, q[0])
+    wq = w.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.int64)
+    ref = (wq * q[0].reshape(-1, 32).astype(np.int64)).sum(1)
+    assert np.array_equal(p.astype(np.int64), ref)
+
+
+def test_q8k_quantize_semantics(orc):
+    # qdot.rs:347-367: scale = amax/127, q = round-half-away(x / scale) clamped; bsums per 16.
+    x = orc.normal(9, 1024)
+    x[:256] = 0.0  # zero block -> scale 0, q 0
+    x[300] = 127.5 * 0.01  # exact half cases exercise round-half-away
+    q, d, bs = orc.q8k_quantize(x)
+    assert d[0, 0] == 0.0 and not q[0, :256].any()
+    ax = np.abs(x.reshape(-1, 256)).max(1)
+    assert np.array_equal(d[0], (ax / np.float32(127.0)).astype(np.float32))
+    recon = q[0].astype(np.float64) * np.repeat(d[0], 256)
+    assert np.all(np.abs(recon - x) <= np.repeat(d[0], 256) * 0.5 + 1e-12)
+    assert np.array_equal(bs[0], q[0].reshape(-1, 16).astype(np.int32).sum(1))
+
+
+@pytest.mark.parametrize("t,n", [(Q8_0, 1024), (Q4_K, 4096)])
+def test_quantizers_round_trip(orc, t, n):
+    x = orc.normal(12, n, 0.0, 0.02)
+    w = orc.quantize(t, x.reshape(1, n))
+    y = orc.dequant(t, w, n)
+    if t == Q8_0:  # |x - y| <= d/2 + |q| * (f16 rounding of d), d = amax/127
+        amax = np.abs(x.reshape(-1, 32)).max(1)
+        bound = np.repeat(amax / 127.0, 32) * (0.5 + 127 * 2.0 ** -11) + 1e-7
+    else:  # per sub-block range / 15 / 2 plus the 6-bit rounding of scale and min
+        r = x.reshape(-1, 32)
+        bound = np.repeat((r.max(1) - np.minimum(r.min(1), 0)) / 15.0, 32) * 1.5 + 1e-4
+    assert np.all(np.abs(x - y) <= bound)
+    assert np.sqrt(np.mean((x - y) ** 2)) / np.sqrt(np.mean(x ** 2)) < (0.01 if t == Q8_0 else 0.12)
+
+
+def test_matmul_regimes(orc):
+    """quant.rs:242/262/282: S>=4 is f32-exact; S<4 carries Q8_K activation error."""
+    rows, cols = 64, 1024
+    w = orc.quantize(Q4_K, orc.normal(21, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    wf = np.stack([orc.dequant(Q4_K, w[r * 576:(r + 1) * 576], cols) for r in range(rows)]).astype(np.float64)
+    for S in (1, 3, 4, 7):
+        x = orc.normal(30 + S, S * cols).reshape(S, cols)
+        e = x.astype(np.float64) @ wf.T
+        for regime in (REGIME_AVX2, REGIME_INT8, REGIME_EXACT):
+            out = orc.matmul(Q4_K, w, rows, cols, x, regime)
+            rel = np.linalg.norm(out - e) / np.linalg.norm(e)
+            exact = (regime == REGIME_EXACT) or (regime == REGIME_AVX2 and S >= 4)
+            assert rel < (1e-6 if exact else 2e-2), (S, regime, rel)
+
+
+def test_route_matches_argsort_of_logits(orc):
+    """transformer.rs:472-496 against a float64 softmax + argsort (distinct logits)."""
+    rng = np.random.default_rng(0)
+    for E, k, norm in [(8, 2, True), (128, 8, True), (64, 6, False)]:
+        logits = rng.standard_normal((50, E)).astype(np.float32) * 3
+        idx, w = orc.route_from_logits(logits, k, norm, 0.0)
+        l64 = logits.astype(np.float64)
+        p = np.exp(l64 - l64.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        ref_idx = np.argsort(-l64, axis=1, kind="stable")[:, :k]
+        assert np.array_equal(idx, ref_idx)
+        ref_w = np.take_along_axis(p, ref_idx, 1)
+        if norm:
+            ref_w = ref_w / ref_w.sum(1, keepdims=True)
+        assert np.allclose(w, ref_w, rtol=2e-6, atol=0)
+    # weights_scale multiplies (MoeInfo.weights_scale, 0 or 1 = none)
+    i1, w1 = orc.route_from_logits(logits[:4], 6, False, 2.5)
+    i0, w0 = orc.route_from_logits(logits[:4], 6, False, 1.0)
+    assert np.array_equal(i0, i1) and np.array_equal(w1, (w0 * np.float32(2.5)).astype(np.float32))
+
+
+def test_route_ties_prefer_lower_index(orc):
+    logits = np.zeros((2, 8), np.float32)
+    logits[1, [6, 2, 5]] = 1.0
+    idx, w = orc.route_from_logits(logits, 3, True, 0.0)
+    assert idx[0].tolist() == [0, 1, 2] and idx[1].tolist() == [2, 5, 6]
+    assert np.allclose(w, 1.0 / 3.0)
+
+
+def test_dispatch_is_stable_sort(orc):
+    rng = np.random.default_rng(3)
+    for S, k, E in [(1, 2, 8), (16, 2, 8), (512, 8, 128), (7, 6, 64)]:
+        idx = np.stack([rng.choice(E, k, replace=False) for _ in range(S)]).astype(np.uint32)
+        perm, off = orc.dispatch(idx, E)
+        assert np.array_equal(perm, np.argsort(idx.reshape(-1), kind="stable"))
+        assert np.array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(idx.reshape(-1), minlength=E))]))
+
+
+def _small_layer(orc, t, E=4, k=2, d=256, ff=256, seed=0):
+    rng_seed = seed * 1000
+    router = orc.normal(rng_seed + 1, E * d, 0.0, 0.02).reshape(E, d)
+    mk = lambda s, r, c: orc.quantize(t, orc.normal(s, r * c, 0.0, 0.02).reshape(r, c))
+    gate = [mk(rng_seed + 10 + e, ff, d) for e in range(E)]
+    up = [mk(rng_seed + 20 + e, ff, d) for e in range(E)]
+    down = [mk(rng_seed + 30 + e, d, ff) for e in range(E)]
+    return orc.Layer(E, k, d, ff, t, t, t, router, gate, up, down)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K])
+def test_moe_ffn_matches_float64_layer(orc, t):
+    """transformer.rs:513-570 against a float64 evaluation of the same layer."""
+    L = _small_layer(orc, t)
+    d, ff, E, k = L.d, L.ff, L.n_expert, L.k
+    rb_d, rb_f = orc.bytes_for(t, d), orc.bytes_for(t, ff)
+    deq = lambda w, r, c, rb: np.stack([orc.dequant(t, w[i * rb:(i + 1) * rb], c) for i in range(r)]).astype(np.float64)
+    G = [deq(L.gate[e], ff, d, rb_d) for e in range(E)]
+    U = [deq(L.up[e], ff, d, rb_d) for e in range(E)]
+    D = [deq(L.down[e], d, ff, rb_f) for e in range(E)]
+    for S in (1, 5, 12):
+        h = orc.normal(77 + S, S * d).reshape(S, d)
+        idx, w = L.route(h)
+        ref = np.zeros((S, d))
+        for s in range(S):
+            for j in range(k):
+                e = idx[s, j]
+                g = G[e] @ h[s].astype(np.float64)
+                u = U[e] @ h[s].astype(np.float64)
+                a = g / (1 + np.exp(-g)) * u
+                ref[s] += w[s, j] * (D[e] @ a)
+        for regime in (REGIME_AVX2, REGIME_EXACT, REGIME_INT8):
+            out = L.moe_ffn(h, regime)
+            rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
+            assert rel < (3e-2 if regime == REGIME_INT8 else 2e-2), (S, regime, rel)
+        # AVX2 with S=12: experts with >=4 rows are f32-exact, the rest carry Q8 error.
+        out = L.moe_ffn(h, REGIME_EXACT)
+        assert np.linalg.norm(out - ref) / np.linalg.norm(ref) < 1e-5
+
+
+def test_matmul_thread_count_independent(orc):
+    rows, cols = 200, 512
+    w = orc.quantize(Q4_K, orc.normal(5, rows * cols, 0, 0.02).reshape(rows, cols))
+    x = orc.normal(6, 2 * cols).reshape(2, cols)
+    a = orc.matmul(Q4_K, w, rows, cols, x, threads=1)
+    b = orc.matmul(Q4_K, w, rows, cols, x, threads=0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_bench_gemv_runs(orc):
+    # quant.rs:348-368 (small sizes here; the full metric runs in bench.py)
+    assert orc.bench_gemv(Q4_K, 256, 4096, 2, 1) > 0
