@@ -1,0 +1,260 @@
+"""MoE-layer tokens/s and % of peak HBM bandwidth, Mixtral-shaped Q4_K layer at decode batch 1.
+
+One step = one Transformer::moe_ffn pass (route, dispatch, gate/up + SwiGLU,
+down, combine) over one token, through kmoe_moe_ffn. Workload: hidden 4096,
+expert FFN 14336, 8 experts, top-2, Q4_K random-init experts (random
+well-formed blocks, as kestrel's own synthetic models are built:
+tools/make_synthetic.py:39-58), router fp32 N(0, 0.02), activations N(0, 1).
+
+Steps rotate over NL distinct layers (NL x 793 MB of experts, default 4 =
+3.2 GB) so the 256 MB Infinity Cache cannot serve repeats; every step reads
+its two experts from HBM. Inputs are resident in HBM before timing starts.
+
+Prints one JSON line (contract in the build brief): value = tokens/s of the
+whole job (one GPU), roofline of the dominant kernel (measured live with HIP
+events on the stream it runs on), cpu_baseline = the oracle (C++ restatement
+of kestrel's AVX2 path) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+D, FF, E, K = 4096, 14336, 8, 2
+Q4_K = 12
+ROW_GU = 4096 // 256 * 144   # 2304 B per gate/up row
+ROW_DN = 14336 // 256 * 144  # 8064 B per down row
+PART = FF * ROW_GU           # 33,030,144 B (gate, up and down parts are equal)
+EXPERT_BYTES = 3 * PART      # 99,090,432 B
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (793 MB each)")
+    ap.add_argument("--tokens", type=int, default=1, help="tokens per step (decode batch)")
+    ap.add_argument("--regime", type=int, default=0)
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a replayed HIP graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    return ap.parse_args()
+
+
+def make_layers(ctx, torch, n_layers: int, seed: int = 0):
+    """Random well-formed Q4_K experts generated on the device (f16 d and dmin
+    overwritten so weights have std ~0.02 and zero mean), router N(0, 0.02)."""
+    import numpy as np
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    dh = np.array([1.4e-4], np.float16).view(np.uint8)
+    mh = np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)
+    hdr = torch.tensor(np.concatenate([dh, mh]), dtype=torch.uint8, device="cuda")
+    rng = np.random.default_rng(seed)
+    for l in range(n_layers):
+        ctx.layer_create(l, E, K, D, FF, Q4_K, Q4_K, Q4_K, True, 0.0)
+        ctx.router_upload(l, (rng.standard_normal((E, D)) * 0.02).astype(np.float32))
+        for e in range(E):
+            for p in range(3):
+                t = torch.randint(0, 256, (PART // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
+                t[:, 0:4] = hdr
+                ctx.expert_upload(l, e, p, t)
+                del t
+    torch.cuda.synchronize()
+
+
+def cpu_baseline(ctx, torch, seconds: float, threads: int):
+    """Oracle moe_ffn (C++ restatement of kestrel's AVX2 path, transformer.rs:513)
+    on layer 0's exact bytes, one token per call, for about `seconds`."""
+    import ctypes
+
+    import numpy as np
+
+    from oracle import pyoracle as orc
+
+    parts = [[None] * 3 for _ in range(E)]
+    for e in range(E):
+        for p in range(3):
+            ptr, n = ctx.expert_part(0, e, p)
+            buf = np.empty(n, np.uint8)
+            ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(ptr), n))
+            parts[e][p] = buf
+    rng = np.random.default_rng(0)
+    router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)  # same stream as make_layers' layer 0
+    L = orc.Layer(E, K, D, FF, Q4_K, Q4_K, Q4_K, router, [p[0] for p in parts], [p[1] for p in parts],
+                  [p[2] for p in parts], True, 0.0)
+    hw = orc.hw_threads()
+    nthreads = max(1, min(threads, hw))
+    h = rng.standard_normal((64, D)).astype(np.float32)
+    L.moe_ffn(h[:1], threads=nthreads)  # warm
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        L.moe_ffn(h[n % 64:n % 64 + 1], threads=nthreads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 5000:
+            break
+    gemv = orc.bench_gemv(Q4_K, 2048, 4096, 50, nthreads)  # quant.rs:348-368 metric
+    return {
+        "value": round(n / el, 3),
+        "unit": "tokens/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"{n} single-token moe_ffn calls on layer 0 (Mixtral shape, Q4_K, AVX2 regime), {el:.1f} s; "
+                  f"host has {hw} hardware threads",
+        "gemv_q4k_2048x4096_GBps": round(gemv / 1e9, 3),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: --gpus must be 1 (no collectives are built)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from kestrel_amd.kmoe import Context
+
+    torch.cuda.set_device(0)
+    ctx = Context(0)
+    ctx.set_regime(a.regime)
+    make_layers(ctx, torch, a.layers)
+    S = a.tokens
+    hpool = torch.randn((a.layers, S, D), dtype=torch.float32, device="cuda")
+    outs = torch.empty((a.layers, S, D), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        l = i % a.layers
+        ctx.moe_ffn(l, hpool[l], outs[l])
+
+    # ---- per-kernel timing pass (HIP events on the library's stream)
+    for i in range(a.layers * 2):
+        step(i)
+    torch.cuda.synchronize()
+    ctx.profile_enable(True)
+    nprof = max(a.layers * 10, 40)
+    for i in range(nprof):
+        step(i)
+    torch.cuda.synchronize()
+    names = ["route_decode", "router_logits", "route_topk", "dispatch", "quant_q8k", "moe_gate_up_dec", "moe_gate_up_int",
+             "quant_slots_q8k", "moe_down_dec", "moe_down_int", "moe_gate_f32", "moe_up_f32", "moe_down_f32",
+             "combine"]
+    kern = {}
+    for n in names:
+        ms, cnt = ctx.profile_read(n)
+        if cnt:
+            kern[n] = {"avg_us": round(ms * 1000.0 / cnt, 3), "launches": cnt}
+    ctx.profile_enable(False)
+
+    # ---- graph capture (one graph per layer) or eager
+    graphs = None
+    if not a.no_graph:
+        try:
+            graphs = []
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for l in range(a.layers):
+                    ctx.set_stream(s)
+                    step(l)
+            torch.cuda.current_stream().wait_stream(s)
+            for l in range(a.layers):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    ctx.set_stream(torch.cuda.current_stream())
+                    step(l)
+                graphs.append(g)
+            ctx.set_stream(torch.cuda.current_stream())
+            # replay check against eager
+            ref = torch.empty_like(outs)
+            for l in range(a.layers):
+                step(l)
+            torch.cuda.synchronize()
+            ref.copy_(outs)
+            outs.zero_()
+            for l in range(a.layers):
+                graphs[l].replay()
+            torch.cuda.synchronize()
+            if not torch.equal(ref, outs):
+                bad = [l for l in range(a.layers) if not torch.equal(ref[l], outs[l])]
+                raise RuntimeError(f"graph replay differs from eager on layers {bad}: max |diff| "
+                                   f"{(ref - outs).abs().max().item():.3e}, nan {int(torch.isnan(ref).sum())}/"
+                                   f"{int(torch.isnan(outs).sum())}")
+        except Exception as ex:  # fall back to eager launches, and say so
+            print(f"# graph capture unavailable: {ex}", file=sys.stderr)
+            graphs = None
+            ctx.set_stream(torch.cuda.current_stream())
+
+    def run(i):
+        if graphs is not None:
+            graphs[i % a.layers].replay()
+        else:
+            step(i)
+
+    for i in range(a.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        run(i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el * 1000.0 / a.steps
+    tok_s = S * a.steps / el
+
+    # touched bytes per step: distinct experts of this batch (2 at b=1) + router
+    touched = 2 * EXPERT_BYTES + E * D * 4 if S == 1 else None
+    gu_name = "moe_gate_up_dec" if "moe_gate_up_dec" in kern else "moe_gate_up_int"
+    gu = kern.get(gu_name)
+    roof = None
+    if gu:
+        # algorithmic bytes of one launch at b=1: gate + up rows of 2 experts,
+        # plus the Q8_K activation row (4096 + 64 + 1024 B) and h out (2 x 14336 x 4 B)
+        alg = 2 * 2 * PART + (4096 + 64 + 1024) + 2 * FF * 4
+        ach = alg / (gu["avg_us"] * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": gu_name, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
+                "alg_bytes_per_launch": alg}
+    res = {
+        "metric": "MoE-layer tokens/sec + % peak HBM GB/s, Mixtral-shape Q4_K decode b=1",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"mixtral-8x7b-moe-layer-q4k-decode-b{S}", "hidden": D, "expert_ffn": FF,
+                   "experts": E, "top_k": K, "tokens_per_step": S, "weights": "Q4_K random-init blocks",
+                   "layers_rotated": a.layers, "regime": ["avx2", "int8", "exact"][a.regime],
+                   "launch": "hip-graph" if graphs is not None else "eager"},
+        "hbm_touched_GBps": round(touched / (ms_step * 1e-3) / 1e9, 1) if touched else None,
+        "hbm_frac": round(touched / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if touched else None,
+        "roofline": roof,
+        "kernels_us": kern,
+        "cpu_baseline": None,
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
+    print(json.dumps(res))
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

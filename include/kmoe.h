@@ -74,9 +74,12 @@ int kmoe_destroy(kmoe_ctx *ctx);
 /* Message of the last failed call on ctx ("" if none). Valid until the next call. */
 const char *kmoe_last_error(const kmoe_ctx *ctx);
 int kmoe_abi_version(void);
-/* Use an external hipStream_t (e.g. the caller's) instead of the context's own.
- * NULL restores the context's stream. */
+/* Run on the caller's hipStream_t instead of the context's own stream. The
+ * handle is used as given: NULL is HIP's default (null) stream, which is
+ * where PyTorch's default stream lives. */
 int kmoe_set_stream(kmoe_ctx *ctx, void *hip_stream);
+/* Go back to the context's own (non-blocking) stream. */
+int kmoe_use_own_stream(kmoe_ctx *ctx);
 void *kmoe_get_stream(kmoe_ctx *ctx);
 int kmoe_synchronize(kmoe_ctx *ctx);
 int kmoe_set_regime(kmoe_ctx *ctx, int regime);

@@ -268,6 +268,20 @@ bool int_path(int regime, int64_t s_rows) {
   return regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2 && s_rows < 4);
 }
 
+// int8-activation matvec: one activation row -> register-resident decode
+// kernel; otherwise (or if the row is too wide for it) the LDS-staged kernel.
+int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *q, const float *d,
+                   const int32_t *s, int64_t s_rows, float *out) {
+  const char *name = t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q8_0";
+  if (s_rows == 1) {
+    hipError_t e = timed(c, name, [&]() { return launch_decode_plain(c->stream, t, w, rows, cols, q, d, s, out); });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
+  LAUNCH(c, name, launch_matvec_int(c->stream, t, w, rows, cols, q, d, s, s_rows, out));
+  return KMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -313,7 +327,12 @@ const char *kmoe_last_error(const kmoe_ctx *c) { return c ? c->err.c_str() : "nu
 
 int kmoe_set_stream(kmoe_ctx *c, void *s) {
   if (!c) return KMOE_E_INVALID;
-  c->stream = s ? (hipStream_t)s : c->own;
+  c->stream = (hipStream_t)s;  // NULL is the null stream, not "our own"
+  return KMOE_OK;
+}
+int kmoe_use_own_stream(kmoe_ctx *c) {
+  if (!c) return KMOE_E_INVALID;
+  c->stream = c->own;
   return KMOE_OK;
 }
 void *kmoe_get_stream(kmoe_ctx *c) { return c ? (void *)c->stream : nullptr; }
@@ -426,9 +445,7 @@ int kmoe_matvec_q8(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows
   if (rows == 0 || s_rows == 0) return KMOE_OK;
   if (!w || !q || !d || !out || (t == KMOE_Q4_K && !bs)) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
-  LAUNCH(c, t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q8_0",
-         launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, bs, s_rows, out));
-  return KMOE_OK;
+  return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, q, d, bs, s_rows, out);
 }
 
 int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, const int32_t *bs,
@@ -490,14 +507,9 @@ int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, i
   int8_t *q = cv.take<int8_t>(s_rows * cols);
   float *d = cv.take<float>(s_rows * (cols / 32));
   int32_t *s = cv.take<int32_t>(s_rows * (cols / 16));
-  if (t == KMOE_Q4_K) {
-    LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, q, d, s));
-    LAUNCH(c, "matvec_q4k", launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out));
-  } else {
-    LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, q, d, s));
-    LAUNCH(c, "matvec_q8_0", launch_matvec_int(c->stream, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out));
-  }
-  return KMOE_OK;
+  if (t == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, q, d, s));
+  else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, q, d, s));
+  return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out);
 }
 
 int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const float *h, int64_t S, int32_t k,
@@ -508,6 +520,21 @@ int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const flo
   if (S == 0) return KMOE_OK;
   if (!router || !h || !idx || !w) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
+  if (S < 4) {  // fused decode routing; its dispatch outputs go to scratch
+    const size_t n = (size_t)S * k;
+    int rc = ensure_ws(c, 4 * align_up(n * 4) + 3 * align_up(((size_t)E + 1) * 4));
+    if (rc) return rc;
+    Carver cv{c->ws};
+    uint32_t *perm = cv.take<uint32_t>(n), *inv = cv.take<uint32_t>(n);
+    uint32_t *off = cv.take<uint32_t>(E + 1);
+    int32_t *na = cv.take<int32_t>(1), *act = cv.take<int32_t>(E);
+    hipError_t e = timed(c, "route_decode", [&]() {
+      return launch_route_decode(c->stream, router, E, d, h, (int32_t)S, k, norm_topk, weights_scale, logits, idx, w,
+                                 perm, off, inv, na, act, 0, nullptr, nullptr, nullptr);
+    });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
   float *lg = logits;
   if (!lg) {
     int rc = ensure_ws(c, align_up((size_t)S * E * 4));
@@ -679,12 +706,28 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   const int regime = c->regime;
   hipStream_t st = c->stream;
 
-  // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531)
-  LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
-  LAUNCH(c, "route_topk",
-         launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk, D.weights_scale, w.idx, w.wsel));
-  LAUNCH(c, "dispatch", launch_dispatch(st, w.idx, slots, (int32_t)E, w.perm, w.offsets, w.inv, w.n_active,
-                                        w.active, w.rank));
+  const int gt = D.gate_type, dt = D.down_type;
+  // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531). With
+  // s_rows < 4 one fused work-group also quantizes x for the int8 path.
+  bool x_quantized = false;
+  {
+    const int qtype = regime == KMOE_REGIME_EXACT ? 0 : gt;
+    hipError_t e = timed(c, "route_decode", [&]() {
+      return launch_route_decode(st, L->router, (int32_t)E, d, h, (int32_t)S, (int32_t)k, D.norm_topk,
+                                 D.weights_scale, w.logits, w.idx, w.wsel, w.perm, w.offsets, w.inv, w.n_active,
+                                 w.active, qtype, w.xq, w.xd, w.xs);
+    });
+    if (e == hipSuccess) {
+      x_quantized = qtype != 0;
+    } else {
+      if (e != hipErrorNotSupported) HIP_OK(c, e);
+      LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
+      LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
+                                                D.weights_scale, w.idx, w.wsel));
+      LAUNCH(c, "dispatch", launch_dispatch(st, w.idx, slots, (int32_t)E, w.perm, w.offsets, w.inv, w.n_active,
+                                            w.active, w.rank));
+    }
+  }
   Routing rt{w.n_active, w.active, w.offsets, w.perm, w.inv, w.wsel, (int32_t)k};
   ExpertTier tier{L->arena, (int64_t)L->expert_stride,
                   {(int64_t)L->part_off[0], (int64_t)L->part_off[1], (int64_t)L->part_off[2]}};
@@ -692,12 +735,41 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // Which regimes can occur: an expert has at most S rows.
   const bool any_int = regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2);
   const bool any_f32 = regime == KMOE_REGIME_EXACT || (regime == KMOE_REGIME_AVX2 && S >= 4);
-  const int gt = D.gate_type, dt = D.down_type;
 
+  // Single token, int8 path: every routed expert has one row. gate/up+SwiGLU
+  // and down+combine run as register-resident decode kernels.
+  if (S == 1 && regime != KMOE_REGIME_EXACT) {
+    if (!x_quantized) {
+      if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, 1, d, w.xq, w.xd, w.xs));
+      else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, 1, d, w.xq, w.xd, w.xs));
+      x_quantized = true;
+    }
+    hipError_t e = timed(c, "moe_gate_up_dec", [&]() {
+      return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h);
+    });
+    if (e != hipErrorNotSupported) {
+      HIP_OK(c, e);
+      LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
+             launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
+      e = timed(c, "moe_down_dec",
+                [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out); });
+      if (e != hipErrorNotSupported) {
+        HIP_OK(c, e);
+        goto done;
+      }
+      // down too wide for registers: finish with the general kernels below
+      LAUNCH(c, "moe_down_int",
+             launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
+      LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
+      goto done;
+    }
+  }
   // expert gate/up + SwiGLU (transformer.rs:551-558)
   if (any_int) {
-    if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
-    else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
+    if (!x_quantized) {
+      if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
+      else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
+    }
     LAUNCH(c, "moe_gate_up_int",
            launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
   }
@@ -716,6 +788,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // combine (transformer.rs:566-570)
   LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
 
+done:
   c->last_idx = w.idx;
   c->last_w = w.wsel;
   c->last_perm = w.perm;

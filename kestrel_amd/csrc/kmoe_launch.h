@@ -37,6 +37,18 @@ struct ExpertTier {
 // Plain: out[s*rows + r] for s < s_rows; activations pre-quantized.
 hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                              const float *xd, const int32_t *xbs, int64_t s_rows, float *out);
+// Single activation row (decode, one token): activation slice held in registers.
+// Return hipErrorNotSupported when the row is too wide for that; callers then
+// use the LDS-staged kernels.
+hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out);
+hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                 const Routing &rt, int max_active, const int8_t *xq, const float *xd,
+                                 const int32_t *xbs, float *h);
+// Down projection + combine for one token: out[r] = sum_e (asc) w_e * y_e[r].
+hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                      const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
+                                      float *out);
 // Block sums (debug path of the same device code).
 hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                              const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins);
@@ -61,6 +73,13 @@ hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_e
                                 int64_t s_rows, float *logits);
 hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w);
+// Decode routing (s_rows < 4) in one work-group: quant::dot-order logits, softmax,
+// top-k, dispatch (perm/offsets/inv/active), and int8 quantization of x when
+// qtype is T_Q4_K (Q8_K rows) or T_Q8_0 (Q8 rows). hipErrorNotSupported when out of range.
+hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
+                               int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
+                               float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs);
 // Stable counting sort by expert. inv/n_active/active may be null.
 hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
                            uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp);

@@ -304,6 +304,408 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode kernel for one activation row per expert (single-token decode).
+// Each lane always handles the same task slots t = lr + i*LPR of every row, so
+// its slice of the Q8_K/Q8 activation row (64+16+4 bytes per Q4_K task, 32+4
+// per Q8_0 block) is loaded once into registers and reused for every row: no
+// LDS staging, no per-row activation traffic. Work-groups stride over a flat
+// list of (expert, row-block) tasks, sized so every CU gets the same number.
+// MODE M_GATE_UP: h[slot, r] = SwiGLU(gate_r . x, up_r . x) for each active expert.
+// MODE M_DOWN_COMBINE: out[r] = sum over active experts in ascending id of
+//   w_e * (down_e[r] . q8k(h[slot_e])) — the down projection and the combine
+//   (transformer.rs:566-570) in one pass; valid when all slots belong to one token.
+// MODE M_PLAIN: out[r] = W[r] . x for one activation row.
+enum { M_DOWN_COMBINE = 4 };
+
+template <int TYPE>
+struct ActSlice;
+template <>
+struct ActSlice<T_Q4_K> {
+  int4 x0, x1, x2, x3, bs;
+  float d;
+};
+template <>
+struct ActSlice<T_Q8_0> {
+  int4 x0, x1;
+  float d;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void act_load(ActSlice<TYPE> &s, const int8_t *xq, const float *xd, const int32_t *xbs,
+                                         int t) {
+  if constexpr (TYPE == T_Q4_K) {
+    const int sb = t >> 2, k = t & 3;
+    const int4 *v = (const int4 *)(xq + 256 * sb + 64 * k);
+    s.x0 = v[0];
+    s.x1 = v[1];
+    s.x2 = v[2];
+    s.x3 = v[3];
+    s.bs = *(const int4 *)(xbs + 16 * sb + 4 * k);
+    s.d = xd[sb];
+  } else {
+    const int4 *v = (const int4 *)(xq + 32 * t);
+    s.x0 = v[0];
+    s.x1 = v[1];
+    s.d = xd[t];
+  }
+}
+
+template <int TYPE>
+struct WTask;
+template <>
+struct WTask<T_Q4_K> {
+  Q4kW w;
+};
+template <>
+struct WTask<T_Q8_0> {
+  Q80W w;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void w_load(WTask<TYPE> &w, const uint8_t *row, int t) {
+  if constexpr (TYPE == T_Q4_K) w.w = q4k_load(row, t);
+  else w.w = q80_load(row, t);
+}
+
+// acc += (float) dot of one task against its activation slice.
+template <int TYPE>
+__device__ __forceinline__ float task_dot(const WTask<TYPE> &wt, int t, const ActSlice<TYPE> &s, float acc) {
+  if constexpr (TYPE == T_Q4_K) {
+    const Q4kW &w = wt.w;
+    const int k = t & 3;
+    int sA, mA, sB, mB;
+    q4k_scale_min_pair(w.hdr.y, w.hdr.z, w.hdr.w, k, sA, mA, sB, mB);
+    const uint32_t m = 0x0f0f0f0fu;
+    int lo = 0, hi = 0;
+    lo = sdot4(w.qa.x & m, (uint32_t)s.x0.x, lo);
+    lo = sdot4(w.qa.y & m, (uint32_t)s.x0.y, lo);
+    lo = sdot4(w.qa.z & m, (uint32_t)s.x0.z, lo);
+    lo = sdot4(w.qa.w & m, (uint32_t)s.x0.w, lo);
+    lo = sdot4(w.qb.x & m, (uint32_t)s.x1.x, lo);
+    lo = sdot4(w.qb.y & m, (uint32_t)s.x1.y, lo);
+    lo = sdot4(w.qb.z & m, (uint32_t)s.x1.z, lo);
+    lo = sdot4(w.qb.w & m, (uint32_t)s.x1.w, lo);
+    hi = sdot4((w.qa.x >> 4) & m, (uint32_t)s.x2.x, hi);
+    hi = sdot4((w.qa.y >> 4) & m, (uint32_t)s.x2.y, hi);
+    hi = sdot4((w.qa.z >> 4) & m, (uint32_t)s.x2.z, hi);
+    hi = sdot4((w.qa.w >> 4) & m, (uint32_t)s.x2.w, hi);
+    hi = sdot4((w.qb.x >> 4) & m, (uint32_t)s.x3.x, hi);
+    hi = sdot4((w.qb.y >> 4) & m, (uint32_t)s.x3.y, hi);
+    hi = sdot4((w.qb.z >> 4) & m, (uint32_t)s.x3.z, hi);
+    hi = sdot4((w.qb.w >> 4) & m, (uint32_t)s.x3.w, hi);
+    const int sumi = sA * lo + sB * hi;
+    const int mins = mA * (s.bs.x + s.bs.y) + mB * (s.bs.z + s.bs.w);
+    const float d = f16_bits_to_f32(w.hdr.x), dmin = f16_bits_to_f32(w.hdr.x >> 16);
+    acc = fmaf(d * s.d, (float)sumi, acc);
+    acc = fmaf(-(dmin * s.d), (float)mins, acc);
+    return acc;
+  } else {
+    const Q80W &w = wt.w;
+    const uint32_t v[9] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w, w.c};
+    uint32_t q[8];
+    float dw;
+    if (w.sh == 0) {
+      dw = f16_bits_to_f32(v[0]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+    } else {
+      dw = f16_bits_to_f32(v[0] >> 16);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = v[i + 1];
+    }
+    int p = 0;
+    p = sdot4(q[0], (uint32_t)s.x0.x, p);
+    p = sdot4(q[1], (uint32_t)s.x0.y, p);
+    p = sdot4(q[2], (uint32_t)s.x0.z, p);
+    p = sdot4(q[3], (uint32_t)s.x0.w, p);
+    p = sdot4(q[4], (uint32_t)s.x1.x, p);
+    p = sdot4(q[5], (uint32_t)s.x1.y, p);
+    p = sdot4(q[6], (uint32_t)s.x1.z, p);
+    p = sdot4(q[7], (uint32_t)s.x1.w, p);
+    return fmaf(dw * s.d, (float)p, acc);
+  }
+}
+
+template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
+__global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int RB = 4 * RPW * RU;  // rows per block-task
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row_in_wave = lane / LPR, lr = lane % LPR;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
+  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t xs_stride = cols / 16;
+  const int64_t bpe = (rows + RB - 1) / RB;
+  int64_t total = bpe;
+  if constexpr (MODE == M_GATE_UP) total = (int64_t)(*a.rt.n_active) * bpe;
+
+  ActSlice<TYPE> act[TPLMAX];
+  if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
+#pragma unroll
+    for (int i = 0; i < TPLMAX; ++i) {
+      const int t = lr + i * LPR;
+      if (i < tpl && t < ntasks) act_load<TYPE>(act[i], a.xq, a.xd, a.xbs, t);
+    }
+  }
+
+  for (int64_t b = blockIdx.x; b < total; b += gridDim.x) {
+    int64_t rblk = b;
+    const uint8_t *W0 = a.w0, *W1 = nullptr;
+    int64_t p0 = 0;
+    if constexpr (MODE == M_GATE_UP) {
+      const int i = (int)(b / bpe);
+      rblk = b - (int64_t)i * bpe;
+      const int e = a.rt.active[i];
+      p0 = a.rt.offsets[e];
+      const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
+      W0 = eb + a.tier.off[0];
+      W1 = eb + a.tier.off[1];
+    }
+    const int64_t r0 = rblk * RB + (int64_t)(wave * RU) * RPW + row_in_wave;
+
+    if constexpr (MODE == M_DOWN_COMBINE) {
+      float o[RU];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) o[u] = 0.0f;
+      const int na = *a.rt.n_active;
+      for (int ia = 0; ia < na; ++ia) {  // ascending expert id
+        const int e = a.rt.active[ia];
+        const int64_t p = a.rt.offsets[e];
+        const float wgt = a.rt.wsel[a.rt.perm[p]];
+        const uint8_t *W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[2];
+#pragma unroll
+        for (int i = 0; i < TPLMAX; ++i) {
+          const int t = lr + i * LPR;
+          if (i < tpl && t < ntasks)
+            act_load<TYPE>(act[i], a.xq + p * cols, a.xd + p * nblk, a.xbs + p * xs_stride, t);
+        }
+        float acc[RU];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) acc[u] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TPLMAX; ++i) {
+          const int t = lr + i * LPR;
+          if (i < tpl && t < ntasks) {
+            WTask<TYPE> w[RU];
+#pragma unroll
+            for (int u = 0; u < RU; ++u) {
+              const int64_t r = r0 + (int64_t)u * RPW;
+              if (r < rows) w_load<TYPE>(w[u], W + r * row_bytes, t);
+            }
+#pragma unroll
+            for (int u = 0; u < RU; ++u) {
+              const int64_t r = r0 + (int64_t)u * RPW;
+              if (r < rows) acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          const float y = group_sum<LPR>(acc[u]);
+          const float t = wgt * y;
+          o[u] = o[u] + t;
+        }
+      }
+      if (lr == 0) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          const int64_t r = r0 + (int64_t)u * RPW;
+          if (r < rows) a.out[r] = o[u];
+        }
+      }
+    } else {
+      float acc0[RU], acc1[RU];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) acc0[u] = acc1[u] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TPLMAX; ++i) {
+        const int t = lr + i * LPR;
+        if (i < tpl && t < ntasks) {
+          WTask<TYPE> w0[RU], w1[RU];
+#pragma unroll
+          for (int u = 0; u < RU; ++u) {
+            const int64_t r = r0 + (int64_t)u * RPW;
+            if (r < rows) {
+              w_load<TYPE>(w0[u], W0 + r * row_bytes, t);
+              if constexpr (MODE == M_GATE_UP) w_load<TYPE>(w1[u], W1 + r * row_bytes, t);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < RU; ++u) {
+            const int64_t r = r0 + (int64_t)u * RPW;
+            if (r < rows) {
+              acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u]);
+              if constexpr (MODE == M_GATE_UP) acc1[u] = task_dot<TYPE>(w1[u], t, act[i], acc1[u]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        acc0[u] = group_sum<LPR>(acc0[u]);
+        if constexpr (MODE == M_GATE_UP) acc1[u] = group_sum<LPR>(acc1[u]);
+      }
+      if (lr == 0) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+          const int64_t r = r0 + (int64_t)u * RPW;
+          if (r >= rows) continue;
+          if constexpr (MODE == M_GATE_UP) {  // SwiGLU (transformer.rs:558)
+            const float g = acc0[u];
+            const float den = 1.0f + expf_cr(-g);
+            const float q = g / den;
+            a.out[p0 * rows + r] = q * acc1[u];
+          } else {
+            a.out[r] = acc0[u];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Down projection + combine for one token, persistent and split over K.
+// One work-group per CU owns a contiguous block of RB rows for every routed
+// expert. Its four waves split each row's tasks into four equal ranges, so a
+// lane holds exactly one (TPL) activation slice per expert and every row's
+// weight bytes stream through one CU; per-wave partial sums meet in LDS.
+// y = ((p0 + p1) + p2) + p3, then o = o + w_e * y in ascending expert id.
+constexpr int kSplitRbMax = 64;
+
+template <int TYPE, int RU, int TPL>
+__global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
+  __shared__ float part[4][kSplitRbMax];
+  __shared__ float outv[kSplitRbMax];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
+  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t xs_stride = cols / 16;
+  const int tpw = (ntasks + 3) / 4;  // tasks per wave
+  const int64_t r0 = (int64_t)blockIdx.x * rb_rows;
+  const int nr = (int)(rows - r0 < rb_rows ? rows - r0 : rb_rows);
+  if (nr <= 0) return;
+  if (threadIdx.x < kSplitRbMax) outv[threadIdx.x] = 0.0f;
+  int tk[TPL];
+  bool tv[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    const int lt = lane + 64 * i;
+    tk[i] = wave * tpw + lt;
+    tv[i] = lt < tpw && tk[i] < ntasks;
+  }
+  const int na = *a.rt.n_active;
+  for (int ia = 0; ia < na; ++ia) {  // ascending expert id
+    const int e = a.rt.active[ia];
+    const int64_t p = a.rt.offsets[e];
+    const float wgt = a.rt.wsel[a.rt.perm[p]];
+    const uint8_t *W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[2];
+    ActSlice<TYPE> act[TPL];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i)
+      if (tv[i]) act_load<TYPE>(act[i], a.xq + p * cols, a.xd + p * nblk, a.xbs + p * xs_stride, tk[i]);
+    for (int rr = 0; rr < nr; rr += RU) {
+      WTask<TYPE> w[RU][TPL];
+#pragma unroll
+      for (int u = 0; u < RU; ++u)
+#pragma unroll
+        for (int i = 0; i < TPL; ++i)
+          if (rr + u < nr && tv[i]) w_load<TYPE>(w[u][i], W + (r0 + rr + u) * row_bytes, tk[i]);
+      float acc[RU];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        acc[u] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TPL; ++i)
+          if (rr + u < nr && tv[i]) acc[u] = task_dot<TYPE>(w[u][i], tk[i], act[i], acc[u]);
+        acc[u] = group_sum<64>(acc[u]);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u)
+          if (rr + u < nr) part[wave][rr + u] = acc[u];
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < nr) {
+      const int t = threadIdx.x;
+      const float y = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+      const float c = wgt * y;
+      outv[t] = outv[t] + c;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < nr) a.out[r0 + threadIdx.x] = outv[threadIdx.x];
+}
+
+int g_cu_count = 0;
+int cu_count() {
+  if (g_cu_count == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      g_cu_count = n;
+    else
+      g_cu_count = 256;
+  }
+  return g_cu_count;
+}
+
+// Geometry of the register kernel for a row of `ntasks` tasks: lanes per row
+// and task slots per lane. Returns false when the activation slice would not
+// fit in registers.
+bool reg_geometry(int type, int ntasks, int &lpr, int &tpl) {
+  if (ntasks >= 64) {
+    lpr = 64;
+  } else {
+    lpr = 16;
+    while (lpr < ntasks) lpr *= 2;
+  }
+  tpl = (ntasks + lpr - 1) / lpr;
+  return type == T_Q4_K ? tpl <= 4 : tpl <= 8;
+}
+
+template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
+hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_tasks) {
+  constexpr int RB = 4 * (64 / LPR) * RU;
+  (void)RB;
+  const int64_t cap = (int64_t)cu_count() * 4;
+  int64_t grid = max_tasks;
+  if (grid > cap) {
+    const int64_t per = (max_tasks + cap - 1) / cap;  // equal task counts per work-group
+    grid = (max_tasks + per - 1) / per;
+  }
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
+  return hipGetLastError();
+}
+
+template <int TYPE, int MODE, int RU>
+hipError_t dispatch_reg(hipStream_t st, const MvArgs &a, int n_groups) {
+  const int64_t nblk = TYPE == T_Q4_K ? a.cols / 256 : a.cols / 32;
+  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  int lpr, tpl;
+  if (!reg_geometry(TYPE, ntasks, lpr, tpl)) return hipErrorNotSupported;
+  const int64_t rb = 4 * (64 / lpr) * RU;
+  const int64_t max_tasks = (a.rows + rb - 1) / rb * n_groups;
+  constexpr int TM = TYPE == T_Q4_K ? 4 : 8;
+  switch (lpr) {
+    case 64:
+      if (tpl == 1) return launch_reg<TYPE, 64, 1, RU, MODE>(st, a, tpl, max_tasks);
+      return launch_reg<TYPE, 64, TM, RU, MODE>(st, a, tpl, max_tasks);
+    case 32:
+      return launch_reg<TYPE, 32, 1, RU, MODE>(st, a, tpl, max_tasks);
+    case 16:
+      return launch_reg<TYPE, 16, 1, RU, MODE>(st, a, tpl, max_tasks);
+    default:
+      return hipErrorNotSupported;
+  }
+}
+
 template <int TYPE, int LPR, int NT, int MODE>
 hipError_t launch_one(hipStream_t st, const MvArgs &a, dim3 grid) {
   const ActLayout<TYPE> L(a.cols);
@@ -358,6 +760,75 @@ bool act_fits(int type, int64_t cols) {
 }
 
 }  // namespace
+
+hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out) {
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.s_rows = 1;
+  a.out = out;
+  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
+  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                 const Routing &rt, int max_active, const int8_t *xq, const float *xd,
+                                 const int32_t *xbs, float *h) {
+  MvArgs a{};
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.out = h;
+  a.tier = tier;
+  a.rt = rt;
+  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
+  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                      const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
+                                      float *out) {
+  MvArgs a{};
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = hq;
+  a.xd = hd;
+  a.xbs = hbs;
+  a.out = out;
+  a.tier = tier;
+  a.rt = rt;
+  const int64_t nblk = type == T_Q4_K ? cols / 256 : cols / 32;
+  const int ntasks = type == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  if (ntasks >= 128 && ntasks <= 4 * 64 * 2) {
+    // persistent split-K: one work-group per CU, rows split evenly
+    const int64_t G = cu_count();
+    int rb = (int)((rows + G - 1) / G);
+    if (rb <= kSplitRbMax) {
+      const unsigned grid = (unsigned)((rows + rb - 1) / rb);
+      const int tpl = (ntasks + 3) / 4 > 64 ? 2 : 1;
+      if (type == T_Q4_K) {
+        if (tpl == 1) hipLaunchKernelGGL((k_down_splitk<T_Q4_K, 6, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        else hipLaunchKernelGGL((k_down_splitk<T_Q4_K, 4, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+      } else {
+        if (tpl == 1) hipLaunchKernelGGL((k_down_splitk<T_Q8_0, 8, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        else hipLaunchKernelGGL((k_down_splitk<T_Q8_0, 4, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+      }
+      return hipGetLastError();
+    }
+  }
+  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_DOWN_COMBINE, 1>(st, a, 1);
+  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_DOWN_COMBINE, 1>(st, a, 1);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                              const float *xd, const int32_t *xbs, int64_t s_rows, float *out) {

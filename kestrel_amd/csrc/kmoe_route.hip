@@ -307,6 +307,274 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ y, Ro
   out[s * d + c] = o;
 }
 
+// ---------------------------------------------------------------------------
+// Decode routing in one work-group (s_rows < 4): logits in quant::dot order,
+// softmax, top-k, renormalisation, dispatch, and the int8 quantization of the
+// activation rows, fused.
+//
+// With s_rows < 4 the reference computes each F32 router logit with
+// quant::dot (quant.rs:208-224): eight chains acc_l = sum of p_{8c+l} in
+// order of c, where each product p = w*x is rounded on its own (no FMA). The
+// products do not depend on the chains, so all 1024 threads form them with
+// coalesced float4 loads and write them to LDS transposed per chain; each
+// chain then reads its products four at a time. The chain additions stay in
+// the reference's order, so the logits are bit-identical.
+struct RouteDecArgs {
+  const float *W;
+  int32_t E;
+  int64_t d;
+  const float *X;
+  int32_t S, k, norm_topk;
+  float weights_scale;
+  float *logits;  // [S, E]: written when the logits are split over work-groups (or asked for)
+  uint32_t *idx;
+  float *wsel;
+  uint32_t *perm, *offsets, *inv;
+  int32_t *n_active, *active;
+  int qtype;  // 0: none, T_Q4_K: Q8_K rows, T_Q8_0: Q8 rows
+  int8_t *xq;
+  float *xd;
+  int32_t *xs;
+};
+
+constexpr int kDecEpw = 8;       // experts per work-group
+constexpr int kDecMaxChunks = 16;  // columns per work-group <= 16 chunks of 512
+
+// Softmax, top-k, renormalisation (transformer.rs:479-495) for S tokens whose
+// logits are in lg[s*E + e] (LDS), then the dispatch and the int8 quantization
+// of x. Runs in one work-group of 1024 threads.
+__device__ void route_tail(const RouteDecArgs &a, const float *lg, float *Pn, int *taken, uint32_t *sel_e,
+                           float *sel_w, uint32_t *cnt) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x, nwaves = nthr >> 6;
+  const int E = a.E;
+  if (wave < a.S) {
+    const int s = wave;
+    const float *row = lg + s * E;
+    float *P = Pn + s * E;
+    int *tk = taken + s * E;
+    float m = -INFINITY;
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, row[e]);
+    m = group_max<64>(m);
+    for (int e = lane; e < E; e += 64) {
+      P[e] = expf_cr(row[e] - m);
+      tk[e] = 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float sum = 0.0f;
+    if (lane == 0) {
+      sum = -0.0f;
+      for (int e = 0; e < E; ++e) sum = sum + P[e];
+    }
+    sum = __shfl(sum, 0);
+    for (int e = lane; e < E; e += 64) P[e] = P[e] / sum;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    for (int j = 0; j < a.k; ++j) {
+      uint64_t best = 0;
+      for (int e = lane; e < E; e += 64) {
+        if (tk[e]) continue;
+        const uint64_t key = ((uint64_t)__float_as_uint(P[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+        best = key > best ? key : best;
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t hi = __shfl_xor((unsigned)(best >> 32), off), lo = __shfl_xor((unsigned)best, off);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        best = o > best ? o : best;
+      }
+      const uint32_t e = 0xffffffffu - (uint32_t)best;
+      if (lane == 0) {
+        tk[e] = 1;
+        sel_e[s * a.k + j] = e;
+        sel_w[s * a.k + j] = P[e];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
+    if (lane == 0) {
+      float *w = &sel_w[s * a.k];
+      if (a.norm_topk) {
+        float ss = -0.0f;
+        for (int j = 0; j < a.k; ++j) ss = ss + w[j];
+        ss = fmaxf(ss, 6.103515625e-05f);
+        for (int j = 0; j < a.k; ++j) w[j] = w[j] / ss;
+      }
+      if (a.weights_scale != 0.0f && a.weights_scale != 1.0f)
+        for (int j = 0; j < a.k; ++j) w[j] = w[j] * a.weights_scale;
+      for (int j = 0; j < a.k; ++j) {
+        a.idx[s * a.k + j] = sel_e[s * a.k + j];
+        a.wsel[s * a.k + j] = w[j];
+      }
+    }
+  }
+  // dispatch: stable counting sort of the S*k <= 64 flat slots by expert
+  const int n = a.S * a.k;
+  for (int e = tid; e < E; e += nthr) cnt[e] = 0;
+  __syncthreads();
+  if (tid < n) atomicAdd(&cnt[sel_e[tid]], 1u);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t run = 0;
+    int na = 0;
+    for (int e = 0; e < E; ++e) {
+      const uint32_t c = cnt[e];
+      a.offsets[e] = run;
+      if (c) a.active[na++] = e;
+      cnt[e] = run;
+      run += c;
+    }
+    a.offsets[E] = run;
+    *a.n_active = na;
+  }
+  __syncthreads();
+  if (tid < n) {
+    const uint32_t e = sel_e[tid];
+    uint32_t r = 0;
+    for (int j = 0; j < tid; ++j) r += sel_e[j] == e ? 1u : 0u;  // earlier slots of the same expert
+    const uint32_t p = cnt[e] + r;
+    a.perm[p] = (uint32_t)tid;
+    a.inv[tid] = p;
+  }
+  // int8 activation rows for the int path
+  const int64_t d = a.d;
+  if (a.qtype == T_Q4_K) {
+    const int64_t nb = (int64_t)a.S * (d / 256);
+    for (int64_t b = wave; b < nb; b += nwaves)
+      wave_quant_q8k_block(a.X + b * 256, a.xq + b * 256, a.xd + b, a.xs + b * 16, lane);
+  } else if (a.qtype == T_Q8_0) {
+    const int64_t nb = (int64_t)a.S * (d / 32);
+    for (int64_t b = (int64_t)wave * 8 + (lane >> 3); b < nb; b += (int64_t)nwaves * 8)
+      group8_quant_q8_block(a.X + b * 32, a.xq + b * 32, a.xd + b, a.xs + b * 2, lane & 7);
+  }
+}
+
+// Logits of experts [8g, 8g+8) for the S (< 4) tokens in quant::dot order
+// (quant.rs:208-224): eight chains acc_l = sum over c of p_{8c+l} in order,
+// p = w*x rounded on its own. Each of the 1024 threads loads its share of W
+// and x for every 512-column chunk at once (one memory latency) and forms
+// the products in registers; chunk by chunk they are transposed into LDS so
+// each chain reads its products four at a time. With a single work-group the
+// tail (top-k, dispatch, quantization) follows in the same kernel.
+template <int NCH>
+__global__ void __launch_bounds__(512) k_route_decode(RouteDecArgs a) {
+  constexpr int KC = 512;    // columns per chunk
+  constexpr int L = KC / 8;  // chain steps per chunk
+  constexpr int CS = L + 4;  // padded chain row (spreads LDS banks)
+  __shared__ __attribute__((aligned(16))) float P[2][kDecEpw * 8 * CS];
+  __shared__ float lg[3 * kMaxExperts];
+  __shared__ float Pn[3 * kMaxExperts];
+  __shared__ int taken[3 * kMaxExperts];
+  __shared__ uint32_t sel_e[64];
+  __shared__ float sel_w[64];
+  __shared__ uint32_t cnt[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int E = a.E;
+  const int64_t d = a.d;
+  const int64_t n8 = d / 8;  // chain length
+  const int e0 = blockIdx.x * kDecEpw;
+  const int ne = E - e0 < kDecEpw ? E - e0 : kDecEpw;
+  const int nchain = ne * 8;
+  const int nch = (int)((n8 * 8 + KC - 1) / KC);
+  const bool vec = (d % 4) == 0;
+  // This thread's 8 products per chunk: expert e0 + te, columns 8c..8c+7 of
+  // the chunk, i.e. step c of each of the expert's eight chains.
+  const int te = tid >> 6, c = tid & 63;
+
+  for (int s = 0; s < a.S; ++s) {
+    const float *x = a.X + (int64_t)s * d;
+    float4 pa[NCH], pb[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      pa[j] = pb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int64_t col = (int64_t)j * KC + 8 * c;
+      if (j < nch && te < ne && col < n8 * 8) {
+        const float *w = a.W + (int64_t)(e0 + te) * d;
+        if (vec) {
+          const float4 w0 = *(const float4 *)(w + col), w1 = *(const float4 *)(w + col + 4);
+          const float4 x0 = *(const float4 *)(x + col), x1 = *(const float4 *)(x + col + 4);
+          pa[j] = make_float4(w0.x * x0.x, w0.y * x0.y, w0.z * x0.z, w0.w * x0.w);
+          pb[j] = make_float4(w1.x * x1.x, w1.y * x1.y, w1.z * x1.z, w1.w * x1.w);
+        } else {
+          float t[8];
+#pragma unroll
+          for (int m = 0; m < 8; ++m) t[m] = w[col + m] * x[col + m];
+          pa[j] = make_float4(t[0], t[1], t[2], t[3]);
+          pb[j] = make_float4(t[4], t[5], t[6], t[7]);
+        }
+      }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j < nch) {
+        float *B = P[j & 1];
+        float *dst = B + (te * 8) * CS + c;
+        dst[0 * CS] = pa[j].x;
+        dst[1 * CS] = pa[j].y;
+        dst[2 * CS] = pa[j].z;
+        dst[3 * CS] = pa[j].w;
+        dst[4 * CS] = pb[j].x;
+        dst[5 * CS] = pb[j].y;
+        dst[6 * CS] = pb[j].z;
+        dst[7 * CS] = pb[j].w;
+        __syncthreads();
+        if (tid < nchain) {
+          const float *row = &B[tid * CS];
+          const int64_t left = n8 - (int64_t)j * L;
+          const int steps = left < L ? (int)left : L;
+          if (steps == L) {
+#pragma unroll 4
+            for (int i = 0; i < L; i += 4) {
+              const float4 v = *(const float4 *)(row + i);
+              acc = acc + v.x;
+              acc = acc + v.y;
+              acc = acc + v.z;
+              acc = acc + v.w;
+            }
+          } else {
+            for (int i = 0; i < steps; ++i) acc = acc + row[i];
+          }
+        }
+      }
+    }
+    // Sum each expert's eight chains in order, then the tail (quant.rs:219-222).
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __shfl(acc, (lane & ~7) + i);
+    if (tid < nchain && (tid & 7) == 0) {
+      const int e = e0 + (tid >> 3);
+      float r = -0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r = r + v[i];
+      for (int64_t cc = n8 * 8; cc < d; ++cc) {
+        const float p = a.W[(int64_t)e * d + cc] * x[cc];
+        r = r + p;
+      }
+      lg[s * E + e] = r;
+      if (a.logits) a.logits[(int64_t)s * E + e] = r;
+    }
+    __syncthreads();
+  }
+  if (gridDim.x == 1) route_tail(a, lg, Pn, taken, sel_e, sel_w, cnt);
+}
+
+// The tail for logits computed by several work-groups.
+__global__ void __launch_bounds__(1024) k_route_finish(RouteDecArgs a) {
+  __shared__ float lg[3 * kMaxExperts];
+  __shared__ float Pn[3 * kMaxExperts];
+  __shared__ int taken[3 * kMaxExperts];
+  __shared__ uint32_t sel_e[64];
+  __shared__ float sel_w[64];
+  __shared__ uint32_t cnt[kMaxExperts];
+  for (int i = threadIdx.x; i < a.S * a.E; i += 1024) lg[i] = a.logits[i];
+  __syncthreads();
+  route_tail(a, lg, Pn, taken, sel_e, sel_w, cnt);
+}
+
 }  // namespace
 
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
@@ -362,4 +630,26 @@ hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int
   return hipGetLastError();
 }
 
+}  // namespace kmoe
+
+namespace kmoe {
+hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
+                               int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
+                               float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs) {
+  if (S < 1 || S > 3 || E < 1 || E > 512 || k < 1 || k > 16 || k > E || S * k > 64) return hipErrorNotSupported;
+  const int64_t nch = (d / 8 * 8 + 511) / 512;
+  if (nch > kDecMaxChunks || d < 8) return hipErrorNotSupported;
+  const int groups = (E + kDecEpw - 1) / kDecEpw;
+  if (groups > 1 && !logits) return hipErrorInvalidValue;  // the split path needs the logits buffer
+  RouteDecArgs a{router, E, d, x, S, k, norm_topk, weights_scale, logits, idx, w, perm, offsets, inv, n_active, active,
+                 qtype, xq, xd, xs};
+  if (nch <= 4) hipLaunchKernelGGL(k_route_decode<4>, dim3(groups), dim3(512), 0, st, a);
+  else if (nch <= 8) hipLaunchKernelGGL(k_route_decode<8>, dim3(groups), dim3(512), 0, st, a);
+  else hipLaunchKernelGGL(k_route_decode<16>, dim3(groups), dim3(512), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || groups == 1) return e;
+  hipLaunchKernelGGL(k_route_finish, dim3(1), dim3(1024), 0, st, a);
+  return hipGetLastError();
+}
 }  // namespace kmoe

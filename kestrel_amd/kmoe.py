@@ -29,6 +29,7 @@ SIGNATURES = {
     "kmoe_last_error": (C.c_char_p, [_P]),
     "kmoe_abi_version": (C.c_int, []),
     "kmoe_set_stream": (C.c_int, [_P, _P]),
+    "kmoe_use_own_stream": (C.c_int, [_P]),
     "kmoe_get_stream": (_P, [_P]),
     "kmoe_synchronize": (C.c_int, [_P]),
     "kmoe_set_regime": (C.c_int, [_P, C.c_int]),

@@ -164,3 +164,44 @@ def test_errors_map_to_status_codes(ctx):
         assert e.value.status == -3
     finally:
         ctx.vram_set_limit(0)
+
+
+def test_device_generated_weights_are_stream_ordered(ctx, orc):
+    """Weights written by torch kernels on its current stream and uploaded at
+    once (no host sync) must be what the kernels read: the library runs on
+    torch's stream, including the null stream."""
+    import ctypes
+
+    import torch
+
+    d, ff, E, k = 1024, 768, 8, 2
+    ctx.layer_create(90, E, k, d, ff, Q4_K, Q4_K, Q4_K)
+    hdr = torch.tensor(np.concatenate([np.array([1.4e-4], np.float16).view(np.uint8),
+                                       np.array([1.05e-3], np.float16).view(np.uint8)]), device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    for e in range(E):
+        for p in range(3):
+            n = ff * row_bytes(Q4_K, d) if p < 2 else d * row_bytes(Q4_K, ff)
+            t = torch.randint(0, 256, (n // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
+            t[:, 0:4] = hdr
+            ctx.expert_upload(90, e, p, t)
+            del t
+    router = orc.normal(3, E * d, 0.0, 0.02).reshape(E, d)
+    ctx.router_upload(90, router)
+    h = torch.randn((4, d), device="cuda") * 2.0  # async producer right before the call
+    out = host(ctx.moe_ffn(90, h))
+    parts = [[None] * 3 for _ in range(E)]
+    for e in range(E):
+        for p in range(3):
+            ptr, n = ctx.expert_part(90, e, p)
+            buf = np.empty(n, np.uint8)
+            ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(ptr), n))
+            assert np.all(buf.reshape(-1, 144)[:, :4] == hdr.cpu().numpy()), (e, p)
+            parts[e][p] = buf
+    ctx.layer_destroy(90)
+    L = orc.Layer(E, k, d, ff, Q4_K, Q4_K, Q4_K, router, [p[0] for p in parts], [p[1] for p in parts],
+                  [p[2] for p in parts], True, 0.0)
+    ref = L.moe_ffn(h.cpu().numpy())
+    assert np.isfinite(out).all()
+    assert rel_l2(out, ref) < TOL
