@@ -47,7 +47,20 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy kernel (torch.neg, MIB in and MIB out) 5 times and exit: "
+                         "the reference point that scales FETCH_SIZE / WRITE_SIZE counters to bytes")
     return ap.parse_args()
+
+
+def copy_probe(torch, mib: int):
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}))
 
 
 def make_layers(ctx, torch, n_layers: int, seed: int = 0):
@@ -128,6 +141,9 @@ def main():
     from kestrel_amd.kmoe import Context
 
     torch.cuda.set_device(0)
+    if a.copy_probe:
+        copy_probe(torch, a.copy_probe)
+        return
     ctx = Context(0)
     ctx.set_regime(a.regime)
     make_layers(ctx, torch, a.layers)

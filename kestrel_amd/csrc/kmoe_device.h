@@ -77,19 +77,18 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8
 // superblock whose 12 scale bytes are the little-endian words s03, s47, s811.
 __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s03, uint32_t s47, uint32_t s811, int k, int &sA,
                                                    int &mA, int &sB, int &mB) {
-  if (k < 2) {
-    const int j = 2 * k;
-    sA = (int)(byte_of(s03, j) & 63u);
-    mA = (int)(byte_of(s47, j) & 63u);
-    sB = (int)(byte_of(s03, j + 1) & 63u);
-    mB = (int)(byte_of(s47, j + 1) & 63u);
-  } else {
-    const int i = 2 * k - 4;  // j - 4 for j = 2k
-    sA = (int)((byte_of(s811, i) & 0xfu) | ((byte_of(s03, i) >> 6) << 4));
-    mA = (int)((byte_of(s811, i) >> 4) | ((byte_of(s47, i) >> 6) << 4));
-    sB = (int)((byte_of(s811, i + 1) & 0xfu) | ((byte_of(s03, i + 1) >> 6) << 4));
-    mB = (int)((byte_of(s811, i + 1) >> 4) | ((byte_of(s47, i + 1) >> 6) << 4));
-  }
+  // Branch-free: both forms are computed from byte index bi = 2*(k&1) and the
+  // one for j = 2k (j < 4 or j >= 4) is selected, so lanes with different k
+  // never diverge.
+  const int bi = 2 * (k & 1);
+  const bool hi = k >= 2;
+  const uint32_t a0 = byte_of(s03, bi), a1 = byte_of(s03, bi + 1);
+  const uint32_t b0 = byte_of(s47, bi), b1 = byte_of(s47, bi + 1);
+  const uint32_t c0 = byte_of(s811, bi), c1 = byte_of(s811, bi + 1);
+  sA = (int)(hi ? ((c0 & 0xfu) | ((a0 >> 6) << 4)) : (a0 & 63u));
+  mA = (int)(hi ? ((c0 >> 4) | ((b0 >> 6) << 4)) : (b0 & 63u));
+  sB = (int)(hi ? ((c1 & 0xfu) | ((a1 >> 6) << 4)) : (a1 & 63u));
+  mB = (int)(hi ? ((c1 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u));
 }
 
 // Dword-aligned 16-byte load (global_load_dwordx4 accepts 4-byte alignment).
