@@ -89,19 +89,11 @@ def make_layers(ctx, torch, n_layers: int, seed: int = 0):
 def cpu_baseline(ctx, torch, seconds: float, threads: int):
     """Oracle moe_ffn (C++ restatement of kestrel's AVX2 path, transformer.rs:513)
     on layer 0's exact bytes, one token per call, for about `seconds`."""
-    import ctypes
-
     import numpy as np
 
     from oracle import pyoracle as orc
 
-    parts = [[None] * 3 for _ in range(E)]
-    for e in range(E):
-        for p in range(3):
-            ptr, n = ctx.expert_part(0, e, p)
-            buf = np.empty(n, np.uint8)
-            ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(ptr), n))
-            parts[e][p] = buf
+    parts = [[ctx.expert_read(0, e, p) for p in range(3)] for e in range(E)]
     rng = np.random.default_rng(0)
     router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)  # same stream as make_layers' layer 0
     L = orc.Layer(E, K, D, FF, Q4_K, Q4_K, Q4_K, router, [p[0] for p in parts], [p[1] for p in parts],

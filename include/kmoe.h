@@ -168,15 +168,23 @@ int kmoe_layer_destroy(kmoe_ctx *ctx, uint32_t layer);
 /* Router tensor blk.L.ffn_gate_inp.weight, F32 [n_expert, n_embd], host bytes. */
 int kmoe_router_upload(kmoe_ctx *ctx, uint32_t layer, const float *router, size_t bytes);
 /* ExpertStore::load/preload_all (expert.rs:251-303, :620-641): copy expert e's
- * part (0 gate, 1 up, 2 down) GGUF bytes verbatim from host memory. */
+ * part (0 gate, 1 up, 2 down) GGUF bytes from host memory. Q8_0 and F32 parts
+ * are stored verbatim; Q4_K parts are stored as tiled rows (same size, the
+ * 16-byte superblock heads first, then the nibble bytes regrouped so a wave's
+ * loads are contiguous); kmoe_expert_read gives back the GGUF bytes. */
 int kmoe_expert_upload(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes, size_t len);
-/* Same from device memory (device-to-device copy). */
+/* Same from device memory (device-to-device copy, tiled on the device for Q4_K). */
 int kmoe_expert_upload_dev(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes_dev,
                            size_t len);
 /* ExpertStore::is_ready (expert.rs:445): 1 when all three parts are resident, else 0. */
 int kmoe_expert_is_ready(kmoe_ctx *ctx, uint32_t layer, uint32_t expert);
-/* ExpertBuf::part (expert.rs:72-76): device pointer and length of a resident part. */
+/* ExpertBuf::part (expert.rs:72-76): device pointer and length of a resident
+ * part, in the tier's layout (tiled rows for Q4_K). */
 int kmoe_expert_part(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void **dev, size_t *len);
+/* ExpertBuf::part bytes as the reference hands them out (expert.rs:72-76):
+ * copy a resident part to host memory in GGUF layout; len must equal the
+ * part's length. Synchronous. */
+int kmoe_expert_read(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, void *host, size_t len);
 /* ExpertStore::bytes_per_expert (expert.rs:269). */
 int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
 

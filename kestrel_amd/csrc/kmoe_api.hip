@@ -53,6 +53,8 @@ struct Layer {
   size_t part_len[3] = {0, 0, 0};
   size_t part_off[3] = {0, 0, 0};
   size_t expert_stride = 0;
+  bool tiled[3] = {false, false, false};  // Q4_K parts are stored as tiled rows
+  int64_t part_rows[3] = {0, 0, 0}, part_nb[3] = {0, 0, 0};
   size_t reserved = 0;
   bool router_ok = false;
   std::vector<uint8_t> loaded;  // bit p set when part p of expert e is resident
@@ -581,6 +583,12 @@ int kmoe_layer_create(kmoe_ctx *c, uint32_t layer, const kmoe_moe_desc *desc) {
   L.part_off[1] = align_up(L.part_len[0]);
   L.part_off[2] = L.part_off[1] + align_up(L.part_len[1]);
   L.expert_stride = L.part_off[2] + align_up(L.part_len[2]);
+  const int32_t ptype[3] = {D.gate_type, D.up_type, D.down_type};
+  for (int p = 0; p < 3; ++p) {
+    L.tiled[p] = ptype[p] == KMOE_Q4_K;
+    L.part_rows[p] = p < 2 ? D.n_ff : D.n_embd;
+    L.part_nb[p] = (p < 2 ? D.n_embd : D.n_ff) / 256;
+  }
   const size_t arena = L.expert_stride * D.n_expert;
   const size_t router = align_up((size_t)D.n_expert * D.n_embd * 4);
   DeviceGuard g(c->device);
@@ -633,7 +641,7 @@ int kmoe_router_upload(kmoe_ctx *c, uint32_t layer, const float *router, size_t 
 }
 
 static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len,
-                         hipMemcpyKind kind) {
+                         bool from_device) {
   if (!c) return KMOE_E_INVALID;
   Layer *L = find_layer(c, layer);
   if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
@@ -641,17 +649,28 @@ static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, 
   if (len != L->part_len[part] || !bytes)
     return fail(c, KMOE_E_INVALID, "expert part bytes %zu != %zu", len, L->part_len[part]);
   DeviceGuard g(c->device);
-  HIP_OK(c, hipMemcpyAsync(L->arena + e * L->expert_stride + L->part_off[part], bytes, len, kind, c->stream));
+  uint8_t *dst = L->arena + e * L->expert_stride + L->part_off[part];
+  if (!L->tiled[part]) {
+    HIP_OK(c, hipMemcpyAsync(dst, bytes, len, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                             c->stream));
+  } else if (from_device) {
+    HIP_OK(c, launch_tq4_convert(c->stream, (const uint8_t *)bytes, dst, L->part_rows[part], L->part_nb[part], true));
+  } else {
+    std::vector<uint8_t> t(len);
+    tq4_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
+    HIP_OK(c, hipMemcpyAsync(dst, t.data(), len, hipMemcpyHostToDevice, c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));  // t is released on return
+  }
   HIP_OK(c, hipStreamSynchronize(c->stream));
   L->loaded[e] |= (uint8_t)(1u << part);
   return KMOE_OK;
 }
 
 int kmoe_expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len) {
-  return expert_upload(c, layer, e, part, bytes, len, hipMemcpyHostToDevice);
+  return expert_upload(c, layer, e, part, bytes, len, false);
 }
 int kmoe_expert_upload_dev(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len) {
-  return expert_upload(c, layer, e, part, bytes, len, hipMemcpyDeviceToDevice);
+  return expert_upload(c, layer, e, part, bytes, len, true);
 }
 
 int kmoe_expert_is_ready(kmoe_ctx *c, uint32_t layer, uint32_t e) {
@@ -669,6 +688,27 @@ int kmoe_expert_part(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, cons
   if (!(L->loaded[e] & (1u << part))) return fail(c, KMOE_E_NOT_LOADED, "expert %u part %d not resident", e, part);
   *dev = L->arena + e * L->expert_stride + L->part_off[part];
   *len = L->part_len[part];
+  return KMOE_OK;
+}
+
+int kmoe_expert_read(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, void *host, size_t len) {
+  if (!c) return KMOE_E_INVALID;
+  const void *src = nullptr;
+  size_t n = 0;
+  int rc = kmoe_expert_part(c, layer, e, part, &src, &n);
+  if (rc) return rc;
+  if (!host || len != n) return fail(c, KMOE_E_INVALID, "expert part bytes %zu != %zu", len, n);
+  Layer *L = find_layer(c, layer);
+  DeviceGuard g(c->device);
+  if (!L->tiled[part]) {
+    HIP_OK(c, hipMemcpyAsync(host, src, n, hipMemcpyDeviceToHost, c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    return KMOE_OK;
+  }
+  std::vector<uint8_t> t(n);
+  HIP_OK(c, hipMemcpyAsync(t.data(), src, n, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  tq4_convert_host(t.data(), (uint8_t *)host, L->part_rows[part], L->part_nb[part], false);
   return KMOE_OK;
 }
 

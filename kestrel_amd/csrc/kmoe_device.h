@@ -98,6 +98,30 @@ __device__ __forceinline__ uint4 load_u4_a4(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Tiled Q4_K rows: the expert tier's HBM layout for Q4_K parts. A row of nb
+// superblocks keeps its 144*nb bytes, reordered:
+//   [0, 16*nb)       the 16-byte head (f16 d, f16 dmin, 12 scale bytes) of
+//                    superblock s at 16*s;
+//   [16*nb, 144*nb)  the nibble bytes in groups of 8 superblocks: group g
+//                    (superblocks 8g .. 8g+ns-1, ns = min(8, nb-8g)) starts at
+//                    16*nb + 1024*g, and its 16-byte chunk j*4*ns + 4*sl + k
+//                    holds nibble bytes [32k+16j, 32k+16j+16) of superblock 8g+sl.
+// A wave whose lanes take consecutive (superblock, k) slots then reads each of
+// its two nibble chunks from one or two contiguous 512-byte runs and its heads
+// from one contiguous run, instead of touching every 144-byte superblock three
+// times.
+__host__ __device__ __forceinline__ int64_t tq4_qs_off(int64_t nb, int64_t sb, int k, int j) {
+  const int64_t g = sb >> 3;
+  const int64_t rem = nb - 8 * g;
+  const int64_t ns = rem < 8 ? rem : 8;
+  return 16 * nb + 1024 * g + 16 * (j * 4 * ns + 4 * (sb & 7) + k);
+}
+// Byte distance from chunk (sb, k, 0) to chunk (sb, k, 1).
+__host__ __device__ __forceinline__ int64_t tq4_j_stride(int64_t nb, int64_t sb) {
+  const int64_t rem = nb - 8 * (sb >> 3);
+  return 64 * (rem < 8 ? rem : 8);
+}
+
 // Correctly rounded expf via double exp. glibc's expf (what the reference's
 // f32::exp calls) is within 0.502 ulp, so the two agree except on inputs
 // whose exact value lies within ~0.002 ulp of a rounding midpoint.

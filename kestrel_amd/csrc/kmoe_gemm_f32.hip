@@ -37,11 +37,13 @@ __device__ __forceinline__ bool f32_regime(int regime, int n) {
   return regime == REGIME_EXACT || (regime == REGIME_AVX2 && n >= 4);
 }
 
-// 16 consecutive dequantized weights of chunk kc, part p (0..3), of one row.
-template <int TYPE>
-__device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p, float *o) {
+// 16 consecutive dequantized weights of chunk kc, part p (0..3), of one row
+// (Q4_K: GGUF bytes, or tiled rows of nb superblocks when TILED).
+template <int TYPE, bool TILED>
+__device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p, int64_t nb, float *o) {
   if constexpr (TYPE == T_Q4_K) {
-    const uint8_t *sb = row + (kc >> 2) * 144;
+    const int64_t sbi = kc >> 2;
+    const uint8_t *sb = row + sbi * (TILED ? 16 : 144);
     const int k = (int)(kc & 3);
     const uint4 hdr = *(const uint4 *)sb;
     const float d = f16_bits_to_f32(hdr.x), dmin = f16_bits_to_f32(hdr.x >> 16);
@@ -50,7 +52,8 @@ __device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p,
     const bool hi = p >= 2;
     const float dl = d * (float)(hi ? sB : sA);
     const float ml = dmin * (float)(hi ? mB : mA);
-    const uint4 q = *(const uint4 *)(sb + 16 + 32 * k + 16 * (p & 1));
+    const uint8_t *qp = TILED ? row + tq4_qs_off(nb, sbi, k, p & 1) : sb + 16 + 32 * k + 16 * (p & 1);
+    const uint4 q = *(const uint4 *)qp;
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -119,7 +122,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   for (int64_t kc = 0; kc < cols / KC; ++kc) {
     float wv[16];
     if (wvalid) {
-      dequant16<TYPE>(wrow, kc, dpart, wv);
+      dequant16<TYPE, MODE != G_PLAIN>(wrow, kc, dpart, cols / 256, wv);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) wv[i] = 0.0f;

@@ -33,6 +33,12 @@ struct ExpertTier {
   int64_t off[3];
 };
 
+// ---- expert tier layout (kmoe_layout.hip): GGUF Q4_K rows <-> tiled Q4_K rows
+// (rows of nb superblocks; src and dst must not overlap).
+hipError_t launch_tq4_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
+                              bool to_tiled);
+void tq4_convert_host(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb, bool to_tiled);
+
 // ---- int8 matvecs (kmoe_matvec.hip)
 // Plain: out[s*rows + r] for s < s_rows; activations pre-quantized.
 hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,

@@ -10,11 +10,13 @@
 // reference's bit for bit; the fp32 epilogue sums in a different order, which
 // moves the result by a few ulp (checked against a 1e-3 relative L2 bound).
 //
-// Layout and mapping. Weights stay in GGUF bytes. A Q4_K "task" is one
-// quarter of a 144-byte superblock: the 16-byte header (d, dmin, 12 scale
-// bytes) plus 32 bytes of nibbles (64 weights of sub-blocks 2k and 2k+1).
-// Four consecutive lanes read one superblock, so a wave's loads cover whole
-// superblocks contiguously. A Q8_0 task is one 34-byte block, read as nine
+// Layout and mapping. Plain matvecs read GGUF bytes; the grouped (expert)
+// kernels read the expert tier, whose Q4_K rows are tiled (tq4_qs_off in
+// kmoe_device.h). A Q4_K "task" is one quarter of a 144-byte superblock: the
+// 16-byte header (d, dmin, 12 scale bytes) plus 32 bytes of nibbles (64
+// weights of sub-blocks 2k and 2k+1). Lanes take consecutive tasks, so in the
+// tiled layout each wave load instruction covers one or two contiguous runs of
+// bytes. A Q8_0 task is one 34-byte block, read as nine
 // dwords from the dword-aligned address below it. LPR lanes share a row
 // (LPR = 64 for 4096-wide Q4_K rows: one row per wave per step); they reduce
 // with DPP and cross-row shuffles. Activations (int8 rows, their scales and
@@ -76,13 +78,23 @@ __device__ __forceinline__ uint4 ld_nt(const uint8_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ Q4kW q4k_load(const uint8_t *row, int t) {
-  const uint8_t *sb = row + (int64_t)(t >> 2) * 144;
+// Task t of a row of nb superblocks, GGUF bytes or tiled rows (expert tier).
+template <bool TILED>
+__device__ __forceinline__ Q4kW q4k_load(const uint8_t *row, int t, int64_t nb) {
+  const int64_t sb = t >> 2;
   const int k = t & 3;
   Q4kW w;
-  w.hdr = ld_nt(sb);
-  w.qa = ld_nt(sb + 16 + 32 * k);
-  w.qb = ld_nt(sb + 32 + 32 * k);
+  if constexpr (TILED) {
+    const uint8_t *qa = row + tq4_qs_off(nb, sb, k, 0);
+    w.hdr = ld_nt(row + 16 * sb);
+    w.qa = ld_nt(qa);
+    w.qb = ld_nt(qa + tq4_j_stride(nb, sb));
+  } else {
+    const uint8_t *s = row + sb * 144;
+    w.hdr = ld_nt(s);
+    w.qa = ld_nt(s + 16 + 32 * k);
+    w.qb = ld_nt(s + 32 + 32 * k);
+  }
   return w;
 }
 
@@ -227,9 +239,10 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
         for (int t = lr; t < ntasks; t += LPR) {
           if constexpr (TYPE == T_Q4_K) {
             const int sb = t >> 2, k = t & 3;
-            const Q4kW w0 = q4k_load(row0, t);
+            constexpr bool TL = MODE == M_GATE_UP || MODE == M_DOWN;  // expert tier rows are tiled
+            const Q4kW w0 = q4k_load<TL>(row0, t, nblk);
             Q4kW w1;
-            if constexpr (MODE == M_GATE_UP) w1 = q4k_load(row1, t);
+            if constexpr (MODE == M_GATE_UP) w1 = q4k_load<TL>(row1, t, nblk);
             const float d0 = f16_bits_to_f32(w0.hdr.x), m0 = f16_bits_to_f32(w0.hdr.x >> 16);
 #pragma unroll
             for (int tk = 0; tk < NT; ++tk) {
@@ -373,9 +386,9 @@ struct WTask<T_Q8_0> {
   Q80W w;
 };
 
-template <int TYPE>
-__device__ __forceinline__ void w_load(WTask<TYPE> &w, const uint8_t *row, int t) {
-  if constexpr (TYPE == T_Q4_K) w.w = q4k_load(row, t);
+template <int TYPE, bool TILED>
+__device__ __forceinline__ void w_load(WTask<TYPE> &w, const uint8_t *row, int t, int64_t nblk) {
+  if constexpr (TYPE == T_Q4_K) w.w = q4k_load<TILED>(row, t, nblk);
   else w.w = q80_load(row, t);
 }
 
@@ -504,7 +517,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
               const int64_t r = r0 + (int64_t)u * RPW;
-              if (r < rows) w_load<TYPE>(w[u], W + r * row_bytes, t);
+              if (r < rows) w_load<TYPE, true>(w[u], W + r * row_bytes, t, nblk);
             }
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
@@ -540,8 +553,9 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
             if (r < rows) {
-              w_load<TYPE>(w0[u], W0 + r * row_bytes, t);
-              if constexpr (MODE == M_GATE_UP) w_load<TYPE>(w1[u], W1 + r * row_bytes, t);
+              constexpr bool TL = MODE == M_GATE_UP;  // expert tier rows are tiled, plain rows are GGUF
+              w_load<TYPE, TL>(w0[u], W0 + r * row_bytes, t, nblk);
+              if constexpr (MODE == M_GATE_UP) w_load<TYPE, TL>(w1[u], W1 + r * row_bytes, t, nblk);
             }
           }
 #pragma unroll
@@ -578,141 +592,6 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   }
 }
 
-// Software-pipelined decode matvec (M_PLAIN, M_GATE_UP): while a block-task
-// is computed, the weights of the work-group's next block-task are already in
-// flight, so every wave keeps memory requests outstanding across tasks.
-template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
-__global__ void __launch_bounds__(256) k_mv_reg_pipe(MvArgs a, int tpl) {
-  constexpr int RPW = 64 / LPR;
-  constexpr int RB = 4 * RPW * RU;  // rows per block-task
-  constexpr int NM = MODE == M_GATE_UP ? 2 : 1;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row_in_wave = lane / LPR, lr = lane % LPR;
-  const int64_t cols = a.cols, rows = a.rows;
-  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
-  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
-  const int64_t bpe = (rows + RB - 1) / RB;
-  int64_t total = bpe;
-  if constexpr (MODE == M_GATE_UP) total = (int64_t)(*a.rt.n_active) * bpe;
-  int64_t b = blockIdx.x;
-  if (b >= total) return;
-
-  ActSlice<TYPE> act[TPLMAX];
-#pragma unroll
-  for (int i = 0; i < TPLMAX; ++i) act_load<TYPE>(act[i], a.xq, a.xd, a.xbs, min(lr + i * LPR, ntasks - 1));
-
-  struct Task {
-    const uint8_t *W[NM];
-    int64_t p0, r0;
-  };
-  auto decode = [&](int64_t bb) {
-    Task tk;
-    int64_t rblk = bb;
-    tk.p0 = 0;
-    if constexpr (MODE == M_GATE_UP) {
-      const int i = (int)(bb / bpe);
-      rblk = bb - (int64_t)i * bpe;
-      const int e = a.rt.active[i];
-      tk.p0 = a.rt.offsets[e];
-      const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
-      tk.W[0] = eb + a.tier.off[0];
-      tk.W[NM - 1] = eb + a.tier.off[1];
-    } else {
-      tk.W[0] = a.w0;
-    }
-    tk.r0 = rblk * RB + (int64_t)(wave * RU) * RPW + row_in_wave;
-    return tk;
-  };
-  WTask<TYPE> cur[NM][RU][TPLMAX], nxt[NM][RU][TPLMAX];
-  // Loads are unconditional (row and task indices clamped into range) so the
-  // loop has no divergent branches: the compiler can then count outstanding
-  // loads exactly and keep the next block-task's loads in flight.
-  auto load = [&](const Task &tk, WTask<TYPE> (&w)[NM][RU][TPLMAX]) {
-#pragma unroll
-    for (int i = 0; i < TPLMAX; ++i) {
-      const int t = min(lr + i * LPR, ntasks - 1);
-#pragma unroll
-      for (int u = 0; u < RU; ++u) {
-        const int64_t r = min(tk.r0 + (int64_t)u * RPW, rows - 1);
-#pragma unroll
-        for (int m = 0; m < NM; ++m) w_load<TYPE>(w[m][u][i], tk.W[m] + r * row_bytes, t);
-      }
-    }
-  };
-  // One block-task: weights in w, activation slices in act.
-  auto compute = [&](const Task &tc, WTask<TYPE> (&w)[NM][RU][TPLMAX]) {
-    float acc[NM][RU];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int u = 0; u < RU; ++u) acc[m][u] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < TPLMAX; ++i) {
-      const int t = lr + i * LPR;
-      const bool tv = i < tpl && t < ntasks;
-      const int tc_ = min(t, ntasks - 1);
-#pragma unroll
-      for (int u = 0; u < RU; ++u)
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          const float v = task_dot<TYPE>(w[m][u][i], tc_, act[i], acc[m][u]);
-          acc[m][u] = tv ? v : acc[m][u];
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int u = 0; u < RU; ++u) acc[m][u] = group_sum<LPR>(acc[m][u]);
-    if (lr == 0) {
-#pragma unroll
-      for (int u = 0; u < RU; ++u) {
-        const int64_t r = tc.r0 + (int64_t)u * RPW;
-        if (r >= rows) continue;
-        if constexpr (MODE == M_GATE_UP) {  // SwiGLU (transformer.rs:558)
-          const float g = acc[0][u];
-          const float den = 1.0f + expf_cr(-g);
-          const float q = g / den;
-          a.out[tc.p0 * rows + r] = q * acc[NM - 1][u];
-        } else {
-          a.out[r] = acc[0][u];
-        }
-      }
-    }
-  };
-  // Ping-pong between two register sets: the next block-task's loads are in
-  // flight while the current one is computed, and no register copies force
-  // an early wait on them.
-  const int64_t step = gridDim.x;
-  Task ta = decode(b);
-  load(ta, cur);
-  for (;;) {
-    Task tb;
-    const bool hb = b + step < total;
-    if (hb) {
-      tb = decode(b + step);
-      load(tb, nxt);
-    }
-    compute(ta, cur);
-    if (!hb) break;
-    b += step;
-    const bool ha = b + step < total;
-    if (ha) {
-      ta = decode(b + step);
-      load(ta, cur);
-    }
-    compute(tb, nxt);
-    if (!ha) break;
-    b += step;
-  }
-}
-
-// Down projection + combine for one token, persistent and split over K.
-// One work-group per CU owns a contiguous block of RB rows for every routed
-// expert. Its four waves split each row's tasks into four equal ranges, so a
-// lane holds exactly one (TPL) activation slice per expert and every row's
-// weight bytes stream through one CU; per-wave partial sums meet in LDS.
-// y = ((p0 + p1) + p2) + p3, then o = o + w_e * y in ascending expert id.
 constexpr int kSplitRbMax = 64;
 
 template <int TYPE, int RU, int TPL>
@@ -761,13 +640,14 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   };
   WTask<TYPE> cur[RU][TPL], nxt[RU][TPL];
   ActSlice<TYPE> act[TPL], act_n[TPL];
-  // Unconditional loads with clamped indices (no divergent branches, see k_mv_reg_pipe).
+  // Unconditional loads with clamped indices: a divergent branch around the
+  // loads would make the compiler wait for all of them at the join.
   auto load_w = [&](const Item &im, WTask<TYPE> (&w)[RU][TPL]) {
 #pragma unroll
     for (int u = 0; u < RU; ++u)
 #pragma unroll
       for (int i = 0; i < TPL; ++i)
-        w_load<TYPE>(w[u][i], im.W + (r0 + min(im.rr + u, nr - 1)) * row_bytes, min(tk[i], ntasks - 1));
+        w_load<TYPE, true>(w[u][i], im.W + (r0 + min(im.rr + u, nr - 1)) * row_bytes, min(tk[i], ntasks - 1), nblk);
   };
   auto load_act = [&](const Item &im, ActSlice<TYPE> (&s)[TPL]) {
 #pragma unroll
@@ -836,199 +716,15 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   if (threadIdx.x < nr) a.out[r0 + threadIdx.x] = outv[threadIdx.x];
 }
 
-// ---------------------------------------------------------------------------
-// Streaming decode matvec for Q4_K (one activation row per expert).
-//
-// Memory side: each wave owns a run of RU consecutive rows of each matrix it
-// reads (RU*row_bytes contiguous bytes per matrix) and loads it linearly:
-// lane l fetches 16-byte chunks l, l+64, ... so every wave instruction covers
-// 1 KB of contiguous weights. (Loading by task instead — header plus two
-// strided 16-byte pieces per lane — touches about twice the cache lines per
-// useful byte and caps at ~4.7 TB/s on MI355X; the linear stream reaches
-// ~6.8 TB/s.) Chunks go to registers first, then to the wave's LDS buffer;
-// the next item's chunks are already in flight in registers while the
-// current item is computed from LDS.
-// Compute side: lane l of a row handles tasks t = l + 64 i (superblock t/4,
-// quarter t%4) reading its 48 bytes and its activation slice from LDS.
-// The activation rows (Q8_K: q, 16-sums, scales) are staged in LDS once per
-// work-group.
-enum { S_GATE_UP = 0, S_PLAIN = 1 };
-
-struct StreamArgs {
-  const uint8_t *w0;  // S_PLAIN
-  int64_t rows, cols;
-  const int8_t *xq;
-  const float *xd;
-  const int32_t *xbs;
-  float *out;
-  ExpertTier tier;
-  Routing rt;
-  int ru;  // rows per wave item
-};
-
-template <int MODE, int CPL, int TPLM>
-__global__ void __launch_bounds__(256) k_stream_q4k(StreamArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int NM = MODE == S_GATE_UP ? 2 : 1;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t cols = a.cols, rows = a.rows;
-  const int64_t nblk = cols / 256;
-  const int ntasks = (int)(4 * nblk);
-  const int tpl = (ntasks + 63) / 64;
-  const int64_t row_bytes = nblk * 144;
-  const int RU = a.ru;
-  // LDS: activation row [q | bsums | d], then one weight buffer per wave
-  const int64_t aq = (cols + 15) & ~15ll, as = (cols / 4 + 15) & ~15ll, ad = (nblk * 4 + 15) & ~15ll;
-  uint8_t *act = lds;
-  uint8_t *wbuf = lds + (int64_t)wave * RU * NM * row_bytes;
-  (void)aq;
-  (void)as;
-  (void)ad;
-  const int64_t seg = (int64_t)RU * row_bytes;  // bytes of one matrix in an item
-  const int nchunk = (int)(NM * seg / 16);
-
-  (void)act;
-  // The activation slices of this lane's tasks are the same for every row:
-  // held in registers for the whole kernel.
-  ActSlice<T_Q4_K> xs[TPLM];
-#pragma unroll
-  for (int i = 0; i < TPLM; ++i) act_load<T_Q4_K>(xs[i], a.xq, a.xd, a.xbs, min(lane + 64 * i, ntasks - 1));
-
-  const int64_t ipe = (rows + RU - 1) / RU;  // items per expert (or per matrix)
-  int64_t nitems = ipe;
-  if constexpr (MODE == S_GATE_UP) nitems = (int64_t)(*a.rt.n_active) * ipe;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wave, gstep = (int64_t)gridDim.x * 4;
-  if (gw >= nitems) return;
-
-  struct Item {
-    const uint8_t *W[NM];
-    int64_t r0, p0;
-  };
-  auto decode = [&](int64_t it) {
-    Item im;
-    int64_t ri = it;
-    im.p0 = 0;
-    if constexpr (MODE == S_GATE_UP) {
-      const int i = (int)(it / ipe);
-      ri = it - (int64_t)i * ipe;
-      const int e = a.rt.active[i];
-      im.p0 = a.rt.offsets[e];
-      const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
-      im.W[0] = eb + a.tier.off[0];
-      im.W[NM - 1] = eb + a.tier.off[1];
-    } else {
-      im.W[0] = a.w0;
-    }
-    im.r0 = ri * RU;
-    return im;
-  };
-  uint4 stg[CPL];
-  // Linear chunk c of an item: matrix m = c / segc, byte 16*(c - m*segc) of
-  // the rows r0..; the per-lane offsets do not depend on the item.
-  const int segc = (int)(seg / 16);
-  int coff[CPL];
-  bool cm[CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    int c = lane + 64 * j;
-    c = c < nchunk ? c : nchunk - 1;
-    cm[j] = NM == 2 && c >= segc;
-    coff[j] = 16 * (cm[j] ? c - segc : c);
-  }
-  const int64_t lim = rows * row_bytes - 16;  // last item of a matrix may run past its rows
-  auto fetch = [&](const Item &im) {
-    const int64_t base = im.r0 * row_bytes;
-    const bool tail = base + seg > rows * row_bytes;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      int64_t off = base + coff[j];
-      if (tail) off = off < lim ? off : lim;
-      const uint8_t *W = (NM == 2 && cm[j]) ? im.W[NM - 1] : im.W[0];
-      stg[j] = ld_nt(W + off);
-    }
-  };
-  auto stash = [&]() {
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      if (c < nchunk) ((uint4 *)wbuf)[c] = stg[j];
-    }
-  };
-  int64_t it = gw;
-  Item cur = decode(it);
-  fetch(cur);
-  for (;;) {
-    stash();  // waits for this item's chunks; LDS ops of one wave stay in order
-    const int64_t nx = it + gstep;
-    Item nxt = cur;
-    if (nx < nitems) {
-      nxt = decode(nx);
-      fetch(nxt);  // in flight during the compute below
-    }
-    for (int u = 0; u < RU; ++u) {
-      const int64_t r = cur.r0 + u;
-      float acc[NM];
-#pragma unroll
-      for (int m = 0; m < NM; ++m) acc[m] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < TPLM; ++i) {
-        const int t = lane + 64 * i;
-        if (i < tpl && t < ntasks) {
-          const int sb = t >> 2, k = t & 3;
-          const ActSlice<T_Q4_K> &s = xs[i];
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            const uint8_t *rb = wbuf + ((int64_t)m * RU + u) * row_bytes + (int64_t)sb * 144;
-            WTask<T_Q4_K> w;
-            w.w.hdr = *(const uint4 *)rb;
-            w.w.qa = *(const uint4 *)(rb + 16 + 32 * k);
-            w.w.qb = *(const uint4 *)(rb + 32 + 32 * k);
-            acc[m] = task_dot<T_Q4_K>(w, t, s, acc[m]);
-          }
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < NM; ++m) acc[m] = group_sum<64>(acc[m]);
-      if (lane == 0 && r < rows) {
-        if constexpr (MODE == S_GATE_UP) {  // SwiGLU (transformer.rs:558)
-          const float g = acc[0];
-          const float den = 1.0f + expf_cr(-g);
-          const float q = g / den;
-          a.out[cur.p0 * rows + r] = q * acc[NM - 1];
-        } else {
-          a.out[r] = acc[0];
-        }
-      }
-    }
-    if (nx >= nitems) break;
-    it = nx;
-    cur = nxt;
-  }
-}
-
 // Launch-shape knobs, read once: KMOE_GRID_MULT (work-groups per CU cap for
-// the pipelined matvec, default 4) and KMOE_DOWN_WG_PER_CU (split-K down,
-// default 1). Used for sweeps; the defaults are the measured best.
+// the register matvec, default 4) and KMOE_DOWN_WG_PER_CU (split-K down,
+// default 2). Used for sweeps; the defaults are the measured best.
 int env_int(const char *name, int dflt) {
   const char *v = getenv(name);
   if (!v || !*v) return dflt;
   const int x = atoi(v);
   return x > 0 ? x : dflt;
 }
-// KMOE_DECODE_KERNEL: "reg" (default), "pipe" or "stream" for the
-// single-row gate/up and plain matvecs.
-int decode_kernel() {
-  static const int v = [] {
-    const char *e = getenv("KMOE_DECODE_KERNEL");
-    if (!e) return 0;
-    if (!strcmp(e, "pipe")) return 1;
-    if (!strcmp(e, "stream")) return 2;
-    return 0;
-  }();
-  return v;
-}
-bool use_pipe() { return decode_kernel() == 1; }
-bool use_stream() { return decode_kernel() == 2; }
 int grid_mult() {
   static const int v = env_int("KMOE_GRID_MULT", 4);
   return v;
@@ -1076,10 +772,7 @@ hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_task
     grid = (max_tasks + per - 1) / per;
   }
   if (grid < 1) grid = 1;
-  if (MODE == M_DOWN_COMBINE || !use_pipe())
-    hipLaunchKernelGGL((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
-  else
-    hipLaunchKernelGGL((k_mv_reg_pipe<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
+  hipLaunchKernelGGL((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
   return hipGetLastError();
 }
 
@@ -1158,47 +851,6 @@ bool act_fits(int type, int64_t cols) {
   return 3 * per <= 65536;
 }
 
-// Streaming launcher: picks RU so that chunks per lane fit CPL and the LDS
-// (activation row + 4 wave buffers) allows two work-groups per CU.
-template <int MODE>
-hipError_t launch_stream(hipStream_t st, StreamArgs a, int n_groups) {
-  constexpr int NM = MODE == S_GATE_UP ? 2 : 1;
-  const int64_t nblk = a.cols / 256;
-  const int64_t row_bytes = nblk * 144;
-  const int ntasks = (int)(4 * nblk);
-  if (ntasks < 64 || ntasks > 256) return hipErrorNotSupported;
-  const int64_t actb = 0;  // activation slices live in registers
-  int ru = 8;
-  while (ru > 1 && (NM * ru * row_bytes / 16 > 64 * 24 || actb + 4 * NM * ru * row_bytes > 80 * 1024)) --ru;
-  const int cpl = (int)((NM * ru * row_bytes / 16 + 63) / 64);
-  if (cpl > 24 || actb + 4 * NM * ru * row_bytes > 160 * 1024) return hipErrorNotSupported;
-  a.ru = ru;
-  const size_t shmem = (size_t)(actb + 4 * NM * ru * row_bytes);
-  const int64_t items = (a.rows + ru - 1) / ru * n_groups;
-  int64_t grid = (items + 3) / 4;
-  const int64_t cap = (int64_t)cu_count() * grid_mult();
-  if (grid > cap) grid = cap;
-  const int tplm = (ntasks + 63) / 64;
-#define KMOE_STREAM(CPLV, TPLV)                                                                      \
-  do {                                                                                               \
-    hipError_t e_ = hipFuncSetAttribute((const void *)k_stream_q4k<MODE, CPLV, TPLV>,                \
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);     \
-    if (e_ != hipSuccess) return e_;                                                                 \
-    hipLaunchKernelGGL((k_stream_q4k<MODE, CPLV, TPLV>), dim3((unsigned)grid), dim3(256), shmem, st, a); \
-    return hipGetLastError();                                                                        \
-  } while (0)
-  if (tplm == 1) {
-    if (cpl <= 8) KMOE_STREAM(8, 1);
-    if (cpl <= 12) KMOE_STREAM(12, 1);
-    if (cpl <= 18) KMOE_STREAM(18, 1);
-    KMOE_STREAM(24, 1);
-  }
-  if (cpl <= 8) KMOE_STREAM(8, 4);
-  if (cpl <= 16) KMOE_STREAM(16, 4);
-  KMOE_STREAM(24, 4);
-#undef KMOE_STREAM
-}
-
 }  // namespace
 
 hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
@@ -1212,18 +864,6 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   a.xbs = xbs;
   a.s_rows = 1;
   a.out = out;
-  if (type == T_Q4_K && use_stream()) {
-    StreamArgs sa{};
-    sa.w0 = w;
-    sa.rows = rows;
-    sa.cols = cols;
-    sa.xq = xq;
-    sa.xd = xd;
-    sa.xbs = xbs;
-    sa.out = out;
-    hipError_t e = launch_stream<S_PLAIN>(st, sa, 1);
-    if (e != hipErrorNotSupported) return e;
-  }
   if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
   return hipErrorInvalidValue;
@@ -1241,19 +881,6 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   a.out = h;
   a.tier = tier;
   a.rt = rt;
-  if (type == T_Q4_K && use_stream()) {
-    StreamArgs sa{};
-    sa.rows = rows;
-    sa.cols = cols;
-    sa.xq = xq;
-    sa.xd = xd;
-    sa.xbs = xbs;
-    sa.out = h;
-    sa.tier = tier;
-    sa.rt = rt;
-    hipError_t e = launch_stream<S_GATE_UP>(st, sa, max_active);
-    if (e != hipErrorNotSupported) return e;
-  }
   if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
   return hipErrorInvalidValue;

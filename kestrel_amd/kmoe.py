@@ -55,6 +55,7 @@ SIGNATURES = {
     "kmoe_expert_upload_dev": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
     "kmoe_expert_is_ready": (C.c_int, [_P, _u32, _u32]),
     "kmoe_expert_part": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_P), C.POINTER(_sz)]),
+    "kmoe_expert_read": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
     "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
     "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
@@ -259,6 +260,13 @@ class Context:
         p, n = _P(), _sz()
         self.check(self.lib.kmoe_expert_part(self.h, layer, e, part, C.byref(p), C.byref(n)))
         return p.value, n.value
+
+    def expert_read(self, layer: int, e: int, part: int) -> np.ndarray:
+        """The part's GGUF bytes (ExpertBuf::part), whatever the tier's layout."""
+        _, n = self.expert_part(layer, e, part)
+        buf = np.empty(n, np.uint8)
+        self.check(self.lib.kmoe_expert_read(self.h, layer, e, part, buf.ctypes.data, n))
+        return buf
 
     def bytes_per_expert(self, layer: int) -> int:
         v = _u64()

@@ -130,9 +130,52 @@ def test_expert_tier_serves_correct_slices(ctx):
                 buf = np.empty(n // 4, np.float32)
                 ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(p), n))
                 assert np.all(buf == l * 1000 + e * 10 + k)
+            for k in range(3):
+                assert np.all(ctx.expert_read(l, e, k).view(np.float32) == l * 1000 + e * 10 + k)
         assert ctx.bytes_per_expert(l) == 3 * 256 * 8 * 34
     ctx.layer_destroy(0)
     ctx.layer_destroy(1)
+
+
+def _tiled_reference(g: np.ndarray, rows: int, nb: int) -> np.ndarray:
+    """Tiled Q4_K rows written out chunk by chunk from the layout's definition:
+    heads first, then per group of 8 superblocks the chunks (j, superblock, k)."""
+    out = np.empty_like(g)
+    for r in range(rows):
+        row = g[r * 144 * nb:(r + 1) * 144 * nb].reshape(nb, 144)
+        parts = [row[:, :16].reshape(-1)]
+        for g0 in range(0, nb, 8):
+            sbs = row[g0:min(nb, g0 + 8), 16:].reshape(-1, 4, 2, 16)  # (superblock, k, j, 16 bytes)
+            parts.append(sbs.transpose(2, 0, 1, 3).reshape(-1))
+        out[r * 144 * nb:(r + 1) * 144 * nb] = np.concatenate(parts)
+    return out
+
+
+@pytest.mark.parametrize("d,ff", [(4096, 512), (1024, 14336 // 7), (768, 2304)])
+def test_q4k_tier_layout_round_trip(ctx, d, ff):
+    """Q4_K parts are stored as tiled rows: host and device uploads produce the
+    same bytes, the layout matches its definition (heads, then 8-superblock
+    groups, partial last group included), and kmoe_expert_read restores GGUF."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(d + ff)
+    ctx.layer_create(95, 4, 2, d, ff, Q4_K, Q4_K, Q4_K)
+    try:
+        for p in range(3):
+            rows, nb = (ff, d // 256) if p < 2 else (d, ff // 256)
+            g = rng.integers(0, 256, rows * nb * 144, dtype=np.uint8)
+            ctx.expert_upload(95, 0, p, g)
+            ctx.expert_upload(95, 1, p, torch.from_numpy(g).cuda())
+            for e in (0, 1):
+                ptr, n = ctx.expert_part(95, e, p)
+                raw = np.empty(n, np.uint8)
+                ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, raw.ctypes.data, ctypes.c_void_p(ptr), n))
+                assert np.array_equal(raw, _tiled_reference(g, rows, nb)), (p, e)
+                assert np.array_equal(ctx.expert_read(95, e, p), g), (p, e)
+    finally:
+        ctx.layer_destroy(95)
 
 
 def test_errors_map_to_status_codes(ctx):
@@ -194,9 +237,7 @@ def test_device_generated_weights_are_stream_ordered(ctx, orc):
     parts = [[None] * 3 for _ in range(E)]
     for e in range(E):
         for p in range(3):
-            ptr, n = ctx.expert_part(90, e, p)
-            buf = np.empty(n, np.uint8)
-            ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, buf.ctypes.data, ctypes.c_void_p(ptr), n))
+            buf = ctx.expert_read(90, e, p)
             assert np.all(buf.reshape(-1, 144)[:, :4] == hdr.cpu().numpy()), (e, p)
             parts[e][p] = buf
     ctx.layer_destroy(90)
