@@ -73,6 +73,7 @@ struct kmoe_ctx {
   hipStream_t stream = nullptr;
   std::string err;
   int regime = KMOE_REGIME_AVX2;
+  uint32_t *counters = nullptr;  // device, 64 completion counters, zero between calls
   uint64_t vram_limit = 0;
   uint64_t vram_reserved = 0;
   std::map<uint32_t, Layer> layers;
@@ -303,6 +304,12 @@ int kmoe_create(int device, kmoe_ctx **out) {
     return KMOE_E_HIP;
   }
   c->stream = c->own;
+  // completion counters of multi-work-group kernels; zero between calls
+  if (hipMalloc((void **)&c->counters, 256) != hipSuccess || hipMemset(c->counters, 0, 256) != hipSuccess) {
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return KMOE_E_HIP;
+  }
   size_t fr = 0, tot = 0;
   if (hipMemGetInfo(&fr, &tot) == hipSuccess) c->vram_limit = tot;
   *out = c;
@@ -320,6 +327,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   }
   for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->counters) (void)hipFree(c->counters);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
   return KMOE_OK;
@@ -524,15 +532,17 @@ int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const flo
   DeviceGuard g(c->device);
   if (S < 4) {  // fused decode routing; its dispatch outputs go to scratch
     const size_t n = (size_t)S * k;
-    int rc = ensure_ws(c, 4 * align_up(n * 4) + 3 * align_up(((size_t)E + 1) * 4));
+    int rc = ensure_ws(c, 4 * align_up(n * 4) + 3 * align_up(((size_t)E + 1) * 4) + align_up((size_t)S * E * 4));
     if (rc) return rc;
     Carver cv{c->ws};
     uint32_t *perm = cv.take<uint32_t>(n), *inv = cv.take<uint32_t>(n);
     uint32_t *off = cv.take<uint32_t>(E + 1);
     int32_t *na = cv.take<int32_t>(1), *act = cv.take<int32_t>(E);
+    float *lgs = cv.take<float>(S * E);
+    float *lg_out = logits ? logits : lgs;
     hipError_t e = timed(c, "route_decode", [&]() {
-      return launch_route_decode(c->stream, router, E, d, h, (int32_t)S, k, norm_topk, weights_scale, logits, idx, w,
-                                 perm, off, inv, na, act, 0, nullptr, nullptr, nullptr);
+      return launch_route_decode(c->stream, router, E, d, h, (int32_t)S, k, norm_topk, weights_scale, lg_out, idx, w,
+                                 perm, off, inv, na, act, 0, nullptr, nullptr, nullptr, c->counters);
     });
     if (e == hipSuccess) return KMOE_OK;
     if (e != hipErrorNotSupported) HIP_OK(c, e);
@@ -755,7 +765,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
     hipError_t e = timed(c, "route_decode", [&]() {
       return launch_route_decode(st, L->router, (int32_t)E, d, h, (int32_t)S, (int32_t)k, D.norm_topk,
                                  D.weights_scale, w.logits, w.idx, w.wsel, w.perm, w.offsets, w.inv, w.n_active,
-                                 w.active, qtype, w.xq, w.xd, w.xs);
+                                 w.active, qtype, w.xq, w.xd, w.xs, c->counters);
     });
     if (e == hipSuccess) {
       x_quantized = qtype != 0;

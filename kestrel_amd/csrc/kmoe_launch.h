@@ -79,13 +79,16 @@ hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_e
                                 int64_t s_rows, float *logits);
 hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w);
-// Decode routing (s_rows < 4) in one work-group: quant::dot-order logits, softmax,
-// top-k, dispatch (perm/offsets/inv/active), and int8 quantization of x when
-// qtype is T_Q4_K (Q8_K rows) or T_Q8_0 (Q8 rows). hipErrorNotSupported when out of range.
+// Decode routing (s_rows < 4): quant::dot-order logits (one work-group per
+// expert), then in the last work-group to finish softmax, top-k, dispatch
+// (perm/offsets/inv/active); int8 quantization of x when qtype is T_Q4_K
+// (Q8_K rows) or T_Q8_0 (Q8 rows). logits [S, E] is required; *done must be 0
+// and is 0 again when the kernel ends (calls on one counter must not overlap).
+// hipErrorNotSupported when out of range.
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
                                int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
                                float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
-                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs);
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done);
 // Stable counting sort by expert. inv/n_active/active may be null.
 hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
                            uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp);

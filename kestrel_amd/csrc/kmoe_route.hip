@@ -326,7 +326,7 @@ struct RouteDecArgs {
   const float *X;
   int32_t S, k, norm_topk;
   float weights_scale;
-  float *logits;  // [S, E]: written when the logits are split over work-groups (or asked for)
+  float *logits;  // [S, E]
   uint32_t *idx;
   float *wsel;
   uint32_t *perm, *offsets, *inv;
@@ -335,244 +335,291 @@ struct RouteDecArgs {
   int8_t *xq;
   float *xd;
   int32_t *xs;
+  uint32_t *done;  // finished work-groups; 0 between calls (the last one resets it)
+  int vec;         // W, X 16-byte aligned and d % 4 == 0
 };
 
-constexpr int kDecEpw = 8;       // experts per work-group
-constexpr int kDecMaxChunks = 16;  // columns per work-group <= 16 chunks of 512
+constexpr int kDecMaxD = 8192;  // columns whose products one work-group holds in LDS
 
-// Softmax, top-k, renormalisation (transformer.rs:479-495) for S tokens whose
-// logits are in lg[s*E + e] (LDS), then the dispatch and the int8 quantization
-// of x. Runs in one work-group of 1024 threads.
-__device__ void route_tail(const RouteDecArgs &a, const float *lg, float *Pn, int *taken, uint32_t *sel_e,
-                           float *sel_w, uint32_t *cnt) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x, nwaves = nthr >> 6;
-  const int E = a.E;
+// Wave-uniform reductions: DPP inside each 16-lane row, then the four row
+// results read into scalars (no LDS round trips).
+__device__ __forceinline__ uint32_t wave_umax_u(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
+  const uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_umin_u(uint32_t v) {
+  v = min(v, (uint32_t)dpp_i<kDppXor1>((int)v));
+  v = min(v, (uint32_t)dpp_i<kDppXor2>((int)v));
+  v = min(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
+  v = min(v, (uint32_t)dpp_i<kDppMirror>((int)v));
+  const uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
+  return min(min(a, b), min(c, d));
+}
+__device__ __forceinline__ float wave_fmax_u(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  const int iv = __builtin_bit_cast(int, v);
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Softmax, top-k and renormalisation (transformer.rs:479-495) for the S <= 3
+// tokens whose logits the work-groups wrote, then the dispatch (the stable
+// sort of the S*k flat slots by expert). Run by the last work-group to finish.
+// Expert lane + 64*i is held by lane `lane`, i < NPER (E <= 64*NPER).
+template <int NPER>
+__device__ void route_dec_tail(const RouteDecArgs &a, float *P, uint32_t *sel, int *first) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = a.E, K = a.k, n = a.S * a.k;
   if (wave < a.S) {
     const int s = wave;
-    const float *row = lg + s * E;
-    float *P = Pn + s * E;
-    int *tk = taken + s * E;
+    float *p = P + s * kMaxExperts;
+    float lv[NPER];
     float m = -INFINITY;
-    for (int e = lane; e < E; e += 64) m = fmaxf(m, row[e]);
-    m = group_max<64>(m);
-    for (int e = lane; e < E; e += 64) {
-      P[e] = expf_cr(row[e] - m);
-      tk[e] = 0;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    float sum = 0.0f;
-    if (lane == 0) {
-      sum = -0.0f;
-      for (int e = 0; e < E; ++e) sum = sum + P[e];
-    }
-    sum = __shfl(sum, 0);
-    for (int e = lane; e < E; e += 64) P[e] = P[e] / sum;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    for (int j = 0; j < a.k; ++j) {
-      uint64_t best = 0;
-      for (int e = lane; e < E; e += 64) {
-        if (tk[e]) continue;
-        const uint64_t key = ((uint64_t)__float_as_uint(P[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
-        best = key > best ? key : best;
-      }
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t hi = __shfl_xor((unsigned)(best >> 32), off), lo = __shfl_xor((unsigned)best, off);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        best = o > best ? o : best;
+    for (int i = 0; i < NPER; ++i) {
+      const int e = lane + 64 * i;
+      // written by other work-groups of this launch: read past this CU's L1
+      lv[i] = e < E ? __hip_atomic_load(a.logits + s * E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+      m = fmaxf(m, lv[i]);
+    }
+    m = wave_fmax_u(m);
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int e = lane + 64 * i;
+      lv[i] = expf_cr(lv[i] - m);
+      if (e < E) p[e] = lv[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float sum = -0.0f;  // in expert order
+    if (lane == 0) {
+      int e = 0;
+      for (; e + 4 <= E; e += 4) {
+        const float4 v = *(const float4 *)(p + e);
+        sum = sum + v.x;
+        sum = sum + v.y;
+        sum = sum + v.z;
+        sum = sum + v.w;
       }
-      const uint32_t e = 0xffffffffu - (uint32_t)best;
-      if (lane == 0) {
-        tk[e] = 1;
-        sel_e[s * a.k + j] = e;
-        sel_w[s * a.k + j] = P[e];
+      for (; e < E; ++e) sum = sum + p[e];
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) lv[i] = lv[i] / sum;
+    // k rounds: largest p (compared as bits: p >= +0), ties to the lower expert index
+    uint32_t taken = 0;
+    float wk[16];
+    for (int j = 0; j < K; ++j) {
+      uint32_t best = 0;
+      int bi = NPER;
+#pragma unroll
+      for (int i = 0; i < NPER; ++i) {
+        const int e = lane + 64 * i;
+        const uint32_t u = __float_as_uint(lv[i]);
+        if (e < E && !((taken >> i) & 1u) && (bi == NPER || u > best)) {
+          best = u;
+          bi = i;
+        }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      const uint32_t mx = wave_umax_u(bi == NPER ? 0u : best);
+      const bool has = bi != NPER && best == mx;
+      const uint32_t es = wave_umin_u(has ? (uint32_t)(64 * bi + lane) : 0xffffffffu);
+      const int ib = (int)(es >> 6), lw = (int)(es & 63);
+      if (lane == lw) taken |= 1u << ib;
+      float mine = lv[0];
+#pragma unroll
+      for (int i = 1; i < NPER; ++i) mine = i == ib ? lv[i] : mine;
+      wk[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), lw));
+      if (lane == 0) sel[s * K + j] = es;
     }
     if (lane == 0) {
-      float *w = &sel_w[s * a.k];
       if (a.norm_topk) {
         float ss = -0.0f;
-        for (int j = 0; j < a.k; ++j) ss = ss + w[j];
+        for (int j = 0; j < K; ++j) ss = ss + wk[j];
         ss = fmaxf(ss, 6.103515625e-05f);
-        for (int j = 0; j < a.k; ++j) w[j] = w[j] / ss;
+        for (int j = 0; j < K; ++j) wk[j] = wk[j] / ss;
       }
       if (a.weights_scale != 0.0f && a.weights_scale != 1.0f)
-        for (int j = 0; j < a.k; ++j) w[j] = w[j] * a.weights_scale;
-      for (int j = 0; j < a.k; ++j) {
-        a.idx[s * a.k + j] = sel_e[s * a.k + j];
-        a.wsel[s * a.k + j] = w[j];
+        for (int j = 0; j < K; ++j) wk[j] = wk[j] * a.weights_scale;
+      for (int j = 0; j < K; ++j) {
+        a.idx[s * K + j] = sel[s * K + j];
+        a.wsel[s * K + j] = wk[j];
       }
     }
   }
-  // dispatch: stable counting sort of the S*k <= 64 flat slots by expert
-  const int n = a.S * a.k;
-  for (int e = tid; e < E; e += nthr) cnt[e] = 0;
   __syncthreads();
-  if (tid < n) atomicAdd(&cnt[sel_e[tid]], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t run = 0;
-    int na = 0;
-    for (int e = 0; e < E; ++e) {
-      const uint32_t c = cnt[e];
-      a.offsets[e] = run;
-      if (c) a.active[na++] = e;
-      cnt[e] = run;
-      run += c;
+  // dispatch of n <= 48 slots: position = #slots of lower experts + #earlier slots of the same expert
+  uint32_t ej = 0;
+  if (tid < n) {
+    ej = sel[tid];
+    uint32_t lt = 0, eq = 0;
+    for (int i = 0; i < n; ++i) {
+      const uint32_t ei = sel[i];
+      lt += ei < ej ? 1u : 0u;
+      eq += (i < tid && ei == ej) ? 1u : 0u;
     }
-    a.offsets[E] = run;
+    const uint32_t pos = lt + eq;
+    a.perm[pos] = (uint32_t)tid;
+    a.inv[tid] = pos;
+    first[tid] = eq == 0;
+  }
+  for (int e = tid; e <= E; e += blockDim.x) {
+    uint32_t c = 0;
+    for (int i = 0; i < n; ++i) c += sel[i] < (uint32_t)e ? 1u : 0u;
+    a.offsets[e] = c;
+  }
+  __syncthreads();
+  if (tid < n && first[tid]) {
+    int rank = 0;
+    for (int i = 0; i < n; ++i) rank += (first[i] && sel[i] < ej) ? 1 : 0;
+    a.active[rank] = (int32_t)ej;
+  }
+  if (tid == 0) {
+    int na = 0;
+    for (int i = 0; i < n; ++i) na += first[i];
     *a.n_active = na;
   }
-  __syncthreads();
-  if (tid < n) {
-    const uint32_t e = sel_e[tid];
-    uint32_t r = 0;
-    for (int j = 0; j < tid; ++j) r += sel_e[j] == e ? 1u : 0u;  // earlier slots of the same expert
-    const uint32_t p = cnt[e] + r;
-    a.perm[p] = (uint32_t)tid;
-    a.inv[tid] = p;
-  }
-  // int8 activation rows for the int path
-  const int64_t d = a.d;
-  if (a.qtype == T_Q4_K) {
-    const int64_t nb = (int64_t)a.S * (d / 256);
-    for (int64_t b = wave; b < nb; b += nwaves)
-      wave_quant_q8k_block(a.X + b * 256, a.xq + b * 256, a.xd + b, a.xs + b * 16, lane);
-  } else if (a.qtype == T_Q8_0) {
-    const int64_t nb = (int64_t)a.S * (d / 32);
-    for (int64_t b = (int64_t)wave * 8 + (lane >> 3); b < nb; b += (int64_t)nwaves * 8)
-      group8_quant_q8_block(a.X + b * 32, a.xq + b * 32, a.xd + b, a.xs + b * 2, lane & 7);
-  }
 }
 
-// Logits of experts [8g, 8g+8) for the S (< 4) tokens in quant::dot order
-// (quant.rs:208-224): eight chains acc_l = sum over c of p_{8c+l} in order,
-// p = w*x rounded on its own. Each of the 1024 threads loads its share of W
-// and x for every 512-column chunk at once (one memory latency) and forms
-// the products in registers; chunk by chunk they are transposed into LDS so
-// each chain reads its products four at a time. With a single work-group the
-// tail (top-k, dispatch, quantization) follows in the same kernel.
-template <int NCH>
-__global__ void __launch_bounds__(512) k_route_decode(RouteDecArgs a) {
-  constexpr int KC = 512;    // columns per chunk
-  constexpr int L = KC / 8;  // chain steps per chunk
-  constexpr int CS = L + 4;  // padded chain row (spreads LDS banks)
-  __shared__ __attribute__((aligned(16))) float P[2][kDecEpw * 8 * CS];
-  __shared__ float lg[3 * kMaxExperts];
-  __shared__ float Pn[3 * kMaxExperts];
-  __shared__ int taken[3 * kMaxExperts];
-  __shared__ uint32_t sel_e[64];
-  __shared__ float sel_w[64];
-  __shared__ uint32_t cnt[kMaxExperts];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int E = a.E;
-  const int64_t d = a.d;
-  const int64_t n8 = d / 8;  // chain length
-  const int e0 = blockIdx.x * kDecEpw;
-  const int ne = E - e0 < kDecEpw ? E - e0 : kDecEpw;
-  const int nchain = ne * 8;
-  const int nch = (int)((n8 * 8 + KC - 1) / KC);
-  const bool vec = (d % 4) == 0;
-  // This thread's 8 products per chunk: expert e0 + te, columns 8c..8c+7 of
-  // the chunk, i.e. step c of each of the expert's eight chains.
-  const int te = tid >> 6, c = tid & 63;
+// Decode routing (S <= 3 tokens), one work-group per expert e:
+//   logits[s][e] in quant::dot order (quant.rs:208-224): eight chains
+//   acc_l = sum over c of p_{8c+l} in order, each p = w*x rounded on its own,
+//   then -0.0 + acc_0 + ... + acc_7 and the d % 8 tail columns in order.
+// The products of a token go to LDS chain-major; lanes 0..7 of wave 0 fold
+// the chains with their LDS reads two stages ahead, while waves 1..3 quantize
+// this work-group's share of the activation rows for the int path. The last
+// work-group to finish (counter a.done) runs the softmax / top-k / dispatch
+// tail; nothing waits on another work-group.
+template <int NV>
+__global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
+  __shared__ __attribute__((aligned(16))) float T[8 * (kDecMaxD / 8 + 8)];
+  __shared__ float P[3 * kMaxExperts];
+  __shared__ uint32_t sel[64];
+  __shared__ int first[64];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e = blockIdx.x, G = gridDim.x;
+  const int64_t d = a.d, n8 = d / 8;
+  const int cstr = (int)(((n8 + 3) & ~3ll) + 4);
+  const int nq = (int)(2 * n8);  // float4 groups in the first 8*n8 columns
+  const float *w = a.W + (int64_t)e * d;
 
+  float4 wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int q = tid + 256 * v;
+    wv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < nq) wv[v] = a.vec ? *(const float4 *)(w + 4 * q)
+                              : make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+  }
   for (int s = 0; s < a.S; ++s) {
     const float *x = a.X + (int64_t)s * d;
-    float4 pa[NCH], pb[NCH];
+    __syncthreads();  // the previous token's fold has read T
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      pa[j] = pb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      const int64_t col = (int64_t)j * KC + 8 * c;
-      if (j < nch && te < ne && col < n8 * 8) {
-        const float *w = a.W + (int64_t)(e0 + te) * d;
-        if (vec) {
-          const float4 w0 = *(const float4 *)(w + col), w1 = *(const float4 *)(w + col + 4);
-          const float4 x0 = *(const float4 *)(x + col), x1 = *(const float4 *)(x + col + 4);
-          pa[j] = make_float4(w0.x * x0.x, w0.y * x0.y, w0.z * x0.z, w0.w * x0.w);
-          pb[j] = make_float4(w1.x * x1.x, w1.y * x1.y, w1.z * x1.z, w1.w * x1.w);
-        } else {
-          float t[8];
-#pragma unroll
-          for (int m = 0; m < 8; ++m) t[m] = w[col + m] * x[col + m];
-          pa[j] = make_float4(t[0], t[1], t[2], t[3]);
-          pb[j] = make_float4(t[4], t[5], t[6], t[7]);
-        }
+    for (int v = 0; v < NV; ++v) {
+      const int q = tid + 256 * v;
+      if (q < nq) {
+        const float4 xv = a.vec ? *(const float4 *)(x + 4 * q)
+                                : make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+        float *dst = T + (4 * (q & 1)) * cstr + (q >> 1);
+        dst[0 * cstr] = wv[v].x * xv.x;
+        dst[1 * cstr] = wv[v].y * xv.y;
+        dst[2 * cstr] = wv[v].z * xv.z;
+        dst[3 * cstr] = wv[v].w * xv.w;
       }
-    }
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j < nch) {
-        float *B = P[j & 1];
-        float *dst = B + (te * 8) * CS + c;
-        dst[0 * CS] = pa[j].x;
-        dst[1 * CS] = pa[j].y;
-        dst[2 * CS] = pa[j].z;
-        dst[3 * CS] = pa[j].w;
-        dst[4 * CS] = pb[j].x;
-        dst[5 * CS] = pb[j].y;
-        dst[6 * CS] = pb[j].z;
-        dst[7 * CS] = pb[j].w;
-        __syncthreads();
-        if (tid < nchain) {
-          const float *row = &B[tid * CS];
-          const int64_t left = n8 - (int64_t)j * L;
-          const int steps = left < L ? (int)left : L;
-          if (steps == L) {
-#pragma unroll 4
-            for (int i = 0; i < L; i += 4) {
-              const float4 v = *(const float4 *)(row + i);
-              acc = acc + v.x;
-              acc = acc + v.y;
-              acc = acc + v.z;
-              acc = acc + v.w;
-            }
-          } else {
-            for (int i = 0; i < steps; ++i) acc = acc + row[i];
-          }
-        }
-      }
-    }
-    // Sum each expert's eight chains in order, then the tail (quant.rs:219-222).
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __shfl(acc, (lane & ~7) + i);
-    if (tid < nchain && (tid & 7) == 0) {
-      const int e = e0 + (tid >> 3);
-      float r = -0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) r = r + v[i];
-      for (int64_t cc = n8 * 8; cc < d; ++cc) {
-        const float p = a.W[(int64_t)e * d + cc] * x[cc];
-        r = r + p;
-      }
-      lg[s * E + e] = r;
-      if (a.logits) a.logits[(int64_t)s * E + e] = r;
     }
     __syncthreads();
+    if (wave == 0) {
+      float acc = 0.0f;
+      if (lane < 8) {
+        const float *row = T + lane * cstr;
+        const int nst = (int)(n8 / 32);
+        float4 A[8], B[8];
+        auto ld = [&](float4 (&R)[8], int st) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) R[i] = *(const float4 *)(row + 32 * st + 4 * i);
+        };
+        auto add = [&](const float4 (&R)[8]) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            acc = acc + R[i].x;
+            acc = acc + R[i].y;
+            acc = acc + R[i].z;
+            acc = acc + R[i].w;
+          }
+        };
+        if (nst > 0) {
+          // two register stages, the next one's LDS reads in flight while
+          // the current one is added (no branches inside the loop body)
+          ld(A, 0);
+          int st = 0;
+          for (; st + 2 < nst; st += 2) {
+            ld(B, st + 1);
+            add(A);
+            ld(A, st + 2);
+            add(B);
+          }
+          if (st + 1 < nst) {
+            ld(B, st + 1);
+            add(A);
+            add(B);
+          } else {
+            add(A);
+          }
+        }
+        for (int64_t c = (int64_t)nst * 32; c < n8; ++c) acc = acc + row[c];
+      }
+      float r = -0.0f;
+#pragma unroll
+      for (int l = 0; l < 8; ++l) r = r + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), l));
+      if (lane == 0) {
+        for (int64_t c = n8 * 8; c < d; ++c) {
+          const float pr = w[c] * x[c];
+          r = r + pr;
+        }
+        a.logits[(int64_t)s * a.E + e] = r;
+      }
+    } else if (s == 0) {
+      // int8 activation rows: this work-group's blocks, one wave (Q8_K) or
+      // eight lanes (Q8) per block
+      const int wid = e * 3 + (wave - 1), nw = 3 * G;
+      if (a.qtype == T_Q4_K) {
+        const int64_t nb = (int64_t)a.S * (d / 256);
+        for (int64_t b = wid; b < nb; b += nw)
+          wave_quant_q8k_block(a.X + b * 256, a.xq + b * 256, a.xd + b, a.xs + b * 16, lane);
+      } else if (a.qtype == T_Q8_0) {
+        const int64_t nb = (int64_t)a.S * (d / 32);
+        for (int64_t b = (int64_t)wid * 8 + (lane >> 3); b < nb; b += (int64_t)nw * 8)
+          group8_quant_q8_block(a.X + b * 32, a.xq + b * 32, a.xd + b, a.xs + b * 2, lane & 7);
+      }
+    }
   }
-  if (gridDim.x == 1) route_tail(a, lg, Pn, taken, sel_e, sel_w, cnt);
-}
-
-// The tail for logits computed by several work-groups.
-__global__ void __launch_bounds__(1024) k_route_finish(RouteDecArgs a) {
-  __shared__ float lg[3 * kMaxExperts];
-  __shared__ float Pn[3 * kMaxExperts];
-  __shared__ int taken[3 * kMaxExperts];
-  __shared__ uint32_t sel_e[64];
-  __shared__ float sel_w[64];
-  __shared__ uint32_t cnt[kMaxExperts];
-  for (int i = threadIdx.x; i < a.S * a.E; i += 1024) lg[i] = a.logits[i];
   __syncthreads();
-  route_tail(a, lg, Pn, taken, sel_e, sel_w, cnt);
+  if (tid == 0) {
+    __threadfence();  // this work-group's logits and int8 rows before the count
+    last = atomicAdd(a.done, 1u) == (uint32_t)(G - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (a.E <= 64) route_dec_tail<1>(a, P, sel, first);
+  else if (a.E <= 128) route_dec_tail<2>(a, P, sel, first);
+  else if (a.E <= 256) route_dec_tail<4>(a, P, sel, first);
+  else route_dec_tail<8>(a, P, sel, first);
+  if (tid == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -636,20 +683,18 @@ namespace kmoe {
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
                                int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
                                float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
-                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs) {
-  if (S < 1 || S > 3 || E < 1 || E > 512 || k < 1 || k > 16 || k > E || S * k > 64) return hipErrorNotSupported;
-  const int64_t nch = (d / 8 * 8 + 511) / 512;
-  if (nch > kDecMaxChunks || d < 8) return hipErrorNotSupported;
-  const int groups = (E + kDecEpw - 1) / kDecEpw;
-  if (groups > 1 && !logits) return hipErrorInvalidValue;  // the split path needs the logits buffer
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done) {
+  if (S < 1 || S > 3 || E < 1 || E > kMaxExperts || k < 1 || k > 16 || k > E || S * k > 48) return hipErrorNotSupported;
+  if (d < 8 || d > kDecMaxD) return hipErrorNotSupported;
+  if (!logits || !done) return hipErrorInvalidValue;
+  const int vec = d % 4 == 0 && ((uintptr_t)router & 15) == 0 && ((uintptr_t)x & 15) == 0;
   RouteDecArgs a{router, E, d, x, S, k, norm_topk, weights_scale, logits, idx, w, perm, offsets, inv, n_active, active,
-                 qtype, xq, xd, xs};
-  if (nch <= 4) hipLaunchKernelGGL(k_route_decode<4>, dim3(groups), dim3(512), 0, st, a);
-  else if (nch <= 8) hipLaunchKernelGGL(k_route_decode<8>, dim3(groups), dim3(512), 0, st, a);
-  else hipLaunchKernelGGL(k_route_decode<16>, dim3(groups), dim3(512), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || groups == 1) return e;
-  hipLaunchKernelGGL(k_route_finish, dim3(1), dim3(1024), 0, st, a);
+                 qtype, xq, xd, xs, done, vec};
+  const int64_t nq = 2 * (d / 8);
+  if (nq <= 256) hipLaunchKernelGGL(k_route_dec<1>, dim3(E), dim3(256), 0, st, a);
+  else if (nq <= 512) hipLaunchKernelGGL(k_route_dec<2>, dim3(E), dim3(256), 0, st, a);
+  else if (nq <= 1024) hipLaunchKernelGGL(k_route_dec<4>, dim3(E), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(k_route_dec<8>, dim3(E), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 }  // namespace kmoe
