@@ -11,9 +11,11 @@ Steps rotate over NL distinct layers (NL x 793 MB of experts, default 4 =
 its two experts from HBM. Inputs are resident in HBM before timing starts.
 
 Prints one JSON line (contract in the build brief): value = tokens/s of the
-whole job (one GPU), roofline of the dominant kernel (measured live with HIP
-events on the stream it runs on), cpu_baseline = the oracle (C++ restatement
-of kestrel's AVX2 path) timed on this host on a bounded sample.
+whole job (one GPU), roofline of the dominant kernel (its duration measured
+live with HIP events attached to its own dispatch, hipExtLaunchKernelGGL on
+the library's stream; its HBM traffic from the committed rocprofv3 counter
+passes), cpu_baseline = the oracle (C++ restatement of kestrel's AVX2 path)
+timed on this host on a bounded sample.
 """
 from __future__ import annotations
 
@@ -45,12 +47,29 @@ def parse():
     ap.add_argument("--regime", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a replayed HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pcie-steps", type=int, default=200,
+                    help="steps of the host-buffer variant (h copied in, out copied back, synchronous)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain copy kernel (torch.neg, MIB in and MIB out) 5 times and exit: "
                          "the reference point that scales FETCH_SIZE / WRITE_SIZE counters to bytes")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_decode_b1_mixtral_q4k_traffic.txt")
+
+
+def measured_traffic() -> dict:
+    """HBM bytes per launch by library timer name, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a plain copy kernel)."""
+    out = {}
+    if os.path.exists(TRAFFIC_FILE):
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if f and not f[0].startswith("#") and len(f) >= 2:
+                out[f[0]] = int(f[1])
+    return out
 
 
 def copy_probe(torch, mib: int):
@@ -222,6 +241,32 @@ def main():
     ms_step = el * 1000.0 / a.steps
     tok_s = S * a.steps / el
 
+    # ---- host-buffer variant, as the reference's moe_ffn(&[f32]) -> Vec<f32> is
+    # called: pinned h copied in, the layer, out copied back, synchronous per step
+    pcie = None
+    if a.pcie_steps > 0:
+        hh = torch.randn((a.layers, S, D), dtype=torch.float32).pin_memory()
+        ho = torch.empty((a.layers, S, D), dtype=torch.float32).pin_memory()
+        hd = torch.empty((S, D), dtype=torch.float32, device="cuda")
+        od = torch.empty((S, D), dtype=torch.float32, device="cuda")
+        ctx.set_stream(torch.cuda.current_stream())
+
+        def host_step(i):
+            l = i % a.layers
+            hd.copy_(hh[l], non_blocking=True)
+            ctx.moe_ffn(l, hd, od)
+            ho[l].copy_(od, non_blocking=True)
+            torch.cuda.current_stream().synchronize()
+
+        for i in range(min(20, a.pcie_steps)):
+            host_step(i)
+        t1 = time.perf_counter()
+        for i in range(a.pcie_steps):
+            host_step(i)
+        el1 = time.perf_counter() - t1
+        pcie = {"tokens_per_s": round(S * a.pcie_steps / el1, 1), "ms_per_step": round(el1 * 1000 / a.pcie_steps, 5),
+                "steps": a.pcie_steps, "launch": "eager, synchronous per step, pinned host buffers"}
+
     # touched bytes per step: distinct experts of this batch (2 at b=1) + router
     touched = 2 * EXPERT_BYTES + E * D * 4 if S == 1 else None
     gu_name = "moe_gate_up_dec" if "moe_gate_up_dec" in kern else "moe_gate_up_int"
@@ -232,9 +277,11 @@ def main():
         # plus the Q8_K activation row (4096 + 64 + 1024 B) and h out (2 x 14336 x 4 B)
         alg = 2 * 2 * PART + (4096 + 64 + 1024) + 2 * FF * 4
         ach = alg / (gu["avg_us"] * 1e-6) / 1e9
+        tr = measured_traffic().get(gu_name) if S == 1 else None
         roof = {"bound": "hbm", "kernel": gu_name, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
-                "alg_bytes_per_launch": alg}
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": tr,
+                "alg_bytes_per_launch": alg, "avg_us": gu["avg_us"],
+                "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if tr else None}
     res = {
         "metric": "MoE-layer tokens/sec + % peak HBM GB/s, Mixtral-shape Q4_K decode b=1",
         "value": round(tok_s, 2),
@@ -256,6 +303,7 @@ def main():
         "hbm_frac": round(touched / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if touched else None,
         "roofline": roof,
         "kernels_us": kern,
+        "pcie_inclusive": pcie,
         "cpu_baseline": None,
     }
     if not a.no_cpu:

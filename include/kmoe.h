@@ -200,7 +200,9 @@ int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_ro
 int kmoe_moe_last_routing(kmoe_ctx *ctx, uint32_t *idx_dev, float *w_dev, uint32_t *perm_dev,
                           uint32_t *offsets_dev);
 
-/* Per-kernel timing with HIP events on the context's stream (0 = off). */
+/* Per-kernel timing (0 = off): each kernel is launched with start/stop HIP
+ * events taken from its own dispatch packet (hipExtLaunchKernelGGL), on the
+ * context's stream. */
 int kmoe_profile_enable(kmoe_ctx *ctx, int on);
 /* Accumulated time and launch count of the kernel named `kernel` since enable. */
 int kmoe_profile_read(kmoe_ctx *ctx, const char *kernel, double *total_ms, int64_t *launches);

@@ -16,6 +16,10 @@
 #include "../../include/kmoe.h"
 #include "kmoe_launch.h"
 
+namespace kmoe {
+thread_local LaunchTiming g_timing;
+}  // namespace kmoe
+
 using namespace kmoe;
 
 namespace {
@@ -167,11 +171,16 @@ hipError_t timed(kmoe_ctx *c, const char *name, F &&launch) {
   Event2 ev{name, nullptr, nullptr};
   hipError_t e = hipEventCreate(&ev.a);
   if (e == hipSuccess) e = hipEventCreate(&ev.b);
-  if (e == hipSuccess) e = hipEventRecord(ev.a, c->stream);
   if (e != hipSuccess) return e;
+  g_timing = LaunchTiming{ev.a, ev.b};
   e = launch();
-  if (e != hipSuccess) return e;
-  e = hipEventRecord(ev.b, c->stream);
+  const bool used = g_timing.start == nullptr;  // a kernel took the events
+  g_timing = LaunchTiming{};
+  if (e != hipSuccess || !used) {
+    (void)hipEventDestroy(ev.a);
+    (void)hipEventDestroy(ev.b);
+    return e;
+  }
   c->pending.push_back(ev);
   if (c->pending.size() > 4096) prof_drain(c);
   return e;

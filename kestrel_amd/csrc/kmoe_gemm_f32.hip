@@ -169,13 +169,13 @@ template <int MODE>
 hipError_t launch_type(hipStream_t st, int type, const GArgs &a, dim3 grid) {
   switch (type) {
     case T_Q4_K:
-      hipLaunchKernelGGL((k_gemm_f32<T_Q4_K, MODE>), grid, dim3(256), 0, st, a);
+      KMOE_LAUNCH((k_gemm_f32<T_Q4_K, MODE>), grid, dim3(256), 0, st, a);
       break;
     case T_Q8_0:
-      hipLaunchKernelGGL((k_gemm_f32<T_Q8_0, MODE>), grid, dim3(256), 0, st, a);
+      KMOE_LAUNCH((k_gemm_f32<T_Q8_0, MODE>), grid, dim3(256), 0, st, a);
       break;
     case T_F32:
-      hipLaunchKernelGGL((k_gemm_f32<T_F32, MODE>), grid, dim3(256), 0, st, a);
+      KMOE_LAUNCH((k_gemm_f32<T_F32, MODE>), grid, dim3(256), 0, st, a);
       break;
     default:
       return hipErrorInvalidValue;

@@ -1,10 +1,31 @@
 // kmoe_launch.h — host-side launchers of the gfx950 kernels (internal).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace kmoe {
+
+// Kernel timing hook (profiling): while start is set, the next kernel launched
+// through KMOE_LAUNCH on this thread records start/stop at its own dispatch
+// (hipExtLaunchKernelGGL: the begin/end timestamps of the dispatch packet, the
+// ones a kernel trace reports) and clears the hook.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchTiming g_timing;
+
+#define KMOE_LAUNCH(K, G, B, SH, ST, ...)                                                              \
+  do {                                                                                               \
+    if (::kmoe::g_timing.start) {                                                                    \
+      const ::kmoe::LaunchTiming t_ = ::kmoe::g_timing;                                              \
+      ::kmoe::g_timing = ::kmoe::LaunchTiming{};                                                     \
+      hipExtLaunchKernelGGL(K, G, B, SH, ST, t_.start, t_.stop, 0, __VA_ARGS__);                     \
+    } else {                                                                                         \
+      hipLaunchKernelGGL(K, G, B, SH, ST, __VA_ARGS__);                                              \
+    }                                                                                                \
+  } while (0)
 
 enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12 };
 enum { REGIME_AVX2 = 0, REGIME_INT8 = 1, REGIME_EXACT = 2 };

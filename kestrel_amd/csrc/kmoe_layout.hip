@@ -57,10 +57,10 @@ hipError_t launch_tq4_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, 
   if (grid > 65536) grid = 65536;
   const bool aligned = (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
   if (aligned)
-    hipLaunchKernelGGL((k_tq4_convert<true>), dim3((unsigned)grid), dim3(256), 0, st, src, dst, rows, nb,
+    KMOE_LAUNCH((k_tq4_convert<true>), dim3((unsigned)grid), dim3(256), 0, st, src, dst, rows, nb,
                        to_tiled ? 1 : 0);
   else
-    hipLaunchKernelGGL((k_tq4_convert<false>), dim3((unsigned)grid), dim3(256), 0, st, src, dst, rows, nb,
+    KMOE_LAUNCH((k_tq4_convert<false>), dim3((unsigned)grid), dim3(256), 0, st, src, dst, rows, nb,
                        to_tiled ? 1 : 0);
   return hipGetLastError();
 }

@@ -772,7 +772,7 @@ hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_task
     grid = (max_tasks + per - 1) / per;
   }
   if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
+  KMOE_LAUNCH((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
   return hipGetLastError();
 }
 
@@ -802,7 +802,7 @@ template <int TYPE, int LPR, int NT, int MODE>
 hipError_t launch_one(hipStream_t st, const MvArgs &a, dim3 grid) {
   const ActLayout<TYPE> L(a.cols);
   const size_t shmem = (size_t)NT * L.total;
-  hipLaunchKernelGGL((k_matvec_int<TYPE, LPR, NT, MODE>), grid, dim3(256), shmem, st, a);
+  KMOE_LAUNCH((k_matvec_int<TYPE, LPR, NT, MODE>), grid, dim3(256), shmem, st, a);
   return hipGetLastError();
 }
 
@@ -908,11 +908,11 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
       const unsigned grid = (unsigned)((rows + rb - 1) / rb);
       const int tpl = (ntasks + 3) / 4 > 64 ? 2 : 1;
       if (type == T_Q4_K) {
-        if (tpl == 1) hipLaunchKernelGGL((k_down_splitk<T_Q4_K, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-        else hipLaunchKernelGGL((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        else KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
       } else {
-        if (tpl == 1) hipLaunchKernelGGL((k_down_splitk<T_Q8_0, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-        else hipLaunchKernelGGL((k_down_splitk<T_Q8_0, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q8_0, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        else KMOE_LAUNCH((k_down_splitk<T_Q8_0, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
       }
       return hipGetLastError();
     }

@@ -33,7 +33,7 @@ hipError_t launch_quant_q8k(hipStream_t st, const float *x, int64_t rows, int64_
                             int32_t *bsums) {
   const int64_t nb = rows * (cols / 256);
   if (nb == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quant_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, x, nb, q, d, bsums);
+  KMOE_LAUNCH(k_quant_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, x, nb, q, d, bsums);
   return hipGetLastError();
 }
 
@@ -42,7 +42,7 @@ hipError_t launch_quant_q8(hipStream_t st, const float *x, int64_t rows, int64_t
   const int64_t nb = rows * (cols / 32);
   if (nb == 0) return hipSuccess;
   const int64_t waves = (nb + 7) / 8;
-  hipLaunchKernelGGL(k_quant_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, nb, q, d, s16);
+  KMOE_LAUNCH(k_quant_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, nb, q, d, s16);
   return hipGetLastError();
 }
 

@@ -628,7 +628,7 @@ hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_e
                                 int64_t s_rows, float *logits) {
   const int64_t pairs = s_rows * n_expert;
   if (pairs == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_router_logits, dim3((unsigned)((pairs + 15) / 16)), dim3(256), 0, st, router, n_expert, d, x,
+  KMOE_LAUNCH(k_router_logits, dim3((unsigned)((pairs + 15) / 16)), dim3(256), 0, st, router, n_expert, d, x,
                      s_rows, logits);
   return hipGetLastError();
 }
@@ -637,7 +637,7 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w) {
   if (s_rows == 0) return hipSuccess;
   if (n_expert > kMaxExperts || k > 16 || k > n_expert || k <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_route_topk, dim3((unsigned)((s_rows + 3) / 4)), dim3(256), 0, st, logits, s_rows, n_expert, k,
+  KMOE_LAUNCH(k_route_topk, dim3((unsigned)((s_rows + 3) / 4)), dim3(256), 0, st, logits, s_rows, n_expert, k,
                      norm_topk, weights_scale, idx, w);
   return hipGetLastError();
 }
@@ -645,7 +645,7 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
                            uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp) {
   if (n_expert > kMaxExperts || n_expert <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, idx, n_slots, n_expert, perm, offsets, inv, n_active,
+  KMOE_LAUNCH(k_dispatch, dim3(1), dim3(1024), 0, st, idx, n_slots, n_expert, perm, offsets, inv, n_active,
                      active, rank_tmp);
   return hipGetLastError();
 }
@@ -656,12 +656,12 @@ hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t 
   if (n_slots == 0) return hipSuccess;
   if (type == T_Q4_K) {
     const int64_t nb = n_slots * (cols / 256);
-    hipLaunchKernelGGL(k_quant_slots_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
+    KMOE_LAUNCH(k_quant_slots_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
                        idx_flat, regime, q, d, sums);
   } else if (type == T_Q8_0) {
     const int64_t nb = n_slots * (cols / 32);
     const int64_t waves = (nb + 7) / 8;
-    hipLaunchKernelGGL(k_quant_slots_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
+    KMOE_LAUNCH(k_quant_slots_q8, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
                        idx_flat, regime, q, d, sums);
   } else {
     return hipErrorInvalidValue;
@@ -672,7 +672,7 @@ hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t 
 hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out) {
   if (s_rows == 0) return hipSuccess;
   if (rt.topk > 16) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((d + 255) / 256), (unsigned)s_rows), dim3(256), 0, st, y, rt, s_rows,
+  KMOE_LAUNCH(k_combine, dim3((unsigned)((d + 255) / 256), (unsigned)s_rows), dim3(256), 0, st, y, rt, s_rows,
                      d, out);
   return hipGetLastError();
 }
@@ -691,10 +691,10 @@ hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, i
   RouteDecArgs a{router, E, d, x, S, k, norm_topk, weights_scale, logits, idx, w, perm, offsets, inv, n_active, active,
                  qtype, xq, xd, xs, done, vec};
   const int64_t nq = 2 * (d / 8);
-  if (nq <= 256) hipLaunchKernelGGL(k_route_dec<1>, dim3(E), dim3(256), 0, st, a);
-  else if (nq <= 512) hipLaunchKernelGGL(k_route_dec<2>, dim3(E), dim3(256), 0, st, a);
-  else if (nq <= 1024) hipLaunchKernelGGL(k_route_dec<4>, dim3(E), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(k_route_dec<8>, dim3(E), dim3(256), 0, st, a);
+  if (nq <= 256) KMOE_LAUNCH(k_route_dec<1>, dim3(E), dim3(256), 0, st, a);
+  else if (nq <= 512) KMOE_LAUNCH(k_route_dec<2>, dim3(E), dim3(256), 0, st, a);
+  else if (nq <= 1024) KMOE_LAUNCH(k_route_dec<4>, dim3(E), dim3(256), 0, st, a);
+  else KMOE_LAUNCH(k_route_dec<8>, dim3(E), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 }  // namespace kmoe
