@@ -185,6 +185,18 @@ int kmoe_expert_part(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t par
  * copy a resident part to host memory in GGUF layout; len must equal the
  * part's length. Synchronous. */
 int kmoe_expert_read(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, void *host, size_t len);
+/* Shared expert of a layer (qwen2moe, transformer.rs:572-587): dense
+ * ffn_{gate,up}_shexp [n_ff, n_embd] and ffn_down_shexp [n_embd, n_ff] of the
+ * given ggml types, stored as GGUF bytes. kmoe_moe_ffn then adds, after the
+ * routed experts, scale_s * SwiGLU-FFN(h[s]) for every token s (three
+ * quant::matmul over all s_rows rows, in the context's regime), where
+ * scale_s = 1 / (1 + exp(-quant::dot(ffn_gate_inp_shexp, h[s]))) once
+ * kmoe_shared_gate_upload has given that F32 [n_embd] vector, else 1. */
+int kmoe_shared_expert_create(kmoe_ctx *ctx, uint32_t layer, int64_t n_ff, int32_t gate_type, int32_t up_type,
+                              int32_t down_type);
+/* Host GGUF bytes of part 0 (gate), 1 (up) or 2 (down); synchronous. */
+int kmoe_shared_expert_upload(kmoe_ctx *ctx, uint32_t layer, int32_t part, const void *bytes, size_t len);
+int kmoe_shared_gate_upload(kmoe_ctx *ctx, uint32_t layer, const float *gate_inp, size_t bytes);
 /* ExpertStore::bytes_per_expert (expert.rs:269). */
 int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
 

@@ -62,6 +62,17 @@ struct Layer {
   size_t reserved = 0;
   bool router_ok = false;
   std::vector<uint8_t> loaded;  // bit p set when part p of expert e is resident
+  struct Shared {  // qwen2moe shared expert (transformer.rs:572-587), GGUF bytes verbatim
+    bool on = false;
+    int64_t n_ff = 0;
+    int32_t type[3] = {0, 0, 0};
+    uint8_t *arena = nullptr;
+    size_t off[3] = {0, 0, 0}, len[3] = {0, 0, 0};
+    float *gate_inp = nullptr;  // [n_embd] f32, inside the arena
+    bool gate_ok = false;
+    uint8_t loaded = 0;
+    size_t reserved = 0;
+  } sh;
 };
 
 struct Event2 {
@@ -294,6 +305,39 @@ int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t c
   return KMOE_OK;
 }
 
+// Scratch for one int8-quantized activation matrix [s_rows, cols].
+struct QRows {
+  int8_t *q;
+  float *d;
+  int32_t *s;
+};
+QRows carve_qrows(uint8_t *base, int64_t s_rows, int64_t cols, size_t *total) {
+  Carver cv{base};
+  QRows r{cv.take<int8_t>(s_rows * cols), cv.take<float>(s_rows * (cols / 32)), cv.take<int32_t>(s_rows * (cols / 16))};
+  *total = cv.off;
+  return r;
+}
+
+// quant::matmul (quant.rs:229-328) on validated arguments: F32 weights in the
+// reference's summation order; otherwise the context's regime picks the f32
+// GEMM or int8 activations (quantized into qr) and the int8 matvec.
+int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const float *x, int64_t s_rows,
+                float *out, const QRows &qr) {
+  if (t == KMOE_F32) {  // quant.rs:242 (s_rows >= 4) or :311-327 (dequant + quant::dot): summation order kept
+    if (rows > (int64_t)INT32_MAX) return fail(c, KMOE_E_INVALID, "too many rows");
+    LAUNCH(c, "matmul_f32_ordered",
+           launch_router_logits(c->stream, (const float *)w, (int32_t)rows, cols, x, s_rows, out));
+    return KMOE_OK;
+  }
+  if (!int_path(c->regime, s_rows)) {
+    LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out));
+    return KMOE_OK;
+  }
+  if (t == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
+  else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
+  return matvec_q8_impl(c, t, w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);
+}
+
 }  // namespace
 
 extern "C" {
@@ -333,6 +377,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   for (auto &kv : c->layers) {
     (void)hipFree(kv.second.arena);
     (void)hipFree(kv.second.router);
+    if (kv.second.sh.arena) (void)hipFree(kv.second.sh.arena);
   }
   for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
   if (c->ws) (void)hipFree(c->ws);
@@ -505,30 +550,17 @@ int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, i
   if (rows == 0 || s_rows == 0) return KMOE_OK;
   if (!w || !x || !out) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
-  if (t == KMOE_F32) {  // quant.rs:242 (s_rows >= 4) or :311-327 (dequant + quant::dot): summation order kept
-    if (rows > (int64_t)INT32_MAX) return fail(c, KMOE_E_INVALID, "too many rows");
-    LAUNCH(c, "matmul_f32_ordered",
-           launch_router_logits(c->stream, (const float *)w, (int32_t)rows, cols, x, s_rows, out));
-    return KMOE_OK;
+  if (t != KMOE_F32) {
+    int rc = check_quant_shape(c, t, cols);
+    if (rc) return rc;
   }
-  int rc = check_quant_shape(c, t, cols);
+  // int8 activations are quantized into the workspace
+  size_t need = 0;
+  carve_qrows(nullptr, s_rows, cols, &need);
+  int rc = ensure_ws(c, need);
   if (rc) return rc;
-  if (!int_path(c->regime, s_rows)) {
-    LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, (const uint8_t *)w, rows, cols, x, s_rows, out));
-    return KMOE_OK;
-  }
-  // int8 activations, quantized into the workspace
-  size_t need = align_up((size_t)s_rows * cols) + align_up((size_t)s_rows * (cols / 32) * 4) +
-                align_up((size_t)s_rows * (cols / 16) * 4);
-  rc = ensure_ws(c, need);
-  if (rc) return rc;
-  Carver cv{c->ws};
-  int8_t *q = cv.take<int8_t>(s_rows * cols);
-  float *d = cv.take<float>(s_rows * (cols / 32));
-  int32_t *s = cv.take<int32_t>(s_rows * (cols / 16));
-  if (t == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, q, d, s));
-  else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, q, d, s));
-  return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, q, d, s, s_rows, out);
+  QRows qr = carve_qrows(c->ws, s_rows, cols, &need);
+  return matmul_core(c, t, (const uint8_t *)w, rows, cols, x, s_rows, out, qr);
 }
 
 int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const float *h, int64_t S, int32_t k,
@@ -637,6 +669,10 @@ int kmoe_layer_destroy(kmoe_ctx *c, uint32_t layer) {
   (void)hipFree(it->second.arena);
   (void)hipFree(it->second.router);
   release(c, it->second.reserved);
+  if (it->second.sh.arena) {
+    (void)hipFree(it->second.sh.arena);
+    release(c, it->second.sh.reserved);
+  }
   c->layers.erase(it);
   return KMOE_OK;
 }
@@ -710,6 +746,77 @@ int kmoe_expert_part(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, cons
   return KMOE_OK;
 }
 
+int kmoe_shared_expert_create(kmoe_ctx *c, uint32_t layer, int64_t n_ff, int32_t gate_type, int32_t up_type,
+                              int32_t down_type) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (L->sh.arena) return fail(c, KMOE_E_INVALID, "layer %u already has a shared expert", layer);
+  if (n_ff <= 0) return fail(c, KMOE_E_INVALID, "bad n_ff");
+  const int64_t d = L->desc.n_embd;
+  const int32_t ty[3] = {gate_type, up_type, down_type};
+  const int64_t cols[3] = {d, d, n_ff}, rows[3] = {n_ff, n_ff, d};
+  auto &S = L->sh;
+  size_t off = 0;
+  for (int p = 0; p < 3; ++p) {
+    if (block_size(ty[p]) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", ty[p]);
+    if (ty[p] != KMOE_F32) {
+      int rc = check_quant_shape(c, ty[p], cols[p]);
+      if (rc) return rc;
+    }
+    const int64_t rb = bytes_for(ty[p], cols[p]);
+    if (rb < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols[p]);
+    S.len[p] = (size_t)rb * (size_t)rows[p];
+    S.off[p] = off;
+    off += align_up(S.len[p]);
+  }
+  const size_t gate_off = off;
+  off += align_up((size_t)d * 4);
+  DeviceGuard g(c->device);
+  void *p = nullptr;
+  int rc = dev_alloc(c, off, &p, "shared expert");
+  if (rc) return rc;
+  S.arena = (uint8_t *)p;
+  S.reserved = off;
+  S.gate_inp = (float *)(S.arena + gate_off);
+  S.n_ff = n_ff;
+  for (int i = 0; i < 3; ++i) S.type[i] = ty[i];
+  S.on = true;
+  S.loaded = 0;
+  S.gate_ok = false;
+  return KMOE_OK;
+}
+
+int kmoe_shared_expert_upload(kmoe_ctx *c, uint32_t layer, int32_t part, const void *bytes, size_t len) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  auto &S = L->sh;
+  if (!S.arena) return fail(c, KMOE_E_NOT_LOADED, "layer %u has no shared expert", layer);
+  if (part < 0 || part > 2) return fail(c, KMOE_E_INVALID, "part %d", part);
+  if (!bytes || len != S.len[part]) return fail(c, KMOE_E_INVALID, "shared part bytes %zu != %zu", len, S.len[part]);
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(S.arena + S.off[part], bytes, len, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  S.loaded |= (uint8_t)(1u << part);
+  return KMOE_OK;
+}
+
+int kmoe_shared_gate_upload(kmoe_ctx *c, uint32_t layer, const float *gate_inp, size_t bytes) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  auto &S = L->sh;
+  if (!S.arena) return fail(c, KMOE_E_NOT_LOADED, "layer %u has no shared expert", layer);
+  const size_t need = (size_t)L->desc.n_embd * 4;
+  if (!gate_inp || bytes != need) return fail(c, KMOE_E_INVALID, "gate bytes %zu != %zu", bytes, need);
+  DeviceGuard g(c->device);
+  HIP_OK(c, hipMemcpyAsync(S.gate_inp, gate_inp, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  S.gate_ok = true;
+  return KMOE_OK;
+}
+
 int kmoe_expert_read(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, void *host, size_t len) {
   if (!c) return KMOE_E_INVALID;
   const void *src = nullptr;
@@ -751,14 +858,28 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   if (!L->router_ok) return fail(c, KMOE_E_NOT_LOADED, "layer %u router not uploaded", layer);
   for (uint32_t e = 0; e < L->desc.n_expert; ++e)
     if (L->loaded[e] != 7) return fail(c, KMOE_E_NOT_LOADED, "layer %u expert %u not resident", layer, e);
+  if (L->sh.on && L->sh.loaded != 7) return fail(c, KMOE_E_NOT_LOADED, "layer %u shared expert not resident", layer);
   const kmoe_moe_desc &D = L->desc;
   const int64_t E = D.n_expert, k = D.n_expert_used, d = D.n_embd, F = D.n_ff;
   const int64_t slots = S * k;
   if (slots > (int64_t)UINT32_MAX / 2) return fail(c, KMOE_E_INVALID, "too many tokens");
   size_t need = 0;
   carve_moe(nullptr, S, E, k, d, F, &need);
+  const size_t moe_need = align_up(need);
+  size_t sh_need = 0;
+  const int64_t Fs = L->sh.n_ff, mx = d > Fs ? d : Fs;
+  if (L->sh.on) {  // gs, us [S, Fs], ys [S, d], gate logits [S], int8 scratch [S, max(d, Fs)]
+    Carver cv{nullptr};
+    cv.take<float>(S * Fs);
+    cv.take<float>(S * Fs);
+    cv.take<float>(S * d);
+    cv.take<float>(S);
+    size_t q = 0;
+    carve_qrows(nullptr, S, mx, &q);
+    sh_need = cv.off + align_up(q);
+  }
   DeviceGuard g(c->device);
-  int rc = ensure_ws(c, need);
+  int rc = ensure_ws(c, moe_need + sh_need);
   if (rc) return rc;
   size_t tmp;
   MoeWs w = carve_moe(c->ws, S, E, k, d, F, &tmp);
@@ -848,6 +969,22 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
 
 done:
+  if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)
+    auto &SH = L->sh;
+    Carver cv{c->ws + moe_need};
+    float *gs = cv.take<float>(S * Fs), *us = cv.take<float>(S * Fs), *ys = cv.take<float>(S * d);
+    float *gl = cv.take<float>(S);
+    size_t q = 0;
+    QRows qr = carve_qrows(c->ws + moe_need + cv.off, S, mx, &q);
+    rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
+    if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
+    if (rc) return rc;
+    LAUNCH(c, "shared_swiglu", launch_swiglu(st, gs, us, S * Fs));
+    rc = matmul_core(c, SH.type[2], SH.arena + SH.off[2], d, Fs, gs, S, ys, qr);
+    if (rc) return rc;
+    if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, gl, true));
+    LAUNCH(c, "shared_add", launch_shared_add(st, out, ys, SH.gate_ok ? gl : nullptr, S, d));
+  }
   c->last_idx = w.idx;
   c->last_w = w.wsel;
   c->last_perm = w.perm;

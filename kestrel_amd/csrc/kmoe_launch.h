@@ -95,9 +95,10 @@ hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &
                           const float *x, float *out);
 
 // ---- routing (kmoe_route.hip)
-// logits [S, E] = router [E, d] . x [S, d] in the reference's summation order.
+// logits [S, E] = router [E, d] . x [S, d] in the reference's summation order
+// for s_rows (quant::matmul), or always in quant::dot order when qdot is set.
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
-                                int64_t s_rows, float *logits);
+                                int64_t s_rows, float *logits, bool qdot = false);
 hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w);
 // Decode routing (s_rows < 4): quant::dot-order logits (one work-group per
@@ -117,6 +118,12 @@ hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots,
 hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t n_slots, int64_t cols,
                               const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
                               int32_t *sums);
+// ---- shared expert (kmoe_shared.hip)
+// g = g / (1 + exp(-g)) * u over n elements.
+hipError_t launch_swiglu(hipStream_t st, float *g, const float *u, int64_t n);
+// out[s] += sigmoid(logits[s]) * y[s] (logits null: scale 1).
+hipError_t launch_shared_add(hipStream_t st, float *out, const float *y, const float *logits, int64_t S, int64_t d);
+
 // out[s] = sum over the token's experts in ascending id of w * y[slot].
 hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out);
 

@@ -31,14 +31,14 @@ __device__ __forceinline__ float hsum8(const float *v) {
 
 __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__ W, int32_t E, int64_t d,
                                                        const float *__restrict__ X, int64_t S,
-                                                       float *__restrict__ logits) {
+                                                       float *__restrict__ logits, int qdot) {
   const int l16 = threadIdx.x & 15;
   const int64_t pair = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const bool valid = pair < S * E;
   const int64_t s = valid ? pair / E : 0;
   const int e = valid ? (int)(pair % E) : 0;
   int ord;
-  if (S < 4 || (d % 8) != 0) {
+  if (qdot || S < 4 || (d % 8) != 0) {
     ord = ORD_QDOT;
   } else {
     const int64_t s4 = S / 4 * 4;
@@ -625,11 +625,11 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
 }  // namespace
 
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
-                                int64_t s_rows, float *logits) {
+                                int64_t s_rows, float *logits, bool qdot) {
   const int64_t pairs = s_rows * n_expert;
   if (pairs == 0) return hipSuccess;
   KMOE_LAUNCH(k_router_logits, dim3((unsigned)((pairs + 15) / 16)), dim3(256), 0, st, router, n_expert, d, x,
-                     s_rows, logits);
+                     s_rows, logits, qdot ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -56,6 +56,9 @@ SIGNATURES = {
     "kmoe_expert_is_ready": (C.c_int, [_P, _u32, _u32]),
     "kmoe_expert_part": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_P), C.POINTER(_sz)]),
     "kmoe_expert_read": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
+    "kmoe_shared_expert_create": (C.c_int, [_P, _u32, _i64, _i32, _i32, _i32]),
+    "kmoe_shared_expert_upload": (C.c_int, [_P, _u32, _i32, _P, _sz]),
+    "kmoe_shared_gate_upload": (C.c_int, [_P, _u32, _P, _sz]),
     "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
     "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
@@ -267,6 +270,17 @@ class Context:
         buf = np.empty(n, np.uint8)
         self.check(self.lib.kmoe_expert_read(self.h, layer, e, part, buf.ctypes.data, n))
         return buf
+
+    def shared_expert(self, layer: int, n_ff: int, types, gate, up, down, gate_inp=None):
+        """Attach a shared expert (transformer.rs:572-587): GGUF bytes (numpy
+        uint8) of ffn_{gate,up,down}_shexp and the optional F32 gate vector."""
+        self.check(self.lib.kmoe_shared_expert_create(self.h, layer, n_ff, *types))
+        for p, b in enumerate((gate, up, down)):
+            b = np.ascontiguousarray(b, dtype=np.uint8)
+            self.check(self.lib.kmoe_shared_expert_upload(self.h, layer, p, b.ctypes.data, b.nbytes))
+        if gate_inp is not None:
+            g = np.ascontiguousarray(gate_inp, dtype=np.float32)
+            self.check(self.lib.kmoe_shared_gate_upload(self.h, layer, g.ctypes.data, g.nbytes))
 
     def bytes_per_expert(self, layer: int) -> int:
         v = _u64()

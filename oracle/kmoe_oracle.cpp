@@ -1106,6 +1106,44 @@ int orc_moe_ffn(const orc_moe_layer *L, const float *h, size_t s_rows, float *ou
 }
 
 // ---------------------------------------------------------------------------
+// Shared expert, transformer.rs:572-587: g = mm(gate, h), u = mm(up, h),
+// g = g / (1 + exp(-g)) * u, y = mm(down, g); scale per token by
+// 1 / (1 + exp(-quant::dot(gate_inp, h[s]))) (or 1); out[s] += scale * y[s].
+
+int orc_shared_expert_add(const orc_shared_expert *S, const float *h, size_t s_rows, float *out, int regime,
+                          int threads) {
+  const size_t d = (size_t)S->n_embd, ff = (size_t)S->n_ff;
+  const int64_t gb = orc_bytes_for(S->gate_type, (int64_t)d), ub = orc_bytes_for(S->up_type, (int64_t)d),
+                db = orc_bytes_for(S->down_type, (int64_t)ff);
+  if (gb < 0 || ub < 0 || db < 0) return -1;
+  std::vector<float> g(s_rows * ff), u(s_rows * ff), y(s_rows * d);
+  int rc = orc_matmul(S->gate_type, S->gate, (size_t)gb * ff, ff, d, h, s_rows, g.data(), regime, threads);
+  if (!rc) rc = orc_matmul(S->up_type, S->up, (size_t)ub * ff, ff, d, h, s_rows, u.data(), regime, threads);
+  if (rc) return rc;
+  for (size_t i = 0; i < s_rows * ff; ++i) {
+    float gv = g[i];
+    float den = 1.0f + expf(-gv);
+    float q = gv / den;
+    g[i] = q * u[i];
+  }
+  rc = orc_matmul(S->down_type, S->down, (size_t)db * d, d, ff, g.data(), s_rows, y.data(), regime, threads);
+  if (rc) return rc;
+  for (size_t s = 0; s < s_rows; ++s) {
+    float scale = 1.0f;
+    if (S->gate_inp) {
+      float t = orc_quant_dot(S->gate_inp, h + s * d, d);
+      float den = 1.0f + expf(-t);
+      scale = 1.0f / den;
+    }
+    for (size_t c = 0; c < d; ++c) {
+      float p = scale * y[s * d + c];
+      out[s * d + c] = out[s * d + c] + p;
+    }
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
 // bench_gemv, quant.rs:348-368
 
 double orc_bench_gemv(int t, size_t rows, size_t cols, size_t iters, int threads) {

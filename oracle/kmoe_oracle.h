@@ -131,6 +131,20 @@ void orc_dispatch(const uint32_t *idx, size_t s_rows, int k, int n_expert, uint3
 /* Transformer::moe_ffn without the shared expert (transformer.rs:513-570). */
 int orc_moe_ffn(const orc_moe_layer *L, const float *h, size_t s_rows, float *out, int regime, int threads);
 
+/* Shared expert of a layer (qwen2moe, transformer.rs:572-587): dense tensors
+ * ffn_{gate,up}_shexp [n_ff, n_embd], ffn_down_shexp [n_embd, n_ff] (GGUF bytes)
+ * and the optional F32 gate vector ffn_gate_inp_shexp [n_embd]. */
+typedef struct {
+  int64_t n_embd, n_ff;
+  int32_t gate_type, up_type, down_type;
+  const uint8_t *gate, *up, *down;
+  const float *gate_inp; /* NULL: scale 1 */
+} orc_shared_expert;
+/* out[s] += g_s * SwiGLU-FFN(h[s]), g_s = 1/(1+exp(-quant::dot(gate_inp, h[s]))) or 1;
+ * the three products are quant::matmul over all s_rows rows (Transformer::mm). */
+int orc_shared_expert_add(const orc_shared_expert *S, const float *h, size_t s_rows, float *out, int regime,
+                          int threads);
+
 /* ---- bench_gemv, quant.rs:348-368: weight bytes per second ---- */
 double orc_bench_gemv(int t, size_t rows, size_t cols, size_t iters, int threads);
 

@@ -44,6 +44,22 @@ class MoeLayer(C.Structure):
     ]
 
 
+class SharedExpert(C.Structure):
+    """orc_shared_expert (kmoe_oracle.h)."""
+
+    _fields_ = [
+        ("n_embd", C.c_int64),
+        ("n_ff", C.c_int64),
+        ("gate_type", C.c_int32),
+        ("up_type", C.c_int32),
+        ("down_type", C.c_int32),
+        ("gate", _P),
+        ("up", _P),
+        ("down", _P),
+        ("gate_inp", _P),
+    ]
+
+
 _lib = None
 
 
@@ -85,6 +101,7 @@ def lib():
             "orc_route_from_logits": (None, [_P, _sz, C.c_int, C.c_int, C.c_int, C.c_float, _P, _P]),
             "orc_dispatch": (None, [_P, _sz, C.c_int, C.c_int, _P, _P]),
             "orc_moe_ffn": (C.c_int, [C.POINTER(MoeLayer), _P, _sz, _P, C.c_int, C.c_int]),
+            "orc_shared_expert_add": (C.c_int, [C.POINTER(SharedExpert), _P, _sz, _P, C.c_int, C.c_int]),
             "orc_bench_gemv": (C.c_double, [C.c_int, _sz, _sz, _sz, C.c_int]),
             "orc_hw_threads": (C.c_int, []),
         }
@@ -253,6 +270,21 @@ class Layer:
         if rc != 0:
             raise ValueError(f"orc_moe_ffn failed rc={rc}")
         return out
+
+
+def shared_expert_add(out: np.ndarray, h: np.ndarray, d: int, ff: int, types, gate, up, down, gate_inp=None,
+                      regime: int = REGIME_AVX2, threads: int = 0) -> np.ndarray:
+    """transformer.rs:572-587 applied to a copy of out [S, d]; returns it."""
+    h = np.ascontiguousarray(np.atleast_2d(h), dtype=np.float32)
+    o = np.array(out, dtype=np.float32, copy=True).reshape(h.shape[0], d)
+    bufs = [np.ascontiguousarray(b, dtype=np.uint8) for b in (gate, up, down)]
+    gi = None if gate_inp is None else np.ascontiguousarray(gate_inp, dtype=np.float32)
+    sx = SharedExpert(d, ff, types[0], types[1], types[2], bufs[0].ctypes.data, bufs[1].ctypes.data,
+                      bufs[2].ctypes.data, None if gi is None else gi.ctypes.data)
+    rc = lib().orc_shared_expert_add(C.byref(sx), _p(h), h.shape[0], _p(o), regime, threads)
+    if rc != 0:
+        raise ValueError(f"orc_shared_expert_add failed rc={rc}")
+    return o
 
 
 def route_from_logits(logits: np.ndarray, k: int, norm_topk=True, weights_scale=0.0):

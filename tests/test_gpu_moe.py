@@ -246,3 +246,50 @@ def test_device_generated_weights_are_stream_ordered(ctx, orc):
     ref = L.moe_ffn(h.cpu().numpy())
     assert np.isfinite(out).all()
     assert rel_l2(out, ref) < TOL
+
+
+# --------------------------------------------------------------- shared expert
+@pytest.mark.parametrize("wtype,ffs", [(Q8_0, 1024), (Q4_K, 1536)])
+@pytest.mark.parametrize("with_gate", [False, True])
+def test_shared_expert_layer(ctx, orc, wtype, ffs, with_gate):
+    """qwen2moe layer (transformer.rs:572-587): routed experts plus a shared
+    expert scaled by sigmoid(quant::dot(ffn_gate_inp_shexp, h)) or 1."""
+    d, ff = 1024, 512
+    spec = LayerSpec(8, 2, d, ff, wtype, seed=31 + wtype)
+    sh = [orc.quantize(wtype, orc.normal(900 + p, (ffs * d), 0.0, 0.02).reshape(*((ffs, d) if p < 2 else (d, ffs))))
+          for p in range(3)]
+    gi = orc.normal(950, d, 0.0, 0.05) if with_gate else None
+    L = spec.oracle_layer()
+    for S, regime in [(1, 0), (3, 0), (6, 0), (5, 1), (4, 2)]:
+        lid = _layer_id[0]
+        _layer_id[0] += 1
+        spec.upload(ctx, lid)
+        try:
+            ctx.shared_expert(lid, ffs, (wtype, wtype, wtype), sh[0], sh[1], sh[2], gi)
+            h = orc.normal(960 + S, S * d).reshape(S, d)
+            ctx.set_regime(regime)
+            out = host(ctx.moe_ffn(lid, dev(h)))
+        finally:
+            ctx.set_regime(0)
+            ctx.layer_destroy(lid)
+        ref = orc.shared_expert_add(L.moe_ffn(h, regime), h, d, ffs, (wtype, wtype, wtype), sh[0], sh[1], sh[2], gi,
+                                    regime)
+        e = rel_l2(out, ref)
+        assert e < TOL, (S, regime, e)
+
+
+def test_shared_expert_errors(ctx):
+    from kestrel_amd.kmoe import KmoeError
+
+    ctx.layer_create(97, 8, 2, 256, 256, Q8_0, Q8_0, Q8_0)
+    try:
+        with pytest.raises(KmoeError) as e:  # gate vector before the shared expert exists
+            ctx.check(ctx.lib.kmoe_shared_gate_upload(ctx.h, 97, None, 0))
+        assert e.value.status == -5
+        ctx.check(ctx.lib.kmoe_shared_expert_create(ctx.h, 97, 512, Q8_0, Q8_0, Q8_0))
+        with pytest.raises(KmoeError) as e:  # wrong part size
+            b = np.zeros(10, np.uint8)
+            ctx.check(ctx.lib.kmoe_shared_expert_upload(ctx.h, 97, 0, b.ctypes.data, b.nbytes))
+        assert e.value.status == -1
+    finally:
+        ctx.layer_destroy(97)

@@ -315,3 +315,40 @@ def test_matmul_thread_count_independent(orc):
 def test_bench_gemv_runs(orc):
     # quant.rs:348-368 (small sizes here; the full metric runs in bench.py)
     assert orc.bench_gemv(Q4_K, 256, 4096, 2, 1) > 0
+
+
+# ------------------------------------------------------------- shared expert
+def _shared_case(orc, S, t, seed):
+    from tests.helpers import LayerSpec
+
+    d, ff = 1024, 768 if t == Q4_K else 512
+    spec = LayerSpec(1, 1, d, ff, t, seed=seed)
+    h = orc.normal(seed + 5, S * d).reshape(S, d)
+    return spec, h, d, ff
+
+
+@pytest.mark.parametrize("S", [1, 3, 4, 9])
+@pytest.mark.parametrize("regime", [0, 1, 2])
+def test_shared_expert_equals_single_expert_layer(orc, S, regime):
+    """With no gate vector the shared expert adds exactly what a 1-expert, top-1
+    layer with the same tensors computes: routing gives weight exp(0)/1 = 1 to
+    every row and its matmul runs over the same S rows (same regime)."""
+    for t in (Q8_0, Q4_K):
+        spec, h, d, ff = _shared_case(orc, S, t, seed=S + 10 * regime)
+        ref = spec.oracle_layer().moe_ffn(h, regime)
+        got = orc.shared_expert_add(np.zeros((S, d), np.float32), h, d, ff, (t, t, t), spec.gate[0], spec.up[0],
+                                    spec.down[0], None, regime)
+        assert np.array_equal(got, ref)
+
+
+def test_shared_expert_gate_is_sigmoid_of_quant_dot(orc):
+    S, t = 5, Q8_0
+    spec, h, d, ff = _shared_case(orc, S, t, seed=3)
+    gi = orc.normal(77, d, 0.0, 0.05)
+    y = orc.shared_expert_add(np.zeros((S, d), np.float32), h, d, ff, (t, t, t), spec.gate[0], spec.up[0],
+                              spec.down[0], None)
+    base = orc.normal(78, S * d).reshape(S, d)
+    got = orc.shared_expert_add(base, h, d, ff, (t, t, t), spec.gate[0], spec.up[0], spec.down[0], gi)
+    g = 1.0 / (1.0 + np.exp(-(h.astype(np.float64) @ gi.astype(np.float64))))
+    want = base.astype(np.float64) + g[:, None] * y.astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
