@@ -185,8 +185,11 @@ def main():
             kern[n] = {"avg_us": round(ms * 1000.0 / cnt, 3), "launches": cnt}
     ctx.profile_enable(False)
 
-    # ---- graph capture (one graph per layer) or eager
+    # ---- graph capture or eager. One graph holds a pass over all rotated
+    # layers (consecutive MoE layers, as a decode step's graph holds them);
+    # one graph per layer covers a step count that is not a multiple of it.
     graphs = None
+    whole = None
     if not a.no_graph:
         try:
             graphs = []
@@ -203,39 +206,50 @@ def main():
                     ctx.set_stream(torch.cuda.current_stream())
                     step(l)
                 graphs.append(g)
+            whole = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(whole):
+                ctx.set_stream(torch.cuda.current_stream())
+                for l in range(a.layers):
+                    step(l)
             ctx.set_stream(torch.cuda.current_stream())
-            # replay check against eager
+            # replay check against eager, for both graph forms
             ref = torch.empty_like(outs)
             for l in range(a.layers):
                 step(l)
             torch.cuda.synchronize()
             ref.copy_(outs)
-            outs.zero_()
-            for l in range(a.layers):
-                graphs[l].replay()
-            torch.cuda.synchronize()
-            if not torch.equal(ref, outs):
-                bad = [l for l in range(a.layers) if not torch.equal(ref[l], outs[l])]
-                raise RuntimeError(f"graph replay differs from eager on layers {bad}: max |diff| "
-                                   f"{(ref - outs).abs().max().item():.3e}, nan {int(torch.isnan(ref).sum())}/"
-                                   f"{int(torch.isnan(outs).sum())}")
+            for form in ("per-layer", "whole"):
+                outs.zero_()
+                if form == "whole":
+                    whole.replay()
+                else:
+                    for l in range(a.layers):
+                        graphs[l].replay()
+                torch.cuda.synchronize()
+                if not torch.equal(ref, outs):
+                    bad = [l for l in range(a.layers) if not torch.equal(ref[l], outs[l])]
+                    raise RuntimeError(f"{form} graph replay differs from eager on layers {bad}: max |diff| "
+                                       f"{(ref - outs).abs().max().item():.3e}")
         except Exception as ex:  # fall back to eager launches, and say so
             print(f"# graph capture unavailable: {ex}", file=sys.stderr)
-            graphs = None
+            graphs = whole = None
             ctx.set_stream(torch.cuda.current_stream())
 
-    def run(i):
-        if graphs is not None:
-            graphs[i % a.layers].replay()
-        else:
-            step(i)
+    def run_steps(n):
+        """n consecutive steps (layers 0, 1, ... rotating)."""
+        if graphs is None:
+            for i in range(n):
+                step(i)
+            return
+        for _ in range(n // a.layers):
+            whole.replay()
+        for l in range(n % a.layers):
+            graphs[l].replay()
 
-    for i in range(a.warmup):
-        run(i)
+    run_steps(a.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(a.steps):
-        run(i)
+    run_steps(a.steps)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     ms_step = el * 1000.0 / a.steps
@@ -298,7 +312,7 @@ def main():
         "config": {"workload": f"mixtral-8x7b-moe-layer-q4k-decode-b{S}", "hidden": D, "expert_ffn": FF,
                    "experts": E, "top_k": K, "tokens_per_step": S, "weights": "Q4_K random-init blocks",
                    "layers_rotated": a.layers, "regime": ["avx2", "int8", "exact"][a.regime],
-                   "launch": "hip-graph" if graphs is not None else "eager"},
+                   "launch": (f"hip-graph ({a.layers} layers per replay)" if graphs is not None else "eager")},
         "hbm_touched_GBps": round(touched / (ms_step * 1e-3) / 1e9, 1) if touched else None,
         "hbm_frac": round(touched / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4) if touched else None,
         "roofline": roof,

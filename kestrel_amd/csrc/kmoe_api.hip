@@ -890,17 +890,23 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531). With
   // s_rows < 4 one fused work-group also quantizes x for the int8 path.
   bool x_quantized = false;
+  // Single token on the int8 path with Q4_K experts: the router kernel only
+  // produces the logits (and the int8 row) and the gate/up kernel selects the
+  // experts itself, publishing the routing for the kernels after it.
+  bool select_in_gate_up = S == 1 && regime != KMOE_REGIME_EXACT &&
+                           decode_gate_up_can_select(gt, d, (int32_t)E, (int32_t)k);
   {
     const int qtype = regime == KMOE_REGIME_EXACT ? 0 : gt;
     hipError_t e = timed(c, "route_decode", [&]() {
       return launch_route_decode(st, L->router, (int32_t)E, d, h, (int32_t)S, (int32_t)k, D.norm_topk,
                                  D.weights_scale, w.logits, w.idx, w.wsel, w.perm, w.offsets, w.inv, w.n_active,
-                                 w.active, qtype, w.xq, w.xd, w.xs, c->counters);
+                                 w.active, qtype, w.xq, w.xd, w.xs, select_in_gate_up ? nullptr : c->counters);
     });
     if (e == hipSuccess) {
       x_quantized = qtype != 0;
     } else {
       if (e != hipErrorNotSupported) HIP_OK(c, e);
+      select_in_gate_up = false;
       LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
       LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
                                                 D.weights_scale, w.idx, w.wsel));
@@ -924,13 +930,38 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, 1, d, w.xq, w.xd, w.xs));
       x_quantized = true;
     }
+    DecSelect ds;
+    ds.logits = w.logits;
+    ds.E = (int32_t)E;
+    ds.K = (int32_t)k;
+    ds.norm_topk = D.norm_topk;
+    ds.weights_scale = D.weights_scale;
+    ds.idx = w.idx;
+    ds.wsel = w.wsel;
+    ds.perm = w.perm;
+    ds.offsets = w.offsets;
+    ds.inv = w.inv;
+    ds.n_active = w.n_active;
+    ds.active = w.active;
     hipError_t e = timed(c, "moe_gate_up_dec", [&]() {
-      return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h);
+      return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h,
+                                   select_in_gate_up ? &ds : nullptr);
     });
+    if (e == hipErrorNotSupported && select_in_gate_up) {  // complete the routing from the logits, then as below
+      LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
+                                                D.weights_scale, w.idx, w.wsel));
+      LAUNCH(c, "dispatch", launch_dispatch(st, w.idx, slots, (int32_t)E, w.perm, w.offsets, w.inv, w.n_active,
+                                            w.active, w.rank));
+      select_in_gate_up = false;
+      e = timed(c, "moe_gate_up_dec", [&]() {
+        return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h, nullptr);
+      });
+    }
     if (e != hipErrorNotSupported) {
       HIP_OK(c, e);
+      // one row per expert: every slot is on the int8 path in either int8 regime
       LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
-             launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
+             launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
       e = timed(c, "moe_down_dec",
                 [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out); });
       if (e != hipErrorNotSupported) {

@@ -98,6 +98,15 @@ __device__ __forceinline__ uint4 load_u4_a4(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Work-group barrier ordering LDS only: unlike __syncthreads it does not wait
+// for outstanding global loads, so loads issued for the next item stay in
+// flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Tiled Q4_K rows: the expert tier's HBM layout for Q4_K parts. A row of nb
 // superblocks keeps its 144*nb bytes, reordered:
 //   [0, 16*nb)       the 16-byte head (f16 d, f16 dmin, 12 scale bytes) of

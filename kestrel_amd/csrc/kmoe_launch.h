@@ -69,9 +69,40 @@ hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t
 // use the LDS-staged kernels.
 hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                                const int8_t *xq, const float *xd, const int32_t *xbs, float *out);
+struct DecSelect;
+// sel: the kernel selects the token's experts from its logits and writes the
+// routing (Q4_K only; hipErrorNotSupported otherwise).
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                 const int32_t *xbs, float *h);
+                                 const int32_t *xbs, float *h, const DecSelect *sel = nullptr);
+// Whether launch_decode_gate_up can select the experts for this layer shape.
+bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K);
+// Expert selection done inside the decode gate/up kernel: the token's logits
+// [E] and where to publish the routing (the arrays of Routing, writable).
+struct DecSelect {
+  const float *logits = nullptr;
+  int32_t E = 0, K = 0, norm_topk = 0;
+  float weights_scale = 0.0f;
+  uint32_t *idx = nullptr;
+  float *wsel = nullptr;
+  uint32_t *perm = nullptr, *offsets = nullptr, *inv = nullptr;
+  int32_t *n_active = nullptr, *active = nullptr;
+};
+// Tiled Q4_K gate/up + SwiGLU for one token (kmoe_decode.hip): RU rows per
+// wave step, about wg_per_cu_x16/16 work-groups per CU. With sel the kernel
+// selects the experts itself (E <= 256, max_active == K) and writes the
+// routing; without it the routing is read from rt. hipErrorNotSupported for
+// rows narrower than 48 quarters or wider than 128.
+bool dec_gate_up_tq4_supported(int64_t cols, int ru);
+hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
+                                  const int32_t *xbs, float *h, int ru, int wg_per_cu_x16,
+                                  const DecSelect *sel = nullptr);
+// Tiled Q4_K down projection + combine for one token (kmoe_decode.hip): the k
+// active slots' Q8_K rows staged in LDS, one wave per output row.
+bool dec_down_tq4_supported(int64_t rows, int64_t cols, int k);
+hipError_t launch_dec_down_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols, const Routing &rt,
+                               int k, const int8_t *hq, const float *hd, const int32_t *hbs, float *out);
 // Down projection + combine for one token: out[r] = sum_e (asc) w_e * y_e[r].
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
@@ -106,7 +137,8 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 // (perm/offsets/inv/active); int8 quantization of x when qtype is T_Q4_K
 // (Q8_K rows) or T_Q8_0 (Q8 rows). logits [S, E] is required; *done must be 0
 // and is 0 again when the kernel ends (calls on one counter must not overlap).
-// hipErrorNotSupported when out of range.
+// With done null only the logits and the int8 rows are produced (the caller's
+// next kernel selects the experts). hipErrorNotSupported when out of range.
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
                                int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
                                float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,

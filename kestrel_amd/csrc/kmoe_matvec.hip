@@ -633,7 +633,8 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
     Item im;
     const int ia = it / nb;
     const int e = a.rt.active[ia];
-    im.p = a.rt.offsets[e];
+    // one token: the ia-th active expert's single slot is at position ia
+    im.p = a.s_rows == 1 ? ia : a.rt.offsets[e];
     im.W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[2];
     im.rr = (it - ia * nb) * RU;
     return im;
@@ -656,6 +657,9 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   };
   // One (expert, row-batch) item; finishes the expert after its last batch.
   auto compute = [&](int it, const Item &ic, WTask<TYPE> (&w)[RU][TPL], ActSlice<TYPE> (&ac)[TPL]) {
+    const bool last = (it + 1) % nb == 0;  // this expert's last row batch
+    float wgt = 0.0f;
+    if (last) wgt = a.rt.wsel[a.rt.perm[ic.p]];  // issued early, used after the dots
     float acc[RU];
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
@@ -672,16 +676,16 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
       for (int u = 0; u < RU; ++u)
         if (ic.rr + u < nr) part[wave][ic.rr + u] = acc[u];
     }
-    if ((it + 1) % nb == 0) {  // this expert's rows are done: y = sum of the wave partials, combine
-      __syncthreads();
+    if (last) {  // y = sum of the wave partials, combine. LDS-only barriers: the
+                 // next item's weight loads stay in flight.
+      lds_barrier();
       if (threadIdx.x < nr) {
         const int t = threadIdx.x;
         const float y = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
-        const float wgt = a.rt.wsel[a.rt.perm[ic.p]];
         const float c = wgt * y;
         outv[t] = outv[t] + c;
       }
-      __syncthreads();
+      lds_barrier();
     }
   };
   // Ping-pong register sets (weights and activation slices): item it+1's
@@ -727,6 +731,31 @@ int env_int(const char *name, int dflt) {
 }
 int grid_mult() {
   static const int v = env_int("KMOE_GRID_MULT", 4);
+  return v;
+}
+// Tiled gate/up decode kernel: KMOE_GU_RU rows per wave step (1, 2 or 4,
+// default 2) and KMOE_GU_WGPC16 = 16 x work-groups per CU (default 32).
+int gu_ru() {
+  static const int v = env_int("KMOE_GU_RU", 2);
+  return v;
+}
+int gu_wgpc16() {
+  static const int v = env_int("KMOE_GU_WGPC16", 32);
+  return v;
+}
+// KMOE_DOWN_RU: rows per split-K item (1, 2 or 4, default 4).
+int down_ru() {
+  static const int v = env_int("KMOE_DOWN_RU", 4);
+  return v;
+}
+// KMOE_DOWN_KERNEL=rows selects the whole-row down kernel (activation rows
+// staged in LDS, one wave per output row) for single-token Q4_K down; the
+// default is the split-K kernel, measured as fast or faster on MI355X.
+bool use_dec_down() {
+  static const bool v = [] {
+    const char *e = getenv("KMOE_DOWN_KERNEL");
+    return e && !strcmp(e, "rows");
+  }();
   return v;
 }
 int down_wg_per_cu() {
@@ -869,9 +898,13 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   return hipErrorInvalidValue;
 }
 
+bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
+  return type == T_Q4_K && E <= 256 && K <= 16 && K <= E && dec_gate_up_tq4_supported(cols, gu_ru());
+}
+
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                 const int32_t *xbs, float *h) {
+                                 const int32_t *xbs, float *h, const DecSelect *sel) {
   MvArgs a{};
   a.rows = rows;
   a.cols = cols;
@@ -881,7 +914,13 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   a.out = h;
   a.tier = tier;
   a.rt = rt;
-  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
+  if (type == T_Q4_K) {
+    const hipError_t e =
+        launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel);
+    if (e != hipErrorNotSupported || sel) return e;
+    return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
+  }
+  if (sel) return hipErrorNotSupported;
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
   return hipErrorInvalidValue;
 }
@@ -890,6 +929,7 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
                                       float *out) {
   MvArgs a{};
+  a.s_rows = 1;
   a.rows = rows;
   a.cols = cols;
   a.xq = hq;
@@ -900,6 +940,9 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
   a.rt = rt;
   const int64_t nblk = type == T_Q4_K ? cols / 256 : cols / 32;
   const int ntasks = type == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  // one token: its topk experts are distinct, so k slots are active
+  if (type == T_Q4_K && use_dec_down() && dec_down_tq4_supported(rows, cols, rt.topk))
+    return launch_dec_down_tq4(st, tier, rows, cols, rt, rt.topk, hq, hd, hbs, out);
   if (ntasks >= 128 && ntasks <= 4 * 64 * 2) {
     // persistent split-K: one work-group per CU, rows split evenly
     const int64_t G = (int64_t)cu_count() * down_wg_per_cu();
@@ -908,8 +951,14 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
       const unsigned grid = (unsigned)((rows + rb - 1) / rb);
       const int tpl = (ntasks + 3) / 4 > 64 ? 2 : 1;
       if (type == T_Q4_K) {
-        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-        else KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        if (tpl == 1) {
+          const int ru = down_ru();
+          if (ru == 1) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 1, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+          else if (ru == 2) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+          else KMOE_LAUNCH((k_down_splitk<T_Q4_K, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        } else {
+          KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        }
       } else {
         if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q8_0, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
         else KMOE_LAUNCH((k_down_splitk<T_Q8_0, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);

@@ -17,6 +17,7 @@
 // One lane per chain (16 lanes per logit); lane 0 of the 16 combines them.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
+#include "kmoe_select.h"
 
 namespace kmoe {
 
@@ -341,39 +342,6 @@ struct RouteDecArgs {
 
 constexpr int kDecMaxD = 8192;  // columns whose products one work-group holds in LDS
 
-// Wave-uniform reductions: DPP inside each 16-lane row, then the four row
-// results read into scalars (no LDS round trips).
-__device__ __forceinline__ uint32_t wave_umax_u(uint32_t v) {
-  v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
-  const uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
-  return max(max(a, b), max(c, d));
-}
-__device__ __forceinline__ uint32_t wave_umin_u(uint32_t v) {
-  v = min(v, (uint32_t)dpp_i<kDppXor1>((int)v));
-  v = min(v, (uint32_t)dpp_i<kDppXor2>((int)v));
-  v = min(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
-  v = min(v, (uint32_t)dpp_i<kDppMirror>((int)v));
-  const uint32_t a = __builtin_amdgcn_readlane((int)v, 0), b = __builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane((int)v, 32), d = __builtin_amdgcn_readlane((int)v, 48);
-  return min(min(a, b), min(c, d));
-}
-__device__ __forceinline__ float wave_fmax_u(float v) {
-  v = fmaxf(v, dpp_f<kDppXor1>(v));
-  v = fmaxf(v, dpp_f<kDppXor2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_f<kDppMirror>(v));
-  const int iv = __builtin_bit_cast(int, v);
-  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
-  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
-  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
-  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
-  return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
 // Softmax, top-k and renormalisation (transformer.rs:479-495) for the S <= 3
 // tokens whose logits the work-groups wrote, then the dispatch (the stable
 // sort of the S*k flat slots by expert). Run by the last work-group to finish.
@@ -384,78 +352,20 @@ __device__ void route_dec_tail(const RouteDecArgs &a, float *P, uint32_t *sel, i
   const int E = a.E, K = a.k, n = a.S * a.k;
   if (wave < a.S) {
     const int s = wave;
-    float *p = P + s * kMaxExperts;
     float lv[NPER];
-    float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
       const int e = lane + 64 * i;
       // written by other work-groups of this launch: read past this CU's L1
       lv[i] = e < E ? __hip_atomic_load(a.logits + s * E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-      m = fmaxf(m, lv[i]);
     }
-    m = wave_fmax_u(m);
-#pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-      const int e = lane + 64 * i;
-      lv[i] = expf_cr(lv[i] - m);
-      if (e < E) p[e] = lv[i];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    float sum = -0.0f;  // in expert order
-    if (lane == 0) {
-      int e = 0;
-      for (; e + 4 <= E; e += 4) {
-        const float4 v = *(const float4 *)(p + e);
-        sum = sum + v.x;
-        sum = sum + v.y;
-        sum = sum + v.z;
-        sum = sum + v.w;
-      }
-      for (; e < E; ++e) sum = sum + p[e];
-    }
-    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
-#pragma unroll
-    for (int i = 0; i < NPER; ++i) lv[i] = lv[i] / sum;
-    // k rounds: largest p (compared as bits: p >= +0), ties to the lower expert index
-    uint32_t taken = 0;
+    uint32_t sj[16];
     float wk[16];
-    for (int j = 0; j < K; ++j) {
-      uint32_t best = 0;
-      int bi = NPER;
-#pragma unroll
-      for (int i = 0; i < NPER; ++i) {
-        const int e = lane + 64 * i;
-        const uint32_t u = __float_as_uint(lv[i]);
-        if (e < E && !((taken >> i) & 1u) && (bi == NPER || u > best)) {
-          best = u;
-          bi = i;
-        }
-      }
-      const uint32_t mx = wave_umax_u(bi == NPER ? 0u : best);
-      const bool has = bi != NPER && best == mx;
-      const uint32_t es = wave_umin_u(has ? (uint32_t)(64 * bi + lane) : 0xffffffffu);
-      const int ib = (int)(es >> 6), lw = (int)(es & 63);
-      if (lane == lw) taken |= 1u << ib;
-      float mine = lv[0];
-#pragma unroll
-      for (int i = 1; i < NPER; ++i) mine = i == ib ? lv[i] : mine;
-      wk[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), lw));
-      if (lane == 0) sel[s * K + j] = es;
-    }
+    wave_route_one<NPER>(lv, E, K, a.norm_topk, a.weights_scale, P + s * kMaxExperts, sj, wk);
     if (lane == 0) {
-      if (a.norm_topk) {
-        float ss = -0.0f;
-        for (int j = 0; j < K; ++j) ss = ss + wk[j];
-        ss = fmaxf(ss, 6.103515625e-05f);
-        for (int j = 0; j < K; ++j) wk[j] = wk[j] / ss;
-      }
-      if (a.weights_scale != 0.0f && a.weights_scale != 1.0f)
-        for (int j = 0; j < K; ++j) wk[j] = wk[j] * a.weights_scale;
       for (int j = 0; j < K; ++j) {
-        a.idx[s * K + j] = sel[s * K + j];
+        sel[s * K + j] = sj[j];
+        a.idx[s * K + j] = sj[j];
         a.wsel[s * K + j] = wk[j];
       }
     }
@@ -607,6 +517,7 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
       }
     }
   }
+  if (!a.done) return;  // logits only: the selection happens in the next kernel
   __syncthreads();
   if (tid == 0) {
     __threadfence();  // this work-group's logits and int8 rows before the count
@@ -686,7 +597,7 @@ hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, i
                                int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done) {
   if (S < 1 || S > 3 || E < 1 || E > kMaxExperts || k < 1 || k > 16 || k > E || S * k > 48) return hipErrorNotSupported;
   if (d < 8 || d > kDecMaxD) return hipErrorNotSupported;
-  if (!logits || !done) return hipErrorInvalidValue;
+  if (!logits) return hipErrorInvalidValue;
   const int vec = d % 4 == 0 && ((uintptr_t)router & 15) == 0 && ((uintptr_t)x & 15) == 0;
   RouteDecArgs a{router, E, d, x, S, k, norm_topk, weights_scale, logits, idx, w, perm, offsets, inv, n_active, active,
                  qtype, xq, xd, xs, done, vec};
