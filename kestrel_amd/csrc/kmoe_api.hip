@@ -296,6 +296,13 @@ bool int_path(int regime, int64_t s_rows) {
 int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *q, const float *d,
                    const int32_t *s, int64_t s_rows, float *out) {
   const char *name = t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q8_0";
+  if (t == KMOE_Q4_K && s_rows >= mfma_min_rows()) {  // int8 matrix cores
+    hipError_t e = timed(c, "matvec_q4k_mfma", [&]() {
+      return launch_plain_mfma(c->stream, w, rows, cols, q, d, s, s_rows, out, nullptr, nullptr);
+    });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
   if (s_rows == 1) {
     hipError_t e = timed(c, name, [&]() { return launch_decode_plain(c->stream, t, w, rows, cols, q, d, s, out); });
     if (e == hipSuccess) return KMOE_OK;
@@ -520,6 +527,14 @@ int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, 
   if (rows == 0 || s_rows == 0) return KMOE_OK;
   if (!w || !q || !bs || !sumi || !mins) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
+  if (s_rows >= mfma_min_rows()) {  // the matrix-core kernel's integers (same rows as the matmul above)
+    hipError_t e = timed(c, "block_sums_q4k_mfma", [&]() {
+      return launch_plain_mfma(c->stream, (const uint8_t *)w, rows, cols, q, nullptr, bs, s_rows, nullptr, sumi,
+                               mins);
+    });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
   LAUNCH(c, "block_sums_q4k",
          launch_block_sums(c->stream, KMOE_Q4_K, (const uint8_t *)w, rows, cols, q, bs, s_rows, sumi, mins));
   return KMOE_OK;
@@ -921,6 +936,8 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // Which regimes can occur: an expert has at most S rows.
   const bool any_int = regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2);
   const bool any_f32 = regime == KMOE_REGIME_EXACT || (regime == KMOE_REGIME_AVX2 && S >= 4);
+  // Int8 regime with many token rows: grouped products on the int8 matrix cores.
+  const bool mfma = regime == KMOE_REGIME_INT8 && S >= mfma_min_rows();
 
   // Single token, int8 path: every routed expert has one row. gate/up+SwiGLU
   // and down+combine run as register-resident decode kernels.
@@ -981,8 +998,15 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
       if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
     }
-    LAUNCH(c, "moe_gate_up_int",
-           launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
+    hipError_t e = hipErrorNotSupported;
+    if (mfma && gt == KMOE_Q4_K)
+      e = timed(c, "moe_gate_up_mfma", [&]() {
+        return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h);
+      });
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+    else
+      LAUNCH(c, "moe_gate_up_int",
+             launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
   }
   if (any_f32) {
     LAUNCH(c, "moe_gate_f32", launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, h, w.h));
@@ -992,8 +1016,15 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   if (any_int) {
     LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
            launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
-    LAUNCH(c, "moe_down_int",
-           launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
+    hipError_t e = hipErrorNotSupported;
+    if (mfma && dt == KMOE_Q4_K)
+      e = timed(c, "moe_down_mfma", [&]() {
+        return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y);
+      });
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+    else
+      LAUNCH(c, "moe_down_int",
+             launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
   }
   if (any_f32) LAUNCH(c, "moe_down_f32", launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, w.h, w.y));
   // combine (transformer.rs:566-570)

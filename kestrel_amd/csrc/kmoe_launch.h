@@ -116,6 +116,21 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
                           const float *xd, const int32_t *xbs, float *out);
 
+// ---- int8 matrix-core path (kmoe_mfma.hip), Q4_K weights x Q8_K rows
+// Token rows at which the matrix-core kernels take over (KMOE_MFMA_MIN_ROWS, default 8).
+int mfma_min_rows();
+bool moe_mfma_supported(int64_t rows, int64_t cols);
+// Grouped over the expert tier, as launch_moe_int (mode 0 gate/up + SwiGLU, 1 down).
+// hipErrorNotSupported: shape or activation alignment (16 B) not covered.
+hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
+                           const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
+                           const int32_t *abs, float *out);
+// Plain GGUF rows: out[s*rows + r], or, with sumi/mins set, the per-block
+// integer accumulators at [(s*rows + r)*nb + b] (ad unused).
+hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *aq,
+                             const float *ad, const int32_t *abs, int64_t s_rows, float *out, int32_t *sumi,
+                             int32_t *mins);
+
 // ---- f32 path (kmoe_gemm_f32.hip): dequantized weights x f32 activations
 // Plain: out[s*rows + r].
 hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const float *x,

@@ -64,12 +64,36 @@ def test_quantize_q8_bit_exact(ctx, orc, rows, cols):
     assert np.array_equal(host(s16), rs)
 
 
-@pytest.mark.parametrize("rows,cols,S", [(64, 4096, 1), (37, 14336, 2), (16, 2048, 3), (9, 768, 1), (130, 4096, 3)])
+# S >= 8 runs the int8 matrix-core kernel (ragged row tiles, several 128-row token passes).
+@pytest.mark.parametrize("rows,cols,S", [(64, 4096, 1), (37, 14336, 2), (16, 2048, 3), (9, 768, 1), (130, 4096, 3),
+                                         (70, 4096, 8), (33, 768, 40), (130, 1024, 200), (64, 14336, 9)])
 def test_q4k_block_sums_bit_exact(ctx, orc, rows, cols, S):
     w = random_blocks(Q4_K, rows, cols, seed=rows + cols)
     w[:: 144 * 5 + 7] = 0xFF  # every scale/min/nibble pattern, including the 6-bit high bits
     x = orc.normal(cols + S, S * cols).reshape(S, cols)
     q, d, bs = orc.q8k_quantize(x)
+    sumi, mins = ctx.q4k_block_sums(dev(w), rows, cols, dev(q), dev(bs))
+    sumi, mins = host(sumi), host(mins)
+    rb = row_bytes(Q4_K, cols)
+    for s in range(S):
+        for r in range(rows):
+            es, em = orc.q4k_block_acc(w[r * rb:(r + 1) * rb], cols, q[s], bs[s])
+            assert np.array_equal(sumi[s, r], es), (s, r)
+            assert np.array_equal(mins[s, r], em), (s, r)
+
+
+@pytest.mark.parametrize("S", [1, 8, 33])
+def test_q4k_block_sums_extreme_ranges(ctx, orc, S):
+    """Largest integer magnitudes: every activation +-127 (16-sums +-2032), every
+    6-bit scale and min 63, every nibble 15, next to all-zero superblocks."""
+    rows, cols = 40, 1024
+    w = np.full(rows * row_bytes(Q4_K, cols), 0xFF, np.uint8)
+    w[: 144 * 3] = 0
+    sign = np.where(orc.normal(5 + S, S * cols).reshape(S, cols) < 0, -1.0, 1.0).astype(np.float32)
+    sign[:, 256:512] = 1.0  # a superblock of all +127
+    sign[:, 512:768] = -1.0  # and one of all -127
+    q, d, bs = orc.q8k_quantize(sign * 3.0)
+    assert np.abs(q).min() == 127
     sumi, mins = ctx.q4k_block_sums(dev(w), rows, cols, dev(q), dev(bs))
     sumi, mins = host(sumi), host(mins)
     rb = row_bytes(Q4_K, cols)

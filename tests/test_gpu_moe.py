@@ -103,6 +103,25 @@ def test_mixtral_shape_decode_b1(ctx, orc):
     check(run_layer(ctx, orc, spec, 1, 0, seed=11))
 
 
+def test_mixtral_shape_prefill_512_int8(ctx, orc):
+    """Config 3 at 512 tokens on the int path for every row (the int8
+    matrix-core kernels): about 128 rows per expert, so some experts take a
+    second 128-row pass."""
+    spec = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=3, quantized=False)
+    r = run_layer(ctx, orc, spec, 512, 1, seed=12)
+    counts = np.diff(r["off"].astype(np.int64))
+    assert counts.max() > 128, counts
+    check(r)
+
+
+@pytest.mark.parametrize("S,E,k", [(300, 4, 2), (129, 2, 2), (9, 16, 4)])
+def test_q4k_moe_int8_token_passes(ctx, orc, S, E, k):
+    """Grouped int8 path with experts of 0, few and more than 128 rows (token
+    passes of 128), and every token on both experts when E == k."""
+    spec = LayerSpec(E, k, 512, 768, Q4_K, seed=S)
+    check(run_layer(ctx, orc, spec, S, 1, seed=2000 + S))
+
+
 def test_norm_topk_off_and_weights_scale(ctx, orc):
     spec = LayerSpec(16, 4, 1024, 512, Q8_0, seed=9, norm_topk=False, weights_scale=2.5)
     check(run_layer(ctx, orc, spec, 6, 0, seed=3))
