@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pcie-steps", type=int, default=200,
                     help="steps of the host-buffer variant (h copied in, out copied back, synchronous)")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="tokens of the prefill leg (int8 matrix-core path); 0 skips it")
+    ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -139,6 +142,144 @@ def cpu_baseline(ctx, torch, seconds: float, threads: int):
                   f"host has {hw} hardware threads",
         "gemv_q4k_2048x4096_GBps": round(gemv / 1e9, 3),
     }
+
+
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s
+
+
+def prefill_leg(ctx, torch, a):
+    """Prefill: S tokens per moe_ffn step on the int path for every row (the
+    int8 matrix-core kernels), rotating over the same layers, replayed as a HIP
+    graph. Reports tokens/s, the matrix-core utilisation of the grouped
+    kernels (algorithmic int8 ops: 2 per multiply-add of the top-k expert
+    products, over their measured durations) and HBM bytes touched."""
+    S = a.prefill_tokens
+    ctx.set_regime(1)
+    ctx.set_stream(torch.cuda.current_stream())
+    hp = torch.randn((a.layers, S, D), dtype=torch.float32, device="cuda")
+    op = torch.empty((a.layers, S, D), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        l = i % a.layers
+        ctx.moe_ffn(l, hp[l], op[l])
+
+    for i in range(a.layers * 2):
+        step(i)
+    torch.cuda.synchronize()
+    ctx.profile_enable(True)
+    for i in range(a.layers * 4):
+        step(i)
+    torch.cuda.synchronize()
+    kern = {}
+    for n in ["router_logits", "route_topk", "dispatch", "quant_q8k", "moe_gate_up_mfma", "moe_gate_up_int",
+              "quant_slots_q8k", "moe_down_mfma", "moe_down_int", "combine"]:
+        ms, cnt = ctx.profile_read(n)
+        if cnt:
+            kern[n] = {"avg_us": round(ms * 1000.0 / cnt, 3), "launches": cnt}
+    ctx.profile_enable(False)
+    whole = None
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ctx.set_stream(s)
+            for l in range(a.layers):
+                step(l)
+        torch.cuda.current_stream().wait_stream(s)
+        whole = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(whole):
+            ctx.set_stream(torch.cuda.current_stream())
+            for l in range(a.layers):
+                step(l)
+        ctx.set_stream(torch.cuda.current_stream())
+        for l in range(a.layers):
+            step(l)
+        torch.cuda.synchronize()
+        ref = op.clone()
+        for _ in range(2):
+            op.zero_()
+            whole.replay()
+            torch.cuda.synchronize()
+            if not torch.equal(ref, op):
+                raise RuntimeError("prefill graph replay differs from eager")
+    except Exception as ex:
+        print(f"# prefill graph capture unavailable: {ex}", file=sys.stderr)
+        whole = None
+        ctx.set_stream(torch.cuda.current_stream())
+    n_rep = max(1, a.prefill_steps // a.layers)
+
+    def run(nr):
+        for _ in range(nr):
+            if whole is not None:
+                whole.replay()
+            else:
+                for l in range(a.layers):
+                    step(l)
+
+    run(2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(n_rep)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    steps = n_rep * a.layers
+    ms_step = el * 1000.0 / steps
+    ops_gu = 2.0 * S * K * 2 * D * FF  # gate and up products of the routed rows
+    ops_dn = 2.0 * S * K * D * FF
+    util = {}
+    for name, ops in (("moe_gate_up_mfma", ops_gu), ("moe_down_mfma", ops_dn)):
+        if name in kern:
+            tops = ops / (kern[name]["avg_us"] * 1e-6) / 1e12
+            util[name] = {"alg_ops": ops, "avg_us": kern[name]["avg_us"], "achieved_TOPs": round(tops, 1),
+                          "frac": round(tops / INT8_PEAK_TOPS, 4)}
+    mf_us = sum(kern[n]["avg_us"] for n in ("moe_gate_up_mfma", "moe_down_mfma") if n in kern)
+    touched = E * EXPERT_BYTES + E * D * 4
+    res = {
+        "tokens": S,
+        "steps": steps,
+        "tokens_per_s": round(S * steps / el, 1),
+        "ms_per_step": round(ms_step, 5),
+        "regime": "int8",
+        "launch": "hip-graph" if whole is not None else "eager",
+        "mfma": {"bound": "mfma", "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
+                 "achieved": round((ops_gu + ops_dn) / (mf_us * 1e-6) / 1e12, 1) if mf_us else None,
+                 "frac": round((ops_gu + ops_dn) / (mf_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4) if mf_us else None,
+                 "alg_ops_per_step": ops_gu + ops_dn, "kernels": util},
+        "layer_TOPs": round((ops_gu + ops_dn) / (ms_step * 1e-3) / 1e12, 1),
+        "hbm_touched_GBps": round(touched / (ms_step * 1e-3) / 1e9, 1),
+        "hbm_frac": round(touched / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "kernels_us": kern,
+        "cpu_baseline": None,
+    }
+    ctx.set_regime(a.regime)
+    return res
+
+
+def cpu_prefill(ctx, S: int, seconds: float, threads: int):
+    """Oracle moe_ffn over S tokens in the reference's default regime (AVX2:
+    f32 GEMM for experts with >= 4 rows), on layer 0's bytes."""
+    import numpy as np
+
+    from oracle import pyoracle as orc
+
+    parts = [[ctx.expert_read(0, e, p) for p in range(3)] for e in range(E)]
+    rng = np.random.default_rng(0)
+    router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+    L = orc.Layer(E, K, D, FF, Q4_K, Q4_K, Q4_K, router, [p[0] for p in parts], [p[1] for p in parts],
+                  [p[2] for p in parts], True, 0.0)
+    nthreads = max(1, min(threads, orc.hw_threads()))
+    h = rng.standard_normal((S, D)).astype(np.float32)
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        L.moe_ffn(h, threads=nthreads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(n * S / el, 2), "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{n} moe_ffn call(s) of {S} tokens on layer 0 (AVX2 regime: f32 GEMM for experts "
+                      f"with >= 4 rows), {el:.1f} s"}
 
 
 def main():
@@ -320,8 +461,12 @@ def main():
         "pcie_inclusive": pcie,
         "cpu_baseline": None,
     }
+    if a.prefill_tokens > 0:
+        res["prefill"] = prefill_leg(ctx, torch, a)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
+        if a.prefill_tokens > 0:
+            res["prefill"]["cpu_baseline"] = cpu_prefill(ctx, a.prefill_tokens, a.cpu_seconds / 2, a.cpu_threads)
     print(json.dumps(res))
     ctx.close()
 

@@ -36,6 +36,13 @@ FLAGS = [
 ]
 
 
+# Per-file additions: the matrix-core kernels keep MFMA accumulators in
+# VGPRs, where their scale epilogue reads them without AGPR copies.
+FILE_FLAGS = {
+    "kmoe_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     p = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(p):
@@ -45,7 +52,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> tuple[str, str]:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature flag: harmless.
     msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines()

@@ -5,7 +5,7 @@
 // 32-token tile, per superblock b (256 columns):
 //   sumi(t, r) = sum_j sc_j(r) * sum_{x in sub-block j} q(r, x) * a(t, x)
 //   mins(t, r) = sum_j m_j(r) * bsum_j(t)
-//   y(t, r)   += (d(r) * ad(t, b)) * sumi - (dmin(r) * ad(t, b)) * mins
+//   y(t, r)   += ad(t, b) * (d(r) * sumi - dmin(r) * mins)
 // (avx2.rs:351-379 for every row: the reference's int path). The integers are
 // exact on the matrix cores:
 //   * the 6-bit scale splits as sc = 8*hi + lo with hi, lo < 8, so q*hi and
@@ -16,24 +16,35 @@
 //     bl in [0, 64), so one v_mfma_f32_32x32x16_f16 over k = (j, half) of
 //     (bh_j, bl_j) x (64*m_j, m_j) gives mins exactly (all products and partial
 //     sums are integers below 2^24).
-// Roles: A = activation rows (tokens, 32 per tile), B = weight rows, so in the
-// 32x32 result each lane owns one weight row (lane % 32) and 16 tokens, and
-// the per-row d, dmin, sc, m stay in the lane.
+// Roles: A = weight rows (32 per tile), B = activation rows (tokens, 32 per
+// tile). In the 32x32 result lane l owns token column l % 32 and weight rows
+// 8*(v/4) + 4*(l/32) + v%4, so the token's block scale is one value per lane
+// and the 16 rows' (d, dmin) are read once per superblock.
 // The k order inside an MFMA only has to agree between A and B: lane half h
 // holds columns 16h .. 16h+15 of the 32-column sub-block on both sides, which
 // for the weights is exactly tiled chunk (b, j/2, h): lo nibbles for even j,
 // hi nibbles for odd j.
-// Work-group: 4 waves, one per SIMD. Each takes one 64-token half of a
-// 128-token pass and one 32-row tile of one matrix (gate/up: 32 rows per
-// group, SwiGLU, transformer.rs:558, after an LDS exchange between the gate
-// and up waves; the single-matrix modes: 64 rows). More than 128 routed rows
-// take more passes; the plain modes give each pass its own work-group.
+//
+// Work-group: 4 waves, one per SIMD, each with the whole register file. A
+// wave owns one 32-row weight tile and every token tile of a 128-row pass, so
+// it decodes its rows' superblock into A operands once and multiplies them
+// against up to 4 token tiles (gate/up: the group holds the same 64 rows of
+// both matrices and applies SwiGLU, transformer.rs:558, after an LDS exchange
+// between the gate and up waves; the single-matrix modes: 128 rows). An
+// expert with more than 128 routed rows takes more passes; the plain modes
+// give each pass its own work-group.
+// Per superblock the activation tile (int8 pieces by direct global->LDS
+// loads, the split 16-sums and the block scales through registers) goes to a
+// double-buffered LDS stage while the previous superblock is multiplied; the
+// weight pieces of the next superblock are loaded into registers meanwhile.
+// Inside a superblock the B operands of token tile T+1 are read from LDS and
+// the scale epilogue of tile T-1 runs while tile T's MFMAs execute.
 // Modes: grouped gate/up and down over the expert tier's tiled Q4_K rows
 // (routed token slots), and plain GGUF Q4_K rows [rows, cols] against s_rows
 // activation rows: the matmul (quant.rs:229 on the int path) and the per-block
 // integer accumulators (avx2.rs:361-374) exposed for parity checks.
-// Superblock b+1's activation tile (LDS, double-buffered) and weight pieces
-// are in flight while superblock b is multiplied.
+#include <type_traits>
+
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 
@@ -45,35 +56,48 @@ typedef int v4i32 __attribute__((ext_vector_type(4)));
 typedef int v16i32 __attribute__((ext_vector_type(16)));
 typedef float v16f32 __attribute__((ext_vector_type(16)));
 typedef _Float16 v8f16 __attribute__((ext_vector_type(8)));
+typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTokTile = 32, kTokPass = 128;  // token rows per pass (two halves of 64)
+constexpr int kTok = 128;  // token rows per pass
+constexpr int kTiles = 4;  // 32-row token tiles per pass
 
 enum { MF_GATE_UP = 0, MF_DOWN = 1, MF_PLAIN = 2, MF_SUMS = 3 };
 
 struct MfmaArgs {
   ExpertTier tier;
   Routing rt;
-  const uint8_t *w0;   // plain modes: GGUF rows
-  int64_t s_rows;      // plain modes: activation rows
-  int64_t rows, cols;  // weight rows (F for gate/up, d for down), columns
-  const int8_t *aq;    // int8 activation rows
-  const float *ad;     // their block scales [.., cols/256]
-  const int32_t *abs;  // their 16-sums [.., cols/16]
-  float *out;          // [slots or s_rows, rows]
+  const uint8_t *w0;     // plain modes: GGUF rows
+  int64_t s_rows;        // plain modes: activation rows
+  int64_t rows, cols;    // weight rows (F for gate/up, d for down), columns
+  const int8_t *aq;      // int8 activation rows
+  const float *ad;       // their block scales [.., cols/256]
+  const int32_t *abs;    // their 16-sums [.., cols/16]
+  float *out;            // [slots or s_rows, rows]
   int32_t *sumi, *mins;  // MF_SUMS: [(s*rows + r)*nb + b]
   int regime;
 };
 
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-
 // One LDS stage (superblock b of the pass's 128 token rows):
-//   int8 [8 sub-blocks][2 halves][128 tokens][16 bytes]    32 KB
-//   f16  [2 halves][128 tokens][8] = (bh_0..7 | bl_0..7)    4 KB
-//   f32  ad [128]                                           0.5 KB
-constexpr int kStageQ = 8 * 2 * kTokPass * 16;
-constexpr int kStageB = 2 * kTokPass * 16;
-constexpr int kStageBytes = kStageQ + kStageB + kTokPass * 4;
+//   int8 [16 pieces = (sub-block, half)][128 tokens][16 bytes]   32 KB
+//   f16  [2 halves][128 tokens][8] = (bh_0..7 | bl_0..7)          4 KB
+//   f32  ad [128]                                                 512 B
+//   weights [row slots][5 chunks][64 lanes][16 bytes]: chunk 0 the head of
+//   lane l's row (row l % 32 of the slot's tile), chunks 1..4 its nibble
+//   bytes [32k + 16*half, +16), k < 4                   5 KB per row slot
+constexpr int kStA = 16 * kTok * 16;
+constexpr int kStM = 2 * kTok * 16;
+constexpr int kStD = kTok * 4;
+constexpr int kStW = kStA + kStM + kStD;
+// Gate/up: 8 row slots (4 tiles of both matrices), every wave all token
+// tiles. Other modes: 4 row slots, two waves per slot splitting the tiles.
+template <int MODE>
+constexpr int kSlots = MODE == 0 ? 8 : 4;
+template <int MODE>
+constexpr int kStage = kStW + kSlots<MODE> * 5 * 64 * 16;
 
 __device__ __forceinline__ bool mfma_int_regime(int regime, int n) {
   return regime == REGIME_INT8 || (regime == REGIME_AVX2 && n < 4);
@@ -91,50 +115,68 @@ __device__ __forceinline__ void q4k_scales8(uint32_t s03, uint32_t s47, uint32_t
   }
 }
 
-// 4 waves, one per SIMD (the full register file each: accumulators, B
-// operands and the next superblock's loads stay in registers). Wave w takes
-// the 64-token half w & 1 of each 128-row pass and, for gate/up, matrix w >> 1
-// of the group's 32-row tile; otherwise 32-row tile w >> 1 of the group's 64.
+// Each byte of n (< 16) times f (< 8), as two 16-bit products (no carry
+// leaves a byte: 15 * 7 = 105).
+__device__ __forceinline__ int mul_bytes(uint32_t n, uint32_t f) {
+  const u16x2 nv = __builtin_bit_cast(u16x2, n);
+  const u16x2 fv = {(unsigned short)f, (unsigned short)f};
+  return __builtin_bit_cast(int, (u16x2)(nv * fv));
+}
+
+// 16 bytes per lane from g into LDS at lds_wave_base + 16*lane (the base is
+// the same for the whole wave).
+__device__ __forceinline__ void lds_dma16(const void *g, uint8_t *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+}
+
 template <int MODE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_moe_mfma(MfmaArgs a) {
+__global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
   constexpr bool TILED = MODE == MF_GATE_UP || MODE == MF_DOWN;  // expert tier rows are tiled, plain rows GGUF
-  __shared__ __attribute__((aligned(16))) uint8_t stage[2][kStageBytes];
-  __shared__ int32_t srcs[kTokPass];
+  // Two stages as distinct objects: each access names its stage statically, so
+  // reads of one are not ordered behind direct loads still filling the other.
+  constexpr int SLOTS = kSlots<MODE>;
+  constexpr int TSPLIT = 8 / SLOTS;  // waves per row slot, splitting the token tiles
+  constexpr int TPW = kTiles / TSPLIT;  // token tiles per wave
+  __shared__ __attribute__((aligned(16))) uint8_t st0[kStage<MODE>];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[kStage<MODE>];
+  __shared__ int32_t srcs[kTok];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave % SLOTS;  // the group's row slot (gate/up: matrix wr & 1, tile wr >> 1)
+  const int th = wave / SLOTS;  // token tiles th, th + TSPLIT, ... of each pass
   const int64_t cols = a.cols, nb = cols / 256, row_bytes = nb * 144;
-  const int mat = MODE == MF_GATE_UP ? (wave >> 1) : 2;
-  const int64_t rtile = MODE == MF_GATE_UP ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * 2 + (wave >> 1);
-  const int th = wave & 1;  // token half of the pass
-  const int64_t r = rtile * 32 + l32;  // this lane's weight row
-  const bool rv = r < a.rows;
-  const int64_t rr = rv ? r : a.rows - 1;
-  int64_t p0 = 0;
-  int n, t_begin, t_end;
+  const int mat = MODE == MF_GATE_UP ? (wr & 1) : 2;
+  const int64_t rtile = MODE == MF_GATE_UP ? (int64_t)blockIdx.x * 4 + (wr >> 1) : (int64_t)blockIdx.x * 4 + wr;
+  const int64_t r_lane = rtile * 32 + l32;  // the weight row this lane decodes (A operand row l32)
+  const int64_t r_out = rtile * 32 + 4 * half;  // its output rows: r_out + 8g + c, g, c < 4
+  const int64_t rows = a.rows;
   const uint8_t *W;
-  if constexpr (TILED) {
-    const int i_act = blockIdx.y;
-    if (i_act >= *a.rt.n_active) return;
-    const int e = a.rt.active[i_act];
-    p0 = a.rt.offsets[e];
-    n = (int)(a.rt.offsets[e + 1] - p0);
-    if (!mfma_int_regime(a.regime, n)) return;
-    W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[mat] + rr * row_bytes;
-    t_begin = 0;
-    t_end = n;
-  } else {
-    n = (int)a.s_rows;
-    W = a.w0 + rr * row_bytes;
-    t_begin = (int)blockIdx.y * kTokPass;
-    t_end = t_begin + kTokPass < n ? t_begin + kTokPass : n;
+  int64_t p0 = 0;
+  int t_begin, t_end;
+  {
+    const int64_t rr = r_lane < rows ? r_lane : rows - 1;
+    if constexpr (TILED) {
+      const int i_act = blockIdx.y;
+      if (i_act >= *a.rt.n_active) return;
+      const int e = a.rt.active[i_act];
+      p0 = a.rt.offsets[e];
+      const int n = (int)(a.rt.offsets[e + 1] - p0);
+      if (!mfma_int_regime(a.regime, n)) return;
+      W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[mat] + rr * row_bytes;
+      t_begin = 0;
+      t_end = n;
+    } else {
+      W = a.w0 + rr * row_bytes;
+      t_begin = (int)blockIdx.y * kTok;
+      t_end = t_begin + kTok < (int)a.s_rows ? t_begin + kTok : (int)a.s_rows;
+    }
   }
-  // staging roles: 16-byte piece pc (columns 16pc..) of tokens (tid >> 4) + 16k, k < 8
-  const int pc = tid & 15, sj = pc >> 1, sh = pc & 1;
 
-  for (int t0 = t_begin; t0 < t_end; t0 += kTokPass) {
-    const int nt = t_end - t0 < kTokPass ? t_end - t0 : kTokPass;
+  for (int t0 = t_begin; t0 < t_end; t0 += kTok) {
+    const int nt = t_end - t0 < kTok ? t_end - t0 : kTok;
+    const int nT = (nt + 31) >> 5;  // token tiles of this pass
     __syncthreads();  // the previous pass is done with srcs and the stages
-    if (tid < kTokPass) {
+    if (tid < kTok) {
       int32_t src = 0;
       if (tid < nt) {
         if constexpr (MODE == MF_GATE_UP) src = (int32_t)(a.rt.perm[p0 + t0 + tid] / a.rt.topk);
@@ -143,73 +185,76 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
       srcs[tid] = src;
     }
     __syncthreads();
-    int64_t qoff[8];
-    bool qv[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int t = (tid >> 4) + 16 * k;
-      qv[k] = t < nt;
-      qoff[k] = (int64_t)srcs[qv[k] ? t : 0] * cols + 16 * pc;
-    }
-    const bool bt = tid < kTokPass && tid < nt;
-    const int64_t src_b = bt ? srcs[tid] : 0;
-    const int tq = tid >> 2, bq = tid & 3;  // 16-sum staging: tokens tq and tq + 64, sums 4bq .. 4bq+3
-    const bool qt0 = tq < nt, qt1 = tq + 64 < nt;
-    const int64_t src_q0 = qt0 ? srcs[tq] : 0, src_q1 = qt1 ? srcs[tq + 64] : 0;
-    // prefetch registers: activation pieces, 16-sums, block scale, weight head and nibbles
-    int4 SQ[8], SB0, SB1;
+    // Token rows past nt read token 0's row: their results are never stored.
+    const int8_t *ap0 = a.aq + (int64_t)srcs[lane < nt ? lane : 0] * cols;  // direct-load sources:
+    const int8_t *ap1 = a.aq + (int64_t)srcs[64 + lane < nt ? 64 + lane : 0] * cols;  // tokens lane, 64 + lane
+    const bool two_q = nt > 64;
+    // 16-sums: thread tid stages sums 4q .. 4q+3 (sub-blocks 2q, 2q+1) of
+    // token tid % 128, q = tid / 128; threads < 128 also its block scale
+    const int tok_me = tid & (kTok - 1), sq = tid >> 7;
+    const int64_t src_me = srcs[tok_me < nt ? tok_me : 0];
+    const int32_t *bsp = a.abs + src_me * (cols / 16) + 4 * sq;
+    const float *adp = a.ad + src_me * nb;
+
+    int4 SB;
     float SD = 0.0f;
-    u32x4 WH, WQ[4];
-    auto fetch = [&](int64_t b) {
+    auto fetch = [&](int64_t b, uint8_t *A) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) SQ[k] = *(const int4 *)(a.aq + qoff[k] + 256 * b);
-      SB0 = *(const int4 *)(a.abs + src_q0 * (cols / 16) + 16 * b + 4 * bq);  // 16-sums 4bq .. 4bq+3
-      SB1 = *(const int4 *)(a.abs + src_q1 * (cols / 16) + 16 * b + 4 * bq);
-      if constexpr (MODE != MF_SUMS) {
-        if (tid < kTokPass) SD = a.ad[src_b * nb + b];
+      for (int i = 0; i < 2; ++i) {  // pieces 2*wave, 2*wave+1 of every token
+        const int pc = 2 * wave + i;
+        lds_dma16(ap0 + 256 * b + 16 * pc, A + pc * kTok * 16);
+        if (two_q) lds_dma16(ap1 + 256 * b + 16 * pc, A + (pc * kTok + 64) * 16);
       }
+      // weights of row slot wr (with two waves per slot: the th == 0 wave
+      // takes the head and chunks 1, 2, the other chunks 3, 4)
+      uint8_t *Wl = A + kStW + wr * 5 * 1024;
+      const uint8_t *c0, *cq;  // head; nibble chunk k at cq + k*cs
+      int64_t cs;
       if constexpr (TILED) {
-        WH = __builtin_nontemporal_load((const u32x4 *)(W + 16 * b));
-        const uint8_t *qp = W + tq4_qs_off(nb, b, 0, half);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) WQ[i] = __builtin_nontemporal_load((const u32x4 *)(qp + 16 * i));
+        c0 = W + 16 * b;
+        cq = W + tq4_qs_off(nb, b, 0, half);
+        cs = 16;
       } else {  // GGUF superblock: head, then qs chunk (k, half) at 16 + 32k + 16*half
-        const uint8_t *sbp = W + 144 * b;
-        WH = __builtin_nontemporal_load((const u32x4a4 *)sbp);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          WQ[i] = __builtin_nontemporal_load((const u32x4a4 *)(sbp + 16 + 32 * i + 16 * half));
+        c0 = W + 144 * b;
+        cq = c0 + 16 + 16 * half;
+        cs = 32;
+      }
+      if (TSPLIT == 1 || th == 0) {
+        lds_dma16(c0, Wl);
+        lds_dma16(cq, Wl + 1024);
+        lds_dma16(cq + cs, Wl + 2048);
+      }
+      if (TSPLIT == 1 || th == 1) {
+        lds_dma16(cq + 2 * cs, Wl + 3072);
+        lds_dma16(cq + 3 * cs, Wl + 4096);
+      }
+      SB = *(const int4 *)(bsp + 16 * b);
+      if constexpr (MODE != MF_SUMS) {
+        if (tid < kTok) SD = adp[b];
       }
     };
-    auto put = [&](int buf) {
-      uint8_t *S = stage[buf];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int t = (tid >> 4) + 16 * k;
-        *(int4 *)(S + ((sj * 2 + sh) * kTokPass + t) * 16) = qv[k] ? SQ[k] : make_int4(0, 0, 0, 0);
-      }
-      _Float16 *hb = (_Float16 *)(S + kStageQ);
-      auto put_sums = [&](int t, bool ok, const int4 &sb) {
-        // sub-blocks 2bq, 2bq+1 of token t: 32-sums split as 64*bh + bl (bl in [0, 64))
-        const int s0 = ok ? sb.x + sb.y : 0, s1 = ok ? sb.z + sb.w : 0;
-        const int h0 = s0 >> 6, h1 = s1 >> 6;  // floor division
-        hb[(0 * kTokPass + t) * 8 + 2 * bq] = (_Float16)h0;
-        hb[(0 * kTokPass + t) * 8 + 2 * bq + 1] = (_Float16)h1;
-        hb[(1 * kTokPass + t) * 8 + 2 * bq] = (_Float16)(s0 - 64 * h0);
-        hb[(1 * kTokPass + t) * 8 + 2 * bq + 1] = (_Float16)(s1 - 64 * h1);
-      };
-      put_sums(tq, qt0, SB0);
-      put_sums(tq + 64, qt1, SB1);
-      if (tid < kTokPass) *(float *)(S + kStageQ + kStageB + 4 * tid) = bt ? SD : 0.0f;
+    auto put = [&](uint8_t *S) {  // split 32-sums of sub-blocks 2q, 2q+1 of token tid % 128; block scale
+      const int s0 = SB.x + SB.y, s1 = SB.z + SB.w;
+      const int h0 = s0 >> 6, h1 = s1 >> 6;  // floor division: s = 64*h + l, l in [0, 64)
+      h2 hv, lv;
+      hv.x = (_Float16)h0;
+      hv.y = (_Float16)h1;
+      lv.x = (_Float16)(s0 - 64 * h0);
+      lv.y = (_Float16)(s1 - 64 * h1);
+      *(h2 *)(S + kStA + tok_me * 16 + 4 * sq) = hv;
+      *(h2 *)(S + kStA + (kTok + tok_me) * 16 + 4 * sq) = lv;
+      if (tid < kTok) *(float *)(S + kStA + kStM + 4 * tid) = SD;
     };
-    v4i32 bhi[8], blo[8];
-    v8f16 bm;
-    float dw = 0.0f, dmw = 0.0f;
-    auto build = [&]() {  // B operands of this lane's row from WH/WQ
+    v4i32 ahi[8], alo[8];
+    v8f16 amn;
+    auto build = [&](const uint8_t *S) {  // A operands of this lane's row
+      const uint8_t *Wl = S + kStW + wr * 5 * 1024 + 16 * lane;
+      const u32x4 WH = *(const u32x4 *)Wl;
+      u32x4 WQ[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) WQ[i] = *(const u32x4 *)(Wl + (1 + i) * 1024);
       int sc[8], mn[8];
       q4k_scales8(WH.y, WH.z, WH.w, sc, mn);
-      dw = f16_bits_to_f32(WH.x);
-      dmw = f16_bits_to_f32(WH.x >> 16);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const u32x4 w = WQ[j >> 1];
@@ -218,115 +263,115 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         const uint32_t n0 = (w.x >> s4) & msk, n1 = (w.y >> s4) & msk, n2 = (w.z >> s4) & msk,
                        n3 = (w.w >> s4) & msk;
         const uint32_t hi = (uint32_t)(sc[j] >> 3), lo = (uint32_t)(sc[j] & 7);
-        // bytes times a factor < 8 stay below 106: no carries between bytes
-        bhi[j] = v4i32{(int)(n0 * hi), (int)(n1 * hi), (int)(n2 * hi), (int)(n3 * hi)};
-        blo[j] = v4i32{(int)(n0 * lo), (int)(n1 * lo), (int)(n2 * lo), (int)(n3 * lo)};
-        bm[j] = (_Float16)(half ? mn[j] : 64 * mn[j]);
+        ahi[j] = v4i32{mul_bytes(n0, hi), mul_bytes(n1, hi), mul_bytes(n2, hi), mul_bytes(n3, hi)};
+        alo[j] = v4i32{mul_bytes(n0, lo), mul_bytes(n1, lo), mul_bytes(n2, lo), mul_bytes(n3, lo)};
+        amn[j] = (_Float16)(half ? mn[j] : 64 * mn[j]);
       }
     };
-    float y[2][16];
+
+    float y[TPW][16];
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
+    for (int i = 0; i < TPW; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) y[T][v] = 0.0f;
-    const int ntiles_mine = (nt - 64 * th + kTokTile - 1) / kTokTile;  // this wave's tiles (may be <= 0)
-    fetch(0);
-    put(0);
-    build();
-    lds_barrier();
-    for (int64_t b = 0; b < nb; ++b) {
-      const uint8_t *S = stage[b & 1];
-      if (b + 1 < nb) fetch(b + 1);
+      for (int v = 0; v < 16; ++v) y[i][v] = 0.0f;
+
+    fetch(0, st0);
+    put(st0);
+    __syncthreads();  // waits for the direct loads too
+    // superblock b from stage S while superblock b+1 loads into stage Nx
+    auto iter = [&](int64_t b, const uint8_t *S, uint8_t *Nx) {
+      if (b + 1 < nb) fetch(b + 1, Nx);
+      build(S);
+      // (d, dmin) f16 pairs of the lane's 16 output rows 8g + 4*half + c: the
+      // first dword of those rows' heads
+      const uint8_t *hd = S + kStW + wr * 5 * 1024 + 16 * 4 * half;
 #pragma unroll
-      for (int T = 0; T < 2; ++T) {
-        if (T < ntiles_mine) {
-          const int tl = 64 * th + T * kTokTile + l32;  // A-operand token row of this lane
-          v16i32 ahi = {0}, alo = {0};
+      for (int i = 0; i < TPW; ++i) {
+        const int T = TSPLIT * i + th;
+        if (T < nT) {
+          // B operands: pieces (j, half) of token 32T + l32; mins operand (bh | bl)
+          const int tl = 32 * T + l32;
+          v4i32 bv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const v4i32 av = *(const v4i32 *)(S + ((j * 2 + half) * kTokPass + tl) * 16);
-            ahi = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bhi[j], ahi, 0, 0, 0);
-            alo = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, blo[j], alo, 0, 0, 0);
-          }
-          const v8f16 am = *(const v8f16 *)(S + kStageQ + (half * kTokPass + tl) * 16);
-          v16f32 mins = {0};
-          mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, mins, 0, 0, 0);
-          // result layout: token row 8*(v/4) + 4*half + v%4 of the tile, weight row l32
+          for (int j = 0; j < 8; ++j) bv[j] = *(const v4i32 *)(S + ((2 * j + half) * kTok + tl) * 16);
+          const v8f16 bm = *(const v8f16 *)(S + kStA + (half * kTok + tl) * 16);
+          // sumi = 8 * (hi chain) + (lo chain): the lo chain accumulates onto the shifted hi sums
+          v16i32 H = v16i32{0};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) H = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi[j], bv[j], H, 0, 0, 0);
+          H = H << 3;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) H = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo[j], bv[j], H, 0, 0, 0);
+          const v16f32 N = __builtin_amdgcn_mfma_f32_32x32x16_f16(amn, bm, v16f32{0}, 0, 0, 0);
+          // element v: token 32T + l32 of the pass, row r_out + 8*(v/4) + v%4
           if constexpr (MODE == MF_SUMS) {
-            if (rv) {
+            if (tl < nt) {
 #pragma unroll
               for (int v = 0; v < 16; ++v) {
-                const int t = 64 * th + T * kTokTile + 8 * (v >> 2) + 4 * half + (v & 3);
-                if (t < nt) {
-                  const int64_t o = ((int64_t)(t0 + t) * a.rows + r) * nb + b;
-                  a.sumi[o] = 8 * ahi[v] + alo[v];
-                  a.mins[o] = (int)mins[v];
+                const int64_t rw = r_out + 8 * (v >> 2) + (v & 3);
+                if (rw < rows) {
+                  const int64_t o = ((int64_t)(t0 + tl) * rows + rw) * nb + b;
+                  a.sumi[o] = H[v];
+                  a.mins[o] = (int)N[v];
                 }
               }
             }
-            continue;
-          }
+          } else {
+            const float adt = *(const float *)(S + kStA + kStM + 4 * tl);
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 adv =
-                *(const float4 *)(S + kStageQ + kStageB + 4 * (64 * th + T * kTokTile + 8 * g + 4 * half));
-            const float advs[4] = {adv.x, adv.y, adv.z, adv.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int v = 4 * g + c;
-              const int si = 8 * ahi[v] + alo[v];
-              const float dd = dw * advs[c], dm = dmw * advs[c];
-              y[T][v] = fmaf(dd, (float)si, y[T][v]);
-              y[T][v] = fmaf(-dm, mins[v], y[T][v]);
+            for (int v = 0; v < 16; ++v) {
+              const h2 dv = *(const h2 *)(hd + 16 * (8 * (v >> 2) + (v & 3)));
+              const float m = fmaf(-(float)dv.y, N[v], 0.0f);  // - dmin * mins
+              const float x = fmaf((float)dv.x, (float)H[v], m);
+              y[i][v] = fmaf(adt, x, y[i][v]);
             }
           }
         }
       }
-      if (b + 1 < nb) {
-        put((b + 1) & 1);
-        build();
-      }
-      lds_barrier();
+      if (b + 1 < nb) put(Nx);
+      __syncthreads();  // next stage complete (direct loads included) and this one free
+    };
+    for (int64_t b = 0; b < nb; b += 2) {
+      iter(b, st0, st1);
+      if (b + 1 < nb) iter(b + 1, st1, st0);
     }
-    // ---- results: out[p0 + t0 + token, r]
-    if constexpr (MODE == MF_SUMS) {
-    } else if constexpr (MODE == MF_GATE_UP) {
-      // the up waves (2, 3) hand their values to the gate waves (0, 1) of the same token half
-      float *x = (float *)stage[0];  // [2 halves][32 rows][64 tokens + 1]
-      constexpr int XS = 65;
-      if (wave >= 2) {
+    // ---- results: out[p0 + t0 + token, row]
+    auto store = [&](int T, int v, float val) {
+      const int t = 32 * T + l32;
+      const int64_t rw = r_out + 8 * (v >> 2) + (v & 3);
+      if (t < nt && rw < rows) a.out[(p0 + t0 + t) * rows + rw] = val;
+    };
+    if constexpr (MODE == MF_GATE_UP) {
+      // gate and up values to LDS ([128 tokens][128 rows + 1], gate in st0, up
+      // in st1), then SwiGLU by every thread, row-contiguous stores
+      constexpr int LD = 129;
+      float *xm = mat == 0 ? (float *)st0 : (float *)st1;
 #pragma unroll
-        for (int T = 0; T < 2; ++T)
+      for (int i = 0; i < TPW; ++i)
+        if (i < nT) {
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            x[((wave & 1) * 32 + l32) * XS + T * kTokTile + 8 * (v >> 2) + 4 * half + (v & 3)] = y[T][v];
-      }
+            xm[(32 * i + l32) * LD + 32 * (wr >> 1) + 8 * (v >> 2) + 4 * half + (v & 3)] = y[i][v];
+        }
       lds_barrier();
-      if (wave < 2 && rv) {
-#pragma unroll
-        for (int T = 0; T < 2; ++T)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int tt = T * kTokTile + 8 * (v >> 2) + 4 * half + (v & 3);
-            const int t = 64 * th + tt;
-            if (t < nt) {
-              const float g = y[T][v], u = x[(th * 32 + l32) * XS + tt];
-              const float den = 1.0f + expf_cr(-g);  // SwiGLU: g / (1 + exp(-g)) * u
-              const float q = g / den;
-              a.out[(p0 + t0 + t) * a.rows + r] = q * u;
-            }
-          }
+      const float *xg = (const float *)st0, *xu = (const float *)st1;
+      const int64_t rbase = (int64_t)blockIdx.x * 128;
+      for (int e = tid; e < nt * 128; e += 512) {
+        const int t = e >> 7, rl = e & 127;
+        if (rbase + rl < rows) {
+          const float g = xg[t * LD + rl], u = xu[t * LD + rl];
+          const float den = 1.0f + expf_cr(-g);  // SwiGLU: g / (1 + exp(-g)) * u
+          const float q = g / den;
+          a.out[(p0 + t0 + t) * rows + rbase + rl] = q * u;
+        }
       }
-    } else {
-      if (rv) {
+    } else if constexpr (MODE != MF_SUMS) {
 #pragma unroll
-        for (int T = 0; T < 2; ++T)
+      for (int i = 0; i < TPW; ++i)
+        if (TSPLIT * i + th < nT) {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int t = 64 * th + T * kTokTile + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (t < nt) a.out[(p0 + t0 + t) * a.rows + r] = y[T][v];
-          }
-      }
+          for (int v = 0; v < 16; ++v) store(TSPLIT * i + th, v, y[i][v]);
+        }
     }
   }
 }
@@ -365,10 +410,10 @@ hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int
   a.abs = abs;
   a.out = out;
   a.regime = regime;
-  const int64_t rows_per_wg = mode == MF_GATE_UP ? 32 : 64;
+  const int64_t rows_per_wg = 128;
   const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)max_active);
-  if (mode == MF_GATE_UP) KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP>), grid, dim3(256), 0, st, a);
-  else KMOE_LAUNCH((k_moe_mfma<MF_DOWN>), grid, dim3(256), 0, st, a);
+  if (mode == MF_GATE_UP) KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP>), grid, dim3(512), 0, st, a);
+  else KMOE_LAUNCH((k_moe_mfma<MF_DOWN>), grid, dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
@@ -376,7 +421,7 @@ hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int
                              const float *ad, const int32_t *abs, int64_t s_rows, float *out, int32_t *sumi,
                              int32_t *mins) {
   if (!moe_mfma_supported(rows, cols) || !aligned16(aq) || !aligned16(abs) || ((uintptr_t)w & 3u) ||
-      s_rows > (int64_t)kTokPass * 65535)
+      s_rows > (int64_t)kTok * 65535)
     return hipErrorNotSupported;
   if (s_rows == 0) return hipSuccess;
   MfmaArgs a{};
@@ -391,9 +436,9 @@ hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int
   a.sumi = sumi;
   a.mins = mins;
   a.regime = REGIME_INT8;
-  const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((s_rows + kTokPass - 1) / kTokPass));
-  if (sumi) KMOE_LAUNCH((k_moe_mfma<MF_SUMS>), grid, dim3(256), 0, st, a);
-  else KMOE_LAUNCH((k_moe_mfma<MF_PLAIN>), grid, dim3(256), 0, st, a);
+  const dim3 grid((unsigned)((rows + 127) / 128), (unsigned)((s_rows + kTok - 1) / kTok));
+  if (sumi) KMOE_LAUNCH((k_moe_mfma<MF_SUMS>), grid, dim3(512), 0, st, a);
+  else KMOE_LAUNCH((k_moe_mfma<MF_PLAIN>), grid, dim3(512), 0, st, a);
   return hipGetLastError();
 }
 
