@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the prefill leg (int8 matrix-core path); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other measured rows (decode b=8/32, dense matvec, Qwen3-shaped layer)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -252,6 +254,142 @@ def prefill_leg(ctx, torch, a):
         "cpu_baseline": None,
     }
     ctx.set_regime(a.regime)
+    return res
+
+
+def graph_time(torch, ctx, fns, reps: int) -> float:
+    """Seconds per run of fns (library launches on the current stream), captured
+    once as a HIP graph after an eager run that sizes the workspace."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ctx.set_stream(s)
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.set_stream(torch.cuda.current_stream())
+        for f in fns:
+            f()
+    ctx.set_stream(torch.cuda.current_stream())
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / reps
+    del g
+    return el
+
+
+def batch_leg(ctx, torch, layers: int, S: int, regime: int):
+    """Mixtral-shaped decode at S tokens per step over the rotated layers; HBM
+    bytes from the distinct experts each layer's routing touched."""
+    ctx.set_regime(regime)
+    ctx.set_stream(torch.cuda.current_stream())
+    hp = torch.randn((layers, S, D), dtype=torch.float32, device="cuda")
+    op = torch.empty_like(hp)
+    touched = []
+    for l in range(layers):
+        ctx.moe_ffn(l, hp[l], op[l])
+        idx = ctx.last_routing(S, K, E)[0]
+        touched.append(len(set(idx.cpu().numpy().ravel().tolist())))
+    t = graph_time(torch, ctx, [lambda l=l: ctx.moe_ffn(l, hp[l], op[l]) for l in range(layers)], 20) / layers
+    tb = (sum(touched) / layers) * EXPERT_BYTES + E * D * 4
+    ctx.set_regime(0)
+    return {"tokens": S, "regime": ["avx2", "int8", "exact"][regime], "tokens_per_s": round(S / t, 1),
+            "ms_per_step": round(t * 1e3, 5), "experts_touched": sum(touched) / layers,
+            "hbm_touched_GBps": round(tb / t / 1e9, 1), "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def matvec_leg(ctx, torch, pool_bytes: float = 2.2e9):
+    """Dense Q4_K matvec at decode batch 1 (quant::matmul, one activation row)
+    over a pool of distinct weight copies larger than the Infinity Cache."""
+    import numpy as np
+
+    from kestrel_amd import kmoe
+
+    ctx.set_regime(0)
+    dh = np.array([1.4e-4], np.float16).view(np.uint8)
+    mh = np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)
+    hdr = torch.tensor(np.concatenate([dh, mh]), dtype=torch.uint8, device="cuda")
+    out = {}
+    for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
+        nbytes = rows * (cols // 256) * 144
+        copies = int(-(-pool_bytes // nbytes))
+        pool = torch.randint(0, 256, (copies, nbytes // 144, 144), dtype=torch.uint8, device="cuda")
+        pool[:, :, 0:4] = hdr
+        x = torch.randn((1, cols), dtype=torch.float32, device="cuda")
+        y = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+        lib = ctx.lib
+
+        def call(i):
+            ctx.check(lib.kmoe_matmul(ctx.h, Q4_K, kmoe._ptr(pool[i]), nbytes, rows, cols, kmoe._ptr(x), 1,
+                                      kmoe._ptr(y)))
+
+        t = graph_time(torch, ctx, [lambda i=i: call(i) for i in range(copies)], 5) / copies
+        b = nbytes + cols * 4 + rows * 4
+        out[f"{rows}x{cols}"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1),
+                                 "frac": round(b / t / 1e9 / HBM_PEAK_GBPS, 4), "pool_copies": copies}
+        del pool
+    torch.cuda.empty_cache()
+    return out
+
+
+def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
+    """Qwen3-30B-A3B-shaped layer: hidden 2048, FFN 768, 128 experts, top-8,
+    Q4_K random-init experts, router N(0, 0.02) plus a rank-1 Zipf(1.1) bias
+    over a seeded expert permutation (activations N(1, 1) carry it into the
+    logits). Layers rotate (4 x 340 MB) past the Infinity Cache."""
+    import numpy as np
+
+    E4, K4, D4, F4 = 128, 8, 2048, 768
+    part = F4 * (D4 // 256) * 144
+    dh = np.array([1.4e-4], np.float16).view(np.uint8)
+    mh = np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)
+    hdr = torch.tensor(np.concatenate([dh, mh]), dtype=torch.uint8, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    base = 100
+    for l in range(layers):
+        ctx.layer_create(base + l, E4, K4, D4, F4, Q4_K, Q4_K, Q4_K, True, 0.0)
+        router = rng.standard_normal((E4, D4)) * 0.02
+        rank = rng.permutation(E4) + 1
+        router += (-1.1 * np.log(rank.astype(np.float64)) / D4)[:, None]
+        ctx.router_upload(base + l, router.astype(np.float32))
+        for e in range(E4):
+            for p in range(3):
+                t = torch.randint(0, 256, (part // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
+                t[:, 0:4] = hdr
+                ctx.expert_upload(base + l, e, p, t)
+    torch.cuda.synchronize()
+    expert_bytes = 3 * part
+    res = []
+    for S, regime in ((1, 0), (16, 0), (128, 0), (512, 0), (2048, 0), (512, 1), (2048, 1)):
+        ctx.set_regime(regime)
+        ctx.set_stream(torch.cuda.current_stream())
+        hp = torch.randn((layers, S, D4), dtype=torch.float32, device="cuda") + 1.0
+        op = torch.empty_like(hp)
+        touched = []
+        for l in range(layers):
+            ctx.moe_ffn(base + l, hp[l], op[l])
+            idx = ctx.last_routing(S, K4, E4)[0]
+            touched.append(len(set(idx.cpu().numpy().ravel().tolist())))
+        reps = 50 if S <= 128 else 10
+        t = graph_time(torch, ctx, [lambda l=l: ctx.moe_ffn(base + l, hp[l], op[l]) for l in range(layers)], reps)
+        t /= layers
+        tb = (sum(touched) / layers) * expert_bytes + E4 * D4 * 4
+        res.append({"tokens": S, "regime": ["avx2", "int8", "exact"][regime], "tokens_per_s": round(S / t, 1),
+                    "us_per_step": round(t * 1e6, 2), "experts_touched": sum(touched) / layers,
+                    "hbm_touched_GBps": round(tb / t / 1e9, 1)})
+    ctx.set_regime(0)
+    for l in range(layers):
+        ctx.layer_destroy(base + l)
+    torch.cuda.empty_cache()
     return res
 
 
@@ -463,6 +601,10 @@ def main():
     }
     if a.prefill_tokens > 0:
         res["prefill"] = prefill_leg(ctx, torch, a)
+    if not a.no_extra:
+        res["decode_batches"] = [batch_leg(ctx, torch, a.layers, S2, rg) for S2 in (8, 32) for rg in (0, 1)]
+        res["matvec_q4k"] = matvec_leg(ctx, torch)
+        res["qwen3"] = qwen3_leg(ctx, torch)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
         if a.prefill_tokens > 0:

@@ -84,6 +84,16 @@ void *kmoe_get_stream(kmoe_ctx *ctx);
 int kmoe_synchronize(kmoe_ctx *ctx);
 int kmoe_set_regime(kmoe_ctx *ctx, int regime);
 int kmoe_get_regime(const kmoe_ctx *ctx);
+/* No counterpart in the reference: how a single-token kmoe_moe_ffn runs.
+ * KMOE_DECODE_SEPARATE (default): one kernel per stage (router, gate/up that
+ * selects the experts, Q8_K of h, down + combine). KMOE_DECODE_FUSED: the
+ * whole layer as one persistent kernel where the shape allows (Q4_K experts,
+ * int path); its work-groups wait on each other, so the grid must be
+ * resident, and a wait past its bound is reported by kmoe_synchronize as
+ * KMOE_E_HIP. Both give the same routing; output bits are the same wherever
+ * both run the same per-row reductions. */
+enum { KMOE_DECODE_SEPARATE = 0, KMOE_DECODE_FUSED = 1 };
+int kmoe_set_decode_path(kmoe_ctx *ctx, int path);
 
 /* ------------------------------------------------- Tier::Vram accounting */
 /* Ledger::reserve for Tier::Vram (ledger.rs:75): every device byte the context

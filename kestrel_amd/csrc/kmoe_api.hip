@@ -82,13 +82,19 @@ struct Event2 {
 
 }  // namespace
 
+// Device completion counters per context: words [0, 64) for the decode
+// router, [64, kCounterWords) for the fused single-token layer.
+constexpr int kCounterWords = 4096;
+constexpr int kFusedSync = 64;
+
 struct kmoe_ctx {
   int device = 0;
   hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
   std::string err;
   int regime = KMOE_REGIME_AVX2;
-  uint32_t *counters = nullptr;  // device, 64 completion counters, zero between calls
+  uint32_t *counters = nullptr;  // device, kCounterWords completion counters, zero between calls
+  int decode_path = 0;           // KMOE_DECODE_SEPARATE or KMOE_DECODE_FUSED
   uint64_t vram_limit = 0;
   uint64_t vram_reserved = 0;
   std::map<uint32_t, Layer> layers;
@@ -365,7 +371,8 @@ int kmoe_create(int device, kmoe_ctx **out) {
   }
   c->stream = c->own;
   // completion counters of multi-work-group kernels; zero between calls
-  if (hipMalloc((void **)&c->counters, 256) != hipSuccess || hipMemset(c->counters, 0, 256) != hipSuccess) {
+  if (hipMalloc((void **)&c->counters, kCounterWords * 4) != hipSuccess ||
+      hipMemset(c->counters, 0, kCounterWords * 4) != hipSuccess) {
     (void)hipStreamDestroy(c->own);
     delete c;
     return KMOE_E_HIP;
@@ -412,6 +419,13 @@ int kmoe_synchronize(kmoe_ctx *c) {
   if (!c) return KMOE_E_INVALID;
   DeviceGuard g(c->device);
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  // a fused single-token layer that gave up waiting leaves word 3 of its sync area set
+  uint32_t flag = 0;
+  HIP_OK(c, hipMemcpy(&flag, c->counters + kFusedSync + 3, 4, hipMemcpyDeviceToHost));
+  if (flag) {
+    HIP_OK(c, hipMemset(c->counters + kFusedSync + 3, 0, 4));
+    return fail(c, KMOE_E_HIP, "fused decode layer: a work-group waited past its bound (grid not resident?)");
+  }
   return KMOE_OK;
 }
 
@@ -422,6 +436,13 @@ int kmoe_set_regime(kmoe_ctx *c, int regime) {
   return KMOE_OK;
 }
 int kmoe_get_regime(const kmoe_ctx *c) { return c ? c->regime : -1; }
+
+int kmoe_set_decode_path(kmoe_ctx *c, int path) {
+  if (!c) return KMOE_E_INVALID;
+  if (path != KMOE_DECODE_SEPARATE && path != KMOE_DECODE_FUSED) return fail(c, KMOE_E_INVALID, "bad path %d", path);
+  c->decode_path = path;
+  return KMOE_OK;
+}
 
 int kmoe_vram_set_limit(kmoe_ctx *c, uint64_t limit) {
   if (!c) return KMOE_E_INVALID;
@@ -902,6 +923,33 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   hipStream_t st = c->stream;
 
   const int gt = D.gate_type, dt = D.down_type;
+  // One token on the int path over tiled Q4_K experts, on request: the whole
+  // layer as one persistent kernel (route, select, gate/up, Q8_K of h, down,
+  // combine).
+  if (S == 1 && regime != KMOE_REGIME_EXACT && c->decode_path == KMOE_DECODE_FUSED && gt == KMOE_Q4_K &&
+      D.up_type == KMOE_Q4_K && dt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && L->tiled[2] &&
+      layer_dec_fused_supported(d, F, (int32_t)E, (int32_t)k)) {
+    DecSelect pub;
+    pub.E = (int32_t)E;
+    pub.K = (int32_t)k;
+    pub.idx = w.idx;
+    pub.wsel = w.wsel;
+    pub.perm = w.perm;
+    pub.offsets = w.offsets;
+    pub.inv = w.inv;
+    pub.n_active = w.n_active;
+    pub.active = w.active;
+    ExpertTier ft{L->arena, (int64_t)L->expert_stride,
+                  {(int64_t)L->part_off[0], (int64_t)L->part_off[1], (int64_t)L->part_off[2]}};
+    hipError_t e = timed(c, "moe_layer_fused", [&]() {
+      return launch_layer_dec_fused(st, L->router, (int32_t)E, d, h, (int32_t)k, D.norm_topk, D.weights_scale, ft, F,
+                                    w.logits, w.xq, w.xd, w.xs, w.h, w.hq, w.hd, w.hs, out, pub,
+                                    c->counters + kFusedSync);
+    });
+    if (e == hipSuccess) goto done;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
+  {
   // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531). With
   // s_rows < 4 one fused work-group also quantizes x for the int8 path.
   bool x_quantized = false;
@@ -1029,6 +1077,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   if (any_f32) LAUNCH(c, "moe_down_f32", launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, w.h, w.y));
   // combine (transformer.rs:566-570)
   LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
+  }
 
 done:
   if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)

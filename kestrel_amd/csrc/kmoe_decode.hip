@@ -18,12 +18,11 @@
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 #include "kmoe_select.h"
+#include "kmoe_tq4.h"
 
 namespace kmoe {
 
 namespace {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct DecArgs {
   ExpertTier tier;
@@ -36,38 +35,6 @@ struct DecArgs {
   int32_t groups_per_expert;  // work-groups along the rows of one expert
   DecSelect sel;              // logits given: this kernel selects the experts
 };
-
-struct Slice {
-  int4 x0, x1, x2, x3;  // 64 activation bytes: elements 64k .. 64k+63 of superblock sb
-  int bsA, bsB;         // sums of the 32-element halves (sub-blocks 2k, 2k+1)
-  float d;              // block scale
-};
-
-__device__ __forceinline__ int q4k_quarter(const u32x4 &hd, const u32x4 &qa, const u32x4 &qb, int k, const Slice &s,
-                                           int &mins) {
-  int sA, mA, sB, mB;
-  q4k_scale_min_pair(hd.y, hd.z, hd.w, k, sA, mA, sB, mB);
-  const uint32_t m = 0x0f0f0f0fu;
-  int lo = 0, hi = 0;
-  lo = sdot4(qa.x & m, (uint32_t)s.x0.x, lo);
-  lo = sdot4(qa.y & m, (uint32_t)s.x0.y, lo);
-  lo = sdot4(qa.z & m, (uint32_t)s.x0.z, lo);
-  lo = sdot4(qa.w & m, (uint32_t)s.x0.w, lo);
-  lo = sdot4(qb.x & m, (uint32_t)s.x1.x, lo);
-  lo = sdot4(qb.y & m, (uint32_t)s.x1.y, lo);
-  lo = sdot4(qb.z & m, (uint32_t)s.x1.z, lo);
-  lo = sdot4(qb.w & m, (uint32_t)s.x1.w, lo);
-  hi = sdot4((qa.x >> 4) & m, (uint32_t)s.x2.x, hi);
-  hi = sdot4((qa.y >> 4) & m, (uint32_t)s.x2.y, hi);
-  hi = sdot4((qa.z >> 4) & m, (uint32_t)s.x2.z, hi);
-  hi = sdot4((qa.w >> 4) & m, (uint32_t)s.x2.w, hi);
-  hi = sdot4((qb.x >> 4) & m, (uint32_t)s.x3.x, hi);
-  hi = sdot4((qb.y >> 4) & m, (uint32_t)s.x3.y, hi);
-  hi = sdot4((qb.z >> 4) & m, (uint32_t)s.x3.z, hi);
-  hi = sdot4((qb.w >> 4) & m, (uint32_t)s.x3.w, hi);
-  mins = mA * s.bsA + mB * s.bsB;
-  return sA * lo + sB * hi;
-}
 
 // TPL task slots per lane (a row has 4*nb <= 64*TPL quarters), RU rows per step.
 // NPER = 0: the routing (active experts, slot offsets) is given. NPER > 0:
@@ -95,37 +62,13 @@ __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
     uint32_t sj[16];
     float wj[16];
     wave_route_one<NPER>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P[wave], sj, wj);
-    // rank of each selected expert among the selection (all distinct)
     uint32_t rk[16];
+    selection_ranks(sj, q.K, rk);
     e = -1;
-    for (int j = 0; j < q.K; ++j) {
-      uint32_t r = 0;
-      for (int jj = 0; jj < q.K; ++jj) r += sj[jj] < sj[j] ? 1u : 0u;
-      rk[j] = r;
-      if ((int)r == slot_i) e = (int)sj[j];
-    }
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {  // publish the routing of the token
-      uint32_t mysel = 0, myrk = 0;
-      float myw = 0.0f;
-      for (int j = 0; j < q.K; ++j) {
-        mysel = lane == j ? sj[j] : mysel;
-        myrk = lane == j ? rk[j] : myrk;
-        myw = lane == j ? wj[j] : myw;
-      }
-      if (lane < q.K) {
-        q.idx[lane] = mysel;
-        q.wsel[lane] = myw;
-        q.perm[myrk] = (uint32_t)lane;
-        q.inv[lane] = myrk;
-        q.active[myrk] = (int32_t)mysel;
-      }
-      if (lane == 0) *q.n_active = q.K;
-      for (int ee = lane; ee <= q.E; ee += 64) {
-        uint32_t c = 0;
-        for (int j = 0; j < q.K; ++j) c += sj[j] < (uint32_t)ee ? 1u : 0u;
-        q.offsets[ee] = c;
-      }
-    }
+    for (int j = 0; j < q.K; ++j)
+      if ((int)rk[j] == slot_i) e = (int)sj[j];
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)  // publish the routing of the token
+      publish_selection(sj, wj, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
     if (e < 0) return;
     p = slot_i;
   }

@@ -148,20 +148,53 @@ __device__ __forceinline__ uint32_t pack_i8x4(int8_t a, int8_t b, int8_t c, int8
   return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) | ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
+// Loads and stores coherent across the device (agent scope, relaxed): data
+// that work-groups of one kernel hand to each other without cache fences.
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int4 ld_agent4(const void *p) {
+  const uint32_t *u = (const uint32_t *)p;
+  return make_int4((int)ld_agent(u), (int)ld_agent(u + 1), (int)ld_agent(u + 2), (int)ld_agent(u + 3));
+}
+
 // Q8KRow::quantize of one 256-element block by one full wave (qdot.rs:353-365).
 // Lane l owns elements 4l..4l+3. Writes q[0..256), *d, bsums[0..16).
+// COHERENT: x read and the results written with agent-scope accesses.
+template <bool COHERENT = false>
 __device__ __forceinline__ void wave_quant_q8k_block(const float *x, int8_t *q, float *d, int32_t *bsums, int lane) {
-  const float4 v = *(const float4 *)(x + 4 * lane);
+  float4 v;
+  if constexpr (COHERENT) {
+    const float *xp = x + 4 * lane;
+    v = make_float4(ld_agent(xp), ld_agent(xp + 1), ld_agent(xp + 2), ld_agent(xp + 3));
+  } else {
+    v = *(const float4 *)(x + 4 * lane);
+  }
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   amax = group_max<64>(amax);
   const float scale = amax / 127.0f;
   const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
   const int8_t a = q8_round(v.x * inv), b = q8_round(v.y * inv), c = q8_round(v.z * inv), e = q8_round(v.w * inv);
-  *(uint32_t *)(q + 4 * lane) = pack_i8x4(a, b, c, e);
   int s = (int)a + (int)b + (int)c + (int)e;
   s = group_sum_i<4>(s);
-  if ((lane & 3) == 0) bsums[lane >> 2] = s;
-  if (lane == 0) *d = scale;
+  if constexpr (COHERENT) {
+    st_agent((uint32_t *)(q + 4 * lane), pack_i8x4(a, b, c, e));
+    if ((lane & 3) == 0) st_agent((uint32_t *)(bsums + (lane >> 2)), (uint32_t)s);
+    if (lane == 0) st_agent(d, scale);
+  } else {
+    *(uint32_t *)(q + 4 * lane) = pack_i8x4(a, b, c, e);
+    if ((lane & 3) == 0) bsums[lane >> 2] = s;
+    if (lane == 0) *d = scale;
+  }
 }
 
 // Q8Row::quantize of one 32-element block by an aligned group of 8 lanes

@@ -116,6 +116,16 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
                           const float *xd, const int32_t *xbs, float *out);
 
+// ---- the whole single-token layer in one persistent kernel (kmoe_fused.hip):
+// Q4_K tiled experts; routing published into pub's arrays; sync: zeroed
+// device words (16 + K*F/256 of them), zero again after the kernel, word 3 a
+// sticky time-out flag. hipErrorNotSupported for shapes it does not cover.
+bool layer_dec_fused_supported(int64_t d, int64_t F, int32_t E, int32_t K);
+hipError_t launch_layer_dec_fused(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t K,
+                                  int32_t norm_topk, float weights_scale, const ExpertTier &tier, int64_t F,
+                                  float *logits, int8_t *xq, float *xd, int32_t *xs, float *h, int8_t *hq, float *hd,
+                                  int32_t *hs, float *out, const DecSelect &pub, uint32_t *sync);
+
 // ---- int8 matrix-core path (kmoe_mfma.hip), Q4_K weights x Q8_K rows
 // Token rows at which the matrix-core kernels take over (KMOE_MFMA_MIN_ROWS, default 8).
 int mfma_min_rows();

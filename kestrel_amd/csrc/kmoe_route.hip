@@ -17,6 +17,7 @@
 // One lane per chain (16 lanes per logit); lane 0 of the 16 combines them.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
+#include "kmoe_logit.h"
 #include "kmoe_select.h"
 
 namespace kmoe {
@@ -340,7 +341,6 @@ struct RouteDecArgs {
   int vec;         // W, X 16-byte aligned and d % 4 == 0
 };
 
-constexpr int kDecMaxD = 8192;  // columns whose products one work-group holds in LDS
 
 // Softmax, top-k and renormalisation (transformer.rs:479-495) for the S <= 3
 // tokens whose logits the work-groups wrote, then the dispatch (the stable
@@ -415,97 +415,27 @@ __device__ void route_dec_tail(const RouteDecArgs &a, float *P, uint32_t *sel, i
 // tail; nothing waits on another work-group.
 template <int NV>
 __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
-  __shared__ __attribute__((aligned(16))) float T[8 * (kDecMaxD / 8 + 8)];
+  __shared__ __attribute__((aligned(16))) float T[kLogitLds];
   __shared__ float P[3 * kMaxExperts];
   __shared__ uint32_t sel[64];
   __shared__ int first[64];
   __shared__ int last;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int e = blockIdx.x, G = gridDim.x;
-  const int64_t d = a.d, n8 = d / 8;
-  const int cstr = (int)(((n8 + 3) & ~3ll) + 4);
-  const int nq = (int)(2 * n8);  // float4 groups in the first 8*n8 columns
+  const int64_t d = a.d;
+  const int nq = (int)(2 * (d / 8));  // float4 groups in the first 8*(d/8) columns
   const float *w = a.W + (int64_t)e * d;
 
   float4 wv[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int q = tid + 256 * v;
-    wv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (q < nq) wv[v] = a.vec ? *(const float4 *)(w + 4 * q)
-                              : make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
-  }
+  logit_row_load<NV>(w, nq, a.vec, wv, tid);
   for (int s = 0; s < a.S; ++s) {
     const float *x = a.X + (int64_t)s * d;
     __syncthreads();  // the previous token's fold has read T
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int q = tid + 256 * v;
-      if (q < nq) {
-        const float4 xv = a.vec ? *(const float4 *)(x + 4 * q)
-                                : make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
-        float *dst = T + (4 * (q & 1)) * cstr + (q >> 1);
-        dst[0 * cstr] = wv[v].x * xv.x;
-        dst[1 * cstr] = wv[v].y * xv.y;
-        dst[2 * cstr] = wv[v].z * xv.z;
-        dst[3 * cstr] = wv[v].w * xv.w;
-      }
-    }
-    __syncthreads();
-    if (wave == 0) {
-      float acc = 0.0f;
-      if (lane < 8) {
-        const float *row = T + lane * cstr;
-        const int nst = (int)(n8 / 32);
-        float4 A[8], B[8];
-        auto ld = [&](float4 (&R)[8], int st) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) R[i] = *(const float4 *)(row + 32 * st + 4 * i);
-        };
-        auto add = [&](const float4 (&R)[8]) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            acc = acc + R[i].x;
-            acc = acc + R[i].y;
-            acc = acc + R[i].z;
-            acc = acc + R[i].w;
-          }
-        };
-        if (nst > 0) {
-          // two register stages, the next one's LDS reads in flight while
-          // the current one is added (no branches inside the loop body)
-          ld(A, 0);
-          int st = 0;
-          for (; st + 2 < nst; st += 2) {
-            ld(B, st + 1);
-            add(A);
-            ld(A, st + 2);
-            add(B);
-          }
-          if (st + 1 < nst) {
-            ld(B, st + 1);
-            add(A);
-            add(B);
-          } else {
-            add(A);
-          }
-        }
-        for (int64_t c = (int64_t)nst * 32; c < n8; ++c) acc = acc + row[c];
-      }
-      float r = -0.0f;
-#pragma unroll
-      for (int l = 0; l < 8; ++l) r = r + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), l));
-      if (lane == 0) {
-        for (int64_t c = n8 * 8; c < d; ++c) {
-          const float pr = w[c] * x[c];
-          r = r + pr;
-        }
-        a.logits[(int64_t)s * a.E + e] = r;
-      }
-    } else if (s == 0) {
+    const float r = wg_logit<NV>(wv, w, x, d, a.vec, T, [&](int wv_) {
+      if (s != 0) return;
       // int8 activation rows: this work-group's blocks, one wave (Q8_K) or
       // eight lanes (Q8) per block
-      const int wid = e * 3 + (wave - 1), nw = 3 * G;
+      const int wid = e * 3 + (wv_ - 1), nw = 3 * G;
       if (a.qtype == T_Q4_K) {
         const int64_t nb = (int64_t)a.S * (d / 256);
         for (int64_t b = wid; b < nb; b += nw)
@@ -515,7 +445,8 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
         for (int64_t b = (int64_t)wid * 8 + (lane >> 3); b < nb; b += (int64_t)nw * 8)
           group8_quant_q8_block(a.X + b * 32, a.xq + b * 32, a.xd + b, a.xs + b * 2, lane & 7);
       }
-    }
+    });
+    if (tid == 0) a.logits[(int64_t)s * a.E + e] = r;
   }
   if (!a.done) return;  // logits only: the selection happens in the next kernel
   __syncthreads();

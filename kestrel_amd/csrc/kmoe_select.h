@@ -115,4 +115,44 @@ __device__ __forceinline__ void wave_route_one(float (&lv)[NPER], int E, int K, 
     for (int j = 0; j < K; ++j) w[j] = w[j] * wscale;
 }
 
+// Rank of each selected expert among the selection (all ids distinct): the
+// slot of selection entry j is rk[j], slots in ascending expert id.
+__device__ __forceinline__ void selection_ranks(const uint32_t (&sj)[16], int K, uint32_t (&rk)[16]) {
+  for (int j = 0; j < K; ++j) {
+    uint32_t r = 0;
+    for (int jj = 0; jj < K; ++jj) r += sj[jj] < sj[j] ? 1u : 0u;
+    rk[j] = r;
+  }
+}
+
+// The routing of one token from its selection, written by one wave: idx and
+// weights in selection order, perm / inv between selection entry and slot,
+// the active experts by slot, their count and the per-expert slot offsets
+// [E + 1] (the dispatch of transformer.rs:525-531 for one token).
+__device__ __forceinline__ void publish_selection(const uint32_t (&sj)[16], const float (&wj)[16],
+                                                  const uint32_t (&rk)[16], int K, int E, int lane, uint32_t *idx,
+                                                  float *wsel, uint32_t *perm, uint32_t *inv, int32_t *active,
+                                                  int32_t *n_active, uint32_t *offsets) {
+  uint32_t mysel = 0, myrk = 0;
+  float myw = 0.0f;
+  for (int j = 0; j < K; ++j) {
+    mysel = lane == j ? sj[j] : mysel;
+    myrk = lane == j ? rk[j] : myrk;
+    myw = lane == j ? wj[j] : myw;
+  }
+  if (lane < K) {
+    idx[lane] = mysel;
+    wsel[lane] = myw;
+    perm[myrk] = (uint32_t)lane;
+    inv[lane] = myrk;
+    active[myrk] = (int32_t)mysel;
+  }
+  if (lane == 0) *n_active = K;
+  for (int ee = lane; ee <= E; ee += 64) {
+    uint32_t c = 0;
+    for (int j = 0; j < K; ++j) c += sj[j] < (uint32_t)ee ? 1u : 0u;
+    offsets[ee] = c;
+  }
+}
+
 }  // namespace kmoe

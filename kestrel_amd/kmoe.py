@@ -33,6 +33,7 @@ SIGNATURES = {
     "kmoe_get_stream": (_P, [_P]),
     "kmoe_synchronize": (C.c_int, [_P]),
     "kmoe_set_regime": (C.c_int, [_P, C.c_int]),
+    "kmoe_set_decode_path": (C.c_int, [_P, C.c_int]),
     "kmoe_get_regime": (C.c_int, [_P]),
     "kmoe_vram_set_limit": (C.c_int, [_P, _u64]),
     "kmoe_vram_usage": (C.c_int, [_P, C.POINTER(_u64), C.POINTER(_u64)]),
@@ -156,6 +157,10 @@ class Context:
 
     def sync(self):
         self.check(self.lib.kmoe_synchronize(self.h))
+
+    def set_decode_path(self, path: int):
+        """0: one kernel per stage (default); 1: one persistent kernel for a single-token layer where supported."""
+        self.check(self.lib.kmoe_set_decode_path(self.h, path))
 
     def set_regime(self, regime: int):
         self.check(self.lib.kmoe_set_regime(self.h, regime))
