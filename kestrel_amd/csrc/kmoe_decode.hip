@@ -154,7 +154,136 @@ __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
   }
 }
 
+// Rows of one matrix against one Q8_K activation row (quant::matmul at one
+// row on the int path, quant.rs:262-309: dot_q4_k_8k per row), with the
+// structure of the gate/up kernel above: lane-constant offsets inside a row,
+// the activation slice in registers, 3 loads per task and row, RU rows per
+// wave step; lane u of the wave ends with row r0+u. Rows in GGUF order (head
+// at 144*sb, nibble chunk (k, j) at 144*sb + 16 + 32k + 16j; rows need only
+// 4-byte alignment) or tiled (tq4_qs_off).
+struct RowsArgs {
+  const uint8_t *W;
+  int64_t rows, cols;
+  const int8_t *xq;
+  const float *xd;
+  const int32_t *xbs;
+  float *out;
+  int32_t groups;  // work-groups striding over the rows
+};
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+template <bool TILED, int TPL, int RU>
+__global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nb = a.cols / 256, ntasks = 4 * nb;
+  const int64_t row_bytes = nb * 144;
+  uint32_t oh[TPL], oa[TPL], ob[TPL];
+  bool tv[TPL];
+  Slice s[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    const int64_t t0 = lane + 64 * i;
+    tv[i] = t0 < ntasks;
+    const int64_t t = tv[i] ? t0 : ntasks - 1;
+    const int64_t sb = t >> 2;
+    const int k = (int)(t & 3);
+    if constexpr (TILED) {
+      oh[i] = (uint32_t)(16 * sb);
+      oa[i] = (uint32_t)tq4_qs_off(nb, sb, k, 0);
+      ob[i] = oa[i] + (uint32_t)tq4_j_stride(nb, sb);
+    } else {
+      oh[i] = (uint32_t)(144 * sb);
+      oa[i] = oh[i] + 16 + 32 * k;
+      ob[i] = oa[i] + 16;
+    }
+    const int4 *xv = (const int4 *)(a.xq + 256 * sb + 64 * k);
+    s[i].x0 = xv[0];
+    s[i].x1 = xv[1];
+    s[i].x2 = xv[2];
+    s[i].x3 = xv[3];
+    const int4 bs = *(const int4 *)(a.xbs + 16 * sb + 4 * k);
+    s[i].bsA = bs.x + bs.y;
+    s[i].bsB = bs.z + bs.w;
+    s[i].d = a.xd[sb];
+  }
+  const int kq = lane & 3;
+  const int64_t rows = a.rows;
+  for (int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU; r0 < rows; r0 += (int64_t)a.groups * 4 * RU) {
+    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const uint8_t *row = a.W + (r0 + u < rows ? r0 + u : rows - 1) * row_bytes;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        if constexpr (TILED) {
+          hw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + oh[i]));
+          aw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + oa[i]));
+          bw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + ob[i]));
+        } else {
+          hw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + oh[i]));
+          aw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + oa[i]));
+          bw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + ob[i]));
+        }
+      }
+    }
+    float res = 0.0f;  // lane u < RU: row r0+u
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        int m;
+        const int si = q4k_quarter(hw[u][i], aw[u][i], bw[u][i], kq, s[i], m);
+        const float dd = f16_bits_to_f32(hw[u][i].x) * s[i].d, mf = f16_bits_to_f32(hw[u][i].x >> 16) * s[i].d;
+        const float v = fmaf(dd, (float)si, -(mf * (float)m));
+        acc += tv[i] ? v : 0.0f;
+      }
+      acc = group_sum<64>(acc);
+      res = lane == u ? acc : res;
+    }
+    if (lane < RU && r0 + lane < rows) a.out[r0 + lane] = res;
+  }
+}
+
 }  // namespace
+
+bool dec_rows_supported(int64_t cols) {
+  if (cols % 256 != 0) return false;
+  const int64_t ntasks = 4 * (cols / 256);
+  return ntasks >= 48 && ntasks <= 256;
+}
+
+hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+                           const float *xd, const int32_t *xbs, float *out) {
+  if (rows <= 0) return hipSuccess;
+  if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u) || (tiled && ((uintptr_t)w & 15u)) || ((uintptr_t)xq & 15u) ||
+      ((uintptr_t)xbs & 15u))
+    return hipErrorNotSupported;
+  const int tpl = (int)((4 * (cols / 256) + 63) / 64);
+  const int ru = tpl <= 2 ? 2 : 1;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0};
+  // work-group steps of 4*RU rows, spread evenly over about two groups per CU
+  const int64_t need = (rows + 4 * ru - 1) / (4 * ru);
+  const int64_t cap = 2LL * cus;
+  const int64_t per = (need + cap - 1) / cap;
+  a.groups = (int32_t)((need + per - 1) / per);
+  const dim3 grid((unsigned)a.groups);
+#define KMOE_DEC_ROWS(TL)                                                                      \
+  do {                                                                                         \
+    if (tpl == 1) KMOE_LAUNCH((k_dec_rows<TL, 1, 2>), grid, dim3(256), 0, st, a);              \
+    else if (tpl == 2) KMOE_LAUNCH((k_dec_rows<TL, 2, 2>), grid, dim3(256), 0, st, a);         \
+    else if (tpl == 3) KMOE_LAUNCH((k_dec_rows<TL, 3, 1>), grid, dim3(256), 0, st, a);         \
+    else KMOE_LAUNCH((k_dec_rows<TL, 4, 1>), grid, dim3(256), 0, st, a);                       \
+  } while (0)
+  if (tiled) KMOE_DEC_ROWS(true);
+  else KMOE_DEC_ROWS(false);
+#undef KMOE_DEC_ROWS
+  return hipGetLastError();
+}
 
 bool dec_gate_up_tq4_supported(int64_t cols, int ru) {
   if (cols % 256 != 0) return false;

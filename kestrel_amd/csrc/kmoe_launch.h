@@ -98,6 +98,13 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
                                   const Routing &rt, int max_active, const int8_t *xq, const float *xd,
                                   const int32_t *xbs, float *h, int ru, int wg_per_cu_x16,
                                   const DecSelect *sel = nullptr);
+// Q4_K rows of one matrix (GGUF bytes, or tiled) against one Q8_K row:
+// out[r] (kmoe_decode.hip). hipErrorNotSupported for rows narrower than 48 or wider than
+// 256 quarter-superblocks or misaligned pointers (activations 16 bytes, GGUF
+// rows 4, tiled rows 16).
+bool dec_rows_supported(int64_t cols);
+hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+                           const float *xd, const int32_t *xbs, float *out);
 // Tiled Q4_K down projection + combine for one token (kmoe_decode.hip): the k
 // active slots' Q8_K rows staged in LDS, one wave per output row.
 bool dec_down_tq4_supported(int64_t rows, int64_t cols, int k);

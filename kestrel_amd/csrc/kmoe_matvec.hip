@@ -893,7 +893,11 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   a.xbs = xbs;
   a.s_rows = 1;
   a.out = out;
-  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
+  if (type == T_Q4_K) {
+    const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out);
+    if (e != hipErrorNotSupported) return e;
+    return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
+  }
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
   return hipErrorInvalidValue;
 }

@@ -117,6 +117,7 @@ def test_q8_0_block_sums_bit_exact(ctx, orc, rows, cols, S):
 
 
 @pytest.mark.parametrize("t,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 14336, 4096), (Q4_K, 4096, 14336),
+                                         (Q4_K, 1001, 3072), (Q4_K, 77, 8192), (Q4_K, 3, 12288), (Q4_K, 4099, 2048),
                                          (Q8_0, 512, 1024), (Q8_0, 1024, 512)])
 def test_matvec_decode_matches_oracle(ctx, orc, t, rows, cols):
     """Dense quantized matvec at decode batch 1 (the C2 shapes for Q4_K)."""
