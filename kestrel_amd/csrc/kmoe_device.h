@@ -162,6 +162,17 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ void st_agent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint32_t add_agent(uint32_t *c, uint32_t v) {
+  return __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until this wave's vector memory operations have completed (s_waitcnt
+// vmcnt(0): gfx9 encoding, expcnt and lgkmcnt left at their maxima). Agent-
+// scope stores are then visible to every CU, so a counter update issued after
+// this wait (by this wave, or by another wave of the work-group after a
+// barrier) publishes them; a barrier alone waits only for LDS traffic.
+__device__ __forceinline__ void vm_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ int4 ld_agent4(const void *p) {
   const uint32_t *u = (const uint32_t *)p;
   return make_int4((int)ld_agent(u), (int)ld_agent(u + 1), (int)ld_agent(u + 2), (int)ld_agent(u + 3));

@@ -72,9 +72,6 @@ __device__ __forceinline__ bool wait_count(const uint32_t *c, uint32_t target) {
   }
   return false;
 }
-__device__ __forceinline__ uint32_t add_agent(uint32_t *c, uint32_t v) {
-  return __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // DC = 1: d <= 4096 (router rows in 4 float4 registers per thread, one gate/up
 // task per lane); DC = 2: d <= 8192. NPER: logits per lane in the selection.
@@ -106,6 +103,7 @@ __global__ void __launch_bounds__(256) k_layer_dec(FusedArgs a) {
         wave_quant_q8k_block<true>(a.X + b * 256, a.xq + b * 256, a.xd + b, a.xs + b * 16, lane);
     });
     if (tid == 0) st_agent(&a.logits[g], r);
+    vm_wait();  // the logit and this group's int8 rows before the count
     __syncthreads();
     if (tid == 0) add_agent(&sync[SY_LOGITS], 1u);
   }
@@ -220,6 +218,7 @@ __global__ void __launch_bounds__(256) k_layer_dec(FusedArgs a) {
     // each step wrote rows [8j, 8j+8) of the slot: count them per 256-row
     // block; the work-group completing a block quantizes it
     if (tid == 0) nq_s = 0;
+    vm_wait();  // the h rows before their counts
     __syncthreads();
     if (wave == 0) {  // one lane per step: the counter updates travel together
       for (int64_t j = m + (int64_t)lane * Q; j < NS; j += 64 * (int64_t)Q) {
@@ -238,6 +237,7 @@ __global__ void __launch_bounds__(256) k_layer_dec(FusedArgs a) {
         const int64_t b = (int64_t)slot * nbf + qlist[i];
         wave_quant_q8k_block<true>(a.h + b * 256, a.hq + b * 256, a.hd + b, a.hs + b * 16, lane);
       }
+      vm_wait();  // the quantized blocks before their count
       __syncthreads();
       if (tid == 0) add_agent(&sync[SY_QUANT], (uint32_t)nq);
     }
@@ -349,6 +349,7 @@ __global__ void __launch_bounds__(256) k_layer_dec(FusedArgs a) {
   }
 
   // ---- leave; the last work-group clears the counters
+  vm_wait();
   __syncthreads();
   if (tid == 0) {
     if (!ok) st_agent(&sync[SY_TIMEOUT], 1u);
