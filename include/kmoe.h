@@ -50,8 +50,8 @@ typedef enum {
 } kmoe_status;
 
 /* ggml type ids, kestrel-gguf types.rs:67-107. Kernels exist for F32
- * (router), Q8_0 and Q4_K. */
-enum { KMOE_F32 = 0, KMOE_Q8_0 = 8, KMOE_Q4_K = 12 };
+ * (router), Q8_0, Q4_K and Q6_K. */
+enum { KMOE_F32 = 0, KMOE_Q8_0 = 8, KMOE_Q4_K = 12, KMOE_Q6_K = 14 };
 
 /* Arithmetic regime of the quantized matmuls (quant.rs:229-328).
  * KMOE_REGIME_AVX2 (default): the reference on an AVX2+FMA host. A matmul
@@ -132,11 +132,18 @@ int kmoe_quantize_q8(kmoe_ctx *ctx, const float *x_dev, int64_t s_rows, int64_t 
  * nsb = cols/256. Computed by the same device code as the matvec. */
 int kmoe_q4k_block_sums(kmoe_ctx *ctx, const void *w_dev, int64_t rows, int64_t cols, const int8_t *q_dev,
                         const int32_t *bsums_dev, int64_t s_rows, int32_t *sumi_dev, int32_t *mins_dev);
+/* Integer accumulators of the Q6_K x Q8_K dot (avx2.rs:398-414), per
+ * (token s, row r, superblock b): sumi = sum_g sc_g * sum(q . x) over the 16
+ * groups of 16 weights (q the unsigned 6-bit values) and offs = sum_g sc_g *
+ * bsum_g, so the block's dot is d * xd * (sumi - 32 * offs). Layout as
+ * kmoe_q4k_block_sums. Computed by the same device code as the matvec. */
+int kmoe_q6k_block_sums(kmoe_ctx *ctx, const void *w_dev, int64_t rows, int64_t cols, const int8_t *q_dev,
+                        const int32_t *bsums_dev, int64_t s_rows, int32_t *sumi_dev, int32_t *offs_dev);
 /* Per-block int32 dot of Q8_0 x Q8 (avx2.rs:51-56), at [(s*rows + r)*nb + b], nb = cols/32. */
 int kmoe_q8_0_block_sums(kmoe_ctx *ctx, const void *w_dev, int64_t rows, int64_t cols, const int8_t *q_dev,
                          int64_t s_rows, int32_t *p_dev);
 /* Matvec on pre-quantized activations: the int8 path of kmoe_matmul with the
- * caller's Q8_K (Q4_K weights) or Q8 (Q8_0 weights, bsums unused) rows. */
+ * caller's Q8_K (Q4_K, Q6_K weights) or Q8 (Q8_0 weights, bsums unused) rows. */
 int kmoe_matvec_q8(kmoe_ctx *ctx, int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols,
                    const int8_t *q_dev, const float *d_dev, const int32_t *bsums_dev, int64_t s_rows, float *out_dev);
 

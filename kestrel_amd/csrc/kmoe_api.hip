@@ -29,6 +29,7 @@ int64_t block_size(int t) {
     case KMOE_F32: return 1;
     case KMOE_Q8_0: return 32;
     case KMOE_Q4_K: return 256;
+    case KMOE_Q6_K: return 256;
     default: return -1;
   }
 }
@@ -37,6 +38,7 @@ int64_t type_size(int t) {
     case KMOE_F32: return 4;
     case KMOE_Q8_0: return 34;
     case KMOE_Q4_K: return 144;
+    case KMOE_Q6_K: return 210;
     default: return -1;
   }
 }
@@ -278,11 +280,13 @@ int ensure_ws(kmoe_ctx *c, size_t need) {
   return KMOE_OK;
 }
 
-bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q8_0; }
+bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K || t == KMOE_Q8_0; }
+// K-quants take Q8_K activations (quant.rs:262-281); Q8_0 takes Q8 rows.
+bool is_kq(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K; }
 
 // Row-shape checks shared by the quantized kernels.
 int check_quant_shape(kmoe_ctx *c, int t, int64_t cols) {
-  if (!supported_weight(t)) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel (Q8_0=8, Q4_K=12)", t);
+  if (!supported_weight(t)) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel (Q8_0=8, Q4_K=12, Q6_K=14)", t);
   if (bytes_for(t, cols) < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
   if (t == KMOE_Q8_0 && cols % 64 != 0)
     return fail(c, KMOE_E_UNSUPPORTED, "Q8_0 rows need cols %% 64 == 0 (dword-aligned row starts), got %lld",
@@ -301,7 +305,7 @@ bool int_path(int regime, int64_t s_rows) {
 // kernel; otherwise (or if the row is too wide for it) the LDS-staged kernel.
 int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *q, const float *d,
                    const int32_t *s, int64_t s_rows, float *out) {
-  const char *name = t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q8_0";
+  const char *name = t == KMOE_Q4_K ? "matvec_q4k" : (t == KMOE_Q6_K ? "matvec_q6k" : "matvec_q8_0");
   if (t == KMOE_Q4_K && s_rows >= mfma_min_rows()) {  // int8 matrix cores
     hipError_t e = timed(c, "matvec_q4k_mfma", [&]() {
       return launch_plain_mfma(c->stream, w, rows, cols, q, d, s, s_rows, out, nullptr, nullptr);
@@ -346,7 +350,7 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
     LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out));
     return KMOE_OK;
   }
-  if (t == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
+  if (is_kq(t)) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   return matvec_q8_impl(c, t, w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);
 }
@@ -535,7 +539,7 @@ int kmoe_matvec_q8(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows
     return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows,
                 (long long)bytes_for(t, cols));
   if (rows == 0 || s_rows == 0) return KMOE_OK;
-  if (!w || !q || !d || !out || (t == KMOE_Q4_K && !bs)) return fail(c, KMOE_E_INVALID, "null pointer");
+  if (!w || !q || !d || !out || (is_kq(t) && !bs)) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
   return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, q, d, bs, s_rows, out);
 }
@@ -558,6 +562,19 @@ int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, 
   }
   LAUNCH(c, "block_sums_q4k",
          launch_block_sums(c->stream, KMOE_Q4_K, (const uint8_t *)w, rows, cols, q, bs, s_rows, sumi, mins));
+  return KMOE_OK;
+}
+
+int kmoe_q6k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, const int32_t *bs,
+                        int64_t s_rows, int32_t *sumi, int32_t *offs) {
+  if (!c) return KMOE_E_INVALID;
+  int rc = check_quant_shape(c, KMOE_Q6_K, cols);
+  if (rc) return rc;
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !q || !bs || !sumi || !offs) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "block_sums_q6k",
+         launch_block_sums(c->stream, KMOE_Q6_K, (const uint8_t *)w, rows, cols, q, bs, s_rows, sumi, offs));
   return KMOE_OK;
 }
 
@@ -991,7 +1008,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // and down+combine run as register-resident decode kernels.
   if (S == 1 && regime != KMOE_REGIME_EXACT) {
     if (!x_quantized) {
-      if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, 1, d, w.xq, w.xd, w.xs));
+      if (is_kq(gt)) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, 1, d, w.xq, w.xd, w.xs));
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, 1, d, w.xq, w.xd, w.xs));
       x_quantized = true;
     }
@@ -1025,7 +1042,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
     if (e != hipErrorNotSupported) {
       HIP_OK(c, e);
       // one row per expert: every slot is on the int8 path in either int8 regime
-      LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
+      LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
              launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
       e = timed(c, "moe_down_dec",
                 [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out); });
@@ -1043,7 +1060,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   // expert gate/up + SwiGLU (transformer.rs:551-558)
   if (any_int) {
     if (!x_quantized) {
-      if (gt == KMOE_Q4_K) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
+      if (is_kq(gt)) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
     }
     hipError_t e = hipErrorNotSupported;
@@ -1062,7 +1079,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   }
   // down (transformer.rs:559-560)
   if (any_int) {
-    LAUNCH(c, dt == KMOE_Q4_K ? "quant_slots_q8k" : "quant_slots_q8",
+    LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
            launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
     hipError_t e = hipErrorNotSupported;
     if (mfma && dt == KMOE_Q4_K)

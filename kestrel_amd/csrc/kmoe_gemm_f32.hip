@@ -62,6 +62,23 @@ __device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p,
       const float t = dl * (float)nib;
       o[i] = t - ml;
     }
+  } else if constexpr (TYPE == T_Q6_K) {  // quant.rs:180-201: y = (d * sc) * (q - 32)
+    // chunk kc = quarter k of superblock kc/4 (half h, nibble np); part p is
+    // weights 16*(p&1).. of row ri = 2*np + (p>>1) of the half
+    typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
+    const uint8_t *blk = row + (kc >> 2) * 210;
+    const int k = (int)(kc & 3), h = k >> 1, np = k & 1, ri = 2 * np + (p >> 1), l0 = 16 * (p & 1);
+    const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+    const float ds = d * (float)(int8_t)blk[192 + 8 * h + 2 * ri + (p & 1)];
+    const u32x4u2 ql = *(const u32x4u2 *)(blk + 64 * h + 32 * (ri & 1) + l0);
+    const u32x4u2 qh = *(const u32x4u2 *)(blk + 128 + 32 * h + l0);
+    const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+      const int q = (int)((np ? (lb >> 4) : (lb & 0xfu)) | (((hb >> (2 * ri)) & 3u) << 4)) - 32;
+      o[i] = ds * (float)q;
+    }
   } else if constexpr (TYPE == T_Q8_0) {
     const int64_t b = 2 * kc + (p >> 1);
     const uint8_t *blk = row + b * 34;
@@ -82,7 +99,10 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   __shared__ float Xs[TT][PAD];
   const int tid = threadIdx.x;
   const int64_t rows = a.rows, cols = a.cols;
-  const int64_t row_bytes = TYPE == T_Q4_K ? cols / 256 * 144 : (TYPE == T_Q8_0 ? cols / 32 * 34 : cols * 4);
+  const int64_t row_bytes = TYPE == T_Q4_K   ? cols / 256 * 144
+                            : TYPE == T_Q6_K ? cols / 256 * 210
+                            : TYPE == T_Q8_0 ? cols / 32 * 34
+                                             : cols * 4;
 
   int n;
   int64_t p0 = 0;
@@ -173,6 +193,9 @@ hipError_t launch_type(hipStream_t st, int type, const GArgs &a, dim3 grid) {
       break;
     case T_Q8_0:
       KMOE_LAUNCH((k_gemm_f32<T_Q8_0, MODE>), grid, dim3(256), 0, st, a);
+      break;
+    case T_Q6_K:
+      KMOE_LAUNCH((k_gemm_f32<T_Q6_K, MODE>), grid, dim3(256), 0, st, a);
       break;
     case T_F32:
       KMOE_LAUNCH((k_gemm_f32<T_F32, MODE>), grid, dim3(256), 0, st, a);

@@ -27,7 +27,9 @@ extern thread_local LaunchTiming g_timing;
     }                                                                                                \
   } while (0)
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12 };
+enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+// K-quants read Q8_K activations (256-blocks with 16-sums): Q4_K and Q6_K.
+constexpr bool is_kquant(int t) { return t == T_Q4_K || t == T_Q6_K; }
 enum { REGIME_AVX2 = 0, REGIME_INT8 = 1, REGIME_EXACT = 2 };
 
 // ---- activation quantizers (kmoe_quant.hip)

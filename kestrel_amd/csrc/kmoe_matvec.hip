@@ -5,6 +5,9 @@
 //     sumi_b = sum_j sc_j * sum_{32 elems of j} q*x,  mins_b = sum_j m_j * (bsum pair of j)
 //     y += (d_b * xd_b) * sumi_b - (dmin_b * xd_b) * mins_b
 //   Q8_0 x Q8 (avx2.rs:49-58): per block b, p_b = sum q*x, y += (d_b * xd_b) * p_b
+//   Q6_K x Q8_K (avx2.rs:384-419): per superblock b, with 6-bit q in 0..63 and
+//     signed 16-element scales sc_g, t_b = sum_g sc_g * (sum_{16 elems} q*x - 32 * bsum_g)
+//     y += (d_b * xd_b) * t_b
 // The integers are exact (int32, no saturation: max |pair| is 2*15*127 for
 // Q4_K and 2*128*127 for Q8_0), so sumi_b, mins_b and p_b equal the
 // reference's bit for bit; the fp32 epilogue sums in a different order, which
@@ -53,14 +56,31 @@ __device__ __forceinline__ bool int_regime(int regime, int n) {
   return regime == REGIME_INT8 || (regime == REGIME_AVX2 && n < 4);
 }
 
+// Block geometry per weight type: elements and bytes per block, tasks per
+// block (a K-quant task is a quarter superblock, 64 weights).
+template <int TYPE>
+struct QT;
+template <>
+struct QT<T_Q4_K> {
+  static constexpr int EL = 256, BYTES = 144, TPB = 4;
+};
+template <>
+struct QT<T_Q6_K> {
+  static constexpr int EL = 256, BYTES = 210, TPB = 4;
+};
+template <>
+struct QT<T_Q8_0> {
+  static constexpr int EL = 32, BYTES = 34, TPB = 1;
+};
+
 // Bytes per activation row in LDS, 16-byte aligned pieces: q, sums, scales.
 template <int TYPE>
 struct ActLayout {
   int64_t q, s, d, total;
   __host__ __device__ ActLayout(int64_t cols) {
     q = (cols + 15) & ~15ll;
-    s = TYPE == T_Q4_K ? ((cols / 16 * 4 + 15) & ~15ll) : 0;  // Q8_0 never reads the 16-sums
-    const int64_t nd = TYPE == T_Q4_K ? cols / 256 : cols / 32;
+    s = is_kquant(TYPE) ? ((cols / 16 * 4 + 15) & ~15ll) : 0;  // Q8_0 never reads the 16-sums
+    const int64_t nd = cols / QT<TYPE>::EL;
     d = (nd * 4 + 15) & ~15ll;
     total = q + s + d;
   }
@@ -128,6 +148,68 @@ __device__ __forceinline__ void q4k_ints(const Q4kW &w, int k, const int8_t *xq_
   mins = mA * (bs.x + bs.y) + mB * (bs.z + bs.w);
 }
 
+// Q6_K (quant.rs:180-201): 210-byte superblocks of ql[128] (low 4 bits),
+// qh[64] (high 2 bits), sc[16] (signed scales of 16 elements) and the f16 d at
+// byte 208. Task t is quarter k of superblock t/4: half h = k/2, nibble
+// p = k%2. Its 64 weights are rows ri = 2p (weights 0-31) and 2p+1 (32-63) of
+// half h; weight l of row ri is nibble p of ql[64h + 32*(ri&1) + l] with bits
+// 2ri..2ri+1 of qh[32h + l] above it, scaled by sc[8h + 2ri + l/16].
+// Superblocks start on 2-byte boundaries; the 16-byte loads rely on the
+// target's unaligned global access.
+struct Q6kW {
+  uint4 l0, l1, l2, l3;  // ql[64h, 64h+64)
+  uint4 h0, h1;          // qh[32h, 32h+32)
+  uint32_t sc;           // sc[8h+4p, 8h+4p+4)
+  uint32_t d;            // f16 bits of d
+};
+typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32u2 __attribute__((aligned(2)));
+__device__ __forceinline__ uint4 ld_nt_u2(const uint8_t *p) {
+  const u32x4u2 v = __builtin_nontemporal_load((const u32x4u2 *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ Q6kW q6k_load(const uint8_t *row, int t) {
+  const int64_t sb = t >> 2;
+  const int k = t & 3, h = k >> 1, p = k & 1;
+  const uint8_t *b = row + sb * 210;
+  Q6kW w;
+  w.l0 = ld_nt_u2(b + 64 * h);
+  w.l1 = ld_nt_u2(b + 64 * h + 16);
+  w.l2 = ld_nt_u2(b + 64 * h + 32);
+  w.l3 = ld_nt_u2(b + 64 * h + 48);
+  w.h0 = ld_nt_u2(b + 128 + 32 * h);
+  w.h1 = ld_nt_u2(b + 128 + 32 * h + 16);
+  w.sc = __builtin_nontemporal_load((const u32u2 *)(b + 192 + 8 * h + 4 * p));
+  w.d = __builtin_nontemporal_load((const uint16_t *)(b + 208));
+  return w;
+}
+// Integer part of one Q6_K task: sumi = sum_g sc_g * sum q*x over its four
+// 16-weight groups, offs = sum_g sc_g * bsum_g (avx2.rs:398-414).
+__device__ __forceinline__ void q6k_ints(const Q6kW &w, int k, const int4 &x0, const int4 &x1, const int4 &x2,
+                                         const int4 &x3, const int4 &bs, int &sumi, int &offs) {
+  const int sn = 4 * (k & 1);  // nibble shift; the qh bits of row 2p sit at 4p, of row 2p+1 at 4p+2
+  const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x03030303u;
+  const uint32_t L[16] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w,
+                          w.l2.x, w.l2.y, w.l2.z, w.l2.w, w.l3.x, w.l3.y, w.l3.z, w.l3.w};
+  const uint32_t H[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+  const uint32_t X[16] = {(uint32_t)x0.x, (uint32_t)x0.y, (uint32_t)x0.z, (uint32_t)x0.w,
+                          (uint32_t)x1.x, (uint32_t)x1.y, (uint32_t)x1.z, (uint32_t)x1.w,
+                          (uint32_t)x2.x, (uint32_t)x2.y, (uint32_t)x2.z, (uint32_t)x2.w,
+                          (uint32_t)x3.x, (uint32_t)x3.y, (uint32_t)x3.z, (uint32_t)x3.w};
+  int g[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t qa = ((L[i] >> sn) & m4) | (((H[i] >> sn) & m2) << 4);
+    const uint32_t qb = ((L[8 + i] >> sn) & m4) | (((H[i] >> (sn + 2)) & m2) << 4);
+    g[i >> 2] = sdot4(qa, X[i], g[i >> 2]);
+    g[2 + (i >> 2)] = sdot4(qb, X[8 + i], g[2 + (i >> 2)]);
+  }
+  const int s0 = (int)(int8_t)(w.sc & 0xff), s1 = (int)(int8_t)((w.sc >> 8) & 0xff);
+  const int s2 = (int)(int8_t)((w.sc >> 16) & 0xff), s3 = (int)(int8_t)(w.sc >> 24);
+  sumi = s0 * g[0] + s1 * g[1] + s2 * g[2] + s3 * g[3];
+  offs = s0 * bs.x + s1 * bs.y + s2 * bs.z + s3 * bs.w;
+}
+
 struct Q80W {
   uint4 a, b;
   uint32_t c;
@@ -178,9 +260,9 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row_in_wave = lane / LPR, lr = lane % LPR;
   const int64_t cols = a.cols, rows = a.rows;
-  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
-  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
   const int64_t xs_stride = cols / 16, xd_stride = nblk;
   const ActLayout<TYPE> L(cols);
 
@@ -218,7 +300,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
       char *dst = smem + t * L.total;
       const uint32_t *sq = (const uint32_t *)(a.xq + src * cols);
       for (int64_t i = threadIdx.x; i < cols / 4; i += 256) ((uint32_t *)dst)[i] = sq[i];
-      if constexpr (TYPE == T_Q4_K) {
+      if constexpr (is_kquant(TYPE)) {
         const int32_t *ss = a.xbs + src * xs_stride;
         for (int64_t i = threadIdx.x; i < xs_stride; i += 256) ((int32_t *)(dst + L.q))[i] = ss[i];
       }
@@ -268,6 +350,38 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                     q4k_ints(w1, k, xq_sb, xbs_sb, si, mi);
                     acc1[tk] = fmaf(d1 * xd, (float)si, acc1[tk]);
                     acc1[tk] = fmaf(-(m1 * xd), (float)mi, acc1[tk]);
+                  }
+                }
+              }
+            }
+          } else if constexpr (TYPE == T_Q6_K) {
+            const int sb = t >> 2, k = t & 3;
+            const Q6kW w0 = q6k_load(row0, t);
+            Q6kW w1;
+            if constexpr (MODE == M_GATE_UP) w1 = q6k_load(row1, t);
+            const float d0 = f16_bits_to_f32(w0.d);
+#pragma unroll
+            for (int tk = 0; tk < NT; ++tk) {
+              if (tk < nt) {
+                const char *act = smem + tk * L.total;
+                const int4 *xv = (const int4 *)((const int8_t *)act + sb * 256 + 64 * k);
+                const int4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+                const int4 bs = *((const int4 *)(act + L.q) + sb * 4 + k);
+                const float xd = ((const float *)(act + L.q + L.s))[sb];
+                int si, oi;
+                q6k_ints(w0, k, x0, x1, x2, x3, bs, si, oi);
+                if constexpr (MODE == M_SUMS) {
+                  const int ss = group_sum_i<4>(si), os = group_sum_i<4>(oi);
+                  if (k == 0) {
+                    const int64_t o = ((int64_t)(c0 + tk) * rows + r) * nblk + sb;
+                    a.isumi[o] = ss;
+                    a.imins[o] = os;
+                  }
+                } else {
+                  acc0[tk] = fmaf(d0 * xd, (float)(si - 32 * oi), acc0[tk]);
+                  if constexpr (MODE == M_GATE_UP) {
+                    q6k_ints(w1, k, x0, x1, x2, x3, bs, si, oi);
+                    acc1[tk] = fmaf(f16_bits_to_f32(w1.d) * xd, (float)(si - 32 * oi), acc1[tk]);
                   }
                 }
               }
@@ -350,6 +464,11 @@ struct ActSlice<T_Q4_K> {
   float d;
 };
 template <>
+struct ActSlice<T_Q6_K> {
+  int4 x0, x1, x2, x3, bs;
+  float d;
+};
+template <>
 struct ActSlice<T_Q8_0> {
   int4 x0, x1;
   float d;
@@ -358,7 +477,7 @@ struct ActSlice<T_Q8_0> {
 template <int TYPE>
 __device__ __forceinline__ void act_load(ActSlice<TYPE> &s, const int8_t *xq, const float *xd, const int32_t *xbs,
                                          int t) {
-  if constexpr (TYPE == T_Q4_K) {
+  if constexpr (is_kquant(TYPE)) {
     const int sb = t >> 2, k = t & 3;
     const int4 *v = (const int4 *)(xq + 256 * sb + 64 * k);
     s.x0 = v[0];
@@ -385,10 +504,16 @@ template <>
 struct WTask<T_Q8_0> {
   Q80W w;
 };
+template <>
+struct WTask<T_Q6_K> {
+  Q6kW w;
+};
 
+// Q6_K rows are never tiled: TILED applies to Q4_K only.
 template <int TYPE, bool TILED>
 __device__ __forceinline__ void w_load(WTask<TYPE> &w, const uint8_t *row, int t, int64_t nblk) {
   if constexpr (TYPE == T_Q4_K) w.w = q4k_load<TILED>(row, t, nblk);
+  else if constexpr (TYPE == T_Q6_K) w.w = q6k_load(row, t);
   else w.w = q80_load(row, t);
 }
 
@@ -424,6 +549,10 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE> &wt, int t, const Ac
     acc = fmaf(d * s.d, (float)sumi, acc);
     acc = fmaf(-(dmin * s.d), (float)mins, acc);
     return acc;
+  } else if constexpr (TYPE == T_Q6_K) {
+    int sumi, offs;
+    q6k_ints(wt.w, t & 3, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
+    return fmaf(f16_bits_to_f32(wt.w.d) * s.d, (float)(sumi - 32 * offs), acc);
   } else {
     const Q80W &w = wt.w;
     const uint32_t v[9] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w, w.c};
@@ -458,9 +587,9 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row_in_wave = lane / LPR, lr = lane % LPR;
   const int64_t cols = a.cols, rows = a.rows;
-  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
-  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
   const int64_t xs_stride = cols / 16;
   const int64_t bpe = (rows + RB - 1) / RB;
   int64_t total = bpe;
@@ -600,9 +729,9 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   __shared__ float outv[kSplitRbMax];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t cols = a.cols, rows = a.rows;
-  const int64_t nblk = TYPE == T_Q4_K ? cols / 256 : cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
-  const int64_t row_bytes = nblk * (TYPE == T_Q4_K ? 144 : 34);
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
   const int64_t xs_stride = cols / 16;
   const int tpw = (ntasks + 3) / 4;  // tasks per wave
   const int64_t r0 = (int64_t)blockIdx.x * rb_rows;
@@ -787,7 +916,7 @@ bool reg_geometry(int type, int ntasks, int &lpr, int &tpl) {
     while (lpr < ntasks) lpr *= 2;
   }
   tpl = (ntasks + lpr - 1) / lpr;
-  return type == T_Q4_K ? tpl <= 4 : tpl <= 8;
+  return is_kquant(type) ? tpl <= 4 : tpl <= 8;
 }
 
 template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
@@ -807,13 +936,13 @@ hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_task
 
 template <int TYPE, int MODE, int RU>
 hipError_t dispatch_reg(hipStream_t st, const MvArgs &a, int n_groups) {
-  const int64_t nblk = TYPE == T_Q4_K ? a.cols / 256 : a.cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t nblk = a.cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
   int lpr, tpl;
   if (!reg_geometry(TYPE, ntasks, lpr, tpl)) return hipErrorNotSupported;
   const int64_t rb = 4 * (64 / lpr) * RU;
   const int64_t max_tasks = (a.rows + rb - 1) / rb * n_groups;
-  constexpr int TM = TYPE == T_Q4_K ? 4 : 8;
+  constexpr int TM = is_kquant(TYPE) ? 4 : 8;
   switch (lpr) {
     case 64:
       if (tpl == 1) return launch_reg<TYPE, 64, 1, RU, MODE>(st, a, tpl, max_tasks);
@@ -854,8 +983,8 @@ int pick_lpr(int ntasks) {
 
 template <int TYPE, int MODE>
 hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_max) {
-  const int64_t nblk = TYPE == T_Q4_K ? a.cols / 256 : a.cols / 32;
-  const int ntasks = TYPE == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t nblk = a.cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
   const int lpr = pick_lpr(ntasks);
 #define KMOE_LPR_CASE(LPRV)                                                                          \
   case LPRV:                                                                                         \
@@ -876,7 +1005,7 @@ hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_ma
 constexpr int kRowsPerBlock = 64;
 
 bool act_fits(int type, int64_t cols) {
-  const int64_t per = type == T_Q4_K ? ActLayout<T_Q4_K>(cols).total : ActLayout<T_Q8_0>(cols).total;
+  const int64_t per = is_kquant(type) ? ActLayout<T_Q4_K>(cols).total : ActLayout<T_Q8_0>(cols).total;
   return 3 * per <= 65536;
 }
 
@@ -898,6 +1027,7 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
     if (e != hipErrorNotSupported) return e;
     return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
   }
+  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_PLAIN, 2>(st, a, 1);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
   return hipErrorInvalidValue;
 }
@@ -925,6 +1055,7 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
     return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
   }
   if (sel) return hipErrorNotSupported;
+  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
   return hipErrorInvalidValue;
 }
@@ -942,8 +1073,8 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
   a.out = out;
   a.tier = tier;
   a.rt = rt;
-  const int64_t nblk = type == T_Q4_K ? cols / 256 : cols / 32;
-  const int ntasks = type == T_Q4_K ? (int)(4 * nblk) : (int)nblk;
+  const int64_t nblk = cols / (is_kquant(type) ? 256 : 32);
+  const int ntasks = (int)((is_kquant(type) ? 4 : 1) * nblk);
   // one token: its topk experts are distinct, so k slots are active
   if (type == T_Q4_K && use_dec_down() && dec_down_tq4_supported(rows, cols, rt.topk))
     return launch_dec_down_tq4(st, tier, rows, cols, rt, rt.topk, hq, hd, hbs, out);
@@ -963,6 +1094,9 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
         } else {
           KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
         }
+      } else if (type == T_Q6_K) {  // 26 registers per task: fewer rows per item
+        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q6_K, 2, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+        else KMOE_LAUNCH((k_down_splitk<T_Q6_K, 1, 2>), dim3(grid), dim3(256), 0, st, a, rb);
       } else {
         if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q8_0, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
         else KMOE_LAUNCH((k_down_splitk<T_Q8_0, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
@@ -971,6 +1105,7 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
     }
   }
   if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_DOWN_COMBINE, 1>(st, a, 1);
+  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_DOWN_COMBINE, 1>(st, a, 1);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_DOWN_COMBINE, 1>(st, a, 1);
   return hipErrorInvalidValue;
 }
@@ -992,6 +1127,7 @@ hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t
   dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   const int nt = s_rows == 1 ? 1 : 3;
   if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_PLAIN>(st, a, grid, nt);
+  if (type == T_Q6_K) return dispatch_lpr_nt<T_Q6_K, M_PLAIN>(st, a, grid, nt);
   if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_PLAIN>(st, a, grid, nt);
   return hipErrorInvalidValue;
 }
@@ -1011,10 +1147,11 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
   a.imins = mins;
   a.rows_per_block = kRowsPerBlock;
   dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  // The Q8_0 scales are not read by the sums; Q4_K's dw/xd are not either, but
+  // The Q8_0 scales are not read by the sums; the K-quants' dw/xd are not either, but
   // the staging copies xd: give it a valid dummy of the right length.
   a.xd = (const float *)xq;  // nblk*4 bytes <= cols bytes are readable there
   if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_SUMS>(st, a, grid, 1);
+  if (type == T_Q6_K) return dispatch_lpr_nt<T_Q6_K, M_SUMS>(st, a, grid, 1);
   if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_SUMS>(st, a, grid, 1);
   return hipErrorInvalidValue;
 }
@@ -1041,6 +1178,9 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
   if (type == T_Q4_K)
     return mode == 0 ? dispatch_lpr_nt<T_Q4_K, M_GATE_UP>(st, a, grid, nt)
                      : dispatch_lpr_nt<T_Q4_K, M_DOWN>(st, a, grid, nt);
+  if (type == T_Q6_K)
+    return mode == 0 ? dispatch_lpr_nt<T_Q6_K, M_GATE_UP>(st, a, grid, nt)
+                     : dispatch_lpr_nt<T_Q6_K, M_DOWN>(st, a, grid, nt);
   if (type == T_Q8_0)
     return mode == 0 ? dispatch_lpr_nt<T_Q8_0, M_GATE_UP>(st, a, grid, nt)
                      : dispatch_lpr_nt<T_Q8_0, M_DOWN>(st, a, grid, nt);

@@ -333,7 +333,7 @@ struct RouteDecArgs {
   float *wsel;
   uint32_t *perm, *offsets, *inv;
   int32_t *n_active, *active;
-  int qtype;  // 0: none, T_Q4_K: Q8_K rows, T_Q8_0: Q8 rows
+  int qtype;  // 0: none, T_Q4_K or T_Q6_K: Q8_K rows, T_Q8_0: Q8 rows
   int8_t *xq;
   float *xd;
   int32_t *xs;
@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
       // int8 activation rows: this work-group's blocks, one wave (Q8_K) or
       // eight lanes (Q8) per block
       const int wid = e * 3 + (wv_ - 1), nw = 3 * G;
-      if (a.qtype == T_Q4_K) {
+      if (is_kquant(a.qtype)) {
         const int64_t nb = (int64_t)a.S * (d / 256);
         for (int64_t b = wid; b < nb; b += nw)
           wave_quant_q8k_block(a.X + b * 256, a.xq + b * 256, a.xd + b, a.xs + b * 16, lane);
@@ -496,7 +496,7 @@ hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t 
                               const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
                               int32_t *sums) {
   if (n_slots == 0) return hipSuccess;
-  if (type == T_Q4_K) {
+  if (is_kquant(type)) {
     const int64_t nb = n_slots * (cols / 256);
     KMOE_LAUNCH(k_quant_slots_q8k, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, h, n_slots, cols, rt,
                        idx_flat, regime, q, d, sums);

@@ -15,7 +15,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkmoe.so")
 
-F32, Q8_0, Q4_K = 0, 8, 12
+F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
 REGIME_AVX2, REGIME_INT8, REGIME_EXACT = 0, 1, 2
 BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144)}
 
@@ -45,6 +45,7 @@ SIGNATURES = {
     "kmoe_quantize_q8k": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _P]),
     "kmoe_quantize_q8": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _P]),
     "kmoe_q4k_block_sums": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _i64, _P, _P]),
+    "kmoe_q6k_block_sums": (C.c_int, [_P, _P, _i64, _i64, _P, _P, _i64, _P, _P]),
     "kmoe_q8_0_block_sums": (C.c_int, [_P, _P, _i64, _i64, _P, _i64, _P]),
     "kmoe_matvec_q8": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _P, _P, _i64, _P]),
     "kmoe_route": (C.c_int, [_P, _P, _i32, _i64, _P, _i64, _i32, _i32, _f, _P, _P, _P]),
@@ -216,6 +217,15 @@ class Context:
         self.check(self.lib.kmoe_q4k_block_sums(self.h, _ptr(w), rows, cols, _ptr(q), _ptr(bs), S, _ptr(sumi),
                                                 _ptr(mins)))
         return sumi, mins
+
+    def q6k_block_sums(self, w, rows, cols, q, bs):
+        S = q.shape[0]
+        nb = cols // 256
+        sumi = self._empty((S, rows, nb), self.torch.int32)
+        offs = self._empty((S, rows, nb), self.torch.int32)
+        self.check(self.lib.kmoe_q6k_block_sums(self.h, _ptr(w), rows, cols, _ptr(q), _ptr(bs), S, _ptr(sumi),
+                                                _ptr(offs)))
+        return sumi, offs
 
     def q8_0_block_sums(self, w, rows, cols, q):
         S = q.shape[0]

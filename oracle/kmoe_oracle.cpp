@@ -390,6 +390,50 @@ void orc_quantize_q4_k(const float *x, size_t n, uint8_t *out) {
   }
 }
 
+void orc_quantize_q6_k(const float *x, size_t n, uint8_t *out) {
+  // Ours (kestrel only reads Q6_K). Sub-block j (16 elements) gets a signed
+  // scale sc_j = round(amax_j / 32 / d) with d = max_j(amax_j / 32) / 127;
+  // q = clamp(round(x / (d sc_j)), -32, 31) + 32, packed as quant.rs:180-201
+  // reads it: element h*128 + 32*ri + l -> low (ri < 2) or high nibble of
+  // ql[h*64 + 32*(ri&1) + l] and bits 2*ri..2*ri+1 of qh[h*32 + l].
+  for (size_t b = 0; b < n / 256; ++b) {
+    const float *xs = x + 256 * b;
+    uint8_t *blk = out + 210 * b;
+    float sub[16], mx = 0.0f;
+    for (int j = 0; j < 16; ++j) {
+      float a = 0.0f;
+      for (int l = 0; l < 16; ++l) a = std::max(a, std::fabs(xs[16 * j + l]));
+      sub[j] = a / 32.0f;
+      mx = std::max(mx, sub[j]);
+    }
+    const uint16_t dh = f32_to_f16(mx / 127.0f);
+    const float df = f16_to_f32(dh);
+    int8_t sc[16];
+    for (int j = 0; j < 16; ++j) {
+      float v = df > 0.0f ? std::round(sub[j] / df) : 0.0f;
+      sc[j] = (int8_t)std::min(127.0f, std::max(-127.0f, v));
+    }
+    uint8_t q[256];
+    for (int i = 0; i < 256; ++i) {
+      const float dl = df * (float)sc[i / 16];
+      float v = dl != 0.0f ? std::round(xs[i] / dl) : 0.0f;
+      q[i] = (uint8_t)(std::min(31.0f, std::max(-32.0f, v)) + 32.0f);
+    }
+    std::memset(blk, 0, 210);
+    for (int h = 0; h < 2; ++h)
+      for (int ri = 0; ri < 4; ++ri)
+        for (int l = 0; l < 32; ++l) {
+          const uint8_t v = q[h * 128 + 32 * ri + l];
+          uint8_t &ql = blk[h * 64 + 32 * (ri & 1) + l];
+          ql |= (uint8_t)((v & 0xF) << (ri < 2 ? 0 : 4));
+          blk[128 + h * 32 + l] |= (uint8_t)(((v >> 4) & 3) << (2 * ri));
+        }
+    for (int j = 0; j < 16; ++j) blk[192 + j] = (uint8_t)sc[j];
+    blk[208] = (uint8_t)(dh & 0xff);
+    blk[209] = (uint8_t)(dh >> 8);
+  }
+}
+
 void orc_quantize_rows(int t, const float *x, size_t rows, size_t cols, uint8_t *out, int threads) {
   int64_t rb = orc_bytes_for(t, (int64_t)cols);
   if (rb < 0) return;
@@ -399,6 +443,7 @@ void orc_quantize_rows(int t, const float *x, size_t rows, size_t cols, uint8_t 
     for (size_t r = c * chunk; r < r1; ++r) {
       if (t == ORC_Q8_0) orc_quantize_q8_0(x + r * cols, cols, out + r * rb);
       else if (t == ORC_Q4_K) orc_quantize_q4_k(x + r * cols, cols, out + r * rb);
+      else if (t == ORC_Q6_K) orc_quantize_q6_k(x + r * cols, cols, out + r * rb);
       else if (t == ORC_F32) std::memcpy(out + r * rb, x + r * cols, cols * 4);
     }
   });
@@ -788,6 +833,99 @@ void orc_q4k_block_acc_bruteforce(const uint8_t *w, size_t n, const int8_t *aq, 
   }
 }
 
+// avx2.rs:384-419, integer part: per block the 8 i32 lanes of `sumi` and the
+// offset sum `offs`. The four 32-byte rows r of half h hold 6-bit values
+// (0..63); maddubs pairs them with x, madd applies sc[2r] to bytes 0-15 and
+// sc[2r+1] to bytes 16-31.
+static void q6k_block_lanes(const uint8_t *blk, const int8_t *xq, const int32_t *bsums, __m256i &sumi,
+                            int32_t &offs) {
+  const __m256i m4 = _mm256_set1_epi8(0x0F);
+  const __m256i m3 = _mm256_set1_epi8(0x03);
+  sumi = _mm256_setzero_si256();
+  offs = 0;
+  for (int h = 0; h < 2; ++h) {
+    const uint8_t *ql = blk + h * 64;
+    const __m256i qh = load(blk + 128 + h * 32);
+    const uint8_t *sc = blk + 192 + h * 8;
+    const __m256i qa = load(ql), qb = load(ql + 32);
+    const __m256i r[4] = {
+        _mm256_or_si256(_mm256_and_si256(qa, m4), _mm256_slli_epi16(_mm256_and_si256(qh, m3), 4)),
+        _mm256_or_si256(_mm256_and_si256(qb, m4),
+                        _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 2), m3), 4)),
+        _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(qa, 4), m4),
+                        _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 4), m3), 4)),
+        _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(qb, 4), m4),
+                        _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(qh, 6), m3), 4)),
+    };
+    for (int ri = 0; ri < 4; ++ri) {
+      const int16_t s0 = (int16_t)(int8_t)sc[2 * ri], s1 = (int16_t)(int8_t)sc[2 * ri + 1];
+      const __m256i x = load(xq + h * 128 + ri * 32);
+      const __m256i p = _mm256_madd_epi16(_mm256_maddubs_epi16(r[ri], x),
+                                          _mm256_set_m128i(_mm_set1_epi16(s1), _mm_set1_epi16(s0)));
+      sumi = _mm256_add_epi32(sumi, p);
+      const int k16 = h * 8 + ri * 2;
+      offs += (int32_t)s0 * bsums[k16] + (int32_t)s1 * bsums[k16 + 1];
+    }
+  }
+}
+
+float orc_dot_q6_k_8k(const uint8_t *w, size_t n, const int8_t *aq, const float *ad, const int32_t *abs) {
+  // avx2.rs:384-419
+  __m256 acc = _mm256_setzero_ps();
+  for (size_t b = 0; b < n / 256; ++b) {
+    const uint8_t *blk = w + 210 * b;
+    const float d = f16at(blk + 208) * ad[b];
+    __m256i sumi;
+    int32_t offs;
+    q6k_block_lanes(blk, aq + 256 * b, abs + 16 * b, sumi, offs);
+    // sum sc (q - 32) x = sum sc q x - 32 sum sc sum x
+    acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(sumi), _mm256_set1_ps(d), acc);
+    acc = _mm256_add_ps(acc, _mm256_set_ps(0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, -32.0f * d * (float)offs));
+  }
+  return hsum(acc);
+}
+
+void orc_q6k_block_acc(const uint8_t *w, size_t n, const int8_t *aq, const int32_t *abs, int32_t *sumi_out,
+                       int32_t *offs_out) {
+  for (size_t b = 0; b < n / 256; ++b) {
+    __m256i sumi;
+    int32_t offs;
+    q6k_block_lanes(w + 210 * b, aq + 256 * b, abs + 16 * b, sumi, offs);
+    alignas(32) int32_t lanes[8];
+    _mm256_store_si256((__m256i *)lanes, sumi);
+    int32_t s = 0;
+    for (int i = 0; i < 8; ++i) s += lanes[i];
+    sumi_out[b] = s;
+    offs_out[b] = offs;
+  }
+}
+
+void orc_q6k_block_acc_bruteforce(const uint8_t *w, size_t n, const int8_t *aq, int64_t *sumi, int64_t *offs) {
+  // sumi = sum_j sc_j * sum_{i in 16-block j} q6_i * x_i (q6 in 0..63, read
+  // bit by bit from ql/qh); offs = sum_j sc_j * sum_{i in j} x_i.
+  for (size_t b = 0; b < n / 256; ++b) {
+    const uint8_t *blk = w + 210 * b;
+    int64_t s = 0, o = 0;
+    for (int j = 0; j < 16; ++j) {
+      const int64_t sc = (int8_t)blk[192 + j];
+      int64_t dot = 0, xs = 0;
+      for (int i = 0; i < 16; ++i) {
+        const int e = 16 * j + i, h = e / 128, ri = (e % 128) / 32, l = e % 32;
+        const uint8_t qlb = blk[h * 64 + 32 * (ri & 1) + l];
+        const int lo4 = ri < 2 ? (qlb & 0xF) : (qlb >> 4);
+        const int hi2 = (blk[128 + h * 32 + l] >> (2 * ri)) & 3;
+        const int q6 = lo4 | (hi2 << 4);
+        dot += (int64_t)q6 * aq[256 * b + e];
+        xs += aq[256 * b + e];
+      }
+      s += sc * dot;
+      o += sc * xs;
+    }
+    sumi[b] = s;
+    offs[b] = o;
+  }
+}
+
 void orc_q8_0_block_acc(const uint8_t *w, size_t n, const int8_t *aq, int32_t *p) {
   for (size_t b = 0; b < n / 32; ++b) {
     __m256i qw = load(w + 34 * b + 2);
@@ -936,16 +1074,17 @@ int orc_matmul(int t, const uint8_t *w, size_t w_len, size_t rows, size_t cols, 
       for (size_t r = r0; r < r1; ++r)
         for (size_t s = 0; s < s_rows; ++s) {
           float v;
-          if (t == ORC_Q4_K)
+          if (t == ORC_Q4_K)  // dot_fused_k, qdot.rs:382-390
             v = orc_dot_q4_k_8k(w + r * row_bytes, cols, q.data() + s * cols, d.data() + s * (cols / 256),
                                 bs.data() + s * (cols / 16));
           else
-            v = 0.0f;  // Q6_K x Q8_K is not restated yet
+            v = orc_dot_q6_k_8k(w + r * row_bytes, cols, q.data() + s * cols, d.data() + s * (cols / 256),
+                                bs.data() + s * (cols / 16));
           res[(r - r0) * s_rows + s] = v;
         }
       scatter_tile(r0, r1 - r0, res);
     });
-    return t == ORC_Q4_K ? 0 : -2;
+    return 0;
   }
   // quant.rs:282-310: 32-block Q8 activations.
   if (!exact && qdot_supports(t) && cols % 32 == 0) {

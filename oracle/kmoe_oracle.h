@@ -17,7 +17,9 @@
  *   - unpack == dequant (qdot.rs:301-315), fused == unpacked (avx2.rs:184-223),
  *     Q8_K kernels vs f64 dequantized math (avx2.rs:425-460),
  *     gemm vs naive (avx2.rs:312-330), matmul vs naive (quant.rs:397-411).
- *   - per-superblock integer accumulators: brute-force int64 loops.
+ *   - per-superblock integer accumulators (Q4_K, Q6_K): brute-force int64 loops.
+ *   - Q6_K: dequant known values (hand-built blocks), dot_q6_k_8k vs f64
+ *     dequantized math (avx2.rs:425-460), integers vs brute force.
  *   - route: brute-force O(E^2) selection + closed-form softmax order.
  *   - dispatch: std::stable_sort by expert id.
  *   - quantizers (ours; the reference only reads blocks): round-trip bounds.
@@ -62,6 +64,7 @@ void orc_fill_xorshift_bytes(uint32_t seed, uint8_t *out, size_t n, uint8_t mask
 /* ---- quantizers (ours: kestrel reads blocks but never writes them) ---- */
 void orc_quantize_q8_0(const float *x, size_t n, uint8_t *out);
 void orc_quantize_q4_k(const float *x, size_t n, uint8_t *out);
+void orc_quantize_q6_k(const float *x, size_t n, uint8_t *out);
 void orc_quantize_rows(int t, const float *x, size_t rows, size_t cols, uint8_t *out, int threads);
 
 /* ---- dequantization, quant.rs:63-205 ---- */
@@ -90,6 +93,13 @@ void orc_q4k_block_acc(const uint8_t *w, size_t n, const int8_t *aq, const int32
 /* The same integers by brute force in int64 (the pin for the above). */
 void orc_q4k_block_acc_bruteforce(const uint8_t *w, size_t n, const int8_t *aq, const int32_t *abs, int64_t *sumi,
                                   int64_t *mins);
+/* Q6_K x Q8_K, avx2.rs:384-419. */
+float orc_dot_q6_k_8k(const uint8_t *w, size_t n, const int8_t *aq, const float *ad, const int32_t *abs);
+/* Its per-superblock integers: sumi[b] = sum of the 8 i32 lanes of `sumi`,
+ * offs[b] = `offs` (sum over 16-blocks of sc * bsum). */
+void orc_q6k_block_acc(const uint8_t *w, size_t n, const int8_t *aq, const int32_t *abs, int32_t *sumi, int32_t *offs);
+/* The same integers by brute force in int64 from the raw activations. */
+void orc_q6k_block_acc_bruteforce(const uint8_t *w, size_t n, const int8_t *aq, int64_t *sumi, int64_t *offs);
 /* Per-block integer dot of dot_q8_0 (avx2.rs:51-56): p[b] = sum of i8*i8 over the block. */
 void orc_q8_0_block_acc(const uint8_t *w, size_t n, const int8_t *aq, int32_t *p);
 

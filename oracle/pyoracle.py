@@ -93,6 +93,10 @@ def lib():
             "orc_q4k_block_acc": (None, [_P, _sz, _P, _P, _P, _P]),
             "orc_q4k_block_acc_bruteforce": (None, [_P, _sz, _P, _P, _P, _P]),
             "orc_q8_0_block_acc": (None, [_P, _sz, _P, _P]),
+            "orc_quantize_q6_k": (None, [_P, _sz, _P]),
+            "orc_dot_q6_k_8k": (C.c_float, [_P, _sz, _P, _P, _P]),
+            "orc_q6k_block_acc": (None, [_P, _sz, _P, _P, _P, _P]),
+            "orc_q6k_block_acc_bruteforce": (None, [_P, _sz, _P, _P, _P]),
             "orc_quant_dot": (C.c_float, [_P, _P, _sz]),
             "orc_dot_f32": (C.c_float, [_P, _P, _sz]),
             "orc_gemm_f32": (None, [_P, _sz, _P, _sz, _sz, _P]),
@@ -214,6 +218,22 @@ def q4k_block_acc_bruteforce(w_row: np.ndarray, n: int, q: np.ndarray, bsums: np
     mins = np.empty(nb, np.int64)
     lib().orc_q4k_block_acc_bruteforce(_p(w_row), n, _p(q), _p(bsums), _p(sumi), _p(mins))
     return sumi, mins
+
+
+def q6k_block_acc(w_row: np.ndarray, n: int, q: np.ndarray, bsums: np.ndarray):
+    nb = n // 256
+    sumi = np.empty(nb, np.int32)
+    offs = np.empty(nb, np.int32)
+    lib().orc_q6k_block_acc(_p(w_row), n, _p(q), _p(bsums), _p(sumi), _p(offs))
+    return sumi, offs
+
+
+def q6k_block_acc_bruteforce(w_row: np.ndarray, n: int, q: np.ndarray):
+    nb = n // 256
+    sumi = np.empty(nb, np.int64)
+    offs = np.empty(nb, np.int64)
+    lib().orc_q6k_block_acc_bruteforce(_p(w_row), n, _p(q), _p(sumi), _p(offs))
+    return sumi, offs
 
 
 def q8_0_block_acc(w_row: np.ndarray, n: int, q: np.ndarray):

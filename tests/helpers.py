@@ -4,8 +4,8 @@ from __future__ import annotations
 
 import numpy as np
 
-F32, Q8_0, Q4_K = 0, 8, 12
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144)}
+F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 
 def row_bytes(t: int, cols: int) -> int:
@@ -21,7 +21,8 @@ def random_blocks(t: int, rows: int, cols: int, seed: int, d: float | None = Non
                   dmin: float | None = None) -> np.ndarray:
     """Well-formed blocks of random bytes with f16 scales overwritten, the way
     the reference's kernel tests build them (avx2.rs:198-208, qdot.rs:275-299).
-    Defaults give weights of std ~0.02 (Q4_K: dmin = 7.5 d centres them)."""
+    Defaults give weights of std ~0.02 (Q4_K: dmin = 7.5 d centres them; Q6_K
+    has its f16 d at byte 208)."""
     rng = np.random.default_rng(seed)
     bs, ts = BLOCK[t]
     nb = rows * cols // bs
@@ -31,6 +32,9 @@ def random_blocks(t: int, rows: int, cols: int, seed: int, d: float | None = Non
         dmin = 7.5 * d if dmin is None else dmin
         raw[:, 0:2] = f16_bytes(d)
         raw[:, 2:4] = f16_bytes(dmin)
+    elif t == Q6_K:  # q - 32 uniform (std ~18.5), sc uniform int8 (rms ~74): d*74*18.5 ~ 0.02
+        d = 1.5e-5 if d is None else d
+        raw[:, 208:210] = f16_bytes(d)
     else:
         d = 0.02 / 74.0 if d is None else d
         raw[:, 0:2] = f16_bytes(d)

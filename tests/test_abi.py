@@ -19,7 +19,7 @@ def test_header_declares_the_path():
     names = declared()
     for must in ["kmoe_matmul", "kmoe_quantize_q8k", "kmoe_quantize_q8", "kmoe_route", "kmoe_dispatch",
                  "kmoe_moe_ffn", "kmoe_layer_create", "kmoe_expert_upload", "kmoe_expert_part",
-                 "kmoe_expert_is_ready", "kmoe_q4k_block_sums", "kmoe_last_error"]:
+                 "kmoe_expert_is_ready", "kmoe_q4k_block_sums", "kmoe_q6k_block_sums", "kmoe_last_error"]:
         assert must in names
 
 

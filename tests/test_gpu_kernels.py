@@ -7,7 +7,7 @@ accumulators, routing indices, dispatch permutation); fp32 results within
 import numpy as np
 import pytest
 
-from tests.helpers import Q4_K, Q8_0, F32, random_blocks, rel_l2, row_bytes
+from tests.helpers import Q4_K, Q6_K, Q8_0, F32, random_blocks, rel_l2, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -104,6 +104,25 @@ def test_q4k_block_sums_extreme_ranges(ctx, orc, S):
             assert np.array_equal(mins[s, r], em), (s, r)
 
 
+@pytest.mark.parametrize("rows,cols,S", [(40, 1024, 1), (33, 2048, 3), (9, 768, 2), (5, 14336, 1)])
+def test_q6k_block_sums_bit_exact(ctx, orc, rows, cols, S):
+    """Q6_K x Q8_K integers (avx2.rs:398-414): sumi = sum sc*q*x and offs =
+    sum sc*bsum per superblock, on raw blocks (every 6-bit value, scales of
+    both signs) and on quantized N(0, 0.02) rows."""
+    x = orc.normal(rows + 7 * cols, S * cols).reshape(S, cols)
+    q, d, bs = orc.q8k_quantize(x)
+    rb = row_bytes(Q6_K, cols)
+    raw = random_blocks(Q6_K, rows, cols, seed=rows * 5 + cols)
+    quant = orc.quantize(Q6_K, orc.normal(rows * 3 + cols, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    for w in (raw, quant):
+        sumi, offs = (host(t) for t in ctx.q6k_block_sums(dev(w), rows, cols, dev(q), dev(bs)))
+        for s in range(S):
+            for r in range(rows):
+                es, eo = orc.q6k_block_acc(w[r * rb:(r + 1) * rb], cols, q[s], bs[s])
+                assert np.array_equal(sumi[s, r], es), (s, r)
+                assert np.array_equal(offs[s, r], eo), (s, r)
+
+
 @pytest.mark.parametrize("rows,cols,S", [(40, 1024, 1), (33, 512, 3)])
 def test_q8_0_block_sums_bit_exact(ctx, orc, rows, cols, S):
     w = random_blocks(Q8_0, rows, cols, seed=rows * 3 + cols)  # raw bytes include -128
@@ -118,6 +137,8 @@ def test_q8_0_block_sums_bit_exact(ctx, orc, rows, cols, S):
 
 @pytest.mark.parametrize("t,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 14336, 4096), (Q4_K, 4096, 14336),
                                          (Q4_K, 1001, 3072), (Q4_K, 77, 8192), (Q4_K, 3, 12288), (Q4_K, 4099, 2048),
+                                         (Q6_K, 4096, 4096), (Q6_K, 14336, 4096), (Q6_K, 4096, 14336),
+                                         (Q6_K, 77, 768), (Q6_K, 1001, 3072),
                                          (Q8_0, 512, 1024), (Q8_0, 1024, 512)])
 def test_matvec_decode_matches_oracle(ctx, orc, t, rows, cols):
     """Dense quantized matvec at decode batch 1 (the C2 shapes for Q4_K)."""
@@ -127,17 +148,17 @@ def test_matvec_decode_matches_oracle(ctx, orc, t, rows, cols):
     ref = orc.matmul(t, w, rows, cols, x)
     assert rel_l2(out, ref) < TOL, rel_l2(out, ref)
     # and on the oracle's own Q8_K/Q8 bytes: same integers -> fp32 within a few ulp
-    qf = orc.q8k_quantize if t == Q4_K else orc.q8_quantize
+    qf = orc.q8k_quantize if t in (Q4_K, Q6_K) else orc.q8_quantize
     q, d, s = qf(x)
     out2 = host(ctx.matvec_q8(t, dev(w), rows, cols, dev(q), dev(d), dev(s)))
     assert rel_l2(out2, ref) < 1e-5
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q8_0])
+@pytest.mark.parametrize("t", [Q4_K, Q8_0, Q6_K])
 @pytest.mark.parametrize("S", [1, 2, 3, 4, 5, 8, 17])
 @pytest.mark.parametrize("regime", [0, 1, 2])
 def test_matmul_regimes_match_oracle(ctx, orc, t, S, regime):
-    rows, cols = (192, 1024) if t == Q4_K else (160, 512)
+    rows, cols = (192, 1024) if t in (Q4_K, Q6_K) else (160, 512)
     w = orc.quantize(t, orc.normal(S * 13 + t, rows * cols, 0.0, 0.02).reshape(rows, cols))
     x = orc.normal(S * 101 + regime, S * cols).reshape(S, cols)
     ctx.set_regime(regime)

@@ -3,7 +3,7 @@ against the oracle, and the HBM expert tier's API behaviour."""
 import numpy as np
 import pytest
 
-from tests.helpers import Q4_K, Q8_0, LayerSpec, random_blocks, rel_l2, row_bytes
+from tests.helpers import Q4_K, Q6_K, Q8_0, LayerSpec, random_blocks, rel_l2, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -84,6 +84,29 @@ def test_q4k_moe_small_all_regimes(ctx, orc, S):
     spec = LayerSpec(8, 2, 1024, 768, Q4_K, seed=S)
     for regime in (0, 1, 2):
         check(run_layer(ctx, orc, spec, S, regime, seed=1000 + S))
+
+
+@pytest.mark.parametrize("S", [1, 3, 8, 32])
+def test_q4k_m_layer_with_q6k_down(ctx, orc, S):
+    """Q4_K_M files keep about half of the ffn_down tensors in Q6_K: Q4_K gate
+    and up (tiled in the tier), Q6_K down (GGUF bytes), every regime."""
+    spec = LayerSpec(8, 2, 1024, 768, Q4_K, seed=50 + S, down_type=Q6_K)
+    for regime in (0, 1, 2):
+        check(run_layer(ctx, orc, spec, S, regime, seed=3000 + S))
+
+
+@pytest.mark.parametrize("S", [1, 5, 16])
+def test_q6k_layer_all_parts(ctx, orc, S):
+    spec = LayerSpec(8, 2, 1024, 512, Q6_K, seed=60 + S)
+    for regime in (0, 1, 2):
+        check(run_layer(ctx, orc, spec, S, regime, seed=3100 + S))
+
+
+def test_mixtral_shape_decode_b1_q6k_down(ctx, orc):
+    """Config 3 geometry at decode batch 1 with the Q6_K down projections of a
+    Q4_K_M file (split-K down over 210-byte superblocks)."""
+    spec = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=5, quantized=False, down_type=Q6_K)
+    check(run_layer(ctx, orc, spec, 1, 0, seed=14))
 
 
 def test_qwen3_like_zipf_routing(ctx, orc):
@@ -245,8 +268,8 @@ def test_errors_map_to_status_codes(ctx):
     with pytest.raises(KmoeError) as e:  # weight buffer smaller than rows x row_bytes (quant.rs:233-234)
         ctx.matmul(Q4_K, w, 4, 256, x)
     assert e.value.status == -1
-    with pytest.raises(KmoeError) as e:  # type without a kernel
-        ctx.matmul(14, w, 4, 256, x)
+    with pytest.raises(KmoeError) as e:  # type without a kernel (Q5_K)
+        ctx.matmul(13, w, 4, 256, x)
     assert e.value.status == -2
     with pytest.raises(KmoeError) as e:  # layer never created
         ctx.moe_ffn(77, x)

@@ -41,6 +41,29 @@ def test_q8_0_and_q4_0_known_values(orc):
     assert y[0] == 14.0 and y[16] == 2.0 and y[1] == -16.0
 
 
+def test_q6_k_known_values(orc):
+    """quant.rs:180-201 on a hand-built block: element e = 128h + 32r + l takes
+    the low (r < 2) or high nibble of ql[64h + 32(r&1) + l], bits 2r..2r+1 of
+    qh[32h + l] as bits 4-5, and the signed scale sc[e/16]; y = d*sc*(q - 32)."""
+    b = np.zeros(210, np.uint8)
+    h = orc.f16_bits(0.5)
+    b[208], b[209] = h & 0xFF, h >> 8
+    b[192:208] = 2
+    b[192 + 5] = np.uint8(253)  # sc[5] = -3
+    b[0] = 0x0F                 # e=0: low nibble 15
+    b[128] = 0x03               # e=0: qh bits 0-1 = 3 -> q = 63
+    b[16] = 0x50                # e=80 (h=0, r=2, l=16): high nibble 5
+    b[128 + 16] = 0x10          # e=80: qh bits 4-5 = 1 -> q = 21
+    b[97] = 0x07                # e=161 (h=1, r=1, l=1): low nibble of ql[64+32+1]
+    b[128 + 33] = 0x08          # e=161: qh bits 2-3 = 2 -> q = 39
+    y = orc.dequant(Q6_K, b, 256)
+    assert y[0] == 0.5 * 2 * 31
+    assert y[80] == 0.5 * -3 * (21 - 32)
+    assert y[161] == 0.5 * 2 * (39 - 32)
+    assert y[64] == 0.5 * 2 * -32 and y[255] == 0.5 * 2 * -32
+    assert y[81] == 0.5 * -3 * -32  # rest of sub-block 5: q = 0
+
+
 def test_known_bpw(orc):
     # kestrel-gguf types.rs:300-307
     for t, bpw in [(Q4_0, 4.5), (Q8_0, 8.5), (Q4_K, 4.5), (Q6_K, 6.5625)]:
@@ -144,17 +167,19 @@ def test_gemm_matches_naive(orc):
         assert np.abs(res.reshape(rows, s_rows) - e).max() < 1e-3
 
 
-def test_q8k_kernels_match_dequantized_math(orc):
-    # avx2.rs:425-460 (Q4_K)
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_q8k_kernels_match_dequantized_math(orc, t):
+    # avx2.rs:425-460 (both Q8_K kernels, same inputs and tolerance)
     n = 2048
     i = np.arange(n)
     x = (((i * 53) % 211).astype(np.float32) - 105.0) / np.float32(40.0)
     q, d, bs = orc.q8k_quantize(x)
-    w = _blocks(orc, Q4_K, n, 7, 0.02)
-    uq, usc, umn = orc.unpack(Q4_K, w, n)
+    w = _blocks(orc, t, n, 7, 0.02)
+    uq, usc, umn = orc.unpack(t, w, n)
     wv = (usc[i // 16] * uq.astype(np.float32) - umn[i // 16]).astype(np.float64)
     r = float(np.sum(wv * q[0].astype(np.float64) * d[0][i // 256].astype(np.float64)))
-    got = orc.lib().orc_dot_q4_k_8k(w.ctypes.data, n, q.ctypes.data, d.ctypes.data, bs.ctypes.data)
+    f = orc.lib().orc_dot_q4_k_8k if t == Q4_K else orc.lib().orc_dot_q6_k_8k
+    got = f(w.ctypes.data, n, q.ctypes.data, d.ctypes.data, bs.ctypes.data)
     assert abs(got - r) <= 1e-3 * max(abs(r), 1.0)
 
 
@@ -169,6 +194,19 @@ def test_q4k_block_accumulators_match_bruteforce(orc, seed):
         s, m = orc.q4k_block_acc(ww, n, q[0], bs[0])
         s2, m2 = orc.q4k_block_acc_bruteforce(ww, n, q[0], bs[0])
         assert np.array_equal(s.astype(np.int64), s2) and np.array_equal(m.astype(np.int64), m2)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_q6k_block_accumulators_match_bruteforce(orc, seed):
+    n = 4096
+    x = orc.normal(seed, n)
+    q, d, bs = orc.q8k_quantize(x)
+    w = orc.quantize(Q6_K, orc.normal(seed + 100, n, 0.0, 0.02).reshape(1, n))
+    wr = orc.xorshift_bytes(seed, w.size)  # raw bytes: every 6-bit value and signed scale
+    for ww in (w, wr):
+        s, o = orc.q6k_block_acc(ww, n, q[0], bs[0])
+        s2, o2 = orc.q6k_block_acc_bruteforce(ww, n, q[0])
+        assert np.array_equal(s.astype(np.int64), s2) and np.array_equal(o.astype(np.int64), o2)
 
 
 def test_q8_0_block_accumulators_match_bruteforce(orc):
@@ -195,7 +233,7 @@ def test_q8k_quantize_semantics(orc):
     assert np.array_equal(bs[0], q[0].reshape(-1, 16).astype(np.int32).sum(1))
 
 
-@pytest.mark.parametrize("t,n", [(Q8_0, 1024), (Q4_K, 4096)])
+@pytest.mark.parametrize("t,n", [(Q8_0, 1024), (Q4_K, 4096), (Q6_K, 4096)])
 def test_quantizers_round_trip(orc, t, n):
     x = orc.normal(12, n, 0.0, 0.02)
     w = orc.quantize(t, x.reshape(1, n))
@@ -203,23 +241,31 @@ def test_quantizers_round_trip(orc, t, n):
     if t == Q8_0:  # |x - y| <= d/2 + |q| * (f16 rounding of d), d = amax/127
         amax = np.abs(x.reshape(-1, 32)).max(1)
         bound = np.repeat(amax / 127.0, 32) * (0.5 + 127 * 2.0 ** -11) + 1e-7
-    else:  # per sub-block range / 15 / 2 plus the 6-bit rounding of scale and min
+    elif t == Q4_K:  # per sub-block range / 15 / 2 plus the 6-bit rounding of scale and min
         r = x.reshape(-1, 32)
         bound = np.repeat((r.max(1) - np.minimum(r.min(1), 0)) / 15.0, 32) * 1.5 + 1e-4
+    else:  # step ~ amax_16/32 per 16-block (+ the 8-bit rounding of the scale); +amax clamps to 31 steps
+        r = x.reshape(-1, 16)
+        step = np.abs(r).max(1) / 32.0
+        d = np.repeat(step.reshape(-1, 16).max(1) / 127.0, 16)
+        bound = np.repeat(step + d, 16) * 1.5 + 1e-7
     assert np.all(np.abs(x - y) <= bound)
-    assert np.sqrt(np.mean((x - y) ** 2)) / np.sqrt(np.mean(x ** 2)) < (0.01 if t == Q8_0 else 0.12)
+    tol = {Q8_0: 0.01, Q4_K: 0.12, Q6_K: 0.05}[t]
+    assert np.sqrt(np.mean((x - y) ** 2)) / np.sqrt(np.mean(x ** 2)) < tol
 
 
-def test_matmul_regimes(orc):
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_matmul_regimes(orc, t):
     """quant.rs:242/262/282: S>=4 is f32-exact; S<4 carries Q8_K activation error."""
     rows, cols = 64, 1024
-    w = orc.quantize(Q4_K, orc.normal(21, rows * cols, 0.0, 0.02).reshape(rows, cols))
-    wf = np.stack([orc.dequant(Q4_K, w[r * 576:(r + 1) * 576], cols) for r in range(rows)]).astype(np.float64)
+    rb = orc.bytes_for(t, cols)
+    w = orc.quantize(t, orc.normal(21, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    wf = np.stack([orc.dequant(t, w[r * rb:(r + 1) * rb], cols) for r in range(rows)]).astype(np.float64)
     for S in (1, 3, 4, 7):
         x = orc.normal(30 + S, S * cols).reshape(S, cols)
         e = x.astype(np.float64) @ wf.T
         for regime in (REGIME_AVX2, REGIME_INT8, REGIME_EXACT):
-            out = orc.matmul(Q4_K, w, rows, cols, x, regime)
+            out = orc.matmul(t, w, rows, cols, x, regime)
             rel = np.linalg.norm(out - e) / np.linalg.norm(e)
             exact = (regime == REGIME_EXACT) or (regime == REGIME_AVX2 and S >= 4)
             assert rel < (1e-6 if exact else 2e-2), (S, regime, rel)
@@ -273,7 +319,7 @@ def _small_layer(orc, t, E=4, k=2, d=256, ff=256, seed=0):
     return orc.Layer(E, k, d, ff, t, t, t, router, gate, up, down)
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_K])
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
 def test_moe_ffn_matches_float64_layer(orc, t):
     """transformer.rs:513-570 against a float64 evaluation of the same layer."""
     L = _small_layer(orc, t)
