@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 D, FF, E, K = 4096, 14336, 8, 2
-Q4_K = 12
+Q4_K, Q6_K = 12, 14
 ROW_GU = 4096 // 256 * 144   # 2304 B per gate/up row
 ROW_DN = 14336 // 256 * 144  # 8064 B per down row
 PART = FF * ROW_GU           # 33,030,144 B (gate, up and down parts are equal)
@@ -53,7 +53,8 @@ def parse():
                     help="tokens of the prefill leg (int8 matrix-core path); 0 skips it")
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the other measured rows (decode b=8/32, dense matvec, Qwen3-shaped layer)")
+                    help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
+                         "decode, Qwen3-shaped layer)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -305,29 +306,35 @@ def batch_leg(ctx, torch, layers: int, S: int, regime: int):
             "hbm_touched_GBps": round(tb / t / 1e9, 1), "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def matvec_leg(ctx, torch, pool_bytes: float = 2.2e9):
-    """Dense Q4_K matvec at decode batch 1 (quant::matmul, one activation row)
-    over a pool of distinct weight copies larger than the Infinity Cache."""
+def matvec_leg(ctx, torch, wtype: int = Q4_K, pool_bytes: float = 2.2e9):
+    """Dense Q4_K or Q6_K matvec at decode batch 1 (quant::matmul, one
+    activation row) over a pool of distinct weight copies larger than the
+    Infinity Cache."""
     import numpy as np
 
     from kestrel_amd import kmoe
 
     ctx.set_regime(0)
-    dh = np.array([1.4e-4], np.float16).view(np.uint8)
-    mh = np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)
-    hdr = torch.tensor(np.concatenate([dh, mh]), dtype=torch.uint8, device="cuda")
+    if wtype == Q4_K:  # f16 d, dmin at bytes 0-3: weights of std ~0.02
+        blk, off = 144, 0
+        hdr = np.concatenate([np.array([1.4e-4], np.float16).view(np.uint8),
+                              np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)])
+    else:  # Q6_K: f16 d at bytes 208-209
+        blk, off = 210, 208
+        hdr = np.array([1.5e-5], np.float16).view(np.uint8)
+    hdr = torch.tensor(hdr, dtype=torch.uint8, device="cuda")
     out = {}
     for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
-        nbytes = rows * (cols // 256) * 144
+        nbytes = rows * (cols // 256) * blk
         copies = int(-(-pool_bytes // nbytes))
-        pool = torch.randint(0, 256, (copies, nbytes // 144, 144), dtype=torch.uint8, device="cuda")
-        pool[:, :, 0:4] = hdr
+        pool = torch.randint(0, 256, (copies, nbytes // blk, blk), dtype=torch.uint8, device="cuda")
+        pool[:, :, off:off + hdr.numel()] = hdr
         x = torch.randn((1, cols), dtype=torch.float32, device="cuda")
         y = torch.empty((1, rows), dtype=torch.float32, device="cuda")
         lib = ctx.lib
 
         def call(i):
-            ctx.check(lib.kmoe_matmul(ctx.h, Q4_K, kmoe._ptr(pool[i]), nbytes, rows, cols, kmoe._ptr(x), 1,
+            ctx.check(lib.kmoe_matmul(ctx.h, wtype, kmoe._ptr(pool[i]), nbytes, rows, cols, kmoe._ptr(x), 1,
                                       kmoe._ptr(y)))
 
         t = graph_time(torch, ctx, [lambda i=i: call(i) for i in range(copies)], 5) / copies
@@ -337,6 +344,50 @@ def matvec_leg(ctx, torch, pool_bytes: float = 2.2e9):
         del pool
     torch.cuda.empty_cache()
     return out
+
+
+def q4km_leg(ctx, torch, layers: int = 4, seed: int = 2):
+    """Mixtral-shaped decode at batch 1 with the tensor mix of a Q4_K_M file:
+    Q4_K gate/up, Q6_K down (48,168,960 B per expert), random well-formed
+    blocks, router N(0, 0.02); layers rotated past the Infinity Cache."""
+    import numpy as np
+
+    h4 = torch.tensor(np.concatenate([np.array([1.4e-4], np.float16).view(np.uint8),
+                                      np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)]),
+                      dtype=torch.uint8, device="cuda")
+    h6 = torch.tensor(np.array([1.5e-5], np.float16).view(np.uint8), dtype=torch.uint8, device="cuda")
+    down6 = D * (FF // 256) * 210
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    base = 200
+    for l in range(layers):
+        ctx.layer_create(base + l, E, K, D, FF, Q4_K, Q4_K, Q6_K, True, 0.0)
+        ctx.router_upload(base + l, (rng.standard_normal((E, D)) * 0.02).astype(np.float32))
+        for e in range(E):
+            for p in range(2):
+                t = torch.randint(0, 256, (PART // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
+                t[:, 0:4] = h4
+                ctx.expert_upload(base + l, e, p, t)
+            t = torch.randint(0, 256, (down6 // 210, 210), dtype=torch.uint8, device="cuda", generator=g)
+            t[:, 208:210] = h6
+            ctx.expert_upload(base + l, e, 2, t)
+            del t
+    torch.cuda.synchronize()
+    ctx.set_stream(torch.cuda.current_stream())
+    hp = torch.randn((layers, 1, D), dtype=torch.float32, device="cuda")
+    op = torch.empty_like(hp)
+    for l in range(layers):
+        ctx.moe_ffn(base + l, hp[l], op[l])
+    t = graph_time(torch, ctx, [lambda l=l: ctx.moe_ffn(base + l, hp[l], op[l]) for l in range(layers)], 100)
+    t /= layers
+    tb = K * (2 * PART + down6) + E * D * 4
+    for l in range(layers):
+        ctx.layer_destroy(base + l)
+    torch.cuda.empty_cache()
+    return {"tokens": 1, "weights": "Q4_K gate/up, Q6_K down", "tokens_per_s": round(1 / t, 1),
+            "us_per_step": round(t * 1e6, 2), "bytes_per_token": tb, "hbm_GBps": round(tb / t / 1e9, 1),
+            "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
@@ -603,7 +654,9 @@ def main():
         res["prefill"] = prefill_leg(ctx, torch, a)
     if not a.no_extra:
         res["decode_batches"] = [batch_leg(ctx, torch, a.layers, S2, rg) for S2 in (8, 32) for rg in (0, 1)]
-        res["matvec_q4k"] = matvec_leg(ctx, torch)
+        res["matvec_q4k"] = matvec_leg(ctx, torch, Q4_K)
+        res["matvec_q6k"] = matvec_leg(ctx, torch, Q6_K)
+        res["decode_b1_q4k_m"] = q4km_leg(ctx, torch)
         res["qwen3"] = qwen3_leg(ctx, torch)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)

@@ -59,8 +59,9 @@ struct Layer {
   size_t part_len[3] = {0, 0, 0};
   size_t part_off[3] = {0, 0, 0};
   size_t expert_stride = 0;
-  bool tiled[3] = {false, false, false};  // Q4_K parts are stored as tiled rows
+  bool tiled[3] = {false, false, false};  // Q4_K and Q6_K parts are stored as tiled rows
   int64_t part_rows[3] = {0, 0, 0}, part_nb[3] = {0, 0, 0};
+  int32_t part_type[3] = {0, 0, 0};
   size_t reserved = 0;
   bool router_ok = false;
   std::vector<uint8_t> loaded;  // bit p set when part p of expert e is resident
@@ -689,7 +690,8 @@ int kmoe_layer_create(kmoe_ctx *c, uint32_t layer, const kmoe_moe_desc *desc) {
   L.expert_stride = L.part_off[2] + align_up(L.part_len[2]);
   const int32_t ptype[3] = {D.gate_type, D.up_type, D.down_type};
   for (int p = 0; p < 3; ++p) {
-    L.tiled[p] = ptype[p] == KMOE_Q4_K;
+    L.part_type[p] = ptype[p];
+    L.tiled[p] = ptype[p] == KMOE_Q4_K || ptype[p] == KMOE_Q6_K;
     L.part_rows[p] = p < 2 ? D.n_ff : D.n_embd;
     L.part_nb[p] = (p < 2 ? D.n_embd : D.n_ff) / 256;
   }
@@ -762,10 +764,17 @@ static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, 
     HIP_OK(c, hipMemcpyAsync(dst, bytes, len, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                              c->stream));
   } else if (from_device) {
-    HIP_OK(c, launch_tq4_convert(c->stream, (const uint8_t *)bytes, dst, L->part_rows[part], L->part_nb[part], true));
+    const uint8_t *src = (const uint8_t *)bytes;
+    if (L->part_type[part] == KMOE_Q6_K)
+      HIP_OK(c, launch_tq6_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
+    else
+      HIP_OK(c, launch_tq4_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
   } else {
     std::vector<uint8_t> t(len);
-    tq4_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
+    if (L->part_type[part] == KMOE_Q6_K)
+      tq6_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
+    else
+      tq4_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
     HIP_OK(c, hipMemcpyAsync(dst, t.data(), len, hipMemcpyHostToDevice, c->stream));
     HIP_OK(c, hipStreamSynchronize(c->stream));  // t is released on return
   }
@@ -887,7 +896,10 @@ int kmoe_expert_read(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, void
   std::vector<uint8_t> t(n);
   HIP_OK(c, hipMemcpyAsync(t.data(), src, n, hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  tq4_convert_host(t.data(), (uint8_t *)host, L->part_rows[part], L->part_nb[part], false);
+  if (L->part_type[part] == KMOE_Q6_K)
+    tq6_convert_host(t.data(), (uint8_t *)host, L->part_rows[part], L->part_nb[part], false);
+  else
+    tq4_convert_host(t.data(), (uint8_t *)host, L->part_rows[part], L->part_nb[part], false);
   return KMOE_OK;
 }
 

@@ -131,6 +131,72 @@ __host__ __device__ __forceinline__ int64_t tq4_j_stride(int64_t nb, int64_t sb)
   return 64 * (rem < 8 ? rem : 8);
 }
 
+// Tiled Q6_K rows of the expert tier: the 210 bytes of each superblock
+// regrouped per task (quarter k = 2h + p: rows 2p and 2p+1 of half h, 64
+// weights; see quant.rs:180-201 for the GGUF order). Task (sb, k) owns three
+// 16-byte pieces:
+//   j = 0, 1  nibbles: byte b of the 32 holds weight b of the task's first
+//             row in its low nibble and of its second row in its high nibble;
+//   j = 2     high bits: byte b holds weight b (low nibble) and weight b+16
+//             (high nibble), each nibble the first row's 2 bits then the
+//             second row's.
+// Pieces come in groups of 8 superblocks (1536 bytes); within a group all
+// j = 0 pieces in task order, then j = 1, then j = 2. After the groups: the 16
+// scale bytes of each superblock at 192*nb + 16*sb (the task's four at +4k),
+// then the f16 d of each superblock at 208*nb + 2*sb.
+__host__ __device__ __forceinline__ int64_t tq6_piece_off(int64_t nb, int64_t sb, int k, int j) {
+  const int64_t g = sb >> 3;
+  const int64_t rem = nb - 8 * g;
+  const int64_t ns = rem < 8 ? rem : 8;
+  return 1536 * g + 16 * (j * 4 * ns + 4 * (sb & 7) + k);
+}
+// Byte distance from piece (sb, k, j) to piece (sb, k, j + 1).
+__host__ __device__ __forceinline__ int64_t tq6_j_stride(int64_t nb, int64_t sb) {
+  const int64_t rem = nb - 8 * (sb >> 3);
+  return 64 * (rem < 8 ? rem : 8);
+}
+// GGUF Q6_K superblock blk -> its bytes in the tiled row `row` (nb superblocks).
+__host__ __device__ inline void tq6_pack_sb(const uint8_t *blk, uint8_t *row, int64_t nb, int64_t sb) {
+  const int64_t js = tq6_j_stride(nb, sb);
+  for (int k = 0; k < 4; ++k) {
+    const int h = k >> 1, p = k & 1;
+    uint8_t *n = row + tq6_piece_off(nb, sb, k, 0);
+    for (int b = 0; b < 32; ++b) {
+      const uint8_t lo = blk[64 * h + b], hi = blk[64 * h + 32 + b];
+      const uint8_t a = p ? (uint8_t)(lo >> 4) : (uint8_t)(lo & 0xF);
+      const uint8_t c = p ? (uint8_t)(hi >> 4) : (uint8_t)(hi & 0xF);
+      n[(b >> 4) * js + (b & 15)] = (uint8_t)(a | (c << 4));
+    }
+    uint8_t *hb = n + 2 * js;
+    for (int b = 0; b < 16; ++b)
+      hb[b] = (uint8_t)(((blk[128 + 32 * h + b] >> (4 * p)) & 0xF) |
+                        (((blk[128 + 32 * h + 16 + b] >> (4 * p)) & 0xF) << 4));
+  }
+  for (int i = 0; i < 16; ++i) row[192 * nb + 16 * sb + i] = blk[192 + i];
+  row[208 * nb + 2 * sb] = blk[208];
+  row[208 * nb + 2 * sb + 1] = blk[209];
+}
+// The inverse: tiled row bytes of superblock sb -> its GGUF block.
+__host__ __device__ inline void tq6_unpack_sb(const uint8_t *row, uint8_t *blk, int64_t nb, int64_t sb) {
+  const int64_t js = tq6_j_stride(nb, sb);
+  for (int h = 0; h < 2; ++h) {
+    const uint8_t *n0 = row + tq6_piece_off(nb, sb, 2 * h, 0), *n1 = row + tq6_piece_off(nb, sb, 2 * h + 1, 0);
+    for (int b = 0; b < 32; ++b) {
+      const uint8_t a = n0[(b >> 4) * js + (b & 15)], c = n1[(b >> 4) * js + (b & 15)];
+      blk[64 * h + b] = (uint8_t)((a & 0xF) | ((c & 0xF) << 4));
+      blk[64 * h + 32 + b] = (uint8_t)((a >> 4) | (c & 0xF0));
+    }
+    const uint8_t *h0 = n0 + 2 * js, *h1 = n1 + 2 * js;
+    for (int b = 0; b < 16; ++b) {
+      blk[128 + 32 * h + b] = (uint8_t)((h0[b] & 0xF) | ((h1[b] & 0xF) << 4));
+      blk[128 + 32 * h + 16 + b] = (uint8_t)((h0[b] >> 4) | (h1[b] & 0xF0));
+    }
+  }
+  for (int i = 0; i < 16; ++i) blk[192 + i] = row[192 * nb + 16 * sb + i];
+  blk[208] = row[208 * nb + 2 * sb];
+  blk[209] = row[208 * nb + 2 * sb + 1];
+}
+
 // Correctly rounded expf via double exp. glibc's expf (what the reference's
 // f32::exp calls) is within 0.502 ulp, so the two agree except on inputs
 // whose exact value lies within ~0.002 ulp of a rounding midpoint.

@@ -38,7 +38,7 @@ __device__ __forceinline__ bool f32_regime(int regime, int n) {
 }
 
 // 16 consecutive dequantized weights of chunk kc, part p (0..3), of one row
-// (Q4_K: GGUF bytes, or tiled rows of nb superblocks when TILED).
+// (Q4_K and Q6_K: GGUF bytes, or tiled rows of nb superblocks when TILED).
 template <int TYPE, bool TILED>
 __device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p, int64_t nb, float *o) {
   if constexpr (TYPE == T_Q4_K) {
@@ -66,18 +66,36 @@ __device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p,
     // chunk kc = quarter k of superblock kc/4 (half h, nibble np); part p is
     // weights 16*(p&1).. of row ri = 2*np + (p>>1) of the half
     typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
-    const uint8_t *blk = row + (kc >> 2) * 210;
+    const int64_t sb = kc >> 2;
     const int k = (int)(kc & 3), h = k >> 1, np = k & 1, ri = 2 * np + (p >> 1), l0 = 16 * (p & 1);
-    const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-    const float ds = d * (float)(int8_t)blk[192 + 8 * h + 2 * ri + (p & 1)];
-    const u32x4u2 ql = *(const u32x4u2 *)(blk + 64 * h + 32 * (ri & 1) + l0);
-    const u32x4u2 qh = *(const u32x4u2 *)(blk + 128 + 32 * h + l0);
-    const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+    if constexpr (TILED) {  // tq6_piece_off: nibble piece p&1 (nibble p>>1), high-bit piece (nibble p&1)
+      const uint8_t *p0 = row + tq6_piece_off(nb, sb, k, 0);
+      const int64_t js = tq6_j_stride(nb, sb);
+      const float d = f16_bits_to_f32((uint32_t)row[208 * nb + 2 * sb] | ((uint32_t)row[208 * nb + 2 * sb + 1] << 8));
+      const float ds = d * (float)(int8_t)row[192 * nb + 16 * sb + 4 * k + p];
+      const u32x4u2 nv = *(const u32x4u2 *)(p0 + (p & 1) * js);
+      const u32x4u2 hv = *(const u32x4u2 *)(p0 + 2 * js);
+      const uint32_t nw[4] = {nv.x, nv.y, nv.z, nv.w}, hw[4] = {hv.x, hv.y, hv.z, hv.w};
+      const int nsh = 4 * (p >> 1), hsh = 4 * (p & 1) + 2 * (p >> 1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-      const int q = (int)((np ? (lb >> 4) : (lb & 0xfu)) | (((hb >> (2 * ri)) & 3u) << 4)) - 32;
-      o[i] = ds * (float)q;
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t nb8 = (nw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb8 = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        const int q = (int)(((nb8 >> nsh) & 0xfu) | (((hb8 >> hsh) & 3u) << 4)) - 32;
+        o[i] = ds * (float)q;
+      }
+    } else {
+      const uint8_t *blk = row + sb * 210;
+      const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+      const float ds = d * (float)(int8_t)blk[192 + 8 * h + 2 * ri + (p & 1)];
+      const u32x4u2 ql = *(const u32x4u2 *)(blk + 64 * h + 32 * (ri & 1) + l0);
+      const u32x4u2 qh = *(const u32x4u2 *)(blk + 128 + 32 * h + l0);
+      const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        const int q = (int)((np ? (lb >> 4) : (lb & 0xfu)) | (((hb >> (2 * ri)) & 3u) << 4)) - 32;
+        o[i] = ds * (float)q;
+      }
     }
   } else if constexpr (TYPE == T_Q8_0) {
     const int64_t b = 2 * kc + (p >> 1);

@@ -61,6 +61,10 @@ struct ExpertTier {
 hipError_t launch_tq4_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
                               bool to_tiled);
 void tq4_convert_host(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb, bool to_tiled);
+// The same for Q6_K rows (210 bytes per superblock in both layouts).
+hipError_t launch_tq6_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
+                              bool to_tiled);
+void tq6_convert_host(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb, bool to_tiled);
 
 // ---- int8 matvecs (kmoe_matvec.hip)
 // Plain: out[s*rows + r] for s < s_rows; activations pre-quantized.

@@ -1,5 +1,5 @@
-// kmoe_layout.hip — conversion between GGUF Q4_K rows and the expert tier's
-// tiled Q4_K rows (layout defined at tq4_qs_off in kmoe_device.h).
+// kmoe_layout.hip — conversion between GGUF rows and the expert tier's tiled
+// rows: Q4_K (tq4_qs_off in kmoe_device.h) and Q6_K (tq6_piece_off).
 //
 // A row of nb superblocks is 9*nb 16-byte chunks in both layouts: chunk c < nb
 // is the head of superblock c, chunk nb + 8*sb + p is nibble piece p (bytes
@@ -47,7 +47,38 @@ __global__ void __launch_bounds__(256) k_tq4_convert(const uint8_t *__restrict__
   }
 }
 
+// One thread per Q6_K superblock: a byte-level regrouping (tq6_pack_sb /
+// tq6_unpack_sb), not a chunk permutation.
+__global__ void __launch_bounds__(256) k_tq6_convert(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                     int64_t rows, int64_t nb, int to_tiled) {
+  const int64_t n = rows * nb;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / nb, sb = i - r * nb;
+    const int64_t base = r * 210 * nb;
+    if (to_tiled) tq6_pack_sb(src + base + 210 * sb, dst + base, nb, sb);
+    else tq6_unpack_sb(src + base, dst + base + 210 * sb, nb, sb);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_tq6_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
+                              bool to_tiled) {
+  if (rows <= 0 || nb <= 0) return hipSuccess;
+  int64_t grid = (rows * nb + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  KMOE_LAUNCH(k_tq6_convert, dim3((unsigned)grid), dim3(256), 0, st, src, dst, rows, nb, to_tiled ? 1 : 0);
+  return hipGetLastError();
+}
+
+void tq6_convert_host(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb, bool to_tiled) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t sb = 0; sb < nb; ++sb) {
+      const int64_t base = r * 210 * nb;
+      if (to_tiled) tq6_pack_sb(src + base + 210 * sb, dst + base, nb, sb);
+      else tq6_unpack_sb(src + base, dst + base + 210 * sb, nb, sb);
+    }
+}
 
 hipError_t launch_tq4_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
                               bool to_tiled) {

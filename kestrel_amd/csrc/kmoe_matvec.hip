@@ -29,6 +29,7 @@
 #include "kmoe_launch.h"
 
 #include <cstdlib>
+#include <type_traits>
 #include <cstring>
 
 namespace kmoe {
@@ -210,6 +211,51 @@ __device__ __forceinline__ void q6k_ints(const Q6kW &w, int k, const int4 &x0, c
   offs = s0 * bs.x + s1 * bs.y + s2 * bs.z + s3 * bs.w;
 }
 
+// Task t of a tiled Q6_K row of the expert tier (tq6_piece_off): nibbles
+// n0/n1 (byte b: weight b of the first row low, of the second row high), high
+// bits hb (byte b: weights b and b+16), the task's four scales and d.
+struct Q6kT {
+  uint4 n0, n1, hb;
+  uint32_t sc;
+  uint32_t d;
+};
+__device__ __forceinline__ Q6kT q6t_load(const uint8_t *row, int t, int64_t nb) {
+  const int64_t sb = t >> 2;
+  const int k = t & 3;
+  const uint8_t *p0 = row + tq6_piece_off(nb, sb, k, 0);
+  const int64_t js = tq6_j_stride(nb, sb);
+  Q6kT w;
+  w.n0 = ld_nt_u2(p0);
+  w.n1 = ld_nt_u2(p0 + js);
+  w.hb = ld_nt_u2(p0 + 2 * js);
+  w.sc = __builtin_nontemporal_load((const u32u2 *)(row + 192 * nb + 16 * sb + 4 * k));
+  w.d = __builtin_nontemporal_load((const uint16_t *)(row + 208 * nb + 2 * sb));
+  return w;
+}
+__device__ __forceinline__ void q6t_ints(const Q6kT &w, const int4 &x0, const int4 &x1, const int4 &x2, const int4 &x3,
+                                         const int4 &bs, int &sumi, int &offs) {
+  const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x03030303u;
+  const uint32_t N[8] = {w.n0.x, w.n0.y, w.n0.z, w.n0.w, w.n1.x, w.n1.y, w.n1.z, w.n1.w};
+  const uint32_t H[4] = {w.hb.x, w.hb.y, w.hb.z, w.hb.w};
+  const uint32_t X[16] = {(uint32_t)x0.x, (uint32_t)x0.y, (uint32_t)x0.z, (uint32_t)x0.w,
+                          (uint32_t)x1.x, (uint32_t)x1.y, (uint32_t)x1.z, (uint32_t)x1.w,
+                          (uint32_t)x2.x, (uint32_t)x2.y, (uint32_t)x2.z, (uint32_t)x2.w,
+                          (uint32_t)x3.x, (uint32_t)x3.y, (uint32_t)x3.z, (uint32_t)x3.w};
+  int g[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t hs = i < 4 ? H[i] : (H[i - 4] >> 4);  // weights 4i..4i+3: low nibbles, then high
+    const uint32_t qa = (N[i] & m4) | ((hs & m2) << 4);
+    const uint32_t qb = ((N[i] >> 4) & m4) | (((hs >> 2) & m2) << 4);
+    g[i >> 2] = sdot4(qa, X[i], g[i >> 2]);
+    g[2 + (i >> 2)] = sdot4(qb, X[8 + i], g[2 + (i >> 2)]);
+  }
+  const int s0 = (int)(int8_t)(w.sc & 0xff), s1 = (int)(int8_t)((w.sc >> 8) & 0xff);
+  const int s2 = (int)(int8_t)((w.sc >> 16) & 0xff), s3 = (int)(int8_t)(w.sc >> 24);
+  sumi = s0 * g[0] + s1 * g[1] + s2 * g[2] + s3 * g[3];
+  offs = s0 * bs.x + s1 * bs.y + s2 * bs.z + s3 * bs.w;
+}
+
 struct Q80W {
   uint4 a, b;
   uint32_t c;
@@ -356,9 +402,20 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
             }
           } else if constexpr (TYPE == T_Q6_K) {
             const int sb = t >> 2, k = t & 3;
-            const Q6kW w0 = q6k_load(row0, t);
-            Q6kW w1;
-            if constexpr (MODE == M_GATE_UP) w1 = q6k_load(row1, t);
+            constexpr bool TL = MODE == M_GATE_UP || MODE == M_DOWN;  // expert tier rows are tiled
+            using W6 = typename std::conditional<TL, Q6kT, Q6kW>::type;
+            auto ld6 = [&](const uint8_t *row) {
+              if constexpr (TL) return q6t_load(row, t, nblk);
+              else return q6k_load(row, t);
+            };
+            auto ints6 = [&](const W6 &w, const int4 &a0, const int4 &a1, const int4 &a2, const int4 &a3,
+                             const int4 &b, int &si_, int &oi_) {
+              if constexpr (TL) q6t_ints(w, a0, a1, a2, a3, b, si_, oi_);
+              else q6k_ints(w, k, a0, a1, a2, a3, b, si_, oi_);
+            };
+            const W6 w0 = ld6(row0);
+            W6 w1;
+            if constexpr (MODE == M_GATE_UP) w1 = ld6(row1);
             const float d0 = f16_bits_to_f32(w0.d);
 #pragma unroll
             for (int tk = 0; tk < NT; ++tk) {
@@ -369,7 +426,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                 const int4 bs = *((const int4 *)(act + L.q) + sb * 4 + k);
                 const float xd = ((const float *)(act + L.q + L.s))[sb];
                 int si, oi;
-                q6k_ints(w0, k, x0, x1, x2, x3, bs, si, oi);
+                ints6(w0, x0, x1, x2, x3, bs, si, oi);
                 if constexpr (MODE == M_SUMS) {
                   const int ss = group_sum_i<4>(si), os = group_sum_i<4>(oi);
                   if (k == 0) {
@@ -380,7 +437,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                 } else {
                   acc0[tk] = fmaf(d0 * xd, (float)(si - 32 * oi), acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
-                    q6k_ints(w1, k, x0, x1, x2, x3, bs, si, oi);
+                    ints6(w1, x0, x1, x2, x3, bs, si, oi);
                     acc1[tk] = fmaf(f16_bits_to_f32(w1.d) * xd, (float)(si - 32 * oi), acc1[tk]);
                   }
                 }
@@ -494,32 +551,38 @@ __device__ __forceinline__ void act_load(ActSlice<TYPE> &s, const int8_t *xq, co
   }
 }
 
-template <int TYPE>
+// One task's weight registers; TILED: a row of the expert tier (Q4_K and
+// Q6_K tiled, Q8_0 GGUF bytes either way).
+template <int TYPE, bool TILED>
 struct WTask;
-template <>
-struct WTask<T_Q4_K> {
+template <bool TL>
+struct WTask<T_Q4_K, TL> {
   Q4kW w;
 };
-template <>
-struct WTask<T_Q8_0> {
+template <bool TL>
+struct WTask<T_Q8_0, TL> {
   Q80W w;
 };
 template <>
-struct WTask<T_Q6_K> {
+struct WTask<T_Q6_K, false> {
   Q6kW w;
 };
+template <>
+struct WTask<T_Q6_K, true> {
+  Q6kT w;
+};
 
-// Q6_K rows are never tiled: TILED applies to Q4_K only.
 template <int TYPE, bool TILED>
-__device__ __forceinline__ void w_load(WTask<TYPE> &w, const uint8_t *row, int t, int64_t nblk) {
+__device__ __forceinline__ void w_load(WTask<TYPE, TILED> &w, const uint8_t *row, int t, int64_t nblk) {
   if constexpr (TYPE == T_Q4_K) w.w = q4k_load<TILED>(row, t, nblk);
+  else if constexpr (TYPE == T_Q6_K && TILED) w.w = q6t_load(row, t, nblk);
   else if constexpr (TYPE == T_Q6_K) w.w = q6k_load(row, t);
   else w.w = q80_load(row, t);
 }
 
 // acc += (float) dot of one task against its activation slice.
-template <int TYPE>
-__device__ __forceinline__ float task_dot(const WTask<TYPE> &wt, int t, const ActSlice<TYPE> &s, float acc) {
+template <int TYPE, bool TILED>
+__device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, const ActSlice<TYPE> &s, float acc) {
   if constexpr (TYPE == T_Q4_K) {
     const Q4kW &w = wt.w;
     const int k = t & 3;
@@ -551,7 +614,8 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE> &wt, int t, const Ac
     return acc;
   } else if constexpr (TYPE == T_Q6_K) {
     int sumi, offs;
-    q6k_ints(wt.w, t & 3, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
+    if constexpr (TILED) q6t_ints(wt.w, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
+    else q6k_ints(wt.w, t & 3, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
     return fmaf(f16_bits_to_f32(wt.w.d) * s.d, (float)(sumi - 32 * offs), acc);
   } else {
     const Q80W &w = wt.w;
@@ -642,7 +706,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
         for (int i = 0; i < TPLMAX; ++i) {
           const int t = lr + i * LPR;
           if (i < tpl && t < ntasks) {
-            WTask<TYPE> w[RU];
+            WTask<TYPE, true> w[RU];
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
               const int64_t r = r0 + (int64_t)u * RPW;
@@ -677,7 +741,8 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
       for (int i = 0; i < TPLMAX; ++i) {
         const int t = lr + i * LPR;
         if (i < tpl && t < ntasks) {
-          WTask<TYPE> w0[RU], w1[RU];
+          constexpr bool TLW = MODE == M_GATE_UP;  // expert tier rows are tiled, plain rows are GGUF
+          WTask<TYPE, TLW> w0[RU], w1[RU];
 #pragma unroll
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
@@ -768,11 +833,11 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
     im.rr = (it - ia * nb) * RU;
     return im;
   };
-  WTask<TYPE> cur[RU][TPL], nxt[RU][TPL];
+  WTask<TYPE, true> cur[RU][TPL], nxt[RU][TPL];
   ActSlice<TYPE> act[TPL], act_n[TPL];
   // Unconditional loads with clamped indices: a divergent branch around the
   // loads would make the compiler wait for all of them at the join.
-  auto load_w = [&](const Item &im, WTask<TYPE> (&w)[RU][TPL]) {
+  auto load_w = [&](const Item &im, WTask<TYPE, true> (&w)[RU][TPL]) {
 #pragma unroll
     for (int u = 0; u < RU; ++u)
 #pragma unroll
@@ -785,7 +850,7 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
       act_load<TYPE>(s[i], a.xq + im.p * cols, a.xd + im.p * nblk, a.xbs + im.p * xs_stride, min(tk[i], ntasks - 1));
   };
   // One (expert, row-batch) item; finishes the expert after its last batch.
-  auto compute = [&](int it, const Item &ic, WTask<TYPE> (&w)[RU][TPL], ActSlice<TYPE> (&ac)[TPL]) {
+  auto compute = [&](int it, const Item &ic, WTask<TYPE, true> (&w)[RU][TPL], ActSlice<TYPE> (&ac)[TPL]) {
     const bool last = (it + 1) % nb == 0;  // this expert's last row batch
     float wgt = 0.0f;
     if (last) wgt = a.rt.wsel[a.rt.perm[ic.p]];  // issued early, used after the dots

@@ -258,6 +258,57 @@ def test_q4k_tier_layout_round_trip(ctx, d, ff):
         ctx.layer_destroy(95)
 
 
+def _tiled_q6k_reference(g: np.ndarray, rows: int, nb: int) -> np.ndarray:
+    """Tiled Q6_K rows from the layout's definition: task k = 2h + p of a
+    superblock takes nibble p of ql[64h + b] (low) and ql[64h + 32 + b] (high)
+    for b < 32, and bits 4p..4p+3 of qh[32h + b] (low) and qh[32h + 16 + b]
+    (high) for b < 16; per group of 8 superblocks the 16-byte pieces
+    (j, superblock, k); then the scale bytes, then d."""
+    out = np.empty_like(g)
+    for r in range(rows):
+        blk = g[r * 210 * nb:(r + 1) * 210 * nb].reshape(nb, 210)
+        ql = blk[:, :128].reshape(nb, 2, 64)
+        qh = blk[:, 128:192].reshape(nb, 2, 32)
+        P = np.empty((nb, 4, 3, 16), np.uint8)
+        for k in range(4):
+            h, p = k >> 1, k & 1
+            nib = lambda v: (v >> 4) if p else (v & 0xF)
+            n = nib(ql[:, h, :32]) | (nib(ql[:, h, 32:]) << 4)
+            P[:, k, 0], P[:, k, 1] = n[:, :16], n[:, 16:]
+            P[:, k, 2] = ((qh[:, h, :16] >> (4 * p)) & 0xF) | (((qh[:, h, 16:] >> (4 * p)) & 0xF) << 4)
+        parts = [P[g0:min(nb, g0 + 8)].transpose(2, 0, 1, 3).reshape(-1) for g0 in range(0, nb, 8)]
+        parts += [blk[:, 192:208].reshape(-1), blk[:, 208:210].reshape(-1)]
+        out[r * 210 * nb:(r + 1) * 210 * nb] = np.concatenate(parts)
+    return out
+
+
+@pytest.mark.parametrize("d,ff", [(4096, 512), (1024, 14336 // 7), (768, 2304)])
+def test_q6k_tier_layout_round_trip(ctx, d, ff):
+    """Q6_K parts are stored as tiled rows (per-task nibble and high-bit pieces):
+    host and device uploads agree with the layout's definition, partial groups
+    and odd superblock counts included, and kmoe_expert_read restores GGUF."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(d * 3 + ff)
+    ctx.layer_create(96, 4, 2, d, ff, Q6_K, Q6_K, Q6_K)
+    try:
+        for p in range(3):
+            rows, nb = (ff, d // 256) if p < 2 else (d, ff // 256)
+            g = rng.integers(0, 256, rows * nb * 210, dtype=np.uint8)
+            ctx.expert_upload(96, 0, p, g)
+            ctx.expert_upload(96, 1, p, torch.from_numpy(g).cuda())
+            for e in (0, 1):
+                ptr, n = ctx.expert_part(96, e, p)
+                raw = np.empty(n, np.uint8)
+                ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, raw.ctypes.data, ctypes.c_void_p(ptr), n))
+                assert np.array_equal(raw, _tiled_q6k_reference(g, rows, nb)), (p, e)
+                assert np.array_equal(ctx.expert_read(96, e, p), g), (p, e)
+    finally:
+        ctx.layer_destroy(96)
+
+
 def test_errors_map_to_status_codes(ctx):
     from kestrel_amd.kmoe import KmoeError
 
