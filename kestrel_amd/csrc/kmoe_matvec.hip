@@ -154,14 +154,17 @@ __device__ __forceinline__ void q4k_ints(const Q4kW &w, int k, const int8_t *xq_
 // byte 208. Task t is quarter k of superblock t/4: half h = k/2, nibble
 // p = k%2. Its 64 weights are rows ri = 2p (weights 0-31) and 2p+1 (32-63) of
 // half h; weight l of row ri is nibble p of ql[64h + 32*(ri&1) + l] with bits
-// 2ri..2ri+1 of qh[32h + l] above it, scaled by sc[8h + 2ri + l/16].
-// Superblocks start on 2-byte boundaries; the 16-byte loads rely on the
-// target's unaligned global access.
+// 2ri..2ri+1 of qh[32h + l] above it, scaled by sc[8h + 2ri + l/16]. Both
+// tasks of a half need all 64 ql and 32 qh bytes of it: the two lanes holding
+// tasks 2h and 2h+1 (adjacent lanes) each load one half of those bytes (lane
+// p: ql[64h + 32p, +32) and qh[32h + 16p, +16)) and swap them at use with a
+// DPP move. Superblocks start on 2-byte boundaries; the 16-byte loads rely on
+// the target's unaligned global access.
 struct Q6kW {
-  uint4 l0, l1, l2, l3;  // ql[64h, 64h+64)
-  uint4 h0, h1;          // qh[32h, 32h+32)
-  uint32_t sc;           // sc[8h+4p, 8h+4p+4)
-  uint32_t d;            // f16 bits of d
+  uint4 l0, l1;  // ql[64h + 32p, 64h + 32p + 32)
+  uint4 hq;      // qh[32h + 16p, 32h + 16p + 16)
+  uint32_t sc;   // sc[8h+4p, 8h+4p+4)
+  uint32_t d;    // f16 bits of d
 };
 typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32u2 __attribute__((aligned(2)));
@@ -174,25 +177,35 @@ __device__ __forceinline__ Q6kW q6k_load(const uint8_t *row, int t) {
   const int k = t & 3, h = k >> 1, p = k & 1;
   const uint8_t *b = row + sb * 210;
   Q6kW w;
-  w.l0 = ld_nt_u2(b + 64 * h);
-  w.l1 = ld_nt_u2(b + 64 * h + 16);
-  w.l2 = ld_nt_u2(b + 64 * h + 32);
-  w.l3 = ld_nt_u2(b + 64 * h + 48);
-  w.h0 = ld_nt_u2(b + 128 + 32 * h);
-  w.h1 = ld_nt_u2(b + 128 + 32 * h + 16);
+  w.l0 = ld_nt_u2(b + 64 * h + 32 * p);
+  w.l1 = ld_nt_u2(b + 64 * h + 32 * p + 16);
+  w.hq = ld_nt_u2(b + 128 + 32 * h + 16 * p);
   w.sc = __builtin_nontemporal_load((const u32u2 *)(b + 192 + 8 * h + 4 * p));
   w.d = __builtin_nontemporal_load((const uint16_t *)(b + 208));
   return w;
 }
 // Integer part of one Q6_K task: sumi = sum_g sc_g * sum q*x over its four
-// 16-weight groups, offs = sum_g sc_g * bsum_g (avx2.rs:398-414).
+// 16-weight groups, offs = sum_g sc_g * bsum_g (avx2.rs:398-414). Every lane
+// of the wave's active quads must call it together (the partner exchange).
 __device__ __forceinline__ void q6k_ints(const Q6kW &w, int k, const int4 &x0, const int4 &x1, const int4 &x2,
                                          const int4 &x3, const int4 &bs, int &sumi, int &offs) {
-  const int sn = 4 * (k & 1);  // nibble shift; the qh bits of row 2p sit at 4p, of row 2p+1 at 4p+2
+  const bool p = (k & 1) != 0;
+  const uint32_t own[12] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w,
+                            w.hq.x, w.hq.y, w.hq.z, w.hq.w};
+  uint32_t L[16], H[8];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    const uint32_t o = (uint32_t)dpp_i<kDppXor1>((int)own[i]);  // the partner lane's half
+    if (i < 8) {
+      L[i] = p ? o : own[i];
+      L[8 + i] = p ? own[i] : o;
+    } else {
+      H[i - 8] = p ? o : own[i];
+      H[i - 4] = p ? own[i] : o;
+    }
+  }
+  const int sn = p ? 4 : 0;  // nibble shift; the qh bits of row 2p sit at 4p, of row 2p+1 at 4p+2
   const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x03030303u;
-  const uint32_t L[16] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w,
-                          w.l2.x, w.l2.y, w.l2.z, w.l2.w, w.l3.x, w.l3.y, w.l3.z, w.l3.w};
-  const uint32_t H[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
   const uint32_t X[16] = {(uint32_t)x0.x, (uint32_t)x0.y, (uint32_t)x0.z, (uint32_t)x0.w,
                           (uint32_t)x1.x, (uint32_t)x1.y, (uint32_t)x1.z, (uint32_t)x1.w,
                           (uint32_t)x2.x, (uint32_t)x2.y, (uint32_t)x2.z, (uint32_t)x2.w,
