@@ -234,6 +234,8 @@ struct MoeWs {
   float *hd;
   int32_t *hs;
   float *y;
+  float *part;  // partial sums of the f32 path's column splits
+  int64_t part_floats;
 };
 
 MoeWs carve_moe(uint8_t *base, int64_t S, int64_t E, int64_t k, int64_t d, int64_t F, size_t *total) {
@@ -257,6 +259,10 @@ MoeWs carve_moe(uint8_t *base, int64_t S, int64_t E, int64_t k, int64_t d, int64
   w.hd = cv.take<float>(slots * (F / 32));
   w.hs = cv.take<int32_t>(slots * (F / 16));
   w.y = cv.take<float>(slots * d);
+  const int64_t ma = slots < E ? slots : E;
+  const int64_t pg = gemm_f32_part_floats(F, d, ma, S, slots), pd = gemm_f32_part_floats(d, F, ma, S, slots);
+  w.part_floats = pg > pd ? pg : pd;
+  w.part = w.part_floats > 0 ? cv.take<float>(w.part_floats) : nullptr;
   *total = cv.off;
   return w;
 }
@@ -323,17 +329,28 @@ int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t c
   return KMOE_OK;
 }
 
-// Scratch for one int8-quantized activation matrix [s_rows, cols].
+// Scratch for one int8-quantized activation matrix [s_rows, cols], plus the
+// f32 path's partial sums (part_floats, 0 for none).
 struct QRows {
   int8_t *q;
   float *d;
   int32_t *s;
+  float *part;
+  int64_t part_floats;
 };
-QRows carve_qrows(uint8_t *base, int64_t s_rows, int64_t cols, size_t *total) {
+QRows carve_qrows(uint8_t *base, int64_t s_rows, int64_t cols, size_t *total, int64_t part_floats = 0) {
   Carver cv{base};
-  QRows r{cv.take<int8_t>(s_rows * cols), cv.take<float>(s_rows * (cols / 32)), cv.take<int32_t>(s_rows * (cols / 16))};
+  QRows r{cv.take<int8_t>(s_rows * cols), cv.take<float>(s_rows * (cols / 32)), cv.take<int32_t>(s_rows * (cols / 16)),
+          nullptr, part_floats};
+  r.part = part_floats > 0 ? cv.take<float>(part_floats) : nullptr;
   *total = cv.off;
   return r;
+}
+
+// The f32 path's partial sums for the shared expert's three products.
+int64_t sh_part_floats(int64_t Fs, int64_t d, int64_t S) {
+  const int64_t a = gemm_f32_part_floats(Fs, d, 1, S, S), b = gemm_f32_part_floats(d, Fs, 1, S, S);
+  return a > b ? a : b;
 }
 
 // quant::matmul (quant.rs:229-328) on validated arguments: F32 weights in the
@@ -348,7 +365,7 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
     return KMOE_OK;
   }
   if (!int_path(c->regime, s_rows)) {
-    LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out));
+    LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out, qr.part, qr.part_floats));
     return KMOE_OK;
   }
   if (is_kq(t)) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
@@ -608,12 +625,13 @@ int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, i
     int rc = check_quant_shape(c, t, cols);
     if (rc) return rc;
   }
-  // int8 activations are quantized into the workspace
+  // int8 activations (or the f32 path's partial sums) go to the workspace
+  const int64_t pf = gemm_f32_part_floats(rows, cols, 1, s_rows, s_rows);
   size_t need = 0;
-  carve_qrows(nullptr, s_rows, cols, &need);
+  carve_qrows(nullptr, s_rows, cols, &need, pf);
   int rc = ensure_ws(c, need);
   if (rc) return rc;
-  QRows qr = carve_qrows(c->ws, s_rows, cols, &need);
+  QRows qr = carve_qrows(c->ws, s_rows, cols, &need, pf);
   return matmul_core(c, t, (const uint8_t *)w, rows, cols, x, s_rows, out, qr);
 }
 
@@ -940,7 +958,7 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
     cv.take<float>(S * d);
     cv.take<float>(S);
     size_t q = 0;
-    carve_qrows(nullptr, S, mx, &q);
+    carve_qrows(nullptr, S, mx, &q, sh_part_floats(Fs, d, S));
     sh_need = cv.off + align_up(q);
   }
   DeviceGuard g(c->device);
@@ -1086,8 +1104,10 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
              launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
   }
   if (any_f32) {
-    LAUNCH(c, "moe_gate_f32", launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, h, w.h));
-    LAUNCH(c, "moe_up_f32", launch_moe_f32(st, 1, gt, tier, F, d, rt, regime, max_active, S, h, w.h));
+    LAUNCH(c, "moe_gate_f32",
+           launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h, w.part, w.part_floats));
+    LAUNCH(c, "moe_up_f32",
+           launch_moe_f32(st, 1, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h, w.part, w.part_floats));
   }
   // down (transformer.rs:559-560)
   if (any_int) {
@@ -1103,7 +1123,9 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
       LAUNCH(c, "moe_down_int",
              launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
   }
-  if (any_f32) LAUNCH(c, "moe_down_f32", launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, w.h, w.y));
+  if (any_f32)
+    LAUNCH(c, "moe_down_f32",
+           launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, slots, w.h, w.y, w.part, w.part_floats));
   // combine (transformer.rs:566-570)
   LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
   }
@@ -1115,7 +1137,7 @@ done:
     float *gs = cv.take<float>(S * Fs), *us = cv.take<float>(S * Fs), *ys = cv.take<float>(S * d);
     float *gl = cv.take<float>(S);
     size_t q = 0;
-    QRows qr = carve_qrows(c->ws + moe_need + cv.off, S, mx, &q);
+    QRows qr = carve_qrows(c->ws + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
     rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
     if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
     if (rc) return rc;

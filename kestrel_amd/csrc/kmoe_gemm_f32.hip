@@ -4,13 +4,15 @@
 // Dequantization is dequant_row (quant.rs:82-89 for Q8_0: q * d; quant.rs:
 // 138-155 for Q4_K: (d*sc)*q - (dmin*m), one multiply and one subtract, no
 // FMA), so every weight value equals the reference's bit for bit. The dot
-// products accumulate with FMA in a different order from gemm_f32's 8-lane
-// chains (avx2.rs:230-286): results agree to a few f32 ulp of the sum.
+// products run on the fp32 matrix cores (exact products, fp32 sums) in a
+// different order from gemm_f32's 8-lane chains (avx2.rs:230-286): results
+// agree to a few f32 ulp of the sum.
 //
-// Tiling: a work-group computes 64 weight rows x 16 activation rows. Each
-// K-step of 64 columns dequantizes the weight tile into LDS (4 threads per
-// row, 16 weights each) and stages the activation tile; each thread then owns
-// 4 rows x 1 activation row.
+// Tiling: a work-group computes 64 weight rows x 16 activation rows; the
+// products run on the fp32 matrix cores (see k_gemm_f32). When the row tiles
+// alone give few work-groups (decode batches), the columns are split: each
+// split writes partial sums and a second kernel adds them in split order, so
+// results do not depend on timing.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 
@@ -18,7 +20,7 @@ namespace kmoe {
 
 namespace {
 
-constexpr int TR = 64, TT = 16, KC = 64, PAD = 65;
+constexpr int TR = 64, TT = 16, KC = 64, PAD = 68;  // PAD: 16-byte aligned LDS rows
 
 struct GArgs {
   const uint8_t *w;  // plain
@@ -29,6 +31,11 @@ struct GArgs {
   ExpertTier tier;
   Routing rt;
   int regime;
+  int ntt;          // token tiles
+  int ks;           // column splits (1: no partial sums)
+  int64_t cps;      // column chunks per split
+  float *part;      // [ks][n_slots][rows] partial sums when ks > 1
+  int64_t n_slots;  // activation rows (plain) or slots (grouped)
 };
 
 enum { G_PLAIN = 0, G_GATE = 1, G_UP = 2, G_DOWN = 3 };
@@ -38,23 +45,68 @@ __device__ __forceinline__ bool f32_regime(int regime, int n) {
 }
 
 // 16 consecutive dequantized weights of chunk kc, part p (0..3), of one row
-// (Q4_K and Q6_K: GGUF bytes, or tiled rows of nb superblocks when TILED).
+// (Q4_K and Q6_K: GGUF bytes, or tiled rows of nb superblocks when TILED), in
+// two steps: load16 issues the loads of the raw bytes, convert16 turns them
+// into f32 (so the next chunk's bytes can be in flight meanwhile).
+typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <int TYPE, bool TILED>
-__device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p, int64_t nb, float *o) {
+struct Raw16 {
+  u32x4u2 a, b;    // Q4_K: header, nibbles; Q6_K: low bits, high bits; Q8_0: a = the 16 bytes
+  uint32_t c, d;   // Q6_K: scale byte, f16 d; Q8_0: f16 d
+  float4 f[4];     // F32
+};
+
+template <int TYPE, bool TILED>
+__device__ __forceinline__ Raw16<TYPE, TILED> load16(const uint8_t *row, int64_t kc, int p, int64_t nb) {
+  Raw16<TYPE, TILED> r;
   if constexpr (TYPE == T_Q4_K) {
     const int64_t sbi = kc >> 2;
-    const uint8_t *sb = row + sbi * (TILED ? 16 : 144);
     const int k = (int)(kc & 3);
-    const uint4 hdr = *(const uint4 *)sb;
-    const float d = f16_bits_to_f32(hdr.x), dmin = f16_bits_to_f32(hdr.x >> 16);
+    const uint8_t *sb = row + sbi * (TILED ? 16 : 144);
+    r.a = *(const u32x4u2 *)sb;
+    r.b = *(const u32x4u2 *)(TILED ? row + tq4_qs_off(nb, sbi, k, p & 1) : sb + 16 + 32 * k + 16 * (p & 1));
+  } else if constexpr (TYPE == T_Q6_K) {
+    const int64_t sb = kc >> 2;
+    const int k = (int)(kc & 3), h = k >> 1, np = k & 1, ri = 2 * np + (p >> 1), l0 = 16 * (p & 1);
+    if constexpr (TILED) {  // tq6_piece_off: nibble piece p&1, high-bit piece
+      const uint8_t *p0 = row + tq6_piece_off(nb, sb, k, 0);
+      const int64_t js = tq6_j_stride(nb, sb);
+      r.a = *(const u32x4u2 *)(p0 + (p & 1) * js);
+      r.b = *(const u32x4u2 *)(p0 + 2 * js);
+      r.c = row[192 * nb + 16 * sb + 4 * k + p];
+      r.d = *(const uint16_t *)(row + 208 * nb + 2 * sb);
+    } else {
+      const uint8_t *blk = row + sb * 210;
+      r.a = *(const u32x4u2 *)(blk + 64 * h + 32 * (ri & 1) + l0);
+      r.b = *(const u32x4u2 *)(blk + 128 + 32 * h + l0);
+      r.c = blk[192 + 8 * h + 2 * ri + (p & 1)];
+      r.d = *(const uint16_t *)(blk + 208);
+    }
+  } else if constexpr (TYPE == T_Q8_0) {
+    const uint8_t *blk = row + (2 * kc + (p >> 1)) * 34;
+    r.a = *(const u32x4u2 *)(blk + 2 + 16 * (p & 1));
+    r.d = *(const uint16_t *)blk;
+  } else {  // F32
+    const float4 *f = (const float4 *)((const float *)row + kc * 64 + 16 * p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.f[i] = f[i];
+  }
+  return r;
+}
+
+template <int TYPE, bool TILED>
+__device__ __forceinline__ void convert16(const Raw16<TYPE, TILED> &r, int64_t kc, int p, float *o) {
+  if constexpr (TYPE == T_Q4_K) {  // quant.rs:138-155: (d*sc)*q - (dmin*m)
+    const int k = (int)(kc & 3);
+    const float d = f16_bits_to_f32(r.a.x), dmin = f16_bits_to_f32(r.a.x >> 16);
     int sA, mA, sB, mB;
-    q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, k, sA, mA, sB, mB);
+    q4k_scale_min_pair(r.a.y, r.a.z, r.a.w, k, sA, mA, sB, mB);
     const bool hi = p >= 2;
     const float dl = d * (float)(hi ? sB : sA);
     const float ml = dmin * (float)(hi ? mB : mA);
-    const uint8_t *qp = TILED ? row + tq4_qs_off(nb, sbi, k, p & 1) : sb + 16 + 32 * k + 16 * (p & 1);
-    const uint4 q = *(const uint4 *)qp;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xffu;
@@ -63,59 +115,52 @@ __device__ __forceinline__ void dequant16(const uint8_t *row, int64_t kc, int p,
       o[i] = t - ml;
     }
   } else if constexpr (TYPE == T_Q6_K) {  // quant.rs:180-201: y = (d * sc) * (q - 32)
-    // chunk kc = quarter k of superblock kc/4 (half h, nibble np); part p is
-    // weights 16*(p&1).. of row ri = 2*np + (p>>1) of the half
-    typedef uint32_t u32x4u2 __attribute__((ext_vector_type(4), aligned(2)));
-    const int64_t sb = kc >> 2;
-    const int k = (int)(kc & 3), h = k >> 1, np = k & 1, ri = 2 * np + (p >> 1), l0 = 16 * (p & 1);
-    if constexpr (TILED) {  // tq6_piece_off: nibble piece p&1 (nibble p>>1), high-bit piece (nibble p&1)
-      const uint8_t *p0 = row + tq6_piece_off(nb, sb, k, 0);
-      const int64_t js = tq6_j_stride(nb, sb);
-      const float d = f16_bits_to_f32((uint32_t)row[208 * nb + 2 * sb] | ((uint32_t)row[208 * nb + 2 * sb + 1] << 8));
-      const float ds = d * (float)(int8_t)row[192 * nb + 16 * sb + 4 * k + p];
-      const u32x4u2 nv = *(const u32x4u2 *)(p0 + (p & 1) * js);
-      const u32x4u2 hv = *(const u32x4u2 *)(p0 + 2 * js);
-      const uint32_t nw[4] = {nv.x, nv.y, nv.z, nv.w}, hw[4] = {hv.x, hv.y, hv.z, hv.w};
-      const int nsh = 4 * (p >> 1), hsh = 4 * (p & 1) + 2 * (p >> 1);
+    const int k = (int)(kc & 3), np = k & 1, ri = 2 * np + (p >> 1);
+    const float ds = f16_bits_to_f32(r.d) * (float)(int8_t)r.c;
+    const uint32_t lw[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, hw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    // tiled: nibble p>>1 of the nibble piece, bits 4*(p&1)+2*(p>>1) of the
+    // high-bit piece; GGUF: nibble np of ql, bits 2*ri of qh
+    const int nsh = TILED ? 4 * (p >> 1) : 4 * np;
+    const int hsh = TILED ? 4 * (p & 1) + 2 * (p >> 1) : 2 * ri;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t nb8 = (nw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb8 = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-        const int q = (int)(((nb8 >> nsh) & 0xfu) | (((hb8 >> hsh) & 3u) << 4)) - 32;
-        o[i] = ds * (float)q;
-      }
-    } else {
-      const uint8_t *blk = row + sb * 210;
-      const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-      const float ds = d * (float)(int8_t)blk[192 + 8 * h + 2 * ri + (p & 1)];
-      const u32x4u2 ql = *(const u32x4u2 *)(blk + 64 * h + 32 * (ri & 1) + l0);
-      const u32x4u2 qh = *(const u32x4u2 *)(blk + 128 + 32 * h + l0);
-      const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
-        const int q = (int)((np ? (lb >> 4) : (lb & 0xfu)) | (((hb >> (2 * ri)) & 3u) << 4)) - 32;
-        o[i] = ds * (float)q;
-      }
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xffu, hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+      const int q = (int)(((lb >> nsh) & 0xfu) | (((hb >> hsh) & 3u) << 4)) - 32;
+      o[i] = ds * (float)q;
     }
-  } else if constexpr (TYPE == T_Q8_0) {
-    const int64_t b = 2 * kc + (p >> 1);
-    const uint8_t *blk = row + b * 34;
-    const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    const int8_t *qs = (const int8_t *)(blk + 2 + 16 * (p & 1));
+  } else if constexpr (TYPE == T_Q8_0) {  // quant.rs:82-89: q * d
+    const float d = f16_bits_to_f32(r.d);
+    const uint32_t qw[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = (float)qs[i] * d;
-  } else {  // F32
-    const float *f = (const float *)row + kc * 64 + 16 * p;
+    for (int i = 0; i < 16; ++i) o[i] = (float)(int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 0xffu) * d;
+  } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = f[i];
+    for (int i = 0; i < 4; ++i) {
+      o[4 * i] = r.f[i].x;
+      o[4 * i + 1] = r.f[i].y;
+      o[4 * i + 2] = r.f[i].z;
+      o[4 * i + 3] = r.f[i].w;
+    }
   }
 }
 
+// A work-group computes TR = 64 weight rows x TT = 16 activation rows; each
+// K-step of KC = 64 columns dequantizes the weight tile into LDS (4 threads
+// per row, 16 weights each; the next step's raw bytes are loaded meanwhile)
+// and stages the activation tile. Wave w then multiplies rows [16w, 16w+16)
+// by the 16 activation rows on the fp32 matrix cores (v_mfma_f32_16x16x4f32,
+// exact fp32 products, fp32 sums): MFMA s of the step takes column 16q + s
+// for lane quad q, so each lane reads its 16 values with four ds_read_b128.
+// blockIdx.z = ks * ntt + token tile: with split-K (a.ks > 1) the work-group
+// covers column chunks [ks*cps, (ks+1)*cps) and writes its partial sums to
+// a.part[ks][slot][r]; k_gemm_f32_reduce then adds the splits in ks order.
 template <int TYPE, int MODE>
 __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
-  __shared__ float Ws[TR][PAD];
-  __shared__ float Xs[TT][PAD];
+  constexpr bool TL = MODE != G_PLAIN;  // expert tier rows are tiled
+  __shared__ __attribute__((aligned(16))) float Ws[TR][PAD];
+  __shared__ __attribute__((aligned(16))) float Xs[TT][PAD];
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int64_t rows = a.rows, cols = a.cols;
   const int64_t row_bytes = TYPE == T_Q4_K   ? cols / 256 * 144
                             : TYPE == T_Q6_K ? cols / 256 * 210
@@ -136,9 +181,15 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
     if (!f32_regime(a.regime, n)) return;
     W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[MODE == G_GATE ? 0 : (MODE == G_UP ? 1 : 2)];
   }
-  const int j0 = blockIdx.z * TT;
+  const int tile = (int)(blockIdx.z % a.ntt), ks = (int)(blockIdx.z / a.ntt);
+  const int j0 = tile * TT;
   if (j0 >= n) return;
+  const int64_t nchunk = cols / KC;
+  const int64_t c_begin = (int64_t)ks * a.cps;
+  const int64_t c_end = c_begin + a.cps < nchunk ? c_begin + a.cps : nchunk;
+  if (c_begin >= c_end) return;
   const int64_t r0 = (int64_t)blockIdx.x * TR;
+  const int64_t nb = cols / 256;
 
   // activation row of local token j (absolute row index into a.x)
   auto act_row = [&](int j) -> int64_t {
@@ -147,87 +198,155 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
     else return j;
   };
 
-  const int tok = tid & 15, rg = tid >> 4;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int drow = tid >> 2, dpart = tid & 3;
   const int xtok = tid >> 4, xcol = (tid & 15) * 4;
   const bool xvalid = j0 + xtok < n;
-  const int64_t xr = xvalid ? act_row(j0 + xtok) : 0;
-  const float *xrow = a.x + xr * cols;
+  const float *xrow = a.x + (xvalid ? act_row(j0 + xtok) : 0) * cols + xcol;
   const bool wvalid = r0 + drow < rows;
-  const uint8_t *wrow = W + (r0 + drow) * row_bytes;
+  const uint8_t *wrow = W + (wvalid ? r0 + drow : 0) * row_bytes;
 
-  for (int64_t kc = 0; kc < cols / KC; ++kc) {
+  Raw16<TYPE, TL> cur{}, nxt{};
+  float4 xc = make_float4(0.f, 0.f, 0.f, 0.f), xn = xc;
+  if (wvalid) cur = load16<TYPE, TL>(wrow, c_begin, dpart, nb);
+  if (xvalid) xc = *(const float4 *)(xrow + c_begin * KC);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const float4 *wa = (const float4 *)&Ws[16 * wave + (lane & 15)][16 * (lane >> 4)];
+  const float4 *xb = (const float4 *)&Xs[lane & 15][16 * (lane >> 4)];
+
+  for (int64_t kc = c_begin; kc < c_end; ++kc) {
+    if (kc + 1 < c_end) {
+      if (wvalid) nxt = load16<TYPE, TL>(wrow, kc + 1, dpart, nb);
+      if (xvalid) xn = *(const float4 *)(xrow + (kc + 1) * KC);
+    }
     float wv[16];
     if (wvalid) {
-      dequant16<TYPE, MODE != G_PLAIN>(wrow, kc, dpart, cols / 256, wv);
+      convert16<TYPE, TL>(cur, kc, dpart, wv);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) wv[i] = 0.0f;
     }
+    float4 *wd = (float4 *)&Ws[drow][dpart * 16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Ws[drow][dpart * 16 + i] = wv[i];
-    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (xvalid) xv = *(const float4 *)(xrow + kc * KC + xcol);
-    Xs[xtok][xcol + 0] = xv.x;
-    Xs[xtok][xcol + 1] = xv.y;
-    Xs[xtok][xcol + 2] = xv.z;
-    Xs[xtok][xcol + 3] = xv.w;
+    for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+    *(float4 *)&Xs[xtok][xcol] = xc;
     __syncthreads();
-#pragma unroll 8
-    for (int kk = 0; kk < KC; ++kk) {
-      const float xk = Xs[tok][kk];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = fmaf(Ws[4 * rg + i][kk], xk, acc[i]);
+    for (int m = 0; m < 4; ++m) {
+      const float4 A = wa[m], B = xb[m];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, acc, 0, 0, 0);
     }
     __syncthreads();
+    cur = nxt;
+    xc = xn;
   }
 
-  const int j = j0 + tok;
+  // lane holds rows 4*(lane/16) + v of the wave's 16, activation row lane%16
+  const int j = j0 + (lane & 15);
   if (j >= n) return;
+  const int64_t slot = MODE == G_PLAIN ? (int64_t)j : p0 + j;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = r0 + 4 * rg + i;
+  for (int v = 0; v < 4; ++v) {
+    const int64_t r = r0 + 16 * wave + 4 * (lane >> 4) + v;
     if (r >= rows) continue;
-    if constexpr (MODE == G_PLAIN) {
-      a.out[(int64_t)j * rows + r] = acc[i];
-    } else if constexpr (MODE == G_GATE || MODE == G_DOWN) {
-      a.out[(p0 + j) * rows + r] = acc[i];
+    const float y = acc[v];
+    if (a.ks > 1) {
+      a.part[((int64_t)ks * a.n_slots + slot) * rows + r] = y;
+    } else if constexpr (MODE == G_PLAIN || MODE == G_GATE || MODE == G_DOWN) {
+      a.out[slot * rows + r] = y;
     } else {  // G_UP: SwiGLU with the gate value stored by G_GATE (transformer.rs:558)
-      float *o = a.out + (p0 + j) * rows + r;
+      float *o = a.out + slot * rows + r;
       const float g = *o;
       const float den = 1.0f + expf_cr(-g);
       const float q = g / den;
-      *o = q * acc[i];
+      *o = q * y;
     }
   }
 }
 
+// Sum of the a.ks partial results in split order, then the mode's store.
 template <int MODE>
-hipError_t launch_type(hipStream_t st, int type, const GArgs &a, dim3 grid) {
-  switch (type) {
-    case T_Q4_K:
-      KMOE_LAUNCH((k_gemm_f32<T_Q4_K, MODE>), grid, dim3(256), 0, st, a);
-      break;
-    case T_Q8_0:
-      KMOE_LAUNCH((k_gemm_f32<T_Q8_0, MODE>), grid, dim3(256), 0, st, a);
-      break;
-    case T_Q6_K:
-      KMOE_LAUNCH((k_gemm_f32<T_Q6_K, MODE>), grid, dim3(256), 0, st, a);
-      break;
-    case T_F32:
-      KMOE_LAUNCH((k_gemm_f32<T_F32, MODE>), grid, dim3(256), 0, st, a);
-      break;
-    default:
-      return hipErrorInvalidValue;
+__global__ void __launch_bounds__(256) k_gemm_f32_reduce(GArgs a) {
+  const int64_t rows = a.rows;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  int n;
+  int64_t p0 = 0;
+  if constexpr (MODE == G_PLAIN) {
+    n = (int)a.s_rows;
+  } else {
+    const int i = blockIdx.y;
+    if (i >= *a.rt.n_active) return;
+    const int e = a.rt.active[i];
+    p0 = a.rt.offsets[e];
+    n = (int)(a.rt.offsets[e + 1] - p0);
+    if (!f32_regime(a.regime, n)) return;
   }
+  for (int j = 0; j < n; ++j) {
+    const int64_t slot = p0 + j;
+    float v = a.part[slot * rows + r];
+    for (int k = 1; k < a.ks; ++k) v += a.part[((int64_t)k * a.n_slots + slot) * rows + r];
+    if constexpr (MODE == G_UP) {
+      float *o = a.out + slot * rows + r;
+      const float g = *o;
+      const float den = 1.0f + expf_cr(-g);
+      const float q = g / den;
+      *o = q * v;
+    } else {
+      a.out[slot * rows + r] = v;
+    }
+  }
+}
+
+// Split-K factor: enough work-groups (about 4096, counting the groups that
+// exit at once) when the row tiles alone are few; 1 when they are many.
+int splits_for(int64_t rows, int64_t cols, int64_t groups) {
+  const int64_t tiles = (rows + TR - 1) / TR * groups;
+  const int64_t nchunk = cols / KC;
+  int64_t ks = (4096 + tiles - 1) / tiles;
+  if (ks > nchunk / 8) ks = nchunk / 8;
+  if (ks > 16) ks = 16;
+  return ks < 1 ? 1 : (int)ks;
+}
+
+template <int MODE>
+hipError_t launch_type(hipStream_t st, int type, GArgs a, int64_t rows_x, int groups, int64_t max_rows,
+                       int64_t part_floats) {
+  a.ntt = (int)((max_rows + TT - 1) / TT);
+  a.ks = splits_for(a.rows, a.cols, (int64_t)groups * a.ntt);
+  if ((int64_t)a.ks * a.n_slots * a.rows > part_floats || !a.part) a.ks = 1;
+  const int64_t nchunk = a.cols / KC;
+  a.cps = (nchunk + a.ks - 1) / a.ks;
+  const dim3 grid((unsigned)rows_x, (unsigned)groups, (unsigned)(a.ntt * a.ks));
+#define KMOE_GEMM(TY) KMOE_LAUNCH((k_gemm_f32<TY, MODE>), grid, dim3(256), 0, st, a)
+  switch (type) {
+    case T_Q4_K: KMOE_GEMM(T_Q4_K); break;
+    case T_Q8_0: KMOE_GEMM(T_Q8_0); break;
+    case T_Q6_K: KMOE_GEMM(T_Q6_K); break;
+    case T_F32: KMOE_GEMM(T_F32); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef KMOE_GEMM
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.ks == 1) return e;
+  KMOE_LAUNCH((k_gemm_f32_reduce<MODE>), dim3((unsigned)((a.rows + 255) / 256), (unsigned)groups), dim3(256), 0,
+              st, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
+int64_t gemm_f32_part_floats(int64_t rows, int64_t cols, int64_t groups, int64_t max_rows, int64_t n_slots) {
+  if (rows <= 0 || cols % KC != 0 || max_rows <= 0) return 0;
+  const int64_t ntt = (max_rows + TT - 1) / TT;
+  const int ks = splits_for(rows, cols, groups * ntt);
+  return ks > 1 ? (int64_t)ks * n_slots * rows : 0;
+}
+
 hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const float *x,
-                             int64_t s_rows, float *out) {
+                             int64_t s_rows, float *out, float *part, int64_t part_floats) {
   if (rows == 0 || s_rows == 0) return hipSuccess;
   if (cols % KC != 0) return hipErrorInvalidValue;
   GArgs a{};
@@ -237,13 +356,14 @@ hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t
   a.x = x;
   a.s_rows = s_rows;
   a.out = out;
-  dim3 grid((unsigned)((rows + TR - 1) / TR), 1, (unsigned)((s_rows + TT - 1) / TT));
-  return launch_type<G_PLAIN>(st, type, a, grid);
+  a.part = part;
+  a.n_slots = s_rows;
+  return launch_type<G_PLAIN>(st, type, a, (rows + TR - 1) / TR, 1, s_rows, part_floats);
 }
 
 hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t max_rows_per_expert,
-                          const float *x, float *out) {
+                          int64_t n_slots, const float *x, float *out, float *part, int64_t part_floats) {
   if (rows == 0 || max_active == 0 || max_rows_per_expert == 0) return hipSuccess;
   if (cols % KC != 0) return hipErrorInvalidValue;
   GArgs a{};
@@ -254,12 +374,13 @@ hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &
   a.tier = tier;
   a.rt = rt;
   a.regime = regime;
-  dim3 grid((unsigned)((rows + TR - 1) / TR), (unsigned)max_active,
-            (unsigned)((max_rows_per_expert + TT - 1) / TT));
+  a.part = part;
+  a.n_slots = n_slots;
+  const int64_t rx = (rows + TR - 1) / TR;
   switch (mode) {
-    case 0: return launch_type<G_GATE>(st, type, a, grid);
-    case 1: return launch_type<G_UP>(st, type, a, grid);
-    case 2: return launch_type<G_DOWN>(st, type, a, grid);
+    case 0: return launch_type<G_GATE>(st, type, a, rx, max_active, max_rows_per_expert, part_floats);
+    case 1: return launch_type<G_UP>(st, type, a, rx, max_active, max_rows_per_expert, part_floats);
+    case 2: return launch_type<G_DOWN>(st, type, a, rx, max_active, max_rows_per_expert, part_floats);
     default: return hipErrorInvalidValue;
   }
 }

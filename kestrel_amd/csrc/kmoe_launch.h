@@ -155,13 +155,18 @@ hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int
                              int32_t *mins);
 
 // ---- f32 path (kmoe_gemm_f32.hip): dequantized weights x f32 activations
+// Partial-sum floats the launchers below use for this shape (0: no column
+// split); groups = 1 (plain) or max_active, max_rows = most activation rows of
+// one group, n_slots = all activation rows (plain) or slots (grouped). With a
+// smaller buffer (or none) they run unsplit.
+int64_t gemm_f32_part_floats(int64_t rows, int64_t cols, int64_t groups, int64_t max_rows, int64_t n_slots);
 // Plain: out[s*rows + r].
 hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const float *x,
-                             int64_t s_rows, float *out);
+                             int64_t s_rows, float *out, float *part, int64_t part_floats);
 // Grouped: mode 0 = gate (store g into h), 1 = up (h = silu(h) * u), 2 = down (store y).
 hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t max_rows_per_expert,
-                          const float *x, float *out);
+                          int64_t n_slots, const float *x, float *out, float *part, int64_t part_floats);
 
 // ---- routing (kmoe_route.hip)
 // logits [S, E] = router [E, d] . x [S, d] in the reference's summation order

@@ -363,7 +363,9 @@ def test_device_generated_weights_are_stream_ordered(ctx, orc):
             del t
     router = orc.normal(3, E * d, 0.0, 0.02).reshape(E, d)
     ctx.router_upload(90, router)
-    h = torch.randn((4, d), device="cuda") * 2.0  # async producer right before the call
+    gh = torch.Generator(device="cuda")
+    gh.manual_seed(7)  # a fixed input: an unseeded one can land an int8 rounding of h on a midpoint
+    h = torch.randn((4, d), device="cuda", generator=gh) * 2.0  # async producer right before the call
     out = host(ctx.moe_ffn(90, h))
     parts = [[None] * 3 for _ in range(E)]
     for e in range(E):
