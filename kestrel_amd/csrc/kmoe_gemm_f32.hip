@@ -8,8 +8,8 @@
 // different order from gemm_f32's 8-lane chains (avx2.rs:230-286): results
 // agree to a few f32 ulp of the sum.
 //
-// Tiling: a work-group computes 64 weight rows x 16 activation rows; the
-// products run on the fp32 matrix cores (see k_gemm_f32). When the row tiles
+// Tiling: a work-group computes 64 weight rows x 16 or 64 activation rows;
+// the products run on the fp32 matrix cores (see k_gemm_f32). When the row tiles
 // alone give few work-groups (decode batches), the columns are split: each
 // split writes partial sums and a second kernel adds them in split order, so
 // results do not depend on timing.
@@ -20,7 +20,7 @@ namespace kmoe {
 
 namespace {
 
-constexpr int TR = 64, TT = 16, KC = 64, PAD = 68;  // PAD: 16-byte aligned LDS rows
+constexpr int TR = 64, KC = 64, PAD = 68;  // PAD: 16-byte aligned LDS rows
 
 struct GArgs {
   const uint8_t *w;  // plain
@@ -31,9 +31,9 @@ struct GArgs {
   ExpertTier tier;
   Routing rt;
   int regime;
-  int ntt;          // token tiles
-  int ks;           // column splits (1: no partial sums)
-  int64_t cps;      // column chunks per split
+  int ntt;       // token tiles
+  int ks;        // column splits (1: no partial sums)
+  int64_t cps;   // column chunks per split
   float *part;      // [ks][n_slots][rows] partial sums when ks > 1
   int64_t n_slots;  // activation rows (plain) or slots (grouped)
 };
@@ -144,21 +144,27 @@ __device__ __forceinline__ void convert16(const Raw16<TYPE, TILED> &r, int64_t k
   }
 }
 
-// A work-group computes TR = 64 weight rows x TT = 16 activation rows; each
-// K-step of KC = 64 columns dequantizes the weight tile into LDS (4 threads
-// per row, 16 weights each; the next step's raw bytes are loaded meanwhile)
-// and stages the activation tile. Wave w then multiplies rows [16w, 16w+16)
-// by the 16 activation rows on the fp32 matrix cores (v_mfma_f32_16x16x4f32,
-// exact fp32 products, fp32 sums): MFMA s of the step takes column 16q + s
-// for lane quad q, so each lane reads its 16 values with four ds_read_b128.
-// blockIdx.z = ks * ntt + token tile: with split-K (a.ks > 1) the work-group
-// covers column chunks [ks*cps, (ks+1)*cps) and writes its partial sums to
-// a.part[ks][slot][r]; k_gemm_f32_reduce then adds the splits in ks order.
-template <int TYPE, int MODE>
+// A work-group computes TR = 64 weight rows x TN activation rows (TN = 16 for
+// batches below kLargeBatch rows, 64 from there: the weights are dequantized
+// once per TN rows). Each K-step of KC = 64 columns dequantizes
+// the weight tile into LDS (4 threads per row, 16 weights each; the raw bytes
+// of the next PF steps are in flight) and stages the activation tile. Wave w
+// then multiplies rows [16w, 16w+16) by the TN activation rows on the fp32
+// matrix cores (v_mfma_f32_16x16x4f32, exact fp32 products, fp32 sums): MFMA
+// s of the step takes column 16q + s for lane quad q, so each lane reads its
+// 16 values with four ds_read_b128. blockIdx.z = ks * ntt + token tile: with
+// split-K (ks > 1) the work-group covers column chunks [ks*cps, (ks+1)*cps)
+// and writes its partial sums to a.part[ks][slot][r]; k_gemm_f32_reduce then
+// adds the splits in ks order.
+constexpr int kLargeBatch = 256;  // batches from this size take the TN = 64 kernel
+
+template <int TYPE, int MODE, int TN>
 __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   constexpr bool TL = MODE != G_PLAIN;  // expert tier rows are tiled
+  constexpr int PF = TN == 16 ? 4 : 2;
+  constexpr int NX = TN / 16;  // activation float4 per thread and step; accumulator tiles per wave
   __shared__ __attribute__((aligned(16))) float Ws[TR][PAD];
-  __shared__ __attribute__((aligned(16))) float Xs[TT][PAD];
+  __shared__ __attribute__((aligned(16))) float Xs[TN][PAD];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t rows = a.rows, cols = a.cols;
@@ -181,12 +187,14 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
     if (!f32_regime(a.regime, n)) return;
     W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[MODE == G_GATE ? 0 : (MODE == G_UP ? 1 : 2)];
   }
-  const int tile = (int)(blockIdx.z % a.ntt), ks = (int)(blockIdx.z / a.ntt);
-  const int j0 = tile * TT;
+  const int ntt = a.ntt, ksn = a.ks;
+  const int64_t cps = a.cps;
+  const int tile = (int)(blockIdx.z % ntt), ks = (int)(blockIdx.z / ntt);
+  const int j0 = tile * TN;
   if (j0 >= n) return;
   const int64_t nchunk = cols / KC;
-  const int64_t c_begin = (int64_t)ks * a.cps;
-  const int64_t c_end = c_begin + a.cps < nchunk ? c_begin + a.cps : nchunk;
+  const int64_t c_begin = (int64_t)ks * cps;
+  const int64_t c_end = c_begin + cps < nchunk ? c_begin + cps : nchunk;
   if (c_begin >= c_end) return;
   const int64_t r0 = (int64_t)blockIdx.x * TR;
   const int64_t nb = cols / 256;
@@ -199,74 +207,110 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   };
 
   const int drow = tid >> 2, dpart = tid & 3;
-  const int xtok = tid >> 4, xcol = (tid & 15) * 4;
-  const bool xvalid = j0 + xtok < n;
-  const float *xrow = a.x + (xvalid ? act_row(j0 + xtok) : 0) * cols + xcol;
+  const int xcol = (tid & 15) * 4;
+  const float *xrow[NX];
+  bool xvalid[NX];
+#pragma unroll
+  for (int u = 0; u < NX; ++u) {
+    const int xt = (tid >> 4) + 16 * u;
+    xvalid[u] = j0 + xt < n;
+    xrow[u] = a.x + (xvalid[u] ? act_row(j0 + xt) : 0) * cols + xcol;
+  }
   const bool wvalid = r0 + drow < rows;
   const uint8_t *wrow = W + (wvalid ? r0 + drow : 0) * row_bytes;
 
-  Raw16<TYPE, TL> cur{}, nxt{};
-  float4 xc = make_float4(0.f, 0.f, 0.f, 0.f), xn = xc;
-  if (wvalid) cur = load16<TYPE, TL>(wrow, c_begin, dpart, nb);
-  if (xvalid) xc = *(const float4 *)(xrow + c_begin * KC);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // the raw bytes of the next PF column chunks are in flight (a ring of
+  // registers, refilled as each chunk is converted)
+  Raw16<TYPE, TL> raw[PF];
+  float4 xr[PF][NX];
+#pragma unroll
+  for (int d = 0; d < PF; ++d) {
+#pragma unroll
+    for (int u = 0; u < NX; ++u) xr[d][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c_begin + d < c_end) {
+      if (wvalid) raw[d] = load16<TYPE, TL>(wrow, c_begin + d, dpart, nb);
+#pragma unroll
+      for (int u = 0; u < NX; ++u)
+        if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (c_begin + d) * KC);
+    }
+  }
+  f32x4 acc[NX];
+#pragma unroll
+  for (int u = 0; u < NX; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float4 *wa = (const float4 *)&Ws[16 * wave + (lane & 15)][16 * (lane >> 4)];
-  const float4 *xb = (const float4 *)&Xs[lane & 15][16 * (lane >> 4)];
 
-  for (int64_t kc = c_begin; kc < c_end; ++kc) {
-    if (kc + 1 < c_end) {
-      if (wvalid) nxt = load16<TYPE, TL>(wrow, kc + 1, dpart, nb);
-      if (xvalid) xn = *(const float4 *)(xrow + (kc + 1) * KC);
-    }
-    float wv[16];
-    if (wvalid) {
-      convert16<TYPE, TL>(cur, kc, dpart, wv);
-    } else {
+  for (int64_t k0 = c_begin; k0 < c_end; k0 += PF) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) wv[i] = 0.0f;
-    }
-    float4 *wd = (float4 *)&Ws[drow][dpart * 16];
+    for (int d = 0; d < PF; ++d) {
+      const int64_t kc = k0 + d;
+      if (kc < c_end) {
+        float wv[16];
+        if (wvalid) {
+          convert16<TYPE, TL>(raw[d], kc, dpart, wv);
+        } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
-    *(float4 *)&Xs[xtok][xcol] = xc;
-    __syncthreads();
+          for (int i = 0; i < 16; ++i) wv[i] = 0.0f;
+        }
+        float4 xc[NX];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const float4 A = wa[m], B = xb[m];
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, acc, 0, 0, 0);
+        for (int u = 0; u < NX; ++u) xc[u] = xr[d][u];
+        if (kc + PF < c_end) {  // refill this slot with chunk kc + PF
+          if (wvalid) raw[d] = load16<TYPE, TL>(wrow, kc + PF, dpart, nb);
+#pragma unroll
+          for (int u = 0; u < NX; ++u)
+            if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (kc + PF) * KC);
+        }
+        float4 *wd = (float4 *)&Ws[drow][dpart * 16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+#pragma unroll
+        for (int u = 0; u < NX; ++u) *(float4 *)&Xs[(tid >> 4) + 16 * u][xcol] = xc[u];
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const float4 A = wa[m];
+#pragma unroll
+          for (int u = 0; u < NX; ++u) {
+            const float4 B = ((const float4 *)&Xs[16 * u + (lane & 15)][16 * (lane >> 4)])[m];
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, acc[u], 0, 0, 0);
+          }
+        }
+        __syncthreads();
+      }
     }
-    __syncthreads();
-    cur = nxt;
-    xc = xn;
   }
 
-  // lane holds rows 4*(lane/16) + v of the wave's 16, activation row lane%16
-  const int j = j0 + (lane & 15);
-  if (j >= n) return;
-  const int64_t slot = MODE == G_PLAIN ? (int64_t)j : p0 + j;
+  // lane holds rows 4*(lane/16) + v of the wave's 16, activation row
+  // 16u + lane%16 of the tile
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int64_t r = r0 + 16 * wave + 4 * (lane >> 4) + v;
-    if (r >= rows) continue;
-    const float y = acc[v];
-    if (a.ks > 1) {
-      a.part[((int64_t)ks * a.n_slots + slot) * rows + r] = y;
-    } else if constexpr (MODE == G_PLAIN || MODE == G_GATE || MODE == G_DOWN) {
-      a.out[slot * rows + r] = y;
-    } else {  // G_UP: SwiGLU with the gate value stored by G_GATE (transformer.rs:558)
-      float *o = a.out + slot * rows + r;
-      const float g = *o;
-      const float den = 1.0f + expf_cr(-g);
-      const float q = g / den;
-      *o = q * y;
+  for (int u = 0; u < NX; ++u) {
+    const int j = j0 + 16 * u + (lane & 15);
+    if (j >= n) continue;
+    const int64_t slot = MODE == G_PLAIN ? (int64_t)j : p0 + j;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t r = r0 + 16 * wave + 4 * (lane >> 4) + v;
+      if (r >= rows) continue;
+      const float y = acc[u][v];
+      if (ksn > 1) {
+        a.part[((int64_t)ks * a.n_slots + slot) * rows + r] = y;
+      } else if constexpr (MODE == G_PLAIN || MODE == G_GATE || MODE == G_DOWN) {
+        a.out[slot * rows + r] = y;
+      } else {  // G_UP: SwiGLU with the gate value stored by G_GATE (transformer.rs:558)
+        float *o = a.out + slot * rows + r;
+        const float g = *o;
+        const float den = 1.0f + expf_cr(-g);
+        const float q = g / den;
+        *o = q * y;
+      }
     }
   }
 }
 
-// Sum of the a.ks partial results in split order, then the mode's store.
+// Sum of a group's a.ks partial results in split order, then the mode's store.
 template <int MODE>
 __global__ void __launch_bounds__(256) k_gemm_f32_reduce(GArgs a) {
   const int64_t rows = a.rows;
@@ -311,16 +355,30 @@ int splits_for(int64_t rows, int64_t cols, int64_t groups) {
   return ks < 1 ? 1 : (int)ks;
 }
 
+// Launch shape: tile width TN, token tiles, splits, chunks per split.
+void shape_for(int64_t rows, int64_t cols, int groups, int64_t max_rows, int &tn, int &ntt, int &ks, int64_t &cps) {
+  tn = max_rows >= kLargeBatch ? 64 : 16;
+  ntt = (int)((max_rows + tn - 1) / tn);
+  ks = splits_for(rows, cols, (int64_t)groups * ntt);
+  const int64_t nchunk = cols / KC;
+  cps = (nchunk + ks - 1) / ks;
+}
+
 template <int MODE>
 hipError_t launch_type(hipStream_t st, int type, GArgs a, int64_t rows_x, int groups, int64_t max_rows,
                        int64_t part_floats) {
-  a.ntt = (int)((max_rows + TT - 1) / TT);
-  a.ks = splits_for(a.rows, a.cols, (int64_t)groups * a.ntt);
-  if ((int64_t)a.ks * a.n_slots * a.rows > part_floats || !a.part) a.ks = 1;
-  const int64_t nchunk = a.cols / KC;
-  a.cps = (nchunk + a.ks - 1) / a.ks;
+  int tn;
+  shape_for(a.rows, a.cols, groups, max_rows, tn, a.ntt, a.ks, a.cps);
+  if (!a.part || (int64_t)a.ks * a.n_slots * a.rows > part_floats) {
+    a.ks = 1;
+    a.cps = a.cols / KC;
+  }
   const dim3 grid((unsigned)rows_x, (unsigned)groups, (unsigned)(a.ntt * a.ks));
-#define KMOE_GEMM(TY) KMOE_LAUNCH((k_gemm_f32<TY, MODE>), grid, dim3(256), 0, st, a)
+#define KMOE_GEMM(TY)                                                               \
+  do {                                                                              \
+    if (tn == 16) KMOE_LAUNCH((k_gemm_f32<TY, MODE, 16>), grid, dim3(256), 0, st, a); \
+    else KMOE_LAUNCH((k_gemm_f32<TY, MODE, 64>), grid, dim3(256), 0, st, a);         \
+  } while (0)
   switch (type) {
     case T_Q4_K: KMOE_GEMM(T_Q4_K); break;
     case T_Q8_0: KMOE_GEMM(T_Q8_0); break;
@@ -340,8 +398,9 @@ hipError_t launch_type(hipStream_t st, int type, GArgs a, int64_t rows_x, int gr
 
 int64_t gemm_f32_part_floats(int64_t rows, int64_t cols, int64_t groups, int64_t max_rows, int64_t n_slots) {
   if (rows <= 0 || cols % KC != 0 || max_rows <= 0) return 0;
-  const int64_t ntt = (max_rows + TT - 1) / TT;
-  const int ks = splits_for(rows, cols, groups * ntt);
+  int tn, ntt, ks;
+  int64_t cps;
+  shape_for(rows, cols, (int)groups, max_rows, tn, ntt, ks, cps);
   return ks > 1 ? (int64_t)ks * n_slots * rows : 0;
 }
 
