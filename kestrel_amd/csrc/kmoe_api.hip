@@ -288,6 +288,15 @@ int ensure_ws(kmoe_ctx *c, size_t need) {
 }
 
 bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K || t == KMOE_Q8_0; }
+// The few-rows kernels for decode batches run unless KMOE_SMALL=0.
+bool small_enabled() {
+  static const bool on = [] {
+    const char *v = getenv("KMOE_SMALL");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 // K-quants take Q8_K activations (quant.rs:262-281); Q8_0 takes Q8 rows.
 bool is_kq(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K; }
 
@@ -1087,21 +1096,34 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
       goto done;
     }
   }
+  // Experts with a few rows on the int path (decode batches), tiled Q4_K:
+  // the few-rows kernels; experts with more rows take the kernels after them.
+  const bool small_ok = small_enabled() && S >= 2;
   // expert gate/up + SwiGLU (transformer.rs:551-558)
   if (any_int) {
     if (!x_quantized) {
       if (is_kq(gt)) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
     }
-    hipError_t e = hipErrorNotSupported;
-    if (mfma && gt == KMOE_Q4_K)
-      e = timed(c, "moe_gate_up_mfma", [&]() {
-        return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h);
+    int small_rows = 0;  // experts with 1..small_rows rows are done
+    if (small_ok && gt == KMOE_Q4_K && L->tiled[0] && small_supported(F, d, 0)) {
+      const hipError_t e = timed(c, "moe_gate_up_small", [&]() {
+        return launch_small(st, 0, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h);
       });
-    if (e != hipErrorNotSupported) HIP_OK(c, e);
-    else
-      LAUNCH(c, "moe_gate_up_int",
-             launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h));
+      if (e == hipSuccess) small_rows = small_rows_for(d, 0, S);
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (S > small_rows) {
+      hipError_t e = hipErrorNotSupported;
+      if (mfma && gt == KMOE_Q4_K)
+        e = timed(c, "moe_gate_up_mfma", [&]() {
+          return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h, small_rows + 1);
+        });
+      if (e != hipErrorNotSupported) HIP_OK(c, e);
+      else
+        LAUNCH(c, "moe_gate_up_int", launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd,
+                                                    w.xs, w.h, small_rows + 1));
+    }
   }
   if (any_f32) {
     LAUNCH(c, "moe_gate_f32",
@@ -1113,15 +1135,25 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   if (any_int) {
     LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
            launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
-    hipError_t e = hipErrorNotSupported;
-    if (mfma && dt == KMOE_Q4_K)
-      e = timed(c, "moe_down_mfma", [&]() {
-        return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y);
+    int small_rows = 0;
+    if (small_ok && dt == KMOE_Q4_K && L->tiled[2] && small_supported(d, F, 1)) {
+      const hipError_t e = timed(c, "moe_down_small", [&]() {
+        return launch_small(st, 1, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y);
       });
-    if (e != hipErrorNotSupported) HIP_OK(c, e);
-    else
-      LAUNCH(c, "moe_down_int",
-             launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
+      if (e == hipSuccess) small_rows = small_rows_for(F, 1, S);
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (S > small_rows) {
+      hipError_t e = hipErrorNotSupported;
+      if (mfma && dt == KMOE_Q4_K)
+        e = timed(c, "moe_down_mfma", [&]() {
+          return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y, small_rows + 1);
+        });
+      if (e != hipErrorNotSupported) HIP_OK(c, e);
+      else
+        LAUNCH(c, "moe_down_int", launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd,
+                                                 w.hs, w.y, small_rows + 1));
+    }
   }
   if (any_f32)
     LAUNCH(c, "moe_down_f32",

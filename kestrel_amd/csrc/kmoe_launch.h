@@ -125,9 +125,10 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
                              const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins);
 // Grouped MoE, int path: gate+up+SwiGLU -> h [slots, F] f32 (mode 0) or down -> y [slots, d] f32 (mode 1).
 // Experts handled: those whose row count the regime sends to the int path.
+// min_rows: experts with fewer rows are left to another kernel.
 hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
-                          const float *xd, const int32_t *xbs, float *out);
+                          const float *xd, const int32_t *xbs, float *out, int min_rows = 0);
 
 // ---- the whole single-token layer in one persistent kernel (kmoe_fused.hip):
 // Q4_K tiled experts; routing published into pub's arrays; sync: zeroed
@@ -147,12 +148,23 @@ bool moe_mfma_supported(int64_t rows, int64_t cols);
 // hipErrorNotSupported: shape or activation alignment (16 B) not covered.
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out);
+                           const int32_t *abs, float *out, int min_rows = 0);
 // Plain GGUF rows: out[s*rows + r], or, with sumi/mins set, the per-block
 // integer accumulators at [(s*rows + r)*nb + b] (ad unused).
 hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *aq,
                              const float *ad, const int32_t *abs, int64_t s_rows, float *out, int32_t *sumi,
                              int32_t *mins);
+
+// ---- few rows per expert (kmoe_small.hip): tiled Q4_K experts on the int
+// path with 1..small_rows_for() rows (0: the batch is too large for these
+// kernels). mode 0: gate/up + SwiGLU into h [slots, rows]; 1: down into y
+// [slots, rows]. hipErrorNotSupported for row widths outside
+// small_supported() or batches without a few-rows kernel.
+bool small_supported(int64_t rows, int64_t cols, int mode);
+int small_rows_for(int64_t cols, int mode, int64_t max_rows);
+hipError_t launch_small(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
+                        const Routing &rt, int regime, int max_active, int64_t max_rows, const int8_t *xq,
+                        const float *xd, const int32_t *xbs, float *out);
 
 // ---- f32 path (kmoe_gemm_f32.hip): dequantized weights x f32 activations
 // Partial-sum floats the launchers below use for this shape (0: no column

@@ -49,6 +49,7 @@ struct MvArgs {
   Routing rt;
   int regime;
   int rows_per_block;
+  int min_rows;  // grouped modes: experts with fewer rows are another kernel's
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -336,7 +337,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
     const int e = a.rt.active[i];
     p0 = a.rt.offsets[e];
     n = (int)(a.rt.offsets[e + 1] - p0);
-    if (!int_regime(a.regime, n)) return;
+    if (n < a.min_rows || !int_regime(a.regime, n)) return;
     const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
     if constexpr (MODE == M_GATE_UP) {
       W0 = eb + a.tier.off[0];
@@ -1236,7 +1237,7 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
 
 hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
-                          const float *xd, const int32_t *xbs, float *out) {
+                          const float *xd, const int32_t *xbs, float *out, int min_rows) {
   if (rows == 0 || max_active == 0) return hipSuccess;
   if (!act_fits(type, cols)) return hipErrorInvalidValue;
   MvArgs a{};
@@ -1249,6 +1250,7 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
   a.tier = tier;
   a.rt = rt;
   a.regime = regime;
+  a.min_rows = min_rows;
   a.rows_per_block = kRowsPerBlock;
   dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)max_active);
   // A single token routes at most one row to each expert: the NT=1 kernel.

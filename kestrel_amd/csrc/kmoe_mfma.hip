@@ -79,6 +79,7 @@ struct MfmaArgs {
   float *out;            // [slots or s_rows, rows]
   int32_t *sumi, *mins;  // MF_SUMS: [(s*rows + r)*nb + b]
   int regime;
+  int min_rows;          // grouped modes: experts with fewer rows are another kernel's
 };
 
 // One LDS stage (superblock b of the pass's 128 token rows):
@@ -161,7 +162,7 @@ __global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
       const int e = a.rt.active[i_act];
       p0 = a.rt.offsets[e];
       const int n = (int)(a.rt.offsets[e + 1] - p0);
-      if (!mfma_int_regime(a.regime, n)) return;
+      if (n < a.min_rows || !mfma_int_regime(a.regime, n)) return;
       W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[mat] + rr * row_bytes;
       t_begin = 0;
       t_end = n;
@@ -397,7 +398,7 @@ bool moe_mfma_supported(int64_t rows, int64_t cols) {
 
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out) {
+                           const int32_t *abs, float *out, int min_rows) {
   if (!moe_mfma_supported(rows, cols) || !aligned16(aq) || !aligned16(abs)) return hipErrorNotSupported;
   if (max_active == 0) return hipSuccess;
   MfmaArgs a{};
@@ -410,6 +411,7 @@ hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int
   a.abs = abs;
   a.out = out;
   a.regime = regime;
+  a.min_rows = min_rows;
   const int64_t rows_per_wg = 128;
   const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)max_active);
   if (mode == MF_GATE_UP) KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP>), grid, dim3(512), 0, st, a);

@@ -109,6 +109,22 @@ def test_mixtral_shape_decode_b1_q6k_down(ctx, orc):
     check(run_layer(ctx, orc, spec, 1, 0, seed=14))
 
 
+@pytest.mark.parametrize("d,S", [(4096, 2), (4096, 4), (4096, 8), (4096, 16), (8192, 3), (8192, 6)])
+def test_few_rows_per_expert_kernels(ctx, orc, d, S):
+    """Decode batches: experts with 1..8 rows (1..4 at hidden 8192, two tasks
+    per lane) take the register-resident few-rows kernels over tiled Q4_K
+    rows; experts with more rows take the matrix-core or LDS-staged kernels in
+    the same layer. Both int regimes (AVX2: rows < 4 only)."""
+    spec = LayerSpec(8, 2, d, 8192, Q4_K, seed=70 + S, quantized=False)
+    for regime in (0, 1):
+        check(run_layer(ctx, orc, spec, S, regime, seed=3200 + S))
+
+
+def test_few_rows_kernels_with_q6k_down(ctx, orc):
+    spec = LayerSpec(8, 2, 4096, 8192, Q4_K, seed=81, quantized=False, down_type=Q6_K)
+    check(run_layer(ctx, orc, spec, 6, 1, seed=3300))
+
+
 def test_qwen3_like_zipf_routing(ctx, orc):
     """Config 4 geometry (hidden 2048, FFN 768, 128 experts, top-8, Q4_K) with
     Zipf(1.1) load imbalance; activations offset by +1 carry the bias."""
