@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
                          "decode, Qwen3-shaped layer)")
+    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3",
+                    help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
+                         "q4k_m, qwen3)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -652,11 +655,16 @@ def main():
     }
     if a.prefill_tokens > 0:
         res["prefill"] = prefill_leg(ctx, torch, a)
-    if not a.no_extra:
+    legs = set() if a.no_extra else set(x for x in a.legs.split(",") if x)
+    if "batches" in legs:
         res["decode_batches"] = [batch_leg(ctx, torch, a.layers, S2, rg) for S2 in (8, 32) for rg in (0, 1)]
+    if "matvec_q4k" in legs:
         res["matvec_q4k"] = matvec_leg(ctx, torch, Q4_K)
+    if "matvec_q6k" in legs:
         res["matvec_q6k"] = matvec_leg(ctx, torch, Q6_K)
+    if "q4k_m" in legs:
         res["decode_b1_q4k_m"] = q4km_leg(ctx, torch)
+    if "qwen3" in legs:
         res["qwen3"] = qwen3_leg(ctx, torch)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)

@@ -15,6 +15,8 @@
 //     added lane-wise, hsum, then the tail.
 // hsum (avx2.rs:20-27) = ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)).
 // One lane per chain (16 lanes per logit); lane 0 of the 16 combines them.
+// Each chain reads its elements from LDS in the same order it would from
+// global memory (k_router_logits below).
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 #include "kmoe_logit.h"
@@ -31,14 +33,28 @@ __device__ __forceinline__ float hsum8(const float *v) {
   return (a + b) + (c + d);
 }
 
+// Work-group = one weight row e and up to kLgTok activation rows; 16 lanes per
+// logit as above (lanes of the second half-wave pair with the second row).
+// Columns are staged through LDS kLgCh at a time (a multiple of 16, so every
+// element stays in its chain and every chain keeps its order);
+// the chains read LDS, the tails past the last whole group of 8 (or 16) read
+// global memory.
+constexpr int kLgCh = 4096;  // one step for the routers of the shapes here (d <= 4096)
+constexpr int kLgTok = 2;
+
 __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__ W, int32_t E, int64_t d,
                                                        const float *__restrict__ X, int64_t S,
                                                        float *__restrict__ logits, int qdot) {
-  const int l16 = threadIdx.x & 15;
-  const int64_t pair = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool valid = pair < S * E;
-  const int64_t s = valid ? pair / E : 0;
-  const int e = valid ? (int)(pair % E) : 0;
+  __shared__ __attribute__((aligned(16))) float Wc[kLgCh];
+  __shared__ __attribute__((aligned(16))) float Xc[kLgTok][kLgCh];
+  const bool vec = d % 4 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
+  const int tid = threadIdx.x;
+  const int l16 = tid & 15, tok = tid >> 4;
+  const int e = (int)(blockIdx.x % (uint32_t)E);  // blocks: (token block, row) pairs
+  const int64_t s0 = (int64_t)(blockIdx.x / (uint32_t)E) * kLgTok;
+  const int ns = (int)(S - s0 < kLgTok ? S - s0 : kLgTok);
+  const bool valid = tok < ns;
+  const int64_t s = s0 + (valid ? tok : 0);
   int ord;
   if (qdot || S < 4 || (d % 8) != 0) {
     ord = ORD_QDOT;
@@ -51,31 +67,68 @@ __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__
   }
   const float *w = W + (int64_t)e * d;
   const float *x = X + s * d;
-  const int64_t n8 = d / 8;
+  const int64_t n8 = d / 8, n16 = d / 16;
+  const int l = l16 & 7;
+  const int off = l16 < 8 ? 0 : 8;
   float acc = 0.0f;
-  if (valid) {
-    if (ord == ORD_GEMM) {
-      if (l16 < 8) {
-#pragma unroll 8
-        for (int64_t c = 0; c < n8; ++c) acc = fmaf(w[8 * c + l16], x[8 * c + l16], acc);
+  for (int64_t c0 = 0; c0 < d; c0 += kLgCh) {
+    const int cw = (int)(d - c0 < kLgCh ? d - c0 : kLgCh);
+    __syncthreads();  // the previous chunk has been read
+    if (vec) {  // every 16-byte load of the chunk issued before any is stored
+      constexpr int Q = kLgCh / 4 / 256;
+      float4 rv[1 + kLgTok][Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int i = 4 * (q * 256 + tid);
+        rv[0][q] = i < cw ? *(const float4 *)(w + c0 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < kLgTok; ++t)
+          rv[1 + t][q] = i < cw && t < ns ? *(const float4 *)(X + (s0 + t) * d + c0 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-    } else if (ord == ORD_QDOT) {
-      if (l16 < 8) {
-#pragma unroll 8
-        for (int64_t c = 0; c < n8; ++c) {
-          const float p = w[8 * c + l16] * x[8 * c + l16];
-          acc = acc + p;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int i = 4 * (q * 256 + tid);
+        if (i < cw) {
+          *(float4 *)&Wc[i] = rv[0][q];
+#pragma unroll
+          for (int t = 0; t < kLgTok; ++t) *(float4 *)&Xc[t][i] = rv[1 + t][q];
         }
       }
     } else {
-      const int64_t n16 = d / 16;
-      const int l = l16 & 7;
-      const int64_t off = l16 < 8 ? 0 : 8;
+      for (int i = tid; i < cw; i += 256) Wc[i] = w[c0 + i];
+      for (int t = 0; t < ns; ++t)
+        for (int i = tid; i < cw; i += 256) Xc[t][i] = X[(s0 + t) * d + c0 + i];
+    }
+    __syncthreads();
+    if (!valid) continue;
+    if (ord == ORD_GEMM || ord == ORD_QDOT) {
+      if (l16 < 8) {
+        const int64_t cb = c0 / 8, ce = (c0 + cw) / 8 < n8 ? (c0 + cw) / 8 : n8;
+        if (ord == ORD_GEMM) {
 #pragma unroll 8
-      for (int64_t c = 0; c < n16; ++c) acc = fmaf(w[16 * c + off + l], x[16 * c + off + l], acc);
-      if (l16 < 8 && (d - 16 * n16) >= 8) acc = fmaf(w[16 * n16 + l], x[16 * n16 + l], acc);
+          for (int64_t c = cb; c < ce; ++c) {
+            const int o = (int)(8 * c - c0) + l16;
+            acc = fmaf(Wc[o], Xc[tok][o], acc);
+          }
+        } else {
+#pragma unroll 8
+          for (int64_t c = cb; c < ce; ++c) {
+            const int o = (int)(8 * c - c0) + l16;
+            const float p = Wc[o] * Xc[tok][o];
+            acc = acc + p;
+          }
+        }
+      }
+    } else {
+      const int64_t cb = c0 / 16, ce = (c0 + cw) / 16 < n16 ? (c0 + cw) / 16 : n16;
+#pragma unroll 8
+      for (int64_t c = cb; c < ce; ++c) {
+        const int o = (int)(16 * c - c0) + off + l;
+        acc = fmaf(Wc[o], Xc[tok][o], acc);
+      }
     }
   }
+  if (valid && ord == ORD_DOTF32 && l16 < 8 && (d - 16 * n16) >= 8) acc = fmaf(w[16 * n16 + l], x[16 * n16 + l], acc);
   // Gather the 16 chains of this logit in lane 0 of the group.
   float v[16];
   const int base = threadIdx.x & 63 & ~15;
@@ -468,10 +521,11 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
 
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
                                 int64_t s_rows, float *logits, bool qdot) {
-  const int64_t pairs = s_rows * n_expert;
-  if (pairs == 0) return hipSuccess;
-  KMOE_LAUNCH(k_router_logits, dim3((unsigned)((pairs + 15) / 16)), dim3(256), 0, st, router, n_expert, d, x,
-                     s_rows, logits, qdot ? 1 : 0);
+  if (s_rows * n_expert == 0) return hipSuccess;
+  const int64_t blocks = (s_rows + kLgTok - 1) / kLgTok * n_expert;
+  if (blocks > (int64_t)INT32_MAX) return hipErrorInvalidValue;
+  KMOE_LAUNCH(k_router_logits, dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x, s_rows, logits,
+                     qdot ? 1 : 0);
   return hipGetLastError();
 }
 
