@@ -54,10 +54,10 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
-                         "decode, Qwen3-shaped layer)")
-    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3",
+                         "decode, Qwen3-shaped layer, expert-tier preload)")
+    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload",
                     help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
-                         "q4k_m, qwen3)")
+                         "q4k_m, qwen3, preload)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -393,6 +393,60 @@ def q4km_leg(ctx, torch, layers: int = 4, seed: int = 2):
             "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def preload_leg(ctx, torch, reps: int = 3):
+    """Filling the HBM expert tier (ExpertStore::preload_all): one
+    Mixtral-shaped Q4_K_M layer (Q4_K gate/up, Q6_K down, 8 experts, 915 MB
+    of extents) preloaded from a model image in host memory, laid out as a
+    prepared KGUF (one copy per expert) and as a plain GGUF (three), from
+    pageable and from pinned memory, beside one plain pinned host-to-device
+    copy of the same bytes. Rates are expert bytes per second, PCIe included."""
+    import numpy as np
+
+    page, align = 4096, 32
+    au = lambda v, a: (v + a - 1) // a * a
+    s = [PART, PART, D * (FF // 256) * 210]
+    o = [0, au(s[0], align)]
+    o.append(au(o[1] + s[1], align))
+    stride = au(o[2] + s[2], page)
+    expert_bytes = E * sum(s)
+    pinned = torch.empty(E * stride, dtype=torch.uint8, pin_memory=True)
+    pinned.fill_(0x5A)
+    img = np.full(E * stride, 0x5A, np.uint8)
+    gguf_off = [0, E * s[0], E * (s[0] + s[1])]
+    lid = 300
+
+    def run(image, off, strides):
+        ctx.layer_create(lid, E, K, D, FF, Q4_K, Q4_K, Q6_K, True, 0.0)
+        try:
+            ts, copies = [], 0
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                copies = ctx.layer_preload(lid, image, off, strides)
+                ts.append(time.perf_counter() - t0)
+        finally:
+            ctx.layer_destroy(lid)
+        t = sorted(ts)[len(ts) // 2]
+        return {"copies": copies, "ms": round(t * 1e3, 2), "GBps": round(expert_bytes / t / 1e9, 2)}
+
+    out = {"expert_bytes": expert_bytes, "layout_stride": stride}
+    out["kgguf_pageable"] = run(img, [x for x in o], [stride] * 3)
+    out["gguf_pageable"] = run(img[:expert_bytes], gguf_off, s)
+    out["kgguf_pinned"] = run(pinned.numpy(), [x for x in o], [stride] * 3)
+    dst = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    ts = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dst.copy_(pinned, non_blocking=True)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[len(ts) // 2]
+    out["h2d_pinned_copy_GBps"] = round(E * stride / t / 1e9, 2)
+    del dst, pinned
+    torch.cuda.empty_cache()
+    return out
+
+
 def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
     """Qwen3-30B-A3B-shaped layer: hidden 2048, FFN 768, 128 experts, top-8,
     Q4_K random-init experts, router N(0, 0.02) plus a rank-1 Zipf(1.1) bias
@@ -666,6 +720,8 @@ def main():
         res["decode_b1_q4k_m"] = q4km_leg(ctx, torch)
     if "qwen3" in legs:
         res["qwen3"] = qwen3_leg(ctx, torch)
+    if "preload" in legs:
+        res["tier_preload"] = preload_leg(ctx, torch)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
         if a.prefill_tokens > 0:

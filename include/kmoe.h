@@ -186,13 +186,38 @@ int kmoe_layer_destroy(kmoe_ctx *ctx, uint32_t layer);
 int kmoe_router_upload(kmoe_ctx *ctx, uint32_t layer, const float *router, size_t bytes);
 /* ExpertStore::load/preload_all (expert.rs:251-303, :620-641): copy expert e's
  * part (0 gate, 1 up, 2 down) GGUF bytes from host memory. Q8_0 and F32 parts
- * are stored verbatim; Q4_K parts are stored as tiled rows (same size, the
- * 16-byte superblock heads first, then the nibble bytes regrouped so a wave's
- * loads are contiguous); kmoe_expert_read gives back the GGUF bytes. */
+ * are stored verbatim; Q4_K and Q6_K parts are stored as tiled rows (same
+ * size, regrouped so a wave's loads are contiguous), tiled on the device after
+ * a copy into the context's upload staging (or on the host when the VRAM
+ * budget leaves no room for it); kmoe_expert_read gives back the GGUF bytes. */
 int kmoe_expert_upload(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes, size_t len);
-/* Same from device memory (device-to-device copy, tiled on the device for Q4_K). */
+/* Same from device memory (device-to-device copy, tiled on the device). */
 int kmoe_expert_upload_dev(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void *bytes_dev,
                            size_t len);
+/* ExpertBuf as ExpertStore::load fills it (expert.rs:62-76, :293-303): one
+ * host buffer of len bytes holding expert e's file extents, part k (gate, up,
+ * down) at byte part_pos[k]. The whole buffer goes to the device in one
+ * host-to-device copy, then each part is placed into the tier on the device.
+ * The upload staging (device memory counted in the VRAM ledger, kept until
+ * kmoe_destroy) grows to the largest buffer seen; without room for it the
+ * parts are uploaded one by one. Synchronous; all three parts are resident
+ * on return. */
+int kmoe_expert_upload_buf(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, const void *buf, size_t len,
+                           const uint64_t part_pos[3]);
+/* ExpertStore::preload_all (expert.rs:620-641) over a mapped model image:
+ * every expert of the layer, part k of expert e at part_base[k] + e *
+ * part_stride[k] (TensorInfo::slice_offset, kestrel-gguf/src/lib.rs:187-189).
+ * A plain GGUF passes each stacked ffn_{gate,up,down}_exps tensor's data and
+ * its slice bytes; a prepared KGUF passes data offset + o_k and the shared
+ * stride, so an expert's three parts lie together. Per expert the three
+ * ranges are sorted and merged when less than 4096 bytes apart
+ * (ExpertStore::extents_of and coalesce, expert.rs:263-267,
+ * kestrel-model/src/lib.rs:323-336; the bytes between merged ranges are read
+ * too, so they must be readable), and each merged range is one host-to-device
+ * copy: 1 per expert for a KGUF, 3 for a plain GGUF. *copies (may be NULL)
+ * receives the number of copies. Synchronous. */
+int kmoe_layer_preload(kmoe_ctx *ctx, uint32_t layer, const void *const part_base[3], const uint64_t part_stride[3],
+                       uint64_t *copies);
 /* ExpertStore::is_ready (expert.rs:445): 1 when all three parts are resident, else 0. */
 int kmoe_expert_is_ready(kmoe_ctx *ctx, uint32_t layer, uint32_t expert);
 /* ExpertBuf::part (expert.rs:72-76): device pointer and length of a resident

@@ -6,6 +6,7 @@
 // anything is enqueued.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -105,6 +106,9 @@ struct kmoe_ctx {
   // workspace
   uint8_t *ws = nullptr;
   size_t ws_size = 0;
+  // device staging for host uploads of tiled parts and whole expert extents
+  uint8_t *stage = nullptr;
+  size_t stage_size = 0;
   // last moe_ffn routing (pointers into ws) and its sizes
   uint32_t *last_idx = nullptr, *last_perm = nullptr, *last_off = nullptr;
   float *last_w = nullptr;
@@ -287,6 +291,32 @@ int ensure_ws(kmoe_ctx *c, size_t need) {
   return KMOE_OK;
 }
 
+// Device staging for host uploads, grown to the largest request and kept until
+// kmoe_destroy (counted in the ledger). nullptr, with no error left behind,
+// when the budget or hipMalloc refuses it: callers then take the host route.
+uint8_t *staging(kmoe_ctx *c, size_t need) {
+  if (need <= c->stage_size) return c->stage;
+  const std::string keep = c->err;
+  if (c->stage) {
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return nullptr;
+    (void)hipFree(c->stage);
+    release(c, c->stage_size);
+    c->stage = nullptr;
+    c->stage_size = 0;
+  }
+  constexpr size_t kGrain = size_t(2) << 20;
+  const size_t sz = (need + kGrain - 1) / kGrain * kGrain;
+  void *p = nullptr;
+  if (dev_alloc(c, sz, &p, "upload staging")) {
+    (void)hipGetLastError();  // a failed hipMalloc must not surface at the next launch check
+    c->err = keep;
+    return nullptr;
+  }
+  c->stage = (uint8_t *)p;
+  c->stage_size = sz;
+  return c->stage;
+}
+
 bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K || t == KMOE_Q8_0; }
 // The few-rows kernels for decode batches run unless KMOE_SMALL=0.
 bool small_enabled() {
@@ -426,6 +456,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   }
   for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->stage) (void)hipFree(c->stage);
   if (c->counters) (void)hipFree(c->counters);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
@@ -777,6 +808,44 @@ int kmoe_router_upload(kmoe_ctx *c, uint32_t layer, const float *router, size_t 
   return KMOE_OK;
 }
 
+// Enqueue the placement of part `part` of expert e from device memory: a copy
+// for verbatim parts, the tiling kernel for Q4_K / Q6_K.
+static int place_from_device(kmoe_ctx *c, Layer *L, uint32_t e, int part, const uint8_t *src) {
+  uint8_t *dst = L->arena + e * L->expert_stride + L->part_off[part];
+  if (!L->tiled[part])
+    HIP_OK(c, hipMemcpyAsync(dst, src, L->part_len[part], hipMemcpyDeviceToDevice, c->stream));
+  else if (L->part_type[part] == KMOE_Q6_K)
+    HIP_OK(c, launch_tq6_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
+  else
+    HIP_OK(c, launch_tq4_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
+  return KMOE_OK;
+}
+
+// Enqueue the placement of a part from host memory. Verbatim parts go straight
+// into the tier; tiled parts go through the device staging and the tiling
+// kernel, or are tiled on the host when no staging can be had. Returns with
+// the stream synchronized only on the host-tiling route.
+static int place_from_host(kmoe_ctx *c, Layer *L, uint32_t e, int part, const uint8_t *src) {
+  const size_t len = L->part_len[part];
+  uint8_t *dst = L->arena + e * L->expert_stride + L->part_off[part];
+  if (!L->tiled[part]) {
+    HIP_OK(c, hipMemcpyAsync(dst, src, len, hipMemcpyHostToDevice, c->stream));
+    return KMOE_OK;
+  }
+  if (uint8_t *st = staging(c, len)) {
+    HIP_OK(c, hipMemcpyAsync(st, src, len, hipMemcpyHostToDevice, c->stream));
+    return place_from_device(c, L, e, part, st);
+  }
+  std::vector<uint8_t> t(len);
+  if (L->part_type[part] == KMOE_Q6_K)
+    tq6_convert_host(src, t.data(), L->part_rows[part], L->part_nb[part], true);
+  else
+    tq4_convert_host(src, t.data(), L->part_rows[part], L->part_nb[part], true);
+  HIP_OK(c, hipMemcpyAsync(dst, t.data(), len, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));  // t is released on return
+  return KMOE_OK;
+}
+
 static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, const void *bytes, size_t len,
                          bool from_device) {
   if (!c) return KMOE_E_INVALID;
@@ -786,27 +855,105 @@ static int expert_upload(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, 
   if (len != L->part_len[part] || !bytes)
     return fail(c, KMOE_E_INVALID, "expert part bytes %zu != %zu", len, L->part_len[part]);
   DeviceGuard g(c->device);
-  uint8_t *dst = L->arena + e * L->expert_stride + L->part_off[part];
-  if (!L->tiled[part]) {
-    HIP_OK(c, hipMemcpyAsync(dst, bytes, len, from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                             c->stream));
-  } else if (from_device) {
-    const uint8_t *src = (const uint8_t *)bytes;
-    if (L->part_type[part] == KMOE_Q6_K)
-      HIP_OK(c, launch_tq6_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
-    else
-      HIP_OK(c, launch_tq4_convert(c->stream, src, dst, L->part_rows[part], L->part_nb[part], true));
-  } else {
-    std::vector<uint8_t> t(len);
-    if (L->part_type[part] == KMOE_Q6_K)
-      tq6_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
-    else
-      tq4_convert_host((const uint8_t *)bytes, t.data(), L->part_rows[part], L->part_nb[part], true);
-    HIP_OK(c, hipMemcpyAsync(dst, t.data(), len, hipMemcpyHostToDevice, c->stream));
-    HIP_OK(c, hipStreamSynchronize(c->stream));  // t is released on return
-  }
+  const uint8_t *src = (const uint8_t *)bytes;
+  int rc = from_device ? place_from_device(c, L, e, part, src) : place_from_host(c, L, e, part, src);
+  if (rc) return rc;
   HIP_OK(c, hipStreamSynchronize(c->stream));
   L->loaded[e] |= (uint8_t)(1u << part);
+  return KMOE_OK;
+}
+
+int kmoe_expert_upload_buf(kmoe_ctx *c, uint32_t layer, uint32_t e, const void *buf, size_t len,
+                           const uint64_t part_pos[3]) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (e >= L->desc.n_expert || !buf || !part_pos) return fail(c, KMOE_E_INVALID, "expert %u buffer", e);
+  for (int k = 0; k < 3; ++k)
+    if (part_pos[k] > len || L->part_len[k] > len - part_pos[k])
+      return fail(c, KMOE_E_INVALID, "part %d at %llu + %zu bytes overruns the %zu-byte buffer", k,
+                  (unsigned long long)part_pos[k], L->part_len[k], len);
+  DeviceGuard g(c->device);
+  const uint8_t *host = (const uint8_t *)buf;
+  if (uint8_t *st = staging(c, len)) {
+    HIP_OK(c, hipMemcpyAsync(st, host, len, hipMemcpyHostToDevice, c->stream));
+    for (int k = 0; k < 3; ++k) {
+      int rc = place_from_device(c, L, e, k, st + part_pos[k]);
+      if (rc) return rc;
+    }
+  } else {
+    for (int k = 0; k < 3; ++k) {
+      int rc = place_from_host(c, L, e, k, host + part_pos[k]);
+      if (rc) return rc;
+    }
+  }
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  L->loaded[e] = 7;
+  return KMOE_OK;
+}
+
+namespace {
+struct HostRange {
+  uintptr_t start, end;
+};
+}  // namespace
+
+int kmoe_layer_preload(kmoe_ctx *c, uint32_t layer, const void *const part_base[3], const uint64_t part_stride[3],
+                       uint64_t *copies) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (!part_base || !part_stride || !part_base[0] || !part_base[1] || !part_base[2])
+    return fail(c, KMOE_E_INVALID, "need three part bases and strides");
+  constexpr uintptr_t kMergeGap = 4096;  // DIRECT_ALIGN: closer ranges are read as one
+  DeviceGuard g(c->device);
+  uint64_t n_copies = 0;
+  for (uint32_t e = 0; e < L->desc.n_expert; ++e) {
+    HostRange r[3];
+    for (int k = 0; k < 3; ++k) {
+      r[k].start = (uintptr_t)part_base[k] + (uintptr_t)e * part_stride[k];
+      r[k].end = r[k].start + L->part_len[k];
+    }
+    std::sort(r, r + 3, [](const HostRange &a, const HostRange &b) { return a.start < b.start; });
+    HostRange m[3];
+    int nm = 0;
+    for (int k = 0; k < 3; ++k) {
+      if (nm && r[k].start < m[nm - 1].end + kMergeGap) {
+        m[nm - 1].end = std::max(m[nm - 1].end, r[k].end);
+        continue;
+      }
+      m[nm++] = r[k];
+    }
+    size_t pos[3], need = 0;
+    for (int i = 0; i < nm; ++i) {
+      pos[i] = need;
+      need += align_up(m[i].end - m[i].start);
+    }
+    uint8_t *st = staging(c, need);
+    if (!st) {  // no room for the extents: part by part
+      for (int k = 0; k < 3; ++k) {
+        const uint8_t *src = (const uint8_t *)part_base[k] + (size_t)e * part_stride[k];
+        int rc = place_from_host(c, L, e, k, src);
+        if (rc) return rc;
+      }
+      n_copies += 3;
+      continue;
+    }
+    for (int i = 0; i < nm; ++i)
+      HIP_OK(c, hipMemcpyAsync(st + pos[i], (const void *)m[i].start, m[i].end - m[i].start,
+                               hipMemcpyHostToDevice, c->stream));
+    n_copies += nm;
+    for (int k = 0; k < 3; ++k) {
+      const uintptr_t s = (uintptr_t)part_base[k] + (uintptr_t)e * part_stride[k];
+      int i = 0;
+      while (!(s >= m[i].start && s + L->part_len[k] <= m[i].end)) ++i;
+      int rc = place_from_device(c, L, e, k, st + pos[i] + (s - m[i].start));
+      if (rc) return rc;
+    }
+  }
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  std::fill(L->loaded.begin(), L->loaded.end(), (uint8_t)7);
+  if (copies) *copies = n_copies;
   return KMOE_OK;
 }
 

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "libkmoe.so")
 
 F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
 REGIME_AVX2, REGIME_INT8, REGIME_EXACT = 0, 1, 2
-BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144)}
+BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 STATUS = {0: "OK", -1: "INVALID", -2: "UNSUPPORTED", -3: "BUDGET", -4: "HIP", -5: "NOT_LOADED"}
 
@@ -55,6 +55,8 @@ SIGNATURES = {
     "kmoe_router_upload": (C.c_int, [_P, _u32, _P, _sz]),
     "kmoe_expert_upload": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
     "kmoe_expert_upload_dev": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
+    "kmoe_expert_upload_buf": (C.c_int, [_P, _u32, _u32, _P, _sz, C.POINTER(_u64)]),
+    "kmoe_layer_preload": (C.c_int, [_P, _u32, C.POINTER(_P), C.POINTER(_u64), C.POINTER(_u64)]),
     "kmoe_expert_is_ready": (C.c_int, [_P, _u32, _u32]),
     "kmoe_expert_part": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_P), C.POINTER(_sz)]),
     "kmoe_expert_read": (C.c_int, [_P, _u32, _u32, _i32, _P, _sz]),
@@ -129,6 +131,7 @@ class Context:
         self.torch = torch
         self.lib = load_library()
         self.device = device
+        self._descs = {}  # layer -> (n_expert, part lengths)
         h = _P()
         rc = self.lib.kmoe_create(device, C.byref(h))
         if rc != 0:
@@ -255,9 +258,12 @@ class Context:
                      weights_scale=0.0):
         desc = MoeDesc(n_expert, n_used, int(norm_topk), weights_scale, d, ff, gate_type, up_type, down_type)
         self.check(self.lib.kmoe_layer_create(self.h, layer, C.byref(desc)))
+        self._descs[layer] = (n_expert, (bytes_for(gate_type, d) * ff, bytes_for(up_type, d) * ff,
+                                         bytes_for(down_type, ff) * d))
 
     def layer_destroy(self, layer: int):
         self.check(self.lib.kmoe_layer_destroy(self.h, layer))
+        self._descs.pop(layer, None)
 
     def router_upload(self, layer: int, router: np.ndarray):
         r = np.ascontiguousarray(router, dtype=np.float32)
@@ -270,6 +276,32 @@ class Context:
         else:  # torch device tensor
             self.check(self.lib.kmoe_expert_upload_dev(self.h, layer, e, part, _ptr(data),
                                                        data.numel() * data.element_size()))
+
+    def expert_upload_buf(self, layer: int, e: int, buf: np.ndarray, part_pos):
+        """ExpertBuf (expert.rs:62-76): one host buffer with the expert's
+        extents, part k at byte part_pos[k]; one host-to-device copy."""
+        b = np.ascontiguousarray(buf).view(np.uint8)
+        pos = (_u64 * 3)(*[int(p) for p in part_pos])
+        self.check(self.lib.kmoe_expert_upload_buf(self.h, layer, e, b.ctypes.data, b.nbytes, pos))
+
+    def layer_preload(self, layer: int, image: np.ndarray, part_off, part_stride) -> int:
+        """ExpertStore::preload_all (expert.rs:620-641) from a model image in
+        host memory (a mapped GGUF or KGUF): part k of expert e starts at byte
+        part_off[k] + e * part_stride[k] of `image`. Returns the number of
+        host-to-device copies (one per merged extent)."""
+        img = np.ascontiguousarray(image).view(np.uint8)
+        if layer not in self._descs:
+            raise ValueError(f"layer {layer} not created by this context")
+        n_expert, lens = self._descs[layer]
+        for k, n in enumerate(lens):
+            end = int(part_off[k]) + (n_expert - 1) * int(part_stride[k]) + n
+            if int(part_off[k]) < 0 or int(part_stride[k]) < 0 or end > img.nbytes:
+                raise ValueError(f"part {k}: expert extents end at {end} > image of {img.nbytes} bytes")
+        base = (_P * 3)(*[img.ctypes.data + int(o) for o in part_off])
+        stride = (_u64 * 3)(*[int(s) for s in part_stride])
+        copies = _u64()
+        self.check(self.lib.kmoe_layer_preload(self.h, layer, base, stride, C.byref(copies)))
+        return copies.value
 
     def expert_is_ready(self, layer: int, e: int) -> bool:
         return self.lib.kmoe_expert_is_ready(self.h, layer, e) == 1

@@ -93,3 +93,45 @@ class LayerSpec:
             ctx.expert_upload(layer, e, 0, self.gate[e])
             ctx.expert_upload(layer, e, 1, self.up[e])
             ctx.expert_upload(layer, e, 2, self.down[e])
+
+
+def _align(v: int, a: int) -> int:
+    return (v + a - 1) // a * a
+
+
+def expert_images(spec: "LayerSpec", seed: int = 0, align: int = 32, page: int = 4096):
+    """The layer's routed experts as the two file layouts hold them, each an
+    image of host bytes with junk in every gap, and (part offsets, strides):
+
+    - plain GGUF: three stacked tensors ffn_{gate,up,down}_exps, each at an
+      `align`-aligned offset, expert e's slice at offset + e * slice_bytes
+      (TensorInfo::slice_offset, kestrel-gguf/src/lib.rs:187-189);
+    - prepared KGUF: expert e is [gate_e | up_e | down_e] with each part
+      `align`-aligned inside the block and the block padded to a page; the
+      three tensors share that stride (kestrel-model/src/prepare.rs:118-131).
+    """
+    rng = np.random.default_rng(seed + 99)
+    parts = (spec.gate, spec.up, spec.down)
+    s = [len(p[0]) for p in parts]
+    E = spec.n_expert
+    # plain: a page of other tensors first, then the three stacked tensors
+    off = [page + 64]
+    for k in (1, 2):
+        off.append(_align(off[-1] + E * s[k - 1], align))
+    plain = rng.integers(0, 256, off[2] + E * s[2] + 100, dtype=np.uint8)
+    for k in range(3):
+        for e in range(E):
+            plain[off[k] + e * s[k]:off[k] + (e + 1) * s[k]] = parts[k][e]
+    plain_layout = (off, s)
+    # prepared: page-aligned group start, parts aligned inside a page-padded block
+    o = [0, _align(s[0], align)]
+    o.append(_align(o[1] + s[1], align))
+    stride = _align(o[2] + s[2], page)
+    start = 2 * page
+    kg = rng.integers(0, 256, start + E * stride, dtype=np.uint8)
+    for e in range(E):
+        for k in range(3):
+            b = start + e * stride + o[k]
+            kg[b:b + s[k]] = parts[k][e]
+    kg_layout = ([start + x for x in o], [stride] * 3)
+    return (plain, plain_layout), (kg, kg_layout)

@@ -325,6 +325,156 @@ def test_q6k_tier_layout_round_trip(ctx, d, ff):
         ctx.layer_destroy(96)
 
 
+def _tier_bytes(ctx, layer, E):
+    import ctypes
+
+    out = []
+    for e in range(E):
+        for k in range(3):
+            p, n = ctx.expert_part(layer, e, k)
+            raw = np.empty(n, np.uint8)
+            ctx.check(ctx.lib.kmoe_copy_d2h(ctx.h, raw.ctypes.data, ctypes.c_void_p(p), n))
+            out.append(raw)
+    return out
+
+
+def _ffn(ctx, layer, h):
+    return host(ctx.moe_ffn(layer, dev(h)))
+
+
+@pytest.mark.parametrize("wtype,down,d,ff", [(Q4_K, Q6_K, 512, 768), (Q8_0, Q8_0, 256, 512),
+                                             (Q6_K, Q4_K, 256, 1280)])
+def test_prepared_layout_preloads_identical_experts_in_one_copy(ctx, orc, wtype, down, d, ff):
+    """expert.rs:755-777: a prepared container serves the same experts as the
+    plain GGUF in one read per expert instead of three. Here the whole layer
+    is preloaded (preload_all) from both images: one host-to-device copy per
+    expert from the KGUF, three from the GGUF, and the tier, kmoe_expert_read
+    and the layer's output are identical to part-by-part uploads."""
+    from tests.helpers import expert_images
+
+    E = 8
+    spec = LayerSpec(E, 2, d, ff, wtype, seed=31, down_type=down)
+    (plain, (poff, pstride)), (kg, (koff, kstride)) = expert_images(spec, seed=31)
+    ids = (140, 141, 142)
+    spec.upload(ctx, ids[0])
+    try:
+        for lid in ids[1:]:
+            ctx.layer_create(lid, E, 2, d, ff, wtype, wtype, down)
+            ctx.router_upload(lid, spec.router)
+            assert not ctx.expert_is_ready(lid, 0)
+        assert ctx.layer_preload(ids[1], plain, poff, pstride) == 3 * E
+        assert ctx.layer_preload(ids[2], kg, koff, kstride) == E
+        want = _tier_bytes(ctx, ids[0], E)
+        for lid in ids[1:]:
+            assert all(ctx.expert_is_ready(lid, e) for e in range(E))
+            got = _tier_bytes(ctx, lid, E)
+            assert all(np.array_equal(a, b) for a, b in zip(got, want)), lid
+            for e in range(E):
+                for k, src in enumerate((spec.gate, spec.up, spec.down)):
+                    assert np.array_equal(ctx.expert_read(lid, e, k), src[e]), (lid, e, k)
+        h = orc.normal(8, 5 * d).reshape(5, d)
+        outs = [_ffn(ctx, lid, h) for lid in ids]
+        assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+        assert rel_l2(outs[2], spec.oracle_layer().moe_ffn(h, 0)) < TOL
+    finally:
+        for lid in ids:
+            ctx.layer_destroy(lid)
+
+
+@pytest.mark.parametrize("wtype,down", [(Q4_K, Q6_K), (Q8_0, Q4_K)])
+def test_expert_buffer_upload_one_copy(ctx, orc, wtype, down):
+    """ExpertBuf (expert.rs:62-76): the extents of one expert in one host
+    buffer, parts at arbitrary positions (odd ones included, as a head offset
+    inside an aligned read gives) and in file order rather than part order;
+    the tier holds what part-by-part uploads give."""
+    E, d, ff = 4, 256, 512
+    spec = LayerSpec(E, 2, d, ff, wtype, seed=41, down_type=down)
+    rng = np.random.default_rng(41)
+    spec.upload(ctx, 143)
+    ctx.layer_create(144, E, 2, d, ff, wtype, wtype, down)
+    ctx.router_upload(144, spec.router)
+    try:
+        for e in range(E):
+            g, u, dn = spec.gate[e], spec.up[e], spec.down[e]
+            pos_down = 4096 + 2 * e + 1
+            pos_gate = pos_down + len(dn) + 4000 + 3
+            pos_up = pos_gate + len(g) + 17
+            buf = rng.integers(0, 256, pos_up + len(u) + 4096, dtype=np.uint8)
+            buf[pos_gate:pos_gate + len(g)] = g
+            buf[pos_up:pos_up + len(u)] = u
+            buf[pos_down:pos_down + len(dn)] = dn
+            ctx.expert_upload_buf(144, e, buf, (pos_gate, pos_up, pos_down))
+            assert ctx.expert_is_ready(144, e)
+        want, got = _tier_bytes(ctx, 143, E), _tier_bytes(ctx, 144, E)
+        assert all(np.array_equal(a, b) for a, b in zip(got, want))
+        h = orc.normal(9, 3 * d).reshape(3, d)
+        assert np.array_equal(_ffn(ctx, 143, h), _ffn(ctx, 144, h))
+    finally:
+        ctx.layer_destroy(143)
+        ctx.layer_destroy(144)
+
+
+def test_uploads_without_room_for_staging_go_part_by_part(orc):
+    """With the VRAM budget (ledger.rs:75-102) too tight for the upload
+    staging, the uploads still succeed part by part (tiled on the host) and
+    stay within the budget: the staging is an optimisation, never an error."""
+    from kestrel_amd.kmoe import Context
+    from tests.helpers import expert_images
+
+    E, d, ff = 4, 256, 512
+    spec = LayerSpec(E, 2, d, ff, Q4_K, seed=51, down_type=Q6_K)
+    _, (kg, (koff, kstride)) = expert_images(spec, seed=51)
+    c = Context(0)
+    try:
+        base, _ = c.vram_usage()
+        c.layer_create(1, E, 2, d, ff, Q4_K, Q4_K, Q6_K)
+        after, _ = c.vram_usage()
+        c.vram_set_limit(after + 4096)
+        c.router_upload(1, spec.router)
+        assert c.layer_preload(1, kg, koff, kstride) == 3 * E
+        for e in range(E):
+            for k, src in enumerate((spec.gate, spec.up, spec.down)):
+                assert np.array_equal(c.expert_read(1, e, k), src[e]), (e, k)
+        buf = np.concatenate([spec.gate[0], spec.up[0], spec.down[0]])
+        c.expert_upload_buf(1, 0, buf, (0, len(spec.gate[0]), len(spec.gate[0]) + len(spec.up[0])))
+        c.expert_upload(1, 1, 2, spec.down[1])
+        assert c.vram_usage()[0] <= after + 4096
+        c.vram_set_limit(0)  # room for the moe_ffn workspace
+        h = orc.normal(10, 2 * d).reshape(2, d)
+        out = host(c.moe_ffn(1, dev(h)))
+        assert rel_l2(out, spec.oracle_layer().moe_ffn(h, 0)) < TOL
+        assert base < after
+    finally:
+        c.sync()
+        c.close()
+
+
+def test_extent_upload_errors(ctx):
+    import ctypes
+
+    from kestrel_amd.kmoe import KmoeError
+
+    ctx.layer_create(145, 4, 2, 256, 256, Q4_K, Q4_K, Q4_K)
+    try:
+        n = row_bytes(Q4_K, 256) * 256
+        buf = np.zeros(3 * n, np.uint8)
+        with pytest.raises(KmoeError) as e:  # part overruns the buffer
+            ctx.expert_upload_buf(145, 0, buf, (0, n, 2 * n + 1))
+        assert e.value.status == -1
+        with pytest.raises(KmoeError) as e:  # expert out of range
+            ctx.expert_upload_buf(145, 4, buf, (0, n, 2 * n))
+        assert e.value.status == -1
+        assert not ctx.expert_is_ready(145, 0)
+        with pytest.raises(ValueError):  # the image ends before expert 3's parts
+            ctx.layer_preload(145, np.zeros(4 * n, np.uint8), (0, n, 2 * n), (3 * n,) * 3)
+        strides = (ctypes.c_uint64 * 3)(n, n, n)
+        bases = (ctypes.c_void_p * 3)(buf.ctypes.data, None, buf.ctypes.data)
+        assert ctx.lib.kmoe_layer_preload(ctx.h, 145, bases, strides, None) == -1
+        assert ctx.lib.kmoe_layer_preload(ctx.h, 999, bases, strides, None) == -5
+    finally:
+        ctx.layer_destroy(145)
+
+
 def test_errors_map_to_status_codes(ctx):
     from kestrel_amd.kmoe import KmoeError
 
