@@ -12,6 +12,10 @@
  *   - ExpertStore's resident tier  (crates/kestrel-memory/src/expert.rs:223-641),
  *     as an HBM-resident expert tier with Tier::Vram accounting
  *     (crates/kestrel-memory/src/ledger.rs:10-14, :75)
+ *   - the rest of the decoder layer of Transformer::forward_chunk_inner
+ *     (transformer.rs:330-467, :591-631): embedding rows, RMSNorm, RoPE, the
+ *     f16 KV cache, causal GQA attention, dense SwiGLU; and greedy
+ *     sampler::argmax (crates/kestrel-engine/src/sampler.rs:104-112)
  *
  * Conventions
  *   - Every entry point returns a kmoe_status (0 = ok). On error the context
@@ -50,8 +54,8 @@ typedef enum {
 } kmoe_status;
 
 /* ggml type ids, kestrel-gguf types.rs:67-107. Kernels exist for F32
- * (router), Q8_0, Q4_K and Q6_K. */
-enum { KMOE_F32 = 0, KMOE_Q8_0 = 8, KMOE_Q4_K = 12, KMOE_Q6_K = 14 };
+ * (router), Q8_0, Q4_K and Q6_K; F16 for embedding rows. */
+enum { KMOE_F32 = 0, KMOE_F16 = 1, KMOE_Q8_0 = 8, KMOE_Q4_K = 12, KMOE_Q6_K = 14 };
 
 /* Arithmetic regime of the quantized matmuls (quant.rs:229-328).
  * KMOE_REGIME_AVX2 (default): the reference on an AVX2+FMA host. A matmul
@@ -253,6 +257,73 @@ int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_ro
  * idx/w [s_rows*k], perm [s_rows*k], offsets [n_expert+1]. */
 int kmoe_moe_last_routing(kmoe_ctx *ctx, uint32_t *idx_dev, float *w_dev, uint32_t *perm_dev,
                           uint32_t *offsets_dev);
+
+/* ---- The rest of the decoder layer (Transformer::forward_chunk_inner,
+ * transformer.rs:375-467) on device buffers, on the context's stream. ----
+ *
+ * Positions: row s of a call sits at position pos0 + s, plus *pos_dev when
+ * pos_dev (a device int32) is non-NULL. A decode step that reads its
+ * position from pos_dev can be captured once as a HIP graph and replayed;
+ * kmoe_argmax / kmoe_pos_advance move the counter on the device. With a
+ * host position, pos0 + s_rows > n_ctx fails with KMOE_E_INVALID ("context
+ * full", EngineError::ContextFull, transformer.rs:278-282); with a device
+ * position, rows past n_ctx are skipped by the kernels. A call that grows the
+ * context's decoder workspace (kmoe_get_rows, and kmoe_attention at a larger
+ * size) allocates: run one call of each size before capturing a graph. */
+
+/* quant::get_row (quant.rs:342-345) for the token embedding lookup
+ * (transformer.rs:381-389): out[s] = row ids[s] of the GGUF table
+ * [n_rows, cols] of type F32, F16, Q8_0, Q4_K or Q6_K, dequantized in
+ * dequant_row's expression order (bit-identical). ids are host token ids;
+ * an id >= n_rows fails with KMOE_E_INVALID ("token id out of range").
+ * Synchronous. */
+int kmoe_get_rows(kmoe_ctx *ctx, int32_t type, const void *table_dev, size_t table_len, int64_t n_rows,
+                  int64_t cols, const uint32_t *ids, int64_t s_rows, float *out_dev);
+/* Same with the ids on the device (a graph-captured decode step); an id
+ * >= n_rows gives a row of zeros. Asynchronous. */
+int kmoe_get_rows_dev(kmoe_ctx *ctx, int32_t type, const void *table_dev, size_t table_len, int64_t n_rows,
+                      int64_t cols, const uint32_t *ids_dev, int64_t s_rows, float *out_dev);
+/* Transformer::rmsnorm (transformer.rs:330-340) over rows of dim: out = x *
+ * (1 / sqrt(mean(x^2) + eps)) * w. When y_dev is non-NULL the residual add
+ * of forward_chunk_inner (transformer.rs:427, :463) comes first: x += y is
+ * stored in x and the norm is taken of the sum. out may be x. */
+int kmoe_rmsnorm(kmoe_ctx *ctx, float *x_dev, const float *y_dev, const float *w_dev, int64_t rows, int64_t dim,
+                 float eps, float *out_dev);
+/* Transformer::rope (transformer.rs:342-358), in place on x [s_rows,
+ * n_heads, head_dim]: pairs (i, i + rope_dim/2) when neox (every
+ * architecture but llama, transformer.rs:242), else (2i, 2i+1), rotated by
+ * position * inv_freq[i] (inv_freq [rope_dim/2] f32 on the device, built as
+ * at transformer.rs:216-226). */
+int kmoe_rope(kmoe_ctx *ctx, float *x_dev, int64_t s_rows, int32_t n_heads, int32_t head_dim, int32_t rope_dim,
+              int64_t pos0, const int32_t *pos_dev, const float *inv_freq_dev, int32_t neox);
+/* KV cache store (transformer.rs:411-418): k, v [s_rows, kv_width] f32 to
+ * f16 (round to nearest even, half::f16::from_f32) at rows position + s of
+ * the caches [n_ctx, kv_width]. */
+int kmoe_kv_store(kmoe_ctx *ctx, const float *k_dev, const float *v_dev, int64_t s_rows, int64_t kv_width,
+                  int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, uint16_t *k_cache_dev,
+                  uint16_t *v_cache_dev);
+/* Transformer::attention (transformer.rs:591-631): causal GQA for s_rows
+ * queries q [s_rows, n_head, head_dim] (after RoPE) over the f16 caches
+ * [n_ctx, n_kv * head_dim]; query s attends positions 0 ..= position(s),
+ * head h reads kv head h / (n_head / n_kv). out [s_rows, n_head * head_dim].
+ * Scores use quant::dot's summation order (bit-identical); the softmax is
+ * taken over chunks of 64 positions and merged, within 1e-6 relative of the
+ * reference's single pass. head_dim 64 or 128. */
+int kmoe_attention(kmoe_ctx *ctx, const float *q_dev, const uint16_t *k_cache_dev, const uint16_t *v_cache_dev,
+                   int64_t s_rows, int32_t n_head, int32_t n_kv, int32_t head_dim, int64_t pos0,
+                   const int32_t *pos_dev, int64_t n_ctx, float *out_dev);
+/* Dense SwiGLU (transformer.rs:455): out = g / (1 + exp(-g)) * u, n elements. */
+int kmoe_swiglu(kmoe_ctx *ctx, const float *gate_dev, const float *up_dev, int64_t n, float *out_dev);
+/* Bias rows (transformer.rs:394-401): x[r] += b for rows of cols. */
+int kmoe_add_rows(kmoe_ctx *ctx, float *x_dev, const float *b_dev, int64_t rows, int64_t cols);
+/* sampler::argmax (sampler.rs:104-112, greedy sampling): out_dev[0] = the
+ * first index of the largest of logits[0..n). When pos_dev is non-NULL,
+ * *pos_dev += advance afterwards (the end of a graph-captured decode step). */
+int kmoe_argmax(kmoe_ctx *ctx, const float *logits_dev, int64_t n, uint32_t *out_dev, int32_t *pos_dev,
+                int32_t advance);
+/* *pos_dev += by on the device (no counterpart: the position counter of
+ * graph-captured steps). */
+int kmoe_pos_advance(kmoe_ctx *ctx, int32_t *pos_dev, int32_t by);
 
 /* Per-kernel timing (0 = off): each kernel is launched with start/stop HIP
  * events taken from its own dispatch packet (hipExtLaunchKernelGGL), on the

@@ -109,6 +109,9 @@ struct kmoe_ctx {
   // device staging for host uploads of tiled parts and whole expert extents
   uint8_t *stage = nullptr;
   size_t stage_size = 0;
+  // decoder ops: attention partials and token ids copied from the host
+  uint8_t *dws = nullptr;
+  size_t dws_size = 0;
   // last moe_ffn routing (pointers into ws) and its sizes
   uint32_t *last_idx = nullptr, *last_perm = nullptr, *last_off = nullptr;
   float *last_w = nullptr;
@@ -291,6 +294,26 @@ int ensure_ws(kmoe_ctx *c, size_t need) {
   return KMOE_OK;
 }
 
+// Decoder-op workspace, grown on demand (a call that would grow it must not
+// be inside a graph capture: callers run one call of each size first).
+int ensure_dws(kmoe_ctx *c, size_t need) {
+  if (need <= c->dws_size) return KMOE_OK;
+  const size_t sz = align_up(need + need / 4);
+  if (c->dws) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    HIP_OK(c, hipFree(c->dws));
+    release(c, c->dws_size);
+    c->dws = nullptr;
+    c->dws_size = 0;
+  }
+  void *p = nullptr;
+  int rc = dev_alloc(c, sz, &p, "decoder workspace");
+  if (rc) return rc;
+  c->dws = (uint8_t *)p;
+  c->dws_size = sz;
+  return KMOE_OK;
+}
+
 // Device staging for host uploads, grown to the largest request and kept until
 // kmoe_destroy (counted in the ledger). nullptr, with no error left behind,
 // when the budget or hipMalloc refuses it: callers then take the host route.
@@ -457,6 +480,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
   if (c->ws) (void)hipFree(c->ws);
   if (c->stage) (void)hipFree(c->stage);
+  if (c->dws) (void)hipFree(c->dws);
   if (c->counters) (void)hipFree(c->counters);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
@@ -1344,6 +1368,160 @@ int kmoe_moe_last_routing(kmoe_ctx *c, uint32_t *idx, float *wv, uint32_t *perm,
   if (wv) HIP_OK(c, hipMemcpyAsync(wv, c->last_w, n * 4, hipMemcpyDeviceToDevice, c->stream));
   if (perm) HIP_OK(c, hipMemcpyAsync(perm, c->last_perm, n * 4, hipMemcpyDeviceToDevice, c->stream));
   if (off) HIP_OK(c, hipMemcpyAsync(off, c->last_off, (size_t)(c->last_E + 1) * 4, hipMemcpyDeviceToDevice, c->stream));
+  return KMOE_OK;
+}
+
+// ------------------------------------------------------------- the rest of the decoder layer
+
+static int check_table(kmoe_ctx *c, int32_t t, size_t table_len, int64_t n_rows, int64_t cols, int64_t *rb) {
+  if (t != KMOE_F32 && t != KMOE_F16 && t != KMOE_Q8_0 && t != KMOE_Q4_K && t != KMOE_Q6_K)
+    return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no row kernel", t);
+  *rb = t == KMOE_F16 ? 2 * cols : bytes_for(t, cols);
+  if (n_rows <= 0 || cols <= 0 || *rb < 0)
+    return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
+  if ((uint64_t)table_len < (uint64_t)*rb * (uint64_t)n_rows)
+    return fail(c, KMOE_E_INVALID, "table buffer %zu < %lld x %lld", table_len, (long long)n_rows, (long long)*rb);
+  return KMOE_OK;
+}
+
+int kmoe_get_rows(kmoe_ctx *c, int32_t t, const void *table, size_t table_len, int64_t n_rows, int64_t cols,
+                  const uint32_t *ids, int64_t s_rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  int64_t rb = 0;
+  int rc = check_table(c, t, table_len, n_rows, cols, &rb);
+  if (rc) return rc;
+  if (s_rows < 0) return fail(c, KMOE_E_INVALID, "negative size");
+  if (s_rows == 0) return KMOE_OK;
+  if (!table || !ids || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  for (int64_t s = 0; s < s_rows; ++s)
+    if (ids[s] >= (uint64_t)n_rows) return fail(c, KMOE_E_INVALID, "token id %u out of range", ids[s]);
+  DeviceGuard g(c->device);
+  rc = ensure_dws(c, (size_t)s_rows * 4);
+  if (rc) return rc;
+  uint32_t *ids_dev = (uint32_t *)c->dws;
+  HIP_OK(c, hipMemcpyAsync(ids_dev, ids, (size_t)s_rows * 4, hipMemcpyHostToDevice, c->stream));
+  LAUNCH(c, "get_rows", launch_get_rows(c->stream, t, (const uint8_t *)table, rb, n_rows, cols, ids_dev, s_rows, out));
+  HIP_OK(c, hipStreamSynchronize(c->stream));  // the ids buffer is reused by the next call
+  return KMOE_OK;
+}
+
+int kmoe_get_rows_dev(kmoe_ctx *c, int32_t t, const void *table, size_t table_len, int64_t n_rows, int64_t cols,
+                      const uint32_t *ids_dev, int64_t s_rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  int64_t rb = 0;
+  int rc = check_table(c, t, table_len, n_rows, cols, &rb);
+  if (rc) return rc;
+  if (s_rows < 0) return fail(c, KMOE_E_INVALID, "negative size");
+  if (s_rows == 0) return KMOE_OK;
+  if (!table || !ids_dev || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "get_rows", launch_get_rows(c->stream, t, (const uint8_t *)table, rb, n_rows, cols, ids_dev, s_rows, out));
+  return KMOE_OK;
+}
+
+int kmoe_rmsnorm(kmoe_ctx *c, float *x, const float *y, const float *w, int64_t rows, int64_t dim, float eps,
+                 float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (rows < 0 || dim <= 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  if (rows == 0) return KMOE_OK;
+  if (!x || !w || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "rmsnorm", launch_add_rmsnorm(c->stream, x, y, w, rows, dim, eps, out));
+  return KMOE_OK;
+}
+
+// Position checks shared by rope, kv_store and attention: with a host
+// position the rows must fit the context (EngineError::ContextFull,
+// transformer.rs:278-282); a device position is checked by the kernels.
+static int check_pos(kmoe_ctx *c, int64_t pos0, const int32_t *pos_dev, int64_t s_rows, int64_t n_ctx) {
+  if (pos0 < 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "negative position or size");
+  if (!pos_dev && n_ctx > 0 && pos0 + s_rows > n_ctx)
+    return fail(c, KMOE_E_INVALID, "context full: need %lld positions, n_ctx %lld", (long long)(pos0 + s_rows),
+                (long long)n_ctx);
+  return KMOE_OK;
+}
+
+int kmoe_rope(kmoe_ctx *c, float *x, int64_t s_rows, int32_t n_heads, int32_t head_dim, int32_t rope_dim,
+              int64_t pos0, const int32_t *pos_dev, const float *inv_freq, int32_t neox) {
+  if (!c) return KMOE_E_INVALID;
+  if (n_heads <= 0 || head_dim <= 0 || rope_dim <= 0 || rope_dim > head_dim || rope_dim % 2)
+    return fail(c, KMOE_E_INVALID, "rope: need 0 < rope_dim <= head_dim, rope_dim even");
+  int rc = check_pos(c, pos0, pos_dev, s_rows, 0);
+  if (rc) return rc;
+  if (s_rows == 0) return KMOE_OK;
+  if (!x || !inv_freq) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "rope", launch_rope(c->stream, x, s_rows, n_heads, head_dim, rope_dim, pos0, pos_dev, inv_freq, neox));
+  return KMOE_OK;
+}
+
+int kmoe_kv_store(kmoe_ctx *c, const float *k, const float *v, int64_t s_rows, int64_t kv_width, int64_t pos0,
+                  const int32_t *pos_dev, int64_t n_ctx, uint16_t *k_cache, uint16_t *v_cache) {
+  if (!c) return KMOE_E_INVALID;
+  if (kv_width <= 0 || n_ctx <= 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  int rc = check_pos(c, pos0, pos_dev, s_rows, n_ctx);
+  if (rc) return rc;
+  if (s_rows == 0) return KMOE_OK;
+  if (!k || !v || !k_cache || !v_cache) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "kv_store", launch_kv_store(c->stream, k, v, s_rows, kv_width, pos0, pos_dev, n_ctx, k_cache, v_cache));
+  return KMOE_OK;
+}
+
+int kmoe_attention(kmoe_ctx *c, const float *q, const uint16_t *k_cache, const uint16_t *v_cache, int64_t s_rows,
+                   int32_t n_head, int32_t n_kv, int32_t head_dim, int64_t pos0, const int32_t *pos_dev,
+                   int64_t n_ctx, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
+    return fail(c, KMOE_E_INVALID, "attention: need n_head %% n_kv == 0 and n_ctx > 0");
+  if (!attn_supported_hd(head_dim)) return fail(c, KMOE_E_UNSUPPORTED, "head_dim %d (kernels: 64, 128)", head_dim);
+  int rc = check_pos(c, pos0, pos_dev, s_rows, n_ctx);
+  if (rc) return rc;
+  if (s_rows == 0) return KMOE_OK;
+  if (!q || !k_cache || !v_cache || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  const int chunks = attn_chunks(pos_dev ? n_ctx : pos0 + s_rows);
+  rc = ensure_dws(c, (size_t)attn_part_floats(s_rows, n_head, head_dim, chunks) * 4);
+  if (rc) return rc;
+  LAUNCH(c, "attention", launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0,
+                                          pos_dev, n_ctx, chunks, (float *)c->dws, out));
+  return KMOE_OK;
+}
+
+int kmoe_swiglu(kmoe_ctx *c, const float *gate, const float *up, int64_t n, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (n < 0) return fail(c, KMOE_E_INVALID, "negative size");
+  if (n == 0) return KMOE_OK;
+  if (!gate || !up || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "swiglu", launch_swiglu(c->stream, gate, up, n, out));
+  return KMOE_OK;
+}
+
+int kmoe_add_rows(kmoe_ctx *c, float *x, const float *b, int64_t rows, int64_t cols) {
+  if (!c) return KMOE_E_INVALID;
+  if (rows < 0 || cols <= 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  if (rows == 0) return KMOE_OK;
+  if (!x || !b) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "add_rows", launch_add_rows(c->stream, x, b, rows, cols));
+  return KMOE_OK;
+}
+
+int kmoe_argmax(kmoe_ctx *c, const float *logits, int64_t n, uint32_t *out, int32_t *pos_dev, int32_t advance) {
+  if (!c) return KMOE_E_INVALID;
+  if (n <= 0) return fail(c, KMOE_E_INVALID, "argmax of an empty vector");
+  if (!logits || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "argmax", launch_argmax(c->stream, logits, n, out, pos_dev, advance));
+  return KMOE_OK;
+}
+
+int kmoe_pos_advance(kmoe_ctx *c, int32_t *pos_dev, int32_t by) {
+  if (!c) return KMOE_E_INVALID;
+  if (!pos_dev) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "pos_advance", launch_pos_advance(c->stream, pos_dev, by));
   return KMOE_OK;
 }
 

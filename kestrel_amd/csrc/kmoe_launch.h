@@ -27,7 +27,7 @@ extern thread_local LaunchTiming g_timing;
     }                                                                                                \
   } while (0)
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 // K-quants read Q8_K activations (256-blocks with 16-sums): Q4_K and Q6_K.
 constexpr bool is_kquant(int t) { return t == T_Q4_K || t == T_Q6_K; }
 enum { REGIME_AVX2 = 0, REGIME_INT8 = 1, REGIME_EXACT = 2 };
@@ -213,5 +213,31 @@ hipError_t launch_shared_add(hipStream_t st, float *out, const float *y, const f
 
 // out[s] = sum over the token's experts in ascending id of w * y[slot].
 hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out);
+
+
+// ---- the rest of the decoder layer (kmoe_decoder.hip) ----
+// Rows ids[0..s_rows) of a GGUF table [n_rows, cols] of type t (F32, F16,
+// Q8_0, Q4_K, Q6_K), dequantized to f32 out [s_rows, cols].
+hipError_t launch_get_rows(hipStream_t st, int t, const uint8_t *table, int64_t row_bytes, int64_t n_rows,
+                           int64_t cols, const uint32_t *ids, int64_t s_rows, float *out);
+hipError_t launch_add_rmsnorm(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
+                              float eps, float *out);
+hipError_t launch_rope(hipStream_t st, float *x, int64_t s_rows, int n_heads, int hd, int rd, int64_t pos0,
+                       const int32_t *pos_dev, const float *inv_freq, int neox);
+hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64_t s_rows, int64_t kvw,
+                           int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, uint16_t *kc, uint16_t *vc);
+// Chunks of 64 positions covering n_max positions, and the partials' size.
+int attn_chunks(int64_t n_max);
+int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int chunks);
+bool attn_supported_hd(int hd);
+hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
+                            int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int chunks,
+                            float *part, float *out);
+hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, int64_t n, float *out);
+hipError_t launch_add_rows(hipStream_t st, float *x, const float *b, int64_t rows, int64_t cols);
+// argmax of l[0..n) into out[0]; pos_dev (may be null) += advance afterwards.
+hipError_t launch_argmax(hipStream_t st, const float *l, int64_t n, uint32_t *out, int32_t *pos_dev,
+                         int32_t advance);
+hipError_t launch_pos_advance(hipStream_t st, int32_t *pos_dev, int32_t by);
 
 }  // namespace kmoe

@@ -15,9 +15,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkmoe.so")
 
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
 REGIME_AVX2, REGIME_INT8, REGIME_EXACT = 0, 1, 2
-BLOCK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 STATUS = {0: "OK", -1: "INVALID", -2: "UNSUPPORTED", -3: "BUDGET", -4: "HIP", -5: "NOT_LOADED"}
 
@@ -66,6 +66,16 @@ SIGNATURES = {
     "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
     "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
+    "kmoe_get_rows": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
+    "kmoe_get_rows_dev": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
+    "kmoe_rmsnorm": (C.c_int, [_P, _P, _P, _P, _i64, _i64, _f, _P]),
+    "kmoe_rope": (C.c_int, [_P, _P, _i64, _i32, _i32, _i32, _i64, _P, _P, _i32]),
+    "kmoe_kv_store": (C.c_int, [_P, _P, _P, _i64, _i64, _i64, _P, _i64, _P, _P]),
+    "kmoe_attention": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i64, _P, _i64, _P]),
+    "kmoe_swiglu": (C.c_int, [_P, _P, _P, _i64, _P]),
+    "kmoe_add_rows": (C.c_int, [_P, _P, _P, _i64, _i64]),
+    "kmoe_argmax": (C.c_int, [_P, _P, _i64, _P, _P, _i32]),
+    "kmoe_pos_advance": (C.c_int, [_P, _P, _i32]),
     "kmoe_profile_enable": (C.c_int, [_P, C.c_int]),
     "kmoe_profile_read": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(_i64)]),
 }
@@ -188,6 +198,67 @@ class Context:
         self.check(self.lib.kmoe_matmul(self.h, t, _ptr(w), w.numel() * w.element_size(), rows, cols, _ptr(x),
                                         x.shape[0], _ptr(out)))
         return out
+
+    # ------------------------------------------------ rest of the decoder layer
+    def get_rows(self, t: int, table, n_rows: int, cols: int, ids, out=None):
+        """quant::get_row for token ids (host sequence, or a device uint32/int32 tensor)."""
+        if hasattr(ids, "data_ptr"):
+            s_rows = ids.numel()
+            out = self._empty((s_rows, cols), self.torch.float32) if out is None else out
+            self.check(self.lib.kmoe_get_rows_dev(self.h, t, _ptr(table), table.numel() * table.element_size(),
+                                                  n_rows, cols, _ptr(ids), s_rows, _ptr(out)))
+            return out
+        a = np.ascontiguousarray(ids, dtype=np.uint32).reshape(-1)
+        out = self._empty((a.size, cols), self.torch.float32) if out is None else out
+        self.check(self.lib.kmoe_get_rows(self.h, t, _ptr(table), table.numel() * table.element_size(), n_rows,
+                                          cols, a.ctypes.data, a.size, _ptr(out)))
+        return out
+
+    def rmsnorm(self, x, w, eps: float, y=None, out=None):
+        """Transformer::rmsnorm over the last axis of x; with y, x += y first (in place)."""
+        dim = w.numel()
+        out = self.torch.empty_like(x) if out is None else out
+        self.check(self.lib.kmoe_rmsnorm(self.h, _ptr(x), _ptr(y), _ptr(w), x.numel() // dim, dim, eps, _ptr(out)))
+        return out
+
+    def rope(self, x, n_heads: int, head_dim: int, rope_dim: int, pos0: int, inv_freq, neox: bool, pos_dev=None):
+        """Transformer::rope in place on x [S, n_heads*head_dim]."""
+        s_rows = x.numel() // (n_heads * head_dim)
+        self.check(self.lib.kmoe_rope(self.h, _ptr(x), s_rows, n_heads, head_dim, rope_dim, pos0, _ptr(pos_dev),
+                                      _ptr(inv_freq), int(neox)))
+        return x
+
+    def kv_store(self, k, v, kv_width: int, pos0: int, n_ctx: int, k_cache, v_cache, pos_dev=None):
+        s_rows = k.numel() // kv_width
+        self.check(self.lib.kmoe_kv_store(self.h, _ptr(k), _ptr(v), s_rows, kv_width, pos0, _ptr(pos_dev), n_ctx,
+                                          _ptr(k_cache), _ptr(v_cache)))
+
+    def attention(self, q, k_cache, v_cache, n_head: int, n_kv: int, head_dim: int, pos0: int, n_ctx: int,
+                  pos_dev=None, out=None):
+        """Transformer::attention: q [S, n_head*head_dim] -> [S, n_head*head_dim]."""
+        s_rows = q.numel() // (n_head * head_dim)
+        out = self._empty((s_rows, n_head * head_dim), self.torch.float32) if out is None else out
+        self.check(self.lib.kmoe_attention(self.h, _ptr(q), _ptr(k_cache), _ptr(v_cache), s_rows, n_head, n_kv,
+                                           head_dim, pos0, _ptr(pos_dev), n_ctx, _ptr(out)))
+        return out
+
+    def swiglu(self, g, u, out=None):
+        out = self.torch.empty_like(g) if out is None else out
+        self.check(self.lib.kmoe_swiglu(self.h, _ptr(g), _ptr(u), g.numel(), _ptr(out)))
+        return out
+
+    def add_rows(self, x, b):
+        cols = b.numel()
+        self.check(self.lib.kmoe_add_rows(self.h, _ptr(x), _ptr(b), x.numel() // cols, cols))
+        return x
+
+    def argmax(self, logits, out=None, pos_dev=None, advance: int = 0):
+        out = self._empty((1,), self.torch.int32) if out is None else out
+        self.check(self.lib.kmoe_argmax(self.h, _ptr(logits), logits.numel(), _ptr(out), _ptr(pos_dev), advance))
+        return out
+
+    def pos_advance(self, pos_dev, by: int = 1):
+        self.check(self.lib.kmoe_pos_advance(self.h, _ptr(pos_dev), by))
 
     def quantize_q8k(self, x):
         S, n = x.shape

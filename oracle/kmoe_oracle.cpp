@@ -279,6 +279,9 @@ int64_t orc_bytes_for(int t, int64_t n) {  // types.rs:184-191
 
 float orc_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
 uint16_t orc_f32_to_f16(float f) { return f32_to_f16(f); }
+void orc_f32_to_f16_n(const float *x, uint16_t *out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = f32_to_f16(x[i]);
+}
 
 // ---------------------------------------------------------------------------
 // Generators
@@ -1280,6 +1283,109 @@ int orc_shared_expert_add(const orc_shared_expert *S, const float *h, size_t s_r
     }
   }
   return 0;
+}
+
+// ---------------------------------------------------------------------------
+// The rest of the decoder layer, transformer.rs:216-226, 330-467, 591-631
+
+void orc_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float eps, float *out) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float *xi = x + r * dim;
+    float ss = -0.0f;  // Rust's float Sum starts from -0.0 and adds in order
+    for (size_t j = 0; j < dim; ++j) {
+      float p = xi[j] * xi[j];
+      ss = ss + p;
+    }
+    ss = ss / (float)dim;
+    const float rr = 1.0f / std::sqrt(ss + eps);
+    for (size_t j = 0; j < dim; ++j) {
+      float t = xi[j] * rr;
+      out[r * dim + j] = t * w[j];
+    }
+  }
+}
+
+void orc_rope_inv_freq(float base, size_t rope_dim, const float *freqs, float *inv_freq) {
+  for (size_t i = 0; i < rope_dim / 2; ++i) {
+    const float e = -(2.0f * (float)i) / (float)rope_dim;
+    inv_freq[i] = powf(base, e);
+    if (freqs) inv_freq[i] = inv_freq[i] / freqs[i];
+  }
+}
+
+void orc_rope(float *x, size_t s_rows, size_t n_heads, size_t hd, size_t rd, size_t pos0, const float *inv_freq,
+              int neox) {
+  for (size_t s = 0; s < s_rows; ++s) {
+    const float p = (float)(pos0 + s);
+    for (size_t h = 0; h < n_heads; ++h) {
+      float *v = x + (s * n_heads + h) * hd;
+      for (size_t i = 0; i < rd / 2; ++i) {
+        const float ang = p * inv_freq[i];
+        const float sn = sinf(ang), cs = cosf(ang);
+        const size_t a = neox ? i : 2 * i, b = neox ? i + rd / 2 : 2 * i + 1;
+        const float x0 = v[a], x1 = v[b];
+        float t0 = x0 * cs, t1 = x1 * sn;
+        v[a] = t0 - t1;
+        t0 = x0 * sn;
+        t1 = x1 * cs;
+        v[b] = t0 + t1;
+      }
+    }
+  }
+}
+
+void orc_attention(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t s_rows, size_t nh,
+                   size_t nkv, size_t hd, size_t pos0, float *out) {
+  const size_t group = nh / nkv, kvw = nkv * hd, n_tot = pos0 + s_rows;
+  const float scale = 1.0f / std::sqrt((float)hd);
+  std::vector<float> kf(n_tot * kvw), vf(n_tot * kvw);
+  for (size_t i = 0; i < n_tot * kvw; ++i) {
+    kf[i] = f16_to_f32(k_cache[i]);
+    vf[i] = f16_to_f32(v_cache[i]);
+  }
+  std::vector<float> scores;
+  for (size_t i = 0; i < s_rows * nh; ++i) {
+    const size_t s = i / nh, h = i % nh, kvh = h / group, n = pos0 + s + 1;
+    const float *qv = q + (s * nh + h) * hd;
+    float *o = out + i * hd;
+    for (size_t j = 0; j < hd; ++j) o[j] = 0.0f;
+    scores.assign(n, 0.0f);
+    float m = -INFINITY;
+    for (size_t p = 0; p < n; ++p) {
+      scores[p] = orc_quant_dot(qv, kf.data() + p * kvw + kvh * hd, hd) * scale;
+      m = std::max(m, scores[p]);  // f32::max over the fold, NaN-free inputs
+    }
+    float sum = 0.0f;
+    for (size_t p = 0; p < n; ++p) {
+      scores[p] = expf(scores[p] - m);
+      sum = sum + scores[p];
+    }
+    const float inv = 1.0f / sum;
+    for (size_t p = 0; p < n; ++p) {
+      const float w = scores[p] * inv;
+      const float *vr = vf.data() + p * kvw + kvh * hd;
+      for (size_t j = 0; j < hd; ++j) {
+        float t = w * vr[j];
+        o[j] = o[j] + t;
+      }
+    }
+  }
+}
+
+void orc_swiglu(const float *g, const float *u, size_t n, float *out) {
+  for (size_t i = 0; i < n; ++i) {
+    const float gv = g[i];
+    const float den = 1.0f + expf(-gv);
+    const float t = gv / den;
+    out[i] = t * u[i];
+  }
+}
+
+uint32_t orc_argmax(const float *l, size_t n) {
+  size_t best = 0;
+  for (size_t i = 1; i < n; ++i)
+    if (l[i] > l[best]) best = i;
+  return (uint32_t)best;
 }
 
 // ---------------------------------------------------------------------------

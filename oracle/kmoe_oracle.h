@@ -54,6 +54,7 @@ int64_t orc_bytes_for(int t, int64_t n); /* -1 if n is not a multiple of the blo
 /* ---- f16 (half 2.7.1 semantics: exact IEEE conversion) ---- */
 float orc_f16_to_f32(uint16_t h);
 uint16_t orc_f32_to_f16(float f); /* round to nearest even */
+void orc_f32_to_f16_n(const float *x, uint16_t *out, size_t n); /* half::f16::from_f32 per element */
 
 /* ---- deterministic generators ---- */
 /* splitmix64 -> uniform in (0,1) -> Box-Muller in double -> float */
@@ -154,6 +155,27 @@ typedef struct {
  * the three products are quant::matmul over all s_rows rows (Transformer::mm). */
 int orc_shared_expert_add(const orc_shared_expert *S, const float *h, size_t s_rows, float *out, int regime,
                           int threads);
+
+/* ---- the rest of the decoder layer, transformer.rs:216-226, 330-467, 591-631 ---- */
+/* Transformer::rmsnorm (transformer.rs:330-340): per row of dim, the sum of
+ * squares in order, r = 1/sqrt(ss/dim + eps), out = x * r * w. */
+void orc_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float eps, float *out);
+/* RoPE frequencies (transformer.rs:216-226): inv_freq[i] = base^(-(2i)/rope_dim),
+ * divided by freqs[i] when freqs (rope_freqs.weight) is non-NULL. */
+void orc_rope_inv_freq(float base, size_t rope_dim, const float *freqs, float *inv_freq);
+/* Transformer::rope (transformer.rs:342-358), in place on x [s_rows, n_heads, head_dim]:
+ * row s at position pos0 + s; pairs (i, i + rope_dim/2) when neox, else (2i, 2i+1). */
+void orc_rope(float *x, size_t s_rows, size_t n_heads, size_t head_dim, size_t rope_dim, size_t pos0,
+              const float *inv_freq, int neox);
+/* Transformer::attention (transformer.rs:591-631): causal GQA for s_rows queries
+ * q [s_rows, n_head, head_dim] at positions pos0.., over the f16 caches
+ * [>= pos0 + s_rows, n_kv * head_dim]; out [s_rows, n_head * head_dim]. */
+void orc_attention(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t s_rows, size_t n_head,
+                   size_t n_kv, size_t head_dim, size_t pos0, float *out);
+/* Dense SwiGLU (transformer.rs:455): out = g / (1 + exp(-g)) * u. */
+void orc_swiglu(const float *g, const float *u, size_t n, float *out);
+/* sampler::argmax (sampler.rs:104-112): the first index of the largest value. */
+uint32_t orc_argmax(const float *l, size_t n);
 
 /* ---- bench_gemv, quant.rs:348-368: weight bytes per second ---- */
 double orc_bench_gemv(int t, size_t rows, size_t cols, size_t iters, int threads);

@@ -106,6 +106,13 @@ def lib():
             "orc_dispatch": (None, [_P, _sz, C.c_int, C.c_int, _P, _P]),
             "orc_moe_ffn": (C.c_int, [C.POINTER(MoeLayer), _P, _sz, _P, C.c_int, C.c_int]),
             "orc_shared_expert_add": (C.c_int, [C.POINTER(SharedExpert), _P, _sz, _P, C.c_int, C.c_int]),
+            "orc_f32_to_f16_n": (None, [_P, _P, _sz]),
+            "orc_rmsnorm": (None, [_P, _P, _sz, _sz, C.c_float, _P]),
+            "orc_rope_inv_freq": (None, [C.c_float, _sz, _P, _P]),
+            "orc_rope": (None, [_P, _sz, _sz, _sz, _sz, _sz, _P, C.c_int]),
+            "orc_attention": (None, [_P, _P, _P, _sz, _sz, _sz, _sz, _sz, _P]),
+            "orc_argmax": (C.c_uint32, [_P, _sz]),
+            "orc_swiglu": (None, [_P, _P, _sz, _P]),
             "orc_bench_gemv": (C.c_double, [C.c_int, _sz, _sz, _sz, C.c_int]),
             "orc_hw_threads": (C.c_int, []),
         }
@@ -331,3 +338,171 @@ def bench_gemv(t: int, rows: int, cols: int, iters: int, threads: int = 0) -> fl
 
 def hw_threads() -> int:
     return lib().orc_hw_threads()
+
+
+# ---------------------------------------------------------------- decoder layer
+def f16_store(x: np.ndarray) -> np.ndarray:
+    """half::f16::from_f32 per element (the KV cache store): uint16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Transformer::rmsnorm (transformer.rs:330-340) over the last axis."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    dim = w.size
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), _p(w), x.size // dim, dim, eps, _p(out))
+    return out
+
+
+def rope_inv_freq(base: float, rope_dim: int, freqs=None) -> np.ndarray:
+    out = np.empty(rope_dim // 2, np.float32)
+    f = None if freqs is None else np.ascontiguousarray(freqs, dtype=np.float32)
+    lib().orc_rope_inv_freq(base, rope_dim, None if f is None else _p(f), _p(out))
+    return out
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, rope_dim: int, pos0: int, inv_freq: np.ndarray,
+         neox: bool) -> np.ndarray:
+    """Transformer::rope (transformer.rs:342-358) on a copy of x [S, n_heads*head_dim]."""
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    S = y.size // (n_heads * head_dim)
+    f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    lib().orc_rope(_p(y), S, n_heads, head_dim, rope_dim, pos0, _p(f), int(neox))
+    return y
+
+
+def attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, n_head: int, n_kv: int, head_dim: int,
+              pos0: int) -> np.ndarray:
+    """Transformer::attention (transformer.rs:591-631); caches are uint16 f16
+    bits [positions, n_kv*head_dim] holding at least pos0 + S rows."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    S = q.size // (n_head * head_dim)
+    kc = np.ascontiguousarray(k_cache, dtype=np.uint16)
+    vc = np.ascontiguousarray(v_cache, dtype=np.uint16)
+    assert kc.size >= (pos0 + S) * n_kv * head_dim and vc.size == kc.size
+    out = np.empty((S, n_head * head_dim), np.float32)
+    lib().orc_attention(_p(q), _p(kc), _p(vc), S, n_head, n_kv, head_dim, pos0, _p(out))
+    return out
+
+
+def argmax(logits: np.ndarray) -> int:
+    l = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    return int(lib().orc_argmax(_p(l), l.size))
+
+
+def swiglu(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.empty_like(g)
+    lib().orc_swiglu(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+class Transformer:
+    """Transformer::forward (transformer.rs:278-302, 375-467) restated over
+    the oracle's kernels, for parity tests of whole decode stacks.
+
+    hp: arch ("llama" rotates pairs (2i, 2i+1), the others (i, i + rd/2)),
+    n_layer, n_embd, n_head, n_head_kv, head_dim, rope_dim, rope_freq_base,
+    rms_eps, n_ctx, n_batch; MoE models add n_expert, n_expert_used,
+    norm_topk, weights_scale. tensors: GGUF name -> (ggml type, dims with the
+    contiguous dimension first, uint8 bytes)."""
+
+    def __init__(self, hp: dict, tensors: dict, regime: int = REGIME_AVX2, threads: int = 0):
+        self.hp, self.t, self.regime, self.threads = hp, tensors, regime, threads
+        self.d, self.nh, self.nkv, self.hd = hp["n_embd"], hp["n_head"], hp["n_head_kv"], hp["head_dim"]
+        self.neox = hp["arch"] != "llama"
+        self.n_ctx = hp["n_ctx"]
+        freqs = self.vec("rope_freqs.weight") if "rope_freqs.weight" in tensors else None
+        self.inv_freq = rope_inv_freq(hp["rope_freq_base"], hp["rope_dim"], freqs)
+        kvw = self.nkv * self.hd
+        self.k_cache = [np.zeros((self.n_ctx, kvw), np.uint16) for _ in range(hp["n_layer"])]
+        self.v_cache = [np.zeros((self.n_ctx, kvw), np.uint16) for _ in range(hp["n_layer"])]
+        self.cached = 0
+        self.moe = {}
+        for l in range(hp["n_layer"]):
+            p = f"blk.{l}."
+            if p + "ffn_gate_exps.weight" not in tensors:
+                continue
+            E = hp["n_expert"]
+            parts = []
+            for name in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"):
+                ty, dims, b = tensors[p + name + ".weight"]
+                parts.append((ty, np.split(np.ascontiguousarray(b, dtype=np.uint8), E)))
+            ff = tensors[p + "ffn_gate_exps.weight"][1][1]
+            router = self.vec(p + "ffn_gate_inp.weight").reshape(E, self.d)
+            self.moe[l] = Layer(E, hp["n_expert_used"], self.d, ff, parts[0][0], parts[1][0], parts[2][0], router,
+                                parts[0][1], parts[1][1], parts[2][1], hp.get("norm_topk", True),
+                                hp.get("weights_scale", 0.0))
+
+    def vec(self, name: str) -> np.ndarray:
+        ty, dims, b = self.t[name]
+        return dequant(ty, b, int(np.prod(dims)))
+
+    def mm(self, name: str, x: np.ndarray) -> np.ndarray:
+        ty, dims, b = self.t[name]
+        return matmul(ty, b, int(np.prod(dims[1:])), dims[0], x, self.regime, self.threads)
+
+    def forward(self, tokens) -> np.ndarray:
+        tokens = list(tokens)
+        if not tokens:
+            raise ValueError("forward() needs at least one token")
+        if self.cached + len(tokens) > self.n_ctx:
+            raise ValueError("context full")
+        n_batch = max(1, self.hp.get("n_batch", 512))
+        logits = None
+        for i in range(0, len(tokens), n_batch):
+            logits = self._chunk(tokens[i:i + n_batch])
+        return logits
+
+    def _chunk(self, tokens) -> np.ndarray:
+        hp, d, nh, nkv, hd = self.hp, self.d, self.nh, self.nkv, self.hd
+        S, pos0, eps = len(tokens), self.cached, hp["rms_eps"]
+        ety, edims, eb = self.t["token_embd.weight"]
+        rb = bytes_for(ety, d)
+        x = np.empty((S, d), np.float32)
+        for s, tok in enumerate(tokens):
+            if tok >= edims[1]:
+                raise ValueError(f"token id {tok} out of range")
+            x[s] = dequant(ety, eb[tok * rb:(tok + 1) * rb], d)
+        kvw = nkv * hd
+        for l in range(hp["n_layer"]):
+            p = f"blk.{l}."
+            h = rmsnorm(x, self.vec(p + "attn_norm.weight"), eps)
+            q, k, v = (self.mm(p + f"attn_{n}.weight", h) for n in ("q", "k", "v"))
+            for n, y in (("q", q), ("k", k), ("v", v)):
+                if p + f"attn_{n}.bias" in self.t:
+                    y += self.vec(p + f"attn_{n}.bias")[None, :]
+            if p + "attn_q_norm.weight" in self.t:
+                q = rmsnorm(q.reshape(-1, hd), self.vec(p + "attn_q_norm.weight"), eps).reshape(S, nh * hd)
+            if p + "attn_k_norm.weight" in self.t:
+                k = rmsnorm(k.reshape(-1, hd), self.vec(p + "attn_k_norm.weight"), eps).reshape(S, kvw)
+            q = rope(q, nh, hd, hp["rope_dim"], pos0, self.inv_freq, self.neox)
+            k = rope(k, nkv, hd, hp["rope_dim"], pos0, self.inv_freq, self.neox)
+            self.k_cache[l][pos0:pos0 + S] = f16_store(k)
+            self.v_cache[l][pos0:pos0 + S] = f16_store(v)
+            ctx = attention(q, self.k_cache[l], self.v_cache[l], nh, nkv, hd, pos0)
+            x = x + self.mm(p + "attn_output.weight", ctx)
+            h = rmsnorm(x, self.vec(p + "ffn_norm.weight"), eps)
+            if l in self.moe:
+                y = self.moe[l].moe_ffn(h, self.regime, self.threads)
+                if p + "ffn_gate_shexp.weight" in self.t:
+                    ts = [self.t[p + f"ffn_{n}_shexp.weight"] for n in ("gate", "up", "down")]
+                    gi = self.vec(p + "ffn_gate_inp_shexp.weight") if p + "ffn_gate_inp_shexp.weight" in self.t \
+                        else None
+                    y = shared_expert_add(y, h, d, ts[0][1][1], [t[0] for t in ts], ts[0][2], ts[1][2], ts[2][2],
+                                          gi, self.regime, self.threads)
+            else:
+                g = self.mm(p + "ffn_gate.weight", h)
+                u = self.mm(p + "ffn_up.weight", h)
+                y = self.mm(p + "ffn_down.weight", swiglu(g, u))
+            x = x + y
+        self.cached += S
+        normed = rmsnorm(x[S - 1:S], self.vec("output_norm.weight"), eps)
+        head = "output.weight" if "output.weight" in self.t else "token_embd.weight"
+        return self.mm(head, normed)[0]

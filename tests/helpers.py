@@ -135,3 +135,71 @@ def expert_images(spec: "LayerSpec", seed: int = 0, align: int = 32, page: int =
             kg[b:b + s[k]] = parts[k][e]
     kg_layout = ([start + x for x in o], [stride] * 3)
     return (plain, plain_layout), (kg, kg_layout)
+
+
+def decoder_model(arch: str = "llama", n_layer: int = 2, d: int = 256, nh: int = 4, nkv: int = 2, hd: int = 64,
+                  ff: int = 512, vocab: int = 1000, n_ctx: int = 256, n_batch: int = 512, moe: dict | None = None,
+                  wtype: int = Q4_K, embed_type: int = Q8_0, head_type: int | None = Q6_K, bias: bool = False,
+                  qk_norm: bool = False, shared_ff: int = 0, seed: int = 0, rope_dim: int | None = None):
+    """A small decoder as kestrel's Transformer reads it: (hp, tensors) with
+    GGUF names, tensors = name -> (ggml type, dims with the contiguous
+    dimension first, bytes). Weights are the oracle's quantization of
+    seeded normals; norms are 1 + N(0, 0.1). head_type None ties the output
+    to the embedding. moe = dict(n_expert, n_expert_used, norm_topk,
+    weights_scale, types=(gate, up, down))."""
+    from oracle import pyoracle as orc
+
+    s = [seed * 1000 + 1]
+
+    def normal(n, std=1.0, mean=0.0):
+        s[0] += 1
+        return orc.normal(s[0], n, mean, std)
+
+    def mat(t, rows, cols, std):
+        return (t, [cols, rows], orc.quantize(t, normal(rows * cols, std).reshape(rows, cols)))
+
+    def f32(v, dims):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        return (F32, list(dims), v.view(np.uint8).reshape(-1))
+
+    hp = dict(arch=arch, n_layer=n_layer, n_embd=d, n_head=nh, n_head_kv=nkv, head_dim=hd,
+              rope_dim=rope_dim or hd, rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=n_ctx, n_batch=n_batch)
+    T = {"token_embd.weight": mat(embed_type, vocab, d, 1.0),
+         "output_norm.weight": f32(1.0 + normal(d, 0.1), [d])}
+    if head_type is not None:
+        T["output.weight"] = mat(head_type, vocab, d, 0.05)
+    if moe:
+        hp.update(n_expert=moe["n_expert"], n_expert_used=moe["n_expert_used"],
+                  norm_topk=moe.get("norm_topk", True), weights_scale=moe.get("weights_scale", 0.0))
+    for l in range(n_layer):
+        p = f"blk.{l}."
+        T[p + "attn_norm.weight"] = f32(1.0 + normal(d, 0.1), [d])
+        T[p + "ffn_norm.weight"] = f32(1.0 + normal(d, 0.1), [d])
+        T[p + "attn_q.weight"] = mat(wtype, nh * hd, d, 0.08)
+        T[p + "attn_k.weight"] = mat(wtype, nkv * hd, d, 0.08)
+        T[p + "attn_v.weight"] = mat(wtype, nkv * hd, d, 0.05)
+        T[p + "attn_output.weight"] = mat(wtype, d, nh * hd, 0.05)
+        if bias:
+            for n, w in (("q", nh * hd), ("k", nkv * hd), ("v", nkv * hd)):
+                T[p + f"attn_{n}.bias"] = f32(normal(w, 0.1), [w])
+        if qk_norm:
+            T[p + "attn_q_norm.weight"] = f32(1.0 + normal(hd, 0.1), [hd])
+            T[p + "attn_k_norm.weight"] = f32(1.0 + normal(hd, 0.1), [hd])
+        if moe:
+            E = moe["n_expert"]
+            tg, tu, tdn = moe.get("types", (wtype, wtype, wtype))
+            T[p + "ffn_gate_inp.weight"] = f32(normal(E * d, 0.05), [d, E])
+            for n, t, rows, cols in (("gate", tg, ff, d), ("up", tu, ff, d), ("down", tdn, d, ff)):
+                b = np.concatenate([orc.quantize(t, normal(rows * cols, 0.03).reshape(rows, cols))
+                                    for _ in range(E)])
+                T[p + f"ffn_{n}_exps.weight"] = (t, [cols, rows, E], b)
+            if shared_ff:
+                T[p + "ffn_gate_shexp.weight"] = mat(wtype, shared_ff, d, 0.03)
+                T[p + "ffn_up_shexp.weight"] = mat(wtype, shared_ff, d, 0.03)
+                T[p + "ffn_down_shexp.weight"] = mat(Q8_0, d, shared_ff, 0.03)
+                T[p + "ffn_gate_inp_shexp.weight"] = f32(normal(d, 0.05), [d])
+        else:
+            T[p + "ffn_gate.weight"] = mat(wtype, ff, d, 0.03)
+            T[p + "ffn_up.weight"] = mat(wtype, ff, d, 0.03)
+            T[p + "ffn_down.weight"] = mat(wtype, d, ff, 0.03)
+    return hp, T

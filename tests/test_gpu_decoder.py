@@ -1,0 +1,260 @@
+"""The rest of the decoder layer on the GPU (include/kmoe.h decoder ops and
+kestrel_amd.decoder) against the oracle's restatement of
+Transformer::forward (transformer.rs:278-302, 330-467, 591-631)."""
+import numpy as np
+import pytest
+
+from tests.helpers import F32, Q4_K, Q6_K, Q8_0, decoder_model, random_blocks, rel_l2, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+F16 = 1
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+
+    from kestrel_amd.kmoe import Context
+
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    c = Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("t,cols", [(F32, 96), (F16, 64), (Q8_0, 320), (Q4_K, 512), (Q6_K, 768)])
+def test_get_rows_bit_exact(ctx, orc, t, cols):
+    rng = np.random.default_rng(t + cols)
+    n_rows = 50
+    if t == F32:
+        table = rng.standard_normal(n_rows * cols).astype(np.float32).view(np.uint8)
+    elif t == F16:
+        table = rng.standard_normal(n_rows * cols).astype(np.float16).view(np.uint8)
+    else:
+        table = random_blocks(t, n_rows, cols, seed=t)
+    rb = table.size // n_rows
+    ids = [0, 49, 7, 7, 23]
+    got = host(ctx.get_rows(t, dev(table), n_rows, cols, ids))
+    ref = np.stack([orc.dequant(t, table[i * rb:(i + 1) * rb], cols) for i in ids])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    import torch
+
+    got_dev = host(ctx.get_rows(t, dev(table), n_rows, cols, torch.tensor(ids, dtype=torch.int32).cuda()))
+    assert np.array_equal(got_dev.view(np.uint32), ref.view(np.uint32))
+
+
+def test_get_rows_rejects_out_of_range_ids(ctx):
+    from kestrel_amd.kmoe import KmoeError
+
+    table = dev(np.zeros(10 * 34, np.uint8))
+    with pytest.raises(KmoeError) as e:  # EngineError "token id out of range" (transformer.rs:384-386)
+        ctx.get_rows(Q8_0, table, 10, 32, [3, 10])
+    assert e.value.status == -1
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 4096), (7, 2048), (64, 128)])
+def test_rmsnorm_with_residual(ctx, orc, rows, dim):
+    rng = np.random.default_rng(rows)
+    x = (rng.standard_normal((rows, dim)) * 2).astype(np.float32)
+    y = rng.standard_normal((rows, dim)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    got = host(ctx.rmsnorm(dev(x), dev(w), 1e-5))
+    assert rel_l2(got, orc.rmsnorm(x, w, 1e-5)) < 1e-6
+    xd = dev(x)
+    got = host(ctx.rmsnorm(xd, dev(w), 1e-5, y=dev(y)))
+    assert np.array_equal(host(xd), x + y)  # the residual add is stored
+    assert rel_l2(got, orc.rmsnorm(x + y, w, 1e-5)) < 1e-6
+    ctx.rmsnorm(xd, dev(w), 1e-5, out=xd)  # in place
+    assert rel_l2(host(xd), orc.rmsnorm(x + y, w, 1e-5)) < 1e-6
+
+
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("nh,hd,rd,S,pos0", [(8, 128, 128, 1, 0), (4, 64, 32, 9, 1000), (2, 128, 64, 3, 70000)])
+def test_rope(ctx, orc, neox, nh, hd, rd, S, pos0):
+    import torch
+
+    rng = np.random.default_rng(nh * S)
+    x = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    f = orc.rope_inv_freq(10000.0, rd)
+    ref = orc.rope(x, nh, hd, rd, pos0, f, neox)
+    got = host(ctx.rope(dev(x), nh, hd, rd, pos0, dev(f), neox))
+    assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max())
+    pos = torch.tensor([pos0 - 1], dtype=torch.int32).cuda()
+    got2 = host(ctx.rope(dev(x), nh, hd, rd, 1, dev(f), neox, pos_dev=pos))  # device position + pos0
+    assert np.array_equal(got2, got)
+
+
+def test_kv_store_bit_exact_at_host_and_device_positions(ctx, orc):
+    import torch
+
+    rng = np.random.default_rng(3)
+    kvw, n_ctx = 256, 40
+    k = (rng.standard_normal((5, kvw)) * 100).astype(np.float32)
+    v = rng.standard_normal((5, kvw)).astype(np.float32)
+    kc = torch.zeros((n_ctx, kvw), dtype=torch.int16).cuda()
+    vc = torch.zeros_like(kc)
+    ctx.kv_store(dev(k), dev(v), kvw, 10, n_ctx, kc, vc)
+    pos = torch.tensor([30], dtype=torch.int32).cuda()
+    ctx.kv_store(dev(k[:2]), dev(v[:2]), kvw, 0, n_ctx, kc, vc, pos_dev=pos)
+    K, V = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    assert np.array_equal(K[10:15], orc.f16_store(k)) and np.array_equal(V[10:15], orc.f16_store(v))
+    assert np.array_equal(K[30:32], orc.f16_store(k[:2]))
+    assert not K[:10].any() and not K[15:30].any() and not K[32:].any()
+    from kestrel_amd.kmoe import KmoeError
+
+    with pytest.raises(KmoeError):  # EngineError::ContextFull (transformer.rs:280-282)
+        ctx.kv_store(dev(k), dev(v), kvw, 36, n_ctx, kc, vc)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,S,pos0", [(8, 8, 64, 1, 0), (8, 2, 64, 1, 63), (8, 2, 128, 1, 64),
+                                              (32, 8, 128, 1, 200), (16, 4, 128, 37, 0), (4, 1, 64, 20, 50),
+                                              (16, 2, 128, 1, 1023)])
+def test_attention(ctx, orc, nh, nkv, hd, S, pos0):
+    import torch
+
+    rng = np.random.default_rng(nh + S + pos0)
+    n_ctx = 1024
+    kvw = nkv * hd
+    kc = orc.f16_store(rng.standard_normal((n_ctx, kvw)) * 2)
+    vc = orc.f16_store(rng.standard_normal((n_ctx, kvw)))
+    q = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    ref = orc.attention(q, kc, vc, nh, nkv, hd, pos0)
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    got = host(ctx.attention(dev(q), kd, vd, nh, nkv, hd, pos0, n_ctx))
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    pos = torch.tensor([pos0], dtype=torch.int32).cuda()
+    got2 = host(ctx.attention(dev(q), kd, vd, nh, nkv, hd, 0, n_ctx, pos_dev=pos))
+    assert np.abs(got2 - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_swiglu_add_rows_argmax(ctx, orc):
+    rng = np.random.default_rng(9)
+    g = (rng.standard_normal(5000) * 4).astype(np.float32)
+    u = rng.standard_normal(5000).astype(np.float32)
+    got = host(ctx.swiglu(dev(g), dev(u)))
+    ref = orc.swiglu(g, u)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    x = rng.standard_normal((3, 40)).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    assert np.array_equal(host(ctx.add_rows(dev(x), dev(b))), x + b)
+    for l in (np.array([1, 3, 3, 2], np.float32), np.array([0, np.nan, 5, 5], np.float32),
+              np.array([np.nan, 1, 2], np.float32), rng.standard_normal(151936).astype(np.float32),
+              np.full(70000, -1.0, np.float32)):
+        assert int(host(ctx.argmax(dev(l)))[0]) == orc.argmax(l)
+
+
+MODELS = {
+    "llama_dense": dict(arch="llama", n_layer=2, d=256, nh=4, nkv=2, hd=64, ff=512, vocab=1000),
+    "llama_dense_tied_q8": dict(arch="llama", n_layer=2, d=256, nh=4, nkv=4, hd=64, ff=512, vocab=700,
+                                wtype=Q8_0, head_type=None, embed_type=Q4_K, rope_dim=32),
+    "qwen3moe": dict(arch="qwen3moe", n_layer=2, d=512, nh=8, nkv=2, hd=64, ff=256, vocab=900, qk_norm=True,
+                     moe=dict(n_expert=8, n_expert_used=2, types=(Q4_K, Q4_K, Q6_K))),
+    "qwen2moe_shared_bias": dict(arch="qwen2moe", n_layer=2, d=256, nh=4, nkv=2, hd=64, ff=256, vocab=800,
+                                 bias=True, shared_ff=512, moe=dict(n_expert=8, n_expert_used=4)),
+    "mixtral_like_hd128": dict(arch="llama", n_layer=2, d=512, nh=4, nkv=2, hd=128, ff=512, vocab=600,
+                               moe=dict(n_expert=4, n_expert_used=2), n_batch=4),
+}
+
+
+@pytest.mark.parametrize("regime", [2, 0])
+@pytest.mark.parametrize("name", list(MODELS))
+def test_decoder_forward_matches_oracle(ctx, orc, name, regime):
+    """Prompt (chunked by n_batch where set), then single-token steps, the
+    last row's logits compared with the oracle's Transformer at every call.
+
+    Exact regime (f32 activations everywhere, KESTREL_EXACT): within 1e-3
+    relative L2 and 2e-3 of the logit scale (the reference's bound against
+    llama.cpp in that mode, tests/oracle.rs:75-77, 115). AVX2 regime (int8
+    activations below 4 rows, the reference host's default): an f32
+    difference of 1e-7 can flip one int8 rounding, which moves an output by
+    1/127 of its block's largest value, so the bound is the reference's own
+    for its int8 path, 6e-2 of the logit scale (tests/oracle.rs:124-126)."""
+    from kestrel_amd.decoder import Decoder
+
+    hp, T = decoder_model(seed=list(MODELS).index(name) + 1, **MODELS[name])
+    ref = orc.Transformer(hp, T, regime=regime)
+    ctx.set_regime(regime)
+    dec = Decoder(ctx, hp, T)
+    try:
+        rng = np.random.default_rng(5)
+        prompt = rng.integers(0, T["token_embd.weight"][1][1], 9).tolist()
+        steps = [prompt] + [[int(t)] for t in rng.integers(0, T["token_embd.weight"][1][1], 4)]
+        for toks in steps:
+            a = host(dec.forward(toks))
+            b = ref.forward(toks)
+            scale = max(1.0, float(np.abs(b).max()))
+            md = float(np.abs(a - b).max())
+            if regime == 2:
+                assert rel_l2(a, b) < 1e-3 and md <= 2e-3 * scale, (name, len(toks), rel_l2(a, b), md, scale)
+            else:
+                assert md <= 6e-2 * scale, (name, len(toks), md, scale)
+        assert dec.cached == ref.cached == 13
+    finally:
+        ctx.set_regime(0)
+        dec.close()
+
+
+@pytest.mark.parametrize("name", ["llama_dense", "qwen3moe"])
+def test_greedy_decode_graph_matches_eager_and_oracle(ctx, orc, name):
+    """Greedy decoding (sampler.rs:58-59) with the step captured once as a
+    HIP graph and replayed: the same tokens as eager steps, and (exact
+    regime) as the oracle's argmax over its own logits fed back step by step,
+    checked up to the first step whose top two logits are within 1e-3 of
+    the logit scale (a near-tie may part the sequences legitimately)."""
+    from kestrel_amd.decoder import Decoder
+
+    hp, T = decoder_model(seed=7, **MODELS[name])
+    prompt = [5, 17, 99, 3]
+    outs = []
+    ctx.set_regime(2)
+    try:
+        for use_graph in (True, False):
+            dec = Decoder(ctx, hp, T)
+            try:
+                logits = host(dec.forward(prompt))
+                first = int(np.argmax(logits))
+                toks = host(dec.decode_greedy(first, 12, use_graph=use_graph)).tolist()
+                outs.append([first] + toks)
+            finally:
+                dec.close()
+    finally:
+        ctx.set_regime(0)
+    assert outs[0] == outs[1]
+    ref = orc.Transformer(hp, T, regime=2)
+    l = ref.forward(prompt)
+    seq = [orc.argmax(l)]
+    for i in range(12):
+        l = ref.forward([seq[-1]])
+        top = np.sort(l)[-2:]
+        if top[1] - top[0] < 1e-3 * max(1.0, float(np.abs(l).max())):
+            break
+        seq.append(orc.argmax(l))
+    assert len(seq) >= 4 and outs[0][:len(seq)] == seq
+
+
+def test_decoder_context_full(ctx):
+    from kestrel_amd.decoder import Decoder
+
+    hp, T = decoder_model(n_ctx=8, seed=3, **{k: v for k, v in MODELS["llama_dense"].items()})
+    dec = Decoder(ctx, hp, T)
+    try:
+        dec.forward([1, 2, 3, 4, 5])
+        with pytest.raises(ValueError):
+            dec.forward([1, 2, 3, 4])
+    finally:
+        dec.close()
