@@ -57,7 +57,7 @@ def parse():
                          "decode, Qwen3-shaped layer, expert-tier preload)")
     ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload",
                     help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
-                         "q4k_m, qwen3, preload)")
+                         "q4k_m, qwen3, preload, decode_stack)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -447,6 +447,103 @@ def preload_leg(ctx, torch, reps: int = 3):
     return out
 
 
+def synthetic_blocks(t: int, n_blocks: int, scale: float, rng):
+    """Random well-formed blocks with dequantized std ~scale, built the way
+    kestrel's synthetic models are (tools/make_synthetic.py:38-58): Q4_K with
+    every 6-bit scale and min at 32 and dmin = 7.5 d (zero-mean weights), Q6_K
+    with int8 scales 16..47."""
+    import numpy as np
+
+    f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
+    if t == Q4_K:
+        raw = rng.integers(0, 256, size=(n_blocks, 144), dtype=np.uint8)
+        d = scale / (32 * 4.61)
+        raw[:, 0:2] = f16(d)
+        raw[:, 2:4] = f16(7.5 * d)
+        raw[:, 4:16] = np.array([160] * 8 + [0] * 4, np.uint8)
+    else:
+        raw = rng.integers(0, 256, size=(n_blocks, 210), dtype=np.uint8)
+        raw[:, 192:208] = (raw[:, 192:208] % 32 + 16).astype(np.uint8)
+        raw[:, 208:210] = f16(scale / 600.0)
+    return raw.reshape(-1)
+
+
+MOE6B = dict(layers=24, embd=2048, ff=1536, heads=16, kv_heads=4, vocab=32000, experts=32, experts_used=4)
+
+
+def decode_stack_leg(ctx, torch, prompt: int = 128, steps: int = 256):
+    """A whole decode stack on the GPU: kestrel's synthetic `moe-6b` shape
+    (tools/make_synthetic.py:27: llama architecture, 24 layers, hidden 2048,
+    16 heads / 4 KV heads, 32 experts of FFN 1536, top-4, vocab 32000; Q4_K
+    weights, Q6_K head, F32 norms and router), every weight resident in HBM.
+    A 128-token prompt of uniform random ids, then greedy decode steps, each
+    one token through all layers, the head and argmax, replayed as one HIP
+    graph. Expert and attention bytes are shared between layers on the host
+    (each layer still gets its own copy in HBM); routers differ per layer."""
+    import numpy as np
+
+    from kestrel_amd.decoder import Decoder
+
+    c = MOE6B
+    L, d, ff, H, KV, V, NE, NU = (c[k] for k in ("layers", "embd", "ff", "heads", "kv_heads", "vocab", "experts",
+                                                  "experts_used"))
+    hd = d // H
+    rng = np.random.default_rng(11)
+    q4 = lambda rows, cols, sc: (Q4_K, [cols, rows], synthetic_blocks(Q4_K, rows * cols // 256, sc, rng))
+    f32 = lambda v, dims: (0, list(dims), np.ascontiguousarray(v, np.float32).view(np.uint8).reshape(-1))
+    hp = dict(arch="llama", n_layer=L, n_embd=d, n_head=H, n_head_kv=KV, head_dim=hd, rope_dim=hd,
+              rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=prompt + steps + 8, n_batch=512, n_expert=NE,
+              n_expert_used=NU, norm_topk=False, weights_scale=0.0)
+    T = {"token_embd.weight": q4(V, d, 1.0), "output_norm.weight": f32(np.ones(d), [d]),
+         "output.weight": (Q6_K, [d, V], synthetic_blocks(Q6_K, V * d // 256, 1.0 / np.sqrt(d), rng))}
+    shared = {"attn_q.weight": q4(H * hd, d, 1 / np.sqrt(d)), "attn_k.weight": q4(KV * hd, d, 1 / np.sqrt(d)),
+              "attn_v.weight": q4(KV * hd, d, 1 / np.sqrt(d)), "attn_output.weight": q4(d, H * hd, 1 / np.sqrt(d))}
+    gate = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(d), rng))
+    up = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(d), rng))
+    down = (Q4_K, [ff, d, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(ff), rng))
+    for l in range(L):
+        p = f"blk.{l}."
+        T.update({p + k: v for k, v in shared.items()})
+        T[p + "attn_norm.weight"] = f32(np.ones(d), [d])
+        T[p + "ffn_norm.weight"] = f32(np.ones(d), [d])
+        T[p + "ffn_gate_inp.weight"] = f32(rng.standard_normal(NE * d) * (4.0 / np.sqrt(d)), [d, NE])
+        T[p + "ffn_gate_exps.weight"], T[p + "ffn_up_exps.weight"], T[p + "ffn_down_exps.weight"] = gate, up, down
+    ctx.set_stream(torch.cuda.current_stream())
+    t0 = time.perf_counter()
+    dec = Decoder(ctx, hp, T)
+    torch.cuda.synchronize()
+    load_s = time.perf_counter() - t0
+    try:
+        ids = rng.integers(0, V, prompt).tolist()
+        dec.forward(ids[:8])  # sizes the workspaces; its positions are then reset
+        dec.cached = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = dec.forward(ids)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        first = int(torch.argmax(logits).item())
+        dec.decode_greedy(first, 4)  # captures the step graph, warms it
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = dec.decode_greedy(first, steps - 4)
+        torch.cuda.synchronize()
+        dec_s = time.perf_counter() - t0
+        n_distinct = int(torch.unique(toks).numel())
+    finally:
+        dec.close()
+        torch.cuda.empty_cache()
+    per_layer_attn = (H * hd + 2 * KV * hd) * d // 256 * 144 + d * (H * hd) // 256 * 144
+    per_expert = 3 * ff * d // 256 * 144
+    tb = L * (per_layer_attn + NU * per_expert + NE * d * 4) + V * d // 256 * 210
+    n = steps - 4
+    return {"model": "synthetic moe-6b (llama arch)", "layers": L, "prompt_tokens": prompt,
+            "prefill_tokens_per_s": round(prompt / prefill_s, 1), "decode_steps": n,
+            "decode_tokens_per_s": round(n / dec_s, 1), "ms_per_token": round(dec_s / n * 1e3, 3),
+            "weight_bytes_per_token": tb, "hbm_GBps": round(tb * n / dec_s / 1e9, 1),
+            "distinct_tokens": n_distinct, "load_s": round(load_s, 1)}
+
+
 def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
     """Qwen3-30B-A3B-shaped layer: hidden 2048, FFN 768, 128 experts, top-8,
     Q4_K random-init experts, router N(0, 0.02) plus a rank-1 Zipf(1.1) bias
@@ -722,6 +819,8 @@ def main():
         res["qwen3"] = qwen3_leg(ctx, torch)
     if "preload" in legs:
         res["tier_preload"] = preload_leg(ctx, torch)
+    if "decode_stack" in legs:
+        res["decode_stack"] = decode_stack_leg(ctx, torch)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
         if a.prefill_tokens > 0:
