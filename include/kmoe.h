@@ -289,6 +289,17 @@ int kmoe_get_rows_dev(kmoe_ctx *ctx, int32_t type, const void *table_dev, size_t
  * stored in x and the norm is taken of the sum. out may be x. */
 int kmoe_rmsnorm(kmoe_ctx *ctx, float *x_dev, const float *y_dev, const float *w_dev, int64_t rows, int64_t dim,
                  float eps, float *out_dev);
+/* Transformer::rmsnorm then Transformer::mm of the normed rows (the
+ * attention projections, transformer.rs:391-393, and the head, :462-466):
+ * h = rmsnorm(x, norm_w) after x += y when y_dev is non-NULL (as
+ * kmoe_rmsnorm), out = quant::matmul(W, h) as kmoe_matmul. Where the
+ * context's regime takes the integer path, the norm kernel also writes the
+ * int8 rows the matvec reads, one pass fewer; the results are bit-identical
+ * to kmoe_rmsnorm followed by kmoe_matmul. h_dev [s_rows, cols] receives the
+ * normed rows. */
+int kmoe_norm_matmul(kmoe_ctx *ctx, float *x_dev, const float *y_dev, const float *norm_w_dev, float eps,
+                     int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols, int64_t s_rows,
+                     float *h_dev, float *out_dev);
 /* Transformer::rope (transformer.rs:342-358), in place on x [s_rows,
  * n_heads, head_dim]: pairs (i, i + rope_dim/2) when neox (every
  * architecture but llama, transformer.rs:242), else (2i, 2i+1), rotated by
@@ -308,10 +319,20 @@ int kmoe_kv_store(kmoe_ctx *ctx, const float *k_dev, const float *v_dev, int64_t
  * head h reads kv head h / (n_head / n_kv). out [s_rows, n_head * head_dim].
  * Scores use quant::dot's summation order (bit-identical); the softmax is
  * taken over chunks of 64 positions and merged, within 1e-6 relative of the
- * reference's single pass. head_dim 64 or 128. */
+ * reference's single pass. head_dim 64 or 128, at most 16 query heads per
+ * kv head. */
 int kmoe_attention(kmoe_ctx *ctx, const float *q_dev, const uint16_t *k_cache_dev, const uint16_t *v_cache_dev,
                    int64_t s_rows, int32_t n_head, int32_t n_kv, int32_t head_dim, int64_t pos0,
                    const int32_t *pos_dev, int64_t n_ctx, float *out_dev);
+/* RoPE of q and k followed by the KV cache store (transformer.rs:406-418) in
+ * one pass: q is rotated into q_out [s_rows, n_head * head_dim] (q_out must
+ * not overlap q), k is rotated and stored with v as f16 at rows position + s
+ * of the caches; k itself is left as it was. Same values as kmoe_rope on q
+ * and k followed by kmoe_kv_store. rope_dim <= 256. */
+int kmoe_rope_kv_store(kmoe_ctx *ctx, const float *q_dev, const float *k_dev, const float *v_dev, int64_t s_rows,
+                       int32_t n_head, int32_t n_kv, int32_t head_dim, int32_t rope_dim, int64_t pos0,
+                       const int32_t *pos_dev, const float *inv_freq_dev, int32_t neox, int64_t n_ctx,
+                       float *q_out_dev, uint16_t *k_cache_dev, uint16_t *v_cache_dev);
 /* Dense SwiGLU (transformer.rs:455): out = g / (1 + exp(-g)) * u, n elements. */
 int kmoe_swiglu(kmoe_ctx *ctx, const float *gate_dev, const float *up_dev, int64_t n, float *out_dev);
 /* Bias rows (transformer.rs:394-401): x[r] += b for rows of cols. */

@@ -109,9 +109,12 @@ struct kmoe_ctx {
   // device staging for host uploads of tiled parts and whole expert extents
   uint8_t *stage = nullptr;
   size_t stage_size = 0;
-  // decoder ops: attention partials and token ids copied from the host
+  // decoder ops: token ids copied from the host; attention counters
+  // (zero between calls) followed by its cross-work-group partials
   uint8_t *dws = nullptr;
   size_t dws_size = 0;
+  uint8_t *aws = nullptr;
+  size_t aws_size = 0, aws_counters = 0;
   // last moe_ffn routing (pointers into ws) and its sizes
   uint32_t *last_idx = nullptr, *last_perm = nullptr, *last_off = nullptr;
   float *last_w = nullptr;
@@ -314,6 +317,32 @@ int ensure_dws(kmoe_ctx *c, size_t need) {
   return KMOE_OK;
 }
 
+// Attention workspace: `counters` zero words, then partials. Grown (and its
+// counters cleared) outside any graph capture: callers run one call of each
+// size first.
+int ensure_aws(kmoe_ctx *c, size_t counters, size_t part_bytes) {
+  const size_t cb = align_up(counters * 4);
+  if (cb <= c->aws_counters && cb + part_bytes <= c->aws_size) return KMOE_OK;
+  const size_t ncb = std::max(cb, c->aws_counters);
+  const size_t need = ncb + std::max(part_bytes, c->aws_size - c->aws_counters);
+  const size_t sz = align_up(need + need / 4);
+  if (c->aws) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    HIP_OK(c, hipFree(c->aws));
+    release(c, c->aws_size);
+    c->aws = nullptr;
+    c->aws_size = c->aws_counters = 0;
+  }
+  void *p = nullptr;
+  int rc = dev_alloc(c, sz, &p, "attention workspace");
+  if (rc) return rc;
+  HIP_OK(c, hipMemset(p, 0, ncb));
+  c->aws = (uint8_t *)p;
+  c->aws_size = sz;
+  c->aws_counters = ncb;
+  return KMOE_OK;
+}
+
 // Device staging for host uploads, grown to the largest request and kept until
 // kmoe_destroy (counted in the ledger). nullptr, with no error left behind,
 // when the budget or hipMalloc refuses it: callers then take the host route.
@@ -481,6 +510,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   if (c->ws) (void)hipFree(c->ws);
   if (c->stage) (void)hipFree(c->stage);
   if (c->dws) (void)hipFree(c->dws);
+  if (c->aws) (void)hipFree(c->aws);
   if (c->counters) (void)hipFree(c->counters);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
@@ -1430,6 +1460,40 @@ int kmoe_rmsnorm(kmoe_ctx *c, float *x, const float *y, const float *w, int64_t 
   return KMOE_OK;
 }
 
+int kmoe_norm_matmul(kmoe_ctx *c, float *x, const float *y, const float *norm_w, float eps, int t, const void *w,
+                     size_t w_len, int64_t rows, int64_t cols, int64_t s_rows, float *h, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (rows < 0 || cols <= 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  const int64_t rb = bytes_for(t, cols);
+  if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
+  if (rb < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
+  if ((uint64_t)w_len < (uint64_t)rb * (uint64_t)rows)
+    return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows, (long long)rb);
+  if (s_rows == 0) return KMOE_OK;
+  if (!x || !norm_w || !w || !h || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  if (t != KMOE_F32) {
+    int rc = check_quant_shape(c, t, cols);
+    if (rc) return rc;
+  }
+  const int64_t pf = gemm_f32_part_floats(rows, cols, 1, s_rows, s_rows);
+  size_t need = 0;
+  carve_qrows(nullptr, s_rows, cols, &need, pf);
+  int rc = ensure_ws(c, need);
+  if (rc) return rc;
+  QRows qr = carve_qrows(c->ws, s_rows, cols, &need, pf);
+  if (t != KMOE_F32 && int_path(c->regime, s_rows) && rows > 0) {
+    hipError_t e = timed(c, "rmsnorm_quant", [&]() {
+      return launch_rmsnorm_quant(c->stream, x, y, norm_w, s_rows, cols, eps, h, is_kq(t), qr.q, qr.d, qr.s);
+    });
+    if (e == hipSuccess) return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
+  LAUNCH(c, "rmsnorm", launch_add_rmsnorm(c->stream, x, y, norm_w, s_rows, cols, eps, h));
+  if (rows == 0) return KMOE_OK;
+  return matmul_core(c, t, (const uint8_t *)w, rows, cols, h, s_rows, out, qr);
+}
+
 // Position checks shared by rope, kv_store and attention: with a host
 // position the rows must fit the context (EngineError::ContextFull,
 // transformer.rs:278-282); a device position is checked by the kernels.
@@ -1474,17 +1538,40 @@ int kmoe_attention(kmoe_ctx *c, const float *q, const uint16_t *k_cache, const u
   if (!c) return KMOE_E_INVALID;
   if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
     return fail(c, KMOE_E_INVALID, "attention: need n_head %% n_kv == 0 and n_ctx > 0");
-  if (!attn_supported_hd(head_dim)) return fail(c, KMOE_E_UNSUPPORTED, "head_dim %d (kernels: 64, 128)", head_dim);
+  if (!attn_supported(head_dim, n_head / n_kv))
+    return fail(c, KMOE_E_UNSUPPORTED, "head_dim %d, %d query heads per kv head (kernels: 64 or 128, <= 16)",
+                head_dim, n_head / n_kv);
   int rc = check_pos(c, pos0, pos_dev, s_rows, n_ctx);
   if (rc) return rc;
   if (s_rows == 0) return KMOE_OK;
   if (!q || !k_cache || !v_cache || !out) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
-  const int chunks = attn_chunks(pos_dev ? n_ctx : pos0 + s_rows);
-  rc = ensure_dws(c, (size_t)attn_part_floats(s_rows, n_head, head_dim, chunks) * 4);
+  const int supers = attn_supers(pos_dev ? n_ctx : std::min(n_ctx, pos0 + s_rows));
+  rc = ensure_aws(c, (size_t)s_rows * n_kv, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
   if (rc) return rc;
-  LAUNCH(c, "attention", launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0,
-                                          pos_dev, n_ctx, chunks, (float *)c->dws, out));
+  LAUNCH(c, "attention",
+         launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0, pos_dev, n_ctx,
+                          supers, (float *)(c->aws + c->aws_counters), (uint32_t *)c->aws, out));
+  return KMOE_OK;
+}
+
+int kmoe_rope_kv_store(kmoe_ctx *c, const float *q, const float *k, const float *v, int64_t s_rows, int32_t n_head,
+                       int32_t n_kv, int32_t head_dim, int32_t rope_dim, int64_t pos0, const int32_t *pos_dev,
+                       const float *inv_freq, int32_t neox, int64_t n_ctx, float *q_out, uint16_t *k_cache,
+                       uint16_t *v_cache) {
+  if (!c) return KMOE_E_INVALID;
+  if (n_head <= 0 || n_kv <= 0 || head_dim <= 0 || rope_dim <= 0 || rope_dim > head_dim || rope_dim % 2 ||
+      rope_dim > 256 || n_ctx <= 0)
+    return fail(c, KMOE_E_INVALID, "rope: need 0 < rope_dim <= min(head_dim, 256), rope_dim even");
+  int rc = check_pos(c, pos0, pos_dev, s_rows, n_ctx);
+  if (rc) return rc;
+  if (s_rows == 0) return KMOE_OK;
+  if (!q || !k || !v || !inv_freq || !q_out || !k_cache || !v_cache)
+    return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  LAUNCH(c, "rope_kv",
+         launch_rope_kv(c->stream, q, k, v, s_rows, n_head, n_kv, head_dim, rope_dim, pos0, pos_dev, inv_freq, neox,
+                        n_ctx, q_out, k_cache, v_cache));
   return KMOE_OK;
 }
 

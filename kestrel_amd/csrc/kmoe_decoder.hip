@@ -114,6 +114,78 @@ __global__ void __launch_bounds__(256) k_add_rmsnorm(float *x, const float *__re
   }
 }
 
+// The same for rows with dim % 4 == 0 and dim <= 1024 * NCH, the row held in
+// registers: thread t owns the float4 slots t + 256 k (elements 4t + 1024k
+// .. +3), and every load is issued before the first use. QT 1 also writes
+// the Q8_K quantization of the output (Q8KRow::quantize, qdot.rs:347-367;
+// dim % 256 == 0: wave w of chunk k holds block 4k + w), QT 2 the Q8 one
+// (Q8Row::quantize, qdot.rs:30-49; dim % 32 == 0: 8-lane groups hold blocks),
+// for the integer matvec that follows.
+template <int NCH, int QT>
+__global__ void __launch_bounds__(256) k_rmsnorm_regs(float *x, const float *__restrict__ y,
+                                                      const float *__restrict__ w, int64_t dim, float eps, float *out,
+                                                      int8_t *__restrict__ q, float *__restrict__ qd,
+                                                      int32_t *__restrict__ qs) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int t = threadIdx.x;
+  const int n4 = (int)(dim / 4);
+  float4 *xr = (float4 *)(x + r * dim);
+  const float4 *yr = (const float4 *)(y + r * dim);
+  const float4 *wr = (const float4 *)w;
+  float4 v[NCH], ww[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int i = t + 256 * k;
+    if (i < n4) {
+      v[k] = xr[i];
+      ww[k] = wr[i];
+    }
+  }
+  if (y) {
+    float4 yy[NCH];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+      if (t + 256 * k < n4) yy[k] = yr[t + 256 * k];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+      if (t + 256 * k < n4) {
+        v[k].x = v[k].x + yy[k].x;
+        v[k].y = v[k].y + yy[k].y;
+        v[k].z = v[k].z + yy[k].z;
+        v[k].w = v[k].w + yy[k].w;
+        xr[t + 256 * k] = v[k];
+      }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+    if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
+  ss = wg_sum256(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)dim + eps);
+  float4 *orow = (float4 *)(out + r * dim);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int i = t + 256 * k;
+    if (i < n4) {
+      float4 h;
+      h.x = (v[k].x * rr) * ww[k].x;
+      h.y = (v[k].y * rr) * ww[k].y;
+      h.z = (v[k].z * rr) * ww[k].z;
+      h.w = (v[k].w * rr) * ww[k].w;
+      orow[i] = h;
+      if constexpr (QT == 1) {
+        const int64_t b = 4 * k + (t >> 6);
+        wave_quant_q8k_vals(h, q + r * dim + 256 * b, qd + r * (dim / 256) + b, qs + r * (dim / 16) + 16 * b,
+                            t & 63);
+      } else if constexpr (QT == 2) {
+        const int64_t b = (4 * (int64_t)i) / 32;
+        group8_quant_q8_vals(h, q + r * dim + 32 * b, qd + r * (dim / 32) + b, qs + r * (dim / 16) + 2 * b, t & 7);
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ int64_t position(int64_t pos0, const int32_t *pos_dev) {
   return pos0 + (pos_dev ? (int64_t)*pos_dev : 0);
 }
@@ -158,143 +230,196 @@ __global__ void __launch_bounds__(256) k_kv_store(const float *__restrict__ k, c
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA attention (Transformer::attention, transformer.rs:591-631) as a
-// split softmax over chunks of 64 cache positions.
+// RoPE of q and k and the KV cache store in one pass (transformer.rs:406-418):
+// one work-group per row; the row's sin/cos table (from double precision, as
+// in k_rope) is built in LDS, q is rotated into q_out and the rotated k and v
+// go to the caches as f16.
+__global__ void __launch_bounds__(256) k_rope_kv(const float *__restrict__ q, const float *__restrict__ k,
+                                                 const float *__restrict__ v, int nh, int nkv, int hd, int rd,
+                                                 int64_t pos0, const int32_t *__restrict__ pos_dev,
+                                                 const float *__restrict__ inv_freq, int neox, int64_t n_ctx,
+                                                 float *__restrict__ q_out, uint16_t *__restrict__ kc,
+                                                 uint16_t *__restrict__ vc) {
+  __shared__ float sn[128], cs[128];
+  const int64_t s = blockIdx.x;
+  const int half = rd / 2;
+  const int64_t p = position(pos0, pos_dev) + s;
+  if (threadIdx.x < half) {
+    const float ang = (float)p * inv_freq[threadIdx.x];
+    sn[threadIdx.x] = (float)sin((double)ang);
+    cs[threadIdx.x] = (float)cos((double)ang);
+  }
+  __syncthreads();
+  const int nq = nh * hd, kvw = nkv * hd;
+  // element e of a head: its rotated value from the pair it belongs to
+  auto rot = [&](const float *row, int e) -> float {
+    const int h = e / hd, dd = e - h * hd;
+    if (dd >= rd) return row[e];
+    const float *base = row + h * hd;
+    int i, a, b;
+    bool first;
+    if (neox) {
+      first = dd < half;
+      i = first ? dd : dd - half;
+      a = i;
+      b = i + half;
+    } else {
+      first = (dd & 1) == 0;
+      i = dd >> 1;
+      a = 2 * i;
+      b = 2 * i + 1;
+    }
+    const float x0 = base[a], x1 = base[b];
+    return first ? x0 * cs[i] - x1 * sn[i] : x0 * sn[i] + x1 * cs[i];
+  };
+  const float *qr = q + s * nq;
+  for (int e = threadIdx.x; e < nq; e += 256) q_out[s * nq + e] = rot(qr, e);
+  if (p < 0 || p >= n_ctx) return;
+  const float *kr = k + s * kvw;
+  for (int e = threadIdx.x; e < kvw; e += 256) {
+    kc[p * kvw + e] = __builtin_bit_cast(uint16_t, (_Float16)rot(kr, e));
+    vc[p * kvw + e] = __builtin_bit_cast(uint16_t, (_Float16)v[s * kvw + e]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA attention (Transformer::attention, transformer.rs:591-631).
 //
-// Work-group (kv head g, query row s, chunk c) stages the chunk's K and V
-// rows (f16) in LDS, then each wave takes query heads of the group: lane l
-// scores position 64c + l with quant::dot's eight-accumulator order
-// (quant.rs:208-224) times 1/sqrt(hd), the wave takes the chunk's max m and
-// e_p = exp(score - m), and lanes over head dims accumulate sum_p e_p V[p].
-// The partial (m, sum e, acc) goes to the workspace; k_attn_combine merges
-// the chunks of a (row, head): out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// Work-group (kv head g, query row s, chunk c of 64 cache positions); wave w
+// takes query heads w, w + 4, ... of the group. Lane l loads position l's K
+// row of head g into registers and scores it against the head's q (read with
+// scalar loads: the address is uniform over the wave) in quant::dot's
+// eight-accumulator order (quant.rs:208-224), times 1/sqrt(hd); the wave
+// takes the chunk's max m and e = exp(score - m), and lanes over head dims
+// accumulate sum e V from V rows in registers, the weights broadcast with
+// readlane. With one chunk the result is final; otherwise every work-group of
+// the row hands (m, sum e, acc) over with agent-scope stores and a counter,
+// and the last to arrive merges them (out = sum acc e^(m - M) / sum l e^(m - M))
+// and resets the counter.
 constexpr int kAttnChunk = 64;
+constexpr int kMaxGroup = 16;
 
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn_chunk(const float *__restrict__ q, const uint16_t *__restrict__ kc,
-                                                    const uint16_t *__restrict__ vc, int64_t s_rows, int nh,
-                                                    int nkv, int64_t pos0, const int32_t *__restrict__ pos_dev,
-                                                    int64_t n_ctx, int chunks, float *__restrict__ part) {
-  constexpr int RW = HD / 2 + 1;  // LDS row stride in dwords (odd: conflict-free column reads)
-  __shared__ uint32_t Ks[kAttnChunk * RW];
-  __shared__ uint32_t Vs[kAttnChunk * RW];
-  __shared__ float Qs[4][HD];
-  __shared__ float Ps[4][kAttnChunk];
+__global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                  const uint16_t *__restrict__ vc, int64_t s_rows, int nh, int nkv,
+                                                  int64_t pos0, const int32_t *__restrict__ pos_dev, int64_t n_ctx,
+                                                  int nch_grid, float *part, uint32_t *counters,
+                                                  float *__restrict__ out) {
+  constexpr int KV4 = HD / 8;   // uint4 pieces (8 halves) per K row
+  constexpr int DPL = HD / 64;  // head dims per lane
+  __shared__ uint32_t last;
   const int64_t bid = blockIdx.x;
-  const int c = (int)(bid % chunks);
-  const int64_t s = (bid / chunks) % s_rows;
-  const int g = (int)(bid / chunks / s_rows);
+  const int c = (int)(bid % nch_grid);
+  const int64_t s = (bid / nch_grid) % s_rows;
+  const int g = (int)(bid / nch_grid / s_rows);
   int64_t n = position(pos0, pos_dev) + s + 1;
   if (n > n_ctx) n = n_ctx;
-  const int64_t p0 = (int64_t)c * kAttnChunk;
-  if (p0 >= n) return;
-  const int np = (int)(n - p0 < kAttnChunk ? n - p0 : kAttnChunk);
-  const int64_t kvw = (int64_t)nkv * HD;
-  // stage K and V rows [p0, p0 + np) of head g: HD/2 dwords per row
-  for (int e = threadIdx.x; e < np * (HD / 2); e += 256) {
-    const int r = e / (HD / 2), w = e % (HD / 2);
-    const int64_t off = (p0 + r) * kvw + (int64_t)g * HD;
-    Ks[r * RW + w] = ((const uint32_t *)(kc + off))[w];
-    Vs[r * RW + w] = ((const uint32_t *)(vc + off))[w];
-  }
+  const int nch = (int)((n + kAttnChunk - 1) / kAttnChunk);
+  if (c >= nch) return;
   const int group = nh / nkv;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const float scale = 1.0f / sqrtf((float)HD);
-  __syncthreads();
-  for (int hh0 = 0; hh0 < group; hh0 += 4) {
-    const int hh = hh0 + wave;
-    const bool on = hh < group;
-    const int h = g * group + hh;
-    if (on)
-      for (int j = lane; j < HD; j += 64) Qs[wave][j] = q[(s * nh + h) * (int64_t)HD + j];
-    __syncthreads();
-    if (on) {
-      float sc = -INFINITY;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t kvw = (int64_t)nkv * HD;
+  const int64_t p0 = (int64_t)c * kAttnChunk;
+  const int np = (int)(n - p0 < kAttnChunk ? n - p0 : kAttnChunk);
+  if (wave < group) {
+    uint4 kr[KV4];
+    if (lane < np) {
+      const uint4 *src = (const uint4 *)(kc + (p0 + lane) * kvw + (int64_t)g * HD);
+#pragma unroll
+      for (int j = 0; j < KV4; ++j) kr[j] = src[j];
+    }
+    uint32_t vr[DPL == 2 ? 64 : 1];
+    uint16_t vh[DPL == 1 ? 64 : 1];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      if (j < np) {
+        const uint16_t *vrow = vc + (p0 + j) * kvw + (int64_t)g * HD;
+        if constexpr (DPL == 2) vr[j] = ((const uint32_t *)vrow)[lane];
+        else vh[j] = vrow[lane];
+      }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int hh = wave; hh < group; hh += 4) {
+      const int64_t h = (int64_t)g * group + hh;
+      const float *qh = q + (s * nh + h) * HD;
+      float sc_ = -INFINITY;
       if (lane < np) {
         float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        const uint32_t *kr = Ks + lane * RW;
-#pragma unroll 4
-        for (int c8 = 0; c8 < HD; c8 += 8) {
 #pragma unroll
-          for (int i = 0; i < 8; i += 2) {
-            const uint32_t kw = kr[(c8 + i) / 2];
-            const float k0 = f16_bits_to_f32(kw), k1 = f16_bits_to_f32(kw >> 16);
-            const float a0 = Qs[wave][c8 + i] * k0, a1 = Qs[wave][c8 + i + 1] * k1;
-            acc[i] = acc[i] + a0;
-            acc[i + 1] = acc[i + 1] + a1;
+        for (int j = 0; j < KV4; ++j) {
+          const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float a0 = qh[8 * j + 2 * i] * f16_bits_to_f32(w4[i]);
+            const float a1 = qh[8 * j + 2 * i + 1] * f16_bits_to_f32(w4[i] >> 16);
+            acc[2 * i] = acc[2 * i] + a0;
+            acc[2 * i + 1] = acc[2 * i + 1] + a1;
           }
         }
         float t = -0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) t = t + acc[i];
-        sc = t * scale;
+        sc_ = t * scale;
       }
-      const float m = group_max<64>(sc);
-      const float e = lane < np ? expf(sc - m) : 0.0f;
+      const float m = group_max<64>(sc_);
+      const float e = lane < np ? expf(sc_ - m) : 0.0f;
       const float l = group_sum<64>(e);
-      Ps[wave][lane] = e;
-      // lanes over dims: lane owns HD/64 consecutive dims
-      constexpr int DPL = HD / 64;
       float o[DPL];
 #pragma unroll
       for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
-      __builtin_amdgcn_wave_barrier();
-      for (int p = 0; p < np; ++p) {
-        const float wgt = Ps[wave][p];
-        const uint32_t *vr = Vs + p * RW;
-        if constexpr (DPL == 1) {
-          const uint32_t vw = vr[lane >> 1];
-          o[0] += wgt * f16_bits_to_f32((lane & 1) ? (vw >> 16) : vw);
-        } else {
 #pragma unroll
-          for (int i = 0; i < DPL; i += 2) {
-            const uint32_t vw = vr[(lane * DPL + i) / 2];
-            o[i] += wgt * f16_bits_to_f32(vw);
-            o[i + 1] += wgt * f16_bits_to_f32(vw >> 16);
+      for (int j = 0; j < 64; ++j) {
+        if (j < np) {
+          const float wgt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+          if constexpr (DPL == 2) {
+            o[0] += wgt * f16_bits_to_f32(vr[j]);
+            o[1] += wgt * f16_bits_to_f32(vr[j] >> 16);
+          } else {
+            o[0] += wgt * f16_bits_to_f32(vh[j]);
           }
         }
       }
-      const int64_t pi = ((s * nh + h) * (int64_t)chunks + c);
-      float *pp = part + pi * (HD + 2);
-      if (lane == 0) {
-        pp[0] = m;
-        pp[1] = l;
+      if (nch == 1) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) out[(s * nh + h) * HD + lane * DPL + i] = o[i] * inv;
+      } else {
+        float *pp = part + ((s * nh + h) * nch_grid + c) * (HD + 2);
+        if (lane == 0) {
+          st_agent(pp, m);
+          st_agent(pp + 1, l);
+        }
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) st_agent(pp + 2 + lane * DPL + i, o[i]);
       }
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) pp[2 + lane * DPL + i] = o[i];
     }
-    __syncthreads();
   }
-}
-
-template <int HD>
-__global__ void __launch_bounds__(256) k_attn_combine(const float *__restrict__ part, int64_t s_rows, int nh,
-                                                      int64_t pos0, const int32_t *__restrict__ pos_dev,
-                                                      int64_t n_ctx, int chunks, float *__restrict__ out) {
-  constexpr int DPL = HD / 64;
-  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= s_rows * nh) return;
-  const int lane = threadIdx.x & 63;
-  const int64_t s = pair / nh;
-  int64_t n = position(pos0, pos_dev) + s + 1;
-  if (n > n_ctx) n = n_ctx;
-  const int nc = (int)((n + kAttnChunk - 1) / kAttnChunk);
-  const float *pp = part + pair * chunks * (HD + 2);
-  float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * (HD + 2)]);
-  float L = 0.0f, o[DPL];
+  if (nch == 1) return;
+  vm_wait();  // this wave's partials are written before the counter moves
+  __syncthreads();
+  if (threadIdx.x == 0) last = add_agent(counters + s * nkv + g, 1u);
+  __syncthreads();
+  if (last != (uint32_t)(nch - 1)) return;
+  for (int hh = wave; hh < group; hh += 4) {
+    const int64_t h = (int64_t)g * group + hh;
+    const float *pb = part + (s * nh + h) * nch_grid * (HD + 2);
+    float M = -INFINITY;
+    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ld_agent(pb + cc * (HD + 2)));
+    float L = 0.0f, O[DPL];
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
-  for (int c = 0; c < nc; ++c) {
-    const float *pc = pp + c * (HD + 2);
-    const float f = expf(pc[0] - M);
-    L += pc[1] * f;
+    for (int i = 0; i < DPL; ++i) O[i] = 0.0f;
+    for (int cc = 0; cc < nch; ++cc) {
+      const float *pc = pb + cc * (HD + 2);
+      const float f = expf(ld_agent(pc) - M);
+      L += ld_agent(pc + 1) * f;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) o[i] += pc[2 + lane * DPL + i] * f;
+      for (int i = 0; i < DPL; ++i) O[i] += ld_agent(pc + 2 + lane * DPL + i) * f;
+    }
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) out[(s * nh + h) * HD + lane * DPL + i] = O[i] * inv;
   }
-  const float inv = 1.0f / L;
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) out[pair * HD + lane * DPL + i] = o[i] * inv;
+  if (threadIdx.x == 0) st_agent(counters + s * nkv + g, 0u);  // ready for the next call
 }
 
 // Dense SwiGLU (transformer.rs:455): out = g / (1 + exp(-g)) * u.
@@ -376,11 +501,43 @@ hipError_t launch_get_rows(hipStream_t st, int t, const uint8_t *table, int64_t 
   return hipGetLastError();
 }
 
+// The register-resident kernel applies: dim % 4 == 0, dim <= 8192, 16-byte
+// aligned rows, and the quantization's block size divides dim.
+static bool rmsnorm_regs_ok(const void *x, const void *y, const void *w, const void *out, int64_t dim, int qt) {
+  if (dim % 4 || dim > 8192 || dim < 4) return false;
+  if ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)out) & 15) != 0) return false;
+  if (qt == 1 && dim % 256) return false;
+  if (qt == 2 && dim % 32) return false;
+  return true;
+}
+
+template <int QT>
+static hipError_t launch_rmsnorm_regs(hipStream_t st, float *x, const float *y, const float *w, int64_t rows,
+                                      int64_t dim, float eps, float *out, int8_t *q, float *qd, int32_t *qs) {
+  const int nch = (int)((dim / 4 + 255) / 256);
+  const dim3 g((unsigned)rows), b(256);
+  if (nch <= 1) KMOE_LAUNCH((k_rmsnorm_regs<1, QT>), g, b, 0, st, x, y, w, dim, eps, out, q, qd, qs);
+  else if (nch <= 2) KMOE_LAUNCH((k_rmsnorm_regs<2, QT>), g, b, 0, st, x, y, w, dim, eps, out, q, qd, qs);
+  else if (nch <= 4) KMOE_LAUNCH((k_rmsnorm_regs<4, QT>), g, b, 0, st, x, y, w, dim, eps, out, q, qd, qs);
+  else KMOE_LAUNCH((k_rmsnorm_regs<8, QT>), g, b, 0, st, x, y, w, dim, eps, out, q, qd, qs);
+  return hipGetLastError();
+}
+
 hipError_t launch_add_rmsnorm(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
                               float eps, float *out) {
   if (rows <= 0) return hipSuccess;
+  if (rmsnorm_regs_ok(x, y, w, out, dim, 0))
+    return launch_rmsnorm_regs<0>(st, x, y, w, rows, dim, eps, out, nullptr, nullptr, nullptr);
   KMOE_LAUNCH(k_add_rmsnorm, dim3((unsigned)rows), dim3(256), 0, st, x, y, w, dim, eps, out);
   return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
+                                float eps, float *out, bool q8k, int8_t *q, float *qd, int32_t *qs) {
+  if (rows <= 0) return hipSuccess;
+  if (!rmsnorm_regs_ok(x, y, w, out, dim, q8k ? 1 : 2)) return hipErrorNotSupported;
+  if (q8k) return launch_rmsnorm_regs<1>(st, x, y, w, rows, dim, eps, out, q, qd, qs);
+  return launch_rmsnorm_regs<2>(st, x, y, w, rows, dim, eps, out, q, qd, qs);
 }
 
 hipError_t launch_rope(hipStream_t st, float *x, int64_t s_rows, int n_heads, int hd, int rd, int64_t pos0,
@@ -400,33 +557,36 @@ hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64
   return hipGetLastError();
 }
 
-int attn_chunks(int64_t n_max) { return (int)((n_max + kAttnChunk - 1) / kAttnChunk); }
+int attn_supers(int64_t n_max) { return (int)((n_max + kAttnChunk - 1) / kAttnChunk); }
 
-int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int chunks) {
-  return s_rows * nh * (int64_t)chunks * (hd + 2);
+int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int supers) {
+  return supers <= 1 ? 0 : s_rows * nh * (int64_t)supers * (hd + 2);
 }
 
-bool attn_supported_hd(int hd) { return hd == 64 || hd == 128; }
+bool attn_supported(int hd, int group) { return (hd == 64 || hd == 128) && group >= 1 && group <= kMaxGroup; }
 
 hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
-                            int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int chunks,
-                            float *part, float *out) {
+                            int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int supers,
+                            float *part, uint32_t *counters, float *out) {
   if (s_rows <= 0) return hipSuccess;
-  const unsigned g1 = (unsigned)((int64_t)nkv * s_rows * chunks);
-  const unsigned g2 = blocks(s_rows * nh, 4);
-#define KMOE_ATTN(HD)                                                                                          \
-  do {                                                                                                         \
-    KMOE_LAUNCH(k_attn_chunk<HD>, dim3(g1), dim3(256), 0, st, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx, \
-                chunks, part);                                                                                 \
-    KMOE_LAUNCH(k_attn_combine<HD>, dim3(g2), dim3(256), 0, st, part, s_rows, nh, pos0, pos_dev, n_ctx, chunks,  \
-                out);                                                                                          \
-  } while (0)
-  switch (hd) {
-    case 64: KMOE_ATTN(64); break;
-    case 128: KMOE_ATTN(128); break;
-    default: return hipErrorInvalidValue;
-  }
-#undef KMOE_ATTN
+  const unsigned grid = (unsigned)((int64_t)nkv * s_rows * supers);
+  if (hd == 64)
+    KMOE_LAUNCH(k_attn_dec<64>, dim3(grid), dim3(256), 0, st, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx,
+                supers, part, counters, out);
+  else if (hd == 128)
+    KMOE_LAUNCH(k_attn_dec<128>, dim3(grid), dim3(256), 0, st, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx,
+                supers, part, counters, out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(hipStream_t st, const float *q, const float *k, const float *v, int64_t s_rows, int nh,
+                          int nkv, int hd, int rd, int64_t pos0, const int32_t *pos_dev, const float *inv_freq,
+                          int neox, int64_t n_ctx, float *q_out, uint16_t *kc, uint16_t *vc) {
+  if (s_rows <= 0) return hipSuccess;
+  KMOE_LAUNCH(k_rope_kv, dim3((unsigned)s_rows), dim3(256), 0, st, q, k, v, nh, nkv, hd, rd, pos0, pos_dev, inv_freq,
+              neox, n_ctx, q_out, kc, vc);
   return hipGetLastError();
 }
 

@@ -245,17 +245,10 @@ __device__ __forceinline__ int4 ld_agent4(const void *p) {
 }
 
 // Q8KRow::quantize of one 256-element block by one full wave (qdot.rs:353-365).
-// Lane l owns elements 4l..4l+3. Writes q[0..256), *d, bsums[0..16).
-// COHERENT: x read and the results written with agent-scope accesses.
+// The same from values already in registers: lane l holds elements
+// 4l..4l+3 of the block in v.
 template <bool COHERENT = false>
-__device__ __forceinline__ void wave_quant_q8k_block(const float *x, int8_t *q, float *d, int32_t *bsums, int lane) {
-  float4 v;
-  if constexpr (COHERENT) {
-    const float *xp = x + 4 * lane;
-    v = make_float4(ld_agent(xp), ld_agent(xp + 1), ld_agent(xp + 2), ld_agent(xp + 3));
-  } else {
-    v = *(const float4 *)(x + 4 * lane);
-  }
+__device__ __forceinline__ void wave_quant_q8k_vals(float4 v, int8_t *q, float *d, int32_t *bsums, int lane) {
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   amax = group_max<64>(amax);
   const float scale = amax / 127.0f;
@@ -274,10 +267,23 @@ __device__ __forceinline__ void wave_quant_q8k_block(const float *x, int8_t *q, 
   }
 }
 
+// Lane l owns elements 4l..4l+3. Writes q[0..256), *d, bsums[0..16).
+// COHERENT: x read and the results written with agent-scope accesses.
+template <bool COHERENT = false>
+__device__ __forceinline__ void wave_quant_q8k_block(const float *x, int8_t *q, float *d, int32_t *bsums, int lane) {
+  float4 v;
+  if constexpr (COHERENT) {
+    const float *xp = x + 4 * lane;
+    v = make_float4(ld_agent(xp), ld_agent(xp + 1), ld_agent(xp + 2), ld_agent(xp + 3));
+  } else {
+    v = *(const float4 *)(x + 4 * lane);
+  }
+  wave_quant_q8k_vals<COHERENT>(v, q, d, bsums, lane);
+}
+
 // Q8Row::quantize of one 32-element block by an aligned group of 8 lanes
 // (qdot.rs:36-47). g = lane & 7 owns elements 4g..4g+3.
-__device__ __forceinline__ void group8_quant_q8_block(const float *x, int8_t *q, float *d, int32_t *s16, int g) {
-  const float4 v = *(const float4 *)(x + 4 * g);
+__device__ __forceinline__ void group8_quant_q8_vals(float4 v, int8_t *q, float *d, int32_t *s16, int g) {
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   amax = group_max<8>(amax);
   const float scale = amax / 127.0f;
@@ -288,6 +294,9 @@ __device__ __forceinline__ void group8_quant_q8_block(const float *x, int8_t *q,
   s = group_sum_i<4>(s);
   if ((g & 3) == 0) s16[g >> 2] = s;
   if (g == 0) *d = scale;
+}
+__device__ __forceinline__ void group8_quant_q8_block(const float *x, int8_t *q, float *d, int32_t *s16, int g) {
+  group8_quant_q8_vals(*(const float4 *)(x + 4 * g), q, d, s16, g);
 }
 
 }  // namespace kmoe

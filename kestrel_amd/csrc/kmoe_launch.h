@@ -222,6 +222,46 @@ hipError_t launch_get_rows(hipStream_t st, int t, const uint8_t *table, int64_t 
                            int64_t cols, const uint32_t *ids, int64_t s_rows, float *out);
 hipError_t launch_add_rmsnorm(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
                               float eps, float *out);
+// RMSNorm followed by the Q8_K (q8k) or Q8 quantization of its output, in one
+// kernel; hipErrorNotSupported when the shape or alignment does not allow it.
+hipError_t launch_rmsnorm_quant(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
+                                float eps, float *out, bool q8k, int8_t *q, float *qd, int32_t *qs);
+hipError_t launch_rope(hipStream_t st, float *x, int64_t s_rows, int n_heads, int hd, int rd, int64_t pos0,
+                       const int32_t *pos_dev, const float *inv_freq, int neox);
+hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64_t s_rows, int64_t kvw,
+                           int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, uint16_t *kc, uint16_t *vc);
+// Attention: chunks of 64 positions covering n_max positions, the
+// cross-work-group partials' size (0 for one super-chunk), supported shapes.
+// counters: s_rows * nkv zero words (zero again when the kernel ends).
+int attn_supers(int64_t n_max);
+int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int supers);
+bool attn_supported(int hd, int group);
+hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
+                            int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int supers,
+                            float *part, uint32_t *counters, float *out);
+// RoPE of q (into q_out) and k, and the f16 store of k and v into the caches.
+hipError_t launch_rope_kv(hipStream_t st, const float *q, const float *k, const float *v, int64_t s_rows, int nh,
+                          int nkv, int hd, int rd, int64_t pos0, const int32_t *pos_dev, const float *inv_freq,
+                          int neox, int64_t n_ctx, float *q_out, uint16_t *kc, uint16_t *vc);
+hipError_t launch_swiglu(hipStream_t st, float *g, const float *u, int64_t n);
+// out[s] += sigmoid(logits[s]) * y[s] (logits null: scale 1).
+hipError_t launch_shared_add(hipStream_t st, float *out, const float *y, const float *logits, int64_t S, int64_t d);
+
+// out[s] = sum over the token's experts in ascending id of w * y[slot].
+hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out);
+
+
+// ---- the rest of the decoder layer (kmoe_decoder.hip) ----
+// Rows ids[0..s_rows) of a GGUF table [n_rows, cols] of type t (F32, F16,
+// Q8_0, Q4_K, Q6_K), dequantized to f32 out [s_rows, cols].
+hipError_t launch_get_rows(hipStream_t st, int t, const uint8_t *table, int64_t row_bytes, int64_t n_rows,
+                           int64_t cols, const uint32_t *ids, int64_t s_rows, float *out);
+hipError_t launch_add_rmsnorm(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
+                              float eps, float *out);
+// RMSNorm followed by the Q8_K (q8k) or Q8 quantization of its output, in one
+// kernel; hipErrorNotSupported when the shape or alignment does not allow it.
+hipError_t launch_rmsnorm_quant(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
+                                float eps, float *out, bool q8k, int8_t *q, float *qd, int32_t *qs);
 hipError_t launch_rope(hipStream_t st, float *x, int64_t s_rows, int n_heads, int hd, int rd, int64_t pos0,
                        const int32_t *pos_dev, const float *inv_freq, int neox);
 hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64_t s_rows, int64_t kvw,

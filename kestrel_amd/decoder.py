@@ -104,8 +104,14 @@ class Decoder:
             if p + "ffn_gate_exps.weight" in tensors:
                 L["moe"] = self._moe_layer(l, layer_base + l, tensors)
             else:
-                for n in ("gate", "up", "down"):
-                    L[n] = raw(p + f"ffn_{n}.weight")
+                wg, wu = tensors[p + "ffn_gate.weight"], tensors[p + "ffn_up.weight"]
+                if wg[0] == wu[0] and list(wg[1]) == list(wu[1]):  # gate | up rows in one matmul
+                    cat = np.concatenate([np.ascontiguousarray(w[2], dtype=np.uint8).reshape(-1)[:_nbytes(w[0], w[1])]
+                                          for w in (wg, wu)])
+                    L["wgu"] = (wg[0], [wg[1][0], 2 * wg[1][1]], torch.from_numpy(cat).to(dev))
+                else:
+                    L["gate"], L["up"] = raw(p + "ffn_gate.weight"), raw(p + "ffn_up.weight")
+                L["down"] = raw(p + "ffn_down.weight")
             L["kc"] = torch.zeros((self.n_ctx, kvw), dtype=torch.int16, device=dev)
             L["vc"] = torch.zeros((self.n_ctx, kvw), dtype=torch.int16, device=dev)
             self.layers.append(L)
@@ -153,13 +159,14 @@ class Decoder:
         norm's fused add; the layer returns its own FFN output."""
         ctx, nh, nkv, hd = self.ctx, self.nh, self.nkv, self.hd
         kvw, nq = nkv * hd, nh * hd
-        h = ctx.rmsnorm(x, L["attn_norm"], self.eps, y=f_prev)
         if "wqkv" in L:
-            qkv = self._mm(L["wqkv"], h)
+            ty, dims, t = L["wqkv"]
+            qkv = ctx.norm_matmul(x, L["attn_norm"], self.eps, ty, t, dims[1], dims[0], y=f_prev)
             q, k, v = qkv[:, :nq], qkv[:, nq:nq + kvw], qkv[:, nq + kvw:]
             if S > 1:
                 q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         else:
+            h = ctx.rmsnorm(x, L["attn_norm"], self.eps, y=f_prev)
             q, k, v = self._mm(L["wq"], h), self._mm(L["wk"], h), self._mm(L["wv"], h)
         for n, y in (("q", q), ("k", k), ("v", v)):
             if "b" + n in L:
@@ -168,15 +175,23 @@ class Decoder:
             ctx.rmsnorm(q, L["q_norm"], self.eps, out=q)
         if "k_norm" in L:
             ctx.rmsnorm(k, L["k_norm"], self.eps, out=k)
-        ctx.rope(q, nh, hd, self.rd, pos0, self.inv_freq, self.neox, pos_dev)
-        ctx.rope(k, nkv, hd, self.rd, pos0, self.inv_freq, self.neox, pos_dev)
-        ctx.kv_store(k, v, kvw, pos0, self.n_ctx, L["kc"], L["vc"], pos_dev)
-        a = ctx.attention(q, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, pos_dev)
+        qr = ctx.rope_kv_store(q, k, v, nh, nkv, hd, self.rd, pos0, self.inv_freq, self.neox, self.n_ctx, L["kc"],
+                               L["vc"], pos_dev)
+        a = ctx.attention(qr, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, pos_dev)
         o = self._mm(L["wo"], a)
-        h = ctx.rmsnorm(x, L["ffn_norm"], self.eps, y=o)  # x += o, then the norm of x
         if "moe" in L:
+            h = ctx.rmsnorm(x, L["ffn_norm"], self.eps, y=o)  # x += o, then the norm of x
             return ctx.moe_ffn(L["moe"], h)
-        g, u = self._mm(L["gate"], h), self._mm(L["up"], h)
+        if "wgu" in L:
+            ty, dims, t = L["wgu"]
+            ff = dims[1] // 2
+            gu = ctx.norm_matmul(x, L["ffn_norm"], self.eps, ty, t, dims[1], dims[0], y=o)
+            g, u = gu[:, :ff], gu[:, ff:]
+            if S > 1:
+                g, u = g.contiguous(), u.contiguous()
+        else:
+            h = ctx.rmsnorm(x, L["ffn_norm"], self.eps, y=o)
+            g, u = self._mm(L["gate"], h), self._mm(L["up"], h)
         return self._mm(L["down"], ctx.swiglu(g, u))
 
     def _stack(self, x, S: int, pos0: int, pos_dev):
@@ -184,9 +199,9 @@ class Decoder:
         f = None
         for L in self.layers:
             f = self._layer(L, x, f, S, pos0, pos_dev)
-        normed = self.ctx.rmsnorm(x[S - 1:S], self.out_norm, self.eps, y=f[S - 1:S])
         ty, dims, t = self.head
-        return self.ctx.matmul(ty, t, dims[1], dims[0], normed).reshape(-1)
+        return self.ctx.norm_matmul(x[S - 1:S], self.out_norm, self.eps, ty, t, dims[1], dims[0],
+                                    y=f[S - 1:S]).reshape(-1)
 
     def forward(self, tokens):
         """Transformer::forward: feed host token ids; returns the last row's

@@ -69,9 +69,12 @@ SIGNATURES = {
     "kmoe_get_rows": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
     "kmoe_get_rows_dev": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
     "kmoe_rmsnorm": (C.c_int, [_P, _P, _P, _P, _i64, _i64, _f, _P]),
+    "kmoe_norm_matmul": (C.c_int, [_P, _P, _P, _P, _f, C.c_int, _P, _sz, _i64, _i64, _i64, _P, _P]),
     "kmoe_rope": (C.c_int, [_P, _P, _i64, _i32, _i32, _i32, _i64, _P, _P, _i32]),
     "kmoe_kv_store": (C.c_int, [_P, _P, _P, _i64, _i64, _i64, _P, _i64, _P, _P]),
     "kmoe_attention": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i64, _P, _i64, _P]),
+    "kmoe_rope_kv_store": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i32, _i64, _P, _P, _i32, _i64, _P,
+                                     _P, _P]),
     "kmoe_swiglu": (C.c_int, [_P, _P, _P, _i64, _P]),
     "kmoe_add_rows": (C.c_int, [_P, _P, _P, _i64, _i64]),
     "kmoe_argmax": (C.c_int, [_P, _P, _i64, _P, _P, _i32]),
@@ -221,6 +224,15 @@ class Context:
         self.check(self.lib.kmoe_rmsnorm(self.h, _ptr(x), _ptr(y), _ptr(w), x.numel() // dim, dim, eps, _ptr(out)))
         return out
 
+    def norm_matmul(self, x, norm_w, eps: float, t: int, w, rows: int, cols: int, y=None, h=None):
+        """rmsnorm (x += y first when given) then quant::matmul of the normed rows: -> [S, rows]."""
+        S = x.numel() // cols
+        h = self._empty((S, cols), self.torch.float32) if h is None else h
+        out = self._empty((S, rows), self.torch.float32)
+        self.check(self.lib.kmoe_norm_matmul(self.h, _ptr(x), _ptr(y), _ptr(norm_w), eps, t, _ptr(w),
+                                             w.numel() * w.element_size(), rows, cols, S, _ptr(h), _ptr(out)))
+        return out
+
     def rope(self, x, n_heads: int, head_dim: int, rope_dim: int, pos0: int, inv_freq, neox: bool, pos_dev=None):
         """Transformer::rope in place on x [S, n_heads*head_dim]."""
         s_rows = x.numel() // (n_heads * head_dim)
@@ -232,6 +244,16 @@ class Context:
         s_rows = k.numel() // kv_width
         self.check(self.lib.kmoe_kv_store(self.h, _ptr(k), _ptr(v), s_rows, kv_width, pos0, _ptr(pos_dev), n_ctx,
                                           _ptr(k_cache), _ptr(v_cache)))
+
+    def rope_kv_store(self, q, k, v, n_head: int, n_kv: int, head_dim: int, rope_dim: int, pos0: int, inv_freq,
+                      neox: bool, n_ctx: int, k_cache, v_cache, pos_dev=None, q_out=None):
+        """RoPE of q (into q_out, returned) and k, then the f16 cache store of k and v."""
+        s_rows = q.numel() // (n_head * head_dim)
+        q_out = self._empty((s_rows, n_head * head_dim), self.torch.float32) if q_out is None else q_out
+        self.check(self.lib.kmoe_rope_kv_store(self.h, _ptr(q), _ptr(k), _ptr(v), s_rows, n_head, n_kv, head_dim,
+                                               rope_dim, pos0, _ptr(pos_dev), _ptr(inv_freq), int(neox), n_ctx,
+                                               _ptr(q_out), _ptr(k_cache), _ptr(v_cache)))
+        return q_out
 
     def attention(self, q, k_cache, v_cache, n_head: int, n_kv: int, head_dim: int, pos0: int, n_ctx: int,
                   pos_dev=None, out=None):

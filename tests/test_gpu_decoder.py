@@ -142,6 +142,71 @@ def test_attention(ctx, orc, nh, nkv, hd, S, pos0):
     assert np.abs(got2 - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("t,rows,cols,S,regime", [(Q4_K, 3072, 2048, 1, 0), (Q8_0, 768, 256, 2, 0),
+                                                  (Q6_K, 1000, 512, 1, 1), (Q4_K, 512, 1024, 5, 0),
+                                                  (Q4_K, 256, 768, 3, 2)])
+def test_norm_matmul_is_rmsnorm_then_matmul(ctx, orc, t, rows, cols, S, regime):
+    """The fused norm (+ int8 rows for the integer path) gives the same bits
+    as kmoe_rmsnorm followed by kmoe_matmul, on every path."""
+    rng = np.random.default_rng(rows + S)
+    w = random_blocks(t, rows, cols, seed=rows)
+    x = rng.standard_normal((S, cols)).astype(np.float32)
+    y = rng.standard_normal((S, cols)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    ctx.set_regime(regime)
+    try:
+        x1, x2 = dev(x), dev(x)
+        got = host(ctx.norm_matmul(x1, dev(nw), 1e-5, t, dev(w), rows, cols, y=dev(y)))
+        h = ctx.rmsnorm(x2, dev(nw), 1e-5, y=dev(y))
+        ref = host(ctx.matmul(t, dev(w), rows, cols, h))
+    finally:
+        ctx.set_regime(0)
+    assert np.array_equal(host(x1), host(x2))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_kv_store_is_rope_then_store(ctx, orc, neox):
+    import torch
+
+    rng = np.random.default_rng(11)
+    S, nh, nkv, hd, rd, n_ctx = 3, 8, 2, 128, 64, 64
+    q = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((S, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((S, nkv * hd)).astype(np.float32)
+    f = orc.rope_inv_freq(10000.0, rd)
+    kc = torch.zeros((n_ctx, nkv * hd), dtype=torch.int16).cuda()
+    vc = torch.zeros_like(kc)
+    pos = torch.tensor([20], dtype=torch.int32).cuda()
+    qo = host(ctx.rope_kv_store(dev(q), dev(k), dev(v), nh, nkv, hd, rd, 1, dev(f), neox, n_ctx, kc, vc, pos_dev=pos))
+    # the same bits as kmoe_rope + kmoe_kv_store; the oracle within rounding of sin/cos
+    q_ref = host(ctx.rope(dev(q), nh, hd, rd, 21, dev(f), neox))
+    k_ref = host(ctx.rope(dev(k), nkv, hd, rd, 21, dev(f), neox))
+    assert np.array_equal(qo, q_ref)
+    ro = orc.rope(q, nh, hd, rd, 21, f, neox)
+    assert np.abs(qo - ro).max() <= 2e-6 * np.abs(ro).max()
+    K, V = host(kc).view(np.uint16), host(vc).view(np.uint16)
+    assert np.array_equal(K[21:24], orc.f16_store(k_ref))
+    assert np.array_equal(V[21:24], orc.f16_store(v))
+    assert not K[:21].any() and not K[24:].any()
+
+
+def test_attention_prefill_past_one_super_chunk_twice(ctx, orc):
+    """300 prompt rows (later rows span two 256-position super-chunks and merge
+    across work-groups), run twice: the handoff counters are zero again after
+    every call."""
+    rng = np.random.default_rng(12)
+    nh, nkv, hd, S, n_ctx = 8, 2, 128, 300, 512
+    kc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
+    vc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
+    q = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    ref = orc.attention(q, kc, vc, nh, nkv, hd, 0)
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    for _ in range(2):
+        got = host(ctx.attention(dev(q), kd, vd, nh, nkv, hd, 0, n_ctx))
+        assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
 def test_swiglu_add_rows_argmax(ctx, orc):
     rng = np.random.default_rng(9)
     g = (rng.standard_normal(5000) * 4).astype(np.float32)
