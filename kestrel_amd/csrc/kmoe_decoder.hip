@@ -191,8 +191,8 @@ __device__ __forceinline__ int64_t position(int64_t pos0, const int32_t *pos_dev
 }
 
 // Transformer::rope (transformer.rs:342-358), in place: one thread per
-// (row, pair); sin and cos of the f32 angle are rounded from double
-// precision (glibc's sinf/cosf are correctly rounded up to rare midpoints).
+// (row, pair); sin and cos of the f32 angle from sincosf (within an ulp of
+// the reference's f32::sin_cos).
 __global__ void __launch_bounds__(256) k_rope(float *__restrict__ x, int64_t s_rows, int n_heads, int hd, int rd,
                                               int64_t pos0, const int32_t *__restrict__ pos_dev,
                                               const float *__restrict__ inv_freq, int neox) {
@@ -203,7 +203,8 @@ __global__ void __launch_bounds__(256) k_rope(float *__restrict__ x, int64_t s_r
   const int i = (int)(g % half);
   const float p = (float)(position(pos0, pos_dev) + s);
   const float ang = p * inv_freq[i];
-  const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
   const int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
   for (int h = 0; h < n_heads; ++h) {
     float *v = x + (s * n_heads + h) * (int64_t)hd;
@@ -231,9 +232,12 @@ __global__ void __launch_bounds__(256) k_kv_store(const float *__restrict__ k, c
 
 // ---------------------------------------------------------------------------
 // RoPE of q and k and the KV cache store in one pass (transformer.rs:406-418):
-// one work-group per row; the row's sin/cos table (from double precision, as
-// in k_rope) is built in LDS, q is rotated into q_out and the rotated k and v
-// go to the caches as f16.
+// work-group (row s, group of 4 heads) builds the row's sin/cos table in LDS
+// (sincosf of the f32 angle, within an ulp of glibc's), then one wave per
+// head: q heads are rotated into q_out, k heads rotated and stored with the
+// matching v head as f16 into the caches.
+constexpr int kRopeHeads = 4;
+
 __global__ void __launch_bounds__(256) k_rope_kv(const float *__restrict__ q, const float *__restrict__ k,
                                                  const float *__restrict__ v, int nh, int nkv, int hd, int rd,
                                                  int64_t pos0, const int32_t *__restrict__ pos_dev,
@@ -244,41 +248,47 @@ __global__ void __launch_bounds__(256) k_rope_kv(const float *__restrict__ q, co
   const int64_t s = blockIdx.x;
   const int half = rd / 2;
   const int64_t p = position(pos0, pos_dev) + s;
-  if (threadIdx.x < half) {
-    const float ang = (float)p * inv_freq[threadIdx.x];
-    sn[threadIdx.x] = (float)sin((double)ang);
-    cs[threadIdx.x] = (float)cos((double)ang);
+  for (int i = threadIdx.x; i < half; i += 256) {
+    const float ang = (float)p * inv_freq[i];
+    float sv, cv;
+    sincosf(ang, &sv, &cv);
+    sn[i] = sv;
+    cs[i] = cv;
   }
   __syncthreads();
-  const int nq = nh * hd, kvw = nkv * hd;
-  // element e of a head: its rotated value from the pair it belongs to
-  auto rot = [&](const float *row, int e) -> float {
-    const int h = e / hd, dd = e - h * hd;
-    if (dd >= rd) return row[e];
-    const float *base = row + h * hd;
-    int i, a, b;
-    bool first;
-    if (neox) {
-      first = dd < half;
-      i = first ? dd : dd - half;
-      a = i;
-      b = i + half;
-    } else {
-      first = (dd & 1) == 0;
-      i = dd >> 1;
-      a = 2 * i;
-      b = 2 * i + 1;
+  const int head = blockIdx.y * kRopeHeads + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (head >= nh + nkv) return;
+  const bool is_q = head < nh;
+  const int kh = head - nh;
+  if (!is_q && (p < 0 || p >= n_ctx)) return;
+  const float *row = is_q ? q + (s * nh + head) * (int64_t)hd : k + (s * nkv + kh) * (int64_t)hd;
+  const int64_t kvw = (int64_t)nkv * hd;
+  for (int dd = lane; dd < hd; dd += 64) {
+    float val = row[dd];
+    if (dd < rd) {
+      int i, a, b;
+      bool first;
+      if (neox) {
+        first = dd < half;
+        i = first ? dd : dd - half;
+        a = i;
+        b = i + half;
+      } else {
+        first = (dd & 1) == 0;
+        i = dd >> 1;
+        a = 2 * i;
+        b = 2 * i + 1;
+      }
+      const float x0 = row[a], x1 = row[b];
+      val = first ? x0 * cs[i] - x1 * sn[i] : x0 * sn[i] + x1 * cs[i];
     }
-    const float x0 = base[a], x1 = base[b];
-    return first ? x0 * cs[i] - x1 * sn[i] : x0 * sn[i] + x1 * cs[i];
-  };
-  const float *qr = q + s * nq;
-  for (int e = threadIdx.x; e < nq; e += 256) q_out[s * nq + e] = rot(qr, e);
-  if (p < 0 || p >= n_ctx) return;
-  const float *kr = k + s * kvw;
-  for (int e = threadIdx.x; e < kvw; e += 256) {
-    kc[p * kvw + e] = __builtin_bit_cast(uint16_t, (_Float16)rot(kr, e));
-    vc[p * kvw + e] = __builtin_bit_cast(uint16_t, (_Float16)v[s * kvw + e]);
+    if (is_q) {
+      q_out[(s * nh + head) * (int64_t)hd + dd] = val;
+    } else {
+      kc[p * kvw + (int64_t)kh * hd + dd] = __builtin_bit_cast(uint16_t, (_Float16)val);
+      vc[p * kvw + (int64_t)kh * hd + dd] =
+          __builtin_bit_cast(uint16_t, (_Float16)v[(s * nkv + kh) * (int64_t)hd + dd]);
+    }
   }
 }
 
@@ -585,8 +595,9 @@ hipError_t launch_rope_kv(hipStream_t st, const float *q, const float *k, const 
                           int nkv, int hd, int rd, int64_t pos0, const int32_t *pos_dev, const float *inv_freq,
                           int neox, int64_t n_ctx, float *q_out, uint16_t *kc, uint16_t *vc) {
   if (s_rows <= 0) return hipSuccess;
-  KMOE_LAUNCH(k_rope_kv, dim3((unsigned)s_rows), dim3(256), 0, st, q, k, v, nh, nkv, hd, rd, pos0, pos_dev, inv_freq,
-              neox, n_ctx, q_out, kc, vc);
+  const unsigned gy = (unsigned)((nh + nkv + kRopeHeads - 1) / kRopeHeads);
+  KMOE_LAUNCH(k_rope_kv, dim3((unsigned)s_rows, gy), dim3(256), 0, st, q, k, v, nh, nkv, hd, rd, pos0, pos_dev,
+              inv_freq, neox, n_ctx, q_out, kc, vc);
   return hipGetLastError();
 }
 

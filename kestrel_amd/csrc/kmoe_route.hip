@@ -499,17 +499,22 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
           group8_quant_q8_block(a.X + b * 32, a.xq + b * 32, a.xd + b, a.xs + b * 2, lane & 7);
       }
     });
-    if (tid == 0) a.logits[(int64_t)s * a.E + e] = r;
+    if (tid == 0) {
+      if (a.done) st_agent(a.logits + (int64_t)s * a.E + e, r);  // read by the last work-group below
+      else a.logits[(int64_t)s * a.E + e] = r;
+    }
   }
   if (!a.done) return;  // logits only: the selection happens in the next kernel
   __syncthreads();
   if (tid == 0) {
-    __threadfence();  // this work-group's logits and int8 rows before the count
-    last = atomicAdd(a.done, 1u) == (uint32_t)(G - 1);
+    // The logits went out with agent-scope stores and the tail reads them
+    // with agent-scope loads, so waiting for this thread's stores suffices
+    // (no cache writeback); the int8 rows are read by later kernels only.
+    vm_wait();
+    last = add_agent(a.done, 1u) == (uint32_t)(G - 1);
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   if (a.E <= 64) route_dec_tail<1>(a, P, sel, first);
   else if (a.E <= 128) route_dec_tail<2>(a, P, sel, first);
   else if (a.E <= 256) route_dec_tail<4>(a, P, sel, first);
