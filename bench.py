@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
                          "decode, Qwen3-shaped layer, expert-tier preload)")
-    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload",
+    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload,decode_stack",
                     help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
                          "q4k_m, qwen3, preload, decode_stack)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
