@@ -77,7 +77,7 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
                                const int8_t *xq, const float *xd, const int32_t *xbs, float *out);
 struct DecSelect;
 // sel: the kernel selects the token's experts from its logits and writes the
-// routing (Q4_K only; hipErrorNotSupported otherwise).
+// routing (hipErrorNotSupported where decode_gate_up_can_select is false).
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
                                  const int32_t *xbs, float *h, const DecSelect *sel = nullptr);

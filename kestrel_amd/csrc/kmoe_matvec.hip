@@ -27,6 +27,7 @@
 // activation bytes with ds_read_b128.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
+#include "kmoe_select.h"
 
 #include <cstdlib>
 #include <type_traits>
@@ -50,6 +51,8 @@ struct MvArgs {
   int regime;
   int rows_per_block;
   int min_rows;  // grouped modes: experts with fewer rows are another kernel's
+  int sel_on;    // M_GATE_UP, one token: select the experts from sel.logits here
+  DecSelect sel;
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -658,6 +661,35 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, c
   }
 }
 
+// One token's routing from its logits by wave 0 of a work-group (the
+// selection of wave_route_one): slot_e[i] = the i-th smallest selected expert
+// (the expert of slot i); work-group 0 also publishes the routing for the
+// kernels that follow.
+__device__ __forceinline__ void mv_select(const DecSelect &q, int lane, int32_t *slot_e, float *P, bool publish) {
+  uint32_t sj[16];
+  float wj[16];
+  if (q.E <= 64) {
+    float lv[1] = {lane < q.E ? q.logits[lane] : -INFINITY};
+    wave_route_one<1>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+  } else if (q.E <= 128) {
+    float lv[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) lv[i] = lane + 64 * i < q.E ? q.logits[lane + 64 * i] : -INFINITY;
+    wave_route_one<2>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+  } else {
+    float lv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lv[i] = lane + 64 * i < q.E ? q.logits[lane + 64 * i] : -INFINITY;
+    wave_route_one<4>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+  }
+  uint32_t rk[16];
+  selection_ranks(sj, q.K, rk);
+  if (lane == 0)
+    for (int j = 0; j < q.K; ++j) slot_e[rk[j]] = (int32_t)sj[j];
+  if (publish)
+    publish_selection(sj, wj, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
+}
+
 template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
 __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   constexpr int RPW = 64 / LPR;
@@ -671,7 +703,17 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   const int64_t xs_stride = cols / 16;
   const int64_t bpe = (rows + RB - 1) / RB;
   int64_t total = bpe;
-  if constexpr (MODE == M_GATE_UP) total = (int64_t)(*a.rt.n_active) * bpe;
+  __shared__ int32_t slot_e[16];
+  __shared__ float selP[256];
+  if constexpr (MODE == M_GATE_UP) {
+    if (a.sel_on) {
+      if (wave == 0) mv_select(a.sel, lane, slot_e, selP, blockIdx.x == 0);
+      __syncthreads();
+      total = (int64_t)a.sel.K * bpe;
+    } else {
+      total = (int64_t)(*a.rt.n_active) * bpe;
+    }
+  }
 
   ActSlice<TYPE> act[TPLMAX];
   if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
@@ -689,8 +731,8 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
     if constexpr (MODE == M_GATE_UP) {
       const int i = (int)(b / bpe);
       rblk = b - (int64_t)i * bpe;
-      const int e = a.rt.active[i];
-      p0 = a.rt.offsets[e];
+      const int e = a.sel_on ? slot_e[i] : a.rt.active[i];
+      p0 = a.sel_on ? i : a.rt.offsets[e];
       const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
       W0 = eb + a.tier.off[0];
       W1 = eb + a.tier.off[1];
@@ -1112,7 +1154,14 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
 }
 
 bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
-  return type == T_Q4_K && E <= 256 && K <= 16 && K <= E && dec_gate_up_tq4_supported(cols, gu_ru());
+  if (E > 256 || K > 16 || K > E) return false;
+  if (type == T_Q4_K && dec_gate_up_tq4_supported(cols, gu_ru())) return true;
+  // the register kernels select too, where their geometry fits the row
+  int lpr, tpl;
+  const int64_t el = is_kquant(type) ? 256 : 32;
+  if (cols % el) return false;
+  return (type == T_Q4_K || type == T_Q6_K || type == T_Q8_0) &&
+         reg_geometry(type, (int)((is_kquant(type) ? 4 : 1) * (cols / el)), lpr, tpl);
 }
 
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
@@ -1127,13 +1176,17 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   a.out = h;
   a.tier = tier;
   a.rt = rt;
+  if (sel) {  // one token: the kernel selects the experts from the logits
+    if (sel->E > 256 || sel->K > 16 || sel->K > sel->E || sel->K != max_active) return hipErrorNotSupported;
+    a.sel_on = 1;
+    a.sel = *sel;
+  }
   if (type == T_Q4_K) {
     const hipError_t e =
         launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel);
-    if (e != hipErrorNotSupported || sel) return e;
+    if (e != hipErrorNotSupported) return e;
     return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
   }
-  if (sel) return hipErrorNotSupported;
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
   return hipErrorInvalidValue;

@@ -33,28 +33,31 @@ __device__ __forceinline__ float hsum8(const float *v) {
   return (a + b) + (c + d);
 }
 
-// Work-group = one weight row e and up to kLgTok activation rows; 16 lanes per
-// logit as above (lanes of the second half-wave pair with the second row).
-// Columns are staged through LDS kLgCh at a time (a multiple of 16, so every
-// element stays in its chain and every chain keeps its order);
-// the chains read LDS, the tails past the last whole group of 8 (or 16) read
-// global memory.
-constexpr int kLgCh = 4096;  // one step for the routers of the shapes here (d <= 4096)
-constexpr int kLgTok = 2;
-
+// Work-group = TE weight rows and TT activation rows: 16 lanes per (row,
+// token) logit as above, TE * TT <= 16 logits. Columns are staged through LDS
+// CH at a time (a multiple of 16, so every element stays in its chain and
+// every chain keeps its order); the chains read LDS, the tails past the last
+// whole group of 8 (or 16) read global memory. Decode batches (S <= 8) take
+// one row and two tokens (many small work-groups); larger batches take 4 x 4
+// tiles, so a row is staged once per 4 tokens and a token once per 4 rows.
+template <int TE, int TT, int CH>
 __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__ W, int32_t E, int64_t d,
                                                        const float *__restrict__ X, int64_t S,
                                                        float *__restrict__ logits, int qdot) {
-  __shared__ __attribute__((aligned(16))) float Wc[kLgCh];
-  __shared__ __attribute__((aligned(16))) float Xc[kLgTok][kLgCh];
+  __shared__ __attribute__((aligned(16))) float Wc[TE][CH];
+  __shared__ __attribute__((aligned(16))) float Xc[TT][CH];
   const bool vec = d % 4 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
   const int tid = threadIdx.x;
-  const int l16 = tid & 15, tok = tid >> 4;
-  const int e = (int)(blockIdx.x % (uint32_t)E);  // blocks: (token block, row) pairs
-  const int64_t s0 = (int64_t)(blockIdx.x / (uint32_t)E) * kLgTok;
-  const int ns = (int)(S - s0 < kLgTok ? S - s0 : kLgTok);
-  const bool valid = tok < ns;
-  const int64_t s = s0 + (valid ? tok : 0);
+  const int l16 = tid & 15, pair = tid >> 4;
+  const int ee = pair / TT, tt = pair % TT;
+  const int ntile_e = (E + TE - 1) / TE;
+  const int e0 = (int)(blockIdx.x % (uint32_t)ntile_e) * TE;  // blocks: (token tile, row tile) pairs
+  const int64_t s0 = (int64_t)(blockIdx.x / (uint32_t)ntile_e) * TT;
+  const int ne = E - e0 < TE ? E - e0 : TE;
+  const int ns = (int)(S - s0 < TT ? S - s0 : TT);
+  const bool valid = ee < ne && tt < ns;
+  const int e = e0 + (valid ? ee : 0);
+  const int64_t s = s0 + (valid ? tt : 0);
   int ord;
   if (qdot || S < 4 || (d % 8) != 0) {
     ord = ORD_QDOT;
@@ -71,36 +74,43 @@ __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__
   const int l = l16 & 7;
   const int off = l16 < 8 ? 0 : 8;
   float acc = 0.0f;
-  for (int64_t c0 = 0; c0 < d; c0 += kLgCh) {
-    const int cw = (int)(d - c0 < kLgCh ? d - c0 : kLgCh);
+  for (int64_t c0 = 0; c0 < d; c0 += CH) {
+    const int cw = (int)(d - c0 < CH ? d - c0 : CH);
     __syncthreads();  // the previous chunk has been read
     if (vec) {  // every 16-byte load of the chunk issued before any is stored
-      constexpr int Q = kLgCh / 4 / 256;
-      float4 rv[1 + kLgTok][Q];
+      constexpr int Q = CH / 4 / 256;
+      float4 rv[TE + TT][Q];
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const int i = 4 * (q * 256 + tid);
-        rv[0][q] = i < cw ? *(const float4 *)(w + c0 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int t = 0; t < kLgTok; ++t)
-          rv[1 + t][q] = i < cw && t < ns ? *(const float4 *)(X + (s0 + t) * d + c0 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int r = 0; r < TE; ++r)
+          rv[r][q] = i < cw && r < ne ? *(const float4 *)(W + (int64_t)(e0 + r) * d + c0 + i)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+          rv[TE + t][q] = i < cw && t < ns ? *(const float4 *)(X + (s0 + t) * d + c0 + i)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const int i = 4 * (q * 256 + tid);
         if (i < cw) {
-          *(float4 *)&Wc[i] = rv[0][q];
 #pragma unroll
-          for (int t = 0; t < kLgTok; ++t) *(float4 *)&Xc[t][i] = rv[1 + t][q];
+          for (int r = 0; r < TE; ++r) *(float4 *)&Wc[r][i] = rv[r][q];
+#pragma unroll
+          for (int t = 0; t < TT; ++t) *(float4 *)&Xc[t][i] = rv[TE + t][q];
         }
       }
     } else {
-      for (int i = tid; i < cw; i += 256) Wc[i] = w[c0 + i];
+      for (int r = 0; r < ne; ++r)
+        for (int i = tid; i < cw; i += 256) Wc[r][i] = W[(int64_t)(e0 + r) * d + c0 + i];
       for (int t = 0; t < ns; ++t)
         for (int i = tid; i < cw; i += 256) Xc[t][i] = X[(s0 + t) * d + c0 + i];
     }
     __syncthreads();
     if (!valid) continue;
+    const float *wr = Wc[ee], *xr = Xc[tt];
     if (ord == ORD_GEMM || ord == ORD_QDOT) {
       if (l16 < 8) {
         const int64_t cb = c0 / 8, ce = (c0 + cw) / 8 < n8 ? (c0 + cw) / 8 : n8;
@@ -108,13 +118,13 @@ __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__
 #pragma unroll 8
           for (int64_t c = cb; c < ce; ++c) {
             const int o = (int)(8 * c - c0) + l16;
-            acc = fmaf(Wc[o], Xc[tok][o], acc);
+            acc = fmaf(wr[o], xr[o], acc);
           }
         } else {
 #pragma unroll 8
           for (int64_t c = cb; c < ce; ++c) {
             const int o = (int)(8 * c - c0) + l16;
-            const float p = Wc[o] * Xc[tok][o];
+            const float p = wr[o] * xr[o];
             acc = acc + p;
           }
         }
@@ -124,7 +134,7 @@ __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__
 #pragma unroll 8
       for (int64_t c = cb; c < ce; ++c) {
         const int o = (int)(16 * c - c0) + off + l;
-        acc = fmaf(Wc[o], Xc[tok][o], acc);
+        acc = fmaf(wr[o], xr[o], acc);
       }
     }
   }
@@ -527,10 +537,16 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
                                 int64_t s_rows, float *logits, bool qdot) {
   if (s_rows * n_expert == 0) return hipSuccess;
-  const int64_t blocks = (s_rows + kLgTok - 1) / kLgTok * n_expert;
+  if (s_rows <= 8) {
+    const int64_t blocks = (s_rows + 1) / 2 * n_expert;
+    KMOE_LAUNCH((k_router_logits<1, 2, 4096>), dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x,
+                s_rows, logits, qdot ? 1 : 0);
+    return hipGetLastError();
+  }
+  const int64_t blocks = (s_rows + 3) / 4 * ((n_expert + 3) / 4);
   if (blocks > (int64_t)INT32_MAX) return hipErrorInvalidValue;
-  KMOE_LAUNCH(k_router_logits, dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x, s_rows, logits,
-                     qdot ? 1 : 0);
+  KMOE_LAUNCH((k_router_logits<4, 4, 1024>), dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x, s_rows,
+              logits, qdot ? 1 : 0);
   return hipGetLastError();
 }
 
