@@ -705,15 +705,6 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   int64_t total = bpe;
   __shared__ int32_t slot_e[16];
   __shared__ float selP[256];
-  if constexpr (MODE == M_GATE_UP) {
-    if (a.sel_on) {
-      if (wave == 0) mv_select(a.sel, lane, slot_e, selP, blockIdx.x == 0);
-      __syncthreads();
-      total = (int64_t)a.sel.K * bpe;
-    } else {
-      total = (int64_t)(*a.rt.n_active) * bpe;
-    }
-  }
 
   ActSlice<TYPE> act[TPLMAX];
   if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
@@ -721,6 +712,15 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
     for (int i = 0; i < TPLMAX; ++i) {
       const int t = lr + i * LPR;
       if (i < tpl && t < ntasks) act_load<TYPE>(act[i], a.xq, a.xd, a.xbs, t);
+    }
+  }
+  if constexpr (MODE == M_GATE_UP) {  // after the activation loads are issued, so the two overlap
+    if (a.sel_on) {
+      if (wave == 0) mv_select(a.sel, lane, slot_e, selP, blockIdx.x == 0);
+      __syncthreads();
+      total = (int64_t)a.sel.K * bpe;
+    } else {
+      total = (int64_t)(*a.rt.n_active) * bpe;
     }
   }
 
