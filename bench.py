@@ -55,9 +55,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
                          "decode, Qwen3-shaped layer, expert-tier preload)")
-    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload,decode_stack",
+    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload,decode_stack,measure",
                     help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
-                         "q4k_m, qwen3, preload, decode_stack)")
+                         "q4k_m, qwen3, preload, decode_stack, measure)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -821,6 +821,8 @@ def main():
         res["tier_preload"] = preload_leg(ctx, torch)
     if "decode_stack" in legs:
         res["decode_stack"] = decode_stack_leg(ctx, torch)
+    if "measure" in legs:  # the figures kestrel's planner would otherwise estimate (kmoe_measure)
+        res["planner_inputs"] = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in ctx.measure().items()}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(ctx, torch, a.cpu_seconds, a.cpu_threads)
         if a.prefill_tokens > 0:

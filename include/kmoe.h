@@ -346,6 +346,33 @@ int kmoe_argmax(kmoe_ctx *ctx, const float *logits_dev, int64_t n, uint32_t *out
  * graph-captured steps). */
 int kmoe_pos_advance(kmoe_ctx *ctx, int32_t *pos_dev, int32_t by);
 
+/* ---- Measured figures for the planner's cost model ----
+ * kestrel's planner prices a GPU tier with Bandwidths.vram / .pcie and a
+ * fixed per-layer overhead (crates/kestrel-planner/src/cost.rs:26-83, :102,
+ * :123), and takes the memory bandwidth from a table of known parts marked
+ * as an estimate (crates/kestrel-hw/src/gpu.rs:28-34, :100-113), because it
+ * has no compute API to measure with. kmoe_measure measures them on the
+ * context's device, as kestrel-hw's bench.rs measures the host
+ * (Measurements, bench.rs:13-25):
+ *   hbm_copy_bps   device-to-device copy, bytes read + written per second
+ *   gemv_bps[i]    decode GEMV (one row, the integer path) weight bytes per
+ *                  second for Q4_K, Q6_K, Q8_0 over 14336 x 4096 matrices
+ *                  rotated past the Infinity Cache: the GPU's counterpart of
+ *                  Measurements.cpu_gemv_bytes_per_s
+ *   h2d_bps/d2h_bps pinned host <-> device copies of 128 MiB
+ *   launch_s       cost of one kernel in a stream of launches
+ * It allocates about 250 MB of device memory (through the VRAM ledger) and
+ * 128 MiB of pinned host memory for the duration of the call, and takes
+ * about half a second. Synchronous. */
+typedef struct {
+  uint64_t vram_total, vram_free;
+  double hbm_copy_bps;
+  double gemv_bps[3]; /* KMOE_Q4_K, KMOE_Q6_K, KMOE_Q8_0 */
+  double h2d_bps, d2h_bps;
+  double launch_s;
+} kmoe_gpu_measurements;
+int kmoe_measure(kmoe_ctx *ctx, kmoe_gpu_measurements *out);
+
 /* Per-kernel timing (0 = off): each kernel is launched with start/stop HIP
  * events taken from its own dispatch packet (hipExtLaunchKernelGGL), on the
  * context's stream. */

@@ -1612,6 +1612,121 @@ int kmoe_pos_advance(kmoe_ctx *c, int32_t *pos_dev, int32_t by) {
   return KMOE_OK;
 }
 
+// ------------------------------------------------------------- measurements for the planner
+
+extern "C++" {
+namespace {
+// Seconds per call of f, from HIP events around `reps` calls on the stream.
+template <class F>
+int time_calls(kmoe_ctx *c, int reps, double *sec, F &&f) {
+  hipEvent_t a = nullptr, b = nullptr;
+  HIP_OK(c, hipEventCreate(&a));
+  HIP_OK(c, hipEventCreate(&b));
+  int rc = KMOE_OK;
+  for (int i = 0; i < 2 && !rc; ++i) rc = f(i);  // warm-up
+  if (!rc) {
+    (void)hipEventRecord(a, c->stream);
+    for (int i = 0; i < reps && !rc; ++i) rc = f(i);
+    (void)hipEventRecord(b, c->stream);
+    (void)hipEventSynchronize(b);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, a, b);
+    *sec = ms * 1e-3 / reps;
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return rc;
+}
+}  // namespace
+}  // extern "C++"
+
+int kmoe_measure(kmoe_ctx *c, kmoe_gpu_measurements *m) {
+  if (!c || !m) return KMOE_E_INVALID;
+  DeviceGuard g(c->device);
+  *m = kmoe_gpu_measurements{};
+  size_t fr = 0, tot = 0;
+  HIP_OK(c, hipMemGetInfo(&fr, &tot));
+  m->vram_total = tot;
+  m->vram_free = fr;
+  // Four copies of a Mixtral-sized expert matrix (14336 x 4096), rotated so
+  // repeats miss the 256 MB Infinity Cache; the same buffer serves the copy.
+  constexpr int64_t kRows = 14336, kCols = 4096, kCopies = 4;
+  const int types[3] = {KMOE_Q4_K, KMOE_Q6_K, KMOE_Q8_0};
+  size_t mat = 0;  // room for the largest of the three matrices (Q8_0: 34 bytes per 32 weights)
+  for (int t : types) mat = std::max(mat, (size_t)kRows * (size_t)bytes_for(t, kCols));
+  const size_t buf = mat * kCopies;
+  const size_t pb = std::min(buf, size_t(128) << 20);  // the PCIe copies land in the same buffer
+  void *w = nullptr;
+  int rc = dev_alloc(c, buf, &w, "measurement");
+  if (rc) return rc;
+  auto done = [&](int r) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(w);
+    release(c, buf);
+    return r;
+  };
+  if (hipMemsetAsync(w, 0x11, buf, c->stream) != hipSuccess) return done(fail(c, KMOE_E_HIP, "memset"));
+  // device copy: half the buffer onto the other half
+  double sec = 0.0;
+  rc = time_calls(c, 10, &sec, [&](int) -> int {
+    HIP_OK(c, hipMemcpyAsync((uint8_t *)w + buf / 2, w, buf / 2, hipMemcpyDeviceToDevice, c->stream));
+    return KMOE_OK;
+  });
+  if (rc) return done(rc);
+  m->hbm_copy_bps = (double)buf / sec;  // bytes read + bytes written
+  // decode GEMV (one activation row) per type: weight bytes per second
+  float *x = nullptr, *out = nullptr;
+  rc = ensure_ws(c, 0);
+  const int64_t pf = gemm_f32_part_floats(kRows, kCols, 1, 1, 1);
+  size_t need = 0;
+  carve_qrows(nullptr, 1, kCols, &need, pf);
+  need += align_up((size_t)kCols * 4) + align_up((size_t)kRows * 4);
+  if (!rc) rc = ensure_ws(c, need);
+  if (rc) return done(rc);
+  QRows qr = carve_qrows(c->ws, 1, kCols, &need, pf);
+  x = (float *)(c->ws + need);
+  out = (float *)(c->ws + need + align_up((size_t)kCols * 4));
+  if (hipMemsetAsync(x, 0, (size_t)kCols * 4, c->stream) != hipSuccess) return done(fail(c, KMOE_E_HIP, "memset"));
+  for (int i = 0; i < 3; ++i) {
+    const int t = types[i];
+    const size_t tb = (size_t)kRows * (size_t)bytes_for(t, kCols);  // <= mat: copy k ends by (k + 1) * mat
+    const int saved = c->regime;
+    c->regime = KMOE_REGIME_AVX2;  // one row: the integer path, as a decode step takes it
+    rc = time_calls(c, 20, &sec, [&](int k) -> int {
+      return matmul_core(c, t, (const uint8_t *)w + (size_t)(k % kCopies) * mat, kRows, kCols, x, 1, out, qr);
+    });
+    c->regime = saved;
+    if (rc) return done(rc);
+    m->gemv_bps[i] = (double)tb / sec;
+  }
+  // launch cost: a stream of minimal kernels, per launch
+  rc = time_calls(c, 200, &sec, [&](int) -> int {
+    HIP_OK(c, launch_pos_advance(c->stream, (int32_t *)out, 0));
+    return KMOE_OK;
+  });
+  if (rc) return done(rc);
+  m->launch_s = sec;
+  // PCIe: a pinned host buffer of pb <= buf bytes each way
+  void *host = nullptr;
+  if (hipHostMalloc(&host, pb, hipHostMallocDefault) != hipSuccess)
+    return done(fail(c, KMOE_E_HIP, "hipHostMalloc(%zu)", pb));
+  rc = time_calls(c, 4, &sec, [&](int) -> int {
+    HIP_OK(c, hipMemcpyAsync(w, host, pb, hipMemcpyHostToDevice, c->stream));
+    return KMOE_OK;
+  });
+  if (!rc) {
+    m->h2d_bps = (double)pb / sec;
+    rc = time_calls(c, 4, &sec, [&](int) -> int {
+      HIP_OK(c, hipMemcpyAsync(host, w, pb, hipMemcpyDeviceToHost, c->stream));
+      return KMOE_OK;
+    });
+    if (!rc) m->d2h_bps = (double)pb / sec;
+  }
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipHostFree(host);
+  return done(rc);
+}
+
 // ------------------------------------------------------------- profiling
 
 int kmoe_profile_enable(kmoe_ctx *c, int on) {

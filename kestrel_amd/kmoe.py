@@ -21,6 +21,14 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256,
 
 STATUS = {0: "OK", -1: "INVALID", -2: "UNSUPPORTED", -3: "BUDGET", -4: "HIP", -5: "NOT_LOADED"}
 
+class GpuMeasurements(C.Structure):
+    """kmoe_gpu_measurements (include/kmoe.h)."""
+
+    _fields_ = [("vram_total", C.c_uint64), ("vram_free", C.c_uint64), ("hbm_copy_bps", C.c_double),
+                ("gemv_bps", C.c_double * 3), ("h2d_bps", C.c_double), ("d2h_bps", C.c_double),
+                ("launch_s", C.c_double)]
+
+
 # Every symbol include/kmoe.h declares, with (restype, argtypes).
 _P, _i32, _i64, _u32, _u64, _sz, _f = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -79,6 +87,7 @@ SIGNATURES = {
     "kmoe_add_rows": (C.c_int, [_P, _P, _P, _i64, _i64]),
     "kmoe_argmax": (C.c_int, [_P, _P, _i64, _P, _P, _i32]),
     "kmoe_pos_advance": (C.c_int, [_P, _P, _i32]),
+    "kmoe_measure": (C.c_int, [_P, _P]),
     "kmoe_profile_enable": (C.c_int, [_P, C.c_int]),
     "kmoe_profile_read": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(_i64)]),
 }
@@ -421,6 +430,14 @@ class Context:
         if gate_inp is not None:
             g = np.ascontiguousarray(gate_inp, dtype=np.float32)
             self.check(self.lib.kmoe_shared_gate_upload(self.h, layer, g.ctypes.data, g.nbytes))
+
+    def measure(self) -> dict:
+        """kmoe_measure: the GPU figures kestrel's planner would otherwise estimate."""
+        m = GpuMeasurements()
+        self.check(self.lib.kmoe_measure(self.h, C.byref(m)))
+        return {"vram_total": m.vram_total, "vram_free": m.vram_free, "hbm_copy_bps": m.hbm_copy_bps,
+                "gemv_bps": {"Q4_K": m.gemv_bps[0], "Q6_K": m.gemv_bps[1], "Q8_0": m.gemv_bps[2]},
+                "h2d_bps": m.h2d_bps, "d2h_bps": m.d2h_bps, "launch_s": m.launch_s}
 
     def bytes_per_expert(self, layer: int) -> int:
         v = _u64()
