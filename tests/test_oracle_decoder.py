@@ -147,3 +147,113 @@ def test_argmax_first_of_ties_and_nan():
     assert orc.argmax(np.array([np.nan, 1, 2], np.float32)) == 0  # every comparison with NaN fails
     x = np.random.default_rng(6).standard_normal(32000).astype(np.float32)
     assert orc.argmax(x) == int(np.argmax(x))
+
+
+def _f32_model(rng, arch, n_layer, d, nh, nkv, hd, ff, vocab, bias, qk_norm, rope_dim):
+    """A dense decoder with F32 weights: hp, tensors (GGUF names) and the same
+    weights as float64 arrays."""
+    W, T = {}, {}
+
+    def add(name, a):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        W[name] = a.astype(np.float64)
+        dims = [a.shape[-1]] + ([a.shape[0]] if a.ndim == 2 else [])
+        T[name] = (0, dims, a.view(np.uint8).reshape(-1))
+
+    add("token_embd.weight", rng.standard_normal((vocab, d)))
+    add("output_norm.weight", 1 + 0.1 * rng.standard_normal(d))
+    add("output.weight", 0.05 * rng.standard_normal((vocab, d)))
+    for l in range(n_layer):
+        p = f"blk.{l}."
+        add(p + "attn_norm.weight", 1 + 0.1 * rng.standard_normal(d))
+        add(p + "ffn_norm.weight", 1 + 0.1 * rng.standard_normal(d))
+        add(p + "attn_q.weight", 0.08 * rng.standard_normal((nh * hd, d)))
+        add(p + "attn_k.weight", 0.08 * rng.standard_normal((nkv * hd, d)))
+        add(p + "attn_v.weight", 0.05 * rng.standard_normal((nkv * hd, d)))
+        add(p + "attn_output.weight", 0.05 * rng.standard_normal((d, nh * hd)))
+        if bias:
+            for n, w in (("q", nh * hd), ("k", nkv * hd), ("v", nkv * hd)):
+                add(p + f"attn_{n}.bias", 0.1 * rng.standard_normal(w))
+        if qk_norm:
+            add(p + "attn_q_norm.weight", 1 + 0.1 * rng.standard_normal(hd))
+            add(p + "attn_k_norm.weight", 1 + 0.1 * rng.standard_normal(hd))
+        add(p + "ffn_gate.weight", 0.05 * rng.standard_normal((ff, d)))
+        add(p + "ffn_up.weight", 0.05 * rng.standard_normal((ff, d)))
+        add(p + "ffn_down.weight", 0.05 * rng.standard_normal((d, ff)))
+    hp = dict(arch=arch, n_layer=n_layer, n_embd=d, n_head=nh, n_head_kv=nkv, head_dim=hd, rope_dim=rope_dim,
+              rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=64, n_batch=5)
+    return hp, T, W
+
+
+class _Float64Decoder:
+    """forward_chunk_inner (transformer.rs:375-467) written out in float64
+    numpy: matrix products, complex rotations for RoPE, scipy's softmax, the
+    KV history kept as float16 (the cache's precision)."""
+
+    def __init__(self, hp, W):
+        self.hp, self.W = hp, W
+        self.kc = [[] for _ in range(hp["n_layer"])]
+        self.vc = [[] for _ in range(hp["n_layer"])]
+        rd = hp["rope_dim"]
+        e32 = (-(2.0 * np.arange(rd // 2, dtype=np.float32)) / np.float32(rd)).astype(np.float32)
+        self.inv = np.float64(np.float32(hp["rope_freq_base"])) ** e32.astype(np.float64)
+        self.pos = 0
+
+    def norm(self, x, w):
+        return x / np.sqrt((x ** 2).mean(axis=-1, keepdims=True) + self.hp["rms_eps"]) * w
+
+    def rope(self, x, n_heads, pos):
+        hd, rd = self.hp["head_dim"], self.hp["rope_dim"]
+        y = x.reshape(n_heads, hd).copy()
+        half = rd // 2
+        a = np.arange(half) if self.hp["arch"] != "llama" else 2 * np.arange(half)
+        b = a + half if self.hp["arch"] != "llama" else a + 1
+        z = (y[:, a] + 1j * y[:, b]) * np.exp(1j * pos * self.inv)[None, :]
+        y[:, a], y[:, b] = z.real, z.imag
+        return y.reshape(-1)
+
+    def forward(self, tokens):
+        hp, W = self.hp, self.W
+        nh, nkv, hd = hp["n_head"], hp["n_head_kv"], hp["head_dim"]
+        for tok in tokens:  # one row at a time: causal attention makes rows independent of later ones
+            x = W["token_embd.weight"][tok].copy()
+            for l in range(hp["n_layer"]):
+                p = f"blk.{l}."
+                h = self.norm(x, W[p + "attn_norm.weight"])
+                q, k, v = (W[p + f"attn_{n}.weight"] @ h for n in "qkv")
+                if p + "attn_q.bias" in W:
+                    q, k, v = q + W[p + "attn_q.bias"], k + W[p + "attn_k.bias"], v + W[p + "attn_v.bias"]
+                if p + "attn_q_norm.weight" in W:
+                    q = self.norm(q.reshape(nh, hd), W[p + "attn_q_norm.weight"]).reshape(-1)
+                    k = self.norm(k.reshape(nkv, hd), W[p + "attn_k_norm.weight"]).reshape(-1)
+                q, k = self.rope(q, nh, self.pos), self.rope(k, nkv, self.pos)
+                self.kc[l].append(k.astype(np.float16).astype(np.float64))
+                self.vc[l].append(v.astype(np.float16).astype(np.float64))
+                K = np.stack(self.kc[l]).reshape(-1, nkv, hd)
+                V = np.stack(self.vc[l]).reshape(-1, nkv, hd)
+                att = np.empty(nh * hd)
+                for hh in range(nh):
+                    g = hh // (nh // nkv)
+                    att[hh * hd:(hh + 1) * hd] = softmax(K[:, g, :] @ q[hh * hd:(hh + 1) * hd] / np.sqrt(hd)) @ V[:, g, :]
+                x = x + W[p + "attn_output.weight"] @ att
+                h = self.norm(x, W[p + "ffn_norm.weight"])
+                gte, up = W[p + "ffn_gate.weight"] @ h, W[p + "ffn_up.weight"] @ h
+                x = x + W[p + "ffn_down.weight"] @ (gte / (1 + np.exp(-gte)) * up)
+            self.pos += 1
+        return W["output.weight"] @ self.norm(x, W["output_norm.weight"])
+
+
+@pytest.mark.parametrize("arch,bias,qk_norm,nkv,rope_dim", [("llama", False, False, 2, 64), ("qwen2", True, False, 1, 32),
+                                                           ("qwen3", False, True, 4, 64)])
+def test_transformer_composition_matches_float64(arch, bias, qk_norm, nkv, rope_dim):
+    """The oracle's Transformer (the composition of the pinned parts, in
+    forward_chunk_inner's order) against the same decoder written out in
+    float64, on F32 weights in the exact regime: a prompt chunked by n_batch
+    and then single tokens, every logit within 1e-4 of the scale."""
+    rng = np.random.default_rng(len(arch) + nkv)
+    hp, T, W = _f32_model(rng, arch, 2, 128, 4, nkv, 64, 256, 300, bias, qk_norm, rope_dim)
+    ref = orc.Transformer(hp, T, regime=orc.REGIME_EXACT)
+    f64 = _Float64Decoder(hp, W)
+    for toks in ([3, 17, 5, 99, 250, 7, 1, 2], [11], [200], [0]):
+        a, b = ref.forward(toks), f64.forward(toks)
+        assert np.abs(a - b).max() <= 1e-4 * max(1.0, np.abs(b).max()), (arch, len(toks), np.abs(a - b).max())
