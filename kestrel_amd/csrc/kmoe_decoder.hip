@@ -318,6 +318,7 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   constexpr int KV4 = HD / 8;   // uint4 pieces (8 halves) per K row
   constexpr int DPL = HD / 64;  // head dims per lane
   __shared__ uint32_t last;
+  __shared__ __attribute__((aligned(16))) float Qs[kMaxGroup][HD];
   const int64_t bid = blockIdx.x;
   const int c = (int)(bid % nch_grid);
   const int64_t s = (bid / nch_grid) % s_rows;
@@ -331,15 +332,17 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   const int64_t kvw = (int64_t)nkv * HD;
   const int64_t p0 = (int64_t)c * kAttnChunk;
   const int np = (int)(n - p0 < kAttnChunk ? n - p0 : kAttnChunk);
+  // q of the group's heads into LDS, issued first so it overlaps the K/V loads
+  for (int e = threadIdx.x; e < group * HD; e += 256) Qs[e / HD][e % HD] = q[(s * nh + (int64_t)g * group) * HD + e];
+  uint4 kr[KV4];
+  uint32_t vr[DPL == 2 ? 64 : 1];
+  uint16_t vh[DPL == 1 ? 64 : 1];
   if (wave < group) {
-    uint4 kr[KV4];
     if (lane < np) {
       const uint4 *src = (const uint4 *)(kc + (p0 + lane) * kvw + (int64_t)g * HD);
 #pragma unroll
       for (int j = 0; j < KV4; ++j) kr[j] = src[j];
     }
-    uint32_t vr[DPL == 2 ? 64 : 1];
-    uint16_t vh[DPL == 1 ? 64 : 1];
 #pragma unroll
     for (int j = 0; j < 64; ++j) {
       if (j < np) {
@@ -348,10 +351,13 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
         else vh[j] = vrow[lane];
       }
     }
+  }
+  __syncthreads();  // Qs
+  if (wave < group) {
     const float scale = 1.0f / sqrtf((float)HD);
     for (int hh = wave; hh < group; hh += 4) {
       const int64_t h = (int64_t)g * group + hh;
-      const float *qh = q + (s * nh + h) * HD;
+      const float *qh = Qs[hh];
       float sc_ = -INFINITY;
       if (lane < np) {
         float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -413,17 +419,40 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   for (int hh = wave; hh < group; hh += 4) {
     const int64_t h = (int64_t)g * group + hh;
     const float *pb = part + (s * nh + h) * nch_grid * (HD + 2);
+    // the partials of 8 chunks at a time, every load issued before any use
+    constexpr int B = 8;
     float M = -INFINITY;
-    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ld_agent(pb + cc * (HD + 2)));
+    for (int c0 = 0; c0 < nch; c0 += B) {
+      float mv[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) mv[j] = c0 + j < nch ? ld_agent(pb + (c0 + j) * (HD + 2)) : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < B; ++j) M = fmaxf(M, mv[j]);
+    }
     float L = 0.0f, O[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) O[i] = 0.0f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float *pc = pb + cc * (HD + 2);
-      const float f = expf(ld_agent(pc) - M);
-      L += ld_agent(pc + 1) * f;
+    for (int c0 = 0; c0 < nch; c0 += B) {
+      float mv[B], lv[B], ov[B][DPL];
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) O[i] += ld_agent(pc + 2 + lane * DPL + i) * f;
+      for (int j = 0; j < B; ++j) {
+        if (c0 + j < nch) {
+          const float *pc = pb + (c0 + j) * (HD + 2);
+          mv[j] = ld_agent(pc);
+          lv[j] = ld_agent(pc + 1);
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) ov[j][i] = ld_agent(pc + 2 + lane * DPL + i);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        if (c0 + j < nch) {
+          const float f = expf(mv[j] - M);
+          L += lv[j] * f;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) O[i] += ov[j][i] * f;
+        }
+      }
     }
     const float inv = 1.0f / L;
 #pragma unroll
