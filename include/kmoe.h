@@ -324,6 +324,17 @@ int kmoe_kv_store(kmoe_ctx *ctx, const float *k_dev, const float *v_dev, int64_t
 int kmoe_attention(kmoe_ctx *ctx, const float *q_dev, const uint16_t *k_cache_dev, const uint16_t *v_cache_dev,
                    int64_t s_rows, int32_t n_head, int32_t n_kv, int32_t head_dim, int64_t pos0,
                    const int32_t *pos_dev, int64_t n_ctx, float *out_dev);
+/* Transformer::attention then the output projection, self.mm(attn_output)
+ * (transformer.rs:419-424): attn_dev receives the attention rows as
+ * kmoe_attention writes them, out_dev [s_rows, rows] the projection as
+ * kmoe_matmul computes it. Where the context's regime takes the integer
+ * path, the attention kernel also writes the int8 rows the matvec reads, one
+ * pass fewer; the results are bit-identical to kmoe_attention followed by
+ * kmoe_matmul. */
+int kmoe_attention_matmul(kmoe_ctx *ctx, const float *q_dev, const uint16_t *k_cache_dev,
+                          const uint16_t *v_cache_dev, int64_t s_rows, int32_t n_head, int32_t n_kv, int32_t head_dim,
+                          int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, float *attn_dev, int ggml_type,
+                          const void *w_dev, size_t w_len, int64_t rows, float *out_dev);
 /* RoPE of q and k followed by the KV cache store (transformer.rs:406-418) in
  * one pass: q is rotated into q_out [s_rows, n_head * head_dim] (q_out must
  * not overlap q), k is rotated and stored with v as f16 at rows position + s

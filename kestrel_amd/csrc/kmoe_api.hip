@@ -1555,6 +1555,59 @@ int kmoe_attention(kmoe_ctx *c, const float *q, const uint16_t *k_cache, const u
   return KMOE_OK;
 }
 
+int kmoe_attention_matmul(kmoe_ctx *c, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                          int64_t s_rows, int32_t n_head, int32_t n_kv, int32_t head_dim, int64_t pos0,
+                          const int32_t *pos_dev, int64_t n_ctx, float *attn, int t, const void *w, size_t w_len,
+                          int64_t rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
+    return fail(c, KMOE_E_INVALID, "attention: need n_head %% n_kv == 0 and n_ctx > 0");
+  if (!attn_supported(head_dim, n_head / n_kv))
+    return fail(c, KMOE_E_UNSUPPORTED, "head_dim %d, %d query heads per kv head (kernels: 64 or 128, <= 16)",
+                head_dim, n_head / n_kv);
+  const int64_t cols = (int64_t)n_head * head_dim;
+  const int64_t rb = bytes_for(t, cols);
+  if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
+  if (rb < 0 || rows < 0) return fail(c, KMOE_E_INVALID, "output projection shape");
+  if ((uint64_t)w_len < (uint64_t)rb * (uint64_t)rows)
+    return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows, (long long)rb);
+  int rc = check_pos(c, pos0, pos_dev, s_rows, n_ctx);
+  if (rc) return rc;
+  if (s_rows == 0) return KMOE_OK;
+  if (!q || !k_cache || !v_cache || !attn || !w || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  if (t != KMOE_F32) {
+    rc = check_quant_shape(c, t, cols);
+    if (rc) return rc;
+  }
+  const int supers = attn_supers(pos_dev ? n_ctx : std::min(n_ctx, pos0 + s_rows));
+  rc = ensure_aws(c, (size_t)s_rows * n_kv, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
+  if (rc) return rc;
+  const int64_t pf = gemm_f32_part_floats(rows, cols, 1, s_rows, s_rows);
+  size_t need = 0;
+  carve_qrows(nullptr, s_rows, cols, &need, pf);
+  rc = ensure_ws(c, need);
+  if (rc) return rc;
+  QRows qr = carve_qrows(c->ws, s_rows, cols, &need, pf);
+  float *part = (float *)(c->aws + c->aws_counters);
+  uint32_t *counters = (uint32_t *)c->aws;
+  // Where the projection takes the integer path, the attention kernel writes
+  // its int8 rows too (same values as the projection's own quantization).
+  const int qt = t != KMOE_F32 && int_path(c->regime, s_rows) && rows > 0 ? (is_kq(t) ? 1 : 2) : 0;
+  if (qt) {
+    hipError_t e = timed(c, "attention_q8", [&]() {
+      return launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0, pos_dev, n_ctx,
+                              supers, part, counters, attn, qt, qr.q, qr.d, qr.s);
+    });
+    if (e == hipSuccess) return matvec_q8_impl(c, t, (const uint8_t *)w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
+  LAUNCH(c, "attention", launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0,
+                                          pos_dev, n_ctx, supers, part, counters, attn));
+  if (rows == 0) return KMOE_OK;
+  return matmul_core(c, t, (const uint8_t *)w, rows, cols, attn, s_rows, out, qr);
+}
+
 int kmoe_rope_kv_store(kmoe_ctx *c, const float *q, const float *k, const float *v, int64_t s_rows, int32_t n_head,
                        int32_t n_kv, int32_t head_dim, int32_t rope_dim, int64_t pos0, const int32_t *pos_dev,
                        const float *inv_freq, int32_t neox, int64_t n_ctx, float *q_out, uint16_t *k_cache,

@@ -309,16 +309,45 @@ __global__ void __launch_bounds__(256) k_rope_kv(const float *__restrict__ q, co
 constexpr int kAttnChunk = 64;
 constexpr int kMaxGroup = 16;
 
+// The int8 rows of the attention output for the projection after it: the
+// group's group * HD outputs of row s (staged in LDS) are whole Q8_K blocks
+// (qt 1, group * HD % 256 == 0: one wave per block) or Q8 blocks (qt 2, eight
+// lanes per block), quantized as the matmul's own quantization kernel would.
+template <int HD>
+__device__ __forceinline__ void attn_quant_group(const float *os, int group, int64_t s, int g, int nh, int qt,
+                                                 int8_t *xq, float *xd, int32_t *xs) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)nh * HD, gb = (int64_t)g * group * HD;
+  const int nv = group * HD;
+  if (qt == 1) {
+    for (int b = wave; b < nv / 256; b += 4) {
+      const float4 v = *(const float4 *)(os + 256 * b + 4 * lane);
+      const int64_t blk = (gb / 256) + b;
+      wave_quant_q8k_vals(v, xq + s * row + 256 * blk, xd + s * (row / 256) + blk, xs + s * (row / 16) + 16 * blk,
+                          lane);
+    }
+  } else {
+    for (int b = wave * 8 + (lane >> 3); b < nv / 32; b += 32) {
+      const float4 v = *(const float4 *)(os + 32 * b + 4 * (lane & 7));
+      const int64_t blk = (gb / 32) + b;
+      group8_quant_q8_vals(v, xq + s * row + 32 * blk, xd + s * (row / 32) + blk, xs + s * (row / 16) + 2 * blk,
+                           lane & 7);
+    }
+  }
+}
+
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                   const uint16_t *__restrict__ vc, int64_t s_rows, int nh, int nkv,
                                                   int64_t pos0, const int32_t *__restrict__ pos_dev, int64_t n_ctx,
                                                   int nch_grid, float *part, uint32_t *counters,
-                                                  float *__restrict__ out) {
+                                                  float *__restrict__ out, int qt, int8_t *__restrict__ xq,
+                                                  float *__restrict__ xd, int32_t *__restrict__ xs) {
   constexpr int KV4 = HD / 8;   // uint4 pieces (8 halves) per K row
   constexpr int DPL = HD / 64;  // head dims per lane
   __shared__ uint32_t last;
   __shared__ __attribute__((aligned(16))) float Qs[kMaxGroup][HD];
+  __shared__ __attribute__((aligned(16))) float Os[kMaxGroup][HD];  // the group's outputs, for qt
   const int64_t bid = blockIdx.x;
   const int c = (int)(bid % nch_grid);
   const int64_t s = (bid / nch_grid) % s_rows;
@@ -398,7 +427,11 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
       if (nch == 1) {
         const float inv = 1.0f / l;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) out[(s * nh + h) * HD + lane * DPL + i] = o[i] * inv;
+        for (int i = 0; i < DPL; ++i) {
+          const float r = o[i] * inv;
+          out[(s * nh + h) * HD + lane * DPL + i] = r;
+          Os[hh][lane * DPL + i] = r;
+        }
       } else {
         float *pp = part + ((s * nh + h) * nch_grid + c) * (HD + 2);
         if (lane == 0) {
@@ -410,7 +443,13 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
       }
     }
   }
-  if (nch == 1) return;
+  if (nch == 1) {
+    if (qt) {
+      __syncthreads();
+      attn_quant_group<HD>(&Os[0][0], group, s, g, nh, qt, xq, xd, xs);
+    }
+    return;
+  }
   vm_wait();  // this wave's partials are written before the counter moves
   __syncthreads();
   if (threadIdx.x == 0) last = add_agent(counters + s * nkv + g, 1u);
@@ -456,9 +495,17 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
     }
     const float inv = 1.0f / L;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) out[(s * nh + h) * HD + lane * DPL + i] = O[i] * inv;
+    for (int i = 0; i < DPL; ++i) {
+      const float r = O[i] * inv;
+      out[(s * nh + h) * HD + lane * DPL + i] = r;
+      Os[hh][lane * DPL + i] = r;
+    }
   }
   if (threadIdx.x == 0) st_agent(counters + s * nkv + g, 0u);  // ready for the next call
+  if (qt) {
+    __syncthreads();
+    attn_quant_group<HD>(&Os[0][0], group, s, g, nh, qt, xq, xd, xs);
+  }
 }
 
 // Dense SwiGLU (transformer.rs:455): out = g / (1 + exp(-g)) * u.
@@ -606,15 +653,17 @@ bool attn_supported(int hd, int group) { return (hd == 64 || hd == 128) && group
 
 hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
                             int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int supers,
-                            float *part, uint32_t *counters, float *out) {
+                            float *part, uint32_t *counters, float *out, int qt, int8_t *xq, float *xd,
+                            int32_t *xs) {
   if (s_rows <= 0) return hipSuccess;
+  if (qt == 1 && ((nh / nkv) * hd) % 256 != 0) return hipErrorNotSupported;
   const unsigned grid = (unsigned)((int64_t)nkv * s_rows * supers);
   if (hd == 64)
     KMOE_LAUNCH(k_attn_dec<64>, dim3(grid), dim3(256), 0, st, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx,
-                supers, part, counters, out);
+                supers, part, counters, out, qt, xq, xd, xs);
   else if (hd == 128)
     KMOE_LAUNCH(k_attn_dec<128>, dim3(grid), dim3(256), 0, st, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx,
-                supers, part, counters, out);
+                supers, part, counters, out, qt, xq, xd, xs);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

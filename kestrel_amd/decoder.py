@@ -177,8 +177,9 @@ class Decoder:
             ctx.rmsnorm(k, L["k_norm"], self.eps, out=k)
         qr = ctx.rope_kv_store(q, k, v, nh, nkv, hd, self.rd, pos0, self.inv_freq, self.neox, self.n_ctx, L["kc"],
                                L["vc"], pos_dev)
-        a = ctx.attention(qr, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, pos_dev)
-        o = self._mm(L["wo"], a)
+        ty, dims, t = L["wo"]
+        o = ctx.attention_matmul(qr, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, ty, t,
+                                 int(np.prod(dims[1:])), pos_dev)
         if "moe" in L:
             h = ctx.rmsnorm(x, L["ffn_norm"], self.eps, y=o)  # x += o, then the norm of x
             return ctx.moe_ffn(L["moe"], h)

@@ -81,6 +81,8 @@ SIGNATURES = {
     "kmoe_rope": (C.c_int, [_P, _P, _i64, _i32, _i32, _i32, _i64, _P, _P, _i32]),
     "kmoe_kv_store": (C.c_int, [_P, _P, _P, _i64, _i64, _i64, _P, _i64, _P, _P]),
     "kmoe_attention": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i64, _P, _i64, _P]),
+    "kmoe_attention_matmul": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i64, _P, _i64, _P, C.c_int, _P,
+                                        _sz, _i64, _P]),
     "kmoe_rope_kv_store": (C.c_int, [_P, _P, _P, _P, _i64, _i32, _i32, _i32, _i32, _i64, _P, _P, _i32, _i64, _P,
                                      _P, _P]),
     "kmoe_swiglu": (C.c_int, [_P, _P, _P, _i64, _P]),
@@ -271,6 +273,17 @@ class Context:
         out = self._empty((s_rows, n_head * head_dim), self.torch.float32) if out is None else out
         self.check(self.lib.kmoe_attention(self.h, _ptr(q), _ptr(k_cache), _ptr(v_cache), s_rows, n_head, n_kv,
                                            head_dim, pos0, _ptr(pos_dev), n_ctx, _ptr(out)))
+        return out
+
+    def attention_matmul(self, q, k_cache, v_cache, n_head: int, n_kv: int, head_dim: int, pos0: int, n_ctx: int,
+                         t: int, w, rows: int, pos_dev=None, attn=None):
+        """Transformer::attention then self.mm(attn_output): -> [S, rows]."""
+        s_rows = q.numel() // (n_head * head_dim)
+        attn = self._empty((s_rows, n_head * head_dim), self.torch.float32) if attn is None else attn
+        out = self._empty((s_rows, rows), self.torch.float32)
+        self.check(self.lib.kmoe_attention_matmul(self.h, _ptr(q), _ptr(k_cache), _ptr(v_cache), s_rows, n_head, n_kv,
+                                                  head_dim, pos0, _ptr(pos_dev), n_ctx, _ptr(attn), t, _ptr(w),
+                                                  w.numel() * w.element_size(), rows, _ptr(out)))
         return out
 
     def swiglu(self, g, u, out=None):

@@ -191,6 +191,29 @@ def test_rope_kv_store_is_rope_then_store(ctx, orc, neox):
     assert not K[:21].any() and not K[24:].any()
 
 
+@pytest.mark.parametrize("t,S,pos0,regime", [(Q4_K, 1, 10, 0), (Q4_K, 1, 300, 0), (Q8_0, 2, 70, 0), (Q6_K, 1, 5, 1),
+                                             (Q4_K, 5, 0, 0), (Q4_K, 1, 130, 2)])
+def test_attention_matmul_is_attention_then_matmul(ctx, orc, t, S, pos0, regime):
+    """The int8 rows written by the attention kernel feed the projection with
+    the same bits as kmoe_attention followed by kmoe_matmul, with one chunk or
+    several (the merged path), on every regime's path."""
+    rng = np.random.default_rng(pos0 + S)
+    nh, nkv, hd, n_ctx, rows = 16, 4, 128, 512, 512
+    kc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
+    vc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
+    q = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    w = random_blocks(t, rows, nh * hd, seed=5)
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    ctx.set_regime(regime)
+    try:
+        got = host(ctx.attention_matmul(dev(q), kd, vd, nh, nkv, hd, pos0, n_ctx, t, dev(w), rows))
+        a = ctx.attention(dev(q), kd, vd, nh, nkv, hd, pos0, n_ctx)
+        ref = host(ctx.matmul(t, dev(w), rows, nh * hd, a))
+    finally:
+        ctx.set_regime(0)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_attention_prefill_past_one_super_chunk_twice(ctx, orc):
     """300 prompt rows (later rows span two 256-position super-chunks and merge
     across work-groups), run twice: the handoff counters are zero again after
