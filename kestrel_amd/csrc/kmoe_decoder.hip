@@ -535,11 +535,21 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ l, in
   __shared__ int64_t bi[16];
   float v = -INFINITY;
   int64_t idx = -1;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) {
-    const float x = l[i];
-    if (!isnan(x) && (idx < 0 || x > v)) {  // strided scan: ascending i, first max kept
-      v = x;
-      idx = i;
+  constexpr int U = 8;  // values loaded per thread before any is compared
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 1024 * U) {
+    float xs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * 1024;
+      xs[u] = i < n ? l[i] : __builtin_nanf("");
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {  // strided scan: ascending i, first max kept
+      const float x = xs[u];
+      if (!isnan(x) && (idx < 0 || x > v)) {
+        v = x;
+        idx = i0 + (int64_t)u * 1024;
+      }
     }
   }
   // wave reduction: larger value wins, equal values keep the smaller index
