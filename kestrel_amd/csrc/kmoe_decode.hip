@@ -46,6 +46,34 @@ template <int TPL, int RU, int NPER>
 __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nb = a.cols / 256, ntasks = 4 * nb;
+  const int64_t row_bytes = nb * 144;
+
+  // lane constants: offsets inside a row and the activation slice, whose loads
+  // do not depend on the expert and are issued before the selection
+  uint32_t oh[TPL], oa[TPL], ob[TPL];
+  bool tv[TPL];
+  Slice s[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    const int64_t t0 = lane + 64 * i;
+    tv[i] = t0 < ntasks;
+    const int64_t t = tv[i] ? t0 : ntasks - 1;
+    const int64_t sb = t >> 2;
+    const int k = (int)(t & 3);
+    oh[i] = (uint32_t)(16 * sb);
+    oa[i] = (uint32_t)tq4_qs_off(nb, sb, k, 0);
+    ob[i] = oa[i] + (uint32_t)tq4_j_stride(nb, sb);
+    const int4 *xv = (const int4 *)(a.xq + 256 * sb + 64 * k);
+    s[i].x0 = xv[0];
+    s[i].x1 = xv[1];
+    s[i].x2 = xv[2];
+    s[i].x3 = xv[3];
+    const int4 bs = *(const int4 *)(a.xbs + 16 * sb + 4 * k);
+    s[i].bsA = bs.x + bs.y;
+    s[i].bsB = bs.z + bs.w;
+    s[i].d = a.xd[sb];
+  }
   const int slot_i = blockIdx.y;  // index into the active-expert list
   int e;
   int64_t p;
@@ -72,35 +100,9 @@ __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
     if (e < 0) return;
     p = slot_i;
   }
-  const int64_t nb = a.cols / 256, ntasks = 4 * nb;
-  const int64_t row_bytes = nb * 144;
   const uint8_t *G = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[0];
   const uint8_t *U = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[1];
 
-  // lane constants: offsets inside a row and the activation slice
-  uint32_t oh[TPL], oa[TPL], ob[TPL];
-  bool tv[TPL];
-  Slice s[TPL];
-#pragma unroll
-  for (int i = 0; i < TPL; ++i) {
-    const int64_t t0 = lane + 64 * i;
-    tv[i] = t0 < ntasks;
-    const int64_t t = tv[i] ? t0 : ntasks - 1;
-    const int64_t sb = t >> 2;
-    const int k = (int)(t & 3);
-    oh[i] = (uint32_t)(16 * sb);
-    oa[i] = (uint32_t)tq4_qs_off(nb, sb, k, 0);
-    ob[i] = oa[i] + (uint32_t)tq4_j_stride(nb, sb);
-    const int4 *xv = (const int4 *)(a.xq + 256 * sb + 64 * k);
-    s[i].x0 = xv[0];
-    s[i].x1 = xv[1];
-    s[i].x2 = xv[2];
-    s[i].x3 = xv[3];
-    const int4 bs = *(const int4 *)(a.xbs + 16 * sb + 4 * k);
-    s[i].bsA = bs.x + bs.y;
-    s[i].bsB = bs.z + bs.w;
-    s[i].d = a.xd[sb];
-  }
   const int kq = lane & 3;  // quarter of every slot of this lane (64*i keeps it)
 
   const int64_t rows = a.rows;
