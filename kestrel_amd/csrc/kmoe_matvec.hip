@@ -867,7 +867,9 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
     tk[i] = wave * tpw + lt;
     tv[i] = lt < tpw && tk[i] < ntasks;
   }
-  const int na = *a.rt.n_active;
+  // one token: its top-k experts are distinct, so k slots are active (no
+  // dependent read of the count before the first weight loads)
+  const int na = a.s_rows == 1 ? a.rt.topk : *a.rt.n_active;
   const int nb = (nr + RU - 1) / RU;  // row batches per expert
   const int items = na * nb;          // (expert, batch) in ascending expert id
   if (items == 0) {
