@@ -253,6 +253,14 @@ int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
  * out[s] = sum over the token's experts in ascending id of w * y.
  * h [s_rows, n_embd] f32 in, out [s_rows, n_embd] f32 out (device). */
 int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev);
+/* The feed-forward half of a MoE decoder layer (transformer.rs:430-444):
+ * x += y when y_dev is non-NULL (the attention output, :430), f =
+ * rmsnorm(x, norm_w) (:442, as kmoe_rmsnorm) into f_dev [s_rows, n_embd],
+ * then out = kmoe_moe_ffn(f) (:444). Bit-identical to kmoe_rmsnorm followed
+ * by kmoe_moe_ffn; for one token with 16-byte aligned rows and n_embd % 256
+ * == 0 the router kernel computes the norm itself (one launch fewer). */
+int kmoe_norm_moe_ffn(kmoe_ctx *ctx, uint32_t layer, float *x_dev, const float *y_dev, const float *norm_w_dev,
+                      float eps, int64_t s_rows, float *f_dev, float *out_dev);
 /* Routing state of the last kmoe_moe_ffn on ctx (device copies; any may be NULL):
  * idx/w [s_rows*k], perm [s_rows*k], offsets [n_expert+1]. */
 int kmoe_moe_last_routing(kmoe_ctx *ctx, uint32_t *idx_dev, float *w_dev, uint32_t *perm_dev,

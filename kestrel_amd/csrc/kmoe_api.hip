@@ -1141,7 +1141,10 @@ int kmoe_bytes_per_expert(kmoe_ctx *c, uint32_t layer, uint64_t *bytes) {
 
 // --------------------------------------------------------------- moe_ffn
 
-int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
+// The MoE FFN of h; with norm, h is norm->f and is produced here first
+// (x += y, f = rmsnorm(x) * w), folded into the single-token router kernel
+// where it supports the shapes, else by the norm kernel.
+static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out, const RouteNorm *norm) {
   if (!c) return KMOE_E_INVALID;
   Layer *L = find_layer(c, layer);
   if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
@@ -1178,6 +1181,18 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   MoeWs w = carve_moe(c->ws, S, E, k, d, F, &tmp);
   const int regime = c->regime;
   hipStream_t st = c->stream;
+  // the norm, where the router kernel does not take it
+  bool norm_pending = norm != nullptr;
+  auto run_norm = [&]() -> int {
+    if (!norm_pending) return KMOE_OK;
+    norm_pending = false;
+    LAUNCH(c, "rmsnorm", launch_add_rmsnorm(st, norm->x, norm->y, norm->w, S, d, norm->eps, norm->f));
+    return KMOE_OK;
+  };
+  if (norm_pending && !route_norm_supported(norm, (int32_t)S, d)) {
+    rc = run_norm();
+    if (rc) return rc;
+  }
 
   const int gt = D.gate_type, dt = D.down_type;
   // One token on the int path over tiled Q4_K experts, on request: the whole
@@ -1186,6 +1201,8 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
   if (S == 1 && regime != KMOE_REGIME_EXACT && c->decode_path == KMOE_DECODE_FUSED && gt == KMOE_Q4_K &&
       D.up_type == KMOE_Q4_K && dt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && L->tiled[2] &&
       layer_dec_fused_supported(d, F, (int32_t)E, (int32_t)k)) {
+    rc = run_norm();
+    if (rc) return rc;
     DecSelect pub;
     pub.E = (int32_t)E;
     pub.K = (int32_t)k;
@@ -1220,12 +1237,16 @@ int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *
     hipError_t e = timed(c, "route_decode", [&]() {
       return launch_route_decode(st, L->router, (int32_t)E, d, h, (int32_t)S, (int32_t)k, D.norm_topk,
                                  D.weights_scale, w.logits, w.idx, w.wsel, w.perm, w.offsets, w.inv, w.n_active,
-                                 w.active, qtype, w.xq, w.xd, w.xs, select_in_gate_up ? nullptr : c->counters);
+                                 w.active, qtype, w.xq, w.xd, w.xs, select_in_gate_up ? nullptr : c->counters,
+                                 norm_pending ? norm : nullptr);
     });
     if (e == hipSuccess) {
       x_quantized = qtype != 0;
+      norm_pending = false;
     } else {
       if (e != hipErrorNotSupported) HIP_OK(c, e);
+      rc = run_norm();
+      if (rc) return rc;
       select_in_gate_up = false;
       LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
       LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
@@ -1387,6 +1408,18 @@ done:
   c->last_slots = slots;
   c->last_E = (int32_t)E;
   return KMOE_OK;
+}
+
+int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
+  return moe_ffn(c, layer, h, S, out, nullptr);
+}
+
+int kmoe_norm_moe_ffn(kmoe_ctx *c, uint32_t layer, float *x, const float *y, const float *norm_w, float eps,
+                      int64_t S, float *f, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (S > 0 && (!x || !norm_w || !f)) return fail(c, KMOE_E_INVALID, "null pointer");
+  const RouteNorm n{x, y, norm_w, eps, f};
+  return moe_ffn(c, layer, f, S, out, &n);
 }
 
 int kmoe_moe_last_routing(kmoe_ctx *c, uint32_t *idx, float *wv, uint32_t *perm, uint32_t *off) {

@@ -75,18 +75,6 @@ __global__ void __launch_bounds__(256) k_get_rows(int t, const uint8_t *__restri
   out[s * cols + i] = id < n_rows ? dq_elem(t, table + (int64_t)id * row_bytes, i) : 0.0f;
 }
 
-// Work-group sum of 256 threads, every thread receives the total. The order
-// (per-thread strided partials, wave DPP tree, then four wave sums in order)
-// is fixed, so results repeat exactly.
-__device__ __forceinline__ float wg_sum256(float v, float *red) {
-  v = group_sum<64>(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  return ((red[0] + red[1]) + red[2]) + red[3];
-}
-
 // Transformer::rmsnorm (transformer.rs:330-340) with the residual add of
 // forward_chunk_inner (transformer.rs:427, :463) in front: when y is non-null,
 // x += y is stored first and the norm is taken of the sum. out may alias x

@@ -244,6 +244,18 @@ __device__ __forceinline__ int4 ld_agent4(const void *p) {
   return make_int4((int)ld_agent(u), (int)ld_agent(u + 1), (int)ld_agent(u + 2), (int)ld_agent(u + 3));
 }
 
+// Work-group sum of 256 threads, every thread receives the total. The order
+// (per-thread strided partials, wave DPP tree, then four wave sums in order)
+// is fixed, so results repeat exactly.
+__device__ __forceinline__ float wg_sum256(float v, float *red) {
+  v = group_sum<64>(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 // Q8KRow::quantize of one 256-element block by one full wave (qdot.rs:353-365).
 // The same from values already in registers: lane l holds elements
 // 4l..4l+3 of the block in v.

@@ -194,10 +194,22 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 // and is 0 again when the kernel ends (calls on one counter must not overlap).
 // With done null only the logits and the int8 rows are produced (the caller's
 // next kernel selects the experts). hipErrorNotSupported when out of range.
+// The FFN norm folded into the single-token router (RouteNorm): x += y (y
+// may be null), f = rmsnorm(x) * w with k_rmsnorm_regs' arithmetic, and the
+// router reads f. Needs S == 1, d % 256 == 0, 16-byte aligned rows.
+struct RouteNorm {
+  float *x;
+  const float *y;
+  const float *w;
+  float eps;
+  float *f;
+};
+bool route_norm_supported(const RouteNorm *n, int32_t S, int64_t d);
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
                                int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
                                float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
-                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done);
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done,
+                               const RouteNorm *norm = nullptr);
 // Stable counting sort by expert. inv/n_active/active may be null.
 hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
                            uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp);

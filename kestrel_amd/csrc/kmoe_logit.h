@@ -30,9 +30,12 @@ __device__ __forceinline__ void logit_row_load(const float *w, int nq, bool vec,
 // of wave 0 run the chains with their LDS reads two stages ahead; waves 1..3
 // call spare(wave) meanwhile. The caller synchronizes before reusing T. The
 // logit is returned in thread 0.
-template <int NV, class Spare>
-__device__ __forceinline__ float wg_logit(const float4 (&wv)[NV], const float *w, const float *x, int64_t d, bool vec,
-                                          float *T, Spare &&spare) {
+// xat(v, q) gives x's float4 group q = tid + 256*v (from memory, or from
+// registers when the caller computed x); x itself is read only for the
+// d % 8 tail columns.
+template <int NV, class XAt, class Spare>
+__device__ __forceinline__ float wg_logit_at(const float4 (&wv)[NV], const float *w, XAt &&xat, const float *x,
+                                             int64_t d, float *T, Spare &&spare) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t n8 = d / 8;
   const int cstr = (int)(((n8 + 3) & ~3ll) + 4);
@@ -41,8 +44,7 @@ __device__ __forceinline__ float wg_logit(const float4 (&wv)[NV], const float *w
   for (int v = 0; v < NV; ++v) {
     const int q = tid + 256 * v;
     if (q < nq) {
-      const float4 xv = vec ? *(const float4 *)(x + 4 * q)
-                            : make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+      const float4 xv = xat(v, q);
       float *dst = T + (4 * (q & 1)) * cstr + (q >> 1);
       dst[0 * cstr] = wv[v].x * xv.x;
       dst[1 * cstr] = wv[v].y * xv.y;
@@ -104,6 +106,15 @@ __device__ __forceinline__ float wg_logit(const float4 (&wv)[NV], const float *w
     spare(wave);
   }
   return r;
+}
+
+template <int NV, class Spare>
+__device__ __forceinline__ float wg_logit(const float4 (&wv)[NV], const float *w, const float *x, int64_t d, bool vec,
+                                          float *T, Spare &&spare) {
+  auto xat = [&](int, int q) {
+    return vec ? *(const float4 *)(x + 4 * q) : make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+  };
+  return wg_logit_at<NV>(wv, w, xat, x, d, T, spare);
 }
 
 }  // namespace kmoe

@@ -402,7 +402,75 @@ struct RouteDecArgs {
   int32_t *xs;
   uint32_t *done;  // finished work-groups; 0 between calls (the last one resets it)
   int vec;         // W, X 16-byte aligned and d % 4 == 0
+  RouteNorm norm;  // norm.w non-null: X = rmsnorm(norm.x (+= norm.y)) is computed here
 };
+
+// One token's FFN norm in front of the router (RouteNorm): every work-group
+// forms x + y and the normed row in registers exactly as k_rmsnorm_regs does
+// (float4 groups q = t + 256k, the same sums, wg_sum256, the same products),
+// so the row is the same bits; work-group 0 also stores x + y, the normed row
+// and its int8 rows (qtype) for the gate/up kernel.
+template <int NV>
+__device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h)[NV], bool store, float *red) {
+  const int t = threadIdx.x;
+  const int n4 = (int)(a.d / 4);
+  const RouteNorm &n = a.norm;
+  float4 *xr = (float4 *)n.x;
+  const float4 *yr = (const float4 *)n.y;
+  const float4 *wr = (const float4 *)n.w;
+  float4 v[NV], ww[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = t + 256 * k;
+    if (i < n4) {
+      v[k] = xr[i];
+      ww[k] = wr[i];
+    }
+  }
+  if (yr) {
+    float4 yy[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (t + 256 * k < n4) yy[k] = yr[t + 256 * k];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (t + 256 * k < n4) {
+        v[k].x = v[k].x + yy[k].x;
+        v[k].y = v[k].y + yy[k].y;
+        v[k].z = v[k].z + yy[k].z;
+        v[k].w = v[k].w + yy[k].w;
+      }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
+  ss = wg_sum256(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)a.d + n.eps);
+  float4 *frow = (float4 *)n.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = t + 256 * k;
+    h[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < n4) {
+      h[k].x = (v[k].x * rr) * ww[k].x;
+      h[k].y = (v[k].y * rr) * ww[k].y;
+      h[k].z = (v[k].z * rr) * ww[k].z;
+      h[k].w = (v[k].w * rr) * ww[k].w;
+      if (store) {
+        if (yr) xr[i] = v[k];
+        frow[i] = h[k];
+        if (is_kquant(a.qtype)) {
+          const int64_t b = 4 * k + (t >> 6);
+          wave_quant_q8k_vals(h[k], a.xq + 256 * b, a.xd + b, a.xs + 16 * b, t & 63);
+        } else if (a.qtype == T_Q8_0) {
+          const int64_t b = (4 * (int64_t)i) / 32;
+          group8_quant_q8_vals(h[k], a.xq + 32 * b, a.xd + b, a.xs + 2 * b, t & 7);
+        }
+      }
+    }
+  }
+}
 
 
 // Softmax, top-k and renormalisation (transformer.rs:479-495) for the S <= 3
@@ -483,6 +551,7 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
   __shared__ uint32_t sel[64];
   __shared__ int first[64];
   __shared__ int last;
+  __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int e = blockIdx.x, G = gridDim.x;
   const int64_t d = a.d;
@@ -491,7 +560,16 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
 
   float4 wv[NV];
   logit_row_load<NV>(w, nq, a.vec, wv, tid);
-  for (int s = 0; s < a.S; ++s) {
+  if (a.norm.w) {  // one token, d % 256 == 0: the normed row from registers
+    float4 xr[NV];
+    route_norm_row<NV>(a, xr, e == 0, red);
+    const float r = wg_logit_at<NV>(wv, w, [&](int v, int) { return xr[v]; }, a.norm.f, d, T, [](int) {});
+    if (tid == 0) {
+      if (a.done) st_agent(a.logits + e, r);  // read by the last work-group below
+      else a.logits[e] = r;
+    }
+  }
+  for (int s = 0; s < (a.norm.w ? 0 : a.S); ++s) {
     const float *x = a.X + (int64_t)s * d;
     __syncthreads();  // the previous token's fold has read T
     const float r = wg_logit<NV>(wv, w, x, d, a.vec, T, [&](int wv_) {
@@ -597,16 +675,23 @@ hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int
 }  // namespace kmoe
 
 namespace kmoe {
+bool route_norm_supported(const RouteNorm *n, int32_t S, int64_t d) {
+  if (!n || !n->x || !n->w || !n->f || S != 1 || d % 256 != 0 || d < 256 || d > kDecMaxD) return false;
+  return (((uintptr_t)n->x | (uintptr_t)n->y | (uintptr_t)n->w | (uintptr_t)n->f) & 15) == 0;
+}
+
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,
                                int32_t k, int32_t norm_topk, float weights_scale, float *logits, uint32_t *idx,
                                float *w, uint32_t *perm, uint32_t *offsets, uint32_t *inv, int32_t *n_active,
-                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done) {
+                               int32_t *active, int qtype, int8_t *xq, float *xd, int32_t *xs, uint32_t *done,
+                               const RouteNorm *norm) {
   if (S < 1 || S > 3 || E < 1 || E > kMaxExperts || k < 1 || k > 16 || k > E || S * k > 48) return hipErrorNotSupported;
   if (d < 8 || d > kDecMaxD) return hipErrorNotSupported;
   if (!logits) return hipErrorInvalidValue;
+  if (norm && !route_norm_supported(norm, S, d)) return hipErrorNotSupported;
   const int vec = d % 4 == 0 && ((uintptr_t)router & 15) == 0 && ((uintptr_t)x & 15) == 0;
   RouteDecArgs a{router, E, d, x, S, k, norm_topk, weights_scale, logits, idx, w, perm, offsets, inv, n_active, active,
-                 qtype, xq, xd, xs, done, vec};
+                 qtype, xq, xd, xs, done, vec, norm ? *norm : RouteNorm{}};
   const int64_t nq = 2 * (d / 8);
   if (nq <= 256) KMOE_LAUNCH(k_route_dec<1>, dim3(E), dim3(256), 0, st, a);
   else if (nq <= 512) KMOE_LAUNCH(k_route_dec<2>, dim3(E), dim3(256), 0, st, a);

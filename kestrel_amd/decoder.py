@@ -181,8 +181,9 @@ class Decoder:
         o = ctx.attention_matmul(qr, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, ty, t,
                                  int(np.prod(dims[1:])), pos_dev)
         if "moe" in L:
-            h = ctx.rmsnorm(x, L["ffn_norm"], self.eps, y=o)  # x += o, then the norm of x
-            return ctx.moe_ffn(L["moe"], h)
+            # x += o, the norm of x, then the routed experts (one token: the
+            # router kernel takes the norm)
+            return ctx.norm_moe_ffn(L["moe"], x, L["ffn_norm"], self.eps, y=o)
         if "wgu" in L:
             ty, dims, t = L["wgu"]
             ff = dims[1] // 2

@@ -73,6 +73,7 @@ SIGNATURES = {
     "kmoe_shared_gate_upload": (C.c_int, [_P, _u32, _P, _sz]),
     "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
+    "kmoe_norm_moe_ffn": (C.c_int, [_P, _u32, _P, _P, _P, _f, _i64, _P, _P]),
     "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
     "kmoe_get_rows": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
     "kmoe_get_rows_dev": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
@@ -462,6 +463,16 @@ class Context:
         if out is None:
             out = self._empty((S, d), self.torch.float32)
         self.check(self.lib.kmoe_moe_ffn(self.h, layer, _ptr(h), S, _ptr(out)))
+        return out
+
+    def norm_moe_ffn(self, layer: int, x, norm_w, eps: float, y=None, f=None, out=None):
+        """x += y (when given), f = rmsnorm(x) * norm_w, out = moe_ffn(f); returns out."""
+        S, d = x.shape
+        f = self._empty((S, d), self.torch.float32) if f is None else f
+        if out is None:
+            out = self._empty((S, d), self.torch.float32)
+        self.check(self.lib.kmoe_norm_moe_ffn(self.h, layer, _ptr(x), _ptr(y), _ptr(norm_w), eps, S, _ptr(f),
+                                              _ptr(out)))
         return out
 
     def last_routing(self, S: int, k: int, n_expert: int):

@@ -592,3 +592,38 @@ def test_shared_expert_errors(ctx):
         assert e.value.status == -1
     finally:
         ctx.layer_destroy(97)
+
+
+@pytest.mark.parametrize("wtype,d,ff,S,regime,with_y", [
+    (Q4_K, 1024, 1536, 1, 0, True),   # one token: the router kernel takes the norm (Q8_K rows)
+    (Q4_K, 1024, 1536, 1, 1, False),  # int8 regime, no residual add
+    (Q8_0, 2048, 1024, 1, 0, True),   # Q8 rows for Q8_0 experts
+    (Q4_K, 1024, 1536, 1, 2, True),   # exact regime: no int8 rows
+    (Q4_K, 1024, 1536, 3, 0, True),   # three tokens: the norm kernel, then the layer
+])
+def test_norm_moe_ffn_matches_rmsnorm_then_moe(ctx, orc, wtype, d, ff, S, regime, with_y):
+    """kmoe_norm_moe_ffn against kmoe_rmsnorm followed by kmoe_moe_ffn on the
+    same inputs: x after the residual add, the normed rows f and the layer's
+    output are the same bits, called twice in a row."""
+    import torch
+
+    spec = LayerSpec(32, 4, d, ff, wtype, seed=d + ff + S, quantized=False)
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    ctx.set_regime(regime)
+    try:
+        nw = dev(orc.normal(7 + S, d, 1.0, 0.1))
+        for call in range(2):
+            x0 = orc.normal(50 + call, S * d, 0.0, 1.0).reshape(S, d)
+            y = dev(orc.normal(60 + call, S * d, 0.0, 0.5).reshape(S, d)) if with_y else None
+            xa, xb = dev(x0), dev(x0)
+            fa = ctx.rmsnorm(xa, nw, 1e-5, y=y)
+            a = host(ctx.moe_ffn(lid, fa))
+            fb = torch.empty_like(xb)
+            b = host(ctx.norm_moe_ffn(lid, xb, nw, 1e-5, y=y, f=fb))
+            for u, v in ((host(xa), host(xb)), (host(fa), host(fb)), (a, b)):
+                assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), (call, np.abs(u - v).max())
+    finally:
+        ctx.set_regime(0)
+        ctx.layer_destroy(lid)
