@@ -194,6 +194,22 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 // and is 0 again when the kernel ends (calls on one counter must not overlap).
 // With done null only the logits and the int8 rows are produced (the caller's
 // next kernel selects the experts). hipErrorNotSupported when out of range.
+// The one-token q/k/v projection with RoPE (interleaved pairs) and the KV
+// store in its epilogue (kmoe_matvec.hip): rows [0, nh*hd) are q, then k,
+// then v; out also receives the raw projection. hipErrorNotSupported for
+// neox pairs or row geometries that do not keep a pair in one wave.
+struct QkvRope {
+  int32_t nh, nkv, hd, rd, neox;
+  int64_t pos0;
+  const int32_t *pos_dev;
+  const float *inv_freq;
+  int64_t n_ctx;
+  float *q_out;
+  uint16_t *kc, *vc;
+};
+hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                  const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
+                                  const QkvRope &rope);
 // The FFN norm folded into the single-token router (RouteNorm): x += y (y
 // may be null), f = rmsnorm(x) * w with k_rmsnorm_regs' arithmetic, and the
 // router reads f. Needs S == 1, d % 256 == 0, 16-byte aligned rows.

@@ -53,9 +53,39 @@ struct MvArgs {
   int min_rows;  // grouped modes: experts with fewer rows are another kernel's
   int sel_on;    // M_GATE_UP, one token: select the experts from sel.logits here
   DecSelect sel;
+  QkvRope rope;  // M_QKV: the epilogue of the one-token q/k/v projection
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
+enum { M_QKV = 5 };
+
+// The RoPE + KV store epilogue of a one-token q/k/v projection with
+// interleaved pairs (rows 2i and 2i+1 of a head, dims below rope_dim): row r
+// of q rotates into q_out, of k into the f16 K cache at the position, of v
+// goes to the f16 V cache; the raw projection is stored in out as well. The
+// expressions are k_rope_kv's: x0*cos - x1*sin for the first of a pair,
+// x0*sin + x1*cos for the second, sincosf of (float)position * inv_freq[i].
+__device__ __forceinline__ void qkv_rope_store(const QkvRope &q, int64_t r, float v, float partner) {
+  const int64_t nqr = (int64_t)q.nh * q.hd, kvw = (int64_t)q.nkv * q.hd;
+  const int64_t p = q.pos0 + (q.pos_dev ? (int64_t)*q.pos_dev : 0);
+  if (r < nqr + kvw) {
+    const int dd = (int)(r % q.hd);
+    float val = v;
+    if (dd < q.rd) {
+      const int i = dd >> 1;
+      const bool first = (dd & 1) == 0;
+      const float ang = (float)p * q.inv_freq[i];
+      float sv, cv;
+      sincosf(ang, &sv, &cv);
+      const float x0 = first ? v : partner, x1 = first ? partner : v;
+      val = first ? x0 * cv - x1 * sv : x0 * sv + x1 * cv;
+    }
+    if (r < nqr) q.q_out[r] = val;
+    else if (p >= 0 && p < q.n_ctx) q.kc[p * kvw + (r - nqr)] = __builtin_bit_cast(uint16_t, (_Float16)val);
+  } else if (p >= 0 && p < q.n_ctx) {
+    q.vc[p * kvw + (r - nqr - kvw)] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+}
 
 __device__ __forceinline__ bool int_regime(int regime, int n) {
   return regime == REGIME_INT8 || (regime == REGIME_AVX2 && n < 4);
@@ -823,12 +853,21 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
         acc0[u] = group_sum<LPR>(acc0[u]);
         if constexpr (MODE == M_GATE_UP) acc1[u] = group_sum<LPR>(acc1[u]);
       }
+      float pair[RU];  // M_QKV: row r^1's sum, held by the lanes LPR away (RPW >= 2)
+      if constexpr (MODE == M_QKV) {
+        static_assert(RPW >= 2, "row pairs in one wave");
+#pragma unroll
+        for (int u = 0; u < RU; ++u) pair[u] = __shfl_xor(acc0[u], LPR);
+      }
       if (lr == 0) {
 #pragma unroll
         for (int u = 0; u < RU; ++u) {
           const int64_t r = r0 + (int64_t)u * RPW;
           if (r >= rows) continue;
-          if constexpr (MODE == M_GATE_UP) {  // SwiGLU (transformer.rs:558)
+          if constexpr (MODE == M_QKV) {
+            a.out[r] = acc0[u];
+            qkv_rope_store(a.rope, r, acc0[u], pair[u]);
+          } else if constexpr (MODE == M_GATE_UP) {  // SwiGLU (transformer.rs:558)
             const float g = acc0[u];
             const float den = 1.0f + expf_cr(-g);
             const float q = g / den;
@@ -1192,6 +1231,40 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
   return hipErrorInvalidValue;
+}
+
+template <int TYPE>
+static hipError_t launch_qkv_reg(hipStream_t st, const MvArgs &a) {
+  const int ntasks = (int)(QT<TYPE>::TPB * (a.cols / QT<TYPE>::EL));
+  int lpr, tpl;
+  if (!reg_geometry(TYPE, ntasks, lpr, tpl)) return hipErrorNotSupported;
+  const int64_t tasks32 = (a.rows + 4 * 2 * 2 - 1) / (4 * 2 * 2), tasks16 = (a.rows + 4 * 4 * 2 - 1) / (4 * 4 * 2);
+  if (lpr == 32) return launch_reg<TYPE, 32, 1, 2, M_QKV>(st, a, tpl, tasks32);
+  if (lpr == 16) return launch_reg<TYPE, 16, 1, 2, M_QKV>(st, a, tpl, tasks16);
+  return hipErrorNotSupported;  // one row per wave step: pairs not in one wave
+}
+
+hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                  const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
+                                  const QkvRope &rope) {
+  if (rope.neox || rope.hd <= 0 || rope.hd % 2 || rope.rd % 2 || rope.rd > rope.hd || rope.nh < 1 || rope.nkv < 0 ||
+      rows != (int64_t)(rope.nh + 2 * rope.nkv) * rope.hd)
+    return hipErrorNotSupported;
+  if (!act_fits(type, cols)) return hipErrorNotSupported;
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.s_rows = 1;
+  a.out = out;
+  a.rope = rope;
+  if (type == T_Q4_K) return launch_qkv_reg<T_Q4_K>(st, a);
+  if (type == T_Q6_K) return launch_qkv_reg<T_Q6_K>(st, a);
+  if (type == T_Q8_0) return launch_qkv_reg<T_Q8_0>(st, a);
+  return hipErrorNotSupported;
 }
 
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,

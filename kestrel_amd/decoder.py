@@ -159,6 +159,14 @@ class Decoder:
         norm's fused add; the layer returns its own FFN output."""
         ctx, nh, nkv, hd = self.ctx, self.nh, self.nkv, self.hd
         kvw, nq = nkv * hd, nh * hd
+        plain = not any(n in L for n in ("bq", "bk", "bv", "q_norm", "k_norm"))
+        if "wqkv" in L and S == 1 and plain:
+            # one token: the projection kernel applies RoPE and fills the caches
+            ty, dims, t = L["wqkv"]
+            qr = ctx.norm_matmul_rope_kv(x, L["attn_norm"], self.eps, ty, t, dims[0], nh, nkv, hd, self.rd, pos0,
+                                         self.inv_freq, self.neox, self.n_ctx, L["kc"], L["vc"], y=f_prev,
+                                         pos_dev=pos_dev)
+            return self._attn_ffn(L, x, qr, S, pos0, pos_dev)
         if "wqkv" in L:
             ty, dims, t = L["wqkv"]
             qkv = ctx.norm_matmul(x, L["attn_norm"], self.eps, ty, t, dims[1], dims[0], y=f_prev)
@@ -177,6 +185,11 @@ class Decoder:
             ctx.rmsnorm(k, L["k_norm"], self.eps, out=k)
         qr = ctx.rope_kv_store(q, k, v, nh, nkv, hd, self.rd, pos0, self.inv_freq, self.neox, self.n_ctx, L["kc"],
                                L["vc"], pos_dev)
+        return self._attn_ffn(L, x, qr, S, pos0, pos_dev)
+
+    def _attn_ffn(self, L, x, qr, S, pos0, pos_dev):
+        """Attention from the rotated q and the caches, its projection, then the FFN."""
+        ctx, nh, nkv, hd = self.ctx, self.nh, self.nkv, self.hd
         ty, dims, t = L["wo"]
         o = ctx.attention_matmul(qr, L["kc"], L["vc"], nh, nkv, hd, pos0, self.n_ctx, ty, t,
                                  int(np.prod(dims[1:])), pos_dev)

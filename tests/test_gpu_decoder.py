@@ -346,3 +346,50 @@ def test_decoder_context_full(ctx):
             dec.forward([1, 2, 3, 4])
     finally:
         dec.close()
+
+
+@pytest.mark.parametrize("t,cols,nh,nkv,hd,rd,neox,regime,use_dev", [
+    (Q4_K, 2048, 16, 4, 128, 128, False, 0, False),  # 32 lanes per row: the projection applies RoPE
+    (Q4_K, 1024, 8, 2, 64, 32, False, 1, True),      # 16 lanes per row, partial rope_dim, device position
+    (Q8_0, 2048, 16, 4, 128, 128, False, 0, True),
+    (Q4_K, 4096, 8, 2, 128, 128, False, 0, False),   # 64 lanes per row: separate kernels
+    (Q4_K, 2048, 16, 4, 128, 128, True, 0, False),   # neox pairs: separate kernels
+    (Q4_K, 2048, 16, 4, 128, 128, False, 2, False),  # exact regime: separate kernels
+])
+def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, nkv, hd, rd, neox, regime, use_dev):
+    """kmoe_norm_matmul_rope_kv against kmoe_norm_matmul followed by
+    kmoe_rope_kv_store on one token: the residual, the normed row, the
+    projection, the rotated q and both caches are the same bits, for two
+    positions in a row."""
+    import torch
+
+    rows, n_ctx = (nh + 2 * nkv) * hd, 16
+    nq, kvw = nh * hd, nkv * hd
+    rng = np.random.default_rng(cols + rd)
+    w = dev(random_blocks(t, rows, cols, seed=cols))
+    nw = dev((1 + 0.1 * rng.standard_normal(cols)).astype(np.float32))
+    f = dev(orc.rope_inv_freq(10000.0, rd))
+    caches = [torch.zeros((n_ctx, kvw), dtype=torch.int16).cuda() for _ in range(4)]
+    ctx.set_regime(regime)
+    try:
+        for pos in (5, 6):
+            x = rng.standard_normal((1, cols)).astype(np.float32)
+            y = dev(rng.standard_normal((1, cols)).astype(np.float32))
+            xa, xb = dev(x), dev(x)
+            pos_dev = torch.tensor([pos - 2], dtype=torch.int32).cuda() if use_dev else None
+            p0 = 2 if use_dev else pos
+            ha = torch.empty((1, cols), dtype=torch.float32).cuda()
+            qkva = torch.empty((1, rows), dtype=torch.float32).cuda()
+            qa = ctx.norm_matmul_rope_kv(xa, nw, 1e-5, t, w, cols, nh, nkv, hd, rd, p0, f, neox, n_ctx, caches[0],
+                                         caches[1], y=y, pos_dev=pos_dev, h=ha, qkv=qkva)
+            hb = torch.empty((1, cols), dtype=torch.float32).cuda()
+            qkvb = ctx.norm_matmul(xb, nw, 1e-5, t, w, rows, cols, y=y, h=hb)
+            qb = ctx.rope_kv_store(qkvb[:, :nq], qkvb[:, nq:nq + kvw], qkvb[:, nq + kvw:], nh, nkv, hd, rd, p0, f,
+                                   neox, n_ctx, caches[2], caches[3], pos_dev)
+            for u, v in ((xa, xb), (ha, hb), (qkva, qkvb), (qa, qb)):
+                assert np.array_equal(host(u).view(np.uint32), host(v).view(np.uint32)), pos
+            for u, v in ((caches[0], caches[2]), (caches[1], caches[3])):
+                assert np.array_equal(host(u), host(v)), pos
+            assert host(caches[0])[pos].any() and host(caches[1])[pos].any()
+    finally:
+        ctx.set_regime(0)
