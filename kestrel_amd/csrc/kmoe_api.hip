@@ -90,6 +90,7 @@ struct Event2 {
 // router, [64, kCounterWords) for the fused single-token layer.
 constexpr int kCounterWords = 4096;
 constexpr int kFusedSync = 64;
+constexpr int kNormDone = 1;  // the decode router's residual writer (kmoe_norm_moe_ffn)
 
 struct kmoe_ctx {
   int device = 0;
@@ -1418,7 +1419,7 @@ int kmoe_norm_moe_ffn(kmoe_ctx *c, uint32_t layer, float *x, const float *y, con
                       int64_t S, float *f, float *out) {
   if (!c) return KMOE_E_INVALID;
   if (S > 0 && (!x || !norm_w || !f)) return fail(c, KMOE_E_INVALID, "null pointer");
-  const RouteNorm n{x, y, norm_w, eps, f};
+  const RouteNorm n{x, y, norm_w, eps, f, c->counters + kNormDone};
   return moe_ffn(c, layer, f, S, out, &n);
 }
 

@@ -219,6 +219,7 @@ struct RouteNorm {
   const float *w;
   float eps;
   float *f;
+  uint32_t *done;  // work-groups that have read x; 0 between calls (the last one stores x + y and resets it)
 };
 bool route_norm_supported(const RouteNorm *n, int32_t S, int64_t d);
 hipError_t launch_route_decode(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t S,

@@ -408,10 +408,14 @@ struct RouteDecArgs {
 // One token's FFN norm in front of the router (RouteNorm): every work-group
 // forms x + y and the normed row in registers exactly as k_rmsnorm_regs does
 // (float4 groups q = t + 256k, the same sums, wg_sum256, the same products),
-// so the row is the same bits; work-group 0 also stores x + y, the normed row
-// and its int8 rows (qtype) for the gate/up kernel.
+// so the row is the same bits; work-group 0 also stores the normed row and its
+// int8 rows (qtype) for the gate/up kernel. x + y goes back into x from the
+// last work-group to count itself on n.done, after every work-group's loads
+// of x have returned (each counts after its reduction), so no work-group can
+// read the updated x; that work-group resets the counter.
 template <int NV>
-__device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h)[NV], bool store, float *red) {
+__device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h)[NV], bool store, float *red,
+                                               int *xlast) {
   const int t = threadIdx.x;
   const int n4 = (int)(a.d / 4);
   const RouteNorm &n = a.norm;
@@ -445,7 +449,17 @@ __device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h
 #pragma unroll
   for (int k = 0; k < NV; ++k)
     if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
-  ss = wg_sum256(ss, red);
+  ss = wg_sum256(ss, red);  // its barriers: every thread's loads of x and y have returned
+  if (yr) {
+    if (t == 0) *xlast = add_agent(n.done, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (*xlast) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (t + 256 * k < n4) xr[t + 256 * k] = v[k];
+      if (t == 0) __hip_atomic_store(n.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   const float rr = 1.0f / sqrtf(ss / (float)a.d + n.eps);
   float4 *frow = (float4 *)n.f;
 #pragma unroll
@@ -458,7 +472,6 @@ __device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h
       h[k].z = (v[k].z * rr) * ww[k].z;
       h[k].w = (v[k].w * rr) * ww[k].w;
       if (store) {
-        if (yr) xr[i] = v[k];
         frow[i] = h[k];
         if (is_kquant(a.qtype)) {
           const int64_t b = 4 * k + (t >> 6);
@@ -552,6 +565,7 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
   __shared__ int first[64];
   __shared__ int last;
   __shared__ float red[4];
+  __shared__ int xlast;
   const int tid = threadIdx.x, lane = tid & 63;
   const int e = blockIdx.x, G = gridDim.x;
   const int64_t d = a.d;
@@ -562,7 +576,7 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
   logit_row_load<NV>(w, nq, a.vec, wv, tid);
   if (a.norm.w) {  // one token, d % 256 == 0: the normed row from registers
     float4 xr[NV];
-    route_norm_row<NV>(a, xr, e == 0, red);
+    route_norm_row<NV>(a, xr, e == 0, red, &xlast);
     const float r = wg_logit_at<NV>(wv, w, [&](int v, int) { return xr[v]; }, a.norm.f, d, T, [](int) {});
     if (tid == 0) {
       if (a.done) st_agent(a.logits + e, r);  // read by the last work-group below
@@ -676,7 +690,7 @@ hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int
 
 namespace kmoe {
 bool route_norm_supported(const RouteNorm *n, int32_t S, int64_t d) {
-  if (!n || !n->x || !n->w || !n->f || S != 1 || d % 256 != 0 || d < 256 || d > kDecMaxD) return false;
+  if (!n || !n->x || !n->w || !n->f || !n->done || S != 1 || d % 256 != 0 || d < 256 || d > kDecMaxD) return false;
   return (((uintptr_t)n->x | (uintptr_t)n->y | (uintptr_t)n->w | (uintptr_t)n->f) & 15) == 0;
 }
 
