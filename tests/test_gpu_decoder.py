@@ -4,7 +4,7 @@ Transformer::forward (transformer.rs:278-302, 330-467, 591-631)."""
 import numpy as np
 import pytest
 
-from tests.helpers import F32, Q4_K, Q6_K, Q8_0, decoder_model, random_blocks, rel_l2, row_bytes
+from tests.helpers import F32, Q4_K, Q6_K, Q8_0, LayerSpec, decoder_model, random_blocks, rel_l2, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -393,3 +393,49 @@ def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, 
             assert host(caches[0])[pos].any() and host(caches[1])[pos].any()
     finally:
         ctx.set_regime(0)
+
+
+def test_norm_matmul_rope_kv_rejects_bad_arguments(ctx, orc):
+    """The one-token projection + RoPE entry point reports the errors of the
+    two calls it stands for: odd or oversized rope_dim, a full context at a
+    host position, a missing cache; nothing is written to the caches."""
+    import torch
+
+    from kestrel_amd.kmoe import KmoeError
+
+    nh, nkv, hd, cols, n_ctx = 4, 2, 64, 256, 8
+    rows = (nh + 2 * nkv) * hd
+    w = dev(random_blocks(Q4_K, rows, cols, seed=3))
+    nw = dev(np.ones(cols, np.float32))
+    f = dev(orc.rope_inv_freq(10000.0, hd))
+    kc = torch.zeros((n_ctx, nkv * hd), dtype=torch.int16).cuda()
+    vc = torch.zeros_like(kc)
+    x = dev(np.ones((1, cols), np.float32))
+    for rd, pos in ((hd - 1, 0), (hd + 2, 0), (hd, n_ctx)):
+        with pytest.raises(KmoeError):
+            ctx.norm_matmul_rope_kv(x, nw, 1e-5, Q4_K, w, cols, nh, nkv, hd, rd, pos, f, False, n_ctx, kc, vc)
+    h = torch.empty((1, cols), dtype=torch.float32).cuda()
+    qkv = torch.empty((1, rows), dtype=torch.float32).cuda()
+    q_out = torch.empty((1, nh * hd), dtype=torch.float32).cuda()
+    rc = ctx.lib.kmoe_norm_matmul_rope_kv(ctx.h, x.data_ptr(), None, nw.data_ptr(), 1e-5, Q4_K, w.data_ptr(),
+                                          w.numel(), cols, h.data_ptr(), qkv.data_ptr(), nh, nkv, hd, hd, 0, None,
+                                          f.data_ptr(), 0, n_ctx, q_out.data_ptr(), None, vc.data_ptr())
+    assert rc != 0
+    assert not host(kc).any() and not host(vc).any()
+
+
+def test_norm_moe_ffn_rejects_null_rows(ctx, orc):
+    """kmoe_norm_moe_ffn needs x, the norm weights and f for s_rows > 0."""
+    spec = LayerSpec(8, 2, 256, 256, Q4_K, seed=9)
+    lid = 900
+    spec.upload(ctx, lid)
+    try:
+        x = dev(np.ones((1, 256), np.float32))
+        out = dev(np.zeros((1, 256), np.float32))
+        for args in ((None, x, x), (x, None, x), (x, x, None)):
+            p = [a.data_ptr() if a is not None else None for a in args]
+            rc = ctx.lib.kmoe_norm_moe_ffn(ctx.h, lid, p[0], None, p[1], 1e-5, 1, p[2], out.data_ptr())
+            assert rc != 0
+        assert not host(out).any()
+    finally:
+        ctx.layer_destroy(lid)
