@@ -1,7 +1,7 @@
 // kmoe_oracle.cpp — CPU oracle for the MoE FFN hot path (test infrastructure).
 //
-// This is the checker the HIP path is compared against and the CPU baseline
-// bench.py times; it is never linked into the product library. It restates
+// The HIP path's results are compared against it, and bench.py times it as
+// the CPU baseline; it is never linked into the product library. It restates
 // kestrel's native CPU executor (crates/kestrel-engine, Rust + AVX2/FMA):
 //   quant.rs   — dequant_row, quant::dot, matmul regime switch, bench_gemv
 //   qdot.rs    — Q8Row / Q8KRow activation quantizers, unpack, scalar dot
