@@ -88,16 +88,14 @@ void *kmoe_get_stream(kmoe_ctx *ctx);
 int kmoe_synchronize(kmoe_ctx *ctx);
 int kmoe_set_regime(kmoe_ctx *ctx, int regime);
 int kmoe_get_regime(const kmoe_ctx *ctx);
-/* No counterpart in the reference: how a single-token kmoe_moe_ffn runs.
- * KMOE_DECODE_SEPARATE (default): one kernel per stage (router, gate/up that
- * selects the experts, Q8_K of h, down + combine). KMOE_DECODE_FUSED: the
- * whole layer as one persistent kernel where the shape allows (Q4_K experts,
- * int path); its work-groups wait on each other, so the grid must be
- * resident, and a wait past its bound is reported by kmoe_synchronize as
- * KMOE_E_HIP. Both give the same routing; output bits are the same wherever
- * both run the same per-row reductions. */
-enum { KMOE_DECODE_SEPARATE = 0, KMOE_DECODE_FUSED = 1 };
-int kmoe_set_decode_path(kmoe_ctx *ctx, int path);
+/* No counterpart in the reference (its host path has no device graphs). The
+ * context's workspaces grow on demand, and growing one frees it and
+ * allocates anew; *gen counts those (re)allocations. Work captured into a
+ * HIP graph on this context holds workspace addresses: the graph may be
+ * replayed only while the generation is the one read after its capture, and
+ * must be captured again (after one uncaptured call at the new sizes) once
+ * the generation has moved. */
+int kmoe_workspace_generation(const kmoe_ctx *ctx, uint64_t *gen);
 
 /* ------------------------------------------------- Tier::Vram accounting */
 /* Ledger::reserve for Tier::Vram (ledger.rs:75): every device byte the context
@@ -120,6 +118,14 @@ int kmoe_copy_d2h(kmoe_ctx *ctx, void *dst, const void *src_dev, size_t bytes); 
  * the context picks the arithmetic as the reference does for s_rows. */
 int kmoe_matmul(kmoe_ctx *ctx, int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols,
                 const float *x_dev, int64_t s_rows, float *out_dev);
+
+/* quant::matmul with its own signature (quant.rs:229): matmul(t, w: &[u8],
+ * rows, cols, x: &[f32], out: &mut [f32]). x and out are host memory; w is
+ * host memory (copied to the device for the call) or device memory (a
+ * resident weight, e.g. from kmoe_device_alloc; used in place). Synchronous:
+ * returns once out holds the result. Same arithmetic as kmoe_matmul. */
+int kmoe_matmul_host(kmoe_ctx *ctx, int ggml_type, const void *w, size_t w_len, int64_t rows, int64_t cols,
+                     const float *x, int64_t s_rows, float *out);
 
 /* Q8KRow::quantize (qdot.rs:347-367) per row of x [s_rows, cols], cols % 256 == 0:
  * q [s_rows, cols] i8, d [s_rows, cols/256] f32, bsums [s_rows, cols/16] i32. */
@@ -225,8 +231,18 @@ int kmoe_layer_preload(kmoe_ctx *ctx, uint32_t layer, const void *const part_bas
 /* ExpertStore::is_ready (expert.rs:445): 1 when all three parts are resident, else 0. */
 int kmoe_expert_is_ready(kmoe_ctx *ctx, uint32_t layer, uint32_t expert);
 /* ExpertBuf::part (expert.rs:72-76): device pointer and length of a resident
- * part, in the tier's layout (tiled rows for Q4_K). */
+ * part, in the tier's layout (kmoe_expert_part_layout): tiled rows for Q4_K
+ * and Q6_K parts, GGUF bytes for the others. The entry points that take a raw
+ * weight pointer (kmoe_matmul, kmoe_matvec_q8, the block sums, the decoder
+ * ops) read GGUF rows and refuse a pointer to a tiled part with
+ * KMOE_E_INVALID. */
 int kmoe_expert_part(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, const void **dev, size_t *len);
+/* Layout of a tier part's bytes on the device. No counterpart in the
+ * reference, whose ExpertBuf::part is always GGUF bytes: KMOE_LAYOUT_TILED
+ * rows keep each row's size and bytes in another order (kmoe_expert_read
+ * returns the GGUF bytes). */
+enum { KMOE_LAYOUT_GGUF = 0, KMOE_LAYOUT_TILED = 1 };
+int kmoe_expert_part_layout(kmoe_ctx *ctx, uint32_t layer, uint32_t expert, int32_t part, int32_t *layout);
 /* ExpertBuf::part bytes as the reference hands them out (expert.rs:72-76):
  * copy a resident part to host memory in GGUF layout; len must equal the
  * part's length. Synchronous. */
@@ -253,6 +269,10 @@ int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
  * out[s] = sum over the token's experts in ascending id of w * y.
  * h [s_rows, n_embd] f32 in, out [s_rows, n_embd] f32 out (device). */
 int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev);
+/* Transformer::moe_ffn with its own signature (transformer.rs:513): h:
+ * &[f32] in, the Vec<f32> out, both host memory [s_rows, n_embd] (the
+ * caller's out buffer). Synchronous; same arithmetic as kmoe_moe_ffn. */
+int kmoe_moe_ffn_host(kmoe_ctx *ctx, uint32_t layer, const float *h, int64_t s_rows, float *out);
 /* The feed-forward half of a MoE decoder layer (transformer.rs:430-444):
  * x += y when y_dev is non-NULL (the attention output, :430), f =
  * rmsnorm(x, norm_w) (:442, as kmoe_rmsnorm) into f_dev [s_rows, n_embd],
@@ -261,6 +281,38 @@ int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_ro
  * == 0 the router kernel computes the norm itself (one launch fewer). */
 int kmoe_norm_moe_ffn(kmoe_ctx *ctx, uint32_t layer, float *x_dev, const float *y_dev, const float *norm_w_dev,
                       float eps, int64_t s_rows, float *f_dev, float *out_dev);
+/* Transformer::moe_ffn as kmoe_moe_ffn, observed from inside (the layer
+ * seam's debug outputs). The reference computes these integers
+ * inside dot_q4_k_8k / dot_q6_k_8k / dot_q8_0 (avx2.rs:49-58, :351-379,
+ * :384-419) on the rows moe_ffn gathers (transformer.rs:544-560); this call
+ * returns them from the kernels that produce the layer's output, so parity
+ * of the integer part can be checked bit for bit. Device buffers:
+ *   xq/xd/xs  int8 rows of h (token order) the gate/up products read: Q8_K
+ *             (q [S, d], d [S, d/256], bsums [S, d/16]) for K-quant gate/up,
+ *             Q8 (q [S, d], d [S, d/32], s16 [S, d/16]) for Q8_0;
+ *   hq/hd/hs  int8 rows of the SwiGLU output per slot in dispatch order
+ *             (position p of the permutation), typed by the down part;
+ *   *_sumi, *_mins  per (slot p, weight row r, block b) at [(p*rows + r)*nblk
+ *             + b]: gate and up rows = n_ff, nblk = n_embd / block; down rows
+ *             = n_embd, nblk = n_ff / block. Q4_K: sumi and mins of
+ *             avx2.rs:361-374; Q6_K: sumi and offs (the block's dot is
+ *             d * xd * (sumi - 32 * offs)); Q8_0: p in *_sumi (*_mins unused,
+ *             may be NULL).
+ * Only products on the int path write integers; slots of experts on the f32
+ * path read 0, and their hq rows are not written. xq.. and hq.. may be NULL.
+ * Same routing, dispatch and output bits as kmoe_moe_ffn; slower (integer
+ * atomics). No counterpart entry point in the reference. */
+typedef struct {
+  int8_t *xq;
+  float *xd;
+  int32_t *xs;
+  int8_t *hq;
+  float *hd;
+  int32_t *hs;
+  int32_t *gate_sumi, *gate_mins, *up_sumi, *up_mins, *down_sumi, *down_mins;
+} kmoe_moe_dbg;
+int kmoe_moe_ffn_dbg(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev,
+                     const kmoe_moe_dbg *dbg);
 /* Routing state of the last kmoe_moe_ffn on ctx (device copies; any may be NULL):
  * idx/w [s_rows*k], perm [s_rows*k], offsets [n_expert+1]. */
 int kmoe_moe_last_routing(kmoe_ctx *ctx, uint32_t *idx_dev, float *w_dev, uint32_t *perm_dev,

@@ -86,10 +86,8 @@ struct Event2 {
 
 }  // namespace
 
-// Device completion counters per context: words [0, 64) for the decode
-// router, [64, kCounterWords) for the fused single-token layer.
-constexpr int kCounterWords = 4096;
-constexpr int kFusedSync = 64;
+// Device completion counters per context (words used by the decode router).
+constexpr int kCounterWords = 64;
 constexpr int kNormDone = 1;  // the decode router's residual writer (kmoe_norm_moe_ffn)
 
 struct kmoe_ctx {
@@ -99,7 +97,6 @@ struct kmoe_ctx {
   std::string err;
   int regime = KMOE_REGIME_AVX2;
   uint32_t *counters = nullptr;  // device, kCounterWords completion counters, zero between calls
-  int decode_path = 0;           // KMOE_DECODE_SEPARATE or KMOE_DECODE_FUSED
   uint64_t vram_limit = 0;
   uint64_t vram_reserved = 0;
   std::map<uint32_t, Layer> layers;
@@ -107,9 +104,15 @@ struct kmoe_ctx {
   // workspace
   uint8_t *ws = nullptr;
   size_t ws_size = 0;
+  // bumped whenever ws, dws or aws is (re)allocated: device addresses a
+  // captured graph may hold change only then
+  uint64_t ws_gen = 0;
   // device staging for host uploads of tiled parts and whole expert extents
   uint8_t *stage = nullptr;
   size_t stage_size = 0;
+  // device staging of the host-slice entry points (kmoe_matmul_host, kmoe_moe_ffn_host)
+  uint8_t *hio = nullptr;
+  size_t hio_size = 0;
   // decoder ops: token ids copied from the host; attention counters
   // (zero between calls) followed by its cross-work-group partials
   uint8_t *dws = nullptr;
@@ -295,6 +298,7 @@ int ensure_ws(kmoe_ctx *c, size_t need) {
   if (rc) return rc;
   c->ws = (uint8_t *)p;
   c->ws_size = sz;
+  ++c->ws_gen;
   return KMOE_OK;
 }
 
@@ -315,6 +319,7 @@ int ensure_dws(kmoe_ctx *c, size_t need) {
   if (rc) return rc;
   c->dws = (uint8_t *)p;
   c->dws_size = sz;
+  ++c->ws_gen;
   return KMOE_OK;
 }
 
@@ -341,6 +346,7 @@ int ensure_aws(kmoe_ctx *c, size_t counters, size_t part_bytes) {
   c->aws = (uint8_t *)p;
   c->aws_size = sz;
   c->aws_counters = ncb;
+  ++c->ws_gen;
   return KMOE_OK;
 }
 
@@ -370,6 +376,37 @@ uint8_t *staging(kmoe_ctx *c, size_t need) {
   return c->stage;
 }
 
+// Device staging of the host-slice entry points, grown on demand (counted in
+// the ledger, kept until kmoe_destroy).
+int ensure_hio(kmoe_ctx *c, size_t need) {
+  if (need <= c->hio_size) return KMOE_OK;
+  const size_t sz = align_up(need + need / 4);
+  if (c->hio) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    HIP_OK(c, hipFree(c->hio));
+    release(c, c->hio_size);
+    c->hio = nullptr;
+    c->hio_size = 0;
+  }
+  void *p = nullptr;
+  int rc = dev_alloc(c, sz, &p, "host-slice staging");
+  if (rc) return rc;
+  c->hio = (uint8_t *)p;
+  c->hio_size = sz;
+  return KMOE_OK;
+}
+
+// Whether p is device memory (hipMalloc'd, on any device); host memory, pinned
+// or pageable, is not.
+bool is_device_ptr(const void *p) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();  // an unknown (pageable host) pointer is not an error here
+    return false;
+  }
+  return a.type == hipMemoryTypeDevice;
+}
+
 bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K || t == KMOE_Q8_0; }
 // The few-rows kernels for decode batches run unless KMOE_SMALL=0.
 bool small_enabled() {
@@ -393,6 +430,27 @@ int check_quant_shape(kmoe_ctx *c, int t, int64_t cols) {
   if (cols % 64 != 0) return fail(c, KMOE_E_UNSUPPORTED, "cols %% 64 != 0");
   const int64_t per = cols + cols / 4 + cols / 8 + 48;
   if (3 * per > 65536) return fail(c, KMOE_E_UNSUPPORTED, "cols %lld too wide for the LDS-staged kernels", (long long)cols);
+  return KMOE_OK;
+}
+
+// A raw weight pointer at a tiled (Q4_K / Q6_K) part of an expert tier, as
+// kmoe_expert_part hands it out: the raw-pointer kernels read GGUF rows, so
+// such a pointer is refused instead of giving wrong results.
+int reject_tiled(kmoe_ctx *c, const void *w) {
+  const uint8_t *p = (const uint8_t *)w;
+  for (auto &kv : c->layers) {
+    const Layer &L = kv.second;
+    if (!L.arena || !L.expert_stride) continue;
+    const uint8_t *b = L.arena, *e = L.arena + (size_t)L.desc.n_expert * L.expert_stride;
+    if (p < b || p >= e) continue;
+    const size_t o = (size_t)(p - b) % L.expert_stride;
+    for (int k = 0; k < 3; ++k)
+      if (L.tiled[k] && o >= L.part_off[k] && o < L.part_off[k] + L.part_len[k])
+        return fail(c, KMOE_E_INVALID,
+                    "weight pointer lies in layer %u's tiled expert part %d (KMOE_LAYOUT_TILED, see "
+                    "kmoe_expert_part_layout); this entry point reads GGUF rows",
+                    kv.first, k);
+  }
   return KMOE_OK;
 }
 
@@ -510,6 +568,7 @@ int kmoe_destroy(kmoe_ctx *c) {
   for (auto &kv : c->user_allocs) (void)hipFree(kv.first);
   if (c->ws) (void)hipFree(c->ws);
   if (c->stage) (void)hipFree(c->stage);
+  if (c->hio) (void)hipFree(c->hio);
   if (c->dws) (void)hipFree(c->dws);
   if (c->aws) (void)hipFree(c->aws);
   if (c->counters) (void)hipFree(c->counters);
@@ -536,13 +595,12 @@ int kmoe_synchronize(kmoe_ctx *c) {
   if (!c) return KMOE_E_INVALID;
   DeviceGuard g(c->device);
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  // a fused single-token layer that gave up waiting leaves word 3 of its sync area set
-  uint32_t flag = 0;
-  HIP_OK(c, hipMemcpy(&flag, c->counters + kFusedSync + 3, 4, hipMemcpyDeviceToHost));
-  if (flag) {
-    HIP_OK(c, hipMemset(c->counters + kFusedSync + 3, 0, 4));
-    return fail(c, KMOE_E_HIP, "fused decode layer: a work-group waited past its bound (grid not resident?)");
-  }
+  return KMOE_OK;
+}
+
+int kmoe_workspace_generation(const kmoe_ctx *c, uint64_t *gen) {
+  if (!c || !gen) return KMOE_E_INVALID;
+  *gen = c->ws_gen;
   return KMOE_OK;
 }
 
@@ -553,13 +611,6 @@ int kmoe_set_regime(kmoe_ctx *c, int regime) {
   return KMOE_OK;
 }
 int kmoe_get_regime(const kmoe_ctx *c) { return c ? c->regime : -1; }
-
-int kmoe_set_decode_path(kmoe_ctx *c, int path) {
-  if (!c) return KMOE_E_INVALID;
-  if (path != KMOE_DECODE_SEPARATE && path != KMOE_DECODE_FUSED) return fail(c, KMOE_E_INVALID, "bad path %d", path);
-  c->decode_path = path;
-  return KMOE_OK;
-}
 
 int kmoe_vram_set_limit(kmoe_ctx *c, uint64_t limit) {
   if (!c) return KMOE_E_INVALID;
@@ -645,6 +696,7 @@ int kmoe_quantize_q8(kmoe_ctx *c, const float *x, int64_t s_rows, int64_t cols, 
 int kmoe_matvec_q8(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const int8_t *q,
                    const float *d, const int32_t *bs, int64_t s_rows, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   int rc = check_quant_shape(c, t, cols);
   if (rc) return rc;
   if (rows < 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "negative size");
@@ -660,6 +712,7 @@ int kmoe_matvec_q8(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows
 int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, const int32_t *bs,
                         int64_t s_rows, int32_t *sumi, int32_t *mins) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   int rc = check_quant_shape(c, KMOE_Q4_K, cols);
   if (rc) return rc;
   if (rows == 0 || s_rows == 0) return KMOE_OK;
@@ -681,6 +734,7 @@ int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, 
 int kmoe_q6k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, const int32_t *bs,
                         int64_t s_rows, int32_t *sumi, int32_t *offs) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   int rc = check_quant_shape(c, KMOE_Q6_K, cols);
   if (rc) return rc;
   if (rows == 0 || s_rows == 0) return KMOE_OK;
@@ -694,6 +748,7 @@ int kmoe_q6k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, 
 int kmoe_q8_0_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, const int8_t *q, int64_t s_rows,
                          int32_t *p) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   int rc = check_quant_shape(c, KMOE_Q8_0, cols);
   if (rc) return rc;
   if (rows == 0 || s_rows == 0) return KMOE_OK;
@@ -707,6 +762,7 @@ int kmoe_q8_0_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols,
 int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const float *x,
                 int64_t s_rows, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   if (rows < 0 || cols <= 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "bad shape");
   const int64_t rb = bytes_for(t, cols);
   if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
@@ -728,6 +784,34 @@ int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, i
   if (rc) return rc;
   QRows qr = carve_qrows(c->ws, s_rows, cols, &need, pf);
   return matmul_core(c, t, (const uint8_t *)w, rows, cols, x, s_rows, out, qr);
+}
+
+int kmoe_matmul_host(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const float *x,
+                     int64_t s_rows, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (rows < 0 || cols <= 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "bad shape");
+  const int64_t rb = bytes_for(t, cols);
+  if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
+  if (rb < 0) return fail(c, KMOE_E_INVALID, "cols %lld not a multiple of the block size", (long long)cols);
+  if ((uint64_t)w_len < (uint64_t)rb * (uint64_t)rows)
+    return fail(c, KMOE_E_INVALID, "weight buffer %zu < %lld x %lld", w_len, (long long)rows, (long long)rb);
+  if (rows == 0 || s_rows == 0) return KMOE_OK;
+  if (!w || !x || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  const bool wdev = is_device_ptr(w);
+  const size_t wb = wdev ? 0 : align_up((size_t)(rb * rows)), xb = align_up((size_t)(s_rows * cols) * 4);
+  const size_t ob = (size_t)(s_rows * rows) * 4;
+  int rc = ensure_hio(c, wb + xb + ob);
+  if (rc) return rc;
+  uint8_t *wd = wdev ? (uint8_t *)w : c->hio;
+  float *xd = (float *)(c->hio + wb), *od = (float *)(c->hio + wb + xb);
+  if (!wdev) HIP_OK(c, hipMemcpyAsync(wd, w, (size_t)(rb * rows), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipMemcpyAsync(xd, x, (size_t)(s_rows * cols) * 4, hipMemcpyHostToDevice, c->stream));
+  rc = kmoe_matmul(c, t, wd, wdev ? w_len : (size_t)(rb * rows), rows, cols, xd, s_rows, od);
+  if (rc) return rc;
+  HIP_OK(c, hipMemcpyAsync(out, od, ob, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return KMOE_OK;
 }
 
 int kmoe_route(kmoe_ctx *c, const float *router, int32_t E, int64_t d, const float *h, int64_t S, int32_t k,
@@ -1037,6 +1121,15 @@ int kmoe_expert_part(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, cons
   return KMOE_OK;
 }
 
+int kmoe_expert_part_layout(kmoe_ctx *c, uint32_t layer, uint32_t e, int32_t part, int32_t *layout) {
+  if (!c || !layout) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (e >= L->desc.n_expert || part < 0 || part > 2) return fail(c, KMOE_E_INVALID, "expert %u part %d", e, part);
+  *layout = L->tiled[part] ? KMOE_LAYOUT_TILED : KMOE_LAYOUT_GGUF;
+  return KMOE_OK;
+}
+
 int kmoe_shared_expert_create(kmoe_ctx *c, uint32_t layer, int64_t n_ff, int32_t gate_type, int32_t up_type,
                               int32_t down_type) {
   if (!c) return KMOE_E_INVALID;
@@ -1145,7 +1238,8 @@ int kmoe_bytes_per_expert(kmoe_ctx *c, uint32_t layer, uint64_t *bytes) {
 // The MoE FFN of h; with norm, h is norm->f and is produced here first
 // (x += y, f = rmsnorm(x) * w), folded into the single-token router kernel
 // where it supports the shapes, else by the norm kernel.
-static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out, const RouteNorm *norm) {
+static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out, const RouteNorm *norm,
+                   const kmoe_moe_dbg *dbg = nullptr) {
   if (!c) return KMOE_E_INVALID;
   Layer *L = find_layer(c, layer);
   if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
@@ -1182,6 +1276,26 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   MoeWs w = carve_moe(c->ws, S, E, k, d, F, &tmp);
   const int regime = c->regime;
   hipStream_t st = c->stream;
+  // Capture of the int-path integers (kmoe_moe_ffn_dbg): zeroed here, added to by the kernels.
+  BlockDbg gdbg, ddbg;
+  const BlockDbg *gd = nullptr, *dd = nullptr;
+  const int64_t bel_g = D.gate_type == KMOE_Q8_0 ? 32 : 256, bel_d = D.down_type == KMOE_Q8_0 ? 32 : 256;
+  if (dbg) {
+    const size_t ng = (size_t)slots * F * (d / bel_g) * 4, nd = (size_t)slots * d * (F / bel_d) * 4;
+    int32_t *const arr[6] = {dbg->gate_sumi, dbg->gate_mins, dbg->up_sumi, dbg->up_mins, dbg->down_sumi,
+                             dbg->down_mins};
+    for (int i = 0; i < 6; ++i)
+      if (arr[i]) HIP_OK(c, hipMemsetAsync(arr[i], 0, i < 4 ? ng : nd, st));
+    gdbg.s[0] = dbg->gate_sumi;
+    gdbg.m[0] = dbg->gate_mins;
+    gdbg.s[1] = dbg->up_sumi;
+    gdbg.m[1] = dbg->up_mins;
+    ddbg.s[0] = dbg->down_sumi;
+    ddbg.m[0] = dbg->down_mins;
+    gd = &gdbg;
+    dd = &ddbg;
+  }
+  bool x_int = false, h_int = false;  // int8 rows of x / h were produced (for the capture)
   // the norm, where the router kernel does not take it
   bool norm_pending = norm != nullptr;
   auto run_norm = [&]() -> int {
@@ -1196,34 +1310,6 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   }
 
   const int gt = D.gate_type, dt = D.down_type;
-  // One token on the int path over tiled Q4_K experts, on request: the whole
-  // layer as one persistent kernel (route, select, gate/up, Q8_K of h, down,
-  // combine).
-  if (S == 1 && regime != KMOE_REGIME_EXACT && c->decode_path == KMOE_DECODE_FUSED && gt == KMOE_Q4_K &&
-      D.up_type == KMOE_Q4_K && dt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && L->tiled[2] &&
-      layer_dec_fused_supported(d, F, (int32_t)E, (int32_t)k)) {
-    rc = run_norm();
-    if (rc) return rc;
-    DecSelect pub;
-    pub.E = (int32_t)E;
-    pub.K = (int32_t)k;
-    pub.idx = w.idx;
-    pub.wsel = w.wsel;
-    pub.perm = w.perm;
-    pub.offsets = w.offsets;
-    pub.inv = w.inv;
-    pub.n_active = w.n_active;
-    pub.active = w.active;
-    ExpertTier ft{L->arena, (int64_t)L->expert_stride,
-                  {(int64_t)L->part_off[0], (int64_t)L->part_off[1], (int64_t)L->part_off[2]}};
-    hipError_t e = timed(c, "moe_layer_fused", [&]() {
-      return launch_layer_dec_fused(st, L->router, (int32_t)E, d, h, (int32_t)k, D.norm_topk, D.weights_scale, ft, F,
-                                    w.logits, w.xq, w.xd, w.xs, w.h, w.hq, w.hd, w.hs, out, pub,
-                                    c->counters + kFusedSync);
-    });
-    if (e == hipSuccess) goto done;
-    if (e != hipErrorNotSupported) HIP_OK(c, e);
-  }
   {
   // route (transformer.rs:474-496) and dispatch (transformer.rs:525-531). With
   // s_rows < 4 one fused work-group also quantizes x for the int8 path.
@@ -1287,9 +1373,10 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     ds.inv = w.inv;
     ds.n_active = w.n_active;
     ds.active = w.active;
+    x_int = true;
     hipError_t e = timed(c, "moe_gate_up_dec", [&]() {
       return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h,
-                                   select_in_gate_up ? &ds : nullptr);
+                                   select_in_gate_up ? &ds : nullptr, gd);
     });
     if (e == hipErrorNotSupported && select_in_gate_up) {  // complete the routing from the logits, then as below
       LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
@@ -1298,7 +1385,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
                                             w.active, w.rank));
       select_in_gate_up = false;
       e = timed(c, "moe_gate_up_dec", [&]() {
-        return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h, nullptr);
+        return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h, nullptr, gd);
       });
     }
     if (e != hipErrorNotSupported) {
@@ -1306,15 +1393,16 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       // one row per expert: every slot is on the int8 path in either int8 regime
       LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
              launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
+      h_int = true;
       e = timed(c, "moe_down_dec",
-                [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out); });
+                [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out, dd); });
       if (e != hipErrorNotSupported) {
         HIP_OK(c, e);
         goto done;
       }
       // down too wide for registers: finish with the general kernels below
       LAUNCH(c, "moe_down_int",
-             launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y));
+             launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y, 0, dd));
       LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
       goto done;
     }
@@ -1328,10 +1416,11 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       if (is_kq(gt)) LAUNCH(c, "quant_q8k", launch_quant_q8k(st, h, S, d, w.xq, w.xd, w.xs));
       else LAUNCH(c, "quant_q8", launch_quant_q8(st, h, S, d, w.xq, w.xd, w.xs));
     }
+    x_int = true;
     int small_rows = 0;  // experts with 1..small_rows rows are done
     if (small_ok && gt == KMOE_Q4_K && L->tiled[0] && small_supported(F, d, 0)) {
       const hipError_t e = timed(c, "moe_gate_up_small", [&]() {
-        return launch_small(st, 0, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h);
+        return launch_small(st, 0, tier, F, d, rt, regime, max_active, S, w.xq, w.xd, w.xs, w.h, gd);
       });
       if (e == hipSuccess) small_rows = small_rows_for(d, 0, S);
       else if (e != hipErrorNotSupported) HIP_OK(c, e);
@@ -1340,12 +1429,13 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       hipError_t e = hipErrorNotSupported;
       if (mfma && gt == KMOE_Q4_K)
         e = timed(c, "moe_gate_up_mfma", [&]() {
-          return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h, small_rows + 1);
+          return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h, small_rows + 1,
+                                 gd);
         });
       if (e != hipErrorNotSupported) HIP_OK(c, e);
       else
         LAUNCH(c, "moe_gate_up_int", launch_moe_int(st, 0, gt, tier, F, d, rt, regime, max_active, S, w.xq, w.xd,
-                                                    w.xs, w.h, small_rows + 1));
+                                                    w.xs, w.h, small_rows + 1, gd));
     }
   }
   if (any_f32) {
@@ -1358,10 +1448,11 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   if (any_int) {
     LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
            launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, regime, w.hq, w.hd, w.hs));
+    h_int = true;
     int small_rows = 0;
     if (small_ok && dt == KMOE_Q4_K && L->tiled[2] && small_supported(d, F, 1)) {
       const hipError_t e = timed(c, "moe_down_small", [&]() {
-        return launch_small(st, 1, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y);
+        return launch_small(st, 1, tier, d, F, rt, regime, max_active, S, w.hq, w.hd, w.hs, w.y, dd);
       });
       if (e == hipSuccess) small_rows = small_rows_for(F, 1, S);
       else if (e != hipErrorNotSupported) HIP_OK(c, e);
@@ -1370,12 +1461,13 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       hipError_t e = hipErrorNotSupported;
       if (mfma && dt == KMOE_Q4_K)
         e = timed(c, "moe_down_mfma", [&]() {
-          return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y, small_rows + 1);
+          return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y, small_rows + 1,
+                                 dd);
         });
       if (e != hipErrorNotSupported) HIP_OK(c, e);
       else
         LAUNCH(c, "moe_down_int", launch_moe_int(st, 1, dt, tier, d, F, rt, regime, max_active, S, w.hq, w.hd,
-                                                 w.hs, w.y, small_rows + 1));
+                                                 w.hs, w.y, small_rows + 1, dd));
     }
   }
   if (any_f32)
@@ -1386,6 +1478,24 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   }
 
 done:
+  if (dbg) {  // the int8 rows the products read, as the workspace holds them
+    auto cp = [&](void *dst, const void *src, size_t n) -> int {
+      if (dst && n) HIP_OK(c, hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, st));
+      return KMOE_OK;
+    };
+    if (x_int) {
+      rc = cp(dbg->xq, w.xq, (size_t)S * d);
+      if (!rc) rc = cp(dbg->xd, w.xd, (size_t)S * (d / bel_g) * 4);
+      if (!rc) rc = cp(dbg->xs, w.xs, (size_t)S * (d / 16) * 4);
+      if (rc) return rc;
+    }
+    if (h_int) {
+      rc = cp(dbg->hq, w.hq, (size_t)slots * F);
+      if (!rc) rc = cp(dbg->hd, w.hd, (size_t)slots * (F / bel_d) * 4);
+      if (!rc) rc = cp(dbg->hs, w.hs, (size_t)slots * (F / 16) * 4);
+      if (rc) return rc;
+    }
+  }
   if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)
     auto &SH = L->sh;
     Carver cv{c->ws + moe_need};
@@ -1413,6 +1523,38 @@ done:
 
 int kmoe_moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
   return moe_ffn(c, layer, h, S, out, nullptr);
+}
+
+int kmoe_moe_ffn_dbg(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out, const kmoe_moe_dbg *dbg) {
+  if (!c) return KMOE_E_INVALID;
+  if (!dbg || !dbg->gate_sumi || !dbg->up_sumi || !dbg->down_sumi)
+    return fail(c, KMOE_E_INVALID, "kmoe_moe_ffn_dbg: null capture buffer");
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if ((is_kq(L->desc.gate_type) && (!dbg->gate_mins || !dbg->up_mins)) ||
+      (is_kq(L->desc.down_type) && !dbg->down_mins))
+    return fail(c, KMOE_E_INVALID, "kmoe_moe_ffn_dbg: K-quant parts need their mins/offs buffers");
+  return moe_ffn(c, layer, h, S, out, nullptr, dbg);
+}
+
+int kmoe_moe_ffn_host(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  Layer *L = find_layer(c, layer);
+  if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
+  if (S < 0) return fail(c, KMOE_E_INVALID, "negative s_rows");
+  if (S == 0) return KMOE_OK;
+  if (!h || !out) return fail(c, KMOE_E_INVALID, "null pointer");
+  DeviceGuard g(c->device);
+  const size_t n = (size_t)S * L->desc.n_embd * 4, nb = align_up(n);
+  int rc = ensure_hio(c, 2 * nb);
+  if (rc) return rc;
+  float *hd = (float *)c->hio, *od = (float *)(c->hio + nb);
+  HIP_OK(c, hipMemcpyAsync(hd, h, n, hipMemcpyHostToDevice, c->stream));
+  rc = moe_ffn(c, layer, hd, S, od, nullptr);
+  if (rc) return rc;
+  HIP_OK(c, hipMemcpyAsync(out, od, n, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return KMOE_OK;
 }
 
 int kmoe_norm_moe_ffn(kmoe_ctx *c, uint32_t layer, float *x, const float *y, const float *norm_w, float eps,
@@ -1451,6 +1593,7 @@ static int check_table(kmoe_ctx *c, int32_t t, size_t table_len, int64_t n_rows,
 int kmoe_get_rows(kmoe_ctx *c, int32_t t, const void *table, size_t table_len, int64_t n_rows, int64_t cols,
                   const uint32_t *ids, int64_t s_rows, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, table)) return rc_;
   int64_t rb = 0;
   int rc = check_table(c, t, table_len, n_rows, cols, &rb);
   if (rc) return rc;
@@ -1472,6 +1615,7 @@ int kmoe_get_rows(kmoe_ctx *c, int32_t t, const void *table, size_t table_len, i
 int kmoe_get_rows_dev(kmoe_ctx *c, int32_t t, const void *table, size_t table_len, int64_t n_rows, int64_t cols,
                       const uint32_t *ids_dev, int64_t s_rows, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, table)) return rc_;
   int64_t rb = 0;
   int rc = check_table(c, t, table_len, n_rows, cols, &rb);
   if (rc) return rc;
@@ -1497,6 +1641,7 @@ int kmoe_rmsnorm(kmoe_ctx *c, float *x, const float *y, const float *w, int64_t 
 int kmoe_norm_matmul(kmoe_ctx *c, float *x, const float *y, const float *norm_w, float eps, int t, const void *w,
                      size_t w_len, int64_t rows, int64_t cols, int64_t s_rows, float *h, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   if (rows < 0 || cols <= 0 || s_rows < 0) return fail(c, KMOE_E_INVALID, "bad shape");
   const int64_t rb = bytes_for(t, cols);
   if (block_size(t) < 0) return fail(c, KMOE_E_UNSUPPORTED, "ggml type %d has no kernel", t);
@@ -1594,6 +1739,7 @@ int kmoe_attention_matmul(kmoe_ctx *c, const float *q, const uint16_t *k_cache, 
                           const int32_t *pos_dev, int64_t n_ctx, float *attn, int t, const void *w, size_t w_len,
                           int64_t rows, float *out) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_ctx <= 0)
     return fail(c, KMOE_E_INVALID, "attention: need n_head %% n_kv == 0 and n_ctx > 0");
   if (!attn_supported(head_dim, n_head / n_kv))
@@ -1668,6 +1814,7 @@ int kmoe_norm_matmul_rope_kv(kmoe_ctx *c, float *x, const float *y, const float 
                              const float *inv_freq, int32_t neox, int64_t n_ctx, float *q_out, uint16_t *k_cache,
                              uint16_t *v_cache) {
   if (!c) return KMOE_E_INVALID;
+  if (int rc_ = reject_tiled(c, w)) return rc_;
   if (n_head <= 0 || n_kv <= 0 || head_dim <= 0 || rope_dim <= 0 || rope_dim > head_dim || rope_dim % 2 ||
       rope_dim > 256 || n_ctx <= 0)
     return fail(c, KMOE_E_INVALID, "rope: need 0 < rope_dim <= min(head_dim, 256), rope_dim even");

@@ -56,6 +56,21 @@ struct ExpertTier {
   int64_t off[3];
 };
 
+// Per-block integer accumulators of the int-path expert products, written by
+// the kernels of one captured moe_ffn: per (slot p in dispatch order, weight
+// row r, block b) at [(p*rows + r)*nblk + b], nblk = cols / block elements,
+// the integers of dot_q4_k_8k (sumi, mins), dot_q6_k_8k (sumi, offs) or
+// dot_q8_0 (p; m unused). s[0]/m[0]: gate (or down), s[1]/m[1]: up. The
+// caller zeroes them; kernels add their quarter-superblock parts with integer
+// atomics (exact in any order). All null: no capture.
+struct BlockDbg {
+  int32_t *s[2] = {nullptr, nullptr};
+  int32_t *m[2] = {nullptr, nullptr};
+};
+__device__ __forceinline__ void dbg_add(int32_t *base, int64_t o, int v) {
+  if (base) atomicAdd(base + o, v);
+}
+
 // ---- expert tier layout (kmoe_layout.hip): GGUF Q4_K rows <-> tiled Q4_K rows
 // (rows of nb superblocks; src and dst must not overlap).
 hipError_t launch_tq4_convert(hipStream_t st, const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb,
@@ -80,7 +95,8 @@ struct DecSelect;
 // routing (hipErrorNotSupported where decode_gate_up_can_select is false).
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                 const int32_t *xbs, float *h, const DecSelect *sel = nullptr);
+                                 const int32_t *xbs, float *h, const DecSelect *sel = nullptr,
+                                 const BlockDbg *dbg = nullptr);
 // Whether launch_decode_gate_up can select the experts for this layer shape.
 bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K);
 // Expert selection done inside the decode gate/up kernel: the token's logits
@@ -103,7 +119,7 @@ bool dec_gate_up_tq4_supported(int64_t cols, int ru);
 hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols,
                                   const Routing &rt, int max_active, const int8_t *xq, const float *xd,
                                   const int32_t *xbs, float *h, int ru, int wg_per_cu_x16,
-                                  const DecSelect *sel = nullptr);
+                                  const DecSelect *sel = nullptr, const BlockDbg *dbg = nullptr);
 // Q4_K rows of one matrix (GGUF bytes, or tiled) against one Q8_K row:
 // out[r] (kmoe_decode.hip). hipErrorNotSupported for rows narrower than 48 or wider than
 // 256 quarter-superblocks or misaligned pointers (activations 16 bytes, GGUF
@@ -111,15 +127,10 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
 bool dec_rows_supported(int64_t cols);
 hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                            const float *xd, const int32_t *xbs, float *out);
-// Tiled Q4_K down projection + combine for one token (kmoe_decode.hip): the k
-// active slots' Q8_K rows staged in LDS, one wave per output row.
-bool dec_down_tq4_supported(int64_t rows, int64_t cols, int k);
-hipError_t launch_dec_down_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols, const Routing &rt,
-                               int k, const int8_t *hq, const float *hd, const int32_t *hbs, float *out);
 // Down projection + combine for one token: out[r] = sum_e (asc) w_e * y_e[r].
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
-                                      float *out);
+                                      float *out, const BlockDbg *dbg = nullptr);
 // Block sums (debug path of the same device code).
 hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                              const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins);
@@ -128,17 +139,8 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
 // min_rows: experts with fewer rows are left to another kernel.
 hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
-                          const float *xd, const int32_t *xbs, float *out, int min_rows = 0);
-
-// ---- the whole single-token layer in one persistent kernel (kmoe_fused.hip):
-// Q4_K tiled experts; routing published into pub's arrays; sync: zeroed
-// device words (16 + K*F/256 of them), zero again after the kernel, word 3 a
-// sticky time-out flag. hipErrorNotSupported for shapes it does not cover.
-bool layer_dec_fused_supported(int64_t d, int64_t F, int32_t E, int32_t K);
-hipError_t launch_layer_dec_fused(hipStream_t st, const float *router, int32_t E, int64_t d, const float *x, int32_t K,
-                                  int32_t norm_topk, float weights_scale, const ExpertTier &tier, int64_t F,
-                                  float *logits, int8_t *xq, float *xd, int32_t *xs, float *h, int8_t *hq, float *hd,
-                                  int32_t *hs, float *out, const DecSelect &pub, uint32_t *sync);
+                          const float *xd, const int32_t *xbs, float *out, int min_rows = 0,
+                          const BlockDbg *dbg = nullptr);
 
 // ---- int8 matrix-core path (kmoe_mfma.hip), Q4_K weights x Q8_K rows
 // Token rows at which the matrix-core kernels take over (KMOE_MFMA_MIN_ROWS, default 8).
@@ -148,7 +150,7 @@ bool moe_mfma_supported(int64_t rows, int64_t cols);
 // hipErrorNotSupported: shape or activation alignment (16 B) not covered.
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out, int min_rows = 0);
+                           const int32_t *abs, float *out, int min_rows = 0, const BlockDbg *dbg = nullptr);
 // Plain GGUF rows: out[s*rows + r], or, with sumi/mins set, the per-block
 // integer accumulators at [(s*rows + r)*nb + b] (ad unused).
 hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *aq,
@@ -164,7 +166,7 @@ bool small_supported(int64_t rows, int64_t cols, int mode);
 int small_rows_for(int64_t cols, int mode, int64_t max_rows);
 hipError_t launch_small(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                         const Routing &rt, int regime, int max_active, int64_t max_rows, const int8_t *xq,
-                        const float *xd, const int32_t *xbs, float *out);
+                        const float *xd, const int32_t *xbs, float *out, const BlockDbg *dbg = nullptr);
 
 // ---- f32 path (kmoe_gemm_f32.hip): dequantized weights x f32 activations
 // Partial-sum floats the launchers below use for this shape (0: no column
@@ -275,36 +277,6 @@ hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, 
 hipError_t launch_rope_kv(hipStream_t st, const float *q, const float *k, const float *v, int64_t s_rows, int nh,
                           int nkv, int hd, int rd, int64_t pos0, const int32_t *pos_dev, const float *inv_freq,
                           int neox, int64_t n_ctx, float *q_out, uint16_t *kc, uint16_t *vc);
-hipError_t launch_swiglu(hipStream_t st, float *g, const float *u, int64_t n);
-// out[s] += sigmoid(logits[s]) * y[s] (logits null: scale 1).
-hipError_t launch_shared_add(hipStream_t st, float *out, const float *y, const float *logits, int64_t S, int64_t d);
-
-// out[s] = sum over the token's experts in ascending id of w * y[slot].
-hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out);
-
-
-// ---- the rest of the decoder layer (kmoe_decoder.hip) ----
-// Rows ids[0..s_rows) of a GGUF table [n_rows, cols] of type t (F32, F16,
-// Q8_0, Q4_K, Q6_K), dequantized to f32 out [s_rows, cols].
-hipError_t launch_get_rows(hipStream_t st, int t, const uint8_t *table, int64_t row_bytes, int64_t n_rows,
-                           int64_t cols, const uint32_t *ids, int64_t s_rows, float *out);
-hipError_t launch_add_rmsnorm(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
-                              float eps, float *out);
-// RMSNorm followed by the Q8_K (q8k) or Q8 quantization of its output, in one
-// kernel; hipErrorNotSupported when the shape or alignment does not allow it.
-hipError_t launch_rmsnorm_quant(hipStream_t st, float *x, const float *y, const float *w, int64_t rows, int64_t dim,
-                                float eps, float *out, bool q8k, int8_t *q, float *qd, int32_t *qs);
-hipError_t launch_rope(hipStream_t st, float *x, int64_t s_rows, int n_heads, int hd, int rd, int64_t pos0,
-                       const int32_t *pos_dev, const float *inv_freq, int neox);
-hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64_t s_rows, int64_t kvw,
-                           int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, uint16_t *kc, uint16_t *vc);
-// Chunks of 64 positions covering n_max positions, and the partials' size.
-int attn_chunks(int64_t n_max);
-int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int chunks);
-bool attn_supported_hd(int hd);
-hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
-                            int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int chunks,
-                            float *part, float *out);
 hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, int64_t n, float *out);
 hipError_t launch_add_rows(hipStream_t st, float *x, const float *b, int64_t rows, int64_t cols);
 // argmax of l[0..n) into out[0]; pos_dev (may be null) += advance afterwards.

@@ -54,6 +54,7 @@ struct MvArgs {
   int sel_on;    // M_GATE_UP, one token: select the experts from sel.logits here
   DecSelect sel;
   QkvRope rope;  // M_QKV: the epilogue of the one-token q/k/v projection
+  BlockDbg dbg;  // grouped modes: per-block integers of the part(s) computed
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -436,11 +437,20 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                     a.imins[o] = ms;
                   }
                 } else {
+                  const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + sb;  // grouped modes' capture
+                  if (a.dbg.s[0]) {
+                    atomicAdd(a.dbg.s[0] + o, si);
+                    atomicAdd(a.dbg.m[0] + o, mi);
+                  }
                   acc0[tk] = fmaf(d0 * xd, (float)si, acc0[tk]);
                   acc0[tk] = fmaf(-(m0 * xd), (float)mi, acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
                     const float d1 = f16_bits_to_f32(w1.hdr.x), m1 = f16_bits_to_f32(w1.hdr.x >> 16);
                     q4k_ints(w1, k, xq_sb, xbs_sb, si, mi);
+                    if (a.dbg.s[1]) {
+                      atomicAdd(a.dbg.s[1] + o, si);
+                      atomicAdd(a.dbg.m[1] + o, mi);
+                    }
                     acc1[tk] = fmaf(d1 * xd, (float)si, acc1[tk]);
                     acc1[tk] = fmaf(-(m1 * xd), (float)mi, acc1[tk]);
                   }
@@ -482,9 +492,18 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                     a.imins[o] = os;
                   }
                 } else {
+                  const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + sb;  // grouped modes' capture
+                  if (a.dbg.s[0]) {
+                    atomicAdd(a.dbg.s[0] + o, si);
+                    atomicAdd(a.dbg.m[0] + o, oi);
+                  }
                   acc0[tk] = fmaf(d0 * xd, (float)(si - 32 * oi), acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
                     ints6(w1, x0, x1, x2, x3, bs, si, oi);
+                    if (a.dbg.s[1]) {
+                      atomicAdd(a.dbg.s[1] + o, si);
+                      atomicAdd(a.dbg.m[1] + o, oi);
+                    }
                     acc1[tk] = fmaf(f16_bits_to_f32(w1.d) * xd, (float)(si - 32 * oi), acc1[tk]);
                   }
                 }
@@ -505,10 +524,13 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                 if constexpr (MODE == M_SUMS) {
                   a.isumi[((int64_t)(c0 + tk) * rows + r) * nblk + t] = p;
                 } else {
+                  const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + t;  // grouped modes' capture
+                  if (a.dbg.s[0]) atomicAdd(a.dbg.s[0] + o, p);
                   acc0[tk] = fmaf(dw * xd, (float)p, acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
                     float dw1;
                     const int p1 = q80_int(w1, xq_b, dw1);
+                    if (a.dbg.s[1]) atomicAdd(a.dbg.s[1] + o, p1);
                     acc1[tk] = fmaf(dw1 * xd, (float)p1, acc1[tk]);
                   }
                 }
@@ -627,9 +649,12 @@ __device__ __forceinline__ void w_load(WTask<TYPE, TILED> &w, const uint8_t *row
   else w.w = q80_load(row, t);
 }
 
-// acc += (float) dot of one task against its activation slice.
+// acc += (float) dot of one task against its activation slice. ds / dm
+// (when non-null): the row's per-block integer accumulators, to which this
+// task's integers are added (its block is t / tasks per block).
 template <int TYPE, bool TILED>
-__device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, const ActSlice<TYPE> &s, float acc) {
+__device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, const ActSlice<TYPE> &s, float acc,
+                                          int32_t *ds = nullptr, int32_t *dm = nullptr) {
   if constexpr (TYPE == T_Q4_K) {
     const Q4kW &w = wt.w;
     const int k = t & 3;
@@ -655,6 +680,10 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, c
     hi = sdot4((w.qb.w >> 4) & m, (uint32_t)s.x3.w, hi);
     const int sumi = sA * lo + sB * hi;
     const int mins = mA * (s.bs.x + s.bs.y) + mB * (s.bs.z + s.bs.w);
+    if (ds) {
+      atomicAdd(ds + (t >> 2), sumi);
+      if (dm) atomicAdd(dm + (t >> 2), mins);
+    }
     const float d = f16_bits_to_f32(w.hdr.x), dmin = f16_bits_to_f32(w.hdr.x >> 16);
     acc = fmaf(d * s.d, (float)sumi, acc);
     acc = fmaf(-(dmin * s.d), (float)mins, acc);
@@ -663,6 +692,10 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, c
     int sumi, offs;
     if constexpr (TILED) q6t_ints(wt.w, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
     else q6k_ints(wt.w, t & 3, s.x0, s.x1, s.x2, s.x3, s.bs, sumi, offs);
+    if (ds) {
+      atomicAdd(ds + (t >> 2), sumi);
+      if (dm) atomicAdd(dm + (t >> 2), offs);
+    }
     return fmaf(f16_bits_to_f32(wt.w.d) * s.d, (float)(sumi - 32 * offs), acc);
   } else {
     const Q80W &w = wt.w;
@@ -687,6 +720,7 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, c
     p = sdot4(q[5], (uint32_t)s.x1.y, p);
     p = sdot4(q[6], (uint32_t)s.x1.z, p);
     p = sdot4(q[7], (uint32_t)s.x1.w, p);
+    if (ds) atomicAdd(ds + t, p);
     return fmaf(dw * s.d, (float)p, acc);
   }
 }
@@ -801,7 +835,10 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
               const int64_t r = r0 + (int64_t)u * RPW;
-              if (r < rows) acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u]);
+              const int64_t o = (p * rows + r) * nblk;
+              if (r < rows)
+                acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u], a.dbg.s[0] ? a.dbg.s[0] + o : nullptr,
+                                        a.dbg.m[0] ? a.dbg.m[0] + o : nullptr);
             }
           }
         }
@@ -842,8 +879,16 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
             if (r < rows) {
-              acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u]);
-              if constexpr (MODE == M_GATE_UP) acc1[u] = task_dot<TYPE>(w1[u], t, act[i], acc1[u]);
+              if constexpr (MODE == M_GATE_UP) {
+                const int64_t o = (p0 * rows + r) * nblk;
+                const BlockDbg &g = a.dbg;
+                acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u], g.s[0] ? g.s[0] + o : nullptr,
+                                         g.m[0] ? g.m[0] + o : nullptr);
+                acc1[u] = task_dot<TYPE>(w1[u], t, act[i], acc1[u], g.s[1] ? g.s[1] + o : nullptr,
+                                         g.m[1] ? g.m[1] + o : nullptr);
+              } else {
+                acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u]);
+              }
             }
           }
         }
@@ -883,7 +928,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 
 constexpr int kSplitRbMax = 64;
 
-template <int TYPE, int RU, int TPL>
+template <int TYPE, int RU, int TPL, bool DBG>
 __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   __shared__ float part[4][kSplitRbMax];
   __shared__ float outv[kSplitRbMax];
@@ -957,7 +1002,15 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
       acc[u] = 0.0f;
 #pragma unroll
       for (int i = 0; i < TPL; ++i) {
-        const float v = task_dot<TYPE>(w[u][i], min(tk[i], ntasks - 1), ac[i], acc[u]);
+        int32_t *ds = nullptr, *dm = nullptr;
+        if constexpr (DBG) {
+          if (tv[i] && ic.rr + u < nr) {
+            const int64_t o = (ic.p * rows + r0 + ic.rr + u) * nblk;
+            ds = a.dbg.s[0] + o;
+            dm = a.dbg.m[0] ? a.dbg.m[0] + o : nullptr;
+          }
+        }
+        const float v = task_dot<TYPE>(w[u][i], min(tk[i], ntasks - 1), ac[i], acc[u], ds, dm);
         acc[u] = tv[i] ? v : acc[u];
       }
       acc[u] = group_sum<64>(acc[u]);
@@ -1037,16 +1090,6 @@ int gu_wgpc16() {
 // KMOE_DOWN_RU: rows per split-K item (1, 2 or 4, default 4).
 int down_ru() {
   static const int v = env_int("KMOE_DOWN_RU", 4);
-  return v;
-}
-// KMOE_DOWN_KERNEL=rows selects the whole-row down kernel (activation rows
-// staged in LDS, one wave per output row) for single-token Q4_K down; the
-// default is the split-K kernel, measured as fast or faster on MI355X.
-bool use_dec_down() {
-  static const bool v = [] {
-    const char *e = getenv("KMOE_DOWN_KERNEL");
-    return e && !strcmp(e, "rows");
-  }();
   return v;
 }
 int down_wg_per_cu() {
@@ -1207,8 +1250,9 @@ bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
 
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                 const int32_t *xbs, float *h, const DecSelect *sel) {
+                                 const int32_t *xbs, float *h, const DecSelect *sel, const BlockDbg *dbg) {
   MvArgs a{};
+  if (dbg) a.dbg = *dbg;
   a.rows = rows;
   a.cols = cols;
   a.xq = xq;
@@ -1224,7 +1268,7 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   }
   if (type == T_Q4_K) {
     const hipError_t e =
-        launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel);
+        launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel, dbg);
     if (e != hipErrorNotSupported) return e;
     return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
   }
@@ -1269,8 +1313,9 @@ hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, in
 
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
-                                      float *out) {
+                                      float *out, const BlockDbg *dbg) {
   MvArgs a{};
+  if (dbg) a.dbg = *dbg;
   a.s_rows = 1;
   a.rows = rows;
   a.cols = cols;
@@ -1283,8 +1328,6 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
   const int64_t nblk = cols / (is_kquant(type) ? 256 : 32);
   const int ntasks = (int)((is_kquant(type) ? 4 : 1) * nblk);
   // one token: its topk experts are distinct, so k slots are active
-  if (type == T_Q4_K && use_dec_down() && dec_down_tq4_supported(rows, cols, rt.topk))
-    return launch_dec_down_tq4(st, tier, rows, cols, rt, rt.topk, hq, hd, hbs, out);
   if (ntasks >= 128 && ntasks <= 4 * 64 * 2) {
     // persistent split-K: one work-group per CU, rows split evenly
     const int64_t G = (int64_t)cu_count() * down_wg_per_cu();
@@ -1292,22 +1335,28 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
     if (rb <= kSplitRbMax) {
       const unsigned grid = (unsigned)((rows + rb - 1) / rb);
       const int tpl = (ntasks + 3) / 4 > 64 ? 2 : 1;
+#define KMOE_SPLITK(T, RU, TP)                                                                        \
+  do {                                                                                                \
+    if (dbg) KMOE_LAUNCH((k_down_splitk<T, RU, TP, true>), dim3(grid), dim3(256), 0, st, a, rb);      \
+    else KMOE_LAUNCH((k_down_splitk<T, RU, TP, false>), dim3(grid), dim3(256), 0, st, a, rb);         \
+  } while (0)
       if (type == T_Q4_K) {
         if (tpl == 1) {
           const int ru = down_ru();
-          if (ru == 1) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 1, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-          else if (ru == 2) KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-          else KMOE_LAUNCH((k_down_splitk<T_Q4_K, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
+          if (ru == 1) KMOE_SPLITK(T_Q4_K, 1, 1);
+          else if (ru == 2) KMOE_SPLITK(T_Q4_K, 2, 1);
+          else KMOE_SPLITK(T_Q4_K, 4, 1);
         } else {
-          KMOE_LAUNCH((k_down_splitk<T_Q4_K, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+          KMOE_SPLITK(T_Q4_K, 2, 2);
         }
       } else if (type == T_Q6_K) {  // 26 registers per task: fewer rows per item
-        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q6_K, 2, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-        else KMOE_LAUNCH((k_down_splitk<T_Q6_K, 1, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        if (tpl == 1) KMOE_SPLITK(T_Q6_K, 2, 1);
+        else KMOE_SPLITK(T_Q6_K, 1, 2);
       } else {
-        if (tpl == 1) KMOE_LAUNCH((k_down_splitk<T_Q8_0, 4, 1>), dim3(grid), dim3(256), 0, st, a, rb);
-        else KMOE_LAUNCH((k_down_splitk<T_Q8_0, 2, 2>), dim3(grid), dim3(256), 0, st, a, rb);
+        if (tpl == 1) KMOE_SPLITK(T_Q8_0, 4, 1);
+        else KMOE_SPLITK(T_Q8_0, 2, 2);
       }
+#undef KMOE_SPLITK
       return hipGetLastError();
     }
   }
@@ -1365,10 +1414,11 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
 
 hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t s_rows, const int8_t *xq,
-                          const float *xd, const int32_t *xbs, float *out, int min_rows) {
+                          const float *xd, const int32_t *xbs, float *out, int min_rows, const BlockDbg *dbg) {
   if (rows == 0 || max_active == 0) return hipSuccess;
   if (!act_fits(type, cols)) return hipErrorInvalidValue;
   MvArgs a{};
+  if (dbg) a.dbg = *dbg;
   a.rows = rows;
   a.cols = cols;
   a.xq = xq;

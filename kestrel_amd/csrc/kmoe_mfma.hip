@@ -80,6 +80,7 @@ struct MfmaArgs {
   int32_t *sumi, *mins;  // MF_SUMS: [(s*rows + r)*nb + b]
   int regime;
   int min_rows;          // grouped modes: experts with fewer rows are another kernel's
+  BlockDbg dbg;          // grouped modes with DBG: per-superblock integers (gate/down 0, up 1)
 };
 
 // One LDS stage (superblock b of the pass's 128 token rows):
@@ -130,7 +131,7 @@ __device__ __forceinline__ void lds_dma16(const void *g, uint8_t *lds_wave_base)
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
 }
 
-template <int MODE>
+template <int MODE, bool DBG = false>
 __global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
   constexpr bool TILED = MODE == MF_GATE_UP || MODE == MF_DOWN;  // expert tier rows are tiled, plain rows GGUF
   // Two stages as distinct objects: each access names its stage statically, so
@@ -318,6 +319,20 @@ __global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
               }
             }
           } else {
+            if constexpr (DBG) {  // the superblock's integers, complete in this lane
+              int32_t *ds = a.dbg.s[mat == 1 ? 1 : 0], *dm = a.dbg.m[mat == 1 ? 1 : 0];
+              if (tl < nt) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                  const int64_t rw = r_out + 8 * (v >> 2) + (v & 3);
+                  if (rw < rows) {
+                    const int64_t o = ((p0 + t0 + tl) * rows + rw) * nb + b;
+                    ds[o] = H[v];
+                    dm[o] = (int)N[v];
+                  }
+                }
+              }
+            }
             const float adt = *(const float *)(S + kStA + kStM + 4 * tl);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
@@ -398,7 +413,7 @@ bool moe_mfma_supported(int64_t rows, int64_t cols) {
 
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out, int min_rows) {
+                           const int32_t *abs, float *out, int min_rows, const BlockDbg *dbg) {
   if (!moe_mfma_supported(rows, cols) || !aligned16(aq) || !aligned16(abs)) return hipErrorNotSupported;
   if (max_active == 0) return hipSuccess;
   MfmaArgs a{};
@@ -412,10 +427,16 @@ hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int
   a.out = out;
   a.regime = regime;
   a.min_rows = min_rows;
+  if (dbg) a.dbg = *dbg;
   const int64_t rows_per_wg = 128;
   const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)max_active);
-  if (mode == MF_GATE_UP) KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP>), grid, dim3(512), 0, st, a);
-  else KMOE_LAUNCH((k_moe_mfma<MF_DOWN>), grid, dim3(512), 0, st, a);
+  if (mode == MF_GATE_UP) {
+    if (dbg) KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP, true>), grid, dim3(512), 0, st, a);
+    else KMOE_LAUNCH((k_moe_mfma<MF_GATE_UP>), grid, dim3(512), 0, st, a);
+  } else {
+    if (dbg) KMOE_LAUNCH((k_moe_mfma<MF_DOWN, true>), grid, dim3(512), 0, st, a);
+    else KMOE_LAUNCH((k_moe_mfma<MF_DOWN>), grid, dim3(512), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -200,11 +200,11 @@ __global__ void __launch_bounds__(256) k_route_topk(const float *__restrict__ lo
   float wsel[16];
   uint32_t isel[16];
   for (int j = 0; j < k; ++j) {
-    // Largest p, ties to the lower index: key = (bits(p) << 32) | ~index.
+    // Largest p, ties to the lower index: key = (p_rank_key(p) << 32) | ~index.
     uint64_t best = 0;
     for (int e = lane; e < E; e += 64) {
       if (taken[wave][e]) continue;
-      const uint64_t key = ((uint64_t)__float_as_uint(P[wave][e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+      const uint64_t key = ((uint64_t)p_rank_key(P[wave][e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
       best = key > best ? key : best;
     }
 #pragma unroll

@@ -40,12 +40,19 @@ __device__ __forceinline__ float wave_fmax_u(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Rank key of a routing probability p >= +0 (its bits, monotone in p). A
+// NaN p ranks as +0: the reference's sort comparator treats NaN as equal to
+// everything and falls back to index order (transformer.rs:484), and its
+// softmax makes every p of a row NaN once one logit is NaN or +inf, so such a
+// row selects experts 0..k-1 in index order.
+__device__ __forceinline__ uint32_t p_rank_key(float p) { return p != p ? 0u : __float_as_uint(p); }
+
 // One token, one whole wave. lv[i] holds the logit of expert lane + 64*i
 // (E <= 64*NPER; entries past E are ignored). p is this wave's LDS scratch of
 // at least E floats. On return sel[j] and w[j], j < K, are the selected
 // experts in selection order and their weights, identical in every lane:
 //   p_e = exp(l_e - max) / (sum in expert order), correctly rounded exp;
-//   K rounds of the largest p (compared as bits, p >= +0), ties to the lower
+//   K rounds of the largest p (compared by p_rank_key), ties to the lower
 //   index; if norm_topk, w /= max(sum of the selected p, 2^-14); then w *=
 //   wscale unless wscale is 0 or 1.
 template <int NPER>
@@ -88,7 +95,7 @@ __device__ __forceinline__ void wave_route_one(float (&lv)[NPER], int E, int K, 
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
       const int e = lane + 64 * i;
-      const uint32_t u = __float_as_uint(lv[i]);
+      const uint32_t u = p_rank_key(lv[i]);
       if (e < E && !((taken >> i) & 1u) && (bi == NPER || u > best)) {
         best = u;
         bi = i;

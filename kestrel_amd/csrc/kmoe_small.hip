@@ -38,6 +38,7 @@ struct SmallArgs {
   int regime;
   int32_t groups;      // gate/up: work-groups along one expert's rows
   int32_t rb;          // down: rows per work-group
+  BlockDbg dbg;        // DBG kernels: per-superblock integers (gate/down 0, up 1)
 };
 
 __device__ __forceinline__ bool small_int_regime(int regime, int n) {
@@ -64,8 +65,10 @@ __device__ __forceinline__ TaskW unpack_task(const u32x4 &hd, const u32x4 &qa, c
   w.dmin = f16_bits_to_f32(hd.x >> 16);
   return w;
 }
-// (d*xd) * sumi - (dmin*xd) * mins of one task against one token's slice.
-__device__ __forceinline__ float task_value(const TaskW &w, const Slice &s) {
+// (d*xd) * sumi - (dmin*xd) * mins of one task against one token's slice;
+// with ds non-null, sumi and mins are also added at ds[o] and dm[o].
+__device__ __forceinline__ float task_value(const TaskW &w, const Slice &s, int32_t *ds = nullptr,
+                                            int32_t *dm = nullptr, int64_t o = 0) {
   const int X[16] = {s.x0.x, s.x0.y, s.x0.z, s.x0.w, s.x1.x, s.x1.y, s.x1.z, s.x1.w,
                      s.x2.x, s.x2.y, s.x2.z, s.x2.w, s.x3.x, s.x3.y, s.x3.z, s.x3.w};
   int lo = 0, hi = 0;
@@ -76,6 +79,10 @@ __device__ __forceinline__ float task_value(const TaskW &w, const Slice &s) {
   }
   const int sumi = w.sA * lo + w.sB * hi;
   const int mins = w.mA * s.bsA + w.mB * s.bsB;
+  if (ds) {
+    atomicAdd(ds + o, sumi);
+    atomicAdd(dm + o, mins);
+  }
   return fmaf(w.d * s.d, (float)sumi, -((w.dmin * s.d) * (float)mins));
 }
 
@@ -92,7 +99,7 @@ __device__ __forceinline__ void load_slice(Slice &s, const int8_t *xq, const flo
   s.d = xd[row * (cols / 256) + sb];
 }
 
-template <int TPL, int NT, int RU>
+template <int TPL, int NT, int RU, bool DBG>
 __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -158,7 +165,16 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
           if (j < n) {  // uniform: the expert's row count
-            const float vg = task_value(wg, s[t][j]), vu = task_value(wu, s[t][j]);
+            float vg, vu;
+            if constexpr (DBG) {
+              const bool on = tv[t] && r0 + u < rows;
+              const int64_t o = ((p0 + j) * rows + r0 + u) * nb + ((lane + 64 * t) >> 2);
+              vg = task_value(wg, s[t][j], on ? a.dbg.s[0] : nullptr, a.dbg.m[0], o);
+              vu = task_value(wu, s[t][j], on ? a.dbg.s[1] : nullptr, a.dbg.m[1], o);
+            } else {
+              vg = task_value(wg, s[t][j]);
+              vu = task_value(wu, s[t][j]);
+            }
             gacc[j] += tv[t] ? vg : 0.0f;
             uacc[j] += tv[t] ? vu : 0.0f;
           }
@@ -185,7 +201,7 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
 constexpr int kSmallRbMax = 32;
 constexpr int kSmallBatchMax = 8;  // batches (tokens) up to this size use these kernels
 
-template <int NT, int RU>
+template <int NT, int RU, bool DBG>
 __global__ void __launch_bounds__(256) k_small_down(SmallArgs a) {
   __shared__ float part[4][kSmallRbMax][NT];
   const int lane = threadIdx.x & 63;
@@ -232,7 +248,14 @@ __global__ void __launch_bounds__(256) k_small_down(SmallArgs a) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if (j < n) {  // uniform: the expert's row count
-          float v = task_value(w, s[j]);
+          float v;
+          if constexpr (DBG) {
+            const bool on = tv && b0 + u < nr;
+            v = task_value(w, s[j], on ? a.dbg.s[0] : nullptr, a.dbg.m[0],
+                           ((p0 + j) * rows + r0 + b0 + u) * nb + sb);
+          } else {
+            v = task_value(w, s[j]);
+          }
           v = group_sum<64>(tv ? v : 0.0f);
           if (lane == 0 && b0 + u < nr) part[wave][b0 + u][j] = v;
         }
@@ -282,11 +305,11 @@ int small_rows_for(int64_t cols, int mode, int64_t max_rows) {
 
 hipError_t launch_small(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                         const Routing &rt, int regime, int max_active, int64_t max_rows, const int8_t *xq,
-                        const float *xd, const int32_t *xbs, float *out) {
+                        const float *xd, const int32_t *xbs, float *out, const BlockDbg *dbg) {
   if (rows <= 0 || max_active <= 0) return hipSuccess;
   const int nt = small_rows_for(cols, mode, max_rows);
   if (!small_supported(rows, cols, mode) || nt == 0) return hipErrorNotSupported;
-  SmallArgs a{tier, rt, rows, cols, xq, xd, xbs, out, regime, 0, 0};
+  SmallArgs a{tier, rt, rows, cols, xq, xd, xbs, out, regime, 0, 0, dbg ? *dbg : BlockDbg{}};
   const int cus = small_cus();
   if (mode == 0) {
     const int tpl = 4 * (cols / 256) <= 64 ? 1 : 2;
@@ -299,7 +322,10 @@ hipError_t launch_small(hipStream_t st, int mode, const ExpertTier &tier, int64_
     a.groups = (int32_t)((need + per - 1) / per);
     const dim3 grid((unsigned)a.groups, (unsigned)max_active);
 #define KMOE_SGU(TP, N)                                                          \
-  KMOE_LAUNCH((k_small_gate_up<TP, N, RU>), grid, dim3(256), 0, st, a)
+  do {                                                                           \
+    if (dbg) KMOE_LAUNCH((k_small_gate_up<TP, N, RU, true>), grid, dim3(256), 0, st, a);   \
+    else KMOE_LAUNCH((k_small_gate_up<TP, N, RU, false>), grid, dim3(256), 0, st, a);      \
+  } while (0)
     if (tpl == 1) {
       if (nt == 2) KMOE_SGU(1, 2);
       else KMOE_SGU(1, 4);
@@ -317,8 +343,13 @@ hipError_t launch_small(hipStream_t st, int mode, const ExpertTier &tier, int64_
     if (rb > kSmallRbMax) rb = kSmallRbMax;
     a.rb = (int32_t)rb;
     const dim3 grid((unsigned)((rows + rb - 1) / rb), (unsigned)max_active);
-    if (nt == 2) KMOE_LAUNCH((k_small_down<2, RU>), grid, dim3(256), 0, st, a);
-    else KMOE_LAUNCH((k_small_down<4, RU>), grid, dim3(256), 0, st, a);
+    if (nt == 2) {
+      if (dbg) KMOE_LAUNCH((k_small_down<2, RU, true>), grid, dim3(256), 0, st, a);
+      else KMOE_LAUNCH((k_small_down<2, RU, false>), grid, dim3(256), 0, st, a);
+    } else {
+      if (dbg) KMOE_LAUNCH((k_small_down<4, RU, true>), grid, dim3(256), 0, st, a);
+      else KMOE_LAUNCH((k_small_down<4, RU, false>), grid, dim3(256), 0, st, a);
+    }
   }
   return hipGetLastError();
 }

@@ -119,6 +119,7 @@ class Decoder:
         self.pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
         self.token_dev = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph = None
+        self._graph_gen = None  # the context's workspace generation the graph was captured at
         self._graph_bufs = None
 
     def _moe_layer(self, l: int, lid: int, tensors: dict) -> int:
@@ -262,6 +263,10 @@ class Decoder:
                 out[i:i + 1].copy_(self.token_dev)
             self.cached += n
             return out
+        if self.graph is not None and self.ctx.workspace_generation() != self._graph_gen:
+            # a workspace the graph points into was reallocated since the capture
+            # (a longer prompt chunk, another caller of the context): capture again
+            self.graph = None
         if self.graph is None:
             # warm-up call at the same shapes grows every workspace first
             pos, tok = self.pos_dev.clone(), self.token_dev.clone()
@@ -277,6 +282,7 @@ class Decoder:
             finally:
                 self.ctx.set_stream(torch.cuda.current_stream())
             self.graph = g
+            self._graph_gen = self.ctx.workspace_generation()
             torch.cuda.synchronize()
         for i in range(n):
             self.graph.replay()

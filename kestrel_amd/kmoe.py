@@ -29,6 +29,13 @@ class GpuMeasurements(C.Structure):
                 ("launch_s", C.c_double)]
 
 
+class MoeDbg(C.Structure):
+    """kmoe_moe_dbg (include/kmoe.h): device buffers of one captured moe_ffn."""
+
+    _fields_ = [(n, C.c_void_p) for n in ("xq", "xd", "xs", "hq", "hd", "hs", "gate_sumi", "gate_mins", "up_sumi",
+                                            "up_mins", "down_sumi", "down_mins")]
+
+
 # Every symbol include/kmoe.h declares, with (restype, argtypes).
 _P, _i32, _i64, _u32, _u64, _sz, _f = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float
 SIGNATURES = {
@@ -41,8 +48,8 @@ SIGNATURES = {
     "kmoe_get_stream": (_P, [_P]),
     "kmoe_synchronize": (C.c_int, [_P]),
     "kmoe_set_regime": (C.c_int, [_P, C.c_int]),
-    "kmoe_set_decode_path": (C.c_int, [_P, C.c_int]),
     "kmoe_get_regime": (C.c_int, [_P]),
+    "kmoe_workspace_generation": (C.c_int, [_P, C.POINTER(_u64)]),
     "kmoe_vram_set_limit": (C.c_int, [_P, _u64]),
     "kmoe_vram_usage": (C.c_int, [_P, C.POINTER(_u64), C.POINTER(_u64)]),
     "kmoe_device_alloc": (C.c_int, [_P, _sz, C.POINTER(_P)]),
@@ -73,6 +80,10 @@ SIGNATURES = {
     "kmoe_shared_gate_upload": (C.c_int, [_P, _u32, _P, _sz]),
     "kmoe_bytes_per_expert": (C.c_int, [_P, _u32, C.POINTER(_u64)]),
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
+    "kmoe_moe_ffn_dbg": (C.c_int, [_P, _u32, _P, _i64, _P, _P]),
+    "kmoe_moe_ffn_host": (C.c_int, [_P, _u32, _P, _i64, _P]),
+    "kmoe_matmul_host": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _i64, _P]),
+    "kmoe_expert_part_layout": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_i32)]),
     "kmoe_norm_matmul_rope_kv": (C.c_int, [_P, _P, _P, _P, _f, C.c_int, _P, _sz, _i64, _P, _P, _i32, _i32, _i32,
                                            _i32, _i64, _P, _P, _i32, _i64, _P, _P, _P]),
     "kmoe_norm_moe_ffn": (C.c_int, [_P, _u32, _P, _P, _P, _f, _i64, _P, _P]),
@@ -189,9 +200,11 @@ class Context:
     def sync(self):
         self.check(self.lib.kmoe_synchronize(self.h))
 
-    def set_decode_path(self, path: int):
-        """0: one kernel per stage (default); 1: one persistent kernel for a single-token layer where supported."""
-        self.check(self.lib.kmoe_set_decode_path(self.h, path))
+    def workspace_generation(self) -> int:
+        """kmoe_workspace_generation: changes when a workspace is reallocated."""
+        v = _u64()
+        self.check(self.lib.kmoe_workspace_generation(self.h, C.byref(v)))
+        return v.value
 
     def set_regime(self, regime: int):
         self.check(self.lib.kmoe_set_regime(self.h, regime))
@@ -480,6 +493,53 @@ class Context:
             out = self._empty((S, d), self.torch.float32)
         self.check(self.lib.kmoe_moe_ffn(self.h, layer, _ptr(h), S, _ptr(out)))
         return out
+
+    def moe_ffn_dbg(self, layer: int, h, n_expert_used: int, n_ff: int, gate_type: int, down_type: int):
+        """kmoe_moe_ffn_dbg: (out, dict of the captured device tensors): the
+        int8 rows of h and of the SwiGLU output per slot (dispatch order), and
+        the per-block integers [slots, rows, blocks] of gate, up and down."""
+        t = self.torch
+        S, d = h.shape
+        slots, F = S * n_expert_used, n_ff
+        bg, bd = (32 if gate_type == Q8_0 else 256), (32 if down_type == Q8_0 else 256)
+        cap = dict(xq=self._empty((S, d), t.int8), xd=self._empty((S, d // bg), t.float32),
+                   xs=self._empty((S, d // 16), t.int32), hq=self._empty((slots, F), t.int8),
+                   hd=self._empty((slots, F // bd), t.float32), hs=self._empty((slots, F // 16), t.int32))
+        for n in ("gate", "up"):
+            for m in ("sumi", "mins"):
+                cap[f"{n}_{m}"] = self._empty((slots, F, d // bg), t.int32)
+        for m in ("sumi", "mins"):
+            cap[f"down_{m}"] = self._empty((slots, d, F // bd), t.int32)
+        out = self._empty((S, d), t.float32)
+        dbg = MoeDbg(*[_ptr(cap[n]) for n, _ in MoeDbg._fields_])
+        self.check(self.lib.kmoe_moe_ffn_dbg(self.h, layer, _ptr(h), S, _ptr(out), C.byref(dbg)))
+        return out, cap
+
+    def moe_ffn_host(self, layer: int, h: np.ndarray) -> np.ndarray:
+        """kmoe_moe_ffn_host: host h [S, d] f32 in, host out back (synchronous)."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        out = np.empty_like(h)
+        self.check(self.lib.kmoe_moe_ffn_host(self.h, layer, h.ctypes.data, h.shape[0], out.ctypes.data))
+        return out
+
+    def matmul_host(self, t: int, w, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+        """kmoe_matmul_host: x [S, cols] host f32; w host bytes (numpy) or a
+        device tensor; returns out [S, rows] on the host (synchronous)."""
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+        out = np.empty((x.shape[0], rows), np.float32)
+        if isinstance(w, np.ndarray):
+            w = np.ascontiguousarray(w).view(np.uint8)
+            wp, wn = w.ctypes.data, w.nbytes
+        else:
+            wp, wn = _ptr(w), w.numel() * w.element_size()
+        self.check(self.lib.kmoe_matmul_host(self.h, t, wp, wn, rows, cols, x.ctypes.data, x.shape[0],
+                                             out.ctypes.data))
+        return out
+
+    def expert_part_layout(self, layer: int, e: int, part: int) -> int:
+        v = _i32()
+        self.check(self.lib.kmoe_expert_part_layout(self.h, layer, e, part, C.byref(v)))
+        return v.value
 
     def norm_moe_ffn(self, layer: int, x, norm_w, eps: float, y=None, f=None, out=None):
         """x += y (when given), f = rmsnorm(x) * norm_w, out = moe_ffn(f); returns out."""

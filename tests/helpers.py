@@ -203,3 +203,32 @@ def decoder_model(arch: str = "llama", n_layer: int = 2, d: int = 256, nh: int =
             T[p + "ffn_up.weight"] = mat(wtype, ff, d, 0.03)
             T[p + "ffn_down.weight"] = mat(wtype, d, ff, 0.03)
     return hp, T
+
+
+def midpoint_rows(rows: int, cols: int, block: int, seed: int):
+    """Activation rows whose int8 quantization (Q8Row per 32, Q8KRow per 256;
+    qdot.rs:30-49, :347-367) lands on exact rounding midpoints.
+
+    Each block's largest magnitude is 127 * 2^e, so scale = amax / 127 = 2^e
+    and inv = 2^-e are exact, and every other element is +-(m + 0.5) * 2^e
+    (m in 0..126, even and odd) or an integer multiple of 2^e, so x * inv is
+    exact too. Returns (x f32 [rows, cols], t = x / 2^e as float64): the
+    expected int8 value is sign(t) * floor(|t| + 0.5) (f32::round, half away
+    from zero), which differs from round-half-even wherever m is even."""
+    rng = np.random.default_rng(seed)
+    nb = cols // block
+    e = rng.integers(-7, 3, size=(rows, nb))
+    m = rng.integers(0, 127, size=(rows, nb, block)).astype(np.float64)
+    half = rng.random((rows, nb, block)) < 0.85
+    t = np.where(half, m + 0.5, m) * np.where(rng.random((rows, nb, block)) < 0.5, -1.0, 1.0)
+    pos = rng.integers(0, block, size=(rows, nb))
+    r_i, b_i = np.meshgrid(np.arange(rows), np.arange(nb), indexing="ij")
+    t[r_i, b_i, pos] = np.where(rng.random((rows, nb)) < 0.5, -127.0, 127.0)
+    x = (t * np.ldexp(1.0, e)[:, :, None]).astype(np.float32)
+    assert np.array_equal(x.astype(np.float64), t * np.ldexp(1.0, e)[:, :, None])  # exact in f32
+    return x.reshape(rows, cols), t.reshape(rows, cols)
+
+
+def round_half_away(t: np.ndarray) -> np.ndarray:
+    """Rust f32::round then clamp(-127, 127) as i8, on exact float64 values."""
+    return np.clip(np.sign(t) * np.floor(np.abs(t) + 0.5), -127, 127).astype(np.int8)

@@ -53,6 +53,28 @@ def test_quantize_q8k_bit_exact(ctx, orc, rows, cols):
     assert np.array_equal(host(bs), rbs)
 
 
+@pytest.mark.parametrize("block,rows,cols", [(256, 1, 256), (256, 2, 4096), (256, 3, 14336), (32, 2, 1024),
+                                              (32, 3, 96)])
+def test_quantizers_round_half_away_at_exact_midpoints(ctx, orc, block, rows, cols):
+    """qdot.rs:42 / :361 round half away from zero: blocks with amax =
+    127 * 2^e put most elements on an exact midpoint (helpers.midpoint_rows),
+    where a half-to-even rounding would give another value."""
+    from tests.helpers import midpoint_rows, round_half_away
+
+    x, t = midpoint_rows(rows, cols, block, seed=cols + rows)
+    exp = round_half_away(t)
+    assert (np.rint(t).astype(np.int8) != exp).any()
+    if block == 256:
+        q, d, s = ctx.quantize_q8k(dev(x))
+        rq, rd, rs = orc.q8k_quantize(x)
+    else:
+        q, d, s = ctx.quantize_q8(dev(x))
+        rq, rd, rs = orc.q8_quantize(x)
+    assert np.array_equal(host(q), exp) and np.array_equal(rq, exp)
+    assert np.array_equal(host(d).view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(host(s), rs)
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 32), (3, 1024), (2, 512), (4, 96)])
 def test_quantize_q8_bit_exact(ctx, orc, rows, cols):
     x = orc.normal(rows * 17 + cols, rows * cols).reshape(rows, cols)
@@ -198,6 +220,26 @@ def test_route_matches_oracle(ctx, orc, E, k, d, S, norm, scale):
     # p = expf(v - m): the device uses a correctly rounded expf, glibc's is
     # within 0.502 ulp, so weights agree to a few ulp.
     assert np.allclose(host(w), rw, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("E,k,S", [(8, 2, 1), (8, 2, 3), (8, 2, 5), (128, 8, 1), (128, 8, 6), (64, 6, 2)])
+def test_route_nan_logit_selects_in_index_order(ctx, orc, E, k, S):
+    """A NaN in router row E/2 makes that logit NaN for every token; the
+    reference's softmax then makes every p NaN and its comparator falls back
+    to index order (transformer.rs:479-484): experts 0..k-1, NaN weights. S < 4
+    runs the fused decode router, S >= 4 the logits + top-k kernels."""
+    d = 1024
+    wr = orc.normal(E + 3, E * d, 0.0, 0.02).reshape(E, d)
+    wr[E // 2, 5] = np.nan
+    h = orc.normal(S + 11, S * d).reshape(S, d)
+    idx, w, logits = ctx.route(dev(wr), dev(h), k, True, 0.0)
+    from oracle.pyoracle import Layer
+
+    z = [np.zeros(1, np.uint8)] * E
+    ridx, rw = Layer(E, k, d, 256, Q4_K, Q4_K, Q4_K, wr, z, z, z, True, 0.0).route(h)
+    assert ridx.tolist() == [list(range(k))] * S
+    assert np.array_equal(host(idx).astype(np.uint32), ridx)
+    assert np.isnan(host(w)).all() and np.isnan(rw).all()
 
 
 @pytest.mark.parametrize("S,k,E", [(1, 2, 8), (16, 2, 8), (7, 6, 64), (512, 2, 8), (700, 8, 128), (2048, 8, 128),

@@ -219,11 +219,27 @@ def test_q8_0_block_accumulators_match_bruteforce(orc):
     assert np.array_equal(p.astype(np.int64), ref)
 
 
+@pytest.mark.parametrize("block", [256, 32])
+def test_q8_quantizers_round_half_away_at_exact_midpoints(orc, block):
+    """qdot.rs:42 / :361: `(xs[j] * inv).round() as i32` rounds half away from
+    zero. Blocks with amax = 127 * 2^e make scale and x * inv exact, so most
+    elements sit on a midpoint: a half-to-even rounding (rint) fails here."""
+    from tests.helpers import midpoint_rows, round_half_away
+
+    x, t = midpoint_rows(4, 2048, block, seed=block)
+    exp = round_half_away(t)
+    assert (np.rint(t).astype(np.int8) != exp).sum() > 500  # the inputs tell the two rules apart
+    q, d, s = (orc.q8k_quantize if block == 256 else orc.q8_quantize)(x)
+    assert np.array_equal(q, exp)
+    scale = np.abs(x.reshape(4, -1, block)).max(2) / np.float32(127.0)
+    assert np.array_equal(d, scale.astype(np.float32)) and np.all(np.log2(d) == np.round(np.log2(d)))
+    assert np.array_equal(s, exp.reshape(4, -1, 16).astype(np.int32).sum(2))
+
+
 def test_q8k_quantize_semantics(orc):
-    # qdot.rs:347-367: scale = amax/127, q = round-half-away(x / scale) clamped; bsums per 16.
+    # qdot.rs:347-367: scale = amax/127, q = round(x / scale) clamped; bsums per 16.
     x = orc.normal(9, 1024)
     x[:256] = 0.0  # zero block -> scale 0, q 0
-    x[300] = 127.5 * 0.01  # exact half cases exercise round-half-away
     q, d, bs = orc.q8k_quantize(x)
     assert d[0, 0] == 0.0 and not q[0, :256].any()
     ax = np.abs(x.reshape(-1, 256)).max(1)
@@ -298,6 +314,26 @@ def test_route_ties_prefer_lower_index(orc):
     idx, w = orc.route_from_logits(logits, 3, True, 0.0)
     assert idx[0].tolist() == [0, 1, 2] and idx[1].tolist() == [2, 5, 6]
     assert np.allclose(w, 1.0 / 3.0)
+
+
+def test_route_nan_and_inf_logits_fall_back_to_index_order(orc):
+    """transformer.rs:479-484. A NaN logit leaves m = the max of the others
+    (f32::max skips NaN), so its p and then `sum` are NaN and every p /= sum
+    is NaN; a +inf logit gives exp(inf - inf) = NaN the same way. The sort's
+    comparator maps NaN to Equal and falls back to ascending index, so such a
+    row selects experts 0..k-1 with NaN weights (the 2^-14 floor's f32::max
+    also skips NaN). A -inf logit is just p = 0."""
+    E, k = 16, 4
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((4, E)).astype(np.float32)
+    logits[0, 7] = np.nan
+    logits[1, 3] = np.inf
+    logits[2, :] = np.nan
+    logits[3, 0] = -np.inf
+    idx, w = orc.route_from_logits(logits, k, True, 0.0)
+    assert idx[:3].tolist() == [[0, 1, 2, 3]] * 3 and np.isnan(w[:3]).all()
+    ref = np.argsort(-logits[3].astype(np.float64), kind="stable")[:k]
+    assert idx[3].tolist() == ref.tolist() and 0 not in ref and np.isfinite(w[3]).all()
 
 
 def test_dispatch_is_stable_sort(orc):
