@@ -192,6 +192,27 @@ def test_matmul_regimes_match_oracle(ctx, orc, t, S, regime):
     assert rel_l2(out, ref) < TOL, (S, regime, rel_l2(out, ref))
 
 
+@pytest.mark.parametrize("t,rows,cols,S,regime", [(Q4_K, 512, 4096, 1, 0), (Q4_K, 300, 2048, 5, 0),
+                                                 (Q6_K, 64, 1024, 3, 0), (Q8_0, 100, 1024, 9, 1),
+                                                 (Q4_K, 64, 1024, 12, 1), (F32, 8, 1024, 2, 0)])
+def test_matmul_host_is_matmul(ctx, orc, t, rows, cols, S, regime):
+    """kmoe_matmul_host, quant::matmul's own signature (quant.rs:229: host w,
+    x and out): with host weights (copied for the call) and with resident
+    device weights, the same bits as kmoe_matmul on device buffers."""
+    w = (orc.normal(rows, rows * cols, 0.0, 0.02).view(np.uint8) if t == F32
+         else random_blocks(t, rows, cols, seed=rows + cols))
+    x = orc.normal(S + cols, S * cols).reshape(S, cols)
+    ctx.set_regime(regime)
+    try:
+        ref = host(ctx.matmul(t, dev(w), rows, cols, dev(x)))
+        a = ctx.matmul_host(t, w, rows, cols, x)
+        b = ctx.matmul_host(t, dev(w), rows, cols, x)
+    finally:
+        ctx.set_regime(0)
+    assert np.array_equal(a.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(b.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("E,d,S", [(8, 4096, 1), (8, 4096, 3), (8, 4096, 4), (8, 1024, 16), (128, 2048, 1),
                                    (128, 2048, 7), (64, 2048, 9), (50, 1024, 6), (8, 1000, 5), (8, 1000, 2),
                                    (8, 1004, 5), (8, 1004, 1)])

@@ -135,22 +135,100 @@ def test_qwen3_like_zipf_routing(ctx, orc):
         assert r < TOL
 
 
+_SPECS = {}
+
+
+def mixtral_spec():
+    """Config 3's layer (hidden 4096, FFN 14336, 8 experts, top-2, Q4_K random
+    blocks, 793 MB), built once per module."""
+    if "mixtral" not in _SPECS:
+        _SPECS["mixtral"] = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=3, quantized=False)
+    return _SPECS["mixtral"]
+
+
 def test_mixtral_shape_decode_b1(ctx, orc):
     """Config 3 at decode batch 1: hidden 4096, FFN 14336, 8 experts, top-2,
     Q4_K random blocks (793 MB of experts), router N(0, 0.02)."""
-    spec = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=3, quantized=False)
-    check(run_layer(ctx, orc, spec, 1, 0, seed=11))
+    check(run_layer(ctx, orc, mixtral_spec(), 1, 0, seed=11))
 
 
 def test_mixtral_shape_prefill_512_int8(ctx, orc):
     """Config 3 at 512 tokens on the int path for every row (the int8
     matrix-core kernels): about 128 rows per expert, so some experts take a
     second 128-row pass."""
-    spec = LayerSpec(8, 2, 4096, 14336, Q4_K, seed=3, quantized=False)
-    r = run_layer(ctx, orc, spec, 512, 1, seed=12)
+    r = run_layer(ctx, orc, mixtral_spec(), 512, 1, seed=12)
     counts = np.diff(r["off"].astype(np.int64))
     assert counts.max() > 128, counts
     check(r)
+
+
+@pytest.mark.parametrize("S,regime", [(8, 0), (8, 1), (32, 0), (32, 1), (512, 0)])
+def test_mixtral_shape_at_bench_token_counts(ctx, orc, S, regime):
+    """Config 3 at the token counts the bench reports: decode batches of 8
+    and 32 in the AVX2 regime (f32 GEMM for experts with >= 4 rows,
+    quant.rs:242-260; the int8 path below) and the int8 regime (few-rows and
+    matrix-core kernels), and the 512-token prefill in the AVX2 regime (the
+    reference's own prefill arithmetic: every expert on the f32 GEMM)."""
+    r = run_layer(ctx, orc, mixtral_spec(), S, regime, seed=4000 + S)
+    check(r)
+
+
+@pytest.mark.parametrize("S,regime", [(512, 0), (512, 1), (2048, 0), (2048, 1)])
+def test_qwen3_shape_zipf_at_bench_token_counts(ctx, orc, S, regime):
+    """Config 4 (hidden 2048, FFN 768, 128 experts, top-8, Q4_K, Zipf(1.1)
+    routing) at the bench's prefill token counts, both regimes."""
+    if "qwen3" not in _SPECS:
+        _SPECS["qwen3"] = LayerSpec(128, 8, 2048, 768, Q4_K, seed=4, quantized=False, zipf=1.1)
+    h = orc.normal(41 + S, S * 2048, 1.0, 1.0).reshape(S, 2048)
+    r = run_layer(ctx, orc, _SPECS["qwen3"], S, regime, seed=0, h=h)
+    counts = np.diff(r["off"].astype(np.int64))
+    assert counts.max() > 4 * max(1, counts.min()), counts  # the Zipf bias skews the expert loads
+    check(r)
+
+
+C5_SHARED_FF = 2816  # 2 shared experts of FFN 1408, stored as one *_shexp FFN
+
+
+def c5_spec():
+    """DeepSeek-V2-Lite-shaped MoE layer (config 5's layer): hidden 2048, 64
+    routed experts of FFN 1408, top-6, softmax weights not renormalised
+    (norm_topk_prob false, routed scaling 1), Q4_K gate/up and Q8_0 routed
+    down (1408 columns need a 32-element block type); the 2 shared experts as
+    kestrel holds them, one ffn_*_shexp FFN of width 2816 with no gate
+    (scale 1, transformer.rs:572-587), Q4_K gate/up and Q6_K down."""
+    if "c5" not in _SPECS:
+        spec = LayerSpec(64, 6, 2048, 1408, Q4_K, seed=55, quantized=False, down_type=Q8_0, norm_topk=False,
+                         weights_scale=1.0)
+        sh = [random_blocks(Q4_K, C5_SHARED_FF, 2048, 901), random_blocks(Q4_K, C5_SHARED_FF, 2048, 902),
+              random_blocks(Q6_K, 2048, C5_SHARED_FF, 903)]
+        _SPECS["c5"] = (spec, sh)
+    return _SPECS["c5"]
+
+
+@pytest.mark.parametrize("S", [1, 8, 128])
+@pytest.mark.parametrize("regime", [0, 1, 2])
+def test_c5_deepseek_v2_lite_layer(ctx, orc, S, regime):
+    spec, sh = c5_spec()
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    try:
+        ctx.shared_expert(lid, C5_SHARED_FF, (Q4_K, Q4_K, Q6_K), sh[0], sh[1], sh[2], None)
+        h = orc.normal(70 + S, S * 2048).reshape(S, 2048)
+        ctx.set_regime(regime)
+        out = host(ctx.moe_ffn(lid, dev(h)))
+        idx, w, perm, off = (host(t) for t in ctx.last_routing(S, spec.k, spec.n_expert))
+    finally:
+        ctx.set_regime(0)
+        ctx.layer_destroy(lid)
+    L = spec.oracle_layer()
+    ridx, rw = L.route(h, regime)
+    rperm, roff = orc.dispatch(ridx, spec.n_expert)
+    ref = orc.shared_expert_add(L.moe_ffn(h, regime), h, 2048, C5_SHARED_FF, (Q4_K, Q4_K, Q6_K), sh[0], sh[1], sh[2],
+                                None, regime)
+    check(dict(out=out, ref=ref, idx=idx.view(np.uint32), ridx=ridx, w=w, rw=rw, perm=perm.view(np.uint32),
+               rperm=rperm, off=off.view(np.uint32), roff=roff))
+    assert not np.allclose(rw.sum(1), 1.0)  # no renormalisation: the six weights sum below 1
 
 
 @pytest.mark.parametrize("S,E,k", [(300, 4, 2), (129, 2, 2), (9, 16, 4)])
@@ -208,6 +286,71 @@ def test_expert_tier_serves_correct_slices(ctx):
         assert ctx.bytes_per_expert(l) == 3 * 256 * 8 * 34
     ctx.layer_destroy(0)
     ctx.layer_destroy(1)
+
+
+@pytest.mark.parametrize("S,regime", [(1, 0), (3, 0), (6, 0), (6, 1)])
+def test_moe_ffn_host_is_moe_ffn(ctx, orc, S, regime):
+    """kmoe_moe_ffn_host, moe_ffn's own signature (transformer.rs:513: h:
+    &[f32] in, Vec<f32> out): the same bits as kmoe_moe_ffn on device buffers."""
+    spec = LayerSpec(8, 2, 4096, 1024, Q4_K, seed=31, quantized=False, down_type=Q6_K)
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    try:
+        ctx.set_regime(regime)
+        h = orc.normal(40 + S, S * 4096).reshape(S, 4096)
+        a = ctx.moe_ffn_host(lid, h)
+        b = host(ctx.moe_ffn(lid, dev(h)))
+    finally:
+        ctx.set_regime(0)
+        ctx.layer_destroy(lid)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert rel_l2(a, spec.oracle_layer().moe_ffn(h, regime)) < TOL
+
+
+def test_tiled_parts_report_their_layout_and_raw_kernels_refuse_them(ctx):
+    """kmoe_expert_part hands out tier bytes in the tier's layout: Q4_K and
+    Q6_K parts are tiled rows, Q8_0 parts GGUF bytes. The raw-pointer entry
+    points read GGUF rows, so they refuse a pointer to a tiled part instead
+    of returning wrong numbers; a GGUF (Q8_0) part still works."""
+    import torch
+
+    from kestrel_amd.kmoe import KmoeError
+
+    spec = LayerSpec(2, 1, 1024, 512, Q4_K, seed=5, quantized=False, down_type=Q8_0)
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    try:
+        assert [ctx.expert_part_layout(lid, 1, k) for k in range(3)] == [1, 1, 0]
+        x = torch.ones((1, 1024), dtype=torch.float32, device="cuda")
+        p, n = ctx.expert_part(lid, 1, 0)
+        rc = ctx.lib.kmoe_matmul(ctx.h, Q4_K, p, n, 512, 1024, x.data_ptr(), 1, x.data_ptr())
+        assert rc == -1 and b"tiled" in ctx.lib.kmoe_last_error(ctx.h)
+        with pytest.raises(KmoeError):
+            ctx.matmul_host(Q4_K, _DevBuf(p, n), 512, 1024, np.ones((1, 1024), np.float32))
+        p2, n2 = ctx.expert_part(lid, 1, 2)  # Q8_0 down [1024, 512]: GGUF bytes, usable as is
+        y = ctx.matmul_host(Q8_0, _DevBuf(p2, n2), 1024, 512, np.ones((1, 512), np.float32))
+        ref = ctx.matmul_host(Q8_0, spec.down[1], 1024, 512, np.ones((1, 512), np.float32))
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    finally:
+        ctx.layer_destroy(lid)
+
+
+class _DevBuf:
+    """A raw device pointer with the two methods Context.matmul_host reads."""
+
+    def __init__(self, p, n):
+        self.p, self.n = p, n
+
+    def data_ptr(self):
+        return self.p
+
+    def numel(self):
+        return self.n
+
+    def element_size(self):
+        return 1
 
 
 def _tiled_reference(g: np.ndarray, rows: int, nb: int) -> np.ndarray:
