@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 D, FF, E, K = 4096, 14336, 8, 2
-Q4_K, Q6_K = 12, 14
+Q8_0, Q4_K, Q6_K = 8, 12, 14
 ROW_GU = 4096 // 256 * 144   # 2304 B per gate/up row
 ROW_DN = 14336 // 256 * 144  # 8064 B per down row
 PART = FF * ROW_GU           # 33,030,144 B (gate, up and down parts are equal)
@@ -54,10 +54,11 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=40)
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other measured rows (decode b=8/32, dense Q4_K/Q6_K matvec, Q4_K_M-mix "
-                         "decode, Qwen3-shaped layer, expert-tier preload)")
-    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,preload,decode_stack,measure",
+                         "decode, Qwen3- and DeepSeek-V2-Lite-shaped layers, expert-tier preload, decode stacks)")
+    ap.add_argument("--legs", default="batches,matvec_q4k,matvec_q6k,q4k_m,qwen3,c5_layer,preload,decode_stack,"
+                                      "c5_stack,measure",
                     help="comma list of the other measured rows to run (batches, matvec_q4k, matvec_q6k, "
-                         "q4k_m, qwen3, preload, decode_stack, measure)")
+                         "q4k_m, qwen3, c5_layer, preload, decode_stack, c5_stack, measure)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -114,9 +115,50 @@ def make_layers(ctx, torch, n_layers: int, seed: int = 0):
     torch.cuda.synchronize()
 
 
+def host_cpu() -> dict:
+    """This host's CPU model and the hardware threads and physical cores this
+    process may run on (its affinity mask; kestrel's default thread count is
+    the physical core count, README.md:487)."""
+    aff = set(os.sched_getaffinity(0))
+    model, cores, cur = None, set(), {}
+    try:
+        lines = open("/proc/cpuinfo").read().splitlines() + [""]
+    except OSError:
+        lines = []
+    for line in lines:
+        if not line.strip():
+            if cur and int(cur.get("processor", -1)) in aff:
+                cores.add((cur.get("physical id", "0"), cur.get("core id", cur.get("processor"))))
+                model = model or cur.get("model name")
+            cur = {}
+            continue
+        k, _, v = line.partition(":")
+        cur[k.strip()] = v.strip()
+    return {"cpu_model": model, "hw_threads": len(aff), "physical_cores": len(cores) or len(aff)}
+
+
+def cpu_threads(cap: int) -> int:
+    """kestrel's default: one thread per physical core (capped)."""
+    return max(1, min(cap, host_cpu()["physical_cores"]))
+
+
+def timed_calls(fn, seconds: float, max_calls: int):
+    """Calls fn(i) until `seconds` or `max_calls`; returns (calls, elapsed s)."""
+    fn(0)  # warm
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn(n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= max_calls:
+            return n, el
+
+
 def cpu_baseline(ctx, torch, seconds: float, threads: int):
     """Oracle moe_ffn (C++ restatement of kestrel's AVX2 path, transformer.rs:513)
-    on layer 0's exact bytes, one token per call, for about `seconds`."""
+    on layer 0's exact bytes, one token per call, for about `seconds` with one
+    thread per physical core, then about a third of that on one thread."""
     import numpy as np
 
     from oracle import pyoracle as orc
@@ -126,27 +168,24 @@ def cpu_baseline(ctx, torch, seconds: float, threads: int):
     router = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)  # same stream as make_layers' layer 0
     L = orc.Layer(E, K, D, FF, Q4_K, Q4_K, Q4_K, router, [p[0] for p in parts], [p[1] for p in parts],
                   [p[2] for p in parts], True, 0.0)
-    hw = orc.hw_threads()
-    nthreads = max(1, min(threads, hw))
+    info = host_cpu()
+    nthreads = cpu_threads(threads)
     h = rng.standard_normal((64, D)).astype(np.float32)
-    L.moe_ffn(h[:1], threads=nthreads)  # warm
-    t0 = time.perf_counter()
-    n = 0
-    while True:
-        L.moe_ffn(h[n % 64:n % 64 + 1], threads=nthreads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 5000:
-            break
+    n, el = timed_calls(lambda i: L.moe_ffn(h[i % 64:i % 64 + 1], threads=nthreads), seconds, 5000)
+    n1, el1 = timed_calls(lambda i: L.moe_ffn(h[i % 64:i % 64 + 1], threads=1), seconds / 3, 1000)
     gemv = orc.bench_gemv(Q4_K, 2048, 4096, 50, nthreads)  # quant.rs:348-368 metric
+    gemv1 = orc.bench_gemv(Q4_K, 2048, 4096, 20, 1)
     return {
         "value": round(n / el, 3),
         "unit": "tokens/s",
         "cores": nthreads,
         "kind": "port",
-        "sample": f"{n} single-token moe_ffn calls on layer 0 (Mixtral shape, Q4_K, AVX2 regime), {el:.1f} s; "
-                  f"host has {hw} hardware threads",
+        "sample": f"{n} single-token moe_ffn calls on layer 0 (Mixtral shape, Q4_K, AVX2 regime), {el:.1f} s, "
+                  f"{nthreads} threads (one per physical core)",
+        **info,
+        "one_thread": {"value": round(n1 / el1, 3), "unit": "tokens/s", "sample": f"{n1} calls, {el1:.1f} s"},
         "gemv_q4k_2048x4096_GBps": round(gemv / 1e9, 3),
+        "gemv_q4k_2048x4096_GBps_one_thread": round(gemv1 / 1e9, 3),
     }
 
 
@@ -240,6 +279,19 @@ def prefill_leg(ctx, torch, a):
                           "frac": round(tops / INT8_PEAK_TOPS, 4)}
     mf_us = sum(kern[n]["avg_us"] for n in ("moe_gate_up_mfma", "moe_down_mfma") if n in kern)
     touched = E * EXPERT_BYTES + E * D * 4
+    # The reference's own prefill arithmetic (AVX2 regime: experts with >= 4
+    # rows dequantize to f32 and run the f32 GEMM, quant.rs:242-260), on the
+    # same inputs: its GPU time, and how far the int8 path's outputs are from it.
+    o_int = op.clone()
+    ctx.set_regime(0)
+    t_avx = graph_time(torch, ctx, [lambda l=l: step(l) for l in range(a.layers)], max(1, n_rep // 2)) / a.layers
+    for l in range(a.layers):
+        step(l)
+    torch.cuda.synchronize()
+    o_f32 = op.clone()
+    ctx.set_regime(1)
+    rel = max(float(((o_int[l] - o_f32[l]).double().norm() / o_f32[l].double().norm()).item())
+              for l in range(a.layers))
     res = {
         "tokens": S,
         "steps": steps,
@@ -255,6 +307,10 @@ def prefill_leg(ctx, torch, a):
         "hbm_touched_GBps": round(touched / (ms_step * 1e-3) / 1e9, 1),
         "hbm_frac": round(touched / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "kernels_us": kern,
+        "avx2_regime": {"tokens_per_s": round(S / t_avx, 1), "ms_per_step": round(t_avx * 1e3, 5),
+                        "launch": "hip-graph", "arithmetic": "f32 GEMM on dequantized weights for experts with "
+                                                             ">= 4 rows (every expert at this batch)"},
+        "int8_vs_f32_rel_l2": round(rel, 6),
         "cpu_baseline": None,
     }
     ctx.set_regime(a.regime)
@@ -309,10 +365,13 @@ def batch_leg(ctx, torch, layers: int, S: int, regime: int):
             "hbm_touched_GBps": round(tb / t / 1e9, 1), "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def matvec_leg(ctx, torch, wtype: int = Q4_K, pool_bytes: float = 2.2e9):
+def matvec_leg(ctx, torch, wtype: int = Q4_K, pool_bytes: float = 2.2e9, cpu_seconds: float = 0.0,
+               cpu_cap: int = 16):
     """Dense Q4_K or Q6_K matvec at decode batch 1 (quant::matmul, one
     activation row) over a pool of distinct weight copies larger than the
-    Infinity Cache."""
+    Infinity Cache: the whole call (Q8_K of x, then the matvec) replayed as a
+    graph, the matvec kernel's own time, and (cpu_seconds > 0) the oracle's
+    GEMV at the same shape on this host."""
     import numpy as np
 
     from kestrel_amd import kmoe
@@ -342,8 +401,37 @@ def matvec_leg(ctx, torch, wtype: int = Q4_K, pool_bytes: float = 2.2e9):
 
         t = graph_time(torch, ctx, [lambda i=i: call(i) for i in range(copies)], 5) / copies
         b = nbytes + cols * 4 + rows * 4
-        out[f"{rows}x{cols}"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1),
-                                 "frac": round(b / t / 1e9 / HBM_PEAK_GBPS, 4), "pool_copies": copies}
+        # the matvec kernel alone (its own dispatch timestamps), beside the
+        # activation quantization that precedes it in the call
+        ctx.profile_enable(True)
+        for i in range(copies):
+            call(i)
+        torch.cuda.synchronize()
+        kname = "matvec_q4k" if wtype == Q4_K else "matvec_q6k"
+        ms_k, n_k = ctx.profile_read(kname)
+        ms_q, n_q = ctx.profile_read("quant_q8k")
+        ctx.profile_enable(False)
+        k_us = ms_k * 1e3 / max(1, n_k)
+        # algorithmic bytes of the kernel: the weights, the Q8_K row (cols + cols/16*4 + cols/256*4) and out
+        kb = nbytes + cols + cols // 16 * 4 + cols // 256 * 4 + rows * 4
+        row = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1), "frac": round(b / t / 1e9 / HBM_PEAK_GBPS, 4),
+               "pool_copies": copies,
+               "kernel": {"name": kname, "avg_us": round(k_us, 3), "alg_bytes": kb,
+                          "GBps": round(kb / (k_us * 1e-6) / 1e9, 1),
+                          "frac": round(kb / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                          "quant_q8k_us": round(ms_q * 1e3 / max(1, n_q), 3)}}
+        if cpu_seconds > 0:  # the reference's GEMV metric at this shape (quant.rs:348-368)
+            from oracle import pyoracle as orc
+
+            nt = cpu_threads(cpu_cap)
+            it = max(2, int(cpu_seconds * 20e9 / nbytes / 4))
+            g = orc.bench_gemv(wtype, rows, cols, it, nt)
+            g1 = orc.bench_gemv(wtype, rows, cols, max(2, it // 8), 1)
+            row["cpu_baseline"] = {"value": round(g / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+                                   "one_thread_GBps": round(g1 / 1e9, 3),
+                                   "sample": f"quant::matmul at one row, {it} calls on one {rows}x{cols} matrix "
+                                             f"(xorshift bytes & 0x3f, activations (i % 7) * 0.01)"}
+        out[f"{rows}x{cols}"] = row
         del pool
     torch.cuda.empty_cache()
     return out
@@ -451,10 +539,14 @@ def synthetic_blocks(t: int, n_blocks: int, scale: float, rng):
     """Random well-formed blocks with dequantized std ~scale, built the way
     kestrel's synthetic models are (tools/make_synthetic.py:38-58): Q4_K with
     every 6-bit scale and min at 32 and dmin = 7.5 d (zero-mean weights), Q6_K
-    with int8 scales 16..47."""
+    with int8 scales 16..47, Q8_0 uniform int8 under one scale."""
     import numpy as np
 
     f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
+    if t == Q8_0:  # uniform int8 weights (std ~74) under one f16 scale
+        raw = rng.integers(0, 256, size=(n_blocks, 34), dtype=np.uint8)
+        raw[:, 0:2] = f16(scale / 74.0)
+        return raw.reshape(-1)
     if t == Q4_K:
         raw = rng.integers(0, 256, size=(n_blocks, 144), dtype=np.uint8)
         d = scale / (32 * 4.61)
@@ -468,46 +560,78 @@ def synthetic_blocks(t: int, n_blocks: int, scale: float, rng):
     return raw.reshape(-1)
 
 
-MOE6B = dict(layers=24, embd=2048, ff=1536, heads=16, kv_heads=4, vocab=32000, experts=32, experts_used=4)
+MOE6B = dict(name="synthetic moe-6b (llama arch)", arch="llama", layers=24, embd=2048, ff=1536, heads=16,
+             kv_heads=4, vocab=32000, experts=32, experts_used=4, norm_topk=False, weights_scale=0.0,
+             down_type=Q4_K, shared_ff=0, dense_layers=0, dense_ff=0)
+# DeepSeek-V2-Lite's shape as kestrel can hold it: qwen2moe (the reference's
+# native MoE architecture with shared experts; deepseek2 itself is
+# LlamaCppOnly, kestrel-model/src/adapters.rs:32) with plain multi-head
+# attention in place of MLA, 27 layers of which the first is dense (FFN
+# 10944, first_k_dense_replace = 1), 64 routed experts of FFN 1408, top-6
+# with unrenormalised softmax weights, 2 shared experts as one ungated FFN of
+# 2816; Q4_K_M-style types: Q4_K, Q8_0 where a row is not a multiple of 256
+# (routed down, dense down), Q6_K shared down and head.
+DSV2LITE = dict(name="DeepSeek-V2-Lite-shaped (qwen2moe arch, MHA)", arch="qwen2moe", layers=27, embd=2048,
+                ff=1408, heads=16, kv_heads=16, vocab=102400, experts=64, experts_used=6, norm_topk=False,
+                weights_scale=1.0, down_type=Q8_0, shared_ff=2816, dense_layers=1, dense_ff=10944)
+STACKS = {"moe6b": MOE6B, "dsv2lite": DSV2LITE}
 
 
-def decode_stack_leg(ctx, torch, prompt: int = 128, steps: int = 256):
-    """A whole decode stack on the GPU: kestrel's synthetic `moe-6b` shape
-    (tools/make_synthetic.py:27: llama architecture, 24 layers, hidden 2048,
-    16 heads / 4 KV heads, 32 experts of FFN 1536, top-4, vocab 32000; Q4_K
-    weights, Q6_K head, F32 norms and router), every weight resident in HBM.
-    A 128-token prompt of uniform random ids, then greedy decode steps, each
-    one token through all layers, the head and argmax, replayed as one HIP
-    graph. Expert and attention bytes are shared between layers on the host
-    (each layer still gets its own copy in HBM); routers differ per layer."""
+def _tbytes(t: int, rows: int, cols: int) -> int:
+    el, sz = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}[t]
+    return rows * (cols // el) * sz
+
+
+def decode_stack_leg(ctx, torch, c: dict, prompt: int = 128, steps: int = 256):
+    """A whole decode stack on the GPU through Decoder (Transformer::forward),
+    every weight resident in HBM: a 128-token prompt of uniform random ids,
+    then greedy decode steps, each one token through all layers, the head and
+    argmax, replayed as one HIP graph. c: MOE6B (kestrel's synthetic `moe-6b`,
+    tools/make_synthetic.py:27) or DSV2LITE. Random well-formed blocks; expert,
+    attention and dense-FFN bytes are shared between layers on the host (each
+    layer still gets its own copy in HBM); routers differ per layer."""
     import numpy as np
 
     from kestrel_amd.decoder import Decoder
 
-    c = MOE6B
     L, d, ff, H, KV, V, NE, NU = (c[k] for k in ("layers", "embd", "ff", "heads", "kv_heads", "vocab", "experts",
                                                   "experts_used"))
+    dt, FS, ND, FD = c["down_type"], c["shared_ff"], c["dense_layers"], c["dense_ff"]
     hd = d // H
     rng = np.random.default_rng(11)
-    q4 = lambda rows, cols, sc: (Q4_K, [cols, rows], synthetic_blocks(Q4_K, rows * cols // 256, sc, rng))
+    blk = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+    mat = lambda t, rows, cols, sc: (t, [cols, rows], synthetic_blocks(t, rows * cols // blk[t], sc, rng))
     f32 = lambda v, dims: (0, list(dims), np.ascontiguousarray(v, np.float32).view(np.uint8).reshape(-1))
-    hp = dict(arch="llama", n_layer=L, n_embd=d, n_head=H, n_head_kv=KV, head_dim=hd, rope_dim=hd,
+    hp = dict(arch=c["arch"], n_layer=L, n_embd=d, n_head=H, n_head_kv=KV, head_dim=hd, rope_dim=hd,
               rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=prompt + steps + 8, n_batch=512, n_expert=NE,
-              n_expert_used=NU, norm_topk=False, weights_scale=0.0)
-    T = {"token_embd.weight": q4(V, d, 1.0), "output_norm.weight": f32(np.ones(d), [d]),
-         "output.weight": (Q6_K, [d, V], synthetic_blocks(Q6_K, V * d // 256, 1.0 / np.sqrt(d), rng))}
-    shared = {"attn_q.weight": q4(H * hd, d, 1 / np.sqrt(d)), "attn_k.weight": q4(KV * hd, d, 1 / np.sqrt(d)),
-              "attn_v.weight": q4(KV * hd, d, 1 / np.sqrt(d)), "attn_output.weight": q4(d, H * hd, 1 / np.sqrt(d))}
-    gate = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(d), rng))
-    up = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(d), rng))
-    down = (Q4_K, [ff, d, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, 1 / np.sqrt(ff), rng))
+              n_expert_used=NU, norm_topk=c["norm_topk"], weights_scale=c["weights_scale"])
+    T = {"token_embd.weight": mat(Q4_K, V, d, 1.0), "output_norm.weight": f32(np.ones(d), [d]),
+         "output.weight": mat(Q6_K, V, d, 1.0 / np.sqrt(d))}
+    s_d = 1 / np.sqrt(d)
+    attn = {"attn_q.weight": mat(Q4_K, H * hd, d, s_d), "attn_k.weight": mat(Q4_K, KV * hd, d, s_d),
+            "attn_v.weight": mat(Q4_K, KV * hd, d, s_d), "attn_output.weight": mat(Q4_K, d, H * hd, s_d)}
+    gate = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng))
+    up = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng))
+    down = (dt, [ff, d, NE], synthetic_blocks(dt, NE * ff * d // blk[dt], 1 / np.sqrt(ff), rng))
+    shexp = {}
+    if FS:
+        shexp = {"ffn_gate_shexp.weight": mat(Q4_K, FS, d, s_d), "ffn_up_shexp.weight": mat(Q4_K, FS, d, s_d),
+                 "ffn_down_shexp.weight": mat(Q6_K, d, FS, 1 / np.sqrt(FS))}
+    dense = {}
+    if ND:
+        dense = {"ffn_gate.weight": mat(Q4_K, FD, d, s_d), "ffn_up.weight": mat(Q4_K, FD, d, s_d),
+                 "ffn_down.weight": mat(Q8_0, d, FD, 1 / np.sqrt(FD))}
     for l in range(L):
         p = f"blk.{l}."
-        T.update({p + k: v for k, v in shared.items()})
+        T.update({p + k: v for k, v in attn.items()})
         T[p + "attn_norm.weight"] = f32(np.ones(d), [d])
         T[p + "ffn_norm.weight"] = f32(np.ones(d), [d])
+        if l < ND:
+            T.update({p + k: v for k, v in dense.items()})
+            continue
         T[p + "ffn_gate_inp.weight"] = f32(rng.standard_normal(NE * d) * (4.0 / np.sqrt(d)), [d, NE])
         T[p + "ffn_gate_exps.weight"], T[p + "ffn_up_exps.weight"], T[p + "ffn_down_exps.weight"] = gate, up, down
+        T.update({p + k: v for k, v in shexp.items()})
     ctx.set_stream(torch.cuda.current_stream())
     t0 = time.perf_counter()
     dec = Decoder(ctx, hp, T)
@@ -533,18 +657,21 @@ def decode_stack_leg(ctx, torch, prompt: int = 128, steps: int = 256):
     finally:
         dec.close()
         torch.cuda.empty_cache()
-    per_layer_attn = (H * hd + 2 * KV * hd) * d // 256 * 144 + d * (H * hd) // 256 * 144
-    per_expert = 3 * ff * d // 256 * 144
-    tb = L * (per_layer_attn + NU * per_expert + NE * d * 4) + V * d // 256 * 210
+    attn_b = _tbytes(Q4_K, (H + 2 * KV) * hd, d) + _tbytes(Q4_K, d, H * hd)
+    expert_b = 2 * _tbytes(Q4_K, ff, d) + _tbytes(dt, d, ff)
+    moe_b = NU * expert_b + NE * d * 4 + ((2 * _tbytes(Q4_K, FS, d) + _tbytes(Q6_K, d, FS)) if FS else 0)
+    dense_b = (2 * _tbytes(Q4_K, FD, d) + _tbytes(Q8_0, d, FD)) if ND else 0
+    tb = L * attn_b + ND * dense_b + (L - ND) * moe_b + _tbytes(Q6_K, V, d)
     n = steps - 4
-    return {"model": "synthetic moe-6b (llama arch)", "layers": L, "prompt_tokens": prompt,
+    return {"model": c["name"], "layers": L, "dense_layers": ND, "prompt_tokens": prompt,
             "prefill_tokens_per_s": round(prompt / prefill_s, 1), "decode_steps": n,
             "decode_tokens_per_s": round(n / dec_s, 1), "ms_per_token": round(dec_s / n * 1e3, 3),
             "weight_bytes_per_token": tb, "hbm_GBps": round(tb * n / dec_s / 1e9, 1),
+            "hbm_frac": round(tb * n / dec_s / 1e9 / HBM_PEAK_GBPS, 4),
             "distinct_tokens": n_distinct, "load_s": round(load_s, 1)}
 
 
-def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
+def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1, cpu_seconds: float = 0.0, cpu_cap: int = 16):
     """Qwen3-30B-A3B-shaped layer: hidden 2048, FFN 768, 128 experts, top-8,
     Q4_K random-init experts, router N(0, 0.02) plus a rank-1 Zipf(1.1) bias
     over a seeded expert permutation (activations N(1, 1) carry it into the
@@ -560,12 +687,14 @@ def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
     g.manual_seed(seed)
     rng = np.random.default_rng(seed)
     base = 100
+    routers = []
     for l in range(layers):
         ctx.layer_create(base + l, E4, K4, D4, F4, Q4_K, Q4_K, Q4_K, True, 0.0)
         router = rng.standard_normal((E4, D4)) * 0.02
         rank = rng.permutation(E4) + 1
         router += (-1.1 * np.log(rank.astype(np.float64)) / D4)[:, None]
-        ctx.router_upload(base + l, router.astype(np.float32))
+        routers.append(router.astype(np.float32))
+        ctx.router_upload(base + l, routers[-1])
         for e in range(E4):
             for p in range(3):
                 t = torch.randint(0, 256, (part // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
@@ -588,9 +717,144 @@ def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1):
         t = graph_time(torch, ctx, [lambda l=l: ctx.moe_ffn(base + l, hp[l], op[l]) for l in range(layers)], reps)
         t /= layers
         tb = (sum(touched) / layers) * expert_bytes + E4 * D4 * 4
-        res.append({"tokens": S, "regime": ["avx2", "int8", "exact"][regime], "tokens_per_s": round(S / t, 1),
-                    "us_per_step": round(t * 1e6, 2), "experts_touched": sum(touched) / layers,
-                    "hbm_touched_GBps": round(tb / t / 1e9, 1)})
+        row = {"tokens": S, "regime": ["avx2", "int8", "exact"][regime], "tokens_per_s": round(S / t, 1),
+               "us_per_step": round(t * 1e6, 2), "experts_touched": sum(touched) / layers,
+               "hbm_touched_GBps": round(tb / t / 1e9, 1), "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
+        if S == 1:  # per-kernel times (their own dispatch timestamps) and the gate/up kernel's roofline
+            ctx.profile_enable(True)
+            for i in range(layers * 10):
+                ctx.moe_ffn(base + i % layers, hp[i % layers], op[i % layers])
+            torch.cuda.synchronize()
+            kern = {}
+            for n in ("route_decode", "moe_gate_up_dec", "quant_slots_q8k", "moe_down_dec"):
+                ms, cnt = ctx.profile_read(n)
+                if cnt:
+                    kern[n] = {"avg_us": round(ms * 1000.0 / cnt, 3), "launches": cnt}
+            ctx.profile_enable(False)
+            row["kernels_us"] = kern
+            if "moe_gate_up_dec" in kern:
+                # 8 experts x (gate + up) rows, the Q8_K row of x, h out
+                alg = K4 * 2 * part + (D4 + D4 // 16 * 4 + D4 // 256 * 4) + K4 * F4 * 4
+                ach = alg / (kern["moe_gate_up_dec"]["avg_us"] * 1e-6) / 1e9
+                row["roofline"] = {"bound": "hbm", "kernel": "moe_gate_up_dec", "achieved": round(ach, 1),
+                                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                                   "alg_bytes_per_launch": alg}
+            if cpu_seconds > 0:  # the oracle's moe_ffn on layer 0's bytes, one token per call
+                from oracle import pyoracle as orc
+
+                parts = [[ctx.expert_read(base, e, p) for p in range(3)] for e in range(E4)]
+                L4 = orc.Layer(E4, K4, D4, F4, Q4_K, Q4_K, Q4_K, routers[0], [p[0] for p in parts],
+                               [p[1] for p in parts], [p[2] for p in parts], True, 0.0)
+                hx = (rng.standard_normal((64, D4)) + 1.0).astype(np.float32)
+                nt = cpu_threads(cpu_cap)
+                n, el = timed_calls(lambda i: L4.moe_ffn(hx[i % 64:i % 64 + 1], threads=nt), cpu_seconds, 20000)
+                row["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": nt, "kind": "port",
+                                       "sample": f"{n} single-token moe_ffn calls on layer 0 (AVX2 regime), "
+                                                 f"{el:.1f} s"}
+        res.append(row)
+    ctx.set_regime(0)
+    for l in range(layers):
+        ctx.layer_destroy(base + l)
+    torch.cuda.empty_cache()
+    return res
+
+
+def c5_layer_leg(ctx, torch, layers: int = 4, seed: int = 5, cpu_seconds: float = 0.0, cpu_cap: int = 16):
+    """DeepSeek-V2-Lite-shaped MoE layer (the MoE layer of config 5): hidden
+    2048, 64 routed experts of FFN 1408, top-6, softmax weights not
+    renormalised; Q4_K gate/up, Q8_0 routed down (1408 columns need a
+    32-element block type); 2 shared experts as one ungated ffn_*_shexp FFN of
+    2816 (Q4_K gate/up, Q6_K down). Random well-formed blocks (weights std
+    ~0.02), router N(0, 0.02), layers rotated (4 x 415 MB) past the Infinity
+    Cache. Decode batch 1 (with per-kernel times, the gate/up kernel's
+    roofline and the oracle on this host), 8 and 128 tokens."""
+    import numpy as np
+
+    E5, K5, D5, F5, FS = 64, 6, 2048, 1408, 2816
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    h4 = torch.tensor(np.concatenate([np.array([1.4e-4], np.float16).view(np.uint8),
+                                      np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)]),
+                      dtype=torch.uint8, device="cuda")
+    h8 = torch.tensor(np.array([0.02 / 74.0], np.float16).view(np.uint8), dtype=torch.uint8, device="cuda")
+    gu_b, dn_b = _tbytes(Q4_K, F5, D5), _tbytes(Q8_0, D5, F5)
+    base, routers, shared = 400, [], []
+    for l in range(layers):
+        ctx.layer_create(base + l, E5, K5, D5, F5, Q4_K, Q4_K, Q8_0, False, 1.0)
+        routers.append((rng.standard_normal((E5, D5)) * 0.02).astype(np.float32))
+        ctx.router_upload(base + l, routers[-1])
+        for e in range(E5):
+            for p in range(2):
+                t = torch.randint(0, 256, (gu_b // 144, 144), dtype=torch.uint8, device="cuda", generator=g)
+                t[:, 0:4] = h4
+                ctx.expert_upload(base + l, e, p, t)
+            t = torch.randint(0, 256, (dn_b // 34, 34), dtype=torch.uint8, device="cuda", generator=g)
+            t[:, 0:2] = h8
+            ctx.expert_upload(base + l, e, 2, t)
+        sh = [synthetic_blocks(Q4_K, FS * D5 // 256, 0.02, rng), synthetic_blocks(Q4_K, FS * D5 // 256, 0.02, rng),
+              synthetic_blocks(Q6_K, D5 * FS // 256, 0.02, rng)]
+        ctx.shared_expert(base + l, FS, (Q4_K, Q4_K, Q6_K), *sh, gate_inp=None)
+        shared.append(sh)
+    torch.cuda.synchronize()
+    routed_b = 2 * gu_b + dn_b
+    shared_b = 2 * _tbytes(Q4_K, FS, D5) + _tbytes(Q6_K, D5, FS)
+    res = []
+    for S, regime in ((1, 0), (8, 0), (128, 0), (128, 1)):
+        ctx.set_regime(regime)
+        ctx.set_stream(torch.cuda.current_stream())
+        hp = torch.randn((layers, S, D5), dtype=torch.float32, device="cuda")
+        op = torch.empty_like(hp)
+        touched = []
+        for l in range(layers):
+            ctx.moe_ffn(base + l, hp[l], op[l])
+            touched.append(len(set(ctx.last_routing(S, K5, E5)[0].cpu().numpy().ravel().tolist())))
+        t = graph_time(torch, ctx, [lambda l=l: ctx.moe_ffn(base + l, hp[l], op[l]) for l in range(layers)],
+                       50 if S <= 8 else 10) / layers
+        tb = (sum(touched) / layers) * routed_b + shared_b + E5 * D5 * 4
+        row = {"tokens": S, "regime": ["avx2", "int8", "exact"][regime], "tokens_per_s": round(S / t, 1),
+               "us_per_step": round(t * 1e6, 2), "experts_touched": sum(touched) / layers,
+               "bytes_touched": int(tb), "hbm_touched_GBps": round(tb / t / 1e9, 1),
+               "hbm_frac": round(tb / t / 1e9 / HBM_PEAK_GBPS, 4)}
+        if S == 1:
+            ctx.profile_enable(True)
+            for i in range(layers * 10):
+                ctx.moe_ffn(base + i % layers, hp[i % layers], op[i % layers])
+            torch.cuda.synchronize()
+            kern = {}
+            for n in ("route_decode", "moe_gate_up_dec", "quant_slots_q8", "moe_down_dec", "quant_q8k", "matvec_q4k",
+                      "shared_swiglu", "matvec_q6k", "shared_add"):
+                ms, cnt = ctx.profile_read(n)
+                if cnt:
+                    kern[n] = {"avg_us": round(ms * 1000.0 / cnt, 3), "launches": cnt}
+            ctx.profile_enable(False)
+            row["kernels_us"] = kern
+            if "moe_gate_up_dec" in kern:
+                alg = K5 * 2 * gu_b + (D5 + D5 // 32 * 4 + D5 // 16 * 4) + K5 * F5 * 4
+                ach = alg / (kern["moe_gate_up_dec"]["avg_us"] * 1e-6) / 1e9
+                row["roofline"] = {"bound": "hbm", "kernel": "moe_gate_up_dec", "achieved": round(ach, 1),
+                                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                                   "alg_bytes_per_launch": alg}
+            if cpu_seconds > 0:  # the oracle's moe_ffn + shared expert on layer 0's bytes, one token per call
+                from oracle import pyoracle as orc
+
+                parts = [[ctx.expert_read(base, e, p) for p in range(3)] for e in range(E5)]
+                L5 = orc.Layer(E5, K5, D5, F5, Q4_K, Q4_K, Q8_0, routers[0], [p[0] for p in parts],
+                               [p[1] for p in parts], [p[2] for p in parts], False, 1.0)
+                hx = rng.standard_normal((64, D5)).astype(np.float32)
+                nt = cpu_threads(cpu_cap)
+                sh = shared[0]
+
+                def one(i):
+                    x = hx[i % 64:i % 64 + 1]
+                    orc.shared_expert_add(L5.moe_ffn(x, threads=nt), x, D5, FS, (Q4_K, Q4_K, Q6_K), sh[0], sh[1],
+                                          sh[2], None, 0, nt)
+
+                n, el = timed_calls(one, cpu_seconds, 20000)
+                row["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s", "cores": nt, "kind": "port",
+                                       "sample": f"{n} single-token moe_ffn + shared-expert calls on layer 0 "
+                                                 f"(AVX2 regime), {el:.1f} s"}
+        res.append(row)
     ctx.set_regime(0)
     for l in range(layers):
         ctx.layer_destroy(base + l)
@@ -810,17 +1074,24 @@ def main():
     if "batches" in legs:
         res["decode_batches"] = [batch_leg(ctx, torch, a.layers, S2, rg) for S2 in (8, 32) for rg in (0, 1)]
     if "matvec_q4k" in legs:
-        res["matvec_q4k"] = matvec_leg(ctx, torch, Q4_K)
+        res["matvec_q4k"] = matvec_leg(ctx, torch, Q4_K, cpu_seconds=0.0 if a.no_cpu else a.cpu_seconds / 5,
+                                       cpu_cap=a.cpu_threads)
     if "matvec_q6k" in legs:
         res["matvec_q6k"] = matvec_leg(ctx, torch, Q6_K)
     if "q4k_m" in legs:
         res["decode_b1_q4k_m"] = q4km_leg(ctx, torch)
     if "qwen3" in legs:
-        res["qwen3"] = qwen3_leg(ctx, torch)
+        res["qwen3"] = qwen3_leg(ctx, torch, cpu_seconds=0.0 if a.no_cpu else a.cpu_seconds / 4,
+                                 cpu_cap=a.cpu_threads)
+    if "c5_layer" in legs:
+        res["c5_layer"] = c5_layer_leg(ctx, torch, cpu_seconds=0.0 if a.no_cpu else a.cpu_seconds / 4,
+                                       cpu_cap=a.cpu_threads)
     if "preload" in legs:
         res["tier_preload"] = preload_leg(ctx, torch)
     if "decode_stack" in legs:
-        res["decode_stack"] = decode_stack_leg(ctx, torch)
+        res["decode_stack"] = decode_stack_leg(ctx, torch, MOE6B)
+    if "c5_stack" in legs:
+        res["c5_stack"] = decode_stack_leg(ctx, torch, DSV2LITE)
     if "measure" in legs:  # the figures kestrel's planner would otherwise estimate (kmoe_measure)
         res["planner_inputs"] = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in ctx.measure().items()}
     if not a.no_cpu:
