@@ -269,6 +269,20 @@ int kmoe_bytes_per_expert(kmoe_ctx *ctx, uint32_t layer, uint64_t *bytes);
  * out[s] = sum over the token's experts in ascending id of w * y.
  * h [s_rows, n_embd] f32 in, out [s_rows, n_embd] f32 out (device). */
 int kmoe_moe_ffn(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev);
+/* kmoe_moe_ffn without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, hosts that forbid hipMalloc). Same kernels,
+ * routing, dispatch and output bits as kmoe_moe_ffn, but the workspace is a
+ * fixed 16 MiB device array per GPU (allocated with the library's code
+ * object, held until the process ends) instead of the context's grown one;
+ * a call needing more (many tokens) fails with KMOE_E_INVALID and names the
+ * size. It calls no hipMalloc / hipFree and creates no events (profiling is
+ * suspended for the call). Every call on one GPU, from any context, shares
+ * that array and leaves its contents behind: calls that overlap on one GPU
+ * (other streams, other threads) race, and the caller must order them.
+ * kmoe_moe_last_routing reads the routing from that array until the next
+ * such call. */
+int kmoe_moe_ffn_noalloc(kmoe_ctx *ctx, uint32_t layer, const float *h_dev, int64_t s_rows, float *out_dev);
 /* Transformer::moe_ffn with its own signature (transformer.rs:513): h:
  * &[f32] in, the Vec<f32> out, both host memory [s_rows, n_embd] (the
  * caller's out buffer). Synchronous; same arithmetic as kmoe_moe_ffn. */

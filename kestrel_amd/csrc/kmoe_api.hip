@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -85,6 +86,17 @@ struct Event2 {
 };
 
 }  // namespace
+
+// Workspace of kmoe_moe_ffn_noalloc: a fixed device array, one per GPU (each
+// device holds its own copy at its own address), shared by every call on that
+// GPU and kept until the process ends. Host code never uses this name as an
+// address: the device's address comes from hipGetSymbolAddress at
+// kmoe_create (g_scratch below).
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static void *g_scratch[kMaxDevices];  // device address of scratch per device, null until looked up
+static std::mutex g_scratch_mu;
 
 // Device completion counters per context (words used by the decode router).
 constexpr int kCounterWords = 64;
@@ -551,6 +563,20 @@ int kmoe_create(int device, kmoe_ctx **out) {
   }
   size_t fr = 0, tot = 0;
   if (hipMemGetInfo(&fr, &tot) == hipSuccess) c->vram_limit = tot;
+  if (device < kMaxDevices) {  // this device's copy of the no-alloc scratch (device current here)
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[device]) {
+      void *p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+        (void)hipGetLastError();
+        (void)hipFree(c->counters);
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return KMOE_E_HIP;
+      }
+      g_scratch[device] = p;
+    }
+  }
   *out = c;
   return KMOE_OK;
 }
@@ -1239,7 +1265,7 @@ int kmoe_bytes_per_expert(kmoe_ctx *c, uint32_t layer, uint64_t *bytes) {
 // (x += y, f = rmsnorm(x) * w), folded into the single-token router kernel
 // where it supports the shapes, else by the norm kernel.
 static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out, const RouteNorm *norm,
-                   const kmoe_moe_dbg *dbg = nullptr) {
+                   const kmoe_moe_dbg *dbg = nullptr, uint8_t *fixed_ws = nullptr, size_t fixed_size = 0) {
   if (!c) return KMOE_E_INVALID;
   Layer *L = find_layer(c, layer);
   if (!L) return fail(c, KMOE_E_NOT_LOADED, "layer %u not created", layer);
@@ -1270,10 +1296,20 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     sh_need = cv.off + align_up(q);
   }
   DeviceGuard g(c->device);
-  int rc = ensure_ws(c, moe_need + sh_need);
-  if (rc) return rc;
+  int rc = KMOE_OK;
+  uint8_t *wsb = fixed_ws;  // the caller's fixed workspace, or the context's (grown here)
+  if (fixed_ws) {
+    if (moe_need + sh_need > fixed_size)
+      return fail(c, KMOE_E_INVALID,
+                  "%lld tokens of layer %u need %zu bytes of workspace, past the %zu-byte static scratch",
+                  (long long)S, layer, moe_need + sh_need, fixed_size);
+  } else {
+    rc = ensure_ws(c, moe_need + sh_need);
+    if (rc) return rc;
+    wsb = c->ws;
+  }
   size_t tmp;
-  MoeWs w = carve_moe(c->ws, S, E, k, d, F, &tmp);
+  MoeWs w = carve_moe(wsb, S, E, k, d, F, &tmp);
   const int regime = c->regime;
   hipStream_t st = c->stream;
   // Capture of the int-path integers (kmoe_moe_ffn_dbg): zeroed here, added to by the kernels.
@@ -1498,11 +1534,11 @@ done:
   }
   if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)
     auto &SH = L->sh;
-    Carver cv{c->ws + moe_need};
+    Carver cv{wsb + moe_need};
     float *gs = cv.take<float>(S * Fs), *us = cv.take<float>(S * Fs), *ys = cv.take<float>(S * d);
     float *gl = cv.take<float>(S);
     size_t q = 0;
-    QRows qr = carve_qrows(c->ws + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
+    QRows qr = carve_qrows(wsb + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
     rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
     if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
     if (rc) return rc;
@@ -1555,6 +1591,18 @@ int kmoe_moe_ffn_host(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, fl
   HIP_OK(c, hipMemcpyAsync(out, od, n, hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
   return KMOE_OK;
+}
+
+int kmoe_moe_ffn_noalloc(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float *out) {
+  if (!c) return KMOE_E_INVALID;
+  if (c->device >= kMaxDevices || !g_scratch[c->device])
+    return fail(c, KMOE_E_HIP, "no static scratch on device %d", c->device);
+  // no events either: profiling is suspended for the call
+  const bool prof = c->prof;
+  c->prof = false;
+  const int rc = moe_ffn(c, layer, h, S, out, nullptr, nullptr, (uint8_t *)g_scratch[c->device], kScratchBytes);
+  c->prof = prof;
+  return rc;
 }
 
 int kmoe_norm_moe_ffn(kmoe_ctx *c, uint32_t layer, float *x, const float *y, const float *norm_w, float eps,

@@ -82,6 +82,7 @@ SIGNATURES = {
     "kmoe_moe_ffn": (C.c_int, [_P, _u32, _P, _i64, _P]),
     "kmoe_moe_ffn_dbg": (C.c_int, [_P, _u32, _P, _i64, _P, _P]),
     "kmoe_moe_ffn_host": (C.c_int, [_P, _u32, _P, _i64, _P]),
+    "kmoe_moe_ffn_noalloc": (C.c_int, [_P, _u32, _P, _i64, _P]),
     "kmoe_matmul_host": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _i64, _P]),
     "kmoe_expert_part_layout": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_i32)]),
     "kmoe_norm_matmul_rope_kv": (C.c_int, [_P, _P, _P, _P, _f, C.c_int, _P, _sz, _i64, _P, _P, _i32, _i32, _i32,
