@@ -1285,10 +1285,9 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   const size_t moe_need = align_up(need);
   size_t sh_need = 0;
   const int64_t Fs = L->sh.n_ff, mx = d > Fs ? d : Fs;
-  if (L->sh.on) {  // gs, us [S, Fs], ys [S, d], gate logits [S], int8 scratch [S, max(d, Fs)]
+  if (L->sh.on) {  // gs, us [S, Fs] (one span), ys [S, d], gate logits [S], int8 scratch [S, max(d, Fs)]
     Carver cv{nullptr};
-    cv.take<float>(S * Fs);
-    cv.take<float>(S * Fs);
+    cv.take<float>(2 * S * Fs);
     cv.take<float>(S * d);
     cv.take<float>(S);
     size_t q = 0;
@@ -1535,10 +1534,36 @@ done:
   if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)
     auto &SH = L->sh;
     Carver cv{wsb + moe_need};
-    float *gs = cv.take<float>(S * Fs), *us = cv.take<float>(S * Fs), *ys = cv.take<float>(S * d);
+    float *gs = cv.take<float>(2 * S * Fs), *us = gs + S * Fs, *ys = cv.take<float>(S * d);
     float *gl = cv.take<float>(S);
     size_t q = 0;
     QRows qr = carve_qrows(wsb + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
+    // One token on the int8 path, gate and up of one type stored back to back
+    // (they are one [2 Fs, d] matrix): one product over both reads the int8
+    // row of h already made for the routed experts (the same Q8KRow / Q8Row
+    // quantization), one kernel applies SwiGLU and quantizes its output, and
+    // the down product adds its gated result into out. Same arithmetic as the
+    // general sequence below.
+    const int t0 = SH.type[0], t2 = SH.type[2];
+    if (S == 1 && x_int && int_path(regime, 1) && t0 != KMOE_F32 && SH.type[1] == t0 && t2 != KMOE_F32 &&
+        is_kq(t0) == is_kq(gt) && SH.off[1] == SH.off[0] + SH.len[0]) {
+      if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, gl, true));
+      rc = matvec_q8_impl(c, t0, SH.arena + SH.off[0], 2 * Fs, d, w.xq, w.xd, w.xs, 1, gs);
+      if (rc) return rc;
+      LAUNCH(c, "shared_swiglu_quant", launch_swiglu_quant(st, t2, gs, Fs, qr.q, qr.d, qr.s));
+      const AddEpi epi{SH.gate_ok ? gl : nullptr};
+      const hipError_t e = timed(c, "shared_down_add", [&]() {
+        return launch_decode_plain(st, t2, SH.arena + SH.off[2], d, Fs, qr.q, qr.d, qr.s, out, &epi);
+      });
+      if (e == hipErrorNotSupported) {  // row too wide for registers: plain product, then the add
+        rc = matvec_q8_impl(c, t2, SH.arena + SH.off[2], d, Fs, qr.q, qr.d, qr.s, 1, ys);
+        if (rc) return rc;
+        LAUNCH(c, "shared_add", launch_shared_add(st, out, ys, SH.gate_ok ? gl : nullptr, S, d));
+      } else {
+        HIP_OK(c, e);
+      }
+      goto shared_done;
+    }
     rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
     if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
     if (rc) return rc;
@@ -1548,6 +1573,7 @@ done:
     if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, gl, true));
     LAUNCH(c, "shared_add", launch_shared_add(st, out, ys, SH.gate_ok ? gl : nullptr, S, d));
   }
+shared_done:
   c->last_idx = w.idx;
   c->last_w = w.wsel;
   c->last_perm = w.perm;

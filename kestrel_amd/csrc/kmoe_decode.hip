@@ -182,6 +182,8 @@ struct RowsArgs {
   const int32_t *xbs;
   float *out;
   int32_t groups;  // work-groups striding over the rows
+  int32_t add;     // out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
+  const float *add_logit;
 };
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -223,6 +225,11 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
   }
   const int kq = lane & 3;
   const int64_t rows = a.rows;
+  float add_scale = 1.0f;  // the shared expert's gate (k_shared_add's arithmetic)
+  if (a.add && a.add_logit) {
+    const float den = 1.0f + expf_cr(-*a.add_logit);
+    add_scale = 1.0f / den;
+  }
   for (int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU; r0 < rows; r0 += (int64_t)a.groups * 4 * RU) {
     u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
 #pragma unroll
@@ -256,7 +263,14 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
       acc = group_sum<64>(acc);
       res = lane == u ? acc : res;
     }
-    if (lane < RU && r0 + lane < rows) a.out[r0 + lane] = res;
+    if (lane < RU && r0 + lane < rows) {
+      if (a.add) {
+        const float p = add_scale * res;
+        a.out[r0 + lane] = a.out[r0 + lane] + p;
+      } else {
+        a.out[r0 + lane] = res;
+      }
+    }
   }
 }
 
@@ -269,7 +283,7 @@ bool dec_rows_supported(int64_t cols) {
 }
 
 hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
-                           const float *xd, const int32_t *xbs, float *out) {
+                           const float *xd, const int32_t *xbs, float *out, const AddEpi *epi) {
   if (rows <= 0) return hipSuccess;
   if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u) || (tiled && ((uintptr_t)w & 15u)) || ((uintptr_t)xq & 15u) ||
       ((uintptr_t)xbs & 15u))
@@ -278,7 +292,7 @@ hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t
   const int ru = tpl <= 2 ? 2 : 1;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0};
+  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0, epi ? 1 : 0, epi ? epi->logit : nullptr};
   // work-group steps of 4*RU rows, spread evenly over about two groups per CU
   const int64_t need = (rows + 4 * ru - 1) / (4 * ru);
   const int64_t cap = 2LL * cus;

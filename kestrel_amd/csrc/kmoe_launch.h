@@ -85,11 +85,18 @@ void tq6_convert_host(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t nb
 // Plain: out[s*rows + r] for s < s_rows; activations pre-quantized.
 hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                              const float *xd, const int32_t *xbs, int64_t s_rows, float *out);
+// Epilogue of a one-row matvec that adds into out instead of storing:
+// out[r] = out[r] + scale * y[r], scale = 1 / (1 + exp(-*logit)) or 1 when
+// logit is null (the shared expert's gated add, transformer.rs:584-586).
+struct AddEpi {
+  const float *logit = nullptr;
+};
 // Single activation row (decode, one token): activation slice held in registers.
 // Return hipErrorNotSupported when the row is too wide for that; callers then
-// use the LDS-staged kernels.
+// use the LDS-staged kernels. epi: add into out (see AddEpi).
 hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
-                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out);
+                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
+                               const AddEpi *epi = nullptr);
 struct DecSelect;
 // sel: the kernel selects the token's experts from its logits and writes the
 // routing (hipErrorNotSupported where decode_gate_up_can_select is false).
@@ -126,7 +133,7 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
 // rows 4, tiled rows 16).
 bool dec_rows_supported(int64_t cols);
 hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
-                           const float *xd, const int32_t *xbs, float *out);
+                           const float *xd, const int32_t *xbs, float *out, const AddEpi *epi = nullptr);
 // Down projection + combine for one token: out[r] = sum_e (asc) w_e * y_e[r].
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
@@ -239,6 +246,10 @@ hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t 
 // ---- shared expert (kmoe_shared.hip)
 // g = g / (1 + exp(-g)) * u over n elements.
 hipError_t launch_swiglu(hipStream_t st, float *g, const float *u, int64_t n);
+// SwiGLU of one row whose gate and up values sit side by side (gu [2F]: g
+// then u), quantized for the next product: Q8_K rows (K-quant type) or Q8 rows
+// (Q8_0), written to q, d, s as the activation quantizers write them.
+hipError_t launch_swiglu_quant(hipStream_t st, int type, const float *gu, int64_t F, int8_t *q, float *d, int32_t *s);
 // out[s] += sigmoid(logits[s]) * y[s] (logits null: scale 1).
 hipError_t launch_shared_add(hipStream_t st, float *out, const float *y, const float *logits, int64_t S, int64_t d);
 

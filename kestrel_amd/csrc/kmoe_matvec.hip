@@ -55,6 +55,8 @@ struct MvArgs {
   DecSelect sel;
   QkvRope rope;  // M_QKV: the epilogue of the one-token q/k/v projection
   BlockDbg dbg;  // grouped modes: per-block integers of the part(s) computed
+  int add;        // M_PLAIN: out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
+  const float *add_logit;
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -917,6 +919,14 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
             const float den = 1.0f + expf_cr(-g);
             const float q = g / den;
             a.out[p0 * rows + r] = q * acc1[u];
+          } else if (a.add) {  // the shared expert's gated add (k_shared_add's arithmetic)
+            float scale = 1.0f;
+            if (a.add_logit) {
+              const float den = 1.0f + expf_cr(-*a.add_logit);
+              scale = 1.0f / den;
+            }
+            const float pv = scale * acc0[u];
+            a.out[r] = a.out[r] + pv;
           } else {
             a.out[r] = acc0[u];
           }
@@ -1194,8 +1204,10 @@ hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_ma
 #define KMOE_LPR_CASE(LPRV)                                                                          \
   case LPRV:                                                                                         \
     if constexpr (MODE == M_SUMS) return launch_one<TYPE, LPRV, 1, MODE>(st, a, grid);               \
-    else return nt_max == 1 ? launch_one<TYPE, LPRV, 1, MODE>(st, a, grid)                           \
-                            : launch_one<TYPE, LPRV, 3, MODE>(st, a, grid);
+    else if (nt_max == 1) return launch_one<TYPE, LPRV, 1, MODE>(st, a, grid);                       \
+    else if (nt_max == 16) return launch_one<TYPE, LPRV, 16, MODE>(st, a, grid);                     \
+    else if (nt_max == 8) return launch_one<TYPE, LPRV, 8, MODE>(st, a, grid);                       \
+    else return launch_one<TYPE, LPRV, 3, MODE>(st, a, grid);
   switch (lpr) {
     KMOE_LPR_CASE(64)
     KMOE_LPR_CASE(32)
@@ -1209,6 +1221,17 @@ hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_ma
 
 constexpr int kRowsPerBlock = 64;
 
+// Activation rows staged per pass of the LDS-staged kernel: every weight row
+// is read once per pass, so batches take passes of 16 or 8 rows where the
+// staging fits 64 KB of LDS (3 otherwise; 1 for a single row).
+int pick_nt(int type, int64_t cols, int64_t rows_hint) {
+  if (rows_hint <= 1) return 1;
+  const int64_t per = is_kquant(type) ? ActLayout<T_Q4_K>(cols).total : ActLayout<T_Q8_0>(cols).total;
+  if (rows_hint >= 24 && 16 * per <= 65536) return 16;
+  if (rows_hint >= 6 && 8 * per <= 65536) return 8;
+  return 3;
+}
+
 bool act_fits(int type, int64_t cols) {
   const int64_t per = is_kquant(type) ? ActLayout<T_Q4_K>(cols).total : ActLayout<T_Q8_0>(cols).total;
   return 3 * per <= 65536;
@@ -1217,8 +1240,12 @@ bool act_fits(int type, int64_t cols) {
 }  // namespace
 
 hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
-                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out) {
+                               const int8_t *xq, const float *xd, const int32_t *xbs, float *out, const AddEpi *epi) {
   MvArgs a{};
+  if (epi) {
+    a.add = 1;
+    a.add_logit = epi->logit;
+  }
   a.w0 = w;
   a.rows = rows;
   a.cols = cols;
@@ -1228,7 +1255,7 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   a.s_rows = 1;
   a.out = out;
   if (type == T_Q4_K) {
-    const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out);
+    const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out, epi);
     if (e != hipErrorNotSupported) return e;
     return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
   }
@@ -1381,7 +1408,7 @@ hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t
   a.out = out;
   a.rows_per_block = kRowsPerBlock;
   dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  const int nt = s_rows == 1 ? 1 : 3;
+  const int nt = pick_nt(type, cols, s_rows);
   if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_PLAIN>(st, a, grid, nt);
   if (type == T_Q6_K) return dispatch_lpr_nt<T_Q6_K, M_PLAIN>(st, a, grid, nt);
   if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_PLAIN>(st, a, grid, nt);
@@ -1431,8 +1458,9 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
   a.min_rows = min_rows;
   a.rows_per_block = kRowsPerBlock;
   dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)max_active);
-  // A single token routes at most one row to each expert: the NT=1 kernel.
-  const int nt = s_rows == 1 ? 1 : 3;
+  // A single token routes at most one row to each expert: the NT=1 kernel;
+  // otherwise passes sized for the mean rows per active expert.
+  const int nt = s_rows == 1 ? 1 : pick_nt(type, cols, (s_rows * rt.topk + max_active - 1) / max_active);
   if (type == T_Q4_K)
     return mode == 0 ? dispatch_lpr_nt<T_Q4_K, M_GATE_UP>(st, a, grid, nt)
                      : dispatch_lpr_nt<T_Q4_K, M_DOWN>(st, a, grid, nt);

@@ -697,6 +697,58 @@ def test_shared_expert_layer(ctx, orc, wtype, ffs, with_gate):
         assert e < TOL, (S, regime, e)
 
 
+@pytest.mark.parametrize("types,ffs,with_gate", [
+    ((Q4_K, Q4_K, Q6_K), C5_SHARED_FF, False),  # DeepSeek-V2-Lite's shared experts
+    ((Q4_K, Q4_K, Q4_K), 1536, True),
+    ((Q8_0, Q8_0, Q8_0), 1024, True),
+])
+@pytest.mark.parametrize("regime", [0, 1])
+def test_shared_expert_one_token_bits_of_product_sequence(ctx, orc, types, ffs, with_gate, regime):
+    """One token on the int8 path: the shared expert (one product over the
+    back-to-back gate and up rows, SwiGLU fused with the quantization of its
+    output, down adding its gated result into out) gives the bits of the
+    sequence transformer.rs:572-587 spells out, made of separate calls:
+    quant::matmul of gate and of up (kmoe_matmul, the same int8 products),
+    SwiGLU and sigmoid with a correctly rounded exp, quant::matmul of down, and
+    out + scale * y on top of the routed experts' output."""
+    d = 2048
+    t0, _, t2 = types
+    spec = LayerSpec(16, 4, d, 1024, t0, seed=40 + ffs, quantized=False)
+    sh = [random_blocks(t0, ffs, d, 910), random_blocks(t0, ffs, d, 911), random_blocks(t2, d, ffs, 912)]
+    gi = orc.normal(951, d, 0.0, 0.05) if with_gate else None
+    h = orc.normal(952, d).reshape(1, d)
+    outs = []
+    ctx.set_regime(regime)
+    try:
+        for shared in (True, False):
+            lid = _layer_id[0]
+            _layer_id[0] += 1
+            spec.upload(ctx, lid)
+            try:
+                if shared:
+                    ctx.shared_expert(lid, ffs, types, sh[0], sh[1], sh[2], gi)
+                outs.append(host(ctx.moe_ffn(lid, dev(h))))
+            finally:
+                ctx.layer_destroy(lid)
+        g = host(ctx.matmul(t0, dev(sh[0]), ffs, d, dev(h)))
+        u = host(ctx.matmul(t0, dev(sh[1]), ffs, d, dev(h)))
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)  # correctly rounded up to double rounding
+        a = (g / (np.float32(1.0) + e)) * u
+        y = host(ctx.matmul(t2, dev(sh[2]), d, ffs, dev(a)))
+        scale = np.float32(1.0)
+        if with_gate:
+            gl = host(ctx.matmul(0, dev(gi), 1, d, dev(h)))[0, 0]
+            scale = np.float32(1.0) / (np.float32(1.0) + np.float32(np.exp(-np.float64(gl))))
+    finally:
+        ctx.set_regime(0)
+    exp = outs[1] + scale * y
+    assert np.array_equal(outs[0].view(np.uint32), exp.view(np.uint32)), \
+        int((outs[0].view(np.uint32) != exp.view(np.uint32)).sum())
+    ref = orc.shared_expert_add(spec.oracle_layer().moe_ffn(h, regime), h, d, ffs, types, sh[0], sh[1], sh[2], gi,
+                                regime)
+    assert rel_l2(outs[0], ref) < TOL
+
+
 def test_shared_expert_errors(ctx):
     from kestrel_amd.kmoe import KmoeError
 
