@@ -56,6 +56,7 @@ struct MvArgs {
   QkvRope rope;  // M_QKV: the epilogue of the one-token q/k/v projection
   BlockDbg dbg;  // grouped modes: per-block integers of the part(s) computed
   int add;        // M_PLAIN: out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
+  int32_t chunk;  // LDS-staged plain modes: activation rows per work-group (blockIdx.y picks the chunk)
   const float *add_logit;
 };
 
@@ -362,11 +363,12 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
   const int64_t xs_stride = cols / 16, xd_stride = nblk;
   const ActLayout<TYPE> L(cols);
 
-  int n;
+  int n, c_begin = 0;
   int64_t p0 = 0;
   const uint8_t *W0 = a.w0, *W1 = nullptr;
   if constexpr (MODE == M_PLAIN || MODE == M_SUMS) {
-    n = (int)a.s_rows;
+    c_begin = (int)blockIdx.y * a.chunk;
+    n = (int)(a.s_rows < (int64_t)c_begin + a.chunk ? a.s_rows : (int64_t)c_begin + a.chunk);
   } else {
     const int i = blockIdx.y;
     if (i >= *a.rt.n_active) return;
@@ -385,7 +387,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
   const int64_t r_begin = (int64_t)blockIdx.x * a.rows_per_block;
   const int64_t r_end = r_begin + a.rows_per_block < rows ? r_begin + a.rows_per_block : rows;
 
-  for (int c0 = 0; c0 < n; c0 += NT) {
+  for (int c0 = c_begin; c0 < n; c0 += NT) {
     const int nt = n - c0 < NT ? n - c0 : NT;
     // ---- stage the activation rows of tokens c0..c0+nt in LDS
     for (int t = 0; t < nt; ++t) {
@@ -1221,6 +1223,22 @@ hipError_t dispatch_lpr_nt(hipStream_t st, const MvArgs &a, dim3 grid, int nt_ma
 
 constexpr int kRowsPerBlock = 64;
 
+// Plain-mode grid of the LDS-staged kernel: row blocks of 64 along x, and the
+// activation rows split into chunks (a multiple of nt each) along y so that
+// a launch has about 512 work-groups; each chunk re-reads the weights.
+dim3 plain_grid(MvArgs &a, int64_t rows, int64_t s_rows, int nt) {
+  const int64_t gx = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  int64_t chunks = (s_rows + nt - 1) / nt;
+  const int64_t want = (512 + gx - 1) / gx;
+  if (chunks > want) chunks = want;
+  if (chunks < 1) chunks = 1;
+  int64_t per = (s_rows + chunks - 1) / chunks;
+  per = (per + nt - 1) / nt * nt;
+  chunks = (s_rows + per - 1) / per;
+  a.chunk = (int32_t)per;
+  return dim3((unsigned)gx, (unsigned)chunks);
+}
+
 // Activation rows staged per pass of the LDS-staged kernel: every weight row
 // is read once per pass, so batches take passes of 16 or 8 rows where the
 // staging fits 64 KB of LDS (3 otherwise; 1 for a single row).
@@ -1407,8 +1425,8 @@ hipError_t launch_matvec_int(hipStream_t st, int type, const uint8_t *w, int64_t
   a.s_rows = s_rows;
   a.out = out;
   a.rows_per_block = kRowsPerBlock;
-  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   const int nt = pick_nt(type, cols, s_rows);
+  const dim3 grid = plain_grid(a, rows, s_rows, nt);
   if (type == T_Q4_K) return dispatch_lpr_nt<T_Q4_K, M_PLAIN>(st, a, grid, nt);
   if (type == T_Q6_K) return dispatch_lpr_nt<T_Q6_K, M_PLAIN>(st, a, grid, nt);
   if (type == T_Q8_0) return dispatch_lpr_nt<T_Q8_0, M_PLAIN>(st, a, grid, nt);
@@ -1429,7 +1447,7 @@ hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t
   a.isumi = sumi;
   a.imins = mins;
   a.rows_per_block = kRowsPerBlock;
-  dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  const dim3 grid = plain_grid(a, rows, s_rows, 1);
   // The Q8_0 scales are not read by the sums; the K-quants' dw/xd are not either, but
   // the staging copies xd: give it a valid dummy of the right length.
   a.xd = (const float *)xq;  // nblk*4 bytes <= cols bytes are readable there
