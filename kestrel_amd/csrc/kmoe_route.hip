@@ -235,73 +235,132 @@ __global__ void __launch_bounds__(256) k_route_topk(const float *__restrict__ lo
 }
 
 // Stable counting sort of n flat (token, slot) entries by expert id, in one
-// work-group of 1024 threads. Per chunk of 1024 entries, each wave finds the
-// lanes that share its expert with log2(E) ballots, ranks within the wave by
-// popcount, and a per-expert prefix over the 16 waves (plus a running base
-// from earlier chunks) gives every entry its rank among its expert's entries
-// in flat order — the order BTreeMap<expert, Vec<(token, w)>> fills in.
+// work-group of 1024 threads: every entry's rank among its expert's entries
+// in flat order, the order BTreeMap<expert, Vec<(token, w)>> fills in. Each
+// of the 16 waves owns a contiguous range of entries and walks it twice in
+// steps of 64. In a step the lanes that share an expert are found with
+// log2(E) ballots and ranked by popcount; pass 1 counts each wave's entries
+// per expert, a prefix over the waves (in order) and over the experts gives
+// each (wave, expert) its first position, and pass 2 places the entries.
+// With up to 64*kDispRegs entries per wave the ids are loaded into registers
+// once, all loads in flight together.
+constexpr int kDispRegs = 32;
 __global__ void __launch_bounds__(1024) k_dispatch(const uint32_t *__restrict__ idx, int64_t n, int32_t E,
                                                    uint32_t *__restrict__ perm, uint32_t *__restrict__ offsets,
                                                    uint32_t *__restrict__ inv, int32_t *__restrict__ n_active,
-                                                   int32_t *__restrict__ active, uint32_t *__restrict__ rank) {
-  __shared__ uint32_t hist[16][kMaxExperts];
+                                                   int32_t *__restrict__ active) {
+  __shared__ uint32_t cnt[16][kMaxExperts];
   __shared__ uint32_t base[kMaxExperts];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
-  for (int e = tid; e < E; e += 1024) base[e] = 0;
   for (int w = 0; w < 16; ++w)
-    for (int e = tid; e < E; e += 1024) hist[w][e] = 0;
+    for (int e = tid; e < E; e += 1024) cnt[w][e] = 0;
   __syncthreads();
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
-    const int64_t i = c0 + tid;
-    const uint32_t ev = i < n ? idx[i] : 0u;
-    const bool valid = i < n && ev < (uint32_t)E;  // ids >= E are dropped, never indexed
-    const uint32_t e = valid ? ev : 0u;
-    uint64_t same = __ballot(valid);
+  const int64_t per = ((n + 15) / 16 + 63) / 64 * 64;
+  const int64_t b0 = (int64_t)wave * per, b1 = b0 + per < n ? b0 + per : n;
+  const bool in_regs = per <= 64 * kDispRegs;
+  uint32_t ids[kDispRegs];
+  if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kDispRegs; ++k) {
+      const int64_t i = b0 + 64 * k + lane;
+      ids[k] = i < b1 ? idx[i] : 0u;
+    }
+  }
+  // the id of entry i = b0 + 64k + lane
+  auto id_at = [&](int k, int64_t i) -> uint32_t {
+    if (in_regs) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int kk = 0; kk < kDispRegs; ++kk) v = kk == k ? ids[kk] : v;
+      return v;
+    }
+    return i < b1 ? idx[i] : 0u;
+  };
+  // lanes of this step sharing the lane's expert (ids >= E are dropped, never indexed)
+  auto step = [&](int k, int64_t i, uint32_t &e, bool &valid, uint64_t &same) {
+    const uint32_t ev = id_at(k, i);
+    valid = i < b1 && ev < (uint32_t)E;
+    e = valid ? ev : 0u;
+    same = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1u;
       const uint64_t m = __ballot(valid && bit);
       same &= bit ? m : ~m;
     }
-    const uint32_t wrank = (uint32_t)__popcll(same & lt);
-    if (valid && wrank == 0) hist[wave][e] = (uint32_t)__popcll(same);
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += 1024) {
-      uint32_t run = base[ee];
-      for (int w = 0; w < 16; ++w) {
-        const uint32_t c = hist[w][ee];
-        hist[w][ee] = run;
-        run += c;
-      }
-      base[ee] = run;
-    }
-    __syncthreads();
-    if (valid) rank[i] = hist[wave][e] + wrank;
-    __syncthreads();
-    for (int w = 0; w < 16; ++w)
-      for (int ee = tid; ee < E; ee += 1024) hist[w][ee] = 0;
-    __syncthreads();
-  }
-  if (tid == 0) {
-    uint32_t run = 0;
-    int na = 0;
-    for (int ee = 0; ee < E; ++ee) {
-      offsets[ee] = run;
-      if (base[ee] > 0 && active) active[na++] = ee;
-      run += base[ee];
-      base[ee] = offsets[ee];
-    }
-    offsets[E] = run;
-    if (n_active) *n_active = na;
+  };
+  for (int64_t i0 = b0; i0 < b1; i0 += 64) {  // pass 1: this wave's count per expert
+    uint32_t e;
+    bool valid;
+    uint64_t same;
+    step((int)((i0 - b0) >> 6), i0 + lane, e, valid, same);
+    if (valid && (same & lt) == 0) cnt[wave][e] += (uint32_t)__popcll(same);
   }
   __syncthreads();
-  for (int64_t i = tid; i < n; i += 1024) {
-    if (idx[i] >= (uint32_t)E) continue;
-    const uint32_t p = base[idx[i]] + rank[i];
-    perm[p] = (uint32_t)i;
-    if (inv) inv[i] = p;
+  for (int ee = tid; ee < E; ee += 1024) {  // wave w's first rank per expert; expert totals
+    uint32_t run = 0;
+    for (int w = 0; w < 16; ++w) {
+      const uint32_t c = cnt[w][ee];
+      cnt[w][ee] = run;
+      run += c;
+    }
+    base[ee] = run;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive prefix over the experts; the active ones in ascending order
+    constexpr int PER = kMaxExperts / 64;  // experts per lane
+    uint32_t tot[PER], sum = 0, nz = 0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int ee = PER * lane + k;
+      tot[k] = ee < E ? base[ee] : 0u;
+      sum += tot[k];
+      nz += tot[k] > 0 ? 1u : 0u;
+    }
+    uint32_t isum = sum, inz = nz;  // inclusive scans over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t a = __shfl_up(isum, o), b = __shfl_up(inz, o);
+      if (lane >= o) {
+        isum += a;
+        inz += b;
+      }
+    }
+    uint32_t run = isum - sum, na = inz - nz;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int ee = PER * lane + k;
+      if (ee < E) {
+        offsets[ee] = run;
+        base[ee] = run;
+        if (tot[k] > 0 && active) active[na++] = ee;
+        run += tot[k];
+      }
+    }
+    if (lane == 63) {
+      offsets[E] = isum;
+      if (n_active) *n_active = (int32_t)inz;
+    }
+  }
+  __syncthreads();
+  for (int64_t i0 = b0; i0 < b1; i0 += 64) {  // pass 2: positions in flat order
+    const int64_t i = i0 + lane;
+    uint32_t e;
+    bool valid;
+    uint64_t same;
+    step((int)((i0 - b0) >> 6), i, e, valid, same);
+    const uint32_t wrank = (uint32_t)__popcll(same & lt);
+    const uint32_t before = valid ? cnt[wave][e] : 0u;  // read by every lane before the leader adds
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const uint32_t p = base[e] + before + wrank;
+      perm[p] = (uint32_t)i;
+      if (inv) inv[i] = p;
+      if (wrank == 0) cnt[wave][e] = before + (uint32_t)__popcll(same);
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -338,21 +397,15 @@ __global__ void __launch_bounds__(256) k_quant_slots_q8(const float *__restrict_
   group8_quant_q8_block(h + blk * 32, q + blk * 32, d + blk, s16 + blk * 2, lane & 7);
 }
 
-// out[s, c] = sum over the token's slots in ascending expert id of w * y[slot, c]
-// (multiply, then add; transformer.rs:566-570).
-__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ y, Routing rt, int64_t S, int64_t d,
-                                                 float *__restrict__ out) {
-  const int64_t s = blockIdx.y;
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (s >= S || c >= d) return;
+// The token's slots in ascending slot position (== ascending expert id) and
+// their weights; every thread of the work-group computes the same.
+__device__ __forceinline__ int token_slots(const Routing &rt, int64_t s, uint32_t (&p)[16], float (&w)[16]) {
   const int k = rt.topk;
-  uint32_t p[16];
-  float w[16];
   for (int j = 0; j < k; ++j) {
     p[j] = rt.inv[s * k + j];
     w[j] = rt.wsel[s * k + j];
   }
-  for (int j = 1; j < k; ++j) {  // ascending slot position == ascending expert id
+  for (int j = 1; j < k; ++j) {
     const uint32_t pj = p[j];
     const float wj = w[j];
     int i = j - 1;
@@ -364,6 +417,46 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ y, Ro
     p[i + 1] = pj;
     w[i + 1] = wj;
   }
+  return k;
+}
+
+// k_combine on 16-byte groups: one token per blockIdx.y, columns 4c..4c+3
+// per thread (d % 4 == 0, y and out 16-byte aligned). Same arithmetic.
+__global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ y, Routing rt, int64_t s0, int64_t d,
+                                                  float *__restrict__ out) {
+  const int64_t s = s0 + blockIdx.y;
+  uint32_t p[16];
+  float w[16];
+  const int k = token_slots(rt, s, p, w);
+  const int64_t d4 = d / 4;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < d4; c += (int64_t)gridDim.x * 256) {
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < k; ++j) {
+      const float4 v = ((const float4 *)(y + (int64_t)p[j] * d))[c];
+      float4 t;
+      t.x = w[j] * v.x;
+      t.y = w[j] * v.y;
+      t.z = w[j] * v.z;
+      t.w = w[j] * v.w;
+      o.x = o.x + t.x;
+      o.y = o.y + t.y;
+      o.z = o.z + t.z;
+      o.w = o.w + t.w;
+    }
+    ((float4 *)(out + s * d))[c] = o;
+  }
+}
+
+// out[s, c] = sum over the token's slots in ascending expert id of w * y[slot, c]
+// (multiply, then add; transformer.rs:566-570).
+__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ y, Routing rt, int64_t S, int64_t s0,
+                                                 int64_t d, float *__restrict__ out) {
+  const int64_t s = s0 + blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s >= S || c >= d) return;
+  uint32_t p[16];
+  float w[16];
+  const int k = token_slots(rt, s, p, w);
   float o = 0.0f;
   for (int j = 0; j < k; ++j) {
     const float t = w[j] * y[(int64_t)p[j] * d + c];
@@ -654,8 +747,9 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots, int32_t n_expert, uint32_t *perm,
                            uint32_t *offsets, uint32_t *inv, int32_t *n_active, int32_t *active, uint32_t *rank_tmp) {
   if (n_expert > kMaxExperts || n_expert <= 0) return hipErrorInvalidValue;
+  (void)rank_tmp;
   KMOE_LAUNCH(k_dispatch, dim3(1), dim3(1024), 0, st, idx, n_slots, n_expert, perm, offsets, inv, n_active,
-                     active, rank_tmp);
+                     active);
   return hipGetLastError();
 }
 
@@ -681,8 +775,16 @@ hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t 
 hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int64_t s_rows, int64_t d, float *out) {
   if (s_rows == 0) return hipSuccess;
   if (rt.topk > 16) return hipErrorInvalidValue;
-  KMOE_LAUNCH(k_combine, dim3((unsigned)((d + 255) / 256), (unsigned)s_rows), dim3(256), 0, st, y, rt, s_rows,
-                     d, out);
+  const bool vec = d % 4 == 0 && (((uintptr_t)y | (uintptr_t)out) & 15) == 0;
+  for (int64_t s0 = 0; s0 < s_rows; s0 += 65535) {  // tokens along grid y, at most 65535 per launch
+    const unsigned ny = (unsigned)(s_rows - s0 < 65535 ? s_rows - s0 : 65535);
+    if (vec) {
+      const int64_t d4 = d / 4, gx = (d4 + 255) / 256 < 4 ? (d4 + 255) / 256 : 4;
+      KMOE_LAUNCH(k_combine4, dim3((unsigned)gx, ny), dim3(256), 0, st, y, rt, s0, d, out);
+    } else {
+      KMOE_LAUNCH(k_combine, dim3((unsigned)((d + 255) / 256), ny), dim3(256), 0, st, y, rt, s_rows, s0, d, out);
+    }
+  }
   return hipGetLastError();
 }
 

@@ -215,7 +215,11 @@ def test_matmul_host_is_matmul(ctx, orc, t, rows, cols, S, regime):
 
 @pytest.mark.parametrize("E,d,S", [(8, 4096, 1), (8, 4096, 3), (8, 4096, 4), (8, 1024, 16), (128, 2048, 1),
                                    (128, 2048, 7), (64, 2048, 9), (50, 1024, 6), (8, 1000, 5), (8, 1000, 2),
-                                   (8, 1004, 5), (8, 1004, 1)])
+                                   (8, 1004, 5), (8, 1004, 1),
+                                   # batches: 3x4-kernel and dot_f32 orders side by side (48-row tile
+                                   # remainders, S % 4 tokens, a last column chunk short of the staging width)
+                                   (128, 2048, 270), (50, 1000, 297), (200, 1024, 330), (128, 2048, 512),
+                                   (7, 512, 1031), (8, 1004, 400), (128, 2048, 70)])
 def test_router_logits_bit_exact(ctx, orc, E, d, S):
     """F32 router matmul in the reference's summation order for this S."""
     wr = orc.normal(E * d, E * d, 0.0, 0.02).reshape(E, d)
