@@ -53,9 +53,14 @@ typedef enum {
   KMOE_E_NOT_LOADED = -5   /* layer, router or expert not uploaded */
 } kmoe_status;
 
-/* ggml type ids, kestrel-gguf types.rs:67-107. Kernels exist for F32
- * (router), Q8_0, Q4_K and Q6_K; F16 for embedding rows. */
-enum { KMOE_F32 = 0, KMOE_F16 = 1, KMOE_Q8_0 = 8, KMOE_Q4_K = 12, KMOE_Q6_K = 14 };
+/* ggml type ids, kestrel-gguf types.rs:67-107. kmoe_matmul takes every type
+ * quant::matmul does (quant.rs:48-51): F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1,
+ * Q8_0, Q4_K, Q5_K, Q6_K. The expert tier, kmoe_matvec_q8 and the block-sum
+ * entry points take Q8_0, Q4_K and Q6_K; get_rows F32, F16 and those. */
+enum {
+  KMOE_F32 = 0, KMOE_F16 = 1, KMOE_Q4_0 = 2, KMOE_Q4_1 = 3, KMOE_Q5_0 = 6, KMOE_Q5_1 = 7, KMOE_Q8_0 = 8,
+  KMOE_Q4_K = 12, KMOE_Q5_K = 13, KMOE_Q6_K = 14, KMOE_BF16 = 30
+};
 
 /* Arithmetic regime of the quantized matmuls (quant.rs:229-328).
  * KMOE_REGIME_AVX2 (default): the reference on an AVX2+FMA host. A matmul
@@ -115,7 +120,11 @@ int kmoe_copy_d2h(kmoe_ctx *ctx, void *dst, const void *src_dev, size_t bytes); 
 /* quant::matmul (quant.rs:229): out[s*rows + r] = W[r] . x[s] for W of
  * ggml_type with shape [rows, cols], x [s_rows, cols] f32, out [s_rows, rows] f32.
  * w_len must be >= rows * bytes_for(cols) (quant.rs:233-234). The regime of
- * the context picks the arithmetic as the reference does for s_rows. */
+ * the context picks the arithmetic as the reference does for s_rows. F16,
+ * BF16, Q4_0, Q4_1, Q5_0, Q5_1 and Q5_K give the reference's bits in every
+ * regime: the f32 path dequantizes the rows into the workspace (rows * cols
+ * * 4 bytes) and sums in the reference's order; the int8 path replays the
+ * AVX2 dot of qdot's unpacked rows. */
 int kmoe_matmul(kmoe_ctx *ctx, int ggml_type, const void *w_dev, size_t w_len, int64_t rows, int64_t cols,
                 const float *x_dev, int64_t s_rows, float *out_dev);
 

@@ -26,20 +26,26 @@ using namespace kmoe;
 
 namespace {
 
+// GgmlType block geometry (types.rs:151-181) of the types quant::matmul accepts.
 int64_t block_size(int t) {
   switch (t) {
-    case KMOE_F32: return 1;
-    case KMOE_Q8_0: return 32;
-    case KMOE_Q4_K: return 256;
-    case KMOE_Q6_K: return 256;
+    case KMOE_F32: case KMOE_F16: case KMOE_BF16: return 1;
+    case KMOE_Q4_0: case KMOE_Q4_1: case KMOE_Q5_0: case KMOE_Q5_1: case KMOE_Q8_0: return 32;
+    case KMOE_Q4_K: case KMOE_Q5_K: case KMOE_Q6_K: return 256;
     default: return -1;
   }
 }
 int64_t type_size(int t) {
   switch (t) {
     case KMOE_F32: return 4;
+    case KMOE_F16: case KMOE_BF16: return 2;
+    case KMOE_Q4_0: return 18;
+    case KMOE_Q4_1: return 20;
+    case KMOE_Q5_0: return 22;
+    case KMOE_Q5_1: return 24;
     case KMOE_Q8_0: return 34;
     case KMOE_Q4_K: return 144;
+    case KMOE_Q5_K: return 176;
     case KMOE_Q6_K: return 210;
     default: return -1;
   }
@@ -519,7 +525,21 @@ int64_t sh_part_floats(int64_t Fs, int64_t d, int64_t S) {
 // reference's summation order; otherwise the context's regime picks the f32
 // GEMM or int8 activations (quantized into qr) and the int8 matvec.
 int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const float *x, int64_t s_rows,
-                float *out, const QRows &qr) {
+                float *out, const QRows &qr, float *wf = nullptr) {
+  if (xtype(t)) {  // F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q5_K
+    const int64_t rb = bytes_for(t, cols);
+    if (t == KMOE_F16 || t == KMOE_BF16 || !int_path(c->regime, s_rows)) {
+      // dequant_row into wf, then the F32 weights' path (quant.rs:242-260, :311-327)
+      if (!wf) return fail(c, KMOE_E_INVALID, "no f32 staging for type %d", t);
+      if (rows > (int64_t)INT32_MAX) return fail(c, KMOE_E_INVALID, "too many rows");
+      LAUNCH(c, "dequant_x", launch_dequant_x(c->stream, t, w, rows, cols, rb, wf));
+      LAUNCH(c, "matmul_f32_ordered", launch_router_logits(c->stream, wf, (int32_t)rows, cols, x, s_rows, out));
+      return KMOE_OK;
+    }
+    LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));  // quant.rs:282-310
+    LAUNCH(c, "matvec_unpacked", launch_mv_unpacked(c->stream, t, w, rows, cols, rb, qr.q, qr.d, qr.s, s_rows, out));
+    return KMOE_OK;
+  }
   if (t == KMOE_F32) {  // quant.rs:242 (s_rows >= 4) or :311-327 (dequant + quant::dot): summation order kept
     if (rows > (int64_t)INT32_MAX) return fail(c, KMOE_E_INVALID, "too many rows");
     LAUNCH(c, "matmul_f32_ordered",
@@ -798,18 +818,25 @@ int kmoe_matmul(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, i
   if (rows == 0 || s_rows == 0) return KMOE_OK;
   if (!w || !x || !out) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
-  if (t != KMOE_F32) {
+  const bool xt = xtype(t);
+  if (t != KMOE_F32 && !xt) {
     int rc = check_quant_shape(c, t, cols);
     if (rc) return rc;
   }
-  // int8 activations (or the f32 path's partial sums) go to the workspace
+  // int8 activations (or the f32 path's partial sums) go to the workspace;
+  // the other types' f32 path also stages the dequantized rows there
   const int64_t pf = gemm_f32_part_floats(rows, cols, 1, s_rows, s_rows);
+  const bool staged = xt && (t == KMOE_F16 || t == KMOE_BF16 || !int_path(c->regime, s_rows));
   size_t need = 0;
   carve_qrows(nullptr, s_rows, cols, &need, pf);
+  const size_t wf_off = need;
+  if (staged) need = wf_off + align_up((size_t)rows * (size_t)cols * 4);
   int rc = ensure_ws(c, need);
   if (rc) return rc;
-  QRows qr = carve_qrows(c->ws, s_rows, cols, &need, pf);
-  return matmul_core(c, t, (const uint8_t *)w, rows, cols, x, s_rows, out, qr);
+  size_t qn = 0;
+  QRows qr = carve_qrows(c->ws, s_rows, cols, &qn, pf);
+  return matmul_core(c, t, (const uint8_t *)w, rows, cols, x, s_rows, out, qr,
+                     staged ? (float *)(c->ws + wf_off) : nullptr);
 }
 
 int kmoe_matmul_host(kmoe_ctx *c, int t, const void *w, size_t w_len, int64_t rows, int64_t cols, const float *x,

@@ -243,6 +243,18 @@ hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots,
 hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t n_slots, int64_t cols,
                               const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
                               int32_t *sums);
+// ---- the other weight types of quant::matmul (kmoe_xtypes.hip): F16, BF16,
+// Q4_0, Q4_1, Q5_0, Q5_1, Q5_K (ggml type ids).
+bool xtype(int t);
+// out [rows, cols] f32 = dequant_row of every row (quantized types: cols % 32 == 0).
+hipError_t launch_dequant_x(hipStream_t st, int t, const uint8_t *w, int64_t rows, int64_t cols, int64_t row_bytes,
+                            float *out);
+// out [s_rows, rows] = the reference's int8 dot of each row with each Q8 row
+// (the quantized types except F16/BF16; cols % 32 == 0).
+hipError_t launch_mv_unpacked(hipStream_t st, int t, const uint8_t *w, int64_t rows, int64_t cols,
+                              int64_t row_bytes, const int8_t *xq, const float *xd, const int32_t *s16, int64_t s_rows,
+                              float *out);
+
 // ---- shared expert (kmoe_shared.hip)
 // g = g / (1 + exp(-g)) * u over n elements.
 hipError_t launch_swiglu(hipStream_t st, float *g, const float *u, int64_t n);

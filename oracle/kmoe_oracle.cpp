@@ -244,7 +244,10 @@ inline __m256i mul_i8_i8(__m256i w, __m256i x) {  // avx2.rs:37-41
 inline __m256i load(const void *p) { return _mm256_loadu_si256((const __m256i *)p); }
 
 bool has_fused_k(int t) { return t == ORC_Q4_K || t == ORC_Q6_K; }             // qdot.rs:371-378
-bool qdot_supports(int t) { return t == ORC_Q8_0 || t == ORC_Q4_0 || t == ORC_Q4_K || t == ORC_Q6_K; }  // qdot.rs:60-63 (types built here)
+bool qdot_supports(int t) {  // qdot.rs:60-63
+  return t == ORC_Q8_0 || t == ORC_Q4_0 || t == ORC_Q4_1 || t == ORC_Q5_0 || t == ORC_Q5_1 || t == ORC_Q4_K ||
+         t == ORC_Q5_K || t == ORC_Q6_K;
+}
 
 }  // namespace
 
@@ -255,8 +258,8 @@ int orc_hw_threads(void) { return (int)std::max(1u, std::thread::hardware_concur
 int64_t orc_block_size(int t) {  // types.rs:151-160
   switch (t) {
     case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
-    case ORC_Q4_0: case ORC_Q8_0: return 32;
-    case ORC_Q4_K: case ORC_Q6_K: return 256;
+    case ORC_Q4_0: case ORC_Q4_1: case ORC_Q5_0: case ORC_Q5_1: case ORC_Q8_0: return 32;
+    case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
     default: return -1;
   }
 }
@@ -265,8 +268,12 @@ int64_t orc_type_size(int t) {  // types.rs:163-181
     case ORC_F32: return 4;
     case ORC_F16: case ORC_BF16: return 2;
     case ORC_Q4_0: return 18;
+    case ORC_Q4_1: return 20;
+    case ORC_Q5_0: return 22;
+    case ORC_Q5_1: return 24;
     case ORC_Q8_0: return 34;
     case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
     default: return -1;
   }
@@ -487,6 +494,67 @@ int orc_dequant_row(int t, const uint8_t *src, float *y, size_t n) {
         }
       }
       return 0;
+    case ORC_Q4_1:  // quant.rs:100-111
+      for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + 20 * b;
+        float d = f16at(blk), m = f16at(blk + 2);
+        const uint8_t *qs = blk + 4;
+        for (int j = 0; j < 16; ++j) {
+          y[32 * b + j] = (float)(qs[j] & 0xF) * d + m;
+          y[32 * b + j + 16] = (float)(qs[j] >> 4) * d + m;
+        }
+      }
+      return 0;
+    case ORC_Q5_0:  // quant.rs:112-123
+      for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + 22 * b;
+        float d = f16at(blk);
+        uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+        const uint8_t *qs = blk + 6;
+        for (int j = 0; j < 16; ++j) {
+          uint8_t h0 = (uint8_t)(((qh >> j) << 4) & 0x10), h1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+          y[32 * b + j] = (float)((int)((qs[j] & 0xF) | h0) - 16) * d;
+          y[32 * b + j + 16] = (float)((int)((qs[j] >> 4) | h1) - 16) * d;
+        }
+      }
+      return 0;
+    case ORC_Q5_1:  // quant.rs:124-137
+      for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + 24 * b;
+        float d = f16at(blk), m = f16at(blk + 2);
+        uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) | ((uint32_t)blk[7] << 24);
+        const uint8_t *qs = blk + 8;
+        for (int j = 0; j < 16; ++j) {
+          uint8_t h0 = (uint8_t)(((qh >> j) << 4) & 0x10), h1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+          y[32 * b + j] = (float)((qs[j] & 0xF) | h0) * d + m;
+          y[32 * b + j + 16] = (float)((qs[j] >> 4) | h1) * d + m;
+        }
+      }
+      return 0;
+    case ORC_Q5_K:  // quant.rs:156-179
+      for (size_t b = 0; b < n / 256; ++b) {
+        const uint8_t *blk = src + 176 * b;
+        float d = f16at(blk), dmin = f16at(blk + 2);
+        const uint8_t *scales = blk + 4, *qh = blk + 16, *ql = blk + 48;
+        float *yy = y + 256 * b;
+        uint8_t u1 = 1, u2 = 2;
+        for (int k = 0; k < 4; ++k) {
+          uint8_t s1, m1, s2, m2;
+          scale_min_k4(2 * k, scales, s1, m1);
+          scale_min_k4(2 * k + 1, scales, s2, m2);
+          float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+          float d2 = d * (float)s2, mm2 = dmin * (float)m2;
+          const uint8_t *q = ql + 32 * k;
+          for (int l = 0; l < 32; ++l) {
+            int hi1 = (qh[l] & u1) ? 16 : 0, hi2 = (qh[l] & u2) ? 16 : 0;
+            yy[64 * k + l] = d1 * (float)((q[l] & 0xF) + hi1) - mm1;
+            yy[64 * k + l + 32] = d2 * (float)((q[l] >> 4) + hi2) - mm2;
+          }
+          u1 = (uint8_t)(u1 << 2);
+          u2 = (uint8_t)(u2 << 2);
+        }
+      }
+      return 0;
     case ORC_Q4_K:  // quant.rs:138-155
       for (size_t b = 0; b < n / 256; ++b) {
         const uint8_t *blk = src + 144 * b;
@@ -601,17 +669,61 @@ int orc_unpack(int t, const uint8_t *w, size_t n, int8_t *q, float *sc, float *m
         mn[2 * b + 1] = 0.0f;
       }
       return 0;
+    case ORC_Q4_1:  // qdot.rs:93-108 (bias 0, min = -m)
+      for (size_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = w + 20 * b;
+        float d = f16at(blk), m = -f16at(blk + 2);
+        const uint8_t *qs = blk + 4;
+        for (int j = 0; j < 16; ++j) {
+          q[32 * b + j] = (int8_t)(qs[j] & 0xF);
+          q[32 * b + j + 16] = (int8_t)(qs[j] >> 4);
+        }
+        sc[2 * b] = d;
+        sc[2 * b + 1] = d;
+        mn[2 * b] = m;
+        mn[2 * b + 1] = m;
+      }
+      return 0;
+    case ORC_Q5_0:
+    case ORC_Q5_1:  // qdot.rs:109-128 (Q5_0: bias 16, min 0; Q5_1: bias 0, min = -m)
+      for (size_t b = 0; b < n / 32; ++b) {
+        const size_t bs = t == ORC_Q5_0 ? 22 : 24, off = t == ORC_Q5_0 ? 2 : 4;
+        const uint8_t *blk = w + bs * b;
+        float d = f16at(blk);
+        const int8_t bias = t == ORC_Q5_0 ? 16 : 0;
+        float m = t == ORC_Q5_0 ? 0.0f : -f16at(blk + 2);
+        uint32_t qh = (uint32_t)blk[off] | ((uint32_t)blk[off + 1] << 8) | ((uint32_t)blk[off + 2] << 16) |
+                      ((uint32_t)blk[off + 3] << 24);
+        const uint8_t *qs = blk + off + 4;
+        for (int j = 0; j < 16; ++j) {
+          uint8_t h0 = (uint8_t)(((qh >> j) << 4) & 0x10), h1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+          q[32 * b + j] = (int8_t)((int8_t)((qs[j] & 0xF) | h0) - bias);
+          q[32 * b + j + 16] = (int8_t)((int8_t)((qs[j] >> 4) | h1) - bias);
+        }
+        sc[2 * b] = d;
+        sc[2 * b + 1] = d;
+        mn[2 * b] = m;
+        mn[2 * b + 1] = m;
+      }
+      return 0;
     case ORC_Q4_K:
+    case ORC_Q5_K:  // qdot.rs:129-153
       for (size_t sb = 0; sb < n / 256; ++sb) {
-        const uint8_t *blk = w + 144 * sb;
+        const bool k5 = t == ORC_Q5_K;
+        const uint8_t *blk = w + (k5 ? 176 : 144) * sb;
         float d = f16at(blk), dmin = f16at(blk + 2);
-        const uint8_t *scales = blk + 4, *qs = blk + 16;
+        const uint8_t *scales = blk + 4, *qh = blk + 16, *qs = blk + (k5 ? 48 : 16);
         for (int k = 0; k < 4; ++k) {
           const uint8_t *src = qs + 32 * k;
           size_t base = sb * 256 + k * 64;
           for (int j = 0; j < 32; ++j) {
-            q[base + j] = (int8_t)(src[j] & 0xF);
-            q[base + 32 + j] = (int8_t)(src[j] >> 4);
+            uint8_t lo = src[j] & 0xF, hi = src[j] >> 4;
+            if (k5) {
+              lo = (uint8_t)(lo | (((qh[j] >> (2 * k)) & 1) << 4));
+              hi = (uint8_t)(hi | (((qh[j] >> (2 * k + 1)) & 1) << 4));
+            }
+            q[base + j] = (int8_t)lo;
+            q[base + 32 + j] = (int8_t)hi;
           }
           uint8_t s0, m0, s1, m1;
           scale_min_k4(2 * k, scales, s0, m0);
@@ -1112,7 +1224,12 @@ int orc_matmul(int t, const uint8_t *w, size_t w_len, size_t rows, size_t cols, 
             case ORC_Q8_0: v = orc_dot_q8_0(wr, cols, aq, ad); break;
             case ORC_Q4_0: v = orc_dot_q4_0(wr, cols, aq, ad); break;
             case ORC_Q4_K: v = orc_dot_q4_k(wr, cols, aq, ad, as); break;
-            default: v = 0.0f;
+            default: {  // qdot::unpack + dot (avx2 dot_unpacked), quant.rs:295-302
+              std::vector<int8_t> uq(cols);
+              std::vector<float> usc(cols / 16), umn(cols / 16);
+              orc_unpack(t, wr, cols, uq.data(), usc.data(), umn.data());
+              v = orc_dot_unpacked_avx2(uq.data(), usc.data(), umn.data(), cols, aq, ad, as);
+            }
           }
           res[(r - r0) * s_rows + s] = v;
         }

@@ -12,7 +12,10 @@
  * fuses it. Every function cites the reference file:line it follows.
  *
  * Pinning status (what checks each function; see tests/test_oracle.py):
- *   - dequant_row Q8_0/Q4_0: known values from quant.rs:375-394.
+ *   - dequant_row Q8_0/Q4_0: known values from quant.rs:375-394; Q4_1, Q5_0,
+ *     Q5_1, Q5_K: hand-built blocks whose values follow from the formats.
+ *   - unpack of every qdot type == dequant within 1e-5 (qdot.rs:301-315), the
+ *     unpacked dot against the float dot (qdot.rs:318-334).
  *   - bytes_for / block geometry: types.rs:300-307 (Q4_K 512 -> 288 B).
  *   - unpack == dequant (qdot.rs:301-315), fused == unpacked (avx2.rs:184-223),
  *     Q8_K kernels vs f64 dequantized math (avx2.rs:425-460),
@@ -37,7 +40,10 @@ extern "C" {
 #endif
 
 /* ggml type ids, kestrel-gguf types.rs:67-107 */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_BF16 = 30 };
+enum {
+  ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_Q8_0 = 8, ORC_Q4_K = 12,
+  ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_BF16 = 30
+};
 
 /* Arithmetic regimes of quant::matmul (quant.rs:229-328).
  *  ORC_REGIME_AVX2 : the reference on an AVX2+FMA host: s_rows>=4 -> f32 GEMM,

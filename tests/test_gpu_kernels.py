@@ -283,3 +283,57 @@ def test_dispatch_all_to_one_expert(ctx, orc):
     perm, off = ctx.dispatch(dev(idx.view(np.int32)), 4)
     assert np.array_equal(host(perm).view(np.uint32), np.arange(3000, dtype=np.uint32))
     assert host(off).tolist() == [0, 3000, 3000, 3000, 3000]
+
+
+# ------------------------------------------------- the other quant::matmul types
+_XT = {"Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q5_K": 13, "F16": 1, "BF16": 30}
+
+
+def _xt_weights(orc, t, rows, cols, seed):
+    """qdot.rs:275-299's generator (xorshift32 bytes, the f16 scale and min
+    fields set to 0.002); F16 / BF16 rows of N(0, 0.02)."""
+    if t in (1, 30):
+        v = orc.normal(seed, rows * cols, 0.0, 0.02)
+        return v.astype(np.float16).view(np.uint8) if t == 1 else (v.view(np.uint32) >> 16).astype(np.uint16).view(
+            np.uint8)
+    w = orc.xorshift_bytes(seed, orc.bytes_for(t, rows * cols)).copy()
+    blk = w.reshape(-1, orc.type_size(t))
+    h = orc.f16_bits(0.002)
+    for o in {2: [0], 6: [0], 3: [0, 2], 7: [0, 2], 13: [0, 2]}[t]:
+        blk[:, o] = h & 0xFF
+        blk[:, o + 1] = h >> 8
+    return w
+
+
+@pytest.mark.parametrize("name", list(_XT))
+@pytest.mark.parametrize("regime", [0, 1, 2])
+def test_matmul_other_types_bit_exact(ctx, orc, name, regime):
+    """quant::matmul over F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1 and Q5_K weights:
+    the reference's bits in every regime and row count (dequantize + the f32
+    orders; the AVX2 dot of the unpacked rows with Q8 activations)."""
+    t = _XT[name]
+    rows, cols = 96, 1024
+    w = _xt_weights(orc, t, rows, cols, 17 + t)
+    ctx.set_regime(regime)
+    try:
+        for S in (1, 3, 5, 17):
+            x = orc.normal(40 + S + t, S * cols).reshape(S, cols)
+            out = host(ctx.matmul(t, dev(w), rows, cols, dev(x)))
+            ref = orc.matmul(t, w, rows, cols, x, regime)
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (name, regime, S)
+    finally:
+        ctx.set_regime(0)
+
+
+def test_matmul_other_types_odd_widths_and_host_seam(ctx, orc):
+    """F16 rows of 1000 columns (not a multiple of 8: quant::dot order at
+    every S) and Q5_K through the host-slice entry point."""
+    w = _xt_weights(orc, 1, 40, 1000, 5)
+    for S in (2, 6):
+        x = orc.normal(50 + S, S * 1000).reshape(S, 1000)
+        out = host(ctx.matmul(1, dev(w), 40, 1000, dev(x)))
+        assert np.array_equal(out.view(np.uint32), orc.matmul(1, w, 40, 1000, x).view(np.uint32))
+    w = _xt_weights(orc, 13, 64, 512, 6)
+    x = orc.normal(61, 2 * 512).reshape(2, 512)
+    a = ctx.matmul_host(13, w, 64, 512, x)
+    assert np.array_equal(a.view(np.uint32), orc.matmul(13, w, 64, 512, x).view(np.uint32))

@@ -605,8 +605,8 @@ def test_errors_map_to_status_codes(ctx):
     with pytest.raises(KmoeError) as e:  # weight buffer smaller than rows x row_bytes (quant.rs:233-234)
         ctx.matmul(Q4_K, w, 4, 256, x)
     assert e.value.status == -1
-    with pytest.raises(KmoeError) as e:  # type without a kernel (Q5_K)
-        ctx.matmul(13, w, 4, 256, x)
+    with pytest.raises(KmoeError) as e:  # a type quant::matmul does not take either (Q3_K, quant.rs:48-51)
+        ctx.matmul(11, w, 4, 256, x)
     assert e.value.status == -2
     with pytest.raises(KmoeError) as e:  # layer never created
         ctx.moe_ffn(77, x)

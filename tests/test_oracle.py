@@ -9,14 +9,16 @@ oracle's formula.
 import numpy as np
 import pytest
 
-from oracle.pyoracle import F32, Q4_0, Q4_K, Q6_K, Q8_0, REGIME_AVX2, REGIME_EXACT, REGIME_INT8
+from oracle.pyoracle import (BF16, F16, F32, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, REGIME_AVX2,
+                              REGIME_EXACT, REGIME_INT8)
 
 
 def _blocks(orc, t, n, seed, scale):
     """qdot.rs:275-299 / avx2.rs:198-208: xorshift32 bytes, f16 scales overwritten."""
     w = orc.xorshift_bytes(seed, orc.bytes_for(t, n)).copy()
     bs = orc.type_size(t)
-    offs = {Q8_0: [0], Q4_0: [0], Q4_K: [0, 2], Q6_K: [208]}[t]
+    offs = {Q8_0: [0], Q4_0: [0], Q5_0: [0], Q4_1: [0, 2], Q5_1: [0, 2], Q4_K: [0, 2], Q5_K: [0, 2],
+            Q6_K: [208]}[t]
     h = orc.f16_bits(scale)
     blk = w.reshape(-1, bs)
     for o in offs:
@@ -101,7 +103,64 @@ def test_matmul_matches_naive(orc):
     assert np.abs(out - e).max() < 1e-3
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K])
+def _f16le(v):
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def test_q4_1_q5_0_q5_1_known_values(orc):
+    """Hand-built 32-blocks; element j (< 16) is the low nibble of qs[j], element
+    j + 16 its high nibble; Q5 types take bit j of the 32-bit qh word as bit 4
+    of element j (ggml's block_q5_0 / block_q5_1)."""
+    j = np.arange(16)
+    qs = (j | ((15 - j) << 4)).astype(np.uint8)
+    nib = np.concatenate([j, 15 - j]).astype(np.float64)
+    # Q4_1: d = 0.5, m = -1.0 -> q * d + m
+    b = np.concatenate([_f16le(0.5), _f16le(-1.0), qs])
+    assert np.array_equal(orc.dequant(Q4_1, b, 32), (nib * 0.5 - 1.0).astype(np.float32))
+    qh = 0b1010_0101_1100_0011_0000_1111_1001_0110
+    hbit = np.array([(qh >> i) & 1 for i in range(32)], np.float64)
+    qhb = np.array([qh], np.uint32).view(np.uint8)
+    # Q5_0: d = 0.25 -> ((nibble | bit << 4) - 16) * d
+    b = np.concatenate([_f16le(0.25), qhb, qs])
+    assert np.array_equal(orc.dequant(Q5_0, b, 32), ((nib + 16 * hbit - 16) * 0.25).astype(np.float32))
+    # Q5_1: d = 0.125, m = 2.0 -> (nibble | bit << 4) * d + m
+    b = np.concatenate([_f16le(0.125), _f16le(2.0), qhb, qs])
+    assert np.array_equal(orc.dequant(Q5_1, b, 32), ((nib + 16 * hbit) * 0.125 + 2.0).astype(np.float32))
+
+
+def test_q5_k_known_values(orc):
+    """Hand-built Q5_K superblock (ggml's block_q5_K: d, dmin, 12 scale bytes,
+    qh[32], qs[128]). Sub-blocks 2k and 2k+1 take the low and high nibbles of
+    qs[32k + l] and bits 2k and 2k+1 of qh[l]; sub-block j has scale 2j+1
+    and min j, packed into the 12 scale bytes as scale_min_k4 reads them
+    (quant.rs:54-61)."""
+    d, dmin = 0.5, 0.25
+    sc = np.array([1, 3, 5, 7, 9, 11, 13, 15], np.uint8)  # sub-block j: scale j*2+1 (sub-blocks 0..7)
+    mn = np.array([0, 1, 2, 3, 4, 5, 6, 7], np.uint8)
+    scales = np.zeros(12, np.uint8)
+    scales[0:4] = sc[0:4]  # j < 4: scale = q[j] & 63, min = q[j + 4] & 63
+    scales[4:8] = mn[0:4]
+    scales[8:12] = (sc[4:8] & 0xF) | ((mn[4:8] & 0xF) << 4)  # j >= 4: low 4 bits in q[j + 4]
+    scales[0:4] |= (sc[4:8] >> 4) << 6  # high 2 bits in the top bits of q[j - 4] / q[j]
+    scales[4:8] |= (mn[4:8] >> 4) << 6
+    l = np.arange(32)
+    qs = np.concatenate([((l + k) & 0xF) | (((31 - l - k) & 0xF) << 4) for k in range(4)]).astype(np.uint8)
+    qh = ((l * 37 + 11) & 0xFF).astype(np.uint8)
+    b = np.concatenate([_f16le(d), _f16le(dmin), scales, qh, qs])
+    assert b.size == 176
+    exp = np.empty(256)
+    for k in range(4):
+        for half, s in ((0, 2 * k), (1, 2 * k + 1)):
+            nib = ((l + k) & 0xF) if half == 0 else ((31 - l - k) & 0xF)
+            hi = (qh >> s) & 1
+            exp[64 * k + 32 * half + l] = (d * sc[s]) * (nib + 16 * hi) - dmin * mn[s]
+    got = orc.dequant(Q5_K, b, 256)
+    assert np.allclose(got, exp.astype(np.float32), rtol=0, atol=1e-6)
+    q, usc, umn = orc.unpack(Q5_K, b, 256)
+    assert q.min() >= 0 and q.max() <= 31
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K])
 def test_unpack_matches_dequantization_exactly(orc, t):
     # qdot.rs:301-315
     n = 1024
@@ -113,7 +172,7 @@ def test_unpack_matches_dequantization_exactly(orc, t):
     assert np.all(np.abs(v - wf) <= 1e-5 * np.maximum(np.abs(wf), 1.0))
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K, Q5_1, Q4_1, Q5_0, Q5_K])
 def test_dot_close_to_float(orc, t):
     # qdot.rs:317-333
     n = 1024
@@ -270,12 +329,21 @@ def test_quantizers_round_trip(orc, t, n):
     assert np.sqrt(np.mean((x - y) ** 2)) / np.sqrt(np.mean(x ** 2)) < tol
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q4_0, Q4_1, Q5_0, Q5_1, Q5_K, F16, BF16])
 def test_matmul_regimes(orc, t):
-    """quant.rs:242/262/282: S>=4 is f32-exact; S<4 carries Q8_K activation error."""
+    """quant.rs:242/262/282/311: S>=4 is f32-exact; S<4 carries the int8
+    activations' error (Q8_K or Q8 rows), except F16/BF16 weights, which take
+    dequantize + quant::dot at every S."""
     rows, cols = 64, 1024
     rb = orc.bytes_for(t, cols)
-    w = orc.quantize(t, orc.normal(21, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    if t in (F16, BF16):
+        wf32 = orc.normal(21, rows * cols, 0.0, 0.02)
+        w = wf32.astype(np.float16).view(np.uint8) if t == F16 else \
+            (wf32.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+    elif t in (Q4_K, Q6_K):
+        w = orc.quantize(t, orc.normal(21, rows * cols, 0.0, 0.02).reshape(rows, cols))
+    else:
+        w = _blocks(orc, t, rows * cols, 21, 0.002)
     wf = np.stack([orc.dequant(t, w[r * rb:(r + 1) * rb], cols) for r in range(rows)]).astype(np.float64)
     for S in (1, 3, 4, 7):
         x = orc.normal(30 + S, S * cols).reshape(S, cols)
@@ -283,7 +351,7 @@ def test_matmul_regimes(orc, t):
         for regime in (REGIME_AVX2, REGIME_INT8, REGIME_EXACT):
             out = orc.matmul(t, w, rows, cols, x, regime)
             rel = np.linalg.norm(out - e) / np.linalg.norm(e)
-            exact = (regime == REGIME_EXACT) or (regime == REGIME_AVX2 and S >= 4)
+            exact = (regime == REGIME_EXACT) or (regime == REGIME_AVX2 and S >= 4) or t in (F16, BF16)
             assert rel < (1e-6 if exact else 2e-2), (S, regime, rel)
 
 
