@@ -350,7 +350,9 @@ __device__ __forceinline__ int q80_int(const Q80W &w, const int8_t *xq_b, float 
   return p;
 }
 
-template <int TYPE, int LPR, int NT, int MODE>
+// DBG: the grouped modes also add their per-block integers into a.dbg (the
+// capture of kmoe_moe_ffn_dbg).
+template <int TYPE, int LPR, int NT, int MODE, bool DBG>
 __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int RPW = 64 / LPR;
@@ -442,7 +444,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                   }
                 } else {
                   const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + sb;  // grouped modes' capture
-                  if (a.dbg.s[0]) {
+                  if (DBG && a.dbg.s[0]) {
                     atomicAdd(a.dbg.s[0] + o, si);
                     atomicAdd(a.dbg.m[0] + o, mi);
                   }
@@ -451,7 +453,7 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                   if constexpr (MODE == M_GATE_UP) {
                     const float d1 = f16_bits_to_f32(w1.hdr.x), m1 = f16_bits_to_f32(w1.hdr.x >> 16);
                     q4k_ints(w1, k, xq_sb, xbs_sb, si, mi);
-                    if (a.dbg.s[1]) {
+                    if (DBG && a.dbg.s[1]) {
                       atomicAdd(a.dbg.s[1] + o, si);
                       atomicAdd(a.dbg.m[1] + o, mi);
                     }
@@ -497,14 +499,14 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                   }
                 } else {
                   const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + sb;  // grouped modes' capture
-                  if (a.dbg.s[0]) {
+                  if (DBG && a.dbg.s[0]) {
                     atomicAdd(a.dbg.s[0] + o, si);
                     atomicAdd(a.dbg.m[0] + o, oi);
                   }
                   acc0[tk] = fmaf(d0 * xd, (float)(si - 32 * oi), acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
                     ints6(w1, x0, x1, x2, x3, bs, si, oi);
-                    if (a.dbg.s[1]) {
+                    if (DBG && a.dbg.s[1]) {
                       atomicAdd(a.dbg.s[1] + o, si);
                       atomicAdd(a.dbg.m[1] + o, oi);
                     }
@@ -529,12 +531,12 @@ __global__ void __launch_bounds__(256) k_matvec_int(MvArgs a) {
                   a.isumi[((int64_t)(c0 + tk) * rows + r) * nblk + t] = p;
                 } else {
                   const int64_t o = ((p0 + c0 + tk) * rows + r) * nblk + t;  // grouped modes' capture
-                  if (a.dbg.s[0]) atomicAdd(a.dbg.s[0] + o, p);
+                  if (DBG && a.dbg.s[0]) atomicAdd(a.dbg.s[0] + o, p);
                   acc0[tk] = fmaf(dw * xd, (float)p, acc0[tk]);
                   if constexpr (MODE == M_GATE_UP) {
                     float dw1;
                     const int p1 = q80_int(w1, xq_b, dw1);
-                    if (a.dbg.s[1]) atomicAdd(a.dbg.s[1] + o, p1);
+                    if (DBG && a.dbg.s[1]) atomicAdd(a.dbg.s[1] + o, p1);
                     acc1[tk] = fmaf(dw1 * xd, (float)p1, acc1[tk]);
                   }
                 }
@@ -758,7 +760,9 @@ __device__ __forceinline__ void mv_select(const DecSelect &q, int lane, int32_t 
     publish_selection(sj, wj, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
 }
 
-template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
+// DBG: the grouped modes also add their per-block integers into a.dbg (the
+// capture of kmoe_moe_ffn_dbg); the product instantiation carries none of it.
+template <int TYPE, int LPR, int TPLMAX, int RU, int MODE, bool DBG>
 __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   constexpr int RPW = 64 / LPR;
   constexpr int RB = 4 * RPW * RU;  // rows per block-task
@@ -839,10 +843,15 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
               const int64_t r = r0 + (int64_t)u * RPW;
-              const int64_t o = (p * rows + r) * nblk;
-              if (r < rows)
-                acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u], a.dbg.s[0] ? a.dbg.s[0] + o : nullptr,
-                                        a.dbg.m[0] ? a.dbg.m[0] + o : nullptr);
+              if (r < rows) {
+                if constexpr (DBG) {
+                  const int64_t o = (p * rows + r) * nblk;
+                  acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u], a.dbg.s[0] ? a.dbg.s[0] + o : nullptr,
+                                          a.dbg.m[0] ? a.dbg.m[0] + o : nullptr);
+                } else {
+                  acc[u] = task_dot<TYPE>(w[u], t, act[i], acc[u]);
+                }
+              }
             }
           }
         }
@@ -883,7 +892,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
             if (r < rows) {
-              if constexpr (MODE == M_GATE_UP) {
+              if constexpr (MODE == M_GATE_UP && DBG) {
                 const int64_t o = (p0 * rows + r) * nblk;
                 const BlockDbg &g = a.dbg;
                 acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u], g.s[0] ? g.s[0] + o : nullptr,
@@ -892,6 +901,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
                                          g.m[1] ? g.m[1] + o : nullptr);
               } else {
                 acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u]);
+                if constexpr (MODE == M_GATE_UP) acc1[u] = task_dot<TYPE>(w1[u], t, act[i], acc1[u]);
               }
             }
           }
@@ -1147,7 +1157,13 @@ hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_task
     grid = (max_tasks + per - 1) / per;
   }
   if (grid < 1) grid = 1;
-  KMOE_LAUNCH((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
+  if constexpr (MODE == M_GATE_UP || MODE == M_DOWN_COMBINE) {
+    if (a.dbg.s[0] || a.dbg.s[1]) {
+      KMOE_LAUNCH((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE, true>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
+      return hipGetLastError();
+    }
+  }
+  KMOE_LAUNCH((k_mv_reg<TYPE, LPR, TPLMAX, RU, MODE, false>), dim3((unsigned)grid), dim3(256), 0, st, a, tpl);
   return hipGetLastError();
 }
 
@@ -1177,7 +1193,13 @@ template <int TYPE, int LPR, int NT, int MODE>
 hipError_t launch_one(hipStream_t st, const MvArgs &a, dim3 grid) {
   const ActLayout<TYPE> L(a.cols);
   const size_t shmem = (size_t)NT * L.total;
-  KMOE_LAUNCH((k_matvec_int<TYPE, LPR, NT, MODE>), grid, dim3(256), shmem, st, a);
+  if constexpr (MODE == M_GATE_UP || MODE == M_DOWN) {
+    if (a.dbg.s[0] || a.dbg.s[1]) {
+      KMOE_LAUNCH((k_matvec_int<TYPE, LPR, NT, MODE, true>), grid, dim3(256), shmem, st, a);
+      return hipGetLastError();
+    }
+  }
+  KMOE_LAUNCH((k_matvec_int<TYPE, LPR, NT, MODE, false>), grid, dim3(256), shmem, st, a);
   return hipGetLastError();
 }
 
