@@ -1086,6 +1086,111 @@ __global__ void __launch_bounds__(256) k_down_splitk(MvArgs a, int rb_rows) {
   if (threadIdx.x < nr) a.out[r0 + threadIdx.x] = outv[threadIdx.x];
 }
 
+// Single-token down + combine with a ring of NS register sets: the weight loads
+// of items i+1 .. i+NS-1 are in flight while item i is computed, and item
+// i+NS's loads go out as soon as item i has been computed. Items are (slot,
+// RU-row batch) pairs in ascending expert id, at most NIT of them (the host
+// checks topk * ceil(rb_rows / RU) <= NIT and topk <= 2); the loop over them
+// is unrolled, so every load is unconditional (clamped to the last item) and
+// the compiler's wait counts stay exact. The routing weights come from two
+// direct loads issued before the weight loads (wsel[j] and the slot inv[j] of
+// selection j), so no wait for them sits between weight loads. Same
+// arithmetic and combine order as k_down_splitk: y per row is the sum of the
+// four wave partials ((w0 + w1) + w2) + w3, out = (0 + wgt_0*y_0) + wgt_1*y_1.
+template <int TYPE, int RU, int NIT, int NS, bool DBG>
+__global__ void __launch_bounds__(256) k_down_ring(MvArgs a, int rb_rows) {
+  __shared__ float part[4][kSplitRbMax];
+  __shared__ float outv[kSplitRbMax];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
+  const int64_t xs_stride = cols / 16;
+  const int tpw = (ntasks + 3) / 4;  // tasks per wave (<= 64)
+  const int64_t r0 = (int64_t)blockIdx.x * rb_rows;
+  const int nr = (int)(rows - r0 < rb_rows ? rows - r0 : rb_rows);
+  if (nr <= 0) return;
+  if (threadIdx.x < kSplitRbMax) outv[threadIdx.x] = 0.0f;
+  const int tk = wave * tpw + lane;
+  const bool tv = lane < tpw && tk < ntasks;
+  const int tc = min(tk, ntasks - 1);
+  const int na = a.rt.topk;           // one token: topk distinct experts, slot p = p-th smallest id
+  const int nb = (nr + RU - 1) / RU;  // row batches per expert
+  const int items = na * nb;
+  // selection j's expert slot and weight (lanes j < topk)
+  const int jl = lane < na ? lane : 0;
+  const int32_t e_l = a.rt.active[jl];
+  const uint32_t inv_l = a.rt.inv[jl];
+  const float w_l = a.rt.wsel[jl];
+  const int e0 = __builtin_amdgcn_readfirstlane(e_l);
+  const int e1 = __shfl(e_l, na > 1 ? 1 : 0);
+  const uint8_t *W0 = a.tier.base + (int64_t)e0 * a.tier.stride + a.tier.off[2];
+  const uint8_t *W1 = a.tier.base + (int64_t)__builtin_amdgcn_readfirstlane(e1) * a.tier.stride + a.tier.off[2];
+  ActSlice<TYPE> act0, act1;
+  act_load<TYPE>(act0, a.xq, a.xd, a.xbs, tc);
+  const int p1 = na > 1 ? 1 : 0;
+  act_load<TYPE>(act1, a.xq + p1 * cols, a.xd + p1 * nblk, a.xbs + p1 * xs_stride, tc);
+  WTask<TYPE, true> w[NS][RU];
+  auto issue = [&](int it, WTask<TYPE, true> (&ws)[RU]) {
+    it = min(it, items - 1);
+    const int ia = it / nb;
+    const uint8_t *W = ia == 0 ? W0 : W1;
+    const int rr = (it - ia * nb) * RU;
+#pragma unroll
+    for (int u = 0; u < RU; ++u) w_load<TYPE, true>(ws[u], W + (r0 + min(rr + u, nr - 1)) * row_bytes, tc, nblk);
+  };
+#pragma unroll
+  for (int i = 0; i < NS; ++i) issue(i, w[i]);
+  // the weights of slots 0 and 1: slot p's selection j has inv[j] == p
+  const uint64_t m0 = __ballot(lane < na && inv_l == 0u), m1 = __ballot(lane < na && inv_l == 1u);
+  const float wg0 = __shfl(w_l, m0 ? __builtin_ctzll(m0) : 0);
+  const float wg1 = __shfl(w_l, m1 ? __builtin_ctzll(m1) : 0);
+  // The dots run for every unrolled item, past `items` too (on clamped
+  // duplicates, results dropped): a branch around them would let the compiler
+  // sink the item's loads into it, behind the later items' loads.
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    const int ic = min(i, items - 1);
+    const int ia = ic / nb;
+    const int rr = (ic - ia * nb) * RU;
+    const ActSlice<TYPE> &ac = ia == 0 ? act0 : act1;
+    float acc[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      int32_t *ds = nullptr, *dm = nullptr;
+      if constexpr (DBG) {
+        if (tv && rr + u < nr && i < items) {
+          const int64_t o = ((int64_t)ia * rows + r0 + rr + u) * nblk;
+          ds = a.dbg.s[0] + o;
+          dm = a.dbg.m[0] ? a.dbg.m[0] + o : nullptr;
+        }
+      }
+      const float v = task_dot<TYPE>(w[i % NS][u], tc, ac, 0.0f, ds, dm);
+      acc[u] = group_sum<64>(tv ? v : 0.0f);
+    }
+    if (i < items) {
+      if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < RU; ++u)
+          if (rr + u < nr) part[wave][rr + u] = acc[u];
+      }
+      if ((i + 1) % nb == 0) {  // this expert's last row batch: y and the combine
+        lds_barrier();
+        if (threadIdx.x < nr) {
+          const int t = threadIdx.x;
+          const float y = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+          const float c = (ia == 0 ? wg0 : wg1) * y;
+          outv[t] = outv[t] + c;
+        }
+        lds_barrier();
+      }
+    }
+    if (i + NS < NIT) issue(i + NS, w[i % NS]);
+  }
+  if (threadIdx.x < nr) a.out[r0 + threadIdx.x] = outv[threadIdx.x];
+}
+
 // Launch-shape knobs, read once: KMOE_GRID_MULT (work-groups per CU cap for
 // the register matvec, default 4) and KMOE_DOWN_WG_PER_CU (split-K down,
 // default 2). Used for sweeps; the defaults are the measured best.
@@ -1112,6 +1217,15 @@ int gu_wgpc16() {
 // KMOE_DOWN_RU: rows per split-K item (1, 2 or 4, default 4).
 int down_ru() {
   static const int v = env_int("KMOE_DOWN_RU", 4);
+  return v;
+}
+// KMOE_DOWN_RING: register sets in the single-token Q4_K down ring (2 or 3,
+// default 2; 0 keeps the ping-pong split-K kernel).
+int down_ring() {
+  static const int v = [] {
+    const char *e = getenv("KMOE_DOWN_RING");
+    return e && *e ? atoi(e) : 2;
+  }();
   return v;
 }
 int down_wg_per_cu() {
@@ -1408,6 +1522,27 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
     else KMOE_LAUNCH((k_down_splitk<T, RU, TP, false>), dim3(grid), dim3(256), 0, st, a, rb);         \
   } while (0)
       if (type == T_Q4_K) {
+        if (tpl == 1 && rt.topk <= 2 && down_ring() > 0) {
+          // the ring kernel: 2 rows per item, at most 8 items
+          const int ns = down_ring();
+          const int items = rt.topk * ((rb + 1) / 2);
+          if (items <= 8) {
+#define KMOE_RING(NIT_, NS_)                                                                                      \
+  do {                                                                                                            \
+    if (dbg) KMOE_LAUNCH((k_down_ring<T_Q4_K, 2, NIT_, NS_, true>), dim3(grid), dim3(256), 0, st, a, rb);        \
+    else KMOE_LAUNCH((k_down_ring<T_Q4_K, 2, NIT_, NS_, false>), dim3(grid), dim3(256), 0, st, a, rb);           \
+  } while (0)
+            if (items <= 4) {
+              if (ns <= 2) KMOE_RING(4, 2);
+              else KMOE_RING(4, 3);
+            } else {
+              if (ns <= 2) KMOE_RING(8, 2);
+              else KMOE_RING(8, 3);
+            }
+#undef KMOE_RING
+            return hipGetLastError();
+          }
+        }
         if (tpl == 1) {
           const int ru = down_ru();
           if (ru == 1) KMOE_SPLITK(T_Q4_K, 1, 1);
