@@ -1552,6 +1552,17 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
           KMOE_SPLITK(T_Q4_K, 2, 2);
         }
       } else if (type == T_Q6_K) {  // 26 registers per task: fewer rows per item
+        if (tpl == 1 && rt.topk <= 2 && down_ring() > 0 && rt.topk * ((rb + 1) / 2) <= 8) {
+#define KMOE_RING6(NIT_)                                                                                     \
+  do {                                                                                                       \
+    if (dbg) KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, 2, true>), dim3(grid), dim3(256), 0, st, a, rb);     \
+    else KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, 2, false>), dim3(grid), dim3(256), 0, st, a, rb);        \
+  } while (0)
+          if (rt.topk * ((rb + 1) / 2) <= 4) KMOE_RING6(4);
+          else KMOE_RING6(8);
+#undef KMOE_RING6
+          return hipGetLastError();
+        }
         if (tpl == 1) KMOE_SPLITK(T_Q6_K, 2, 1);
         else KMOE_SPLITK(T_Q6_K, 1, 2);
       } else {
