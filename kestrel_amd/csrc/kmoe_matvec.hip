@@ -1191,6 +1191,77 @@ __global__ void __launch_bounds__(256) k_down_ring(MvArgs a, int rb_rows) {
   if (threadIdx.x < nr) a.out[r0 + threadIdx.x] = outv[threadIdx.x];
 }
 
+// Single-token down + combine over narrow rows (one task slot per lane, LPR
+// lanes per row): the arithmetic and order of k_mv_reg's M_DOWN_COMBINE mode
+// (out[r] = sum over the token's experts in ascending id of w * (down_e[r] .
+// q8(h_slot))), with the experts' loads software-pipelined: a ring of NS
+// register sets (the slot's activation slice and the row's task) keeps the
+// next NS-1 experts' loads in flight while one is reduced. The loop over the
+// KMAX >= topk experts is unrolled and every load unconditional (indices
+// clamped to the last expert), so the compiler's waits stay exact; the expert
+// ids, slots and weights are read once per lane up front (lane j: selection
+// j), so no dependent load sits between the weight loads. WPB waves per
+// work-group, each RPW = 64 / LPR rows.
+template <int TYPE, int LPR, int KMAX, int NS, int WPB, bool DBG>
+__global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int RB = WPB * RPW;  // rows per block-task
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row_in_wave = lane / LPR, lr = lane % LPR;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
+  const int64_t xs_stride = cols / 16;
+  const bool tv = lr < ntasks;
+  const int t = tv ? lr : ntasks - 1;
+  const int K = a.rt.topk;
+  const int jl = lane < K ? lane : 0;
+  const int32_t e_l = a.rt.active[jl];  // expert of slot jl
+  const uint32_t inv_l = a.rt.inv[jl];  // slot of selection jl
+  const float w_l = a.rt.wsel[jl];      // weight of selection jl
+  const int64_t bpe = (rows + RB - 1) / RB;
+  for (int64_t blk = blockIdx.x; blk < bpe; blk += gridDim.x) {
+    const int64_t r = blk * RB + (int64_t)wave * RPW + row_in_wave;
+    const int64_t rc = r < rows ? r : rows - 1;
+    ActSlice<TYPE> act[NS];
+    WTask<TYPE, true> w[NS];
+    auto issue = [&](int ia, int sl) {
+      ia = ia < K ? ia : K - 1;
+      const int e = __builtin_amdgcn_readlane(e_l, ia);
+      const uint8_t *W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[2];
+      act_load<TYPE>(act[sl], a.xq + (int64_t)ia * cols, a.xd + (int64_t)ia * nblk, a.xbs + (int64_t)ia * xs_stride,
+                     t);
+      w_load<TYPE, true>(w[sl], W + rc * row_bytes, t, nblk);
+    };
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) issue(sl, sl);
+    float o = 0.0f;
+#pragma unroll
+    for (int ia = 0; ia < KMAX; ++ia) {  // ascending expert id: slot ia
+      const int sl = ia % NS;
+      const uint64_t m = __ballot(lane < K && inv_l == (uint32_t)ia);
+      const float wgt = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_l), m ? (int)__builtin_ctzll(m) : 0));
+      int32_t *ds = nullptr, *dm = nullptr;
+      if constexpr (DBG) {
+        if (tv && r < rows && ia < K) {
+          const int64_t oo = ((int64_t)ia * rows + r) * nblk;
+          ds = a.dbg.s[0] + oo;
+          dm = a.dbg.m[0] ? a.dbg.m[0] + oo : nullptr;
+        }
+      }
+      const float v = task_dot<TYPE>(w[sl], t, act[sl], 0.0f, ds, dm);
+      const float y = group_sum<LPR>(tv ? v : 0.0f);
+      const float c = wgt * y;
+      const float on = o + c;
+      o = ia < K ? on : o;
+      if (ia + NS < KMAX) issue(ia + NS, sl);
+    }
+    if (lr == 0 && r < rows) a.out[r] = o;
+  }
+}
+
 // Launch-shape knobs, read once: KMOE_GRID_MULT (work-groups per CU cap for
 // the register matvec, default 4) and KMOE_DOWN_WG_PER_CU (split-K down,
 // default 2). Used for sweeps; the defaults are the measured best.
@@ -1225,6 +1296,15 @@ int down_ring() {
   static const int v = [] {
     const char *e = getenv("KMOE_DOWN_RING");
     return e && *e ? atoi(e) : 2;
+  }();
+  return v;
+}
+// KMOE_DOWN_EXP=0 keeps the register kernel's expert loop for single-token
+// down + combine over narrow rows instead of the expert ring.
+int down_exp_ring() {
+  static const int v = [] {
+    const char *e = getenv("KMOE_DOWN_EXP");
+    return e && *e ? atoi(e) : 1;
   }();
   return v;
 }
@@ -1492,6 +1572,48 @@ hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, in
   return hipErrorNotSupported;
 }
 
+// k_mv_down_exp for rows of at most 64 task slots: lanes per row as the
+// register kernel picks them, the smallest KMAX >= topk, 3 register sets, and
+// waves per work-group so that the row blocks number at least two per CU.
+template <int TYPE>
+hipError_t launch_down_exp(hipStream_t st, const MvArgs &a, int ntasks, int topk, bool dbg) {
+  int lpr, tpl;
+  if (!reg_geometry(TYPE, ntasks, lpr, tpl) || tpl != 1) return hipErrorNotSupported;
+  const int rpw = 64 / lpr;
+  int wpb = 4;
+  while (wpb > 1 && (a.rows + rpw * wpb - 1) / (rpw * wpb) < 2 * (int64_t)cu_count()) wpb >>= 1;
+  const int64_t blocks = (a.rows + (int64_t)rpw * wpb - 1) / ((int64_t)rpw * wpb);
+  const int64_t cap = (int64_t)cu_count() * grid_mult() * (4 / wpb);
+  const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);
+  const int kmax = topk <= 2 ? 2 : topk <= 4 ? 4 : topk <= 6 ? 6 : 8;
+#define KMOE_DX(L, KM, WP)                                                                                         \
+  do {                                                                                                             \
+    if (dbg) KMOE_LAUNCH((k_mv_down_exp<TYPE, L, KM, 3, WP, true>), dim3(grid), dim3(64 * WP), 0, st, a);         \
+    else KMOE_LAUNCH((k_mv_down_exp<TYPE, L, KM, 3, WP, false>), dim3(grid), dim3(64 * WP), 0, st, a);            \
+    return hipGetLastError();                                                                                      \
+  } while (0)
+#define KMOE_DX_K(L, WP)             \
+  do {                               \
+    if (kmax == 2) KMOE_DX(L, 2, WP); \
+    if (kmax == 4) KMOE_DX(L, 4, WP); \
+    if (kmax == 6) KMOE_DX(L, 6, WP); \
+    KMOE_DX(L, 8, WP);               \
+  } while (0)
+#define KMOE_DX_W(L)                  \
+  do {                                \
+    if (wpb == 1) KMOE_DX_K(L, 1);    \
+    if (wpb == 2) KMOE_DX_K(L, 2);    \
+    KMOE_DX_K(L, 4);                  \
+  } while (0)
+  if (lpr == 64) KMOE_DX_W(64);
+  if (lpr == 32) KMOE_DX_W(32);
+  if (lpr == 16) KMOE_DX_W(16);
+#undef KMOE_DX_W
+#undef KMOE_DX_K
+#undef KMOE_DX
+  return hipErrorNotSupported;
+}
+
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
                                       float *out, const BlockDbg *dbg) {
@@ -1572,6 +1694,13 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
 #undef KMOE_SPLITK
       return hipGetLastError();
     }
+  }
+  if (down_exp_ring() > 0 && rt.topk <= 8) {
+    hipError_t e = hipErrorNotSupported;
+    if (type == T_Q4_K) e = launch_down_exp<T_Q4_K>(st, a, ntasks, rt.topk, dbg != nullptr);
+    else if (type == T_Q6_K) e = launch_down_exp<T_Q6_K>(st, a, ntasks, rt.topk, dbg != nullptr);
+    else if (type == T_Q8_0) e = launch_down_exp<T_Q8_0>(st, a, ntasks, rt.topk, dbg != nullptr);
+    if (e != hipErrorNotSupported) return e;
   }
   if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_DOWN_COMBINE, 1>(st, a, 1);
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_DOWN_COMBINE, 1>(st, a, 1);
