@@ -89,16 +89,13 @@ __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
     float lv[NPER];
 #pragma unroll
     for (int i = 0; i < NPER; ++i) lv[i] = lane + 64 * i < q.E ? q.logits[lane + 64 * i] : -INFINITY;
-    uint32_t sj[16];
-    float wj[16];
-    wave_route_one<NPER>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P[wave], sj, wj);
-    uint32_t rk[16];
-    selection_ranks(sj, q.K, rk);
-    e = -1;
-    for (int j = 0; j < q.K; ++j)
-      if ((int)rk[j] == slot_i) e = (int)sj[j];
+    uint32_t sl;
+    float wl;
+    wave_route_one<NPER>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P[wave], sl, wl);
+    const uint32_t rk = selection_rank(sl, q.K);
+    e = selection_in_slot(sl, rk, q.K, slot_i);
     if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0)  // publish the routing of the token
-      publish_selection(sj, wj, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
+      publish_selection(sl, wl, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
     if (e < 0) return;
     p = slot_i;
   }

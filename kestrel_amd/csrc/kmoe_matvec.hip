@@ -736,28 +736,26 @@ __device__ __forceinline__ float task_dot(const WTask<TYPE, TILED> &wt, int t, c
 // (the expert of slot i); work-group 0 also publishes the routing for the
 // kernels that follow.
 __device__ __forceinline__ void mv_select(const DecSelect &q, int lane, int32_t *slot_e, float *P, bool publish) {
-  uint32_t sj[16];
-  float wj[16];
+  uint32_t sl;
+  float wl;
   if (q.E <= 64) {
     float lv[1] = {lane < q.E ? q.logits[lane] : -INFINITY};
-    wave_route_one<1>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+    wave_route_one<1>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sl, wl);
   } else if (q.E <= 128) {
     float lv[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) lv[i] = lane + 64 * i < q.E ? q.logits[lane + 64 * i] : -INFINITY;
-    wave_route_one<2>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+    wave_route_one<2>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sl, wl);
   } else {
     float lv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) lv[i] = lane + 64 * i < q.E ? q.logits[lane + 64 * i] : -INFINITY;
-    wave_route_one<4>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sj, wj);
+    wave_route_one<4>(lv, q.E, q.K, q.norm_topk, q.weights_scale, P, sl, wl);
   }
-  uint32_t rk[16];
-  selection_ranks(sj, q.K, rk);
-  if (lane == 0)
-    for (int j = 0; j < q.K; ++j) slot_e[rk[j]] = (int32_t)sj[j];
+  const uint32_t rk = selection_rank(sl, q.K);
+  if (lane < q.K) slot_e[rk] = (int32_t)sl;
   if (publish)
-    publish_selection(sj, wj, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
+    publish_selection(sl, wl, rk, q.K, q.E, lane, q.idx, q.wsel, q.perm, q.inv, q.active, q.n_active, q.offsets);
 }
 
 // DBG: the grouped modes also add their per-block integers into a.dbg (the

@@ -596,15 +596,13 @@ __device__ void route_dec_tail(const RouteDecArgs &a, float *P, uint32_t *sel, i
       // written by other work-groups of this launch: read past this CU's L1
       lv[i] = e < E ? __hip_atomic_load(a.logits + s * E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
     }
-    uint32_t sj[16];
-    float wk[16];
-    wave_route_one<NPER>(lv, E, K, a.norm_topk, a.weights_scale, P + s * kMaxExperts, sj, wk);
-    if (lane == 0) {
-      for (int j = 0; j < K; ++j) {
-        sel[s * K + j] = sj[j];
-        a.idx[s * K + j] = sj[j];
-        a.wsel[s * K + j] = wk[j];
-      }
+    uint32_t sl;
+    float wl;
+    wave_route_one<NPER>(lv, E, K, a.norm_topk, a.weights_scale, P + s * kMaxExperts, sl, wl);
+    if (lane < K) {
+      sel[s * K + lane] = sl;
+      a.idx[s * K + lane] = sl;
+      a.wsel[s * K + lane] = wl;
     }
   }
   __syncthreads();

@@ -49,15 +49,17 @@ __device__ __forceinline__ uint32_t p_rank_key(float p) { return p != p ? 0u : _
 
 // One token, one whole wave. lv[i] holds the logit of expert lane + 64*i
 // (E <= 64*NPER; entries past E are ignored). p is this wave's LDS scratch of
-// at least E floats. On return sel[j] and w[j], j < K, are the selected
-// experts in selection order and their weights, identical in every lane:
+// at least E floats. K <= 16. On return lane j < K holds selection j in
+// sel_l (expert id) and w_l (weight), selection order:
 //   p_e = exp(l_e - max) / (sum in expert order), correctly rounded exp;
 //   K rounds of the largest p (compared by p_rank_key), ties to the lower
-//   index; if norm_topk, w /= max(sum of the selected p, 2^-14); then w *=
-//   wscale unless wscale is 0 or 1.
+//   index; if norm_topk, w /= max(sum of the selected p in selection order,
+//   2^-14); then w *= wscale unless wscale is 0 or 1.
+// The selections stay one per lane (no register arrays indexed at run time,
+// which the target can only address through its slow indexing mode).
 template <int NPER>
 __device__ __forceinline__ void wave_route_one(float (&lv)[NPER], int E, int K, int norm_topk, float wscale, float *p,
-                                               uint32_t (&sel)[16], float (&w)[16]) {
+                                               uint32_t &sel_l, float &w_l) {
   const int lane = threadIdx.x & 63;
   float m = -INFINITY;
 #pragma unroll
@@ -89,6 +91,8 @@ __device__ __forceinline__ void wave_route_one(float (&lv)[NPER], int E, int K, 
 #pragma unroll
   for (int i = 0; i < NPER; ++i) lv[i] = lv[i] / sum;
   uint32_t taken = 0;
+  sel_l = 0;
+  w_l = 0.0f;
   for (int j = 0; j < K; ++j) {
     uint32_t best = 0;
     int bi = NPER;
@@ -109,55 +113,66 @@ __device__ __forceinline__ void wave_route_one(float (&lv)[NPER], int E, int K, 
     float mine = lv[0];
 #pragma unroll
     for (int i = 1; i < NPER; ++i) mine = i == ib ? lv[i] : mine;
-    w[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), lw));
-    sel[j] = es;
+    const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), lw));
+    sel_l = lane == j ? es : sel_l;
+    w_l = lane == j ? wj : w_l;
   }
   if (norm_topk) {
     float ss = -0.0f;
-    for (int j = 0; j < K; ++j) ss = ss + w[j];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_l), j));
+      const float t = ss + v;
+      ss = j < K ? t : ss;
+    }
     ss = fmaxf(ss, 6.103515625e-05f);
-    for (int j = 0; j < K; ++j) w[j] = w[j] / ss;
+    w_l = w_l / ss;
   }
-  if (wscale != 0.0f && wscale != 1.0f)
-    for (int j = 0; j < K; ++j) w[j] = w[j] * wscale;
+  if (wscale != 0.0f && wscale != 1.0f) w_l = w_l * wscale;
 }
 
-// Rank of each selected expert among the selection (all ids distinct): the
-// slot of selection entry j is rk[j], slots in ascending expert id.
-__device__ __forceinline__ void selection_ranks(const uint32_t (&sj)[16], int K, uint32_t (&rk)[16]) {
-  for (int j = 0; j < K; ++j) {
-    uint32_t r = 0;
-    for (int jj = 0; jj < K; ++jj) r += sj[jj] < sj[j] ? 1u : 0u;
-    rk[j] = r;
+// Slot of the lane's selection (lanes j < K; all ids distinct): the number of
+// selections with a smaller expert id, slots in ascending expert id.
+__device__ __forceinline__ uint32_t selection_rank(uint32_t sel_l, int K) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)sel_l, j);
+    r += (j < K && v < sel_l) ? 1u : 0u;
   }
+  return r;
+}
+
+// The expert in slot `slot` (the selection whose rank is slot), or -1 when
+// slot >= K; uniform across the wave.
+__device__ __forceinline__ int selection_in_slot(uint32_t sel_l, uint32_t rk_l, int K, int slot) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t m = __ballot(lane < K && rk_l == (uint32_t)slot);
+  return m ? __builtin_amdgcn_readlane((int)sel_l, (int)__builtin_ctzll(m)) : -1;
 }
 
 // The routing of one token from its selection, written by one wave: idx and
 // weights in selection order, perm / inv between selection entry and slot,
 // the active experts by slot, their count and the per-expert slot offsets
 // [E + 1] (the dispatch of transformer.rs:525-531 for one token).
-__device__ __forceinline__ void publish_selection(const uint32_t (&sj)[16], const float (&wj)[16],
-                                                  const uint32_t (&rk)[16], int K, int E, int lane, uint32_t *idx,
-                                                  float *wsel, uint32_t *perm, uint32_t *inv, int32_t *active,
-                                                  int32_t *n_active, uint32_t *offsets) {
-  uint32_t mysel = 0, myrk = 0;
-  float myw = 0.0f;
-  for (int j = 0; j < K; ++j) {
-    mysel = lane == j ? sj[j] : mysel;
-    myrk = lane == j ? rk[j] : myrk;
-    myw = lane == j ? wj[j] : myw;
-  }
+__device__ __forceinline__ void publish_selection(uint32_t sel_l, float w_l, uint32_t rk_l, int K, int E, int lane,
+                                                  uint32_t *idx, float *wsel, uint32_t *perm, uint32_t *inv,
+                                                  int32_t *active, int32_t *n_active, uint32_t *offsets) {
   if (lane < K) {
-    idx[lane] = mysel;
-    wsel[lane] = myw;
-    perm[myrk] = (uint32_t)lane;
-    inv[lane] = myrk;
-    active[myrk] = (int32_t)mysel;
+    idx[lane] = sel_l;
+    wsel[lane] = w_l;
+    perm[rk_l] = (uint32_t)lane;
+    inv[lane] = rk_l;
+    active[rk_l] = (int32_t)sel_l;
   }
   if (lane == 0) *n_active = K;
   for (int ee = lane; ee <= E; ee += 64) {
     uint32_t c = 0;
-    for (int j = 0; j < K; ++j) c += sj[j] < (uint32_t)ee ? 1u : 0u;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)sel_l, j);
+      c += (j < K && v < (uint32_t)ee) ? 1u : 0u;
+    }
     offsets[ee] = c;
   }
 }
