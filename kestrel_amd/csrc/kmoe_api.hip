@@ -1411,8 +1411,11 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   // Which regimes can occur: an expert has at most S rows.
   const bool any_int = regime == KMOE_REGIME_INT8 || (regime == KMOE_REGIME_AVX2);
   const bool any_f32 = regime == KMOE_REGIME_EXACT || (regime == KMOE_REGIME_AVX2 && S >= 4);
-  // Int8 regime with many token rows: grouped products on the int8 matrix cores.
+  // Int8 regime with many token rows: grouped products on the int8 matrix cores;
+  // while experts average at most 20 rows, those with at most 32 take the
+  // streaming kernel (more rows per expert leave too many on the other one).
   const bool mfma = regime == KMOE_REGIME_INT8 && S >= mfma_min_rows();
+  const int ring_rows = slots <= 20 * E ? 32 : 0;
 
   // Single token, int8 path: every routed expert has one row. gate/up+SwiGLU
   // and down+combine run as register-resident decode kernels.
@@ -1492,7 +1495,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       if (mfma && gt == KMOE_Q4_K)
         e = timed(c, "moe_gate_up_mfma", [&]() {
           return launch_moe_mfma(st, 0, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h, small_rows + 1,
-                                 gd);
+                                 (int)S, ring_rows, gd);
         });
       if (e != hipErrorNotSupported) HIP_OK(c, e);
       else
@@ -1524,7 +1527,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       if (mfma && dt == KMOE_Q4_K)
         e = timed(c, "moe_down_mfma", [&]() {
           return launch_moe_mfma(st, 1, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y, small_rows + 1,
-                                 dd);
+                                 (int)S, ring_rows, dd);
         });
       if (e != hipErrorNotSupported) HIP_OK(c, e);
       else

@@ -153,11 +153,14 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
 // Token rows at which the matrix-core kernels take over (KMOE_MFMA_MIN_ROWS, default 8).
 int mfma_min_rows();
 bool moe_mfma_supported(int64_t rows, int64_t cols);
-// Grouped over the expert tier, as launch_moe_int (mode 0 gate/up + SwiGLU, 1 down).
+// Grouped over the expert tier, as launch_moe_int (mode 0 gate/up + SwiGLU, 1 down),
+// for the experts with min_rows..max_rows rows (max_rows: the most any expert can hold);
+// those with at most ring_rows (<= 32; 0: none) rows take the streaming kernel.
 // hipErrorNotSupported: shape or activation alignment (16 B) not covered.
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out, int min_rows = 0, const BlockDbg *dbg = nullptr);
+                           const int32_t *abs, float *out, int min_rows, int max_rows, int ring_rows,
+                           const BlockDbg *dbg = nullptr);
 // Plain GGUF rows: out[s*rows + r], or, with sumi/mins set, the per-block
 // integer accumulators at [(s*rows + r)*nb + b] (ad unused).
 hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *aq,

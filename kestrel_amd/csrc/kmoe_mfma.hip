@@ -55,6 +55,7 @@ namespace {
 typedef int v4i32 __attribute__((ext_vector_type(4)));
 typedef int v16i32 __attribute__((ext_vector_type(16)));
 typedef float v16f32 __attribute__((ext_vector_type(16)));
+typedef float v4f32 __attribute__((ext_vector_type(4)));
 typedef _Float16 v8f16 __attribute__((ext_vector_type(8)));
 typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -80,6 +81,7 @@ struct MfmaArgs {
   int32_t *sumi, *mins;  // MF_SUMS: [(s*rows + r)*nb + b]
   int regime;
   int min_rows;          // grouped modes: experts with fewer rows are another kernel's
+  int max_rows;          // grouped modes: experts with more rows are another kernel's
   BlockDbg dbg;          // grouped modes with DBG: per-superblock integers (gate/down 0, up 1)
 };
 
@@ -163,7 +165,7 @@ __global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
       const int e = a.rt.active[i_act];
       p0 = a.rt.offsets[e];
       const int n = (int)(a.rt.offsets[e + 1] - p0);
-      if (n < a.min_rows || !mfma_int_regime(a.regime, n)) return;
+      if (n < a.min_rows || n > a.max_rows || !mfma_int_regime(a.regime, n)) return;
       W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[mat] + rr * row_bytes;
       t_begin = 0;
       t_end = n;
@@ -392,6 +394,342 @@ __global__ void __launch_bounds__(512) k_moe_mfma(MfmaArgs a) {
   }
 }
 
+
+// ---- Experts with at most 32 routed rows (decode batches of a few dozen
+// tokens). The kernel above keeps one superblock of loads in flight per
+// work-group and waits for all of it at every barrier; with a single token
+// tile per superblock its compute is short and HBM sits mostly idle. Here:
+//   * work items are (expert, 32*TI weight rows) over the experts with
+//     min_rows..32 rows on the int path; work-group w takes items w,
+//     w + gridDim.x, ... as one chain of stages, so its pipeline does not
+//     drain between items;
+//   * a stage is two superblocks: each lane's weight bytes (the two 16-byte
+//     heads and eight 16-byte nibble chunks of its row, 128 contiguous bytes
+//     in the tiled row, the A operand pieces of the kernel above) go to
+//     registers NS stages deep, with cached loads (a head line serves four
+//     stages); the stage's token tile (int8 pieces, 16-sums and block scales
+//     of the item's <= 32 rows) goes to LDS by direct loads. Every wave
+//     issues the same vector memory instructions per stage, so one counted
+//     wait and one barrier per stage cover the stage;
+//   * gate/up: 4 waves = (row tile 0, 1) x (gate, up), the up waves hand
+//     their sums to the gate waves through LDS for SwiGLU (transformer.rs:558).
+//     Down: 8 waves = (row tile 0..3) x (first, second part of the
+//     superblocks), the second part's sums handed to the first, added in
+//     that order.
+// Per superblock the integers are the kernel above's (sumi = 8 * hi chain +
+// lo chain, here as two accumulators; mins on the f16 matrix cores).
+constexpr int kRingTok = 32;
+// A work-group barrier that orders the compiler's memory accesses around it
+// but waits for nothing itself: a workgroup-scope LDS fence would also wait
+// for every direct global->LDS load in flight, which would drain the ring.
+// The callers issue the exact s_waitcnt the barrier needs first.
+__device__ __forceinline__ void ring_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// ds_write_b128 written out: the compiler's own 16-byte LDS stores lose their
+// alias information, and it then waits for every direct load in flight before
+// them (all of the ring) although none of those writes the stored-to array.
+__device__ __forceinline__ void lds_store16(float *p, v4f32 v) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)p;
+  asm volatile("ds_write_b128 %0, %1" ::"v"(la), "v"(v) : "memory");
+}
+constexpr int kRingItems = 8;      // items per work-group at most (the launcher's grid guarantees it)
+constexpr int kRingExperts = 256;  // experts with rows at most
+template <int MODE>
+constexpr int kRingWaves = MODE == MF_DOWN ? 8 : 4;
+
+template <int MODE, int NS, bool DBG>
+__global__ void __launch_bounds__(kRingWaves<MODE> * 64, 2) k_moe_mfma_ring(MfmaArgs a) {
+  constexpr int NW = kRingWaves<MODE>;
+  constexpr int TI = NW / 2;                   // row tiles per item
+  constexpr int RI = 32 * TI;                  // rows per item
+  constexpr int KS = MODE == MF_DOWN ? 2 : 1;  // superblock parts per item
+  constexpr int G = NW / KS;                   // waves loading one part's token tile
+  constexpr int kA8 = kRingTok * 256;          // int8 rows [32 tokens][16 pieces, swizzled]
+  constexpr int kS16 = kRingTok * 64;          // 16-sums [32 tokens][16]
+  constexpr int kSB = kA8 + kS16;              // one superblock's token tile
+  constexpr int kAd = KS * kSB;                // then per wave: block scales [32 tokens] (twice)
+  constexpr int kStg = kAd + NW * 256;
+  constexpr int NA8 = 8 / G, NB16 = 8 / G;     // direct loads per wave and stage (1 KB and 256 B each)
+  constexpr int OPS = 4 + 1 + 1 + NA8 + NB16;  // vector memory instructions per wave and stage
+  static_assert(NS >= 2 && NS <= 3, "ring depth");
+  // Distinct objects per stage: reads of one stage are not ordered behind the
+  // direct loads still filling the other.
+  __shared__ __attribute__((aligned(16))) uint8_t st0[kStg];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[kStg];
+  __shared__ __attribute__((aligned(16))) uint8_t st2[NS > 2 ? kStg : 16];
+  // per wave: the stage's nibble runs [64 runs][64 B, swizzled], then its heads [32 rows][16 B]
+  __shared__ __attribute__((aligned(16))) uint8_t scr[NW][4096 + 512];
+  __shared__ __attribute__((aligned(16))) float xch[RI][kRingTok + 4];  // the hand-over: [row][token]
+  __shared__ int32_t it_e[kRingItems], it_n[kRingItems], it_rb[kRingItems], it_src[kRingItems][kRingTok];
+  __shared__ uint32_t it_p0[kRingItems];
+  __shared__ int32_t elig[kRingExperts];
+  __shared__ int32_t n_elig;
+
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = wave % TI, grp = wave / TI;  // grp: gate/up the matrix, down the part
+  const int wig = MODE == MF_DOWN ? tile : wave;  // wave's index among the waves loading its part
+  const int mat = MODE == MF_GATE_UP ? grp : 2;
+  const int64_t rows = a.rows, cols = a.cols, nb = cols / 256, row_bytes = nb * 144;
+  const int RB = KS == 1 ? (int)nb : (int)((nb + 1) / 2);  // superblocks per part
+  const int SPI = RB;                                         // stages per item
+  const int b_lo = grp * (KS == 1 ? 0 : RB);
+  const int b_hi = KS == 1 ? (int)nb : (b_lo + RB < nb ? b_lo + RB : (int)nb);  // this part's end
+  const int bpe = (int)((rows + RI - 1) / RI);  // items per expert
+
+  // experts of this kernel, in active order
+  if (wave == 0) {
+    const int na = *a.rt.n_active;
+    int cnt = 0;
+    for (int i0 = 0; i0 < na; i0 += 64) {
+      const int i = i0 + lane;
+      bool ok = false;
+      int e = 0;
+      if (i < na) {
+        e = a.rt.active[i];
+        const int n = (int)(a.rt.offsets[e + 1] - a.rt.offsets[e]);
+        ok = n >= a.min_rows && n <= a.max_rows && mfma_int_regime(a.regime, n);
+      }
+      const uint64_t m = __ballot(ok);
+      if (ok) elig[cnt + __popcll(m & ((1ull << lane) - 1ull))] = e;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) n_elig = cnt;
+  }
+  __syncthreads();
+  const int total = n_elig * bpe;
+  const int nI = (int)blockIdx.x < total ? (total - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+  if (nI == 0) return;
+  for (int x = tid; x < nI * kRingTok; x += NW * 64) {
+    const int k = x / kRingTok, t = x % kRingTok;
+    const int gi = (int)blockIdx.x + k * (int)gridDim.x;
+    const int e = elig[gi / bpe];
+    const uint32_t p0 = a.rt.offsets[e];
+    const int n = (int)(a.rt.offsets[e + 1] - p0);
+    const uint32_t tt = t < n ? (uint32_t)t : 0u;  // rows past n read the first row's data, never stored
+    if constexpr (MODE == MF_GATE_UP) it_src[k][t] = (int32_t)(a.rt.perm[p0 + tt] / (uint32_t)a.rt.topk);
+    else it_src[k][t] = (int32_t)(p0 + tt);
+    if (t == 0) {
+      it_e[k] = e;
+      it_p0[k] = p0;
+      it_n[k] = n;
+      it_rb[k] = gi % bpe;
+    }
+  }
+  __syncthreads();
+
+  uint8_t *const stg[3] = {st0, st1, st2};
+  uint8_t *const myscr = scr[wave];
+  const int T = nI * SPI;
+  const int part_off = MODE == MF_DOWN ? grp * kSB : 0;
+  // Coalesced weight loads. Run rho = 32*h + r is half h of row r's nibble
+  // chunks of the stage's superblock (64 contiguous bytes of the tiled row);
+  // load i takes runs 16*i .. 16*i+15, four lanes per run. The heads load
+  // takes row lane % 32's 16-byte head (the two halves of the wave load the
+  // same rows).
+  u32x4 wc[NS][4], wh[NS];
+  int ik = 0, ib = 0;  // next stage to issue (item, stage in the item); clamped at the last
+  auto issue = [&](int slot) {
+    const int k = ik < nI ? ik : nI - 1, b = ik < nI ? ib : SPI - 1;
+    const bool adv = ik < nI, wrap = ib + 1 == SPI;  // selects, not branches: the cursor stays in registers
+    ik = adv && wrap ? ik + 1 : ik;
+    ib = adv ? (wrap ? 0 : ib + 1) : ib;
+    const uint8_t *E = a.tier.base + (int64_t)it_e[k] * a.tier.stride + a.tier.off[mat];
+    const int64_t r0 = (int64_t)it_rb[k] * RI + tile * 32;
+    auto rowp = [&](int r) {
+      const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
+      return E + rr * row_bytes;
+    };
+    const int64_t bq = b_lo + b < nb ? b_lo + b : nb - 1;
+    const uint8_t *WA = rowp(lane >> 2), *WB = rowp(16 + (lane >> 2));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)  // runs 16*i + lane/4: row (i & 1)*16 + lane/4, half i/2
+      wc[slot][i] = *(const u32x4 *)(((i & 1) ? WB : WA) + tq4_qs_off(nb, bq, 0, i >> 1) + 16 * (lane & 3));
+    wh[slot] = *(const u32x4 *)(rowp(l32) + 16 * bq);
+    // block scales: lane -> row lane % 32
+    __builtin_amdgcn_global_load_lds(a.ad + (int64_t)it_src[k][l32] * nb + bq,
+                                     (__attribute__((address_space(3))) void *)(stg[slot] + kAd + wave * 256), 4, 0,
+                                     0);
+    uint8_t *S = stg[slot] + part_off;
+#pragma unroll
+    for (int i2 = 0; i2 < NA8; ++i2) {  // rows 4i .. 4i+3, 16 lanes each (piece p at slot p ^ (t & 7))
+      const int i = wig * NA8 + i2;
+      const int t = 4 * i + (lane >> 4);
+      const int64_t src = it_src[k][t];
+      lds_dma16(a.aq + src * cols + 256 * bq + 16 * ((lane & 15) ^ (t & 7)), S + i * 1024);
+    }
+#pragma unroll
+    for (int i2 = 0; i2 < NB16; ++i2) {  // 16-sums of rows 4i .. 4i+3
+      const int i = wig * NB16 + i2;
+      const int64_t src_s = it_src[k][4 * i + (lane >> 4)];
+      __builtin_amdgcn_global_load_lds(a.abs + src_s * (cols / 16) + 16 * bq + (lane & 15),
+                                       (__attribute__((address_space(3))) void *)(S + kA8 + i * 256), 4, 0, 0);
+    }
+  };
+
+  float y[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) y[v] = 0.0f;
+  int ck = 0, cb = 0;  // stage being consumed
+  auto consume = [&](int slot) {
+    {
+      const int64_t bb = b_lo + cb;
+      if (bb < b_hi) {  // the second part of an odd superblock count ends one stage early
+        // the runs through the wave's scratch (run rho at rho*64, piece p at
+        // (p ^ ((rho >> 1) & 3))*16) into the operand layout: lane = run; heads likewise
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rho = 16 * i + (lane >> 2), p = lane & 3;
+          lds_store16((float *)(myscr + rho * 64 + ((p ^ ((rho >> 1) & 3)) * 16)),
+                      __builtin_bit_cast(v4f32, wc[slot][i]));
+        }
+        lds_store16((float *)(myscr + 4096 + 16 * l32), __builtin_bit_cast(v4f32, wh[slot]));
+        u32x4 wq[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) wq[p] = *(const u32x4 *)(myscr + lane * 64 + ((p ^ ((lane >> 1) & 3)) * 16));
+        const u32x4 hd = *(const u32x4 *)(myscr + 4096 + 16 * l32);
+        const uint8_t *S = stg[slot] + part_off;
+        int sc[8], mn[8];
+        q4k_scales8(hd.y, hd.z, hd.w, sc, mn);
+        int s16[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int4 v4 = *(const int4 *)(S + kA8 + l32 * 64 + 16 * i);
+          s16[4 * i] = v4.x;
+          s16[4 * i + 1] = v4.y;
+          s16[4 * i + 2] = v4.z;
+          s16[4 * i + 3] = v4.w;
+        }
+        // Roles: A = the 32 rows' int8 pieces, B = the weight operands, so in
+        // the 32x32 result lane l holds weight row l % 32 (its own head's d,
+        // dmin) for the rows 8*(v/4) + 4*(l/32) + v%4 of the item.
+        v8f16 bm, amn;
+        v16i32 H = v16i32{0}, L = v16i32{0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int sj = s16[2 * j] + s16[2 * j + 1];
+          const int hj = sj >> 6;  // floor: sj = 64*hj + (sj - 64*hj), the second part in [0, 64)
+          bm[j] = (_Float16)(half ? sj - 64 * hj : hj);
+          amn[j] = (_Float16)(half ? mn[j] : 64 * mn[j]);
+          const v4i32 bv = *(const v4i32 *)(S + l32 * 256 + (((2 * j + half) ^ (l32 & 7)) * 16));
+          const u32x4 w = wq[j >> 1];
+          const uint32_t msk = 0x0f0f0f0fu;
+          const int s4 = (j & 1) ? 4 : 0;
+          const uint32_t n0 = (w.x >> s4) & msk, n1 = (w.y >> s4) & msk, n2 = (w.z >> s4) & msk,
+                         n3 = (w.w >> s4) & msk;
+          const uint32_t hi = (uint32_t)(sc[j] >> 3), lo = (uint32_t)(sc[j] & 7);
+          const v4i32 ahi = v4i32{mul_bytes(n0, hi), mul_bytes(n1, hi), mul_bytes(n2, hi), mul_bytes(n3, hi)};
+          const v4i32 alo = v4i32{mul_bytes(n0, lo), mul_bytes(n1, lo), mul_bytes(n2, lo), mul_bytes(n3, lo)};
+          H = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv, ahi, H, 0, 0, 0);
+          L = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv, alo, L, 0, 0, 0);
+        }
+        const v16f32 N = __builtin_amdgcn_mfma_f32_32x32x16_f16(bm, amn, v16f32{0}, 0, 0, 0);
+        const v16i32 SI = (H << 3) + L;
+        if constexpr (DBG) {
+          const int k = ck, n = it_n[k];
+          const int64_t rw = (int64_t)it_rb[k] * RI + tile * 32 + l32;
+          if (rw < rows) {
+            int32_t *ds = a.dbg.s[mat == 1 ? 1 : 0], *dm = a.dbg.m[mat == 1 ? 1 : 0];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int t = 8 * (v >> 2) + 4 * half + (v & 3);
+              if (t < n) {
+                const int64_t o = (((int64_t)it_p0[k] + t) * rows + rw) * nb + bb;
+                ds[o] = SI[v];
+                dm[o] = (int)N[v];
+              }
+            }
+          }
+        }
+        const float d = f16_bits_to_f32(hd.x), dmin = f16_bits_to_f32(hd.x >> 16);
+        const float *adl = (const float *)(stg[slot] + kAd + wave * 256);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 a4 = *(const float4 *)(adl + 8 * g + 4 * half);
+          const float at[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int v = 4 * g + c;
+            const float x = fmaf(d, (float)SI[v], -(dmin * N[v]));
+            y[v] = fmaf(at[c], x, y[v]);
+          }
+        }
+      }
+    }
+    if (cb == SPI - 1) {  // the item is complete: hand-over, SwiGLU or the parts' sum, store
+      const int k = ck;
+      if (grp == 1) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          lds_store16(&xch[tile * 32 + l32][8 * g + 4 * half], v4f32{y[4 * g], y[4 * g + 1], y[4 * g + 2], y[4 * g + 3]});
+      }
+      __builtin_amdgcn_s_waitcnt((15 | (3 << 14)) | (7 << 4));  // lgkmcnt(0): the hand-over is written
+      ring_barrier();
+      if (grp == 0) {
+        const int n = it_n[k];
+        const int64_t p0 = it_p0[k], rw = (int64_t)it_rb[k] * RI + tile * 32 + l32;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 o4 = *(const float4 *)&xch[tile * 32 + l32][8 * g + 4 * half];
+          const float ov[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int t = 8 * g + 4 * half + c;
+            float o;
+            if constexpr (MODE == MF_GATE_UP) {
+              const float gv = y[4 * g + c];
+              const float den = 1.0f + expf_cr(-gv);  // SwiGLU: g / (1 + exp(-g)) * u
+              o = gv / den * ov[c];
+            } else {
+              o = y[4 * g + c] + ov[c];
+            }
+            if (t < n && rw < rows) a.out[(p0 + t) * rows + rw] = o;
+          }
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) y[v] = 0.0f;
+    }
+    const bool wrap = cb == SPI - 1;
+    ck = wrap ? ck + 1 : ck;
+    cb = wrap ? 0 : cb + 1;
+  };
+
+  constexpr int kWait = (NS - 2) * OPS;
+  // s_waitcnt: vmcnt(kWait), expcnt(7), lgkmcnt(0)
+  constexpr int kWaitEnc = (kWait & 15) | ((kWait >> 4) << 14) | (7 << 4);
+#pragma unroll
+  for (int u = 0; u < NS - 1; ++u) issue(u);
+  // Every pass of the body issues the same loads (stages past the last are
+  // clamped re-loads), so the compiler's wait counts stay exact.
+  for (int s0 = 0; s0 < T; s0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      __builtin_amdgcn_s_waitcnt(kWaitEnc);  // this wave's loads of stage s0+u are in, its LDS reads done
+      ring_barrier();                        // every wave's, so the slot refilled next is free too
+      issue((u + NS - 1) % NS);
+      if (s0 + u < T) consume(u);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): no direct load outlives the work-group
+}
+
+int g_mfma_cus = 0;
+int mfma_cus() {
+  if (g_mfma_cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      g_mfma_cus = n;
+    else
+      g_mfma_cus = 256;
+  }
+  return g_mfma_cus;
+}
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -411,11 +749,33 @@ bool moe_mfma_supported(int64_t rows, int64_t cols) {
   return rows > 0 && cols > 0 && cols % 256 == 0 && rows < (1ll << 31) / 32 && cols / 256 < (1ll << 24);
 }
 
+// Launch knob, read once: KMOE_MFMA_RING=0 keeps experts with at most 32
+// rows on the kernel above instead of the streaming kernel.
+bool mfma_ring() {
+  static const bool v = [] {
+    const char *e = getenv("KMOE_MFMA_RING");
+    return !(e && *e && atoi(e) == 0);
+  }();
+  return v;
+}
+
+template <int MODE, bool DBG>
+hipError_t launch_ring(hipStream_t st, dim3 grid, const MfmaArgs &a) {
+  static const int ns = [] {
+    const char *e = getenv("KMOE_MFMA_RING_NS");
+    return e && *e && atoi(e) == 2 ? 2 : 3;
+  }();
+  if (ns == 2) KMOE_LAUNCH((k_moe_mfma_ring<MODE, 2, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
+  else KMOE_LAUNCH((k_moe_mfma_ring<MODE, 3, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, const int8_t *aq, const float *ad,
-                           const int32_t *abs, float *out, int min_rows, const BlockDbg *dbg) {
+                           const int32_t *abs, float *out, int min_rows, int max_rows, int ring_rows,
+                           const BlockDbg *dbg) {
   if (!moe_mfma_supported(rows, cols) || !aligned16(aq) || !aligned16(abs)) return hipErrorNotSupported;
-  if (max_active == 0) return hipSuccess;
+  if (max_active == 0 || max_rows < min_rows) return hipSuccess;
   MfmaArgs a{};
   a.tier = tier;
   a.rt = rt;
@@ -427,7 +787,31 @@ hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int
   a.out = out;
   a.regime = regime;
   a.min_rows = min_rows;
+  a.max_rows = max_rows;
   if (dbg) a.dbg = *dbg;
+  ring_rows = ring_rows < kRingTok ? ring_rows : kRingTok;
+  if (mfma_ring() && min_rows <= ring_rows && max_active <= kRingExperts) {
+    // experts with min_rows..32 rows: the streaming kernel, (expert, 64- or 128-row) items,
+    // eight waves per CU
+    const int nw = mode == MF_GATE_UP ? kRingWaves<MF_GATE_UP> : kRingWaves<MF_DOWN>;
+    const int64_t upper = (int64_t)max_active * ((rows + 16 * nw - 1) / (16 * nw));
+    int64_t g = (int64_t)mfma_cus() * (8 / nw);
+    g = g < upper ? g : upper;
+    const int64_t gmin = (upper + kRingItems - 1) / kRingItems;
+    g = g > gmin ? g : gmin;
+    if (g > 0 && g < (1ll << 31)) {
+      MfmaArgs r = a;
+      r.max_rows = ring_rows;
+      hipError_t e;
+      if (mode == MF_GATE_UP) e = dbg ? launch_ring<MF_GATE_UP, true>(st, dim3((unsigned)g), r)
+                                      : launch_ring<MF_GATE_UP, false>(st, dim3((unsigned)g), r);
+      else e = dbg ? launch_ring<MF_DOWN, true>(st, dim3((unsigned)g), r)
+                   : launch_ring<MF_DOWN, false>(st, dim3((unsigned)g), r);
+      if (e != hipSuccess) return e;
+      if (max_rows <= ring_rows) return hipSuccess;
+      a.min_rows = ring_rows + 1;
+    }
+  }
   const int64_t rows_per_wg = 128;
   const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)max_active);
   if (mode == MF_GATE_UP) {
@@ -459,6 +843,7 @@ hipError_t launch_plain_mfma(hipStream_t st, const uint8_t *w, int64_t rows, int
   a.sumi = sumi;
   a.mins = mins;
   a.regime = REGIME_INT8;
+  a.max_rows = 1 << 30;
   const dim3 grid((unsigned)((rows + 127) / 128), (unsigned)((s_rows + kTok - 1) / kTok));
   if (sumi) KMOE_LAUNCH((k_moe_mfma<MF_SUMS>), grid, dim3(512), 0, st, a);
   else KMOE_LAUNCH((k_moe_mfma<MF_PLAIN>), grid, dim3(512), 0, st, a);

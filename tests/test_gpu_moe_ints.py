@@ -152,6 +152,20 @@ def test_headline_kernels_integers_bit_exact_extreme_ranges(ctx, orc):
     assert check_ints(orc, spec, 1, 0, h, *r) == 2
 
 
+def test_batch_kernels_integers_bit_exact_extreme_ranges(ctx, orc):
+    """Decode batch on the int8 path (24 tokens over 4 experts, top-2): the
+    streaming matrix-core kernel for experts with 5..32 rows, on blocks with
+    every byte 0xFF next to random ones and activations all +-127."""
+    spec = LayerSpec(4, 2, 1024, 2048, Q4_K, seed=5, quantized=False)
+    for parts in (spec.gate, spec.up, spec.down):
+        for w in parts:
+            plant_extremes(w, Q4_K)
+    h = np.where(orc.normal(9, 24 * 1024) < 0, -3.0, 3.0).astype(np.float32).reshape(24, 1024)
+    r = run_capture(ctx, orc, spec, 24, 1, h)
+    assert np.abs(r[1]["xq"]).min() == 127
+    assert check_ints(orc, spec, 24, 1, h, *r) > 0
+
+
 @pytest.mark.parametrize("S,regime,d,ff,E,k,types,seed", [
     (1, 0, 4096, 14336, 4, 2, (Q4_K, Q4_K), 1),   # tiled gate/up + split-K down, normal activations
     (1, 1, 4096, 8192, 8, 2, (Q4_K, Q6_K), 2),    # split-K down over tiled Q6_K rows
@@ -163,6 +177,8 @@ def test_headline_kernels_integers_bit_exact_extreme_ranges(ctx, orc):
     (40, 1, 1024, 512, 4, 2, (Q4_K, Q4_K), 8),    # int8 matrix cores
     (12, 1, 1024, 768, 8, 2, (Q4_K, Q6_K), 9),    # matrix cores (gate/up), LDS-staged kernel (Q6_K down)
     (16, 1, 2048, 768, 128, 8, (Q4_K, Q4_K), 10),  # Qwen3 shape
+    (24, 1, 1024, 768, 4, 2, (Q4_K, Q4_K), 12),   # streaming matrix-core kernel (<= 32 rows), 3 down superblocks
+    (32, 1, 2048, 1536, 8, 2, (Q4_K, Q4_K), 13),  # few-rows kernels up to 4 rows, streaming kernel above
     (9, 1, 1024, 512, 8, 2, (Q8_0, Q8_0), 11),    # LDS-staged kernels, Q8_0
 ])
 def test_moe_ffn_integers_bit_exact(ctx, orc, S, regime, d, ff, E, k, types, seed):
