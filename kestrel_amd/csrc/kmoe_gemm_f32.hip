@@ -13,6 +13,8 @@
 // alone give few work-groups (decode batches), the columns are split: each
 // split writes partial sums and a second kernel adds them in split order, so
 // results do not depend on timing.
+#include <type_traits>
+
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 
@@ -21,6 +23,26 @@ namespace kmoe {
 namespace {
 
 constexpr int TR = 64, KC = 64, PAD = 68;  // PAD: 16-byte aligned LDS rows
+
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>), in order.
+template <int I, int N>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F &&f) {
+    f(std::integral_constant<int, I>{});
+    Unroll<I + 1, N>::run(f);
+  }
+};
+template <int N>
+struct Unroll<N, N> {
+  template <class F>
+  __device__ __forceinline__ static void run(F &&) {}
+};
+template <int N, class F>
+__device__ __forceinline__ void unroll(F &&f) {
+  Unroll<0, N>::run(f);
+}
+
 
 struct GArgs {
   const uint8_t *w;  // plain
@@ -55,7 +77,10 @@ template <int TYPE, bool TILED>
 struct Raw16 {
   u32x4u2 a, b;    // Q4_K: header, nibbles; Q6_K: low bits, high bits; Q8_0: a = the 16 bytes
   uint32_t c, d;   // Q6_K: scale byte, f16 d; Q8_0: f16 d
-  float4 f[4];     // F32
+};
+template <bool TILED>
+struct Raw16<T_F32, TILED> {
+  float4 f[4];
 };
 
 template <int TYPE, bool TILED>
@@ -163,8 +188,9 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   constexpr bool TL = MODE != G_PLAIN;  // expert tier rows are tiled
   constexpr int PF = TN == 16 ? 4 : 2;
   constexpr int NX = TN / 16;  // activation float4 per thread and step; accumulator tiles per wave
-  __shared__ __attribute__((aligned(16))) float Ws[TR][PAD];
-  __shared__ __attribute__((aligned(16))) float Xs[TN][PAD];
+  constexpr int NB = TN == 16 ? 2 : 1;  // LDS buffers
+  __shared__ __attribute__((aligned(16))) float Ws[NB][TR][PAD];
+  __shared__ __attribute__((aligned(16))) float Xs[NB][TN][PAD];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t rows = a.rows, cols = a.cols;
@@ -209,76 +235,136 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
   const int drow = tid >> 2, dpart = tid & 3;
   const int xcol = (tid & 15) * 4;
   const float *xrow[NX];
-  bool xvalid[NX];
-#pragma unroll
-  for (int u = 0; u < NX; ++u) {
-    const int xt = (tid >> 4) + 16 * u;
-    xvalid[u] = j0 + xt < n;
-    xrow[u] = a.x + (xvalid[u] ? act_row(j0 + xt) : 0) * cols + xcol;
-  }
-  const bool wvalid = r0 + drow < rows;
-  const uint8_t *wrow = W + (wvalid ? r0 + drow : 0) * row_bytes;
-
-  // the raw bytes of the next PF column chunks are in flight (a ring of
-  // registers, refilled as each chunk is converted)
-  Raw16<TYPE, TL> raw[PF];
-  float4 xr[PF][NX];
-#pragma unroll
-  for (int d = 0; d < PF; ++d) {
-#pragma unroll
-    for (int u = 0; u < NX; ++u) xr[d][u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c_begin + d < c_end) {
-      if (wvalid) raw[d] = load16<TYPE, TL>(wrow, c_begin + d, dpart, nb);
-#pragma unroll
-      for (int u = 0; u < NX; ++u)
-        if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (c_begin + d) * KC);
+  f32x4 acc[NX][2];  // TN == 16: even and odd column quads, added at the end; TN == 64: [0] only
+  if constexpr (TN == 16) {
+    // Rows past the end repeat the last row, token rows past n the last
+    // token row, chunks past the split's end its last chunk: every load is
+    // unconditional, so the compiler's wait counts stay exact and the ring of
+    // PF chunks stays in flight (results of the padding are never stored).
+    const uint8_t *wrow = W + (r0 + drow < rows ? r0 + drow : rows - 1) * row_bytes;
+    {
+      const int xt = tid >> 4;
+      xrow[0] = a.x + act_row(j0 + xt < n ? j0 + xt : n - 1) * cols + xcol;
     }
-  }
-  f32x4 acc[NX];
+    Raw16<TYPE, TL> raw[PF];
+    float4 xr[PF];
+    auto fetch = [&](auto D, int64_t kc) {  // ring slot D <- chunk kc
+      constexpr int d = decltype(D)::value;
+      const int64_t kk = kc < c_end ? kc : c_end - 1;
+      raw[d] = load16<TYPE, TL>(wrow, kk, dpart, nb);
+      xr[d] = *(const float4 *)(xrow[0] + kk * KC);
+    };
+    unroll<PF>([&](auto D) { fetch(D, c_begin + decltype(D)::value); });
+    // Two LDS buffers: chunk kc is multiplied from buffer (kc - c_begin) & 1
+    // while the next chunk is converted into the other, one barrier per
+    // chunk. stage: chunk kc (ring slot D) to buffer b, then slot D <- chunk
+    // kc + PF.
+    auto stage = [&](auto D, int64_t kc, int b) {
+      constexpr int d = decltype(D)::value;
+      float wv[16];
+      convert16<TYPE, TL>(raw[d], kc < c_end ? kc : c_end - 1, dpart, wv);
+      const float4 xc = xr[d];
+      fetch(D, kc + PF);
+      float4 *wd = (float4 *)&Ws[b][drow][dpart * 16];
 #pragma unroll
-  for (int u = 0; u < NX; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float4 *wa = (const float4 *)&Ws[16 * wave + (lane & 15)][16 * (lane >> 4)];
-
-  for (int64_t k0 = c_begin; k0 < c_end; k0 += PF) {
+      for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+      *(float4 *)&Xs[b][tid >> 4][xcol] = xc;
+    };
+    acc[0][0] = acc[0][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    stage(std::integral_constant<int, 0>{}, c_begin, 0);
+    lds_barrier();
+    for (int64_t k0 = c_begin; k0 < c_end; k0 += PF) {
+      unroll<PF>([&](auto D) {
+        constexpr int d = decltype(D)::value;
+        constexpr int b = d & 1;  // (k0 - c_begin) is a multiple of PF, which is even
+        if (k0 + d < c_end) {
+          const float4 *wa = (const float4 *)&Ws[b][16 * wave + (lane & 15)][16 * (lane >> 4)];
 #pragma unroll
-    for (int d = 0; d < PF; ++d) {
-      const int64_t kc = k0 + d;
-      if (kc < c_end) {
-        float wv[16];
-        if (wvalid) {
-          convert16<TYPE, TL>(raw[d], kc, dpart, wv);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) wv[i] = 0.0f;
-        }
-        float4 xc[NX];
-#pragma unroll
-        for (int u = 0; u < NX; ++u) xc[u] = xr[d][u];
-        if (kc + PF < c_end) {  // refill this slot with chunk kc + PF
-          if (wvalid) raw[d] = load16<TYPE, TL>(wrow, kc + PF, dpart, nb);
-#pragma unroll
-          for (int u = 0; u < NX; ++u)
-            if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (kc + PF) * KC);
-        }
-        float4 *wd = (float4 *)&Ws[drow][dpart * 16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
-#pragma unroll
-        for (int u = 0; u < NX; ++u) *(float4 *)&Xs[(tid >> 4) + 16 * u][xcol] = xc[u];
-        __syncthreads();
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const float4 A = wa[m];
-#pragma unroll
-          for (int u = 0; u < NX; ++u) {
-            const float4 B = ((const float4 *)&Xs[16 * u + (lane & 15)][16 * (lane >> 4)])[m];
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, acc[u], 0, 0, 0);
+          for (int m = 0; m < 4; ++m) {
+            const float4 A = wa[m];
+            const float4 B = ((const float4 *)&Xs[b][lane & 15][16 * (lane >> 4)])[m];
+            f32x4 &c = acc[0][m & 1];
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, c, 0, 0, 0);
           }
         }
-        __syncthreads();
+        stage(std::integral_constant<int, (d + 1) % PF>{}, k0 + d + 1, b ^ 1);
+        lds_barrier();
+      });
+    }
+  } else {
+    bool xvalid[NX];
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+      const int xt = (tid >> 4) + 16 * u;
+      xvalid[u] = j0 + xt < n;
+      xrow[u] = a.x + (xvalid[u] ? act_row(j0 + xt) : 0) * cols + xcol;
+    }
+    const bool wvalid = r0 + drow < rows;
+    const uint8_t *wrow = W + (wvalid ? r0 + drow : 0) * row_bytes;
+
+    // the raw bytes of the next PF column chunks are in flight (a ring of
+    // registers, refilled as each chunk is converted)
+    Raw16<TYPE, TL> raw[PF];
+    float4 xr[PF][NX];
+  #pragma unroll
+    for (int d = 0; d < PF; ++d) {
+  #pragma unroll
+      for (int u = 0; u < NX; ++u) xr[d][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c_begin + d < c_end) {
+        if (wvalid) raw[d] = load16<TYPE, TL>(wrow, c_begin + d, dpart, nb);
+  #pragma unroll
+        for (int u = 0; u < NX; ++u)
+          if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (c_begin + d) * KC);
+      }
+    }
+  #pragma unroll
+    for (int u = 0; u < NX; ++u) acc[u][0] = acc[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float4 *wa = (const float4 *)&Ws[0][16 * wave + (lane & 15)][16 * (lane >> 4)];
+
+    for (int64_t k0 = c_begin; k0 < c_end; k0 += PF) {
+  #pragma unroll
+      for (int d = 0; d < PF; ++d) {
+        const int64_t kc = k0 + d;
+        if (kc < c_end) {
+          float wv[16];
+          if (wvalid) {
+            convert16<TYPE, TL>(raw[d], kc, dpart, wv);
+          } else {
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) wv[i] = 0.0f;
+          }
+          float4 xc[NX];
+  #pragma unroll
+          for (int u = 0; u < NX; ++u) xc[u] = xr[d][u];
+          if (kc + PF < c_end) {  // refill this slot with chunk kc + PF
+            if (wvalid) raw[d] = load16<TYPE, TL>(wrow, kc + PF, dpart, nb);
+  #pragma unroll
+            for (int u = 0; u < NX; ++u)
+              if (xvalid[u]) xr[d][u] = *(const float4 *)(xrow[u] + (kc + PF) * KC);
+          }
+          float4 *wd = (float4 *)&Ws[0][drow][dpart * 16];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) wd[i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+  #pragma unroll
+          for (int u = 0; u < NX; ++u) *(float4 *)&Xs[0][(tid >> 4) + 16 * u][xcol] = xc[u];
+          __syncthreads();
+  #pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const float4 A = wa[m];
+  #pragma unroll
+            for (int u = 0; u < NX; ++u) {
+              const float4 B = ((const float4 *)&Xs[0][16 * u + (lane & 15)][16 * (lane >> 4)])[m];
+              acc[u][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.x, B.x, acc[u][0], 0, 0, 0);
+              acc[u][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.y, B.y, acc[u][0], 0, 0, 0);
+              acc[u][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.z, B.z, acc[u][0], 0, 0, 0);
+              acc[u][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(A.w, B.w, acc[u][0], 0, 0, 0);
+            }
+          }
+          __syncthreads();
+        }
       }
     }
   }
@@ -294,7 +380,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int64_t r = r0 + 16 * wave + 4 * (lane >> 4) + v;
       if (r >= rows) continue;
-      const float y = acc[u][v];
+      const float y = TN == 16 ? acc[u][0][v] + acc[u][1][v] : acc[u][0][v];
       if (ksn > 1) {
         a.part[((int64_t)ks * a.n_slots + slot) * rows + r] = y;
       } else if constexpr (MODE == G_PLAIN || MODE == G_GATE || MODE == G_DOWN) {
