@@ -525,49 +525,63 @@ __global__ void __launch_bounds__(kRingWaves<MODE> * 64, 2) k_moe_mfma_ring(Mfma
   uint8_t *const myscr = scr[wave];
   const int T = nI * SPI;
   const int part_off = MODE == MF_DOWN ? grp * kSB : 0;
-  // Coalesced weight loads. Run rho = 32*h + r is half h of row r's nibble
-  // chunks of the stage's superblock (64 contiguous bytes of the tiled row);
-  // load i takes runs 16*i .. 16*i+15, four lanes per run. The heads load
-  // takes row lane % 32's 16-byte head (the two halves of the wave load the
-  // same rows).
   u32x4 wc[NS][4], wh[NS];
   int ik = 0, ib = 0;  // next stage to issue (item, stage in the item); clamped at the last
+  // Per-lane base pointers of the item being issued, recomputed when the
+  // issue cursor enters a new item; a stage then adds scalar offsets only.
+  int ci = -1;
+  const uint8_t *pWA = nullptr, *pWB = nullptr, *pH = nullptr;
+  const float *pAd = nullptr;
+  const int8_t *pA8[NA8];
+  const int32_t *pS16[NB16];
   auto issue = [&](int slot) {
     const int k = ik < nI ? ik : nI - 1, b = ik < nI ? ib : SPI - 1;
     const bool adv = ik < nI, wrap = ib + 1 == SPI;  // selects, not branches: the cursor stays in registers
     ik = adv && wrap ? ik + 1 : ik;
     ib = adv ? (wrap ? 0 : ib + 1) : ib;
-    const uint8_t *E = a.tier.base + (int64_t)it_e[k] * a.tier.stride + a.tier.off[mat];
-    const int64_t r0 = (int64_t)it_rb[k] * RI + tile * 32;
-    auto rowp = [&](int r) {
-      const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
-      return E + rr * row_bytes;
-    };
+    if (k != ci) {
+      ci = k;
+      const uint8_t *E = a.tier.base + (int64_t)it_e[k] * a.tier.stride + a.tier.off[mat];
+      const int64_t r0 = (int64_t)it_rb[k] * RI + tile * 32;
+      auto rowp = [&](int r) {
+        const int64_t rr = r0 + r < rows ? r0 + r : rows - 1;
+        return E + rr * row_bytes;
+      };
+      pWA = rowp(lane >> 2) + 16 * (lane & 3);
+      pWB = rowp(16 + (lane >> 2)) + 16 * (lane & 3);
+      pH = rowp(l32);
+      pAd = a.ad + (int64_t)it_src[k][l32] * nb;
+#pragma unroll
+      for (int i2 = 0; i2 < NA8; ++i2) {
+        const int t = 4 * (wig * NA8 + i2) + (lane >> 4);
+        pA8[i2] = a.aq + (int64_t)it_src[k][t] * cols + 16 * ((lane & 15) ^ (t & 7));
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < NB16; ++i2)
+        pS16[i2] = a.abs + (int64_t)it_src[k][4 * (wig * NB16 + i2) + (lane >> 4)] * (cols / 16) + (lane & 15);
+    }
     const int64_t bq = b_lo + b < nb ? b_lo + b : nb - 1;
-    const uint8_t *WA = rowp(lane >> 2), *WB = rowp(16 + (lane >> 2));
+    // Coalesced weight loads. Run rho = 32*h + r is half h of row r's nibble
+    // chunks of the stage's superblock (64 contiguous bytes of the tiled
+    // row); load i takes runs 16*i .. 16*i+15, four lanes per run. The heads
+    // load takes row lane % 32's 16-byte head (the two halves of the wave
+    // load the same rows).
 #pragma unroll
     for (int i = 0; i < 4; ++i)  // runs 16*i + lane/4: row (i & 1)*16 + lane/4, half i/2
-      wc[slot][i] = *(const u32x4 *)(((i & 1) ? WB : WA) + tq4_qs_off(nb, bq, 0, i >> 1) + 16 * (lane & 3));
-    wh[slot] = *(const u32x4 *)(rowp(l32) + 16 * bq);
+      wc[slot][i] = *(const u32x4 *)(((i & 1) ? pWB : pWA) + tq4_qs_off(nb, bq, 0, i >> 1));
+    wh[slot] = *(const u32x4 *)(pH + 16 * bq);
     // block scales: lane -> row lane % 32
-    __builtin_amdgcn_global_load_lds(a.ad + (int64_t)it_src[k][l32] * nb + bq,
-                                     (__attribute__((address_space(3))) void *)(stg[slot] + kAd + wave * 256), 4, 0,
-                                     0);
+    __builtin_amdgcn_global_load_lds(pAd + bq, (__attribute__((address_space(3))) void *)(stg[slot] + kAd + wave * 256),
+                                     4, 0, 0);
     uint8_t *S = stg[slot] + part_off;
 #pragma unroll
-    for (int i2 = 0; i2 < NA8; ++i2) {  // rows 4i .. 4i+3, 16 lanes each (piece p at slot p ^ (t & 7))
-      const int i = wig * NA8 + i2;
-      const int t = 4 * i + (lane >> 4);
-      const int64_t src = it_src[k][t];
-      lds_dma16(a.aq + src * cols + 256 * bq + 16 * ((lane & 15) ^ (t & 7)), S + i * 1024);
-    }
+    for (int i2 = 0; i2 < NA8; ++i2)  // rows 4i .. 4i+3, 16 lanes each (piece p at slot p ^ (t & 7))
+      lds_dma16(pA8[i2] + 256 * bq, S + (wig * NA8 + i2) * 1024);
 #pragma unroll
-    for (int i2 = 0; i2 < NB16; ++i2) {  // 16-sums of rows 4i .. 4i+3
-      const int i = wig * NB16 + i2;
-      const int64_t src_s = it_src[k][4 * i + (lane >> 4)];
-      __builtin_amdgcn_global_load_lds(a.abs + src_s * (cols / 16) + 16 * bq + (lane & 15),
-                                       (__attribute__((address_space(3))) void *)(S + kA8 + i * 256), 4, 0, 0);
-    }
+    for (int i2 = 0; i2 < NB16; ++i2)  // 16-sums of rows 4i .. 4i+3
+      __builtin_amdgcn_global_load_lds(pS16[i2] + 16 * bq,
+                                       (__attribute__((address_space(3))) void *)(S + kA8 + (wig * NB16 + i2) * 256),
+                                       4, 0, 0);
   };
 
   float y[16];
@@ -761,9 +775,9 @@ bool mfma_ring() {
 
 template <int MODE, bool DBG>
 hipError_t launch_ring(hipStream_t st, dim3 grid, const MfmaArgs &a) {
-  static const int ns = [] {
+  static const int ns = [] {  // KMOE_MFMA_RING_NS: stages in flight plus one (2, default, or 3)
     const char *e = getenv("KMOE_MFMA_RING_NS");
-    return e && *e && atoi(e) == 2 ? 2 : 3;
+    return e && *e && atoi(e) == 3 ? 3 : 2;
   }();
   if (ns == 2) KMOE_LAUNCH((k_moe_mfma_ring<MODE, 2, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
   else KMOE_LAUNCH((k_moe_mfma_ring<MODE, 3, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
