@@ -412,8 +412,10 @@ def matvec_leg(ctx, torch, wtype: int = Q4_K, pool_bytes: float = 2.2e9, cpu_sec
         ms_q, n_q = ctx.profile_read("quant_q8k")
         ctx.profile_enable(False)
         k_us = ms_k * 1e3 / max(1, n_k)
-        # algorithmic bytes of the kernel: the weights, the Q8_K row (cols + cols/16*4 + cols/256*4) and out
-        kb = nbytes + cols + cols // 16 * 4 + cols // 256 * 4 + rows * 4
+        # algorithmic bytes of the kernel: the weights, the Q8_K row (cols + cols/16*4 + cols/256*4) and out;
+        # when no quantization kernel ran, the kernel read the f32 row (cols*4) and quantized it itself
+        xb = cols * 4 if n_q == 0 else cols + cols // 16 * 4 + cols // 256 * 4
+        kb = nbytes + xb + rows * 4
         row = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1), "frac": round(b / t / 1e9 / HBM_PEAK_GBPS, 4),
                "pool_copies": copies,
                "kernel": {"name": kname, "avg_us": round(k_us, 3), "alg_bytes": kb,

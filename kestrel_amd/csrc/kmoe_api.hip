@@ -550,6 +550,18 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
     LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out, qr.part, qr.part_floats));
     return KMOE_OK;
   }
+  // One row of at most 4096 columns: Q8_K of x inside the matvec kernel (every
+  // work-group quantizes the row into LDS), no kernel before it. Measured:
+  // 4096x4096 6.5 -> 5.3 µs, 14336x4096 13.9 -> 12.4 µs per call; at 14336
+  // columns the per-work-group quantization (56 KB of x each) made it slower
+  // (13.6 -> 16.7 µs), so wider rows keep the separate quantization.
+  if (t == KMOE_Q4_K && s_rows == 1 && cols <= 4096) {
+    const hipError_t e = timed(c, "matvec_q4k", [&]() {
+      return launch_dec_rows(c->stream, false, w, rows, cols, nullptr, nullptr, nullptr, out, nullptr, x);
+    });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
   if (is_kq(t)) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   return matvec_q8_impl(c, t, w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);

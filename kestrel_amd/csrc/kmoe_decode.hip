@@ -181,19 +181,41 @@ struct RowsArgs {
   int32_t groups;  // work-groups striding over the rows
   int32_t add;     // out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
   const float *add_logit;
+  const float *xf;  // FX kernels: the f32 row, quantized to Q8_K inside the kernel
 };
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
-template <bool TILED, int TPL, int RU>
+// FX: the f32 activation row is quantized to Q8_K inside the kernel instead
+// of by a kernel before it (Q8KRow::quantize, qdot.rs:347-367, the same
+// arithmetic as k_quant_q8k). Every work-group quantizes the whole row into
+// LDS: thread t loads float4 t + 256*i (block wave + 4i, four values per
+// lane), those loads issued before the first row step's weight loads, so the
+// quantization runs while the weights are in flight.
+constexpr int kFxMaxBlocks = 64;  // Q8_K blocks of the row (cols <= 16384)
+
+template <bool TILED, int TPL, int RU, bool FX>
 __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nb = a.cols / 256, ntasks = 4 * nb;
   const int64_t row_bytes = nb * 144;
+  constexpr int XB = FX ? 4 * TPL : 1;  // FX: blocks per wave (nb <= 16 * TPL)
+  __shared__ __attribute__((aligned(16))) int8_t fq[FX ? kFxMaxBlocks * 256 : 16];
+  __shared__ float fd[FX ? kFxMaxBlocks : 1];
+  __shared__ __attribute__((aligned(16))) int32_t fbs[FX ? kFxMaxBlocks * 16 : 4];
+  float4 xv4[XB];
+  if constexpr (FX) {
+#pragma unroll
+    for (int i = 0; i < XB; ++i) {  // block wave + 4i (clamped to the last; only blocks < nb are kept)
+      const int64_t b = wave + 4 * i < nb ? wave + 4 * i : nb - 1;
+      xv4[i] = *(const float4 *)(a.xf + 256 * b + 4 * lane);
+    }
+  }
   uint32_t oh[TPL], oa[TPL], ob[TPL];
   bool tv[TPL];
-  Slice s[TPL];
+  int64_t tsb[TPL];
+  int tk[TPL];
 #pragma unroll
   for (int i = 0; i < TPL; ++i) {
     const int64_t t0 = lane + 64 * i;
@@ -201,6 +223,8 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
     const int64_t t = tv[i] ? t0 : ntasks - 1;
     const int64_t sb = t >> 2;
     const int k = (int)(t & 3);
+    tsb[i] = sb;
+    tk[i] = k;
     if constexpr (TILED) {
       oh[i] = (uint32_t)(16 * sb);
       oa[i] = (uint32_t)tq4_qs_off(nb, sb, k, 0);
@@ -210,16 +234,23 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
       oa[i] = oh[i] + 16 + 32 * k;
       ob[i] = oa[i] + 16;
     }
-    const int4 *xv = (const int4 *)(a.xq + 256 * sb + 64 * k);
-    s[i].x0 = xv[0];
-    s[i].x1 = xv[1];
-    s[i].x2 = xv[2];
-    s[i].x3 = xv[3];
-    const int4 bs = *(const int4 *)(a.xbs + 16 * sb + 4 * k);
-    s[i].bsA = bs.x + bs.y;
-    s[i].bsB = bs.z + bs.w;
-    s[i].d = a.xd[sb];
   }
+  Slice s[TPL];
+  auto slices = [&](const int8_t *xq, const float *xd, const int32_t *xbs) {
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      const int4 *xv = (const int4 *)(xq + 256 * tsb[i] + 64 * tk[i]);
+      s[i].x0 = xv[0];
+      s[i].x1 = xv[1];
+      s[i].x2 = xv[2];
+      s[i].x3 = xv[3];
+      const int4 bs = *(const int4 *)(xbs + 16 * tsb[i] + 4 * tk[i]);
+      s[i].bsA = bs.x + bs.y;
+      s[i].bsB = bs.z + bs.w;
+      s[i].d = xd[tsb[i]];
+    }
+  };
+  if constexpr (!FX) slices(a.xq, a.xd, a.xbs);
   const int kq = lane & 3;
   const int64_t rows = a.rows;
   float add_scale = 1.0f;  // the shared expert's gate (k_shared_add's arithmetic)
@@ -227,8 +258,7 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
     const float den = 1.0f + expf_cr(-*a.add_logit);
     add_scale = 1.0f / den;
   }
-  for (int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU; r0 < rows; r0 += (int64_t)a.groups * 4 * RU) {
-    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
+  auto load = [&](int64_t r0, u32x4 (&hw)[RU][TPL], u32x4 (&aw)[RU][TPL], u32x4 (&bw)[RU][TPL]) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const uint8_t *row = a.W + (r0 + u < rows ? r0 + u : rows - 1) * row_bytes;
@@ -245,6 +275,9 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
         }
       }
     }
+  };
+  auto reduce_store = [&](int64_t r0, const u32x4 (&hw)[RU][TPL], const u32x4 (&aw)[RU][TPL],
+                          const u32x4 (&bw)[RU][TPL]) {
     float res = 0.0f;  // lane u < RU: row r0+u
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
@@ -268,6 +301,28 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
         a.out[r0 + lane] = res;
       }
     }
+  };
+  const int64_t stride = (int64_t)a.groups * 4 * RU;
+  int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU;
+  if constexpr (FX) {
+    // first row step's weights in flight (rows clamped), then the row's Q8_K
+    // blocks into LDS, then the slices from there; every wave takes part
+    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
+    load(r0, hw, aw, bw);
+#pragma unroll
+    for (int i = 0; i < XB; ++i) {
+      const int b = wave + 4 * i;
+      if (b < nb) wave_quant_q8k_vals(xv4[i], fq + 256 * b, fd + b, fbs + 16 * b, lane);
+    }
+    __syncthreads();
+    slices(fq, fd, fbs);
+    if (r0 < rows) reduce_store(r0, hw, aw, bw);
+    r0 += stride;
+  }
+  for (; r0 < rows; r0 += stride) {
+    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
+    load(r0, hw, aw, bw);
+    reduce_store(r0, hw, aw, bw);
   }
 }
 
@@ -280,31 +335,33 @@ bool dec_rows_supported(int64_t cols) {
 }
 
 hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
-                           const float *xd, const int32_t *xbs, float *out, const AddEpi *epi) {
+                           const float *xd, const int32_t *xbs, float *out, const AddEpi *epi, const float *xf) {
   if (rows <= 0) return hipSuccess;
-  if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u) || (tiled && ((uintptr_t)w & 15u)) || ((uintptr_t)xq & 15u) ||
-      ((uintptr_t)xbs & 15u))
+  if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u) || (tiled && ((uintptr_t)w & 15u)))
+    return hipErrorNotSupported;
+  if (xf ? (((uintptr_t)xf & 15u) || cols / 256 > kFxMaxBlocks) : (((uintptr_t)xq & 15u) || ((uintptr_t)xbs & 15u)))
     return hipErrorNotSupported;
   const int tpl = (int)((4 * (cols / 256) + 63) / 64);
   const int ru = tpl <= 2 ? 2 : 1;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0, epi ? 1 : 0, epi ? epi->logit : nullptr};
+  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0, epi ? 1 : 0, epi ? epi->logit : nullptr, xf};
   // work-group steps of 4*RU rows, spread evenly over about two groups per CU
   const int64_t need = (rows + 4 * ru - 1) / (4 * ru);
   const int64_t cap = 2LL * cus;
   const int64_t per = (need + cap - 1) / cap;
   a.groups = (int32_t)((need + per - 1) / per);
   const dim3 grid((unsigned)a.groups);
-#define KMOE_DEC_ROWS(TL)                                                                      \
+#define KMOE_DEC_ROWS(TL, FX)                                                                  \
   do {                                                                                         \
-    if (tpl == 1) KMOE_LAUNCH((k_dec_rows<TL, 1, 2>), grid, dim3(256), 0, st, a);              \
-    else if (tpl == 2) KMOE_LAUNCH((k_dec_rows<TL, 2, 2>), grid, dim3(256), 0, st, a);         \
-    else if (tpl == 3) KMOE_LAUNCH((k_dec_rows<TL, 3, 1>), grid, dim3(256), 0, st, a);         \
-    else KMOE_LAUNCH((k_dec_rows<TL, 4, 1>), grid, dim3(256), 0, st, a);                       \
+    if (tpl == 1) KMOE_LAUNCH((k_dec_rows<TL, 1, 2, FX>), grid, dim3(256), 0, st, a);          \
+    else if (tpl == 2) KMOE_LAUNCH((k_dec_rows<TL, 2, 2, FX>), grid, dim3(256), 0, st, a);     \
+    else if (tpl == 3) KMOE_LAUNCH((k_dec_rows<TL, 3, 1, FX>), grid, dim3(256), 0, st, a);     \
+    else KMOE_LAUNCH((k_dec_rows<TL, 4, 1, FX>), grid, dim3(256), 0, st, a);                   \
   } while (0)
-  if (tiled) KMOE_DEC_ROWS(true);
-  else KMOE_DEC_ROWS(false);
+  if (xf) KMOE_DEC_ROWS(false, true);  // GGUF rows of kmoe_matmul
+  else if (tiled) KMOE_DEC_ROWS(true, false);
+  else KMOE_DEC_ROWS(false, false);
 #undef KMOE_DEC_ROWS
   return hipGetLastError();
 }

@@ -174,6 +174,10 @@ def test_matvec_decode_matches_oracle(ctx, orc, t, rows, cols):
     q, d, s = qf(x)
     out2 = host(ctx.matvec_q8(t, dev(w), rows, cols, dev(q), dev(d), dev(s)))
     assert rel_l2(out2, ref) < 1e-5
+    # the activation row's quantization is bit-exact wherever it runs (its own
+    # kernel, or inside the Q4_K matvec for rows of at most 4096 columns), so
+    # the whole call equals the matvec on the oracle's bytes bit for bit
+    assert np.array_equal(out, out2)
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q8_0, Q6_K])
