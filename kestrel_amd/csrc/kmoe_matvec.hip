@@ -1279,6 +1279,12 @@ int gu_ru() {
   static const int v = env_int("KMOE_GU_RU", 2);
   return v;
 }
+// Register gate/up kernel (rows too narrow for the tiled kernel):
+// KMOE_REG_GU_RU rows per lane group and step (1 or 2, default 1).
+int reg_gu_ru() {
+  static const int v = env_int("KMOE_REG_GU_RU", 1);
+  return v;
+}
 int gu_wgpc16() {
   static const int v = env_int("KMOE_GU_WGPC16", 32);
   return v;
@@ -1529,6 +1535,7 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
     const hipError_t e =
         launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel, dbg);
     if (e != hipErrorNotSupported) return e;
+    if (reg_gu_ru() == 1) return dispatch_reg<T_Q4_K, M_GATE_UP, 1>(st, a, max_active);
     return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
   }
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
