@@ -1285,6 +1285,12 @@ int reg_gu_ru() {
   static const int v = env_int("KMOE_REG_GU_RU", 1);
   return v;
 }
+// One-row register matvec (decode_plain): KMOE_REG_RU rows per lane group
+// and step (1 or 2, default 1).
+int reg_plain_ru() {
+  static const int v = env_int("KMOE_REG_RU", 1);
+  return v;
+}
 int gu_wgpc16() {
   static const int v = env_int("KMOE_GU_WGPC16", 32);
   return v;
@@ -1495,10 +1501,17 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   if (type == T_Q4_K) {
     const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out, epi);
     if (e != hipErrorNotSupported) return e;
+    if (reg_plain_ru() == 1) return dispatch_reg<T_Q4_K, M_PLAIN, 1>(st, a, 1);
     return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
   }
-  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_PLAIN, 2>(st, a, 1);
-  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
+  if (type == T_Q6_K) {
+    if (reg_plain_ru() == 1) return dispatch_reg<T_Q6_K, M_PLAIN, 1>(st, a, 1);
+    return dispatch_reg<T_Q6_K, M_PLAIN, 2>(st, a, 1);
+  }
+  if (type == T_Q8_0) {
+    if (reg_plain_ru() == 1) return dispatch_reg<T_Q8_0, M_PLAIN, 1>(st, a, 1);
+    return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
+  }
   return hipErrorInvalidValue;
 }
 
