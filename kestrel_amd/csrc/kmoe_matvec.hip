@@ -1291,6 +1291,12 @@ int reg_plain_ru() {
   static const int v = env_int("KMOE_REG_RU", 1);
   return v;
 }
+// q/k/v projection with RoPE (register kernel): KMOE_QKV_RU rows per lane
+// group and step (1 or 2, default 1).
+int qkv_ru() {
+  static const int v = env_int("KMOE_QKV_RU", 1);
+  return v;
+}
 int gu_wgpc16() {
   static const int v = env_int("KMOE_GU_WGPC16", 32);
   return v;
@@ -1561,6 +1567,14 @@ static hipError_t launch_qkv_reg(hipStream_t st, const MvArgs &a) {
   const int ntasks = (int)(QT<TYPE>::TPB * (a.cols / QT<TYPE>::EL));
   int lpr, tpl;
   if (!reg_geometry(TYPE, ntasks, lpr, tpl)) return hipErrorNotSupported;
+  // Rows 2i and 2i+1 sit in one wave at every step for RU 1 and 2: a step's
+  // first row r0 - row_in_wave is a multiple of 64 / LPR.
+  if (qkv_ru() == 1) {
+    const int64_t t32 = (a.rows + 4 * 2 - 1) / (4 * 2), t16 = (a.rows + 4 * 4 - 1) / (4 * 4);
+    if (lpr == 32) return launch_reg<TYPE, 32, 1, 1, M_QKV>(st, a, tpl, t32);
+    if (lpr == 16) return launch_reg<TYPE, 16, 1, 1, M_QKV>(st, a, tpl, t16);
+    return hipErrorNotSupported;  // one row per wave step: pairs not in one wave
+  }
   const int64_t tasks32 = (a.rows + 4 * 2 * 2 - 1) / (4 * 2 * 2), tasks16 = (a.rows + 4 * 4 * 2 - 1) / (4 * 4 * 2);
   if (lpr == 32) return launch_reg<TYPE, 32, 1, 2, M_QKV>(st, a, tpl, tasks32);
   if (lpr == 16) return launch_reg<TYPE, 16, 1, 2, M_QKV>(st, a, tpl, tasks16);
