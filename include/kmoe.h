@@ -1,7 +1,7 @@
 /*
  * kmoe.h — C ABI of the MI355X (gfx950) MoE FFN hot path.
  *
- * This is the seam a Rust FFI crate binds. It replaces,
+ * This is the seam a Rust FFI crate (kestrel-hip-sys) binds. It replaces,
  * behind kestrel's unchanged InferenceSession trait
  * (crates/kestrel-backends/src/lib.rs:60-74):
  *   - quant::matmul                (crates/kestrel-engine/src/quant.rs:229)
