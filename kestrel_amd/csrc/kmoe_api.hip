@@ -426,15 +426,6 @@ bool is_device_ptr(const void *p) {
 }
 
 bool supported_weight(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K || t == KMOE_Q8_0; }
-// The few-rows kernels for decode batches run unless KMOE_SMALL=0.
-bool small_enabled() {
-  static const bool on = [] {
-    const char *v = getenv("KMOE_SMALL");
-    return !(v && v[0] == '0');
-  }();
-  return on;
-}
-
 // K-quants take Q8_K activations (quant.rs:262-281); Q8_0 takes Q8 rows.
 bool is_kq(int t) { return t == KMOE_Q4_K || t == KMOE_Q6_K; }
 
@@ -481,7 +472,7 @@ bool int_path(int regime, int64_t s_rows) {
 int matvec_q8_impl(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *q, const float *d,
                    const int32_t *s, int64_t s_rows, float *out) {
   const char *name = t == KMOE_Q4_K ? "matvec_q4k" : (t == KMOE_Q6_K ? "matvec_q6k" : "matvec_q8_0");
-  if (t == KMOE_Q4_K && s_rows >= mfma_min_rows()) {  // int8 matrix cores
+  if (t == KMOE_Q4_K && s_rows >= kMfmaMinRows) {  // int8 matrix cores
     hipError_t e = timed(c, "matvec_q4k_mfma", [&]() {
       return launch_plain_mfma(c->stream, w, rows, cols, q, d, s, s_rows, out, nullptr, nullptr);
     });
@@ -776,7 +767,7 @@ int kmoe_q4k_block_sums(kmoe_ctx *c, const void *w, int64_t rows, int64_t cols, 
   if (rows == 0 || s_rows == 0) return KMOE_OK;
   if (!w || !q || !bs || !sumi || !mins) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
-  if (s_rows >= mfma_min_rows()) {  // the matrix-core kernel's integers (same rows as the matmul above)
+  if (s_rows >= kMfmaMinRows) {  // the matrix-core kernel's integers (same rows as the matmul above)
     hipError_t e = timed(c, "block_sums_q4k_mfma", [&]() {
       return launch_plain_mfma(c->stream, (const uint8_t *)w, rows, cols, q, nullptr, bs, s_rows, nullptr, sumi,
                                mins);
@@ -1426,7 +1417,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   // Int8 regime with many token rows: grouped products on the int8 matrix cores;
   // while experts average at most 20 rows, those with at most 32 take the
   // streaming kernel (more rows per expert leave too many on the other one).
-  const bool mfma = regime == KMOE_REGIME_INT8 && S >= mfma_min_rows();
+  const bool mfma = regime == KMOE_REGIME_INT8 && S >= kMfmaMinRows;
   const int ring_rows = slots <= 20 * E ? 32 : 0;
 
   // Single token, int8 path: every routed expert has one row. gate/up+SwiGLU
@@ -1486,7 +1477,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   }
   // Experts with a few rows on the int path (decode batches), tiled Q4_K:
   // the few-rows kernels; experts with more rows take the kernels after them.
-  const bool small_ok = small_enabled() && S >= 2;
+  const bool small_ok = S >= 2;
   // expert gate/up + SwiGLU (transformer.rs:551-558)
   if (any_int) {
     if (!x_quantized) {

@@ -366,19 +366,23 @@ hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t
   return hipGetLastError();
 }
 
-bool dec_gate_up_tq4_supported(int64_t cols, int ru) {
+// Launch shape of the tiled gate/up kernel (measured best on the Mixtral and
+// DeepSeek-V2-Lite shapes): 2 rows per wave step, 2 work-groups per CU.
+constexpr int kGuRu = 2;
+constexpr int kGuWgPerCu = 2;
+
+bool dec_gate_up_tq4_supported(int64_t cols) {
   if (cols % 256 != 0) return false;
   const int64_t ntasks = 4 * (cols / 256);
   const int tpl = (int)((ntasks + 63) / 64);
   // a row must fill most of the wave (narrower rows use the lanes-per-row kernels)
-  return ntasks >= 48 && tpl <= 2 && !(tpl == 2 && ru > 2) && (ru == 1 || ru == 2 || ru == 4);
+  return ntasks >= 48 && tpl <= 2;
 }
 
 hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols,
                                   const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                  const int32_t *xbs, float *h, int ru, int wg_per_cu_x16, const DecSelect *sel,
-                                  const BlockDbg *dbg) {
-  if (rows <= 0 || max_active <= 0 || !dec_gate_up_tq4_supported(cols, ru)) return hipErrorNotSupported;
+                                  const int32_t *xbs, float *h, const DecSelect *sel, const BlockDbg *dbg) {
+  if (rows <= 0 || max_active <= 0 || !dec_gate_up_tq4_supported(cols)) return hipErrorNotSupported;
   int nper = 0;
   if (sel) {
     if (sel->E > 256 || sel->K > 16 || sel->K > sel->E || sel->K != max_active) return hipErrorNotSupported;
@@ -390,9 +394,9 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
   DecArgs a{tier, rt, rows, cols, xq, xd, xbs, h, 0, sel ? *sel : DecSelect{}, dbg ? *dbg : BlockDbg{}};
   // work-group steps of 4*RU rows per expert, spread evenly: every work-group
   // gets the same number of steps
-  const int64_t rows_per_wg = 4LL * ru;
+  const int64_t rows_per_wg = 4LL * kGuRu;
   const int64_t need = (rows + rows_per_wg - 1) / rows_per_wg;
-  int64_t cap = (int64_t)cus * wg_per_cu_x16 / 16 / max_active;
+  int64_t cap = (int64_t)cus * kGuWgPerCu / max_active;
   if (cap < 1) cap = 1;
   const int64_t per = (need + cap - 1) / cap;
   const int64_t gx = (need + per - 1) / per;
@@ -410,14 +414,8 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
     if (dbg) KMOE_DEC_GU_D(TPLV, RUV, true);       \
     else KMOE_DEC_GU_D(TPLV, RUV, false);          \
   } while (0)
-  if (tpl == 1) {
-    if (ru == 1) KMOE_DEC_GU(1, 1);
-    else if (ru == 2) KMOE_DEC_GU(1, 2);
-    else KMOE_DEC_GU(1, 4);
-  } else {
-    if (ru == 1) KMOE_DEC_GU(2, 1);
-    else KMOE_DEC_GU(2, 2);
-  }
+  if (tpl == 1) KMOE_DEC_GU(1, kGuRu);
+  else KMOE_DEC_GU(2, kGuRu);
 #undef KMOE_DEC_GU
 #undef KMOE_DEC_GU_D
   return hipGetLastError();

@@ -117,16 +117,16 @@ struct DecSelect {
   uint32_t *perm = nullptr, *offsets = nullptr, *inv = nullptr;
   int32_t *n_active = nullptr, *active = nullptr;
 };
-// Tiled Q4_K gate/up + SwiGLU for one token (kmoe_decode.hip): RU rows per
-// wave step, about wg_per_cu_x16/16 work-groups per CU. With sel the kernel
-// selects the experts itself (E <= 256, max_active == K) and writes the
-// routing; without it the routing is read from rt. hipErrorNotSupported for
-// rows narrower than 48 quarters or wider than 128.
-bool dec_gate_up_tq4_supported(int64_t cols, int ru);
+// Tiled Q4_K gate/up + SwiGLU for one token (kmoe_decode.hip): 2 rows per
+// wave step, about 2 work-groups per CU. With sel the kernel selects the
+// experts itself (E <= 256, max_active == K) and writes the routing; without
+// it the routing is read from rt. hipErrorNotSupported for rows narrower than
+// 48 quarters or wider than 128.
+bool dec_gate_up_tq4_supported(int64_t cols);
 hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_t rows, int64_t cols,
                                   const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                  const int32_t *xbs, float *h, int ru, int wg_per_cu_x16,
-                                  const DecSelect *sel = nullptr, const BlockDbg *dbg = nullptr);
+                                  const int32_t *xbs, float *h, const DecSelect *sel = nullptr,
+                                  const BlockDbg *dbg = nullptr);
 // Q4_K rows of one matrix (GGUF bytes, or tiled) against one Q8_K row:
 // out[r] (kmoe_decode.hip). hipErrorNotSupported for rows narrower than 48 or wider than
 // 256 quarter-superblocks or misaligned pointers (activations 16 bytes, GGUF
@@ -153,8 +153,8 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
                           const BlockDbg *dbg = nullptr);
 
 // ---- int8 matrix-core path (kmoe_mfma.hip), Q4_K weights x Q8_K rows
-// Token rows at which the matrix-core kernels take over (KMOE_MFMA_MIN_ROWS, default 8).
-int mfma_min_rows();
+// Token rows at which the matrix-core kernels take over.
+constexpr int kMfmaMinRows = 8;
 bool moe_mfma_supported(int64_t rows, int64_t cols);
 // Grouped over the expert tier, as launch_moe_int (mode 0 gate/up + SwiGLU, 1 down),
 // for the experts with min_rows..max_rows rows (max_rows: the most any expert can hold);

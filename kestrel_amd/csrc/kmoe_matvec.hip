@@ -1260,74 +1260,14 @@ __global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
   }
 }
 
-// Launch-shape knobs, read once: KMOE_GRID_MULT (work-groups per CU cap for
-// the register matvec, default 4) and KMOE_DOWN_WG_PER_CU (split-K down,
-// default 2). Used for sweeps; the defaults are the measured best.
-int env_int(const char *name, int dflt) {
-  const char *v = getenv(name);
-  if (!v || !*v) return dflt;
-  const int x = atoi(v);
-  return x > 0 ? x : dflt;
-}
-int grid_mult() {
-  static const int v = env_int("KMOE_GRID_MULT", 4);
-  return v;
-}
-// Tiled gate/up decode kernel: KMOE_GU_RU rows per wave step (1, 2 or 4,
-// default 2) and KMOE_GU_WGPC16 = 16 x work-groups per CU (default 32).
-int gu_ru() {
-  static const int v = env_int("KMOE_GU_RU", 2);
-  return v;
-}
-// Register gate/up kernel (rows too narrow for the tiled kernel):
-// KMOE_REG_GU_RU rows per lane group and step (1 or 2, default 1).
-int reg_gu_ru() {
-  static const int v = env_int("KMOE_REG_GU_RU", 1);
-  return v;
-}
-// One-row register matvec (decode_plain): KMOE_REG_RU rows per lane group
-// and step (1 or 2, default 1).
-int reg_plain_ru() {
-  static const int v = env_int("KMOE_REG_RU", 1);
-  return v;
-}
-// q/k/v projection with RoPE (register kernel): KMOE_QKV_RU rows per lane
-// group and step (1 or 2, default 1).
-int qkv_ru() {
-  static const int v = env_int("KMOE_QKV_RU", 1);
-  return v;
-}
-int gu_wgpc16() {
-  static const int v = env_int("KMOE_GU_WGPC16", 32);
-  return v;
-}
-// KMOE_DOWN_RU: rows per split-K item (1, 2 or 4, default 4).
-int down_ru() {
-  static const int v = env_int("KMOE_DOWN_RU", 4);
-  return v;
-}
-// KMOE_DOWN_RING: register sets in the single-token Q4_K down ring (2 or 3,
-// default 2; 0 keeps the ping-pong split-K kernel).
-int down_ring() {
-  static const int v = [] {
-    const char *e = getenv("KMOE_DOWN_RING");
-    return e && *e ? atoi(e) : 2;
-  }();
-  return v;
-}
-// KMOE_DOWN_EXP=0 keeps the register kernel's expert loop for single-token
-// down + combine over narrow rows instead of the expert ring.
-int down_exp_ring() {
-  static const int v = [] {
-    const char *e = getenv("KMOE_DOWN_EXP");
-    return e && *e ? atoi(e) : 1;
-  }();
-  return v;
-}
-int down_wg_per_cu() {
-  static const int v = env_int("KMOE_DOWN_WG_PER_CU", 2);
-  return v;
-}
+// Launch shapes (the measured best of the sweeps kept as measurements):
+// register matvec work-groups capped at 4 per CU; split-K single-token down
+// at 2 work-groups per CU with 4-row items; the single-token Q4_K / Q6_K down
+// ring with 2 register sets.
+constexpr int kGridMult = 4;
+constexpr int kDownWgPerCu = 2;
+constexpr int kDownRu = 4;
+constexpr int kDownRingSets = 2;
 
 int g_cu_count = 0;
 int cu_count() {
@@ -1360,7 +1300,7 @@ template <int TYPE, int LPR, int TPLMAX, int RU, int MODE>
 hipError_t launch_reg(hipStream_t st, const MvArgs &a, int tpl, int64_t max_tasks) {
   constexpr int RB = 4 * (64 / LPR) * RU;
   (void)RB;
-  const int64_t cap = (int64_t)cu_count() * grid_mult();
+  const int64_t cap = (int64_t)cu_count() * kGridMult;
   int64_t grid = max_tasks;
   if (grid > cap) {
     const int64_t per = (max_tasks + cap - 1) / cap;  // equal task counts per work-group
@@ -1507,23 +1447,16 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   if (type == T_Q4_K) {
     const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out, epi);
     if (e != hipErrorNotSupported) return e;
-    if (reg_plain_ru() == 1) return dispatch_reg<T_Q4_K, M_PLAIN, 1>(st, a, 1);
-    return dispatch_reg<T_Q4_K, M_PLAIN, 2>(st, a, 1);
+    return dispatch_reg<T_Q4_K, M_PLAIN, 1>(st, a, 1);
   }
-  if (type == T_Q6_K) {
-    if (reg_plain_ru() == 1) return dispatch_reg<T_Q6_K, M_PLAIN, 1>(st, a, 1);
-    return dispatch_reg<T_Q6_K, M_PLAIN, 2>(st, a, 1);
-  }
-  if (type == T_Q8_0) {
-    if (reg_plain_ru() == 1) return dispatch_reg<T_Q8_0, M_PLAIN, 1>(st, a, 1);
-    return dispatch_reg<T_Q8_0, M_PLAIN, 2>(st, a, 1);
-  }
+  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_PLAIN, 1>(st, a, 1);
+  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 1>(st, a, 1);
   return hipErrorInvalidValue;
 }
 
 bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
   if (E > 256 || K > 16 || K > E) return false;
-  if (type == T_Q4_K && dec_gate_up_tq4_supported(cols, gu_ru())) return true;
+  if (type == T_Q4_K && dec_gate_up_tq4_supported(cols)) return true;
   // the register kernels select too, where their geometry fits the row
   int lpr, tpl;
   const int64_t el = is_kquant(type) ? 256 : 32;
@@ -1551,11 +1484,9 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
     a.sel = *sel;
   }
   if (type == T_Q4_K) {
-    const hipError_t e =
-        launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, gu_ru(), gu_wgpc16(), sel, dbg);
+    const hipError_t e = launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, sel, dbg);
     if (e != hipErrorNotSupported) return e;
-    if (reg_gu_ru() == 1) return dispatch_reg<T_Q4_K, M_GATE_UP, 1>(st, a, max_active);
-    return dispatch_reg<T_Q4_K, M_GATE_UP, 2>(st, a, max_active);
+    return dispatch_reg<T_Q4_K, M_GATE_UP, 1>(st, a, max_active);
   }
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
@@ -1567,17 +1498,11 @@ static hipError_t launch_qkv_reg(hipStream_t st, const MvArgs &a) {
   const int ntasks = (int)(QT<TYPE>::TPB * (a.cols / QT<TYPE>::EL));
   int lpr, tpl;
   if (!reg_geometry(TYPE, ntasks, lpr, tpl)) return hipErrorNotSupported;
-  // Rows 2i and 2i+1 sit in one wave at every step for RU 1 and 2: a step's
-  // first row r0 - row_in_wave is a multiple of 64 / LPR.
-  if (qkv_ru() == 1) {
-    const int64_t t32 = (a.rows + 4 * 2 - 1) / (4 * 2), t16 = (a.rows + 4 * 4 - 1) / (4 * 4);
-    if (lpr == 32) return launch_reg<TYPE, 32, 1, 1, M_QKV>(st, a, tpl, t32);
-    if (lpr == 16) return launch_reg<TYPE, 16, 1, 1, M_QKV>(st, a, tpl, t16);
-    return hipErrorNotSupported;  // one row per wave step: pairs not in one wave
-  }
-  const int64_t tasks32 = (a.rows + 4 * 2 * 2 - 1) / (4 * 2 * 2), tasks16 = (a.rows + 4 * 4 * 2 - 1) / (4 * 4 * 2);
-  if (lpr == 32) return launch_reg<TYPE, 32, 1, 2, M_QKV>(st, a, tpl, tasks32);
-  if (lpr == 16) return launch_reg<TYPE, 16, 1, 2, M_QKV>(st, a, tpl, tasks16);
+  // Rows 2i and 2i+1 sit in one wave at every step: a step's first row
+  // r0 - row_in_wave is a multiple of 64 / LPR.
+  const int64_t t32 = (a.rows + 4 * 2 - 1) / (4 * 2), t16 = (a.rows + 4 * 4 - 1) / (4 * 4);
+  if (lpr == 32) return launch_reg<TYPE, 32, 1, 1, M_QKV>(st, a, tpl, t32);
+  if (lpr == 16) return launch_reg<TYPE, 16, 1, 1, M_QKV>(st, a, tpl, t16);
   return hipErrorNotSupported;  // one row per wave step: pairs not in one wave
 }
 
@@ -1615,7 +1540,7 @@ hipError_t launch_down_exp(hipStream_t st, const MvArgs &a, int ntasks, int topk
   int wpb = 4;
   while (wpb > 1 && (a.rows + rpw * wpb - 1) / (rpw * wpb) < 2 * (int64_t)cu_count()) wpb >>= 1;
   const int64_t blocks = (a.rows + (int64_t)rpw * wpb - 1) / ((int64_t)rpw * wpb);
-  const int64_t cap = (int64_t)cu_count() * grid_mult() * (4 / wpb);
+  const int64_t cap = (int64_t)cu_count() * kGridMult * (4 / wpb);
   const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);
   const int kmax = topk <= 2 ? 2 : topk <= 4 ? 4 : topk <= 6 ? 6 : 8;
 #define KMOE_DX(L, KM, WP)                                                                                         \
@@ -1665,7 +1590,7 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
   // one token: its topk experts are distinct, so k slots are active
   if (ntasks >= 128 && ntasks <= 4 * 64 * 2) {
     // persistent split-K: one work-group per CU, rows split evenly
-    const int64_t G = (int64_t)cu_count() * down_wg_per_cu();
+    const int64_t G = (int64_t)cu_count() * kDownWgPerCu;
     int rb = (int)((rows + G - 1) / G);
     if (rb <= kSplitRbMax) {
       const unsigned grid = (unsigned)((rows + rb - 1) / rb);
@@ -1676,9 +1601,8 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
     else KMOE_LAUNCH((k_down_splitk<T, RU, TP, false>), dim3(grid), dim3(256), 0, st, a, rb);         \
   } while (0)
       if (type == T_Q4_K) {
-        if (tpl == 1 && rt.topk <= 2 && down_ring() > 0) {
+        if (tpl == 1 && rt.topk <= 2) {
           // the ring kernel: 2 rows per item, at most 8 items
-          const int ns = down_ring();
           const int items = rt.topk * ((rb + 1) / 2);
           if (items <= 8) {
 #define KMOE_RING(NIT_, NS_)                                                                                      \
@@ -1686,31 +1610,23 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
     if (dbg) KMOE_LAUNCH((k_down_ring<T_Q4_K, 2, NIT_, NS_, true>), dim3(grid), dim3(256), 0, st, a, rb);        \
     else KMOE_LAUNCH((k_down_ring<T_Q4_K, 2, NIT_, NS_, false>), dim3(grid), dim3(256), 0, st, a, rb);           \
   } while (0)
-            if (items <= 4) {
-              if (ns <= 2) KMOE_RING(4, 2);
-              else KMOE_RING(4, 3);
-            } else {
-              if (ns <= 2) KMOE_RING(8, 2);
-              else KMOE_RING(8, 3);
-            }
+            if (items <= 4) KMOE_RING(4, kDownRingSets);
+            else KMOE_RING(8, kDownRingSets);
 #undef KMOE_RING
             return hipGetLastError();
           }
         }
         if (tpl == 1) {
-          const int ru = down_ru();
-          if (ru == 1) KMOE_SPLITK(T_Q4_K, 1, 1);
-          else if (ru == 2) KMOE_SPLITK(T_Q4_K, 2, 1);
-          else KMOE_SPLITK(T_Q4_K, 4, 1);
+          KMOE_SPLITK(T_Q4_K, kDownRu, 1);
         } else {
           KMOE_SPLITK(T_Q4_K, 2, 2);
         }
       } else if (type == T_Q6_K) {  // 26 registers per task: fewer rows per item
-        if (tpl == 1 && rt.topk <= 2 && down_ring() > 0 && rt.topk * ((rb + 1) / 2) <= 8) {
+        if (tpl == 1 && rt.topk <= 2 && rt.topk * ((rb + 1) / 2) <= 8) {
 #define KMOE_RING6(NIT_)                                                                                     \
   do {                                                                                                       \
-    if (dbg) KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, 2, true>), dim3(grid), dim3(256), 0, st, a, rb);     \
-    else KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, 2, false>), dim3(grid), dim3(256), 0, st, a, rb);        \
+    if (dbg) KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, kDownRingSets, true>), dim3(grid), dim3(256), 0, st, a, rb);     \
+    else KMOE_LAUNCH((k_down_ring<T_Q6_K, 2, NIT_, kDownRingSets, false>), dim3(grid), dim3(256), 0, st, a, rb);        \
   } while (0)
           if (rt.topk * ((rb + 1) / 2) <= 4) KMOE_RING6(4);
           else KMOE_RING6(8);
@@ -1727,7 +1643,7 @@ hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier
       return hipGetLastError();
     }
   }
-  if (down_exp_ring() > 0 && rt.topk <= 8) {
+  if (rt.topk <= 8) {
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q4_K) e = launch_down_exp<T_Q4_K>(st, a, ntasks, rt.topk, dbg != nullptr);
     else if (type == T_Q6_K) e = launch_down_exp<T_Q6_K>(st, a, ntasks, rt.topk, dbg != nullptr);

@@ -748,39 +748,14 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
-// Launch knob, read once: KMOE_MFMA_MIN_ROWS, the token rows from which the
-// matrix-core kernels are used (default 8).
-int mfma_min_rows() {
-  static const int v = [] {
-    const char *e = getenv("KMOE_MFMA_MIN_ROWS");
-    const int x = e && *e ? atoi(e) : 0;
-    return x > 0 ? x : 8;
-  }();
-  return v;
-}
-
 bool moe_mfma_supported(int64_t rows, int64_t cols) {
   return rows > 0 && cols > 0 && cols % 256 == 0 && rows < (1ll << 31) / 32 && cols / 256 < (1ll << 24);
 }
 
-// Launch knob, read once: KMOE_MFMA_RING=0 keeps experts with at most 32
-// rows on the kernel above instead of the streaming kernel.
-bool mfma_ring() {
-  static const bool v = [] {
-    const char *e = getenv("KMOE_MFMA_RING");
-    return !(e && *e && atoi(e) == 0);
-  }();
-  return v;
-}
-
 template <int MODE, bool DBG>
 hipError_t launch_ring(hipStream_t st, dim3 grid, const MfmaArgs &a) {
-  static const int ns = [] {  // KMOE_MFMA_RING_NS: stages in flight plus one (2, default, or 3)
-    const char *e = getenv("KMOE_MFMA_RING_NS");
-    return e && *e && atoi(e) == 3 ? 3 : 2;
-  }();
-  if (ns == 2) KMOE_LAUNCH((k_moe_mfma_ring<MODE, 2, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
-  else KMOE_LAUNCH((k_moe_mfma_ring<MODE, 3, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
+  // two stages: one in flight beside the one being multiplied
+  KMOE_LAUNCH((k_moe_mfma_ring<MODE, 2, DBG>), grid, dim3(kRingWaves<MODE> * 64), 0, st, a);
   return hipGetLastError();
 }
 
@@ -804,7 +779,7 @@ hipError_t launch_moe_mfma(hipStream_t st, int mode, const ExpertTier &tier, int
   a.max_rows = max_rows;
   if (dbg) a.dbg = *dbg;
   ring_rows = ring_rows < kRingTok ? ring_rows : kRingTok;
-  if (mfma_ring() && min_rows <= ring_rows && max_active <= kRingExperts) {
+  if (min_rows <= ring_rows && max_active <= kRingExperts) {
     // experts with min_rows..32 rows: the streaming kernel, (expert, 64- or 128-row) items,
     // eight waves per CU
     const int nw = mode == MF_GATE_UP ? kRingWaves<MF_GATE_UP> : kRingWaves<MF_DOWN>;
