@@ -440,7 +440,10 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   }
   vm_wait();  // this wave's partials are written before the counter moves
   __syncthreads();
-  if (threadIdx.x == 0) last = add_agent(counters + s * nkv + g, 1u);
+  if (threadIdx.x == 0) {
+    last = add_release(counters + s * nkv + g, 1u);
+    if (last == (uint32_t)(nch - 1)) acquire_agent();
+  }
   __syncthreads();
   if (last != (uint32_t)(nch - 1)) return;
   for (int hh = wave; hh < group; hh += 4) {

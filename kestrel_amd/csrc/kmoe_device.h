@@ -228,9 +228,18 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ void st_agent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t add_agent(uint32_t *c, uint32_t v) {
-  return __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Counter of a hand-off between the work-groups of one kernel. Each
+// work-group adds once, with release semantics at agent scope, after every
+// access it hands over (the agent-scope stores of its waves, each wave having
+// waited for them); the add returns the count before it. The work-group that
+// sees the final count then calls acquire_agent() before it reads what the
+// others wrote (or writes what they read): every add continues the release
+// sequence of the earlier ones, so all of their accesses happen before its
+// own.
+__device__ __forceinline__ uint32_t add_release(uint32_t *c, uint32_t v) {
+  return __hip_atomic_fetch_add(c, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 
 // Wait until this wave's vector memory operations have completed (s_waitcnt
 // vmcnt(0): gfx9 encoding, expcnt and lgkmcnt left at their maxima). Agent-

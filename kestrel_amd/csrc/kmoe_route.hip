@@ -544,7 +544,10 @@ __device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h
     if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
   ss = wg_sum256(ss, red);  // its barriers: every thread's loads of x and y have returned
   if (yr) {
-    if (t == 0) *xlast = add_agent(n.done, 1u) == gridDim.x - 1;
+    if (t == 0) {
+      *xlast = add_release(n.done, 1u) == gridDim.x - 1;
+      if (*xlast) acquire_agent();  // every other work-group has read x
+    }
     __syncthreads();
     if (*xlast) {
 #pragma unroll
@@ -700,11 +703,13 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
   if (!a.done) return;  // logits only: the selection happens in the next kernel
   __syncthreads();
   if (tid == 0) {
-    // The logits went out with agent-scope stores and the tail reads them
-    // with agent-scope loads, so waiting for this thread's stores suffices
-    // (no cache writeback); the int8 rows are read by later kernels only.
+    // The logits went out with agent-scope stores, waited for here; the
+    // release add orders them before the counter, and the work-group that
+    // completes it acquires before its tail reads them (with agent-scope
+    // loads). The int8 rows are read by later kernels only.
     vm_wait();
-    last = add_agent(a.done, 1u) == (uint32_t)(G - 1);
+    last = add_release(a.done, 1u) == (uint32_t)(G - 1);
+    if (last) acquire_agent();
   }
   __syncthreads();
   if (!last) return;
