@@ -28,6 +28,9 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from tests.helpers import (DSV2LITE, MOE6B, stack_bytes_per_token, stack_model,  # noqa: E402
+                           synthetic_blocks, tensor_bytes)
+
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 D, FF, E, K = 4096, 14336, 8, 2
 Q8_0, Q4_K, Q6_K = 8, 12, 14
@@ -188,6 +191,17 @@ def cpu_baseline(ctx, torch, seconds: float, threads: int):
         "gemv_q4k_2048x4096_GBps_one_thread": round(gemv1 / 1e9, 3),
     }
 
+
+# Kernel names the library's timing mode reports (kmoe_profile_read).
+PROFILE_NAMES = ("add_rows", "argmax", "attention", "attention_q8", "block_sums_q4k", "block_sums_q4k_mfma",
+                 "block_sums_q6k", "block_sums_q8_0", "combine", "dequant_x", "dispatch", "gemm_f32", "get_rows",
+                 "kv_store", "matmul_f32_ordered", "matvec_q4k", "matvec_q4k_mfma", "matvec_q6k", "matvec_q8_0",
+                 "matvec_qkv_rope", "matvec_unpacked", "moe_down_dec", "moe_down_f32", "moe_down_int",
+                 "moe_down_mfma", "moe_down_small", "moe_gate_f32", "moe_gate_up_dec", "moe_gate_up_int",
+                 "moe_gate_up_mfma", "moe_gate_up_small", "moe_up_f32", "pos_advance", "quant_q8", "quant_q8k",
+                 "quant_slots_q8", "quant_slots_q8k", "rmsnorm", "rmsnorm_quant", "rope", "rope_kv",
+                 "route_decode", "route_topk", "router_logits", "shared_add", "shared_down_add", "shared_gate",
+                 "shared_swiglu", "shared_swiglu_quant", "swiglu")
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s
 
@@ -537,103 +551,28 @@ def preload_leg(ctx, torch, reps: int = 3):
     return out
 
 
-def synthetic_blocks(t: int, n_blocks: int, scale: float, rng):
-    """Random well-formed blocks with dequantized std ~scale, built the way
-    kestrel's synthetic models are (tools/make_synthetic.py:38-58): Q4_K with
-    every 6-bit scale and min at 32 and dmin = 7.5 d (zero-mean weights), Q6_K
-    with int8 scales 16..47, Q8_0 uniform int8 under one scale."""
-    import numpy as np
-
-    f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
-    if t == Q8_0:  # uniform int8 weights (std ~74) under one f16 scale
-        raw = rng.integers(0, 256, size=(n_blocks, 34), dtype=np.uint8)
-        raw[:, 0:2] = f16(scale / 74.0)
-        return raw.reshape(-1)
-    if t == Q4_K:
-        raw = rng.integers(0, 256, size=(n_blocks, 144), dtype=np.uint8)
-        d = scale / (32 * 4.61)
-        raw[:, 0:2] = f16(d)
-        raw[:, 2:4] = f16(7.5 * d)
-        raw[:, 4:16] = np.array([160] * 8 + [0] * 4, np.uint8)
-    else:
-        raw = rng.integers(0, 256, size=(n_blocks, 210), dtype=np.uint8)
-        raw[:, 192:208] = (raw[:, 192:208] % 32 + 16).astype(np.uint8)
-        raw[:, 208:210] = f16(scale / 600.0)
-    return raw.reshape(-1)
-
-
-MOE6B = dict(name="synthetic moe-6b (llama arch)", arch="llama", layers=24, embd=2048, ff=1536, heads=16,
-             kv_heads=4, vocab=32000, experts=32, experts_used=4, norm_topk=False, weights_scale=0.0,
-             down_type=Q4_K, shared_ff=0, dense_layers=0, dense_ff=0)
-# DeepSeek-V2-Lite's shape as kestrel can hold it: qwen2moe (the reference's
-# native MoE architecture with shared experts; deepseek2 itself is
-# LlamaCppOnly, kestrel-model/src/adapters.rs:32) with plain multi-head
-# attention in place of MLA, 27 layers of which the first is dense (FFN
-# 10944, first_k_dense_replace = 1), 64 routed experts of FFN 1408, top-6
-# with unrenormalised softmax weights, 2 shared experts as one ungated FFN of
-# 2816; Q4_K_M-style types: Q4_K, Q8_0 where a row is not a multiple of 256
-# (routed down, dense down), Q6_K shared down and head.
-DSV2LITE = dict(name="DeepSeek-V2-Lite-shaped (qwen2moe arch, MHA)", arch="qwen2moe", layers=27, embd=2048,
-                ff=1408, heads=16, kv_heads=16, vocab=102400, experts=64, experts_used=6, norm_topk=False,
-                weights_scale=1.0, down_type=Q8_0, shared_ff=2816, dense_layers=1, dense_ff=10944)
-STACKS = {"moe6b": MOE6B, "dsv2lite": DSV2LITE}
-
-
-def _tbytes(t: int, rows: int, cols: int) -> int:
-    el, sz = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}[t]
-    return rows * (cols // el) * sz
-
-
-def decode_stack_leg(ctx, torch, c: dict, prompt: int = 128, steps: int = 256):
+def decode_stack_leg(ctx, torch, c: dict, prompt: int = 128, steps: int = 256, cpu_seconds: float = 0.0,
+                     cpu_cap: int = 16):
     """A whole decode stack on the GPU through Decoder (Transformer::forward),
     every weight resident in HBM: a 128-token prompt of uniform random ids,
     then greedy decode steps, each one token through all layers, the head and
     argmax, replayed as one HIP graph. c: MOE6B (kestrel's synthetic `moe-6b`,
     tools/make_synthetic.py:27) or DSV2LITE. Random well-formed blocks; expert,
     attention and dense-FFN bytes are shared between layers on the host (each
-    layer still gets its own copy in HBM); routers differ per layer."""
+    layer still gets its own copy in HBM); routers differ per layer.
+
+    Then a per-kernel pass (eager single-token steps, each launch timed at its
+    dispatch) names the kernels that take the step's time, and with
+    cpu_seconds > 0 the oracle's Transformer (the C++ restatement of kestrel's
+    AVX2 path) decodes the same model on this host's cores as the CPU
+    baseline."""
     import numpy as np
 
     from kestrel_amd.decoder import Decoder
 
-    L, d, ff, H, KV, V, NE, NU = (c[k] for k in ("layers", "embd", "ff", "heads", "kv_heads", "vocab", "experts",
-                                                  "experts_used"))
-    dt, FS, ND, FD = c["down_type"], c["shared_ff"], c["dense_layers"], c["dense_ff"]
-    hd = d // H
+    L, V = c["layers"], c["vocab"]
     rng = np.random.default_rng(11)
-    blk = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-    mat = lambda t, rows, cols, sc: (t, [cols, rows], synthetic_blocks(t, rows * cols // blk[t], sc, rng))
-    f32 = lambda v, dims: (0, list(dims), np.ascontiguousarray(v, np.float32).view(np.uint8).reshape(-1))
-    hp = dict(arch=c["arch"], n_layer=L, n_embd=d, n_head=H, n_head_kv=KV, head_dim=hd, rope_dim=hd,
-              rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=prompt + steps + 8, n_batch=512, n_expert=NE,
-              n_expert_used=NU, norm_topk=c["norm_topk"], weights_scale=c["weights_scale"])
-    T = {"token_embd.weight": mat(Q4_K, V, d, 1.0), "output_norm.weight": f32(np.ones(d), [d]),
-         "output.weight": mat(Q6_K, V, d, 1.0 / np.sqrt(d))}
-    s_d = 1 / np.sqrt(d)
-    attn = {"attn_q.weight": mat(Q4_K, H * hd, d, s_d), "attn_k.weight": mat(Q4_K, KV * hd, d, s_d),
-            "attn_v.weight": mat(Q4_K, KV * hd, d, s_d), "attn_output.weight": mat(Q4_K, d, H * hd, s_d)}
-    gate = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng))
-    up = (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng))
-    down = (dt, [ff, d, NE], synthetic_blocks(dt, NE * ff * d // blk[dt], 1 / np.sqrt(ff), rng))
-    shexp = {}
-    if FS:
-        shexp = {"ffn_gate_shexp.weight": mat(Q4_K, FS, d, s_d), "ffn_up_shexp.weight": mat(Q4_K, FS, d, s_d),
-                 "ffn_down_shexp.weight": mat(Q6_K, d, FS, 1 / np.sqrt(FS))}
-    dense = {}
-    if ND:
-        dense = {"ffn_gate.weight": mat(Q4_K, FD, d, s_d), "ffn_up.weight": mat(Q4_K, FD, d, s_d),
-                 "ffn_down.weight": mat(Q8_0, d, FD, 1 / np.sqrt(FD))}
-    for l in range(L):
-        p = f"blk.{l}."
-        T.update({p + k: v for k, v in attn.items()})
-        T[p + "attn_norm.weight"] = f32(np.ones(d), [d])
-        T[p + "ffn_norm.weight"] = f32(np.ones(d), [d])
-        if l < ND:
-            T.update({p + k: v for k, v in dense.items()})
-            continue
-        T[p + "ffn_gate_inp.weight"] = f32(rng.standard_normal(NE * d) * (4.0 / np.sqrt(d)), [d, NE])
-        T[p + "ffn_gate_exps.weight"], T[p + "ffn_up_exps.weight"], T[p + "ffn_down_exps.weight"] = gate, up, down
-        T.update({p + k: v for k, v in shexp.items()})
+    hp, T = stack_model(c, rng, n_ctx=prompt + steps + 8)
     ctx.set_stream(torch.cuda.current_stream())
     t0 = time.perf_counter()
     dec = Decoder(ctx, hp, T)
@@ -656,21 +595,64 @@ def decode_stack_leg(ctx, torch, c: dict, prompt: int = 128, steps: int = 256):
         torch.cuda.synchronize()
         dec_s = time.perf_counter() - t0
         n_distinct = int(torch.unique(toks).numel())
+        # per-kernel pass: eager steps from the same position, every launch timed
+        nprof = 8
+        dec.cached = prompt
+        dec.decode_greedy(first, 2, use_graph=False)
+        dec.cached = prompt
+        torch.cuda.synchronize()
+        ctx.profile_enable(True)
+        dec.decode_greedy(first, nprof, use_graph=False)
+        torch.cuda.synchronize()
+        per_tok = {}
+        for name in PROFILE_NAMES:
+            ms, cnt = ctx.profile_read(name)
+            if cnt:
+                per_tok[name] = {"us_per_token": round(ms * 1e3 / nprof, 2), "launches_per_token": cnt // nprof}
+        ctx.profile_enable(False)
     finally:
         dec.close()
         torch.cuda.empty_cache()
-    attn_b = _tbytes(Q4_K, (H + 2 * KV) * hd, d) + _tbytes(Q4_K, d, H * hd)
-    expert_b = 2 * _tbytes(Q4_K, ff, d) + _tbytes(dt, d, ff)
-    moe_b = NU * expert_b + NE * d * 4 + ((2 * _tbytes(Q4_K, FS, d) + _tbytes(Q6_K, d, FS)) if FS else 0)
-    dense_b = (2 * _tbytes(Q4_K, FD, d) + _tbytes(Q8_0, d, FD)) if ND else 0
-    tb = L * attn_b + ND * dense_b + (L - ND) * moe_b + _tbytes(Q6_K, V, d)
+    tb = stack_bytes_per_token(c)
     n = steps - 4
-    return {"model": c["name"], "layers": L, "dense_layers": ND, "prompt_tokens": prompt,
-            "prefill_tokens_per_s": round(prompt / prefill_s, 1), "decode_steps": n,
-            "decode_tokens_per_s": round(n / dec_s, 1), "ms_per_token": round(dec_s / n * 1e3, 3),
-            "weight_bytes_per_token": tb, "hbm_GBps": round(tb * n / dec_s / 1e9, 1),
-            "hbm_frac": round(tb * n / dec_s / 1e9 / HBM_PEAK_GBPS, 4),
-            "distinct_tokens": n_distinct, "load_s": round(load_s, 1)}
+    ach = tb * n / dec_s / 1e9
+    top = sorted(per_tok.items(), key=lambda kv: -kv[1]["us_per_token"])
+    roof = {"bound": "hbm", "scope": "whole decode step: weight bytes per token / time per token",
+            "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+            "traffic": None, "bytes_per_token": tb,
+            "dominant_kernel": top[0][0] if top else None,
+            "kernels_per_token": dict(top[:8]),
+            "kernel_sum_us_per_token": round(sum(v["us_per_token"] for _, v in top), 1)}
+    res = {"model": c["name"], "layers": L, "dense_layers": c["dense_layers"], "prompt_tokens": prompt,
+           "prefill_tokens_per_s": round(prompt / prefill_s, 1), "decode_steps": n,
+           "decode_tokens_per_s": round(n / dec_s, 1), "ms_per_token": round(dec_s / n * 1e3, 3),
+           "weight_bytes_per_token": tb, "hbm_GBps": round(ach, 1),
+           "hbm_frac": round(ach / HBM_PEAK_GBPS, 4),
+           "distinct_tokens": n_distinct, "load_s": round(load_s, 1), "roofline": roof}
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_stack(hp, T, c, cpu_seconds, cpu_cap)
+    return res
+
+
+def cpu_stack(hp: dict, T: dict, c: dict, seconds: float, cap: int):
+    """The oracle's Transformer (transformer.rs:278-467 restated over the
+    AVX2-path kernels) decoding the same stack on this host: a 4-token prompt,
+    then single-token greedy steps for about `seconds`, one thread per
+    physical core."""
+    import numpy as np
+
+    from oracle import pyoracle as orc
+
+    nthreads = cpu_threads(cap)
+    ref = orc.Transformer(hp, T, regime=orc.REGIME_AVX2, threads=nthreads)
+    l = ref.forward([1, 2, 3, 4])
+    tok = [orc.argmax(l)]
+    limit = hp["n_ctx"] - ref.cached
+    n, el = timed_calls(lambda i: tok.append(orc.argmax(ref.forward([tok[-1]]))), seconds, limit - 1)
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{c['name']}, {hp['n_layer']} layers: 4-token prompt, then {n + 1} greedy single-token "
+                      f"steps (the first untimed), {el:.1f} s, {nthreads} threads (one per physical core)",
+            "ms_per_token": round(el / n * 1e3, 2), **host_cpu()}
 
 
 def qwen3_leg(ctx, torch, layers: int = 4, seed: int = 1, cpu_seconds: float = 0.0, cpu_cap: int = 16):
@@ -780,7 +762,7 @@ def c5_layer_leg(ctx, torch, layers: int = 4, seed: int = 5, cpu_seconds: float 
                                       np.array([7.5 * 1.4e-4], np.float16).view(np.uint8)]),
                       dtype=torch.uint8, device="cuda")
     h8 = torch.tensor(np.array([0.02 / 74.0], np.float16).view(np.uint8), dtype=torch.uint8, device="cuda")
-    gu_b, dn_b = _tbytes(Q4_K, F5, D5), _tbytes(Q8_0, D5, F5)
+    gu_b, dn_b = tensor_bytes(Q4_K, F5, D5), tensor_bytes(Q8_0, D5, F5)
     base, routers, shared = 400, [], []
     for l in range(layers):
         ctx.layer_create(base + l, E5, K5, D5, F5, Q4_K, Q4_K, Q8_0, False, 1.0)
@@ -800,7 +782,7 @@ def c5_layer_leg(ctx, torch, layers: int = 4, seed: int = 5, cpu_seconds: float 
         shared.append(sh)
     torch.cuda.synchronize()
     routed_b = 2 * gu_b + dn_b
-    shared_b = 2 * _tbytes(Q4_K, FS, D5) + _tbytes(Q6_K, D5, FS)
+    shared_b = 2 * tensor_bytes(Q4_K, FS, D5) + tensor_bytes(Q6_K, D5, FS)
     res = []
     for S, regime in ((1, 0), (8, 0), (128, 0), (128, 1)):
         ctx.set_regime(regime)
@@ -1093,7 +1075,8 @@ def main():
     if "decode_stack" in legs:
         res["decode_stack"] = decode_stack_leg(ctx, torch, MOE6B)
     if "c5_stack" in legs:
-        res["c5_stack"] = decode_stack_leg(ctx, torch, DSV2LITE)
+        res["c5_stack"] = decode_stack_leg(ctx, torch, DSV2LITE, cpu_seconds=0.0 if a.no_cpu else a.cpu_seconds,
+                                           cpu_cap=a.cpu_threads)
     if "measure" in legs:  # the figures kestrel's planner would otherwise estimate (kmoe_measure)
         res["planner_inputs"] = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in ctx.measure().items()}
     if not a.no_cpu:

@@ -232,3 +232,128 @@ def midpoint_rows(rows: int, cols: int, block: int, seed: int):
 def round_half_away(t: np.ndarray) -> np.ndarray:
     """Rust f32::round then clamp(-127, 127) as i8, on exact float64 values."""
     return np.clip(np.sign(t) * np.floor(np.abs(t) + 0.5), -127, 127).astype(np.int8)
+
+
+# ---------------------------------------------------------------- decode stacks
+
+def synthetic_blocks(t: int, n_blocks: int, scale: float, rng):
+    """Random well-formed blocks with dequantized std ~scale, built the way
+    kestrel's synthetic models are (tools/make_synthetic.py:38-58): Q4_K with
+    every 6-bit scale and min at 32 and dmin = 7.5 d (zero-mean weights), Q6_K
+    with int8 scales 16..47, Q8_0 uniform int8 under one scale."""
+    f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
+    if t == Q8_0:  # uniform int8 weights (std ~74) under one f16 scale
+        raw = rng.integers(0, 256, size=(n_blocks, 34), dtype=np.uint8)
+        raw[:, 0:2] = f16(scale / 74.0)
+        return raw.reshape(-1)
+    if t == Q4_K:
+        raw = rng.integers(0, 256, size=(n_blocks, 144), dtype=np.uint8)
+        d = scale / (32 * 4.61)
+        raw[:, 0:2] = f16(d)
+        raw[:, 2:4] = f16(7.5 * d)
+        raw[:, 4:16] = np.array([160] * 8 + [0] * 4, np.uint8)
+    else:
+        raw = rng.integers(0, 256, size=(n_blocks, 210), dtype=np.uint8)
+        raw[:, 192:208] = (raw[:, 192:208] % 32 + 16).astype(np.uint8)
+        raw[:, 208:210] = f16(scale / 600.0)
+    return raw.reshape(-1)
+
+
+MOE6B = dict(name="synthetic moe-6b (llama arch)", arch="llama", layers=24, embd=2048, ff=1536, heads=16,
+             kv_heads=4, vocab=32000, experts=32, experts_used=4, norm_topk=False, weights_scale=0.0,
+             down_type=Q4_K, shared_ff=0, dense_layers=0, dense_ff=0)
+# DeepSeek-V2-Lite's shape as kestrel can hold it: qwen2moe (the reference's
+# native MoE architecture with shared experts; deepseek2 itself is
+# LlamaCppOnly, kestrel-model/src/adapters.rs:32) with plain multi-head
+# attention in place of MLA, 27 layers of which the first is dense (FFN
+# 10944, first_k_dense_replace = 1), 64 routed experts of FFN 1408, top-6
+# with unrenormalised softmax weights, 2 shared experts as one ungated FFN of
+# 2816; Q4_K_M-style types: Q4_K, Q8_0 where a row is not a multiple of 256
+# (routed down, dense down), Q6_K shared down and head.
+DSV2LITE = dict(name="DeepSeek-V2-Lite-shaped (qwen2moe arch, MHA)", arch="qwen2moe", layers=27, embd=2048,
+                ff=1408, heads=16, kv_heads=16, vocab=102400, experts=64, experts_used=6, norm_topk=False,
+                weights_scale=1.0, down_type=Q8_0, shared_ff=2816, dense_layers=1, dense_ff=10944)
+STACKS = {"moe6b": MOE6B, "dsv2lite": DSV2LITE}
+
+
+def tensor_bytes(t: int, rows: int, cols: int) -> int:
+    return rows * row_bytes(t, cols)
+
+
+def stack_model(c: dict, rng, n_ctx: int, n_layer: int | None = None, share: bool = True):
+    """(hp, tensors) of a synthetic decode stack of config c (MOE6B or
+    DSV2LITE) as Transformer::forward reads it (GGUF names, dims with the
+    contiguous dimension first): Q4_K embedding, Q6_K head, Q4_K attention,
+    routed experts Q4_K / Q4_K / c["down_type"], the dense layers' FFN
+    Q4_K / Q4_K / Q8_0, the shared FFN Q4_K / Q4_K / Q6_K; random well-formed
+    blocks, unit norm weights, routers N(0, 16/d) per layer. n_layer cuts the
+    depth (the dense layers stay first). share: attention, expert and dense
+    bytes are one host array for all layers (each layer still gets its own
+    copy in HBM); otherwise every layer draws its own."""
+    L = c["layers"] if n_layer is None else n_layer
+    d, ff, H, KV, V, NE, NU = (c[k] for k in ("embd", "ff", "heads", "kv_heads", "vocab", "experts",
+                                              "experts_used"))
+    dt, FS, ND, FD = c["down_type"], c["shared_ff"], min(c["dense_layers"], L), c["dense_ff"]
+    hd = d // H
+    blk = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+    mat = lambda t, rows, cols, sc: (t, [cols, rows], synthetic_blocks(t, rows * cols // blk[t], sc, rng))
+    f32 = lambda v, dims: (F32, list(dims), np.ascontiguousarray(v, np.float32).view(np.uint8).reshape(-1))
+    hp = dict(arch=c["arch"], n_layer=L, n_embd=d, n_head=H, n_head_kv=KV, head_dim=hd, rope_dim=hd,
+              rope_freq_base=10000.0, rms_eps=1e-5, n_ctx=n_ctx, n_batch=512, n_expert=NE,
+              n_expert_used=NU, norm_topk=c["norm_topk"], weights_scale=c["weights_scale"])
+    T = {"token_embd.weight": mat(Q4_K, V, d, 1.0), "output_norm.weight": f32(np.ones(d), [d]),
+         "output.weight": mat(Q6_K, V, d, 1.0 / np.sqrt(d))}
+    s_d = 1 / np.sqrt(d)
+
+    def attn():
+        return {"attn_q.weight": mat(Q4_K, H * hd, d, s_d), "attn_k.weight": mat(Q4_K, KV * hd, d, s_d),
+                "attn_v.weight": mat(Q4_K, KV * hd, d, s_d), "attn_output.weight": mat(Q4_K, d, H * hd, s_d)}
+
+    def experts():
+        return ((Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng)),
+                (Q4_K, [d, ff, NE], synthetic_blocks(Q4_K, NE * ff * d // 256, s_d, rng)),
+                (dt, [ff, d, NE], synthetic_blocks(dt, NE * ff * d // blk[dt], 1 / np.sqrt(ff), rng)))
+
+    def shexp():
+        if not FS:
+            return {}
+        return {"ffn_gate_shexp.weight": mat(Q4_K, FS, d, s_d), "ffn_up_shexp.weight": mat(Q4_K, FS, d, s_d),
+                "ffn_down_shexp.weight": mat(Q6_K, d, FS, 1 / np.sqrt(FS))}
+
+    def dense():
+        if not ND:
+            return {}
+        return {"ffn_gate.weight": mat(Q4_K, FD, d, s_d), "ffn_up.weight": mat(Q4_K, FD, d, s_d),
+                "ffn_down.weight": mat(Q8_0, d, FD, 1 / np.sqrt(FD))}
+
+    shared = (attn(), experts(), shexp(), dense()) if share else None
+    for l in range(L):
+        a_, ex, sh, dn = shared if share else (attn(), None, None, None)
+        p = f"blk.{l}."
+        T.update({p + k: v for k, v in a_.items()})
+        T[p + "attn_norm.weight"] = f32(np.ones(d), [d])
+        T[p + "ffn_norm.weight"] = f32(np.ones(d), [d])
+        if l < ND:
+            T.update({p + k: v for k, v in (dn if share else dense()).items()})
+            continue
+        T[p + "ffn_gate_inp.weight"] = f32(rng.standard_normal(NE * d) * (4.0 / np.sqrt(d)), [d, NE])
+        g, u, dw = ex if share else experts()
+        T[p + "ffn_gate_exps.weight"], T[p + "ffn_up_exps.weight"], T[p + "ffn_down_exps.weight"] = g, u, dw
+        T.update({p + k: v for k, v in (sh if share else shexp()).items()})
+    return hp, T
+
+
+def stack_bytes_per_token(c: dict, n_layer: int | None = None) -> int:
+    """Weight bytes one decode step reads: every layer's attention, the dense
+    layers' FFN, per MoE layer the experts_used routed experts, the router and
+    the shared FFN, then the head."""
+    L = c["layers"] if n_layer is None else n_layer
+    d, ff, H, KV, V, NE, NU = (c[k] for k in ("embd", "ff", "heads", "kv_heads", "vocab", "experts",
+                                              "experts_used"))
+    dt, FS, ND, FD = c["down_type"], c["shared_ff"], min(c["dense_layers"], L), c["dense_ff"]
+    hd = d // H
+    attn_b = tensor_bytes(Q4_K, (H + 2 * KV) * hd, d) + tensor_bytes(Q4_K, d, H * hd)
+    expert_b = 2 * tensor_bytes(Q4_K, ff, d) + tensor_bytes(dt, d, ff)
+    moe_b = NU * expert_b + NE * d * 4 + ((2 * tensor_bytes(Q4_K, FS, d) + tensor_bytes(Q6_K, d, FS)) if FS else 0)
+    dense_b = (2 * tensor_bytes(Q4_K, FD, d) + tensor_bytes(Q8_0, d, FD)) if ND else 0
+    return L * attn_b + ND * dense_b + (L - ND) * moe_b + tensor_bytes(Q6_K, V, d)

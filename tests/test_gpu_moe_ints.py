@@ -166,6 +166,28 @@ def test_batch_kernels_integers_bit_exact_extreme_ranges(ctx, orc):
     assert check_ints(orc, spec, 24, 1, h, *r) > 0
 
 
+@pytest.mark.parametrize("d,ff,E,k,down_type,norm_topk,seed", [
+    (2048, 768, 128, 8, Q4_K, True, 21),    # Qwen3-30B-A3B shape: register gate/up selecting 8 of 128, k_mv_down_exp<Q4_K>
+    (2048, 1408, 64, 6, Q8_0, False, 22),   # DeepSeek-V2-Lite shape: 6 of 64, Q8_0 down over 44 blocks per row
+    (2048, 1536, 32, 4, Q4_K, False, 23),   # moe-6b shape: 4 of 32, k_mv_down_exp<Q4_K> over 6 superblocks
+])
+def test_single_token_fine_grained_integers_bit_exact_extreme_ranges(ctx, orc, d, ff, E, k, down_type, norm_topk,
+                                                                      seed):
+    """One token through the fine-grained shapes' single-token kernels (the
+    gate/up kernel over narrow rows that selects the experts itself, and the
+    expert-ring down + combine), on blocks with every byte 0xFF next to random
+    ones and activations all +-127: per-block integers of every selected
+    expert's gate, up and down rows bit for bit against the oracle."""
+    spec = LayerSpec(E, k, d, ff, Q4_K, seed=seed, quantized=False, down_type=down_type, norm_topk=norm_topk)
+    for parts, t in ((spec.gate, Q4_K), (spec.up, Q4_K), (spec.down, down_type)):
+        for w in parts:
+            plant_extremes(w, t)
+    h = np.where(orc.normal(seed, d) < 0, -3.0, 3.0).astype(np.float32).reshape(1, d)
+    r = run_capture(ctx, orc, spec, 1, 0, h)
+    assert np.abs(r[1]["xq"]).min() == 127
+    assert check_ints(orc, spec, 1, 0, h, *r) == k
+
+
 @pytest.mark.parametrize("S,regime,d,ff,E,k,types,seed", [
     (1, 0, 4096, 14336, 4, 2, (Q4_K, Q4_K), 1),   # tiled gate/up + split-K down, normal activations
     (1, 1, 4096, 8192, 8, 2, (Q4_K, Q6_K), 2),    # split-K down over tiled Q6_K rows
