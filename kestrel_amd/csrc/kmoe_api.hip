@@ -548,7 +548,7 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
   // (13.6 -> 16.7 µs), so wider rows keep the separate quantization.
   if (t == KMOE_Q4_K && s_rows == 1 && cols <= 4096) {
     const hipError_t e = timed(c, "matvec_q4k", [&]() {
-      return launch_dec_rows(c->stream, false, w, rows, cols, nullptr, nullptr, nullptr, out, nullptr, x);
+      return launch_dec_rows(c->stream, w, rows, cols, nullptr, nullptr, nullptr, out, nullptr, x);
     });
     if (e == hipSuccess) return KMOE_OK;
     if (e != hipErrorNotSupported) HIP_OK(c, e);

@@ -166,11 +166,10 @@ __global__ void __launch_bounds__(256) k_dec_gate_up_tq4(DecArgs a) {
 
 // Rows of one matrix against one Q8_K activation row (quant::matmul at one
 // row on the int path, quant.rs:262-309: dot_q4_k_8k per row), with the
-// structure of the gate/up kernel above: lane-constant offsets inside a row,
-// the activation slice in registers, 3 loads per task and row, RU rows per
-// wave step; lane u of the wave ends with row r0+u. Rows in GGUF order (head
-// at 144*sb, nibble chunk (k, j) at 144*sb + 16 + 32k + 16j; rows need only
-// 4-byte alignment) or tiled (tq4_qs_off).
+// task structure of the gate/up kernel above: lane-constant offsets inside a
+// row, the activation slice in registers, RU rows per wave step; lane u of
+// the wave ends with row r0+u. Rows in GGUF order (head at 144*sb, nibble
+// chunk (k, j) at 144*sb + 16 + 32k + 16j; rows need only 4-byte alignment).
 struct RowsArgs {
   const uint8_t *W;
   int64_t rows, cols;
@@ -179,6 +178,7 @@ struct RowsArgs {
   const int32_t *xbs;
   float *out;
   int32_t groups;  // work-groups striding over the rows
+  int32_t per;     // k_dec_rows_co: row steps of every wave (1, or even)
   int32_t add;     // out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
   const float *add_logit;
   const float *xf;  // FX kernels: the f32 row, quantized to Q8_K inside the kernel
@@ -192,15 +192,24 @@ typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 // LDS: thread t loads float4 t + 256*i (block wave + 4i, four values per
 // lane), those loads issued before the first row step's weight loads, so the
 // quantization runs while the weights are in flight.
-constexpr int kFxMaxBlocks = 64;  // Q8_K blocks of the row (cols <= 16384)
+constexpr int kFxMaxBlocks = 16;  // Q8_K blocks of the row (cols <= 4096)
 
-template <bool TILED, int TPL, int RU, bool FX>
-__global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
+// The rows are read with contiguous loads: in the GGUF order a task's three
+// 16-byte pieces sit at 144*sb, +16+32k and +32+32k, so a load instruction
+// per piece touches 16-byte pieces scattered over its lines (that pattern
+// streams at about 4.6 TB/s on MI355X against 6.85 for a linear read). A
+// wave step covers RU consecutive rows, one contiguous span of RU*144*nb
+// bytes: lane l loads its 16-byte chunks l, l+64, ... (each load instruction
+// one contiguous KB), stores them into the wave's own LDS buffer, and reads
+// its tasks' head and nibble chunks from there.
+template <int TPL, int RU, int NL, bool FX, bool RING = true>
+__global__ void __launch_bounds__(256, 2) k_dec_rows_co(RowsArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nb = a.cols / 256, ntasks = 4 * nb;
   const int64_t row_bytes = nb * 144;
-  constexpr int XB = FX ? 4 * TPL : 1;  // FX: blocks per wave (nb <= 16 * TPL)
+  constexpr int XB = FX ? 4 * TPL : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t stg[4][64 * NL * 16];
   __shared__ __attribute__((aligned(16))) int8_t fq[FX ? kFxMaxBlocks * 256 : 16];
   __shared__ float fd[FX ? kFxMaxBlocks : 1];
   __shared__ __attribute__((aligned(16))) int32_t fbs[FX ? kFxMaxBlocks * 16 : 4];
@@ -212,7 +221,7 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
       xv4[i] = *(const float4 *)(a.xf + 256 * b + 4 * lane);
     }
   }
-  uint32_t oh[TPL], oa[TPL], ob[TPL];
+  uint32_t oh[TPL], oa[TPL];
   bool tv[TPL];
   int64_t tsb[TPL];
   int tk[TPL];
@@ -221,19 +230,10 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
     const int64_t t0 = lane + 64 * i;
     tv[i] = t0 < ntasks;
     const int64_t t = tv[i] ? t0 : ntasks - 1;
-    const int64_t sb = t >> 2;
-    const int k = (int)(t & 3);
-    tsb[i] = sb;
-    tk[i] = k;
-    if constexpr (TILED) {
-      oh[i] = (uint32_t)(16 * sb);
-      oa[i] = (uint32_t)tq4_qs_off(nb, sb, k, 0);
-      ob[i] = oa[i] + (uint32_t)tq4_j_stride(nb, sb);
-    } else {
-      oh[i] = (uint32_t)(144 * sb);
-      oa[i] = oh[i] + 16 + 32 * k;
-      ob[i] = oa[i] + 16;
-    }
+    tsb[i] = t >> 2;
+    tk[i] = (int)(t & 3);
+    oh[i] = (uint32_t)(144 * tsb[i]);
+    oa[i] = oh[i] + 16 + 32 * tk[i];
   }
   Slice s[TPL];
   auto slices = [&](const int8_t *xq, const float *xd, const int32_t *xbs) {
@@ -258,37 +258,44 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
     const float den = 1.0f + expf_cr(-*a.add_logit);
     add_scale = 1.0f / den;
   }
-  auto load = [&](int64_t r0, u32x4 (&hw)[RU][TPL], u32x4 (&aw)[RU][TPL], u32x4 (&bw)[RU][TPL]) {
+  uint8_t *S = stg[wave];
+  // The span of rows r0 .. min(r0 + RU, rows) - 1 into c: chunk indices past
+  // the span's end repeat its last chunk (and a step past the last row reads
+  // row rows - 1), so every load is unconditional and the compiler's counted
+  // waits stay exact; those copies land in unused LDS bytes.
+  auto issue = [&](int64_t r0, u32x4 (&c)[NL]) {
+    const int64_t rb = r0 < rows ? r0 : rows - 1;
+    const int64_t nr = rows - rb < RU ? rows - rb : RU;
+    const int last = (int)(nr * row_bytes / 16) - 1;
+    const uint8_t *base = a.W + rb * row_bytes;
 #pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const uint8_t *row = a.W + (r0 + u < rows ? r0 + u : rows - 1) * row_bytes;
-#pragma unroll
-      for (int i = 0; i < TPL; ++i) {
-        if constexpr (TILED) {
-          hw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + oh[i]));
-          aw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + oa[i]));
-          bw[u][i] = __builtin_nontemporal_load((const u32x4 *)(row + ob[i]));
-        } else {
-          hw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + oh[i]));
-          aw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + oa[i]));
-          bw[u][i] = __builtin_nontemporal_load((const u32x4a4 *)(row + ob[i]));
-        }
-      }
+    for (int n = 0; n < NL; ++n) {
+      const int ci = lane + 64 * n < last ? lane + 64 * n : last;
+      c[n] = __builtin_nontemporal_load((const u32x4a4 *)(base + 16 * ci));
     }
   };
-  auto reduce_store = [&](int64_t r0, const u32x4 (&hw)[RU][TPL], const u32x4 (&aw)[RU][TPL],
-                          const u32x4 (&bw)[RU][TPL]) {
+  auto stage = [&](const u32x4 (&c)[NL]) {
+#pragma unroll
+    for (int n = 0; n < NL; ++n) *(u32x4 *)(S + 16 * (lane + 64 * n)) = c[n];
+  };
+  auto reduce_store = [&](int64_t r0) {
     float res = 0.0f;  // lane u < RU: row r0+u
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       float acc = 0.0f;
+      if (r0 + u < rows) {  // wave-uniform
+        const uint8_t *R = S + u * row_bytes;
 #pragma unroll
-      for (int i = 0; i < TPL; ++i) {
-        int m;
-        const int si = q4k_quarter(hw[u][i], aw[u][i], bw[u][i], kq, s[i], m);
-        const float dd = f16_bits_to_f32(hw[u][i].x) * s[i].d, mf = f16_bits_to_f32(hw[u][i].x >> 16) * s[i].d;
-        const float v = fmaf(dd, (float)si, -(mf * (float)m));
-        acc += tv[i] ? v : 0.0f;
+        for (int i = 0; i < TPL; ++i) {
+          const u32x4 hw = *(const u32x4 *)(R + oh[i]);
+          const u32x4 aw = *(const u32x4 *)(R + oa[i]);
+          const u32x4 bw = *(const u32x4 *)(R + oa[i] + 16);
+          int m;
+          const int si = q4k_quarter(hw, aw, bw, kq, s[i], m);
+          const float dd = f16_bits_to_f32(hw.x) * s[i].d, mf = f16_bits_to_f32(hw.x >> 16) * s[i].d;
+          const float v = fmaf(dd, (float)si, -(mf * (float)m));
+          acc += tv[i] ? v : 0.0f;
+        }
       }
       acc = group_sum<64>(acc);
       res = lane == u ? acc : res;
@@ -302,28 +309,62 @@ __global__ void __launch_bounds__(256) k_dec_rows(RowsArgs a) {
       }
     }
   };
-  const int64_t stride = (int64_t)a.groups * 4 * RU;
-  int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU;
-  if constexpr (FX) {
-    // first row step's weights in flight (rows clamped), then the row's Q8_K
-    // blocks into LDS, then the slices from there; every wave takes part
-    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
-    load(r0, hw, aw, bw);
+  auto prologue = [&]() {
+    if constexpr (FX) {
+      // the row's Q8_K blocks into LDS while the first spans are in flight,
+      // then the slices from there; every wave takes part
 #pragma unroll
-    for (int i = 0; i < XB; ++i) {
-      const int b = wave + 4 * i;
-      if (b < nb) wave_quant_q8k_vals(xv4[i], fq + 256 * b, fd + b, fbs + 16 * b, lane);
+      for (int i = 0; i < XB; ++i) {
+        const int b = wave + 4 * i;
+        if (b < nb) wave_quant_q8k_vals(xv4[i], fq + 256 * b, fd + b, fbs + 16 * b, lane);
+      }
+      __syncthreads();
+      slices(fq, fd, fbs);
     }
-    __syncthreads();
-    slices(fq, fd, fbs);
-    if (r0 < rows) reduce_store(r0, hw, aw, bw);
-    r0 += stride;
+  };
+  // The wave's steps r_j = r_first + j * stride, j < a.per (the same count in
+  // every wave: 1, or even with RING). With RING and two or more steps, two
+  // spans are in flight: the main loop restages and refills both register
+  // sets, the last pair is reduced without refills, so no wave ends with
+  // loads it does not use. Without RING (the widest rows, whose second set
+  // would not fit the registers) one span is in flight.
+  const int64_t stride = (int64_t)a.groups * 4 * RU;
+  const int64_t r_first = ((int64_t)blockIdx.x * 4 + wave) * RU;
+  const int per = a.per;
+  u32x4 c0[NL];
+  if constexpr (!RING) {
+    issue(r_first, c0);
+    prologue();
+    for (int j = 0; j < per; ++j) {
+      stage(c0);
+      if (j + 1 < per) issue(r_first + (j + 1) * stride, c0);
+      reduce_store(r_first + j * stride);
+    }
+    return;
   }
-  for (; r0 < rows; r0 += stride) {
-    u32x4 hw[RU][TPL], aw[RU][TPL], bw[RU][TPL];
-    load(r0, hw, aw, bw);
-    reduce_store(r0, hw, aw, bw);
+  u32x4 c1[NL];
+  if (per == 1) {
+    issue(r_first, c0);
+    prologue();
+    stage(c0);
+    reduce_store(r_first);
+    return;
   }
+  issue(r_first, c0);
+  issue(r_first + stride, c1);
+  prologue();
+  for (int j = 0; j < per - 2; j += 2) {
+    stage(c0);
+    issue(r_first + (j + 2) * stride, c0);
+    reduce_store(r_first + j * stride);
+    stage(c1);
+    issue(r_first + (j + 3) * stride, c1);
+    reduce_store(r_first + (j + 1) * stride);
+  }
+  stage(c0);
+  reduce_store(r_first + (per - 2) * stride);
+  stage(c1);
+  reduce_store(r_first + (per - 1) * stride);
 }
 
 }  // namespace
@@ -334,35 +375,50 @@ bool dec_rows_supported(int64_t cols) {
   return ntasks >= 48 && ntasks <= 256;
 }
 
-hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+hipError_t launch_dec_rows(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                            const float *xd, const int32_t *xbs, float *out, const AddEpi *epi, const float *xf) {
   if (rows <= 0) return hipSuccess;
-  if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u) || (tiled && ((uintptr_t)w & 15u)))
+  if (!dec_rows_supported(cols) || ((uintptr_t)w & 3u)) return hipErrorNotSupported;
+  if (xf ? (((uintptr_t)xf & 15u) || cols / 256 > 16) : (((uintptr_t)xq & 15u) || ((uintptr_t)xbs & 15u)))
     return hipErrorNotSupported;
-  if (xf ? (((uintptr_t)xf & 15u) || cols / 256 > kFxMaxBlocks) : (((uintptr_t)xq & 15u) || ((uintptr_t)xbs & 15u)))
-    return hipErrorNotSupported;
-  const int tpl = (int)((4 * (cols / 256) + 63) / 64);
-  const int ru = tpl <= 2 ? 2 : 1;
+  const int64_t nb = cols / 256;
+  const int tpl = (int)((4 * nb + 63) / 64);
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0, epi ? 1 : 0, epi ? epi->logit : nullptr, xf};
-  // work-group steps of 4*RU rows, spread evenly over about two groups per CU
+  RowsArgs a{w, rows, cols, xq, xd, xbs, out, 0, 0, epi ? 1 : 0, epi ? epi->logit : nullptr, xf};
+  // Rows per step: the larger choice (a step's span at most 576 chunks)
+  // unless that leaves fewer than two work-groups per CU. Steps spread evenly
+  // over at most one work-group per CU (measured best against two and three
+  // at 4096x4096, 14336x4096 and 4096x14336); per wave 1 or an even count for
+  // the ring kernels.
+  const int ru_big = nb <= 16 ? 4 : (nb <= 32 ? 2 : 1);
+  int ru = ru_big;
+  if (ru_big > 1 && (rows + 4 * ru_big - 1) / (4 * ru_big) < 2LL * cus) ru = ru_big / 2;
   const int64_t need = (rows + 4 * ru - 1) / (4 * ru);
-  const int64_t cap = 2LL * cus;
-  const int64_t per = (need + cap - 1) / cap;
+  const int64_t cap = cus;
+  int64_t per = (need + cap - 1) / cap;
+  if (per > 1 && nb <= 56) per = (per + 1) / 2 * 2;
   a.groups = (int32_t)((need + per - 1) / per);
+  a.per = (int32_t)per;
   const dim3 grid((unsigned)a.groups);
-#define KMOE_DEC_ROWS(TL, FX)                                                                  \
-  do {                                                                                         \
-    if (tpl == 1) KMOE_LAUNCH((k_dec_rows<TL, 1, 2, FX>), grid, dim3(256), 0, st, a);          \
-    else if (tpl == 2) KMOE_LAUNCH((k_dec_rows<TL, 2, 2, FX>), grid, dim3(256), 0, st, a);     \
-    else if (tpl == 3) KMOE_LAUNCH((k_dec_rows<TL, 3, 1, FX>), grid, dim3(256), 0, st, a);     \
-    else KMOE_LAUNCH((k_dec_rows<TL, 4, 1, FX>), grid, dim3(256), 0, st, a);                   \
-  } while (0)
-  if (xf) KMOE_DEC_ROWS(false, true);  // GGUF rows of kmoe_matmul
-  else if (tiled) KMOE_DEC_ROWS(true, false);
-  else KMOE_DEC_ROWS(false, false);
-#undef KMOE_DEC_ROWS
+#define KMOE_CO(TP, R, N, FX, RING) KMOE_LAUNCH((k_dec_rows_co<TP, R, N, FX, RING>), grid, dim3(256), 0, st, a)
+  if (xf) {  // x quantized in the kernel: rows of at most 16 superblocks
+    if (ru == 4) KMOE_CO(1, 4, 9, true, true);
+    else KMOE_CO(1, 2, 5, true, true);
+  } else if (tpl == 1) {
+    if (ru == 4) KMOE_CO(1, 4, 9, false, true);
+    else KMOE_CO(1, 2, 5, false, true);
+  } else if (tpl == 2) {
+    if (ru == 2) KMOE_CO(2, 2, 9, false, true);
+    else KMOE_CO(2, 1, 5, false, true);
+  } else if (tpl == 3) {
+    KMOE_CO(3, 1, 7, false, true);
+  } else if (nb <= 56) {
+    KMOE_CO(4, 1, 8, false, true);
+  } else {  // two spans of 64-superblock rows do not fit the registers
+    KMOE_CO(4, 1, 9, false, false);
+  }
+#undef KMOE_CO
   return hipGetLastError();
 }
 

@@ -127,14 +127,14 @@ hipError_t launch_dec_gate_up_tq4(hipStream_t st, const ExpertTier &tier, int64_
                                   const Routing &rt, int max_active, const int8_t *xq, const float *xd,
                                   const int32_t *xbs, float *h, const DecSelect *sel = nullptr,
                                   const BlockDbg *dbg = nullptr);
-// Q4_K rows of one matrix (GGUF bytes, or tiled) against one Q8_K row:
-// out[r] (kmoe_decode.hip). hipErrorNotSupported for rows narrower than 48 or wider than
-// 256 quarter-superblocks or misaligned pointers (activations 16 bytes, GGUF
-// rows 4, tiled rows 16).
+// Q4_K rows of one matrix (GGUF bytes) against one Q8_K row: out[r]
+// (kmoe_decode.hip). hipErrorNotSupported for rows narrower than 48 or wider
+// than 256 quarter-superblocks or misaligned pointers (activations 16 bytes,
+// rows 4).
 bool dec_rows_supported(int64_t cols);
 // xf non-null: the f32 row instead of xq/xd/xbs, quantized to Q8_K inside the
-// kernel (GGUF rows only, at most 64 superblocks, xf 16-byte aligned).
-hipError_t launch_dec_rows(hipStream_t st, bool tiled, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
+// kernel (at most 16 superblocks, xf 16-byte aligned).
+hipError_t launch_dec_rows(hipStream_t st, const uint8_t *w, int64_t rows, int64_t cols, const int8_t *xq,
                            const float *xd, const int32_t *xbs, float *out, const AddEpi *epi = nullptr,
                            const float *xf = nullptr);
 // Down projection + combine for one token: out[r] = sum_e (asc) w_e * y_e[r].

@@ -1445,7 +1445,7 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   a.s_rows = 1;
   a.out = out;
   if (type == T_Q4_K) {
-    const hipError_t e = launch_dec_rows(st, false, w, rows, cols, xq, xd, xbs, out, epi);
+    const hipError_t e = launch_dec_rows(st, w, rows, cols, xq, xd, xbs, out, epi);
     if (e != hipErrorNotSupported) return e;
     return dispatch_reg<T_Q4_K, M_PLAIN, 1>(st, a, 1);
   }
