@@ -1506,11 +1506,26 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
                                                     w.xs, w.h, small_rows + 1, gd));
     }
   }
+  // The f32 regime's experts (quant.rs:242-260): in batches of at most 32
+  // tokens they stream their tiled Q4_K rows once through the few-rows
+  // kernels, gate and up in one launch; larger batches take the staged GEMM.
+  const int f32_lo = regime == KMOE_REGIME_EXACT ? 1 : 4;
+  const int f32_hi = S <= 32 ? (int)S : 0;
   if (any_f32) {
-    LAUNCH(c, "moe_gate_f32",
-           launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h, w.part, w.part_floats));
-    LAUNCH(c, "moe_up_f32",
-           launch_moe_f32(st, 1, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h, w.part, w.part_floats));
+    int f32_done = 0;  // experts with f32_lo..f32_done rows are done
+    if (gt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && f32_hi >= f32_lo) {
+      const hipError_t e = timed(c, "moe_gate_up_f32_rows", [&]() {
+        return launch_f32_rows(st, 0, gt, tier, F, d, rt, regime, max_active, f32_lo, f32_hi, h, w.h);
+      });
+      if (e == hipSuccess) f32_done = f32_hi;
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (S > f32_done) {
+      LAUNCH(c, "moe_gate_f32", launch_moe_f32(st, 0, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h,
+                                               w.part, w.part_floats, f32_done + 1));
+      LAUNCH(c, "moe_up_f32", launch_moe_f32(st, 1, gt, tier, F, d, rt, regime, max_active, S, slots, h, w.h,
+                                             w.part, w.part_floats, f32_done + 1));
+    }
   }
   // down (transformer.rs:559-560)
   if (any_int) {
@@ -1538,9 +1553,19 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
                                                  w.hs, w.y, small_rows + 1, dd));
     }
   }
-  if (any_f32)
-    LAUNCH(c, "moe_down_f32",
-           launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, slots, w.h, w.y, w.part, w.part_floats));
+  if (any_f32) {
+    int f32_done = 0;
+    if (dt == KMOE_Q4_K && L->tiled[2] && f32_hi >= f32_lo) {
+      const hipError_t e = timed(c, "moe_down_f32_rows", [&]() {
+        return launch_f32_rows(st, 1, dt, tier, d, F, rt, regime, max_active, f32_lo, f32_hi, w.h, w.y);
+      });
+      if (e == hipSuccess) f32_done = f32_hi;
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (S > f32_done)
+      LAUNCH(c, "moe_down_f32", launch_moe_f32(st, 2, dt, tier, d, F, rt, regime, max_active, S, slots, w.h, w.y,
+                                               w.part, w.part_floats, f32_done + 1));
+  }
   // combine (transformer.rs:566-570)
   LAUNCH(c, "combine", launch_combine(st, w.y, rt, S, d, out));
   }

@@ -58,6 +58,7 @@ struct GArgs {
   int64_t cps;   // column chunks per split
   float *part;      // [ks][n_slots][rows] partial sums when ks > 1
   int64_t n_slots;  // activation rows (plain) or slots (grouped)
+  int min_rows;     // grouped: experts with fewer rows are another kernel's
 };
 
 enum { G_PLAIN = 0, G_GATE = 1, G_UP = 2, G_DOWN = 3 };
@@ -210,7 +211,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32(GArgs a) {
     const int e = a.rt.active[i];
     p0 = a.rt.offsets[e];
     n = (int)(a.rt.offsets[e + 1] - p0);
-    if (!f32_regime(a.regime, n)) return;
+    if (!f32_regime(a.regime, n) || n < a.min_rows) return;
     W = a.tier.base + (int64_t)e * a.tier.stride + a.tier.off[MODE == G_GATE ? 0 : (MODE == G_UP ? 1 : 2)];
   }
   const int ntt = a.ntt, ksn = a.ks;
@@ -412,7 +413,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32_reduce(GArgs a) {
     const int e = a.rt.active[i];
     p0 = a.rt.offsets[e];
     n = (int)(a.rt.offsets[e + 1] - p0);
-    if (!f32_regime(a.regime, n)) return;
+    if (!f32_regime(a.regime, n) || n < a.min_rows) return;
   }
   for (int j = 0; j < n; ++j) {
     const int64_t slot = p0 + j;
@@ -508,10 +509,12 @@ hipError_t launch_matmul_f32(hipStream_t st, int type, const uint8_t *w, int64_t
 
 hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                           const Routing &rt, int regime, int max_active, int64_t max_rows_per_expert,
-                          int64_t n_slots, const float *x, float *out, float *part, int64_t part_floats) {
-  if (rows == 0 || max_active == 0 || max_rows_per_expert == 0) return hipSuccess;
+                          int64_t n_slots, const float *x, float *out, float *part, int64_t part_floats,
+                          int min_rows) {
+  if (rows == 0 || max_active == 0 || max_rows_per_expert == 0 || max_rows_per_expert < min_rows) return hipSuccess;
   if (cols % KC != 0) return hipErrorInvalidValue;
   GArgs a{};
+  a.min_rows = min_rows;
   a.rows = rows;
   a.cols = cols;
   a.x = x;
