@@ -172,6 +172,32 @@ __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__
 // One wave per token: softmax, top-k, renormalisation (transformer.rs:479-495).
 constexpr int kMaxExperts = 512;
 
+// The same for E <= 64*NPER experts through the single-token selection of the
+// decode kernels (wave_route_one: the logits in lane registers, the sum in
+// expert order, the k rounds as wave reductions without block barriers): one
+// wave per token, four tokens per work-group, the same bits as the kernel
+// below.
+template <int NPER>
+__global__ void __launch_bounds__(256) k_route_topk_w(const float *__restrict__ logits, int64_t S, int32_t E,
+                                                      int32_t k, int32_t norm_topk, float weights_scale,
+                                                      uint32_t *__restrict__ idx, float *__restrict__ wout) {
+  __shared__ __attribute__((aligned(16))) float P[4][64 * NPER];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t s = (int64_t)blockIdx.x * 4 + wave;
+  if (s >= S) return;  // no block barriers below
+  const float *row = logits + s * E;
+  float lv[NPER];
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) lv[i] = lane + 64 * i < E ? row[lane + 64 * i] : -INFINITY;
+  uint32_t sel_l;
+  float w_l;
+  wave_route_one<NPER>(lv, E, k, norm_topk, weights_scale, P[wave], sel_l, w_l);
+  if (lane < k) {
+    idx[s * k + lane] = sel_l;
+    wout[s * k + lane] = w_l;
+  }
+}
+
 __global__ void __launch_bounds__(256) k_route_topk(const float *__restrict__ logits, int64_t S, int32_t E, int32_t k,
                                                     int32_t norm_topk, float weights_scale, uint32_t *__restrict__ idx,
                                                     float *__restrict__ wout) {
@@ -421,15 +447,16 @@ __device__ __forceinline__ int token_slots(const Routing &rt, int64_t s, uint32_
 }
 
 // k_combine on 16-byte groups: one token per blockIdx.y, columns 4c..4c+3
-// per thread (d % 4 == 0, y and out 16-byte aligned). Same arithmetic.
-__global__ void __launch_bounds__(256) k_combine4(const float *__restrict__ y, Routing rt, int64_t s0, int64_t d,
-                                                  float *__restrict__ out) {
+// per thread, one wave per work-group (d % 4 == 0, y and out 16-byte
+// aligned). Same arithmetic.
+__global__ void __launch_bounds__(64) k_combine4(const float *__restrict__ y, Routing rt, int64_t s0, int64_t d,
+                                                 float *__restrict__ out) {
   const int64_t s = s0 + blockIdx.y;
   uint32_t p[16];
   float w[16];
   const int k = token_slots(rt, s, p, w);
   const int64_t d4 = d / 4;
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < d4; c += (int64_t)gridDim.x * 256) {
+  for (int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x; c < d4; c += (int64_t)gridDim.x * 64) {
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j = 0; j < k; ++j) {
       const float4 v = ((const float4 *)(y + (int64_t)p[j] * d))[c];
@@ -742,8 +769,19 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w) {
   if (s_rows == 0) return hipSuccess;
   if (n_expert > kMaxExperts || k > 16 || k > n_expert || k <= 0) return hipErrorInvalidValue;
-  KMOE_LAUNCH(k_route_topk, dim3((unsigned)((s_rows + 3) / 4)), dim3(256), 0, st, logits, s_rows, n_expert, k,
-                     norm_topk, weights_scale, idx, w);
+  const dim3 grid((unsigned)((s_rows + 3) / 4));
+  if (n_expert <= 64)
+    KMOE_LAUNCH(k_route_topk_w<1>, grid, dim3(256), 0, st, logits, s_rows, n_expert, k, norm_topk, weights_scale,
+                idx, w);
+  else if (n_expert <= 128)
+    KMOE_LAUNCH(k_route_topk_w<2>, grid, dim3(256), 0, st, logits, s_rows, n_expert, k, norm_topk, weights_scale,
+                idx, w);
+  else if (n_expert <= 256)
+    KMOE_LAUNCH(k_route_topk_w<4>, grid, dim3(256), 0, st, logits, s_rows, n_expert, k, norm_topk, weights_scale,
+                idx, w);
+  else
+    KMOE_LAUNCH(k_route_topk, grid, dim3(256), 0, st, logits, s_rows, n_expert, k, norm_topk, weights_scale, idx,
+                w);
   return hipGetLastError();
 }
 
@@ -782,8 +820,10 @@ hipError_t launch_combine(hipStream_t st, const float *y, const Routing &rt, int
   for (int64_t s0 = 0; s0 < s_rows; s0 += 65535) {  // tokens along grid y, at most 65535 per launch
     const unsigned ny = (unsigned)(s_rows - s0 < 65535 ? s_rows - s0 : 65535);
     if (vec) {
-      const int64_t d4 = d / 4, gx = (d4 + 255) / 256 < 4 ? (d4 + 255) / 256 : 4;
-      KMOE_LAUNCH(k_combine4, dim3((unsigned)gx, ny), dim3(256), 0, st, y, rt, s0, d, out);
+      // one wave per 64 float4 columns (at most 64 per token), so a small
+      // batch still spreads over many CUs
+      const int64_t d4 = d / 4, gx = (d4 + 63) / 64 < 64 ? (d4 + 63) / 64 : 64;
+      KMOE_LAUNCH(k_combine4, dim3((unsigned)gx, ny), dim3(64), 0, st, y, rt, s0, d, out);
     } else {
       KMOE_LAUNCH(k_combine, dim3((unsigned)((d + 255) / 256), ny), dim3(256), 0, st, y, rt, s_rows, s0, d, out);
     }
