@@ -432,8 +432,9 @@ int kmoe_rope_kv_store(kmoe_ctx *ctx, const float *q_dev, const float *k_dev, co
  * of x over the concatenated q/k/v rows (rows = (n_head + 2 n_kv) head_dim)
  * into qkv_dev [rows] (h_dev [cols] receives the normed row), followed by
  * kmoe_rope_kv_store of its q, k and v parts. Bit-identical to those two
- * calls; on the integer path with interleaved pairs (neox == 0) the
- * projection kernel applies RoPE and stores k and v itself. One token. */
+ * calls; on the integer path with interleaved pairs (neox == 0), or neox
+ * pairs over the whole head (rope_dim == head_dim), the projection kernel
+ * applies RoPE and stores k and v itself. One token. */
 int kmoe_norm_matmul_rope_kv(kmoe_ctx *ctx, float *x_dev, const float *y_dev, const float *norm_w_dev, float eps,
                              int ggml_type, const void *w_dev, size_t w_len, int64_t cols, float *h_dev,
                              float *qkv_dev, int32_t n_head, int32_t n_kv, int32_t head_dim, int32_t rope_dim,

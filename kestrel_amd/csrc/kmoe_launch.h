@@ -218,10 +218,11 @@ hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows
 // and is 0 again when the kernel ends (calls on one counter must not overlap).
 // With done null only the logits and the int8 rows are produced (the caller's
 // next kernel selects the experts). hipErrorNotSupported when out of range.
-// The one-token q/k/v projection with RoPE (interleaved pairs) and the KV
-// store in its epilogue (kmoe_matvec.hip): rows [0, nh*hd) are q, then k,
-// then v; out also receives the raw projection. hipErrorNotSupported for
-// neox pairs or row geometries that do not keep a pair in one wave.
+// The one-token q/k/v projection with RoPE (interleaved pairs, or neox pairs
+// when rope_dim == head_dim) and the KV store in its epilogue
+// (kmoe_matvec.hip): rows [0, nh*hd) are q, then k, then v; out also receives
+// the raw projection. hipErrorNotSupported for partial neox rotation or row
+// geometries that do not keep a pair in one wave.
 struct QkvRope {
   int32_t nh, nkv, hd, rd, neox;
   int64_t pos0;

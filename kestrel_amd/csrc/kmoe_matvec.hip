@@ -64,11 +64,19 @@ enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
 enum { M_QKV = 5 };
 
 // The RoPE + KV store epilogue of a one-token q/k/v projection with
-// interleaved pairs (rows 2i and 2i+1 of a head, dims below rope_dim): row r
+// interleaved pairs (rows 2i and 2i+1 of a head, dims below rope_dim) or
+// neox pairs over the whole head (rows i and i + hd/2): row r
 // of q rotates into q_out, of k into the f16 K cache at the position, of v
 // goes to the f16 V cache; the raw projection is stored in out as well. The
 // expressions are k_rope_kv's: x0*cos - x1*sin for the first of a pair,
 // x0*sin + x1*cos for the second, sincosf of (float)position * inv_freq[i].
+// With neox (rope_dim == head_dim) the kernel runs the rows of a head in the
+// order qkv_row gives, so a wave step's two rows are a pair (i, i + hd/2).
+__device__ __forceinline__ int64_t qkv_row(const QkvRope &q, int64_t r) {
+  if (!q.neox || r >= (int64_t)(q.nh + q.nkv) * q.hd) return r;  // v rows keep their order
+  const int64_t dd = r % q.hd, hb = r - dd;
+  return hb + ((dd & 1) ? (dd >> 1) + q.hd / 2 : dd >> 1);
+}
 __device__ __forceinline__ void qkv_rope_store(const QkvRope &q, int64_t r, float v, float partner) {
   const int64_t nqr = (int64_t)q.nh * q.hd, kvw = (int64_t)q.nkv * q.hd;
   const int64_t p = q.pos0 + (q.pos_dev ? (int64_t)*q.pos_dev : 0);
@@ -76,8 +84,10 @@ __device__ __forceinline__ void qkv_rope_store(const QkvRope &q, int64_t r, floa
     const int dd = (int)(r % q.hd);
     float val = v;
     if (dd < q.rd) {
-      const int i = dd >> 1;
-      const bool first = (dd & 1) == 0;
+      // pairs (2i, 2i+1), or with neox (i, i + rd/2)
+      const int hr = q.rd >> 1;
+      const int i = q.neox ? (dd < hr ? dd : dd - hr) : dd >> 1;
+      const bool first = q.neox ? dd < hr : (dd & 1) == 0;
       const float ang = (float)p * q.inv_freq[i];
       float sv, cv;
       sincosf(ang, &sv, &cv);
@@ -882,7 +892,9 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
             const int64_t r = r0 + (int64_t)u * RPW;
             if (r < rows) {
               constexpr bool TL = MODE == M_GATE_UP;  // expert tier rows are tiled, plain rows are GGUF
-              w_load<TYPE, TL>(w0[u], W0 + r * row_bytes, t, nblk);
+              int64_t rw = r;
+              if constexpr (MODE == M_QKV) rw = qkv_row(a.rope, r);
+              w_load<TYPE, TL>(w0[u], W0 + rw * row_bytes, t, nblk);
               if constexpr (MODE == M_GATE_UP) w_load<TYPE, TL>(w1[u], W1 + r * row_bytes, t, nblk);
             }
           }
@@ -922,8 +934,9 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
           const int64_t r = r0 + (int64_t)u * RPW;
           if (r >= rows) continue;
           if constexpr (MODE == M_QKV) {
-            a.out[r] = acc0[u];
-            qkv_rope_store(a.rope, r, acc0[u], pair[u]);
+            const int64_t rw = qkv_row(a.rope, r);
+            a.out[rw] = acc0[u];
+            qkv_rope_store(a.rope, rw, acc0[u], pair[u]);
           } else if constexpr (MODE == M_GATE_UP) {  // SwiGLU (transformer.rs:558)
             const float g = acc0[u];
             const float den = 1.0f + expf_cr(-g);
@@ -1509,8 +1522,8 @@ static hipError_t launch_qkv_reg(hipStream_t st, const MvArgs &a) {
 hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                                   const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
                                   const QkvRope &rope) {
-  if (rope.neox || rope.hd <= 0 || rope.hd % 2 || rope.rd % 2 || rope.rd > rope.hd || rope.nh < 1 || rope.nkv < 0 ||
-      rows != (int64_t)(rope.nh + 2 * rope.nkv) * rope.hd)
+  if ((rope.neox && rope.rd != rope.hd) || rope.hd <= 0 || rope.hd % 2 || rope.rd % 2 || rope.rd > rope.hd ||
+      rope.nh < 1 || rope.nkv < 0 || rows != (int64_t)(rope.nh + 2 * rope.nkv) * rope.hd)
     return hipErrorNotSupported;
   if (!act_fits(type, cols)) return hipErrorNotSupported;
   MvArgs a{};

@@ -493,19 +493,25 @@ def test_decoder_context_full(ctx):
         dec.close()
 
 
-@pytest.mark.parametrize("t,cols,nh,nkv,hd,rd,neox,regime,use_dev", [
-    (Q4_K, 2048, 16, 4, 128, 128, False, 0, False),  # 32 lanes per row: the projection applies RoPE
-    (Q4_K, 1024, 8, 2, 64, 32, False, 1, True),      # 16 lanes per row, partial rope_dim, device position
-    (Q8_0, 2048, 16, 4, 128, 128, False, 0, True),
-    (Q4_K, 4096, 8, 2, 128, 128, False, 0, False),   # 64 lanes per row: separate kernels
-    (Q4_K, 2048, 16, 4, 128, 128, True, 0, False),   # neox pairs: separate kernels
-    (Q4_K, 2048, 16, 4, 128, 128, False, 2, False),  # exact regime: separate kernels
+@pytest.mark.parametrize("t,cols,nh,nkv,hd,rd,neox,regime,use_dev,fused", [
+    (Q4_K, 2048, 16, 4, 128, 128, False, 0, False, True),  # 32 lanes per row: the projection applies RoPE
+    (Q4_K, 1024, 8, 2, 64, 32, False, 1, True, True),      # 16 lanes per row, partial rope_dim, device position
+    (Q8_0, 2048, 16, 4, 128, 128, False, 0, True, False),  # Q8_0 at 2048 columns: 64 lanes per row
+    (Q8_0, 1024, 16, 4, 128, 128, False, 0, True, True),
+    (Q4_K, 4096, 8, 2, 128, 128, False, 0, False, False),  # 64 lanes per row: separate kernels
+    (Q4_K, 2048, 16, 4, 128, 128, True, 0, False, True),   # neox pairs over the whole head
+    (Q4_K, 1024, 8, 2, 64, 64, True, 1, True, True),       # neox, 16 lanes per row, device position
+    (Q8_0, 1024, 16, 4, 128, 128, True, 0, True, True),
+    (Q4_K, 1024, 8, 2, 64, 32, True, 0, False, False),     # neox over part of the head: separate kernels
+    (Q4_K, 2048, 16, 4, 128, 128, False, 2, False, False),  # exact regime: separate kernels
 ])
-def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, nkv, hd, rd, neox, regime, use_dev):
+def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, nkv, hd, rd, neox, regime, use_dev,
+                                                         fused):
     """kmoe_norm_matmul_rope_kv against kmoe_norm_matmul followed by
     kmoe_rope_kv_store on one token: the residual, the normed row, the
     projection, the rotated q and both caches are the same bits, for two
-    positions in a row."""
+    positions in a row; the RoPE epilogue of the projection ran where the
+    geometry allows it."""
     import torch
 
     rows, n_ctx = (nh + 2 * nkv) * hd, 16
@@ -525,8 +531,11 @@ def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, 
             p0 = 2 if use_dev else pos
             ha = torch.empty((1, cols), dtype=torch.float32).cuda()
             qkva = torch.empty((1, rows), dtype=torch.float32).cuda()
+            ctx.profile_enable(True)
             qa = ctx.norm_matmul_rope_kv(xa, nw, 1e-5, t, w, cols, nh, nkv, hd, rd, p0, f, neox, n_ctx, caches[0],
                                          caches[1], y=y, pos_dev=pos_dev, h=ha, qkv=qkva)
+            assert ctx.profile_read("matvec_qkv_rope")[1] == (1 if fused else 0)
+            ctx.profile_enable(False)
             hb = torch.empty((1, cols), dtype=torch.float32).cuda()
             qkvb = ctx.norm_matmul(xb, nw, 1e-5, t, w, rows, cols, y=y, h=hb)
             qb = ctx.rope_kv_store(qkvb[:, :nq], qkvb[:, nq:nq + kvw], qkvb[:, nq + kvw:], nh, nkv, hd, rd, p0, f,
@@ -537,6 +546,7 @@ def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, 
                 assert np.array_equal(host(u), host(v)), pos
             assert host(caches[0])[pos].any() and host(caches[1])[pos].any()
     finally:
+        ctx.profile_enable(False)
         ctx.set_regime(0)
 
 
