@@ -107,6 +107,7 @@ static std::mutex g_scratch_mu;
 // Device completion counters per context (words used by the decode router).
 constexpr int kCounterWords = 64;
 constexpr int kNormDone = 1;  // the decode router's residual writer (kmoe_norm_moe_ffn)
+constexpr int kFewRows = 3;   // decode batches over narrow rows: experts of 1..3 rows take launch_few_int
 
 struct kmoe_ctx {
   int device = 0;
@@ -1493,7 +1494,16 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       if (e == hipSuccess) small_rows = small_rows_for(d, 0, S);
       else if (e != hipErrorNotSupported) HIP_OK(c, e);
     }
-    if (S > small_rows) {
+    if (small_ok && small_rows == 0 && (gt == KMOE_Q8_0 || (L->tiled[0] && L->tiled[1]))) {  // narrow rows, 1-3 rows
+      const hipError_t e = timed(c, "moe_gate_up_few", [&]() {
+        return launch_few_int(st, 0, gt, tier, F, d, rt, regime, max_active, w.xq, w.xd, w.xs, w.h, kFewRows, gd);
+      });
+      if (e == hipSuccess) small_rows = kFewRows;
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    // AVX2 regime: experts of 4 or more rows are the f32 path's
+    const bool more_int = regime == KMOE_REGIME_INT8 || small_rows < 3;
+    if (S > small_rows && more_int) {
       hipError_t e = hipErrorNotSupported;
       if (mfma && gt == KMOE_Q4_K)
         e = timed(c, "moe_gate_up_mfma", [&]() {
@@ -1540,7 +1550,14 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       if (e == hipSuccess) small_rows = small_rows_for(F, 1, S);
       else if (e != hipErrorNotSupported) HIP_OK(c, e);
     }
-    if (S > small_rows) {
+    if (small_ok && small_rows == 0 && (dt == KMOE_Q8_0 || L->tiled[2])) {
+      const hipError_t e = timed(c, "moe_down_few", [&]() {
+        return launch_few_int(st, 1, dt, tier, d, F, rt, regime, max_active, w.hq, w.hd, w.hs, w.y, kFewRows, dd);
+      });
+      if (e == hipSuccess) small_rows = kFewRows;
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (S > small_rows && (regime == KMOE_REGIME_INT8 || small_rows < 3)) {
       hipError_t e = hipErrorNotSupported;
       if (mfma && dt == KMOE_Q4_K)
         e = timed(c, "moe_down_mfma", [&]() {

@@ -152,6 +152,14 @@ hipError_t launch_moe_int(hipStream_t st, int mode, int type, const ExpertTier &
                           const float *xd, const int32_t *xbs, float *out, int min_rows = 0,
                           const BlockDbg *dbg = nullptr);
 
+// Experts with 1..max_rows (at most 3) rows on the int path, rows of at most
+// 64 task slots (the one-token register kernel's geometry, each weight task
+// dotted with all of the expert's rows): as launch_moe_int, for those experts.
+// hipErrorNotSupported for wider rows or max_rows outside 1..3.
+hipError_t launch_few_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                          const Routing &rt, int regime, int max_active, const int8_t *xq, const float *xd,
+                          const int32_t *xbs, float *out, int max_rows, const BlockDbg *dbg = nullptr);
+
 // ---- int8 matrix-core path (kmoe_mfma.hip), Q4_K weights x Q8_K rows
 // Token rows at which the matrix-core kernels take over.
 constexpr int kMfmaMinRows = 8;

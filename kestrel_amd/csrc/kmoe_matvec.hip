@@ -51,6 +51,7 @@ struct MvArgs {
   int regime;
   int rows_per_block;
   int min_rows;  // grouped modes: experts with fewer rows are another kernel's
+  int max_rows;  // k_few_int: experts with more rows are another kernel's
   int sel_on;    // M_GATE_UP, one token: select the experts from sel.logits here
   DecSelect sel;
   QkvRope rope;  // M_QKV: the epilogue of the one-token q/k/v projection
@@ -1539,6 +1540,144 @@ hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, in
   if (type == T_Q4_K) return launch_qkv_reg<T_Q4_K>(st, a);
   if (type == T_Q6_K) return launch_qkv_reg<T_Q6_K>(st, a);
   if (type == T_Q8_0) return launch_qkv_reg<T_Q8_0>(st, a);
+  return hipErrorNotSupported;
+}
+
+// Experts with 1..NT token rows on the int path (decode batches) over rows too
+// narrow for the tiled few-rows kernels (kmoe_small.hip): the one-token
+// register kernel's lane geometry (LPR lanes per row, one task per lane, RPW
+// rows per wave) with the activation slices of the expert's NT rows in
+// registers, so each weight task is loaded once and dotted with every row of
+// the expert. MODE 0: gate and up rows, SwiGLU (transformer.rs:558), h[slot];
+// the slices are the slots' token rows of the Q8_K/Q8 x. MODE 1: down rows,
+// y[slot]; the slices are the slots' int8 h rows. Items are (active expert,
+// block of 4*RPW rows) in the active list's order; an expert outside
+// [min_rows, max_rows] or off the int path skips its items. Slots past the
+// expert's rows repeat its last (loads unconditional, results dropped).
+// DBG: the per-block integers are added into a.dbg as the other int kernels do.
+template <int TYPE, int LPR, int NT, int MODE, bool DBG>
+__global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int RB = 4 * RPW;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row_in_wave = lane / LPR, lr = lane % LPR;
+  const int64_t cols = a.cols, rows = a.rows;
+  const int64_t nblk = cols / QT<TYPE>::EL;
+  const int ntasks = (int)(QT<TYPE>::TPB * nblk);
+  const int64_t row_bytes = nblk * QT<TYPE>::BYTES;
+  const int64_t xs_stride = cols / 16;
+  const bool tv = lr < ntasks;
+  const int t = tv ? lr : ntasks - 1;
+  const int64_t bpe = (rows + RB - 1) / RB;
+  const int64_t total = (int64_t)(*a.rt.n_active) * bpe;
+  const int K = a.rt.topk;
+  for (int64_t b = blockIdx.x; b < total; b += gridDim.x) {
+    const int i = (int)(b / bpe);
+    const int64_t rblk = b - (int64_t)i * bpe;
+    const int e = a.rt.active[i];
+    const int64_t p0 = a.rt.offsets[e];
+    const int n = (int)(a.rt.offsets[e + 1] - (uint32_t)p0);
+    if (n < a.min_rows || n > a.max_rows || !int_regime(a.regime, n)) continue;
+    const int64_t r = rblk * RB + (int64_t)wave * RPW + row_in_wave;
+    const int64_t rc = r < rows ? r : rows - 1;
+    ActSlice<TYPE> act[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t p = p0 + (j < n ? j : n - 1);
+      const int64_t src = MODE == 0 ? (int64_t)(a.rt.perm[p] / (uint32_t)K) : p;  // token row, or the slot's h row
+      act_load<TYPE>(act[j], a.xq + src * cols, a.xd + src * nblk, a.xbs + src * xs_stride, t);
+    }
+    const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
+    WTask<TYPE, true> w0, w1;
+    w_load<TYPE, true>(w0, eb + a.tier.off[MODE == 0 ? 0 : 2] + rc * row_bytes, t, nblk);
+    if constexpr (MODE == 0) w_load<TYPE, true>(w1, eb + a.tier.off[1] + rc * row_bytes, t, nblk);
+    float g[NT], u[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      int32_t *ds0 = nullptr, *dm0 = nullptr, *ds1 = nullptr, *dm1 = nullptr;
+      if constexpr (DBG) {
+        if (tv && j < n && r < rows) {
+          const int64_t o = ((p0 + j) * rows + r) * nblk;
+          ds0 = a.dbg.s[0] ? a.dbg.s[0] + o : nullptr;
+          dm0 = a.dbg.m[0] ? a.dbg.m[0] + o : nullptr;
+          ds1 = a.dbg.s[1] ? a.dbg.s[1] + o : nullptr;
+          dm1 = a.dbg.m[1] ? a.dbg.m[1] + o : nullptr;
+        }
+      }
+      const float vg = task_dot<TYPE>(w0, t, act[j], 0.0f, ds0, dm0);
+      g[j] = group_sum<LPR>(tv ? vg : 0.0f);
+      if constexpr (MODE == 0) {
+        const float vu = task_dot<TYPE>(w1, t, act[j], 0.0f, ds1, dm1);
+        u[j] = group_sum<LPR>(tv ? vu : 0.0f);
+      }
+    }
+    if (lr == 0 && r < rows) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (j >= n) break;
+        if constexpr (MODE == 0) {  // SwiGLU: g / (1 + exp(-g)) * u
+          const float den = 1.0f + expf_cr(-g[j]);
+          const float q = g[j] / den;
+          a.out[(p0 + j) * rows + r] = q * u[j];
+        } else {
+          a.out[(p0 + j) * rows + r] = g[j];
+        }
+      }
+    }
+  }
+}
+
+template <int TYPE, int MODE>
+static hipError_t launch_few_int_t(hipStream_t st, const MvArgs &a, int lpr, int max_active, bool dbg) {
+  const int rpw = 64 / lpr;
+  const int64_t bpe = (a.rows + 4 * rpw - 1) / (4 * rpw);
+  const int64_t items = (int64_t)max_active * bpe;
+  const int64_t cap = (int64_t)cu_count() * kGridMult;
+  const unsigned grid = (unsigned)(items < cap ? items : cap);
+#define KMOE_FEW(L)                                                                              \
+  do {                                                                                           \
+    if (dbg) KMOE_LAUNCH((k_few_int<TYPE, L, 3, MODE, true>), dim3(grid), dim3(256), 0, st, a);  \
+    else KMOE_LAUNCH((k_few_int<TYPE, L, 3, MODE, false>), dim3(grid), dim3(256), 0, st, a);     \
+    return hipGetLastError();                                                                    \
+  } while (0)
+  if (lpr == 16) KMOE_FEW(16);
+  if (lpr == 32) KMOE_FEW(32);
+  if (lpr == 64) KMOE_FEW(64);
+#undef KMOE_FEW
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_few_int(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                          const Routing &rt, int regime, int max_active, const int8_t *xq, const float *xd,
+                          const int32_t *xbs, float *out, int max_rows, const BlockDbg *dbg) {
+  if (rows <= 0 || max_active <= 0) return hipSuccess;
+  if (max_rows < 1 || max_rows > 3 || !act_fits(type, cols)) return hipErrorNotSupported;
+  const int ntasks = (int)((is_kquant(type) ? 4 : 1) * (cols / (is_kquant(type) ? 256 : 32)));
+  int lpr, tpl;
+  if (!reg_geometry(type, ntasks, lpr, tpl) || tpl != 1) return hipErrorNotSupported;
+  MvArgs a{};
+  if (dbg) a.dbg = *dbg;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = xq;
+  a.xd = xd;
+  a.xbs = xbs;
+  a.out = out;
+  a.tier = tier;
+  a.rt = rt;
+  a.regime = regime;
+  a.min_rows = 1;
+  a.max_rows = max_rows;
+  const bool g = dbg != nullptr;
+  if (type == T_Q4_K)
+    return mode == 0 ? launch_few_int_t<T_Q4_K, 0>(st, a, lpr, max_active, g)
+                     : launch_few_int_t<T_Q4_K, 1>(st, a, lpr, max_active, g);
+  if (type == T_Q6_K)
+    return mode == 0 ? launch_few_int_t<T_Q6_K, 0>(st, a, lpr, max_active, g)
+                     : launch_few_int_t<T_Q6_K, 1>(st, a, lpr, max_active, g);
+  if (type == T_Q8_0)
+    return mode == 0 ? launch_few_int_t<T_Q8_0, 0>(st, a, lpr, max_active, g)
+                     : launch_few_int_t<T_Q8_0, 1>(st, a, lpr, max_active, g);
   return hipErrorNotSupported;
 }
 

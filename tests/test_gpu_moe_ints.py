@@ -198,7 +198,9 @@ def test_single_token_fine_grained_integers_bit_exact_extreme_ranges(ctx, orc, d
     (8, 1, 4096, 8192, 4, 2, (Q4_K, Q4_K), 7),    # few-rows up to 4 rows, matrix cores above
     (40, 1, 1024, 512, 4, 2, (Q4_K, Q4_K), 8),    # int8 matrix cores
     (12, 1, 1024, 768, 8, 2, (Q4_K, Q6_K), 9),    # matrix cores (gate/up), LDS-staged kernel (Q6_K down)
-    (16, 1, 2048, 768, 128, 8, (Q4_K, Q4_K), 10),  # Qwen3 shape
+    (16, 1, 2048, 768, 128, 8, (Q4_K, Q4_K), 10),  # Qwen3 shape: narrow few-rows kernels for 1-3 rows
+    (16, 0, 2048, 768, 128, 8, (Q4_K, Q4_K), 14),  # AVX2: f32 for experts with >= 4 rows, narrow few-rows for 1-3
+    (6, 1, 2048, 1408, 64, 6, (Q4_K, Q8_0), 15),   # DeepSeek-V2-Lite shape: narrow few-rows kernels, Q8_0 down
     (24, 1, 1024, 768, 4, 2, (Q4_K, Q4_K), 12),   # streaming matrix-core kernel (<= 32 rows), 3 down superblocks
     (32, 1, 2048, 1536, 8, 2, (Q4_K, Q4_K), 13),  # few-rows kernels up to 4 rows, streaming kernel above
     (9, 1, 1024, 512, 8, 2, (Q8_0, Q8_0), 11),    # LDS-staged kernels, Q8_0
