@@ -1551,10 +1551,11 @@ hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, in
 // the expert. MODE 0: gate and up rows, SwiGLU (transformer.rs:558), h[slot];
 // the slices are the slots' token rows of the Q8_K/Q8 x. MODE 1: down rows,
 // y[slot]; the slices are the slots' int8 h rows. Items are (active expert,
-// block of 4*RPW rows) in the active list's order; an expert outside
-// [min_rows, max_rows] or off the int path skips its items. Slots past the
+// block of 4*RPW rows) over the experts with min_rows..max_rows rows on the
+// int path, in the active list's order (at most 256 experts). Slots past the
 // expert's rows repeat its last (loads unconditional, results dropped).
 // DBG: the per-block integers are added into a.dbg as the other int kernels do.
+constexpr int kFewMaxExperts = 256;
 template <int TYPE, int LPR, int NT, int MODE, bool DBG>
 __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
   constexpr int RPW = 64 / LPR;
@@ -1569,15 +1570,37 @@ __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
   const bool tv = lr < ntasks;
   const int t = tv ? lr : ntasks - 1;
   const int64_t bpe = (rows + RB - 1) / RB;
-  const int64_t total = (int64_t)(*a.rt.n_active) * bpe;
   const int K = a.rt.topk;
+  // the experts this kernel takes, in active-list order (wave 0 ballots over
+  // the active list), so items are only theirs
+  __shared__ int32_t qe[kFewMaxExperts];
+  __shared__ int32_t nq_s;
+  if (wave == 0) {
+    const int na = *a.rt.n_active;
+    int nq = 0;
+    for (int j0 = 0; j0 < na; j0 += 64) {
+      const int j = j0 + lane;
+      bool ok = false;
+      int e = 0;
+      if (j < na) {
+        e = a.rt.active[j];
+        const int n = (int)(a.rt.offsets[e + 1] - a.rt.offsets[e]);
+        ok = n >= a.min_rows && n <= a.max_rows && int_regime(a.regime, n);
+      }
+      const uint64_t m = __ballot(ok);
+      if (ok) qe[nq + __popcll(m & ((1ull << lane) - 1))] = e;
+      nq += __popcll(m);
+    }
+    if (lane == 0) nq_s = nq;
+  }
+  __syncthreads();
+  const int64_t total = (int64_t)nq_s * bpe;
   for (int64_t b = blockIdx.x; b < total; b += gridDim.x) {
     const int i = (int)(b / bpe);
     const int64_t rblk = b - (int64_t)i * bpe;
-    const int e = a.rt.active[i];
+    const int e = qe[i];
     const int64_t p0 = a.rt.offsets[e];
     const int n = (int)(a.rt.offsets[e + 1] - (uint32_t)p0);
-    if (n < a.min_rows || n > a.max_rows || !int_regime(a.regime, n)) continue;
     const int64_t r = rblk * RB + (int64_t)wave * RPW + row_in_wave;
     const int64_t rc = r < rows ? r : rows - 1;
     ActSlice<TYPE> act[NT];
@@ -1651,7 +1674,8 @@ hipError_t launch_few_int(hipStream_t st, int mode, int type, const ExpertTier &
                           const Routing &rt, int regime, int max_active, const int8_t *xq, const float *xd,
                           const int32_t *xbs, float *out, int max_rows, const BlockDbg *dbg) {
   if (rows <= 0 || max_active <= 0) return hipSuccess;
-  if (max_rows < 1 || max_rows > 3 || !act_fits(type, cols)) return hipErrorNotSupported;
+  if (max_rows < 1 || max_rows > 3 || max_active > kFewMaxExperts || !act_fits(type, cols))
+    return hipErrorNotSupported;
   const int ntasks = (int)((is_kquant(type) ? 4 : 1) * (cols / (is_kquant(type) ? 256 : 32)));
   int lpr, tpl;
   if (!reg_geometry(type, ntasks, lpr, tpl) || tpl != 1) return hipErrorNotSupported;
