@@ -197,7 +197,7 @@ PROFILE_NAMES = ("add_rows", "argmax", "attention", "attention_q8", "block_sums_
                  "block_sums_q6k", "block_sums_q8_0", "combine", "dequant_x", "dispatch", "gemm_f32", "get_rows",
                  "kv_store", "matmul_f32_ordered", "matvec_q4k", "matvec_q4k_mfma", "matvec_q6k", "matvec_q8_0",
                  "matvec_qkv_rope", "matvec_unpacked", "moe_down_dec", "moe_down_f32", "moe_down_f32_rows", "moe_down_few",
-                 "moe_down_int", "moe_gate_up_few",
+                 "moe_down_int", "moe_down_shared", "moe_gate_up_few",
                  "moe_down_mfma", "moe_down_small", "moe_gate_f32", "moe_gate_up_dec", "moe_gate_up_f32_rows", "moe_gate_up_int",
                  "moe_gate_up_mfma", "moe_gate_up_small", "moe_up_f32", "pos_advance", "quant_q8", "quant_q8k",
                  "quant_slots_q8", "quant_slots_q8k", "rmsnorm", "rmsnorm_quant", "rope", "rope_kv",

@@ -1342,6 +1342,40 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
   MoeWs w = carve_moe(wsb, S, E, k, d, F, &tmp);
   const int regime = c->regime;
   hipStream_t st = c->stream;
+  // The shared expert's workspace: gate/up outputs [S, 2 Fs], ys [S, d], its
+  // gate logits [S] and its int8 rows.
+  float *sh_gs = nullptr, *sh_us = nullptr, *sh_ys = nullptr, *sh_gl = nullptr;
+  QRows sh_qr{};
+  if (L->sh.on) {
+    Carver cv{wsb + moe_need};
+    sh_gs = cv.take<float>(2 * S * Fs);
+    sh_us = sh_gs + S * Fs;
+    sh_ys = cv.take<float>(S * d);
+    sh_gl = cv.take<float>(S);
+    size_t q = 0;
+    sh_qr = carve_qrows(wsb + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
+  }
+  // One token on the int8 path, the shared gate and up of one type stored
+  // back to back (one [2 Fs, d] matrix): one product over both reads the int8
+  // row of h made for the routed experts (the same Q8KRow / Q8Row
+  // quantization) and one kernel applies SwiGLU and quantizes its output.
+  auto sh_fast = [&](bool x_is_int) {
+    const auto &SH = L->sh;
+    return L->sh.on && S == 1 && x_is_int && int_path(regime, 1) && SH.type[0] != KMOE_F32 &&
+           SH.type[1] == SH.type[0] && SH.type[2] != KMOE_F32 && is_kq(SH.type[0]) == is_kq(D.gate_type) &&
+           SH.off[1] == SH.off[0] + SH.len[0];
+  };
+  bool sh_front_done = false;  // the shared gate/up and SwiGLU + int8 rows are done
+  bool sh_done = false;        // and its add into out
+  auto sh_front = [&]() -> int {
+    const auto &SH = L->sh;
+    if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, sh_gl, true));
+    const int r = matvec_q8_impl(c, SH.type[0], SH.arena + SH.off[0], 2 * Fs, d, w.xq, w.xd, w.xs, 1, sh_gs);
+    if (r) return r;
+    LAUNCH(c, "shared_swiglu_quant", launch_swiglu_quant(st, SH.type[2], sh_gs, Fs, sh_qr.q, sh_qr.d, sh_qr.s));
+    sh_front_done = true;
+    return KMOE_OK;
+  };
   // Capture of the int-path integers (kmoe_moe_ffn_dbg): zeroed here, added to by the kernels.
   BlockDbg gdbg, ddbg;
   const BlockDbg *gd = nullptr, *dd = nullptr;
@@ -1463,6 +1497,21 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
              launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
       h_int = true;
+      if (!dd && sh_fast(x_int)) {  // the shared expert's down row in the routed down kernel
+        rc = sh_front();
+        if (rc) return rc;
+        const auto &SH = L->sh;
+        const SharedDown sd{SH.type[2], SH.arena + SH.off[2], Fs, sh_qr.q, sh_qr.d, sh_qr.s,
+                            SH.gate_ok ? sh_gl : nullptr};
+        e = timed(c, "moe_down_shared", [&]() {
+          return launch_decode_down_shared(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out, sd);
+        });
+        if (e == hipSuccess) {
+          sh_done = true;
+          goto done;
+        }
+        if (e != hipErrorNotSupported) HIP_OK(c, e);
+      }
       e = timed(c, "moe_down_dec",
                 [&]() { return launch_decode_down_combine(st, dt, tier, d, F, rt, w.hq, w.hd, w.hs, out, dd); });
       if (e != hipErrorNotSupported) {
@@ -1606,26 +1655,19 @@ done:
       if (rc) return rc;
     }
   }
-  if (L->sh.on) {  // shared expert after the routed combine (transformer.rs:572-587)
+  if (L->sh.on && !sh_done) {  // shared expert after the routed combine (transformer.rs:572-587)
     auto &SH = L->sh;
-    Carver cv{wsb + moe_need};
-    float *gs = cv.take<float>(2 * S * Fs), *us = gs + S * Fs, *ys = cv.take<float>(S * d);
-    float *gl = cv.take<float>(S);
-    size_t q = 0;
-    QRows qr = carve_qrows(wsb + moe_need + cv.off, S, mx, &q, sh_part_floats(Fs, d, S));
-    // One token on the int8 path, gate and up of one type stored back to back
-    // (they are one [2 Fs, d] matrix): one product over both reads the int8
-    // row of h already made for the routed experts (the same Q8KRow / Q8Row
-    // quantization), one kernel applies SwiGLU and quantizes its output, and
-    // the down product adds its gated result into out. Same arithmetic as the
-    // general sequence below.
-    const int t0 = SH.type[0], t2 = SH.type[2];
-    if (S == 1 && x_int && int_path(regime, 1) && t0 != KMOE_F32 && SH.type[1] == t0 && t2 != KMOE_F32 &&
-        is_kq(t0) == is_kq(gt) && SH.off[1] == SH.off[0] + SH.len[0]) {
-      if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, gl, true));
-      rc = matvec_q8_impl(c, t0, SH.arena + SH.off[0], 2 * Fs, d, w.xq, w.xd, w.xs, 1, gs);
-      if (rc) return rc;
-      LAUNCH(c, "shared_swiglu_quant", launch_swiglu_quant(st, t2, gs, Fs, qr.q, qr.d, qr.s));
+    float *gs = sh_gs, *us = sh_us, *ys = sh_ys, *gl = sh_gl;
+    const QRows &qr = sh_qr;
+    // One token on the int8 path: the fast front (above), then the down
+    // product adds its gated result into out. Same arithmetic as the general
+    // sequence below.
+    const int t2 = SH.type[2];
+    if (sh_fast(x_int)) {
+      if (!sh_front_done) {
+        rc = sh_front();
+        if (rc) return rc;
+      }
       const AddEpi epi{SH.gate_ok ? gl : nullptr};
       const hipError_t e = timed(c, "shared_down_add", [&]() {
         return launch_decode_plain(st, t2, SH.arena + SH.off[2], d, Fs, qr.q, qr.d, qr.s, out, &epi);

@@ -141,6 +141,26 @@ hipError_t launch_dec_rows(hipStream_t st, const uint8_t *w, int64_t rows, int64
 hipError_t launch_decode_down_combine(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                       const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
                                       float *out, const BlockDbg *dbg = nullptr);
+// The shared expert's down rows (GGUF, type Q4_K or Q6_K) against its int8 row
+// (sh.xq/xd/xbs: Q8_K of SwiGLU(gate, up), as launch_swiglu_quant writes it);
+// logit: its gate's logit (sigmoid scale), or null for an ungated one.
+struct SharedDown {
+  int type;
+  const uint8_t *w;
+  int64_t cols;
+  const int8_t *xq;
+  const float *xd;
+  const int32_t *xbs;
+  const float *logit;
+};
+// launch_decode_down_combine with the shared expert added in the same kernel:
+// out[r] = (sum_e (asc) w_e * y_e[r]) + scale * shared[r], the arithmetic and
+// order of the down + combine kernel followed by the shared add.
+// hipErrorNotSupported (nothing launched) where the two rows do not share a
+// launch shape; then the caller runs them separately.
+hipError_t launch_decode_down_shared(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                     const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
+                                     float *out, const SharedDown &sh);
 // Block sums (debug path of the same device code).
 hipError_t launch_block_sums(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                              const int8_t *xq, const int32_t *xbs, int64_t s_rows, int32_t *sumi, int32_t *mins);

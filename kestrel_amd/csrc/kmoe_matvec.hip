@@ -59,6 +59,14 @@ struct MvArgs {
   int add;        // M_PLAIN: out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
   int32_t chunk;  // LDS-staged plain modes: activation rows per work-group (blockIdx.y picks the chunk)
   const float *add_logit;
+  // k_mv_down_exp with SHT != 0: the shared expert's down rows (GGUF, sh_cols
+  // columns) against its int8 row, added after the routed combine
+  const uint8_t *sh_w;
+  int64_t sh_cols;
+  const int8_t *sh_xq;
+  const float *sh_xd;
+  const int32_t *sh_xbs;
+  const float *sh_logit;
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -1214,7 +1222,7 @@ __global__ void __launch_bounds__(256) k_down_ring(MvArgs a, int rb_rows) {
 // ids, slots and weights are read once per lane up front (lane j: selection
 // j), so no dependent load sits between the weight loads. WPB waves per
 // work-group, each RPW = 64 / LPR rows.
-template <int TYPE, int LPR, int KMAX, int NS, int WPB, bool DBG>
+template <int TYPE, int LPR, int KMAX, int NS, int WPB, bool DBG, int SHT = 0>
 __global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
   constexpr int RPW = 64 / LPR;
   constexpr int RB = WPB * RPW;  // rows per block-task
@@ -1227,6 +1235,24 @@ __global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
   const int64_t xs_stride = cols / 16;
   const bool tv = lr < ntasks;
   const int t = tv ? lr : ntasks - 1;
+  // The shared expert (SHT): its row's task of this lane, its int8 slice
+  // (loaded once) and its gate (k_shared_add's arithmetic: sigmoid of the
+  // logit, 1 without a gate).
+  constexpr int ST = SHT ? SHT : TYPE;
+  const int64_t sh_nblk = SHT ? a.sh_cols / QT<ST>::EL : 0;
+  const int sh_ntasks = (int)(QT<ST>::TPB * sh_nblk);
+  const int64_t sh_row_bytes = sh_nblk * QT<ST>::BYTES;
+  const bool sh_tv = lr < sh_ntasks;
+  const int sh_t = sh_tv ? lr : (SHT ? sh_ntasks - 1 : 0);
+  ActSlice<ST> sh_act;
+  float sh_scale = 1.0f;
+  if constexpr (SHT != 0) {
+    act_load<ST>(sh_act, a.sh_xq, a.sh_xd, a.sh_xbs, sh_t);
+    if (a.sh_logit) {
+      const float den = 1.0f + expf_cr(-*a.sh_logit);
+      sh_scale = 1.0f / den;
+    }
+  }
   const int K = a.rt.topk;
   const int jl = lane < K ? lane : 0;
   const int32_t e_l = a.rt.active[jl];  // expert of slot jl
@@ -1248,6 +1274,8 @@ __global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
     };
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) issue(sl, sl);
+    WTask<ST, false> sh_w;  // the shared row, in flight with the experts' first loads
+    if constexpr (SHT != 0) w_load<ST, false>(sh_w, a.sh_w + rc * sh_row_bytes, sh_t, sh_nblk);
     float o = 0.0f;
 #pragma unroll
     for (int ia = 0; ia < KMAX; ++ia) {  // ascending expert id: slot ia
@@ -1269,6 +1297,12 @@ __global__ void __launch_bounds__(64 * WPB) k_mv_down_exp(MvArgs a) {
       const float on = o + c;
       o = ia < K ? on : o;
       if (ia + NS < KMAX) issue(ia + NS, sl);
+    }
+    if constexpr (SHT != 0) {  // out[r] = combine + scale * shared (transformer.rs:572-587)
+      const float v = task_dot<ST, false>(sh_w, sh_t, sh_act, 0.0f);
+      const float y = group_sum<LPR>(sh_tv ? v : 0.0f);
+      const float pv = sh_scale * y;
+      o = o + pv;
     }
     if (lr == 0 && r < rows) a.out[r] = o;
   }
@@ -1744,6 +1778,74 @@ hipError_t launch_down_exp(hipStream_t st, const MvArgs &a, int ntasks, int topk
 #undef KMOE_DX_W
 #undef KMOE_DX_K
 #undef KMOE_DX
+  return hipErrorNotSupported;
+}
+
+// The register down + combine over narrow rows with the shared expert's down
+// row fused in (k_mv_down_exp<..., SHT>): the launch shape of launch_down_exp,
+// for the shapes where both rows take the same lanes per row and one task
+// slot per lane, the routed experts' top-k at most 8 and 4..8 experts' ring.
+template <int TYPE, int SHT>
+static hipError_t launch_down_shared_t(hipStream_t st, const MvArgs &a, int lpr, int topk) {
+  const int rpw = 64 / lpr;
+  int wpb = 4;
+  while (wpb > 1 && (a.rows + rpw * wpb - 1) / (rpw * wpb) < 2 * (int64_t)cu_count()) wpb >>= 1;
+  const int64_t blocks = (a.rows + (int64_t)rpw * wpb - 1) / ((int64_t)rpw * wpb);
+  const int64_t cap = (int64_t)cu_count() * kGridMult * (4 / wpb);
+  const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);
+  const int kmax = topk <= 4 ? 4 : topk <= 6 ? 6 : 8;
+#define KMOE_DS(L, WP)                                                                                         \
+  do {                                                                                                         \
+    if (kmax == 4) KMOE_LAUNCH((k_mv_down_exp<TYPE, L, 4, 3, WP, false, SHT>), dim3(grid), dim3(64 * WP), 0, st, a); \
+    else if (kmax == 6)                                                                                        \
+      KMOE_LAUNCH((k_mv_down_exp<TYPE, L, 6, 3, WP, false, SHT>), dim3(grid), dim3(64 * WP), 0, st, a);     \
+    else KMOE_LAUNCH((k_mv_down_exp<TYPE, L, 8, 3, WP, false, SHT>), dim3(grid), dim3(64 * WP), 0, st, a);  \
+    return hipGetLastError();                                                                                  \
+  } while (0)
+  if (lpr == 64 && wpb == 4) KMOE_DS(64, 4);
+  if (lpr == 32 && wpb == 2) KMOE_DS(32, 2);
+  if (lpr == 16 && wpb == 1) KMOE_DS(16, 1);
+#undef KMOE_DS
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_decode_down_shared(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
+                                     const Routing &rt, const int8_t *hq, const float *hd, const int32_t *hbs,
+                                     float *out, const SharedDown &sh) {
+  if (rt.topk < 1 || rt.topk > 8 || rows <= 0) return hipErrorNotSupported;
+  const int ntasks = (int)((is_kquant(type) ? 4 : 1) * (cols / (is_kquant(type) ? 256 : 32)));
+  const int sh_ntasks = (int)((is_kquant(sh.type) ? 4 : 1) * (sh.cols / (is_kquant(sh.type) ? 256 : 32)));
+  int lpr, tpl, slpr, stpl;
+  if (!act_fits(type, cols) || !act_fits(sh.type, sh.cols)) return hipErrorNotSupported;
+  if (!reg_geometry(type, ntasks, lpr, tpl) || tpl != 1 || !reg_geometry(sh.type, sh_ntasks, slpr, stpl) ||
+      stpl != 1 || slpr != lpr)
+    return hipErrorNotSupported;
+  MvArgs a{};
+  a.s_rows = 1;
+  a.rows = rows;
+  a.cols = cols;
+  a.xq = hq;
+  a.xd = hd;
+  a.xbs = hbs;
+  a.out = out;
+  a.tier = tier;
+  a.rt = rt;
+  a.sh_w = sh.w;
+  a.sh_cols = sh.cols;
+  a.sh_xq = sh.xq;
+  a.sh_xd = sh.xd;
+  a.sh_xbs = sh.xbs;
+  a.sh_logit = sh.logit;
+#define KMOE_DST(T)                                                                             \
+  do {                                                                                          \
+    if (sh.type == T_Q6_K) return launch_down_shared_t<T, T_Q6_K>(st, a, lpr, rt.topk);        \
+    if (sh.type == T_Q4_K) return launch_down_shared_t<T, T_Q4_K>(st, a, lpr, rt.topk);        \
+    return hipErrorNotSupported;                                                                \
+  } while (0)
+  if (type == T_Q8_0) KMOE_DST(T_Q8_0);
+  if (type == T_Q4_K) KMOE_DST(T_Q4_K);
+  if (type == T_Q6_K) KMOE_DST(T_Q6_K);
+#undef KMOE_DST
   return hipErrorNotSupported;
 }
 

@@ -697,23 +697,27 @@ def test_shared_expert_layer(ctx, orc, wtype, ffs, with_gate):
         assert e < TOL, (S, regime, e)
 
 
-@pytest.mark.parametrize("types,ffs,with_gate", [
-    ((Q4_K, Q4_K, Q6_K), C5_SHARED_FF, False),  # DeepSeek-V2-Lite's shared experts
-    ((Q4_K, Q4_K, Q4_K), 1536, True),
-    ((Q8_0, Q8_0, Q8_0), 1024, True),
+@pytest.mark.parametrize("types,ffs,with_gate,rff,rdown,fused", [
+    ((Q4_K, Q4_K, Q6_K), C5_SHARED_FF, False, 1024, None, False),  # DeepSeek-V2-Lite's shared experts
+    ((Q4_K, Q4_K, Q6_K), C5_SHARED_FF, False, 1408, Q8_0, True),   # ... with its routed Q8_0 down: one down kernel
+    ((Q4_K, Q4_K, Q4_K), 1536, True, 1024, None, False),
+    ((Q4_K, Q4_K, Q4_K), 1536, True, 1536, None, True),           # 32 lanes per row on both: one down kernel
+    ((Q8_0, Q8_0, Q8_0), 1024, True, 1024, None, False),
 ])
 @pytest.mark.parametrize("regime", [0, 1])
-def test_shared_expert_one_token_bits_of_product_sequence(ctx, orc, types, ffs, with_gate, regime):
+def test_shared_expert_one_token_bits_of_product_sequence(ctx, orc, types, ffs, with_gate, rff, rdown, fused, regime):
     """One token on the int8 path: the shared expert (one product over the
     back-to-back gate and up rows, SwiGLU fused with the quantization of its
     output, down adding its gated result into out) gives the bits of the
     sequence transformer.rs:572-587 spells out, made of separate calls:
     quant::matmul of gate and of up (kmoe_matmul, the same int8 products),
     SwiGLU and sigmoid with a correctly rounded exp, quant::matmul of down, and
-    out + scale * y on top of the routed experts' output."""
+    out + scale * y on top of the routed experts' output. Where the routed
+    and shared down rows share a launch shape, both run in one kernel (the
+    library's timing names it), with the same bits."""
     d = 2048
     t0, _, t2 = types
-    spec = LayerSpec(16, 4, d, 1024, t0, seed=40 + ffs, quantized=False)
+    spec = LayerSpec(16, 4, d, rff, t0, seed=40 + ffs, quantized=False, down_type=rdown or t0)
     sh = [random_blocks(t0, ffs, d, 910), random_blocks(t0, ffs, d, 911), random_blocks(t2, d, ffs, 912)]
     gi = orc.normal(951, d, 0.0, 0.05) if with_gate else None
     h = orc.normal(952, d).reshape(1, d)
@@ -727,8 +731,12 @@ def test_shared_expert_one_token_bits_of_product_sequence(ctx, orc, types, ffs, 
             try:
                 if shared:
                     ctx.shared_expert(lid, ffs, types, sh[0], sh[1], sh[2], gi)
+                    ctx.profile_enable(True)
                 outs.append(host(ctx.moe_ffn(lid, dev(h))))
+                if shared:
+                    assert ctx.profile_read("moe_down_shared")[1] == (1 if fused else 0)
             finally:
+                ctx.profile_enable(False)
                 ctx.layer_destroy(lid)
         g = host(ctx.matmul(t0, dev(sh[0]), ffs, d, dev(h)))
         u = host(ctx.matmul(t0, dev(sh[1]), ffs, d, dev(h)))
