@@ -1477,10 +1477,24 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     ds.n_active = w.n_active;
     ds.active = w.active;
     x_int = true;
-    hipError_t e = timed(c, "moe_gate_up_dec", [&]() {
-      return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h,
-                                   select_in_gate_up ? &ds : nullptr, gd);
-    });
+    // The shared expert's gate/up as extra items of the same launch, where the
+    // experts take the register kernel (SwiGLU into its row).
+    bool sgu_done = false;
+    hipError_t e = hipErrorNotSupported;
+    if (!gd && sh_fast(true) && L->sh.type[0] == gt) {
+      const SharedGateUp sgu{L->sh.arena + L->sh.off[0], Fs, sh_gs};
+      e = timed(c, "moe_gate_up_dec", [&]() {
+        return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h,
+                                     select_in_gate_up ? &ds : nullptr, gd, &sgu);
+      });
+      if (e == hipSuccess) sgu_done = true;
+      else if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    if (!sgu_done)
+      e = timed(c, "moe_gate_up_dec", [&]() {
+        return launch_decode_gate_up(st, gt, tier, F, d, rt, max_active, w.xq, w.xd, w.xs, w.h,
+                                     select_in_gate_up ? &ds : nullptr, gd);
+      });
     if (e == hipErrorNotSupported && select_in_gate_up) {  // complete the routing from the logits, then as below
       LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
                                                 D.weights_scale, w.idx, w.wsel));
@@ -1494,12 +1508,22 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     if (e != hipErrorNotSupported) {
       HIP_OK(c, e);
       // one row per expert: every slot is on the int8 path in either int8 regime
-      LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
-             launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
+      if (sgu_done) {  // the slots' and the shared row's int8 rows in one launch
+        const auto &SH = L->sh;
+        LAUNCH(c, "quant_slots_shared", launch_quant_two(st, dt, w.h, slots * F, w.hq, w.hd, w.hs, SH.type[2],
+                                                          sh_gs, Fs, sh_qr.q, sh_qr.d, sh_qr.s));
+        if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, sh_gl, true));
+        sh_front_done = true;
+      } else {
+        LAUNCH(c, is_kq(dt) ? "quant_slots_q8k" : "quant_slots_q8",
+               launch_quant_slots(st, dt, w.h, slots, F, rt, w.idx, KMOE_REGIME_INT8, w.hq, w.hd, w.hs));
+      }
       h_int = true;
       if (!dd && sh_fast(x_int)) {  // the shared expert's down row in the routed down kernel
-        rc = sh_front();
-        if (rc) return rc;
+        if (!sh_front_done) {
+          rc = sh_front();
+          if (rc) return rc;
+        }
         const auto &SH = L->sh;
         const SharedDown sd{SH.type[2], SH.arena + SH.off[2], Fs, sh_qr.q, sh_qr.d, sh_qr.s,
                             SH.gate_ok ? sh_gl : nullptr};

@@ -100,10 +100,27 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
 struct DecSelect;
 // sel: the kernel selects the token's experts from its logits and writes the
 // routing (hipErrorNotSupported where decode_gate_up_can_select is false).
+// The shared expert's gate rows (GGUF, `rows` of them, its up rows right
+// after: one [2 rows, cols] matrix) computed with the routed experts' gate/up
+// (one launch), SwiGLU into h [rows].
+struct SharedGateUp {
+  const uint8_t *w;
+  int64_t rows;
+  float *h;
+};
+// sgu (one token, Q4_K or Q8_0 rows on the register kernel, no dbg): the
+// shared expert's gate/up as extra items; hipErrorNotSupported (nothing
+// launched) where the experts take another kernel.
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
                                  const int32_t *xbs, float *h, const DecSelect *sel = nullptr,
-                                 const BlockDbg *dbg = nullptr);
+                                 const BlockDbg *dbg = nullptr, const SharedGateUp *sgu = nullptr);
+// Two int8 quantizations in one launch: rows A (the routed slots' h, all on
+// the int path, launch_quant_slots' arithmetic for one token) and row B (the
+// shared expert's SwiGLU row), each as Q8_K (K-quant down types) or Q8.
+hipError_t launch_quant_two(hipStream_t st, int type_a, const float *ha, int64_t n_a, int8_t *qa, float *da,
+                            int32_t *sa, int type_b, const float *hb, int64_t n_b, int8_t *qb, float *db,
+                            int32_t *sb);
 // Whether launch_decode_gate_up can select the experts for this layer shape.
 bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K);
 // Expert selection done inside the decode gate/up kernel: the token's logits

@@ -59,6 +59,11 @@ struct MvArgs {
   int add;        // M_PLAIN: out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
   int32_t chunk;  // LDS-staged plain modes: activation rows per work-group (blockIdx.y picks the chunk)
   const float *add_logit;
+  // M_GATE_UP, one token: the shared expert's gate rows (GGUF, sgu_rows of
+  // them, its up rows right after) as extra items, SwiGLU into sgu_h
+  const uint8_t *sgu_w;
+  int64_t sgu_rows;
+  float *sgu_h;
   // k_mv_down_exp with SHT != 0: the shared expert's down rows (GGUF, sh_cols
   // columns) against its int8 row, added after the routed combine
   const uint8_t *sh_w;
@@ -666,6 +671,14 @@ struct WTask<T_Q6_K, true> {
   Q6kT w;
 };
 
+// A GGUF row's task into the registers of a tier kernel (Q4_K: the same
+// Q4kW as the tiled load, from the GGUF offsets; Q8_0 rows are GGUF either way).
+template <int TYPE>
+__device__ __forceinline__ auto wq_load_gguf(const uint8_t *row, int t, int64_t nblk) {
+  if constexpr (TYPE == T_Q4_K) return q4k_load<false>(row, t, nblk);
+  else return q80_load(row, t);
+}
+
 template <int TYPE, bool TILED>
 __device__ __forceinline__ void w_load(WTask<TYPE, TILED> &w, const uint8_t *row, int t, int64_t nblk) {
   if constexpr (TYPE == T_Q4_K) w.w = q4k_load<TILED>(row, t, nblk);
@@ -803,6 +816,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
       if (i < tpl && t < ntasks) act_load<TYPE>(act[i], a.xq, a.xd, a.xbs, t);
     }
   }
+  int64_t routed_total = 0;
   if constexpr (MODE == M_GATE_UP) {  // after the activation loads are issued, so the two overlap
     if (a.sel_on) {
       if (wave == 0) mv_select(a.sel, lane, slot_e, selP, blockIdx.x == 0);
@@ -811,20 +825,32 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
     } else {
       total = (int64_t)(*a.rt.n_active) * bpe;
     }
+    routed_total = total;
+    if (a.sgu_w) total += (a.sgu_rows + RB - 1) / RB;  // the shared expert's row blocks after the experts'
   }
 
   for (int64_t b = blockIdx.x; b < total; b += gridDim.x) {
     int64_t rblk = b;
     const uint8_t *W0 = a.w0, *W1 = nullptr;
     int64_t p0 = 0;
+    bool shared_item = false;  // M_GATE_UP: a block of the shared expert's GGUF rows
+    int64_t rows_i = rows;
     if constexpr (MODE == M_GATE_UP) {
-      const int i = (int)(b / bpe);
-      rblk = b - (int64_t)i * bpe;
-      const int e = a.sel_on ? slot_e[i] : a.rt.active[i];
-      p0 = a.sel_on ? i : a.rt.offsets[e];
-      const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
-      W0 = eb + a.tier.off[0];
-      W1 = eb + a.tier.off[1];
+      if (b >= routed_total) {
+        shared_item = true;
+        rblk = b - routed_total;
+        rows_i = a.sgu_rows;
+        W0 = a.sgu_w;
+        W1 = a.sgu_w + a.sgu_rows * row_bytes;
+      } else {
+        const int i = (int)(b / bpe);
+        rblk = b - (int64_t)i * bpe;
+        const int e = a.sel_on ? slot_e[i] : a.rt.active[i];
+        p0 = a.sel_on ? i : a.rt.offsets[e];
+        const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
+        W0 = eb + a.tier.off[0];
+        W1 = eb + a.tier.off[1];
+      }
     }
     const int64_t r0 = rblk * RB + (int64_t)(wave * RU) * RPW + row_in_wave;
 
@@ -899,10 +925,17 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
-            if (r < rows) {
+            if (r < rows_i) {
               constexpr bool TL = MODE == M_GATE_UP;  // expert tier rows are tiled, plain rows are GGUF
               int64_t rw = r;
               if constexpr (MODE == M_QKV) rw = qkv_row(a.rope, r);
+              if constexpr (MODE == M_GATE_UP && (TYPE == T_Q4_K || TYPE == T_Q8_0)) {
+                if (shared_item) {  // GGUF rows into the same registers (Q4_K and Q8_0 tasks alike)
+                  w0[u].w = wq_load_gguf<TYPE>(W0 + r * row_bytes, t, nblk);
+                  w1[u].w = wq_load_gguf<TYPE>(W1 + r * row_bytes, t, nblk);
+                  continue;
+                }
+              }
               w_load<TYPE, TL>(w0[u], W0 + rw * row_bytes, t, nblk);
               if constexpr (MODE == M_GATE_UP) w_load<TYPE, TL>(w1[u], W1 + r * row_bytes, t, nblk);
             }
@@ -910,8 +943,8 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
           for (int u = 0; u < RU; ++u) {
             const int64_t r = r0 + (int64_t)u * RPW;
-            if (r < rows) {
-              if constexpr (MODE == M_GATE_UP && DBG) {
+            if (r < rows_i) {
+              if constexpr (MODE == M_GATE_UP && DBG) {  // (no shared items with DBG)
                 const int64_t o = (p0 * rows + r) * nblk;
                 const BlockDbg &g = a.dbg;
                 acc0[u] = task_dot<TYPE>(w0[u], t, act[i], acc0[u], g.s[0] ? g.s[0] + o : nullptr,
@@ -941,7 +974,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
 #pragma unroll
         for (int u = 0; u < RU; ++u) {
           const int64_t r = r0 + (int64_t)u * RPW;
-          if (r >= rows) continue;
+          if (r >= rows_i) continue;
           if constexpr (MODE == M_QKV) {
             const int64_t rw = qkv_row(a.rope, r);
             a.out[rw] = acc0[u];
@@ -950,7 +983,8 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
             const float g = acc0[u];
             const float den = 1.0f + expf_cr(-g);
             const float q = g / den;
-            a.out[p0 * rows + r] = q * acc1[u];
+            if (shared_item) a.sgu_h[r] = q * acc1[u];
+            else a.out[p0 * rows + r] = q * acc1[u];
           } else if (a.add) {  // the shared expert's gated add (k_shared_add's arithmetic)
             float scale = 1.0f;
             if (a.add_logit) {
@@ -1515,9 +1549,23 @@ bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
 
 hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                                  const Routing &rt, int max_active, const int8_t *xq, const float *xd,
-                                 const int32_t *xbs, float *h, const DecSelect *sel, const BlockDbg *dbg) {
+                                 const int32_t *xbs, float *h, const DecSelect *sel, const BlockDbg *dbg,
+                                 const SharedGateUp *sgu) {
+  if (sgu) {  // the shared rows as extra items of the register kernel only (Q4_K and Q8_0 rows)
+    if (dbg || (type != T_Q4_K && type != T_Q8_0) || (type == T_Q4_K && dec_gate_up_tq4_supported(cols)) ||
+        sgu->rows <= 0)
+      return hipErrorNotSupported;
+  }
   MvArgs a{};
   if (dbg) a.dbg = *dbg;
+  if (sgu) {
+    a.sgu_w = sgu->w;
+    a.sgu_rows = sgu->rows;
+    a.sgu_h = sgu->h;
+  }
+  // the shared blocks ride on the grid of the experts' (at most one expert's
+  // worth of groups per rows' worth of shared rows)
+  const int sh_groups = sgu ? (int)((sgu->rows + rows - 1) / rows) : 0;
   a.rows = rows;
   a.cols = cols;
   a.xq = xq;
@@ -1534,10 +1582,10 @@ hipError_t launch_decode_gate_up(hipStream_t st, int type, const ExpertTier &tie
   if (type == T_Q4_K) {
     const hipError_t e = launch_dec_gate_up_tq4(st, tier, rows, cols, rt, max_active, xq, xd, xbs, h, sel, dbg);
     if (e != hipErrorNotSupported) return e;
-    return dispatch_reg<T_Q4_K, M_GATE_UP, 1>(st, a, max_active);
+    return dispatch_reg<T_Q4_K, M_GATE_UP, 1>(st, a, max_active + sh_groups);
   }
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_GATE_UP, 2>(st, a, max_active);
-  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active);
+  if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_GATE_UP, 2>(st, a, max_active + sh_groups);
   return hipErrorInvalidValue;
 }
 

@@ -794,6 +794,52 @@ hipError_t launch_dispatch(hipStream_t st, const uint32_t *idx, int64_t n_slots,
   return hipGetLastError();
 }
 
+// One unit per wave: a Q8_K block (KQ) or eight Q8 blocks; segment A's units
+// first, then segment B's.
+template <bool KA, bool KB>
+__global__ void __launch_bounds__(256) k_quant_two(const float *__restrict__ ha, int64_t n_a, int8_t *__restrict__ qa,
+                                                   float *__restrict__ da, int32_t *__restrict__ sa,
+                                                   const float *__restrict__ hb, int64_t n_b, int8_t *__restrict__ qb,
+                                                   float *__restrict__ db, int32_t *__restrict__ sb) {
+  const int lane = threadIdx.x & 63;
+  int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t ua = KA ? n_a / 256 : (n_a / 32 + 7) / 8;
+  const int64_t ub = KB ? n_b / 256 : (n_b / 32 + 7) / 8;
+  if (u < ua) {
+    if constexpr (KA) {
+      wave_quant_q8k_block(ha + u * 256, qa + u * 256, da + u, sa + u * 16, lane);
+    } else {
+      const int64_t blk = u * 8 + (lane >> 3);
+      if (blk < n_a / 32) group8_quant_q8_block(ha + blk * 32, qa + blk * 32, da + blk, sa + blk * 2, lane & 7);
+    }
+    return;
+  }
+  u -= ua;
+  if (u >= ub) return;
+  if constexpr (KB) {
+    wave_quant_q8k_block(hb + u * 256, qb + u * 256, db + u, sb + u * 16, lane);
+  } else {
+    const int64_t blk = u * 8 + (lane >> 3);
+    if (blk < n_b / 32) group8_quant_q8_block(hb + blk * 32, qb + blk * 32, db + blk, sb + blk * 2, lane & 7);
+  }
+}
+
+hipError_t launch_quant_two(hipStream_t st, int type_a, const float *ha, int64_t n_a, int8_t *qa, float *da,
+                            int32_t *sa, int type_b, const float *hb, int64_t n_b, int8_t *qb, float *db,
+                            int32_t *sb) {
+  const bool ka = is_kquant(type_a), kb = is_kquant(type_b);
+  if ((type_a != T_Q8_0 && !ka) || (type_b != T_Q8_0 && !kb) || n_a % (ka ? 256 : 32) || n_b % (kb ? 256 : 32))
+    return hipErrorNotSupported;
+  const int64_t units = (ka ? n_a / 256 : (n_a / 32 + 7) / 8) + (kb ? n_b / 256 : (n_b / 32 + 7) / 8);
+  if (units <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((units + 3) / 4));
+  if (ka && kb) KMOE_LAUNCH((k_quant_two<true, true>), grid, dim3(256), 0, st, ha, n_a, qa, da, sa, hb, n_b, qb, db, sb);
+  else if (ka) KMOE_LAUNCH((k_quant_two<true, false>), grid, dim3(256), 0, st, ha, n_a, qa, da, sa, hb, n_b, qb, db, sb);
+  else if (kb) KMOE_LAUNCH((k_quant_two<false, true>), grid, dim3(256), 0, st, ha, n_a, qa, da, sa, hb, n_b, qb, db, sb);
+  else KMOE_LAUNCH((k_quant_two<false, false>), grid, dim3(256), 0, st, ha, n_a, qa, da, sa, hb, n_b, qb, db, sb);
+  return hipGetLastError();
+}
+
 hipError_t launch_quant_slots(hipStream_t st, int type, const float *h, int64_t n_slots, int64_t cols,
                               const Routing &rt, const uint32_t *idx_flat, int regime, int8_t *q, float *d,
                               int32_t *sums) {
