@@ -554,6 +554,16 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
     if (e == hipSuccess) return KMOE_OK;
     if (e != hipErrorNotSupported) HIP_OK(c, e);
   }
+  // Narrower Q4_K rows and Q6_K rows of at most 4096 columns: the register
+  // kernel quantizes x itself (the kernel the separate quantization would
+  // feed, so the same bits).
+  if ((t == KMOE_Q4_K || t == KMOE_Q6_K) && s_rows == 1 && cols <= 4096) {
+    const hipError_t e = timed(c, t == KMOE_Q4_K ? "matvec_q4k" : "matvec_q6k", [&]() {
+      return launch_decode_plain_fx(c->stream, t, w, rows, cols, x, out);
+    });
+    if (e == hipSuccess) return KMOE_OK;
+    if (e != hipErrorNotSupported) HIP_OK(c, e);
+  }
   if (is_kq(t)) LAUNCH(c, "quant_q8k", launch_quant_q8k(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   else LAUNCH(c, "quant_q8", launch_quant_q8(c->stream, x, s_rows, cols, qr.q, qr.d, qr.s));
   return matvec_q8_impl(c, t, w, rows, cols, qr.q, qr.d, qr.s, s_rows, out);

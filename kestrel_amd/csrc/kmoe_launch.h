@@ -97,6 +97,12 @@ struct AddEpi {
 hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                                const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
                                const AddEpi *epi = nullptr);
+// The same for one f32 activation row quantized to Q8_K inside the kernel
+// (Q4_K and Q6_K rows of at most 4096 columns; the same bits as
+// launch_quant_q8k followed by launch_decode_plain where the rows take the
+// register kernel). hipErrorNotSupported otherwise.
+hipError_t launch_decode_plain_fx(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                  const float *xf, float *out);
 struct DecSelect;
 // sel: the kernel selects the token's experts from its logits and writes the
 // routing (hipErrorNotSupported where decode_gate_up_can_select is false).

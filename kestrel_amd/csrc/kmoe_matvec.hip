@@ -59,6 +59,7 @@ struct MvArgs {
   int add;        // M_PLAIN: out[r] = out[r] + scale * y (AddEpi) instead of out[r] = y
   int32_t chunk;  // LDS-staged plain modes: activation rows per work-group (blockIdx.y picks the chunk)
   const float *add_logit;
+  const float *xf;  // M_PLAIN_FX: the f32 activation row
   // M_GATE_UP, one token: the shared expert's gate rows (GGUF, sgu_rows of
   // them, its up rows right after) as extra items, SwiGLU into sgu_h
   const uint8_t *sgu_w;
@@ -76,6 +77,10 @@ struct MvArgs {
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
 enum { M_QKV = 5 };
+// M_PLAIN with the f32 activation row (a.xf) quantized to Q8_K inside the
+// kernel (K-quant rows of at most kRegFxBlocks superblocks)
+enum { M_PLAIN_FX = 6 };
+constexpr int kRegFxBlocks = 16;
 
 // The RoPE + KV store epilogue of a one-token q/k/v projection with
 // interleaved pairs (rows 2i and 2i+1 of a head, dims below rope_dim) or
@@ -809,7 +814,30 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
   __shared__ float selP[256];
 
   ActSlice<TYPE> act[TPLMAX];
-  if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
+  if constexpr (MODE == M_PLAIN_FX) {
+    // The row's Q8_K blocks into LDS (block wave + 4i, four values per lane:
+    // k_quant_q8k's arithmetic), then every lane's slices from there.
+    __shared__ __attribute__((aligned(16))) int8_t fq[kRegFxBlocks * 256];
+    __shared__ float fd[kRegFxBlocks];
+    __shared__ __attribute__((aligned(16))) int32_t fbs[kRegFxBlocks * 16];
+    float4 xv[kRegFxBlocks / 4];
+#pragma unroll
+    for (int i = 0; i < kRegFxBlocks / 4; ++i) {
+      const int64_t bk = wave + 4 * i < nblk ? wave + 4 * i : nblk - 1;
+      xv[i] = *(const float4 *)(a.xf + 256 * bk + 4 * lane);
+    }
+#pragma unroll
+    for (int i = 0; i < kRegFxBlocks / 4; ++i) {
+      const int bk = wave + 4 * i;
+      if (bk < nblk) wave_quant_q8k_vals(xv[i], fq + 256 * bk, fd + bk, fbs + 16 * bk, lane);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPLMAX; ++i) {
+      const int t = lr + i * LPR;
+      if (i < tpl && t < ntasks) act_load<TYPE>(act[i], fq, fd, fbs, t);
+    }
+  } else if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
 #pragma unroll
     for (int i = 0; i < TPLMAX; ++i) {
       const int t = lr + i * LPR;
@@ -1534,6 +1562,22 @@ hipError_t launch_decode_plain(hipStream_t st, int type, const uint8_t *w, int64
   if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_PLAIN, 1>(st, a, 1);
   if (type == T_Q8_0) return dispatch_reg<T_Q8_0, M_PLAIN, 1>(st, a, 1);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_plain_fx(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                  const float *xf, float *out) {
+  if (!is_kquant(type) || cols % 256 != 0 || cols / 256 > kRegFxBlocks || ((uintptr_t)xf & 15u))
+    return hipErrorNotSupported;
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.xf = xf;
+  a.s_rows = 1;
+  a.out = out;
+  if (type == T_Q4_K) return dispatch_reg<T_Q4_K, M_PLAIN_FX, 1>(st, a, 1);
+  if (type == T_Q6_K) return dispatch_reg<T_Q6_K, M_PLAIN_FX, 1>(st, a, 1);
+  return hipErrorNotSupported;
 }
 
 bool decode_gate_up_can_select(int type, int64_t cols, int32_t E, int32_t K) {
