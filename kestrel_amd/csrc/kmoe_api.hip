@@ -1951,7 +1951,7 @@ int kmoe_attention(kmoe_ctx *c, const float *q, const uint16_t *k_cache, const u
   if (!q || !k_cache || !v_cache || !out) return fail(c, KMOE_E_INVALID, "null pointer");
   DeviceGuard g(c->device);
   const int supers = attn_supers(pos_dev ? n_ctx : std::min(n_ctx, pos0 + s_rows));
-  rc = ensure_aws(c, (size_t)s_rows * n_kv, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
+  rc = ensure_aws(c, (size_t)s_rows * n_head, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
   if (rc) return rc;
   LAUNCH(c, "attention",
          launch_attention(c->stream, q, k_cache, v_cache, s_rows, n_head, n_kv, head_dim, pos0, pos_dev, n_ctx,
@@ -1986,7 +1986,7 @@ int kmoe_attention_matmul(kmoe_ctx *c, const float *q, const uint16_t *k_cache, 
     if (rc) return rc;
   }
   const int supers = attn_supers(pos_dev ? n_ctx : std::min(n_ctx, pos0 + s_rows));
-  rc = ensure_aws(c, (size_t)s_rows * n_kv, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
+  rc = ensure_aws(c, (size_t)s_rows * n_head, (size_t)attn_part_floats(s_rows, n_head, head_dim, supers) * 4);
   if (rc) return rc;
   const int64_t pf = gemm_f32_part_floats(rows, cols, 1, s_rows, s_rows);
   size_t need = 0;

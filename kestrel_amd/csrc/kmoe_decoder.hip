@@ -283,39 +283,126 @@ __global__ void __launch_bounds__(256) k_rope_kv(const float *__restrict__ q, co
 // ---------------------------------------------------------------------------
 // Causal GQA attention (Transformer::attention, transformer.rs:591-631).
 //
-// Work-group (kv head g, query row s, chunk c of 64 cache positions); wave w
-// takes query heads w, w + 4, ... of the group. Lane l loads position l's K
-// row of head g into registers and scores it against the head's q (read with
-// scalar loads: the address is uniform over the wave) in quant::dot's
-// eight-accumulator order (quant.rs:208-224), times 1/sqrt(hd); the wave
-// takes the chunk's max m and e = exp(score - m), and lanes over head dims
-// accumulate sum e V from V rows in registers, the weights broadcast with
-// readlane. With one chunk the result is final; otherwise every work-group of
-// the row hands (m, sum e, acc) over with agent-scope stores and a counter,
-// and the last to arrive merges them (out = sum acc e^(m - M) / sum l e^(m - M))
-// and resets the counter.
+// One wave works one chunk of 64 cache positions for one query head:
+// - loads: the chunk's K and V rows of kv head g as 16-byte pieces, coalesced
+//   (load j of lane l reads piece l % (hd / 8) of row j * RPI + l / (hd / 8),
+//   RPI = 64 / (hd / 8) rows per load); rows past the chunk's end are read
+//   clamped to its last row;
+// - scores: the K pieces turn through the wave's LDS tile so that lane l holds
+//   position l's row; it is scored against the head's q (LDS, broadcast reads)
+//   in quant::dot's eight-accumulator order (quant.rs:208-224), times
+//   1/sqrt(hd), so the scores are bit-identical to the reference's; positions
+//   past the end score -inf;
+// - softmax: the chunk's max m, e = exp(score - m) (0 past the end), l = sum e;
+// - weighted V: lane l keeps its V pieces (head dims 8p .. 8p + 7, p = l %
+//   (hd / 8)) of rows j * RPI + l / (hd / 8) in registers, zeroed past the end,
+//   sums e_r v_r over them in row order with e read from LDS, and the RPI row
+//   classes of a piece are then added in class order across lanes.
+// Chunk partials (m, l, acc) merge as out = sum acc e^(m - M) / sum l e^(m - M)
+// over the chunks in order, M their max.
 constexpr int kAttnChunk = 64;
 constexpr int kMaxGroup = 16;
+// Rows of at most this many chunks run in one work-group per head in the
+// one-row kernel (one chunk per wave). Measured on MI355X with the caches read
+// from HBM (16 heads of 128): 6.7 against 9.0 us at 128 positions, 8.2 against
+// 9.7 us at 256, but 10.9 against 10.2 us at 384, where one CU's loads take
+// longer than spreading the chunks and handing the partials over.
+constexpr int kAttnSpanMax = 4;
+
+// LDS written by lanes of a wave and read by other lanes of the same wave:
+// orders the LDS accesses only, so global loads stay in flight.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One chunk's K rows in LDS, each padded by a piece: the lane-per-row reads of
+// eight lanes then cover the 32 banks once.
+template <int HD>
+struct AttnKTile {
+  uint4 p[kAttnChunk][HD / 8 + 1];
+};
+
+// Load j of lane l: piece l % (HD / 8) of chunk row j * RPI + l / (HD / 8).
+template <int HD>
+__device__ __forceinline__ int64_t attn_piece_off(int64_t kvw, int g, int64_t p0, int np, int j, int lane) {
+  constexpr int KV4 = HD / 8, RPI = 64 / KV4;
+  const int r = j * RPI + lane / KV4;
+  return (p0 + (r < np ? r : np - 1)) * kvw + (int64_t)g * HD + 8 * (lane % KV4);
+}
+
+// q of one head against lane-per-row K: the score of position lane.
+template <int HD>
+__device__ __forceinline__ float attn_score(const float *qh, const uint4 (&kr)[HD / 8], int lane, int np) {
+  constexpr int KV4 = HD / 8;
+  const float scale = 1.0f / sqrtf((float)HD);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < KV4; ++j) {
+    const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = qh[8 * j + 2 * i] * f16_bits_to_f32(w4[i]);
+      const float a1 = qh[8 * j + 2 * i + 1] * f16_bits_to_f32(w4[i] >> 16);
+      acc[2 * i] = acc[2 * i] + a0;
+      acc[2 * i + 1] = acc[2 * i + 1] + a1;
+    }
+  }
+  float t = -0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t = t + acc[i];
+  return lane < np ? t * scale : -INFINITY;
+}
+
+// sum e_r v_r over the chunk for head dims 8p .. 8p + 7, p = lane % (HD / 8)
+// (every lane of piece p receives them); ws[r] = e_r, vp = this lane's pieces.
+// Rows past np contribute +0 * +0 to sums that start at +0.
+template <int HD>
+__device__ __forceinline__ void attn_wv(const float *ws, const uint4 (&vp)[HD / 8], int lane, int np, float (&o8)[8]) {
+  constexpr int KV4 = HD / 8, RPI = 64 / KV4;
+  const int rc = lane / KV4, p = lane % KV4;
+  float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < KV4; ++j) {
+    const int r = j * RPI + rc;
+    const float w = ws[r];
+    const bool live = r < np;
+    const uint32_t u[4] = {live ? vp[j].x : 0u, live ? vp[j].y : 0u, live ? vp[j].z : 0u, live ? vp[j].w : 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] = a[2 * i] + w * f16_bits_to_f32(u[i]);
+      a[2 * i + 1] = a[2 * i + 1] + w * f16_bits_to_f32(u[i] >> 16);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float t = __shfl(a[i], p);
+#pragma unroll
+    for (int c = 1; c < RPI; ++c) t = t + __shfl(a[i], p + c * KV4);
+    o8[i] = t;
+  }
+}
 
 // The int8 rows of the attention output for the projection after it: the
 // group's group * HD outputs of row s (staged in LDS) are whole Q8_K blocks
 // (qt 1, group * HD % 256 == 0: one wave per block) or Q8 blocks (qt 2, eight
 // lanes per block), quantized as the matmul's own quantization kernel would.
-template <int HD>
+template <int HD, int NW = 4>
 __device__ __forceinline__ void attn_quant_group(const float *os, int group, int64_t s, int g, int nh, int qt,
                                                  int8_t *xq, float *xd, int32_t *xs) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)nh * HD, gb = (int64_t)g * group * HD;
   const int nv = group * HD;
   if (qt == 1) {
-    for (int b = wave; b < nv / 256; b += 4) {
+    for (int b = wave; b < nv / 256; b += NW) {
       const float4 v = *(const float4 *)(os + 256 * b + 4 * lane);
       const int64_t blk = (gb / 256) + b;
       wave_quant_q8k_vals(v, xq + s * row + 256 * blk, xd + s * (row / 256) + blk, xs + s * (row / 16) + 16 * blk,
                           lane);
     }
   } else {
-    for (int b = wave * 8 + (lane >> 3); b < nv / 32; b += 32) {
+    for (int b = wave * 8 + (lane >> 3); b < nv / 32; b += 8 * NW) {
       const float4 v = *(const float4 *)(os + 32 * b + 4 * (lane & 7));
       const int64_t blk = (gb / 32) + b;
       group8_quant_q8_vals(v, xq + s * row + 32 * blk, xd + s * (row / 32) + blk, xs + s * (row / 16) + 2 * blk,
@@ -324,19 +411,23 @@ __device__ __forceinline__ void attn_quant_group(const float *os, int group, int
   }
 }
 
+// Work-group bid = (kv head g, query row s, chunk c) of 256 threads; wave w
+// takes query heads w, w + 4, ... of the group over the chunk, whose K rows the
+// work-group loads into its tile together. With one chunk the result is final;
+// otherwise every work-group of the row hands (m, l, acc) over with agent-scope
+// stores and a counter, and the last to arrive merges them and resets the
+// counter. LDS: Qs and Os [kMaxGroup][HD], Ws [4][64], one K tile.
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, const uint16_t *__restrict__ kc,
-                                                  const uint16_t *__restrict__ vc, int64_t s_rows, int nh, int nkv,
-                                                  int64_t pos0, const int32_t *__restrict__ pos_dev, int64_t n_ctx,
-                                                  int nch_grid, float *part, uint32_t *counters,
-                                                  float *__restrict__ out, int qt, int8_t *__restrict__ xq,
-                                                  float *__restrict__ xd, int32_t *__restrict__ xs) {
-  constexpr int KV4 = HD / 8;   // uint4 pieces (8 halves) per K row
-  constexpr int DPL = HD / 64;  // head dims per lane
-  __shared__ uint32_t last;
-  __shared__ __attribute__((aligned(16))) float Qs[kMaxGroup][HD];
-  __shared__ __attribute__((aligned(16))) float Os[kMaxGroup][HD];  // the group's outputs, for qt
-  const int64_t bid = blockIdx.x;
+__device__ __forceinline__ void attn_batch(int64_t bid, const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                           const uint16_t *__restrict__ vc, int64_t s_rows, int nh, int nkv,
+                                           int64_t pos0, const int32_t *__restrict__ pos_dev, int64_t n_ctx,
+                                           int nch_grid, float *part, uint32_t *counters, float *__restrict__ out,
+                                           int qt, int8_t *__restrict__ xq, float *__restrict__ xd,
+                                           int32_t *__restrict__ xs, float (*Qs)[HD], float (*Os)[HD],
+                                           float (*Ws)[kAttnChunk], AttnKTile<HD> &Kt, uint32_t &last) {
+  constexpr int KV4 = HD / 8;
+  constexpr int DPL = HD / 64;  // head dims per lane in the merge
+  constexpr int PW = HD + 2;    // one chunk partial: m, l, acc[HD]
   const int c = (int)(bid % nch_grid);
   const int64_t s = (bid / nch_grid) % s_rows;
   const int g = (int)(bid / nch_grid / s_rows);
@@ -349,92 +440,68 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   const int64_t kvw = (int64_t)nkv * HD;
   const int64_t p0 = (int64_t)c * kAttnChunk;
   const int np = (int)(n - p0 < kAttnChunk ? n - p0 : kAttnChunk);
-  // q of the group's heads into LDS, issued first so it overlaps the K/V loads
+  // q of the group's heads and the chunk's K rows into LDS, V pieces into the
+  // registers of the waves that use them, all issued before any is used
   for (int e = threadIdx.x; e < group * HD; e += 256) Qs[e / HD][e % HD] = q[(s * nh + (int64_t)g * group) * HD + e];
-  uint4 kr[KV4];
-  uint32_t vr[DPL == 2 ? 64 : 1];
-  uint16_t vh[DPL == 1 ? 64 : 1];
-  if (wave < group) {
-    if (lane < np) {
-      const uint4 *src = (const uint4 *)(kc + (p0 + lane) * kvw + (int64_t)g * HD);
+  constexpr int NT = kAttnChunk * KV4 / 256;  // K pieces per thread
+  uint4 kp[NT], vp[KV4];
 #pragma unroll
-      for (int j = 0; j < KV4; ++j) kr[j] = src[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      if (j < np) {
-        const uint16_t *vrow = vc + (p0 + j) * kvw + (int64_t)g * HD;
-        if constexpr (DPL == 2) vr[j] = ((const uint32_t *)vrow)[lane];
-        else vh[j] = vrow[lane];
-      }
-    }
+  for (int i = 0; i < NT; ++i) {
+    const int e = threadIdx.x + 256 * i, r = e / KV4;
+    kp[i] = *(const uint4 *)(kc + (p0 + (r < np ? r : np - 1)) * kvw + (int64_t)g * HD + 8 * (e % KV4));
   }
-  __syncthreads();  // Qs
   if (wave < group) {
-    const float scale = 1.0f / sqrtf((float)HD);
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) vp[j] = *(const uint4 *)(vc + attn_piece_off<HD>(kvw, g, p0, np, j, lane));
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    Kt.p[e / KV4][e % KV4] = kp[i];
+  }
+  lds_barrier();  // Qs, Kt
+  if (wave < group) {
+    uint4 kr[KV4];
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) kr[j] = Kt.p[lane][j];
     for (int hh = wave; hh < group; hh += 4) {
       const int64_t h = (int64_t)g * group + hh;
-      const float *qh = Qs[hh];
-      float sc_ = -INFINITY;
-      if (lane < np) {
-        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < KV4; ++j) {
-          const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float a0 = qh[8 * j + 2 * i] * f16_bits_to_f32(w4[i]);
-            const float a1 = qh[8 * j + 2 * i + 1] * f16_bits_to_f32(w4[i] >> 16);
-            acc[2 * i] = acc[2 * i] + a0;
-            acc[2 * i + 1] = acc[2 * i + 1] + a1;
-          }
-        }
-        float t = -0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t = t + acc[i];
-        sc_ = t * scale;
-      }
+      const float sc_ = attn_score<HD>(Qs[hh], kr, lane, np);
       const float m = group_max<64>(sc_);
       const float e = lane < np ? expf(sc_ - m) : 0.0f;
       const float l = group_sum<64>(e);
-      float o[DPL];
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 64; ++j) {
-        if (j < np) {
-          const float wgt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
-          if constexpr (DPL == 2) {
-            o[0] += wgt * f16_bits_to_f32(vr[j]);
-            o[1] += wgt * f16_bits_to_f32(vr[j] >> 16);
-          } else {
-            o[0] += wgt * f16_bits_to_f32(vh[j]);
-          }
-        }
-      }
+      Ws[wave][lane] = e;
+      wave_lds_sync();
+      float o8[8];
+      attn_wv<HD>(Ws[wave], vp, lane, np, o8);
+      wave_lds_sync();  // the weights are read before the next head writes them
       if (nch == 1) {
         const float inv = 1.0f / l;
+        if (lane < KV4) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-          const float r = o[i] * inv;
-          out[(s * nh + h) * HD + lane * DPL + i] = r;
-          Os[hh][lane * DPL + i] = r;
+          for (int i = 0; i < 8; ++i) {
+            const float r = o8[i] * inv;
+            out[(s * nh + h) * HD + 8 * lane + i] = r;
+            Os[hh][8 * lane + i] = r;
+          }
         }
       } else {
-        float *pp = part + ((s * nh + h) * nch_grid + c) * (HD + 2);
+        float *pp = part + ((s * nh + h) * nch_grid + c) * PW;
         if (lane == 0) {
           st_agent(pp, m);
           st_agent(pp + 1, l);
         }
+        if (lane < KV4) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) st_agent(pp + 2 + lane * DPL + i, o[i]);
+          for (int i = 0; i < 8; ++i) st_agent(pp + 2 + 8 * lane + i, o8[i]);
+        }
       }
     }
   }
   if (nch == 1) {
     if (qt) {
       __syncthreads();
-      attn_quant_group<HD>(&Os[0][0], group, s, g, nh, qt, xq, xd, xs);
+      attn_quant_group<HD>(Os[0], group, s, g, nh, qt, xq, xd, xs);
     }
     return;
   }
@@ -448,14 +515,14 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   if (last != (uint32_t)(nch - 1)) return;
   for (int hh = wave; hh < group; hh += 4) {
     const int64_t h = (int64_t)g * group + hh;
-    const float *pb = part + (s * nh + h) * nch_grid * (HD + 2);
+    const float *pb = part + (s * nh + h) * nch_grid * PW;
     // the partials of 8 chunks at a time, every load issued before any use
     constexpr int B = 8;
     float M = -INFINITY;
     for (int c0 = 0; c0 < nch; c0 += B) {
       float mv[B];
 #pragma unroll
-      for (int j = 0; j < B; ++j) mv[j] = c0 + j < nch ? ld_agent(pb + (c0 + j) * (HD + 2)) : -INFINITY;
+      for (int j = 0; j < B; ++j) mv[j] = c0 + j < nch ? ld_agent(pb + (c0 + j) * PW) : -INFINITY;
 #pragma unroll
       for (int j = 0; j < B; ++j) M = fmaxf(M, mv[j]);
     }
@@ -467,7 +534,7 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
 #pragma unroll
       for (int j = 0; j < B; ++j) {
         if (c0 + j < nch) {
-          const float *pc = pb + (c0 + j) * (HD + 2);
+          const float *pc = pb + (c0 + j) * PW;
           mv[j] = ld_agent(pc);
           lv[j] = ld_agent(pc + 1);
 #pragma unroll
@@ -495,7 +562,129 @@ __global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, c
   if (threadIdx.x == 0) st_agent(counters + s * nkv + g, 0u);  // ready for the next call
   if (qt) {
     __syncthreads();
-    attn_quant_group<HD>(&Os[0][0], group, s, g, nh, qt, xq, xd, xs);
+    attn_quant_group<HD>(Os[0], group, s, g, nh, qt, xq, xd, xs);
+  }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_dec(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                  const uint16_t *__restrict__ vc, int64_t s_rows, int nh, int nkv,
+                                                  int64_t pos0, const int32_t *__restrict__ pos_dev, int64_t n_ctx,
+                                                  int nch_grid, float *part, uint32_t *counters,
+                                                  float *__restrict__ out, int qt, int8_t *__restrict__ xq,
+                                                  float *__restrict__ xd, int32_t *__restrict__ xs) {
+  __shared__ uint32_t last;
+  __shared__ __attribute__((aligned(16))) float Qs[kMaxGroup][HD];
+  __shared__ __attribute__((aligned(16))) float Os[kMaxGroup][HD];
+  __shared__ float Ws[4][kAttnChunk];
+  __shared__ AttnKTile<HD> Kt;
+  attn_batch<HD>(blockIdx.x, q, kc, vc, s_rows, nh, nkv, pos0, pos_dev, n_ctx, nch_grid, part, counters, out, qt, xq,
+                 xd, xs, Qs, Os, Ws, Kt, last);
+}
+
+// The same attention for one query row per call (decode), grid nh x nch_grid
+// work-groups of 256 threads. Rows of at most kAttnSpanMax chunks: work-group
+// h takes query head h, wave w chunk w over the rows of its kv head, with
+// attn_batch's chunk arithmetic; the partials stay in LDS and wave 0 merges
+// them in chunk order with attn_batch's merge expressions, so the output has
+// a batch call's bits and nothing leaves the CU but the result. Longer rows:
+// the work-groups below nkv x nch_grid run attn_batch, whose chunks spread
+// over more CUs (one CU's loads would take longer than the merge's hand-off).
+// QT 2 also writes the head's Q8 rows (32-blocks) for the projection after it;
+// QT 1 (Q8_K, whose blocks span heads) is not taken.
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_one(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                  const uint16_t *__restrict__ vc, int nh, int nkv, int64_t pos0,
+                                                  const int32_t *__restrict__ pos_dev, int64_t n_ctx, int nch_grid,
+                                                  float *part, uint32_t *counters, float *__restrict__ out, int qt,
+                                                  int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                  int32_t *__restrict__ xs) {
+  constexpr int KV4 = HD / 8;
+  constexpr int DPL = HD / 64;
+  constexpr int PW = HD + 2;  // one chunk partial: m, l, acc[HD]
+  __shared__ uint32_t last;
+  __shared__ __attribute__((aligned(16))) float Qs[kMaxGroup][HD];
+  __shared__ __attribute__((aligned(16))) float Os[kMaxGroup][HD];
+  __shared__ float Ws[4][kAttnChunk];
+  __shared__ __attribute__((aligned(16))) float Lp[kAttnSpanMax][PW];
+  __shared__ AttnKTile<HD> Kt[kAttnSpanMax];
+  int64_t n = position(pos0, pos_dev) + 1;
+  if (n > n_ctx) n = n_ctx;
+  const int nch = (int)((n + kAttnChunk - 1) / kAttnChunk);
+  if (nch > kAttnSpanMax) {
+    if (blockIdx.x < nkv * nch_grid)
+      attn_batch<HD>(blockIdx.x, q, kc, vc, 1, nh, nkv, pos0, pos_dev, n_ctx, nch_grid, part, counters, out, qt, xq,
+                     xd, xs, Qs, Os, Ws, Kt[0], last);
+    return;
+  }
+  if (blockIdx.x >= (unsigned)nh) return;
+  const int h = blockIdx.x;
+  const int g = h / (nh / nkv);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c = wave;
+  const bool active = c < nch;
+  const int64_t kvw = (int64_t)nkv * HD;
+  const int64_t p0 = (int64_t)c * kAttnChunk;
+  const int np = active ? (int)(n - p0 < kAttnChunk ? n - p0 : kAttnChunk) : 0;
+  if (threadIdx.x < HD) Qs[0][threadIdx.x] = q[(int64_t)h * HD + threadIdx.x];
+  uint4 kp[KV4], vp[KV4];
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) kp[j] = *(const uint4 *)(kc + attn_piece_off<HD>(kvw, g, p0, np, j, lane));
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) vp[j] = *(const uint4 *)(vc + attn_piece_off<HD>(kvw, g, p0, np, j, lane));
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) Kt[wave].p[j * (64 / KV4) + lane / KV4][lane % KV4] = kp[j];
+  }
+  lds_barrier();  // Qs, the K tiles
+  if (active) {
+    uint4 kr[KV4];
+#pragma unroll
+    for (int j = 0; j < KV4; ++j) kr[j] = Kt[wave].p[lane][j];
+    const float sc_ = attn_score<HD>(Qs[0], kr, lane, np);
+    const float m = group_max<64>(sc_);
+    const float e = lane < np ? expf(sc_ - m) : 0.0f;
+    const float l = group_sum<64>(e);
+    Ws[wave][lane] = e;
+    wave_lds_sync();
+    float o8[8];
+    attn_wv<HD>(Ws[wave], vp, lane, np, o8);
+    if (lane == 0) {
+      Lp[wave][0] = m;
+      Lp[wave][1] = l;
+    }
+    if (lane < KV4) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Lp[wave][2 + 8 * lane + i] = o8[i];
+    }
+  }
+  lds_barrier();  // the chunk partials
+  if (wave != 0) return;
+  float M = -INFINITY, L = 0.0f, O[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) O[i] = 0.0f;
+  for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, Lp[cc][0]);
+  for (int cc = 0; cc < nch; ++cc) {
+    const float f = expf(Lp[cc][0] - M);
+    L += Lp[cc][1] * f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) O[i] += Lp[cc][2 + lane * DPL + i] * f;
+  }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const float r = O[i] * inv;
+    out[(int64_t)h * HD + lane * DPL + i] = r;
+    Os[0][lane * DPL + i] = r;
+  }
+  if (qt == 2) {
+    wave_lds_sync();  // the head's outputs are in LDS
+    const int b = lane >> 3;  // HD / 32 blocks of 8 lanes
+    if (b < HD / 32) {
+      const float4 v = *(const float4 *)(&Os[0][0] + 32 * b + 4 * (lane & 7));
+      const int64_t blk = (int64_t)h * (HD / 32) + b;
+      group8_quant_q8_vals(v, xq + 32 * blk, xd + blk, xs + 2 * blk, lane & 7);
+    }
   }
 }
 
@@ -657,6 +846,19 @@ hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, 
                             float *part, uint32_t *counters, float *out, int qt, int8_t *xq, float *xd,
                             int32_t *xs) {
   if (s_rows <= 0) return hipSuccess;
+  if (s_rows == 1) {  // decode
+    if (qt == 1) return hipErrorNotSupported;  // a work-group per head writes no Q8_K blocks
+    const unsigned g1 = (unsigned)((int64_t)nh * supers);
+    if (hd == 64)
+      KMOE_LAUNCH(k_attn_one<64>, dim3(g1), dim3(256), 0, st, q, kc, vc, nh, nkv, pos0, pos_dev, n_ctx, supers, part,
+                  counters, out, qt, xq, xd, xs);
+    else if (hd == 128)
+      KMOE_LAUNCH(k_attn_one<128>, dim3(g1), dim3(256), 0, st, q, kc, vc, nh, nkv, pos0, pos_dev, n_ctx, supers, part,
+                  counters, out, qt, xq, xd, xs);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (qt == 1 && ((nh / nkv) * hd) % 256 != 0) return hipErrorNotSupported;
   const unsigned grid = (unsigned)((int64_t)nkv * s_rows * supers);
   if (hd == 64)

@@ -353,12 +353,13 @@ hipError_t launch_kv_store(hipStream_t st, const float *k, const float *v, int64
                            int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, uint16_t *kc, uint16_t *vc);
 // Attention: chunks of 64 positions covering n_max positions, the
 // cross-work-group partials' size (0 for one super-chunk), supported shapes.
-// counters: s_rows * nkv zero words (zero again when the kernel ends).
+// counters: s_rows * nh zero words (zero again when the kernel ends).
 int attn_supers(int64_t n_max);
 int64_t attn_part_floats(int64_t s_rows, int nh, int hd, int supers);
 bool attn_supported(int hd, int group);
 // qt 1 / 2 also writes the Q8_K / Q8 rows of out into xq, xd, xs (qt 1 needs
-// (nh / nkv) * hd % 256 == 0, else hipErrorNotSupported); qt 0 writes none.
+// more than one row and (nh / nkv) * hd % 256 == 0, else
+// hipErrorNotSupported: one row runs a work-group per head); qt 0 writes none.
 hipError_t launch_attention(hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc, int64_t s_rows,
                             int nh, int nkv, int hd, int64_t pos0, const int32_t *pos_dev, int64_t n_ctx, int supers,
                             float *part, uint32_t *counters, float *out, int qt = 0, int8_t *xq = nullptr,

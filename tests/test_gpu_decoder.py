@@ -193,13 +193,14 @@ def test_rope_kv_store_is_rope_then_store(ctx, orc, neox):
 
 
 @pytest.mark.parametrize("t,S,pos0,regime", [(Q4_K, 1, 10, 0), (Q4_K, 1, 300, 0), (Q8_0, 2, 70, 0), (Q6_K, 1, 5, 1),
-                                             (Q4_K, 5, 0, 0), (Q4_K, 1, 130, 2)])
+                                             (Q4_K, 5, 0, 0), (Q4_K, 1, 130, 2), (Q8_0, 1, 200, 0),
+                                             (Q8_0, 1, 520, 1)])
 def test_attention_matmul_is_attention_then_matmul(ctx, orc, t, S, pos0, regime):
     """The int8 rows written by the attention kernel feed the projection with
     the same bits as kmoe_attention followed by kmoe_matmul, with one chunk or
     several (the merged path), on every regime's path."""
     rng = np.random.default_rng(pos0 + S)
-    nh, nkv, hd, n_ctx, rows = 16, 4, 128, 512, 512
+    nh, nkv, hd, n_ctx, rows = 16, 4, 128, 1024, 512
     kc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
     vc = orc.f16_store(rng.standard_normal((n_ctx, nkv * hd)))
     q = rng.standard_normal((S, nh * hd)).astype(np.float32)
@@ -213,6 +214,29 @@ def test_attention_matmul_is_attention_then_matmul(ctx, orc, t, S, pos0, regime)
     finally:
         ctx.set_regime(0)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("nh,nkv,hd,S,pos0", [(16, 16, 128, 12, 250), (16, 4, 128, 6, 60), (8, 2, 64, 5, 508),
+                                              (4, 1, 128, 3, 700), (16, 16, 128, 2, 0)])
+def test_attention_one_row_is_row_of_batch(ctx, orc, nh, nkv, hd, S, pos0):
+    """One query row per call (a work-group per head, the chunks over its
+    waves, merged in LDS up to 512 positions and across work-groups beyond)
+    gives the bits of the same row in a batch call (a work-group per chunk),
+    twice in a row: the handoff counters are zero again after each call."""
+    rng = np.random.default_rng(nh + S + pos0)
+    n_ctx = 1024
+    kvw = nkv * hd
+    kc = orc.f16_store(rng.standard_normal((n_ctx, kvw)) * 2)
+    vc = orc.f16_store(rng.standard_normal((n_ctx, kvw)))
+    q = rng.standard_normal((S, nh * hd)).astype(np.float32)
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    batch = host(ctx.attention(dev(q), kd, vd, nh, nkv, hd, pos0, n_ctx))
+    for _ in range(2):
+        for s in range(S):
+            one = host(ctx.attention(dev(q[s:s + 1]), kd, vd, nh, nkv, hd, pos0 + s, n_ctx))
+            assert np.array_equal(one.view(np.uint32), batch[s:s + 1].view(np.uint32)), s
+    ref = orc.attention(q, kc, vc, nh, nkv, hd, pos0)
+    assert np.abs(batch - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
 def test_attention_prefill_past_one_super_chunk_twice(ctx, orc):
