@@ -434,12 +434,18 @@ int kmoe_rope_kv_store(kmoe_ctx *ctx, const float *q_dev, const float *k_dev, co
  * kmoe_rope_kv_store of its q, k and v parts. Bit-identical to those two
  * calls; on the integer path with interleaved pairs (neox == 0), or neox
  * pairs over the whole head (rope_dim == head_dim), the projection kernel
- * applies RoPE and stores k and v itself. One token. */
+ * applies RoPE and stores k and v itself. One token. x_out_dev NULL (or
+ * x_dev): x += y in place. Otherwise x + y goes to x_out_dev [cols] and
+ * x_dev is left as it was (a residual stream kept in two buffers); then, for
+ * K-quant rows of at most 4096 columns on the integer path, the residual add,
+ * the norm and its Q8_K row are formed inside the projection kernel itself:
+ * one launch, the same bits. */
 int kmoe_norm_matmul_rope_kv(kmoe_ctx *ctx, float *x_dev, const float *y_dev, const float *norm_w_dev, float eps,
                              int ggml_type, const void *w_dev, size_t w_len, int64_t cols, float *h_dev,
                              float *qkv_dev, int32_t n_head, int32_t n_kv, int32_t head_dim, int32_t rope_dim,
                              int64_t pos0, const int32_t *pos_dev, const float *inv_freq_dev, int32_t neox,
-                             int64_t n_ctx, float *q_out_dev, uint16_t *k_cache_dev, uint16_t *v_cache_dev);
+                             int64_t n_ctx, float *q_out_dev, uint16_t *k_cache_dev, uint16_t *v_cache_dev,
+                             float *x_out_dev);
 int kmoe_swiglu(kmoe_ctx *ctx, const float *gate_dev, const float *up_dev, int64_t n, float *out_dev);
 /* Bias rows (transformer.rs:394-401): x[r] += b for rows of cols. */
 int kmoe_add_rows(kmoe_ctx *ctx, float *x_dev, const float *b_dev, int64_t rows, int64_t cols);

@@ -2037,9 +2037,10 @@ int kmoe_norm_matmul_rope_kv(kmoe_ctx *c, float *x, const float *y, const float 
                              const void *w, size_t w_len, int64_t cols, float *h, float *qkv, int32_t n_head,
                              int32_t n_kv, int32_t head_dim, int32_t rope_dim, int64_t pos0, const int32_t *pos_dev,
                              const float *inv_freq, int32_t neox, int64_t n_ctx, float *q_out, uint16_t *k_cache,
-                             uint16_t *v_cache) {
+                             uint16_t *v_cache, float *x_out) {
   if (!c) return KMOE_E_INVALID;
   if (int rc_ = reject_tiled(c, w)) return rc_;
+  if (x_out && x_out == x) x_out = nullptr;  // in place
   if (n_head <= 0 || n_kv <= 0 || head_dim <= 0 || rope_dim <= 0 || rope_dim > head_dim || rope_dim % 2 ||
       rope_dim > 256 || n_ctx <= 0)
     return fail(c, KMOE_E_INVALID, "rope: need 0 < rope_dim <= min(head_dim, 256), rope_dim even");
@@ -2047,19 +2048,37 @@ int kmoe_norm_matmul_rope_kv(kmoe_ctx *c, float *x, const float *y, const float 
   if (rc) return rc;
   if (!qkv || !inv_freq || !q_out || !k_cache || !v_cache) return fail(c, KMOE_E_INVALID, "null pointer");
   const int64_t nq = (int64_t)n_head * head_dim, kvw = (int64_t)n_kv * head_dim, rows = nq + 2 * kvw;
+  const bool int1 = t != KMOE_F32 && int_path(c->regime, 1) && block_size(t) > 0 && bytes_for(t, cols) > 0 &&
+                    (uint64_t)w_len >= (uint64_t)bytes_for(t, cols) * (uint64_t)rows && x && norm_w && w && h &&
+                    !check_quant_shape(c, t, cols);
+  const QkvRope rp{n_head, n_kv, head_dim, rope_dim, neox, pos0, pos_dev, inv_freq, n_ctx, q_out, k_cache, v_cache};
+  if (x_out) {
+    if (!x) return fail(c, KMOE_E_INVALID, "null pointer");
+    DeviceGuard g(c->device);
+    if (int1) {  // one kernel: the norm inside the projection (K-quant rows), x + y into x_out
+      const hipError_t e = timed(c, "matvec_qkv_rope", [&]() {
+        const QkvNorm nm{x, y, norm_w, eps, h, x_out};
+        return launch_matvec_qkv_rope_norm(c->stream, t, (const uint8_t *)w, rows, cols, nm, qkv, rp);
+      });
+      if (e == hipSuccess) return KMOE_OK;
+      if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
+    // otherwise the in-place calls below on a copy of x in x_out
+    HIP_OK(c, hipMemcpyAsync(x_out, x, (size_t)cols * 4, hipMemcpyDeviceToDevice, c->stream));
+    x = x_out;
+  }
   // one token on the integer path: norm + int8 rows, then the projection with
   // RoPE and the cache store in its epilogue
-  if (t != KMOE_F32 && int_path(c->regime, 1) && block_size(t) > 0 && bytes_for(t, cols) > 0 &&
-      (uint64_t)w_len >= (uint64_t)bytes_for(t, cols) * (uint64_t)rows && x && norm_w && w && h &&
-      !check_quant_shape(c, t, cols)) {
+  if (int1) {
     DeviceGuard g(c->device);
     size_t need = 0;
     carve_qrows(nullptr, 1, cols, &need, 0);
     rc = ensure_ws(c, need);
     if (rc) return rc;
     QRows qr = carve_qrows(c->ws, 1, cols, &need, 0);
-    const QkvRope rp{n_head, n_kv, head_dim, rope_dim, neox, pos0, pos_dev, inv_freq, n_ctx, q_out, k_cache, v_cache};
-    hipError_t e = launch_rmsnorm_quant(c->stream, x, y, norm_w, 1, cols, eps, h, is_kq(t), qr.q, qr.d, qr.s);
+    hipError_t e = timed(c, "rmsnorm_quant", [&]() {
+      return launch_rmsnorm_quant(c->stream, x, y, norm_w, 1, cols, eps, h, is_kq(t), qr.q, qr.d, qr.s);
+    });
     if (e == hipSuccess) {
       e = timed(c, "matvec_qkv_rope", [&]() {
         return launch_matvec_qkv_rope(c->stream, t, (const uint8_t *)w, rows, cols, qr.q, qr.d, qr.s, qkv, rp);

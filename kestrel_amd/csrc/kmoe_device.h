@@ -265,6 +265,83 @@ __device__ __forceinline__ float wg_sum256(float v, float *red) {
   return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
+// One row's residual add and RMSNorm by a work-group of 256 threads, as
+// k_rmsnorm_regs computes it (transformer.rs:330-340, :427): thread t holds
+// the float4 groups t + 256k of v = x (+ y), ss is the same sum over them then
+// wg_sum256, and h[k] = (v * rr) * w per element, zero past the row (d % 4 ==
+// 0, d <= 1024 * NV, 16-byte aligned rows). Every work-group of the launch
+// calls it. With y and done, v goes back into x from the last work-group to
+// count itself on *done, after every work-group's loads of x have returned
+// (each counts after its reduction), so none can read the updated x; that
+// work-group resets the counter. A non-null xo (another buffer) receives v.
+template <int NV>
+__device__ __forceinline__ void wg_residual_rmsnorm(float *x, const float *y, const float *w, int64_t d, float eps,
+                                                    uint32_t *done, float4 (&h)[NV], float *red, int *xlast,
+                                                    float *xo = nullptr) {
+  const int t = threadIdx.x;
+  const int n4 = (int)(d / 4);
+  float4 *xr = (float4 *)x;
+  const float4 *yr = (const float4 *)y;
+  const float4 *wr = (const float4 *)w;
+  float4 v[NV], ww[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = t + 256 * k;
+    if (i < n4) {
+      v[k] = xr[i];
+      ww[k] = wr[i];
+    }
+  }
+  if (yr) {
+    float4 yy[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (t + 256 * k < n4) yy[k] = yr[t + 256 * k];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (t + 256 * k < n4) {
+        v[k].x = v[k].x + yy[k].x;
+        v[k].y = v[k].y + yy[k].y;
+        v[k].z = v[k].z + yy[k].z;
+        v[k].w = v[k].w + yy[k].w;
+      }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
+  ss = wg_sum256(ss, red);  // its barriers: every thread's loads of x and y have returned
+  if (xo) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (t + 256 * k < n4) ((float4 *)xo)[t + 256 * k] = v[k];
+  }
+  if (yr && done) {
+    if (t == 0) {
+      *xlast = add_release(done, 1u) == gridDim.x - 1;
+      if (*xlast) acquire_agent();  // every other work-group has read x
+    }
+    __syncthreads();
+    if (*xlast) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (t + 256 * k < n4) xr[t + 256 * k] = v[k];
+      if (t == 0) __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  const float rr = 1.0f / sqrtf(ss / (float)d + eps);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    h[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t + 256 * k < n4) {
+      h[k].x = (v[k].x * rr) * ww[k].x;
+      h[k].y = (v[k].y * rr) * ww[k].y;
+      h[k].z = (v[k].z * rr) * ww[k].z;
+      h[k].w = (v[k].w * rr) * ww[k].w;
+    }
+  }
+}
+
 // Q8KRow::quantize of one 256-element block by one full wave (qdot.rs:353-365).
 // The same from values already in registers: lane l holds elements
 // 4l..4l+3 of the block in v.

@@ -286,6 +286,20 @@ struct QkvRope {
 hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
                                   const int8_t *xq, const float *xd, const int32_t *xbs, float *out,
                                   const QkvRope &rope);
+// The same with the residual add and RMSNorm in front (one token, K-quant
+// rows of at most 4096 columns, 16-byte aligned rows): xo = x + y (y may be
+// null; xo another buffer, x is not written), h = rmsnorm(xo) * w with
+// k_rmsnorm_regs' bits, quantized to Q8_K inside the projection kernel;
+// hipErrorNotSupported outside that.
+struct QkvNorm {
+  const float *x;
+  const float *y, *w;
+  float eps;
+  float *h;
+  float *xo;
+};
+hipError_t launch_matvec_qkv_rope_norm(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                       const QkvNorm &nm, float *out, const QkvRope &rope);
 // The FFN norm folded into the single-token router (RouteNorm): x += y (y
 // may be null), f = rmsnorm(x) * w with k_rmsnorm_regs' arithmetic, and the
 // router reads f. Needs S == 1, d % 256 == 0, 16-byte aligned rows.

@@ -73,6 +73,15 @@ struct MvArgs {
   const float *sh_xd;
   const int32_t *sh_xbs;
   const float *sh_logit;
+  // M_QKV_NORM: the residual add and RMSNorm of the one-token row in front
+  // (wg_residual_rmsnorm of nx + ny with weights nw); work-group 0 stores
+  // nx + ny into nxo (another buffer: nx stays as it was) and the normed row
+  // into nh
+  const float *nx;
+  const float *ny, *nw;
+  float neps;
+  float *nxo;
+  float *nh;
 };
 
 enum { M_PLAIN = 0, M_GATE_UP = 1, M_DOWN = 2, M_SUMS = 3 };
@@ -81,6 +90,9 @@ enum { M_QKV = 5 };
 // kernel (K-quant rows of at most kRegFxBlocks superblocks)
 enum { M_PLAIN_FX = 6 };
 constexpr int kRegFxBlocks = 16;
+// M_QKV whose activation row is the residual add and RMSNorm of nx (+ ny),
+// formed and quantized to Q8_K inside the kernel as M_PLAIN_FX does
+enum { M_QKV_NORM = 7 };
 
 // The RoPE + KV store epilogue of a one-token q/k/v projection with
 // interleaved pairs (rows 2i and 2i+1 of a head, dims below rope_dim) or
@@ -837,6 +849,32 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
       const int t = lr + i * LPR;
       if (i < tpl && t < ntasks) act_load<TYPE>(act[i], fq, fd, fbs, t);
     }
+  } else if constexpr (MODE == M_QKV_NORM) {
+    // x (+ y), its RMSNorm (k_rmsnorm_regs' bits) and the Q8_K blocks into
+    // LDS: thread t's float4 group t + 256i is element 4 * lane of block
+    // wave + 4i, the layout of the wave quantizer
+    __shared__ __attribute__((aligned(16))) int8_t fq[kRegFxBlocks * 256];
+    __shared__ float fd[kRegFxBlocks];
+    __shared__ __attribute__((aligned(16))) int32_t fbs[kRegFxBlocks * 16];
+    __shared__ float red[4];
+    __shared__ int xlast;
+    float4 hv[kRegFxBlocks / 4];
+    wg_residual_rmsnorm<kRegFxBlocks / 4>(const_cast<float *>(a.nx), a.ny, a.nw, cols, a.neps, nullptr, hv, red, &xlast,
+                                          blockIdx.x == 0 ? a.nxo : nullptr);
+#pragma unroll
+    for (int i = 0; i < kRegFxBlocks / 4; ++i) {
+      const int bk = wave + 4 * i;
+      if (bk < nblk) {
+        if (blockIdx.x == 0) *(float4 *)(a.nh + 256 * bk + 4 * lane) = hv[i];
+        wave_quant_q8k_vals(hv[i], fq + 256 * bk, fd + bk, fbs + 16 * bk, lane);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPLMAX; ++i) {
+      const int t = lr + i * LPR;
+      if (i < tpl && t < ntasks) act_load<TYPE>(act[i], fq, fd, fbs, t);
+    }
   } else if constexpr (MODE != M_DOWN_COMBINE) {  // one activation row: token 0 (or the plain row)
 #pragma unroll
     for (int i = 0; i < TPLMAX; ++i) {
@@ -956,7 +994,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
             if (r < rows_i) {
               constexpr bool TL = MODE == M_GATE_UP;  // expert tier rows are tiled, plain rows are GGUF
               int64_t rw = r;
-              if constexpr (MODE == M_QKV) rw = qkv_row(a.rope, r);
+              if constexpr (MODE == M_QKV || MODE == M_QKV_NORM) rw = qkv_row(a.rope, r);
               if constexpr (MODE == M_GATE_UP && (TYPE == T_Q4_K || TYPE == T_Q8_0)) {
                 if (shared_item) {  // GGUF rows into the same registers (Q4_K and Q8_0 tasks alike)
                   w0[u].w = wq_load_gguf<TYPE>(W0 + r * row_bytes, t, nblk);
@@ -993,7 +1031,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
         if constexpr (MODE == M_GATE_UP) acc1[u] = group_sum<LPR>(acc1[u]);
       }
       float pair[RU];  // M_QKV: row r^1's sum, held by the lanes LPR away (RPW >= 2)
-      if constexpr (MODE == M_QKV) {
+      if constexpr (MODE == M_QKV || MODE == M_QKV_NORM) {
         static_assert(RPW >= 2, "row pairs in one wave");
 #pragma unroll
         for (int u = 0; u < RU; ++u) pair[u] = __shfl_xor(acc0[u], LPR);
@@ -1003,7 +1041,7 @@ __global__ void __launch_bounds__(256) k_mv_reg(MvArgs a, int tpl) {
         for (int u = 0; u < RU; ++u) {
           const int64_t r = r0 + (int64_t)u * RPW;
           if (r >= rows_i) continue;
-          if constexpr (MODE == M_QKV) {
+          if constexpr (MODE == M_QKV || MODE == M_QKV_NORM) {
             const int64_t rw = qkv_row(a.rope, r);
             a.out[rw] = acc0[u];
             qkv_rope_store(a.rope, rw, acc0[u], pair[u]);
@@ -1644,6 +1682,43 @@ static hipError_t launch_qkv_reg(hipStream_t st, const MvArgs &a) {
   if (lpr == 32) return launch_reg<TYPE, 32, 1, 1, M_QKV>(st, a, tpl, t32);
   if (lpr == 16) return launch_reg<TYPE, 16, 1, 1, M_QKV>(st, a, tpl, t16);
   return hipErrorNotSupported;  // one row per wave step: pairs not in one wave
+}
+
+template <int TYPE>
+static hipError_t launch_qkv_norm_reg(hipStream_t st, const MvArgs &a) {
+  const int ntasks = (int)(QT<TYPE>::TPB * (a.cols / QT<TYPE>::EL));
+  int lpr, tpl;
+  if (!reg_geometry(TYPE, ntasks, lpr, tpl) || tpl != 1) return hipErrorNotSupported;
+  const int64_t t32 = (a.rows + 4 * 2 - 1) / (4 * 2), t16 = (a.rows + 4 * 4 - 1) / (4 * 4);
+  if (lpr == 32) return launch_reg<TYPE, 32, 1, 1, M_QKV_NORM>(st, a, tpl, t32);
+  if (lpr == 16) return launch_reg<TYPE, 16, 1, 1, M_QKV_NORM>(st, a, tpl, t16);
+  return hipErrorNotSupported;
+}
+
+hipError_t launch_matvec_qkv_rope_norm(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                       const QkvNorm &nm, float *out, const QkvRope &rope) {
+  if ((rope.neox && rope.rd != rope.hd) || rope.hd <= 0 || rope.hd % 2 || rope.rd % 2 || rope.rd > rope.hd ||
+      rope.nh < 1 || rope.nkv < 0 || rows != (int64_t)(rope.nh + 2 * rope.nkv) * rope.hd)
+    return hipErrorNotSupported;
+  if (!is_kquant(type) || cols % 256 != 0 || cols / 256 > kRegFxBlocks || !nm.x || !nm.w || !nm.h || !nm.xo ||
+      nm.xo == nm.x || (((uintptr_t)nm.x | (uintptr_t)nm.y | (uintptr_t)nm.w | (uintptr_t)nm.h | (uintptr_t)nm.xo) & 15u))
+    return hipErrorNotSupported;
+  MvArgs a{};
+  a.w0 = w;
+  a.rows = rows;
+  a.cols = cols;
+  a.s_rows = 1;
+  a.out = out;
+  a.rope = rope;
+  a.nx = nm.x;
+  a.ny = nm.y;
+  a.nw = nm.w;
+  a.neps = nm.eps;
+  a.nxo = nm.xo;
+  a.nh = nm.h;
+  if (type == T_Q4_K) return launch_qkv_norm_reg<T_Q4_K>(st, a);
+  if (type == T_Q6_K) return launch_qkv_norm_reg<T_Q6_K>(st, a);
+  return hipErrorNotSupported;
 }
 
 hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,

@@ -526,83 +526,30 @@ struct RouteDecArgs {
 };
 
 // One token's FFN norm in front of the router (RouteNorm): every work-group
-// forms x + y and the normed row in registers exactly as k_rmsnorm_regs does
-// (float4 groups q = t + 256k, the same sums, wg_sum256, the same products),
-// so the row is the same bits; work-group 0 also stores the normed row and its
-// int8 rows (qtype) for the gate/up kernel. x + y goes back into x from the
-// last work-group to count itself on n.done, after every work-group's loads
-// of x have returned (each counts after its reduction), so no work-group can
-// read the updated x; that work-group resets the counter.
+// forms x + y and the normed row in registers (wg_residual_rmsnorm: the bits
+// of k_rmsnorm_regs); work-group 0 also stores the normed row and its int8
+// rows (qtype) for the gate/up kernel, and the last work-group to count
+// itself on n.done stores x + y back into x.
 template <int NV>
 __device__ __forceinline__ void route_norm_row(const RouteDecArgs &a, float4 (&h)[NV], bool store, float *red,
                                                int *xlast) {
   const int t = threadIdx.x;
   const int n4 = (int)(a.d / 4);
   const RouteNorm &n = a.norm;
-  float4 *xr = (float4 *)n.x;
-  const float4 *yr = (const float4 *)n.y;
-  const float4 *wr = (const float4 *)n.w;
-  float4 v[NV], ww[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int i = t + 256 * k;
-    if (i < n4) {
-      v[k] = xr[i];
-      ww[k] = wr[i];
-    }
-  }
-  if (yr) {
-    float4 yy[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-      if (t + 256 * k < n4) yy[k] = yr[t + 256 * k];
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-      if (t + 256 * k < n4) {
-        v[k].x = v[k].x + yy[k].x;
-        v[k].y = v[k].y + yy[k].y;
-        v[k].z = v[k].z + yy[k].z;
-        v[k].w = v[k].w + yy[k].w;
-      }
-  }
-  float ss = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k)
-    if (t + 256 * k < n4) ss += ((v[k].x * v[k].x + v[k].y * v[k].y) + v[k].z * v[k].z) + v[k].w * v[k].w;
-  ss = wg_sum256(ss, red);  // its barriers: every thread's loads of x and y have returned
-  if (yr) {
-    if (t == 0) {
-      *xlast = add_release(n.done, 1u) == gridDim.x - 1;
-      if (*xlast) acquire_agent();  // every other work-group has read x
-    }
-    __syncthreads();
-    if (*xlast) {
-#pragma unroll
-      for (int k = 0; k < NV; ++k)
-        if (t + 256 * k < n4) xr[t + 256 * k] = v[k];
-      if (t == 0) __hip_atomic_store(n.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  const float rr = 1.0f / sqrtf(ss / (float)a.d + n.eps);
+  wg_residual_rmsnorm<NV>(n.x, n.y, n.w, a.d, n.eps, n.done, h, red, xlast);
+  if (!store) return;
   float4 *frow = (float4 *)n.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int i = t + 256 * k;
-    h[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (i < n4) {
-      h[k].x = (v[k].x * rr) * ww[k].x;
-      h[k].y = (v[k].y * rr) * ww[k].y;
-      h[k].z = (v[k].z * rr) * ww[k].z;
-      h[k].w = (v[k].w * rr) * ww[k].w;
-      if (store) {
-        frow[i] = h[k];
-        if (is_kquant(a.qtype)) {
-          const int64_t b = 4 * k + (t >> 6);
-          wave_quant_q8k_vals(h[k], a.xq + 256 * b, a.xd + b, a.xs + 16 * b, t & 63);
-        } else if (a.qtype == T_Q8_0) {
-          const int64_t b = (4 * (int64_t)i) / 32;
-          group8_quant_q8_vals(h[k], a.xq + 32 * b, a.xd + b, a.xs + 2 * b, t & 7);
-        }
+      frow[i] = h[k];
+      if (is_kquant(a.qtype)) {
+        const int64_t b = 4 * k + (t >> 6);
+        wave_quant_q8k_vals(h[k], a.xq + 256 * b, a.xd + b, a.xs + 16 * b, t & 63);
+      } else if (a.qtype == T_Q8_0) {
+        const int64_t b = (4 * (int64_t)i) / 32;
+        group8_quant_q8_vals(h[k], a.xq + 32 * b, a.xd + b, a.xs + 2 * b, t & 7);
       }
     }
   }

@@ -154,20 +154,24 @@ class Decoder:
         ty, dims, t = w
         return self.ctx.matmul(ty, t, int(np.prod(dims[1:])), dims[0], x)
 
-    def _layer(self, L, x, f_prev, S: int, pos0: int, pos_dev):
-        """One decoder layer on the residual stream x [S, d] (updated in
-        place). f_prev, the previous layer's FFN output, joins x in the first
-        norm's fused add; the layer returns its own FFN output."""
+    def _layer(self, L, x, f_prev, S: int, pos0: int, pos_dev, spare=None):
+        """One decoder layer on the residual stream x [S, d]. f_prev, the
+        previous layer's FFN output, joins x in the first norm's fused add.
+        Returns the layer's own FFN output and the buffer that now holds the
+        residual stream: x (updated in place), or spare, a second buffer that
+        one-token layers write x + f_prev into (x is then left as it was)."""
         ctx, nh, nkv, hd = self.ctx, self.nh, self.nkv, self.hd
         kvw, nq = nkv * hd, nh * hd
         plain = not any(n in L for n in ("bq", "bk", "bv", "q_norm", "k_norm"))
         if "wqkv" in L and S == 1 and plain:
-            # one token: the projection kernel applies RoPE and fills the caches
+            # one token: the projection kernel takes the residual add and the
+            # norm (into the other buffer), applies RoPE and fills the caches
             ty, dims, t = L["wqkv"]
+            xr = x if spare is None else spare
             qr = ctx.norm_matmul_rope_kv(x, L["attn_norm"], self.eps, ty, t, dims[0], nh, nkv, hd, self.rd, pos0,
                                          self.inv_freq, self.neox, self.n_ctx, L["kc"], L["vc"], y=f_prev,
-                                         pos_dev=pos_dev)
-            return self._attn_ffn(L, x, qr, S, pos0, pos_dev)
+                                         pos_dev=pos_dev, x_out=spare)
+            return self._attn_ffn(L, xr, qr, S, pos0, pos_dev), xr
         if "wqkv" in L:
             ty, dims, t = L["wqkv"]
             qkv = ctx.norm_matmul(x, L["attn_norm"], self.eps, ty, t, dims[1], dims[0], y=f_prev)
@@ -186,7 +190,7 @@ class Decoder:
             ctx.rmsnorm(k, L["k_norm"], self.eps, out=k)
         qr = ctx.rope_kv_store(q, k, v, nh, nkv, hd, self.rd, pos0, self.inv_freq, self.neox, self.n_ctx, L["kc"],
                                L["vc"], pos_dev)
-        return self._attn_ffn(L, x, qr, S, pos0, pos_dev)
+        return self._attn_ffn(L, x, qr, S, pos0, pos_dev), x
 
     def _attn_ffn(self, L, x, qr, S, pos0, pos_dev):
         """Attention from the rotated q and the caches, its projection, then the FFN."""
@@ -213,8 +217,11 @@ class Decoder:
     def _stack(self, x, S: int, pos0: int, pos_dev):
         """All layers and the head; returns the logits of the last row."""
         f = None
+        spare = self.torch.empty_like(x) if S == 1 else None  # the residual stream's second buffer
         for L in self.layers:
-            f = self._layer(L, x, f, S, pos0, pos_dev)
+            f, xr = self._layer(L, x, f, S, pos0, pos_dev, spare)
+            if xr is not x:
+                x, spare = xr, x
         ty, dims, t = self.head
         return self.ctx.norm_matmul(x[S - 1:S], self.out_norm, self.eps, ty, t, dims[1], dims[0],
                                     y=f[S - 1:S]).reshape(-1)

@@ -87,7 +87,7 @@ SIGNATURES = {
     "kmoe_matmul_host": (C.c_int, [_P, C.c_int, _P, _sz, _i64, _i64, _P, _i64, _P]),
     "kmoe_expert_part_layout": (C.c_int, [_P, _u32, _u32, _i32, C.POINTER(_i32)]),
     "kmoe_norm_matmul_rope_kv": (C.c_int, [_P, _P, _P, _P, _f, C.c_int, _P, _sz, _i64, _P, _P, _i32, _i32, _i32,
-                                           _i32, _i64, _P, _P, _i32, _i64, _P, _P, _P]),
+                                           _i32, _i64, _P, _P, _i32, _i64, _P, _P, _P, _P]),
     "kmoe_norm_moe_ffn": (C.c_int, [_P, _u32, _P, _P, _P, _f, _i64, _P, _P]),
     "kmoe_moe_last_routing": (C.c_int, [_P, _P, _P, _P, _P]),
     "kmoe_get_rows": (C.c_int, [_P, _i32, _P, _sz, _i64, _i64, _P, _i64, _P]),
@@ -276,8 +276,9 @@ class Context:
 
     def norm_matmul_rope_kv(self, x, norm_w, eps: float, t: int, w, cols: int, n_head: int, n_kv: int,
                             head_dim: int, rope_dim: int, pos0: int, inv_freq, neox: bool, n_ctx: int, k_cache,
-                            v_cache, y=None, pos_dev=None, h=None, qkv=None, q_out=None):
-        """One token: norm_matmul over the q/k/v rows, then rope_kv_store of its parts; returns q_out."""
+                            v_cache, y=None, pos_dev=None, h=None, qkv=None, q_out=None, x_out=None):
+        """One token: norm_matmul over the q/k/v rows, then rope_kv_store of its parts; returns q_out.
+        With x_out (another [1, cols] buffer) x + y goes there and x is left as it was."""
         rows = (n_head + 2 * n_kv) * head_dim
         h = self._empty((1, cols), self.torch.float32) if h is None else h
         qkv = self._empty((1, rows), self.torch.float32) if qkv is None else qkv
@@ -285,7 +286,7 @@ class Context:
         self.check(self.lib.kmoe_norm_matmul_rope_kv(
             self.h, _ptr(x), _ptr(y), _ptr(norm_w), eps, t, _ptr(w), w.numel() * w.element_size(), cols, _ptr(h),
             _ptr(qkv), n_head, n_kv, head_dim, rope_dim, pos0, _ptr(pos_dev), _ptr(inv_freq), int(neox), n_ctx,
-            _ptr(q_out), _ptr(k_cache), _ptr(v_cache)))
+            _ptr(q_out), _ptr(k_cache), _ptr(v_cache), _ptr(x_out)))
         return q_out
 
     def rope_kv_store(self, q, k, v, n_head: int, n_kv: int, head_dim: int, rope_dim: int, pos0: int, inv_freq,

@@ -529,13 +529,16 @@ def test_decoder_context_full(ctx):
     (Q4_K, 1024, 8, 2, 64, 32, True, 0, False, False),     # neox over part of the head: separate kernels
     (Q4_K, 2048, 16, 4, 128, 128, False, 2, False, False),  # exact regime: separate kernels
 ])
+@pytest.mark.parametrize("out_of_place", [False, True])
 def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, nkv, hd, rd, neox, regime, use_dev,
-                                                         fused):
+                                                         fused, out_of_place):
     """kmoe_norm_matmul_rope_kv against kmoe_norm_matmul followed by
-    kmoe_rope_kv_store on one token: the residual, the normed row, the
-    projection, the rotated q and both caches are the same bits, for two
-    positions in a row; the RoPE epilogue of the projection ran where the
-    geometry allows it."""
+    kmoe_rope_kv_store on one token: the residual (in place, or into x_out
+    with x untouched), the normed row, the projection, the rotated q and both
+    caches are the same bits, for two positions in a row (with and without
+    the residual add); the RoPE epilogue ran in the projection where the
+    geometry allows it, and with x_out on K-quant rows so did the norm (one
+    kernel)."""
     import torch
 
     rows, n_ctx = (nh + 2 * nkv) * hd, 16
@@ -549,17 +552,25 @@ def test_norm_matmul_rope_kv_is_norm_matmul_then_rope_kv(ctx, orc, t, cols, nh, 
     try:
         for pos in (5, 6):
             x = rng.standard_normal((1, cols)).astype(np.float32)
-            y = dev(rng.standard_normal((1, cols)).astype(np.float32))
+            # the second position without the residual add
+            y = dev(rng.standard_normal((1, cols)).astype(np.float32)) if pos == 5 else None
             xa, xb = dev(x), dev(x)
             pos_dev = torch.tensor([pos - 2], dtype=torch.int32).cuda() if use_dev else None
             p0 = 2 if use_dev else pos
             ha = torch.empty((1, cols), dtype=torch.float32).cuda()
             qkva = torch.empty((1, rows), dtype=torch.float32).cuda()
+            xo = torch.full((1, cols), float("nan"), dtype=torch.float32).cuda() if out_of_place else None
             ctx.profile_enable(True)
             qa = ctx.norm_matmul_rope_kv(xa, nw, 1e-5, t, w, cols, nh, nkv, hd, rd, p0, f, neox, n_ctx, caches[0],
-                                         caches[1], y=y, pos_dev=pos_dev, h=ha, qkv=qkva)
+                                         caches[1], y=y, pos_dev=pos_dev, h=ha, qkv=qkva, x_out=xo)
             assert ctx.profile_read("matvec_qkv_rope")[1] == (1 if fused else 0)
+            one_kernel = fused and out_of_place and t != Q8_0
+            if one_kernel:
+                assert ctx.profile_read("rmsnorm_quant")[1] == 0
             ctx.profile_enable(False)
+            if out_of_place:
+                assert np.array_equal(host(xa).view(np.uint32), x.view(np.uint32))
+                xa = xo
             hb = torch.empty((1, cols), dtype=torch.float32).cuda()
             qkvb = ctx.norm_matmul(xb, nw, 1e-5, t, w, rows, cols, y=y, h=hb)
             qb = ctx.rope_kv_store(qkvb[:, :nq], qkvb[:, nq:nq + kvw], qkvb[:, nq + kvw:], nh, nkv, hd, rd, p0, f,
@@ -598,7 +609,7 @@ def test_norm_matmul_rope_kv_rejects_bad_arguments(ctx, orc):
     q_out = torch.empty((1, nh * hd), dtype=torch.float32).cuda()
     rc = ctx.lib.kmoe_norm_matmul_rope_kv(ctx.h, x.data_ptr(), None, nw.data_ptr(), 1e-5, Q4_K, w.data_ptr(),
                                           w.numel(), cols, h.data_ptr(), qkv.data_ptr(), nh, nkv, hd, hd, 0, None,
-                                          f.data_ptr(), 0, n_ctx, q_out.data_ptr(), None, vc.data_ptr())
+                                          f.data_ptr(), 0, n_ctx, q_out.data_ptr(), None, vc.data_ptr(), None)
     assert rc != 0
     assert not host(kc).any() and not host(vc).any()
 
