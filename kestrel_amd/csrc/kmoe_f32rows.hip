@@ -1,37 +1,10 @@
 // kmoe_f32rows.hip — the reference's f32 regime (quant.rs:242-260: weights
 // dequantized to f32, multiplied with f32 activations; avx2.rs:230-308) for
 // experts that hold a few token rows (decode batches), over the expert tier's
-// tiled Q4_K rows.
-//
-// Streaming instead of staging: a work-group takes a block of 16*RT weight
-// rows of one expert and runs over the whole rows once, its four waves taking
-// a quarter of the superblocks each (split K). In a wave, lane l owns row
-// 16*i + l % 16 of row tile i (i < RT) and, in every 64-column step (a
-// quarter k of a superblock), the 16 columns 16*(l / 16) .. +15. Those 16
-// weights are one tiled nibble chunk (quarter k, half (l / 16) & 1; low
-// nibbles for the first two lane groups, high for the others), dequantized in
-// registers as dequant_row does it (quant.rs:138-155: (d*sc)*q - dmin*m, a
-// multiply and a subtract, so every weight equals the reference's f32 value;
-// d*sc and dmin*m of the lane's four sub-blocks are formed once per
-// superblock) and fed to v_mfma_f32_16x16x4f32 as its A operand: MFMA m of the
-// step takes column 16*(l/16) + m for lane quad l/16. The B operand (the token
-// rows, read from L2: token l % 16, the same 16 columns) is shared by the RT
-// row tiles. The products are exact and the sums fp32 in the matrix core's
-// order (a few ulp from gemm_f32's 8-lane chains); the four waves' partial
-// sums are added in wave order through LDS at the end, so results do not
-// depend on timing. Two steps' nibble chunks and token values and the next
-// superblock's heads are in flight while a step is multiplied; loads are
-// unconditional (rows, tokens and steps past the end are clamped, their
-// results never used) and the last two steps issue none.
-//
-// gate/up: both matrices' rows per lane, so the lane that finishes a row tile
-// holds gate and up of the same (row, token) elements and applies SwiGLU
-// (transformer.rs:558) in registers. down: one matrix.
-#include <type_traits>
-
+// tiled Q4_K rows, streamed once: gate and up in one launch (SwiGLU,
+// transformer.rs:558, in the epilogue), down in another.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
-#include "kmoe_tq4.h"
 
 namespace kmoe {
 
@@ -53,189 +26,261 @@ __device__ __forceinline__ bool rows_f32_regime(int regime, int n) {
   return regime == REGIME_EXACT || (regime == REGIME_AVX2 && n >= 4);
 }
 
-template <int MODE, int TT, int RT>
-__global__ void __launch_bounds__(256, 2) k_f32_rows(F32RowsArgs a) {
-  constexpr int NM = MODE == 0 ? 2 : 1;  // matrices per lane: gate and up, or down
-  constexpr int NACC = RT * NM * TT;     // accumulator tiles per wave
-  __shared__ __attribute__((aligned(16))) f32x4 red[3][NACC][64];  // waves 1..3's partial sums
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// The products run on the matrix cores' bf16 path, exactly.
+// For sub-block j of a superblock, dequant_row's weights are w = A_j*q - B_j
+// (A_j = d*sc_j, B_j = dmin*m_j, q the 4-bit value; quant.rs:138-155), so
+// sum_k w_k x_k = A_j * sum_k q_k x_k - B_j * sum_k x_k. q is exact in bf16,
+// and each x splits exactly into three bf16 pieces (x1 = x with its low 16
+// bits cleared, x2 the same of x - x1, x3 = x - x1 - x2, which has at most 8
+// significant bits), so v_mfma_f32_16x16x32_bf16 (K = 32, one sub-block)
+// forms the exact products q*x1, q*x2, q*x3 and sums them in fp32; the
+// sub-block's result then joins the row's sum as fma(A_j, P, y) and
+// fma(-B_j, S_j, y), S_j the token's fp32 sum of the sub-block's x. The
+// result is the f32 regime's within a few fp32 roundings (the reference's
+// own sum runs in another order too).
+//
+// Work-group: 16 * (4 / KW) weight rows of one expert by up to 16 * TT of
+// its token rows; wave w takes row tile w / KW and, of every KW consecutive
+// superblocks, the (w % KW)-th (KW = 1 for wide experts; narrow ones split the
+// superblocks over the waves so that enough work-groups run). Per round of KW
+// superblocks the 256 threads split the tokens' x into LDS (three bf16 planes
+// per superblock, and the sub-block sums), each wave turns its rows' heads
+// into A_j, B_j in LDS, and for every quarter k a lane converts its 8 nibble
+// bytes of row 16 * tile + l % 16 (bytes 8*(l/16) .. +7 of the quarter's 32:
+// elements 8*(l/16) .. +7 of sub-blocks 2k (low nibbles) and 2k+1 (high)) to
+// the MFMA's A operand; the B operand of lane l is token l % 16's pieces of
+// the same elements. Lane l ends with rows 16 * tile + 4*(l/16) + v, v < 4,
+// of token l % 16 of each token tile; the KW waves of a tile add their sums
+// through LDS in wave order at the end. The next round's x, nibbles and
+// heads are loaded while the current one is multiplied.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr int kX3Pad = 264;           // bf16 per token row of a plane in LDS (256 + 8: two-way bank conflicts at most)
+
+// Pairs of f32 whose low 16 bits are zero, as one dword of two bf16 (first low).
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+template <int MODE, int TT, int KW>
+__global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32RowsArgs a) {
+  constexpr int NM = MODE == 0 ? 2 : 1;
+  constexpr int RT = 4 / KW;  // row tiles per work-group
+  __shared__ __attribute__((aligned(16))) uint16_t xp[KW][3][TT * 16][kX3Pad];  // x pieces by token, column
+  __shared__ float xs[KW][TT * 16][8];                                          // sub-block sums of x by token
+  __shared__ __attribute__((aligned(16))) float ab[4][NM][2][8][16];             // wave, matrix, A|B, sub-block, row
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = wave / KW, kg = wave % KW;
   const int i_act = blockIdx.y;
   if (i_act >= *a.rt.n_active) return;
   const int e = a.rt.active[i_act];
   const int64_t p0 = a.rt.offsets[e];
   const int n = (int)(a.rt.offsets[e + 1] - p0);
   if (n < a.min_rows || n > a.max_rows || !rows_f32_regime(a.regime, n)) return;
+  const int ntt = (n + 15) / 16;  // token tiles of this expert (<= TT)
   const int64_t cols = a.cols, nb = cols / 256, rows = a.rows, row_bytes = nb * 144;
   const int r16 = lane & 15, g = lane >> 4;
-  const bool hi = g >= 2;  // high nibbles: the odd sub-block of each quarter
-  const int64_t r0 = (int64_t)blockIdx.x * (16 * RT);
+  const int64_t rbase = (int64_t)blockIdx.x * (16 * RT) + 16 * tile;
   const uint8_t *E = a.tier.base + (int64_t)e * a.tier.stride;
-  const uint8_t *Wm[RT][NM];
+  const uint8_t *Wr[NM];  // this lane's A-operand row
 #pragma unroll
-  for (int i = 0; i < RT; ++i) {
-    const int64_t r = r0 + 16 * i + r16 < rows ? r0 + 16 * i + r16 : rows - 1;
-#pragma unroll
-    for (int mt = 0; mt < NM; ++mt) Wm[i][mt] = E + a.tier.off[MODE == 0 ? mt : 2] + r * row_bytes;
+  for (int mt = 0; mt < NM; ++mt) {
+    const int64_t r = rbase + r16 < rows ? rbase + r16 : rows - 1;
+    Wr[mt] = E + a.tier.off[MODE == 0 ? mt : 2] + r * row_bytes;
   }
-  // the token row of lane l in tile t (B operand column l % 16)
-  const float *xr[TT];
+  // the split: thread tid takes token tid / 16 (+16t) and columns 16*(tid % 16) .. +15 of each of the round's superblocks
+  const int stok = tid >> 4, sc16 = tid & 15;
+  const float *xrow[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
-    const int tk = 16 * t + r16 < n ? 16 * t + r16 : n - 1;
+    const int tk = 16 * t + stok < n ? 16 * t + stok : n - 1;
     const int64_t src = MODE == 0 ? (int64_t)(a.rt.perm[p0 + tk] / (uint32_t)a.rt.topk) : p0 + tk;
-    xr[t] = a.x + src * cols + 16 * g;
+    xrow[t] = a.x + src * cols + 16 * sc16;
   }
-  // this wave's superblocks [b0, b0 + nbw), its steps j = 4 * (b - b0) + k
-  const int nbq = (int)((nb + 3) / 4);
-  const int b0 = wave * nbq;
-  const int nbw = b0 >= nb ? 0 : ((int)nb - b0 < nbq ? (int)nb - b0 : nbq);
-  const int nsj = 4 * nbw;
-  f32x4 acc[RT][NM][TT];
+  float4 xv[KW][TT][4];
+  uint2 wq[NM][4];  // this wave's superblock: nibble bytes of the 4 quarters
+  u32x4v hd[NM];    // and its head (lanes with g == 0 use it)
+  auto load_round = [&](int64_t b0) {
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-      for (int t = 0; t < TT; ++t) acc[i][mt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (nbw > 0) {
-    u32x4 q[2][RT][NM];
-    float4 xv[2][TT][4];
-    u32x4 hd[RT][NM];           // heads of the next superblock
-    float dl[RT][NM][4], ml[RT][NM][4];  // d*sc, dmin*m of the lane's sub-block in each quarter
-    auto load = [&](int j, int slot) {
-      const int jc = j < nsj ? j : nsj - 1;
-      const int64_t b = b0 + (jc >> 2);
-      const int k = jc & 3;
-      const int s = 4 * (int)b + k;
-#pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) q[slot][i][mt] = *(const u32x4 *)(Wm[i][mt] + tq4_qs_off(nb, b, k, g & 1));
+    for (int q = 0; q < KW; ++q) {
+      const int64_t b = b0 + q < nb ? b0 + q : nb - 1;
 #pragma unroll
       for (int t = 0; t < TT; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xv[slot][t][u] = *(const float4 *)(xr[t] + 64 * s + 4 * u);
-    };
-    auto load_heads = [&](int bl) {  // superblock b0 + bl (clamped)
-      const int64_t b = b0 + (bl < nbw ? bl : nbw - 1);
-#pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) hd[i][mt] = *(const u32x4 *)(Wm[i][mt] + 16 * b);
-    };
-    auto scales = [&]() {  // scale_min_k4 of the heads (quant.rs:54-61), per quarter
-#pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) {
-          const u32x4 h = hd[i][mt];
-          const float d = f16_bits_to_f32(h.x), dmin = f16_bits_to_f32(h.x >> 16);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            int sA, mA, sB, mB;
-            q4k_scale_min_pair(h.y, h.z, h.w, k, sA, mA, sB, mB);
-            dl[i][mt][k] = d * (float)(hi ? sB : sA);
-            ml[i][mt][k] = dmin * (float)(hi ? mB : mA);
-          }
-        }
-    };
-    auto step = [&](int slot, int k) {
-#pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        float w[NM][16];
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) {
-          const uint32_t qw[4] = {q[slot][i][mt].x, q[slot][i][mt].y, q[slot][i][mt].z, q[slot][i][mt].w};
-          const float dk = dl[i][mt][k], mk = ml[i][mt][k];
-#pragma unroll
-          for (int c = 0; c < 16; ++c) {
-            const uint32_t byte = (qw[c >> 2] >> (8 * (c & 3))) & 0xffu;
-            const uint32_t nib = hi ? (byte >> 4) : (byte & 0xfu);
-            const float tq = dk * (float)nib;
-            w[mt][c] = tq - mk;
-          }
-        }
-        // consecutive MFMAs alternate between independent accumulators
-#pragma unroll
-        for (int m = 0; m < 16; ++m)
-#pragma unroll
-          for (int t = 0; t < TT; ++t) {
-            const float4 xq = xv[slot][t][m >> 2];
-            const float b = (m & 3) == 0 ? xq.x : ((m & 3) == 1 ? xq.y : ((m & 3) == 2 ? xq.z : xq.w));
-#pragma unroll
-            for (int mt = 0; mt < NM; ++mt)
-              acc[i][mt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[mt][m], b, acc[i][mt][t], 0, 0, 0);
-          }
-      }
-    };
-    // superblock loop: steps (k = 0, 1) from slots 0, 1, refilled with k = 2, 3,
-    // then those; the next superblock's heads load during its predecessor
-    load_heads(0);
-    load(0, 0);
-    load(1, 1);
-    int bl = 0;
-    for (; bl + 1 < nbw; ++bl) {
-      const int j = 4 * bl;
-      scales();
-      load_heads(bl + 1);
-      step(0, 0);
-      load(j + 2, 0);
-      step(1, 1);
-      load(j + 3, 1);
-      step(0, 2);
-      load(j + 4, 0);
-      step(1, 3);
-      load(j + 5, 1);
+        for (int u = 0; u < 4; ++u) xv[q][t][u] = *(const float4 *)(xrow[t] + 256 * b + 4 * u);
     }
-    // the last superblock: no loads after its quarters 2 and 3
-    scales();
-    step(0, 0);
-    load(4 * bl + 2, 0);
-    step(1, 1);
-    load(4 * bl + 3, 1);
-    step(0, 2);
-    step(1, 3);
-  }
-  // partial sums of waves 1..3 to LDS; wave 0 adds them in wave order
-  if (wave > 0) {
+    const int64_t b = b0 + kg < nb ? b0 + kg : nb - 1;
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
+    for (int mt = 0; mt < NM; ++mt) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wq[mt][k] = *(const uint2 *)(Wr[mt] + tq4_qs_off(nb, b, k, g >> 1) + 8 * (g & 1));
+      hd[mt] = *(const u32x4v *)(Wr[mt] + 16 * b);
+    }
+  };
+  f32x4 acc[NM][TT];
+#pragma unroll
+  for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[mt][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  load_round(0);
+  for (int64_t b0 = 0; b0 < nb; b0 += KW) {
+    // x of the round's superblocks -> three bf16 planes each and the sub-block sums
+#pragma unroll
+    for (int q = 0; q < KW; ++q)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const float v[16] = {xv[q][t][0].x, xv[q][t][0].y, xv[q][t][0].z, xv[q][t][0].w,
+                             xv[q][t][1].x, xv[q][t][1].y, xv[q][t][1].z, xv[q][t][1].w,
+                             xv[q][t][2].x, xv[q][t][2].y, xv[q][t][2].z, xv[q][t][2].w,
+                             xv[q][t][3].x, xv[q][t][3].y, xv[q][t][3].z, xv[q][t][3].w};
+        uint32_t p1[8], p2[8], p3[8];
+        float hs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          uint32_t u1[2], u2[2], u3[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float x = v[i + h];
+            const uint32_t b1 = __float_as_uint(x) & 0xffff0000u;
+            const float r1 = x - __uint_as_float(b1);
+            const uint32_t b2 = __float_as_uint(r1) & 0xffff0000u;
+            const float r2 = r1 - __uint_as_float(b2);
+            u1[h] = b1;
+            u2[h] = b2;
+            u3[h] = __float_as_uint(r2);
+            hs = hs + x;
+          }
+          p1[i / 2] = bf16_pair(u1[0], u1[1]);
+          p2[i / 2] = bf16_pair(u2[0], u2[1]);
+          p3[i / 2] = bf16_pair(u3[0], u3[1]);
+        }
+        const float ss = hs + __shfl_xor(hs, 1);  // the two halves of sub-block sc16 / 2, low half first
+        const int row = 16 * t + stok;
+        uint32_t *d1 = (uint32_t *)&xp[q][0][row][16 * sc16], *d2 = (uint32_t *)&xp[q][1][row][16 * sc16],
+                 *d3 = (uint32_t *)&xp[q][2][row][16 * sc16];
+#pragma unroll
+        for (int c = 0; c < 8; c += 4) {
+          *(u32x4v *)(d1 + c) = u32x4v{p1[c], p1[c + 1], p1[c + 2], p1[c + 3]};
+          *(u32x4v *)(d2 + c) = u32x4v{p2[c], p2[c + 1], p2[c + 2], p2[c + 3]};
+          *(u32x4v *)(d3 + c) = u32x4v{p3[c], p3[c + 1], p3[c + 2], p3[c + 3]};
+        }
+        if ((sc16 & 1) == 0) xs[q][row][sc16 >> 1] = ss;
+      }
+    // the rows' A_j = d*sc_j and B_j = dmin*m_j (dequant_row's factors) of this wave's superblock
+    if (g == 0) {
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        const u32x4v h = hd[mt];
+        const float d = f16_bits_to_f32(h.x), dmin = f16_bits_to_f32(h.x >> 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          int sA, mA, sB, mB;
+          q4k_scale_min_pair(h.y, h.z, h.w, k, sA, mA, sB, mB);
+          ab[wave][mt][0][2 * k][r16] = d * (float)sA;
+          ab[wave][mt][1][2 * k][r16] = dmin * (float)mA;
+          ab[wave][mt][0][2 * k + 1][r16] = d * (float)sB;
+          ab[wave][mt][1][2 * k + 1][r16] = dmin * (float)mB;
+        }
+      }
+    }
+    uint2 wc[NM][4];
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wc[mt][k] = wq[mt][k];
+    const bool live = b0 + kg < nb;  // this wave has a superblock in the round
+    __syncthreads();
+    if (b0 + KW < nb) load_round(b0 + KW);
+    if (live) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bf16x8 aop[NM][2];  // sub-blocks 2k (low nibbles), 2k+1 (high)
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) {
+          uint32_t lo[4], hi[4];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {  // each nibble q, exact in bf16 (the high half of (float)q)
+            const uint32_t w = h ? wc[mt][k].y : wc[mt][k].x;
+            const uint32_t wl = w & 0x0f0f0f0fu, wh = (w >> 4) & 0x0f0f0f0fu;
+            lo[2 * h] = bf16_pair(__float_as_uint((float)(wl & 0xffu)), __float_as_uint((float)((wl >> 8) & 0xffu)));
+            lo[2 * h + 1] =
+                bf16_pair(__float_as_uint((float)((wl >> 16) & 0xffu)), __float_as_uint((float)(wl >> 24)));
+            hi[2 * h] = bf16_pair(__float_as_uint((float)(wh & 0xffu)), __float_as_uint((float)((wh >> 8) & 0xffu)));
+            hi[2 * h + 1] =
+                bf16_pair(__float_as_uint((float)((wh >> 16) & 0xffu)), __float_as_uint((float)(wh >> 24)));
+          }
+          aop[mt][0] = __builtin_bit_cast(bf16x8, u32x4v{lo[0], lo[1], lo[2], lo[3]});
+          aop[mt][1] = __builtin_bit_cast(bf16x8, u32x4v{hi[0], hi[1], hi[2], hi[3]});
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          if (t >= ntt) break;
+          const int tok = 16 * t + r16;
+#pragma unroll
+          for (int sbh = 0; sbh < 2; ++sbh) {
+            const int j = 2 * k + sbh, c0 = 32 * j + 8 * g;
+            const bf16x8 b1 = *(const bf16x8 *)&xp[kg][0][tok][c0];
+            const bf16x8 b2 = *(const bf16x8 *)&xp[kg][1][tok][c0];
+            const bf16x8 b3 = *(const bf16x8 *)&xp[kg][2][tok][c0];
+            const float sj = xs[kg][tok][j];
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+              f32x4 P = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+              P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], b1, P, 0, 0, 0);
+              P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], b2, P, 0, 0, 0);
+              P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], b3, P, 0, 0, 0);
+              const float4 A4 = *(const float4 *)&ab[wave][mt][0][j][4 * g];
+              const float4 B4 = *(const float4 *)&ab[wave][mt][1][j][4 * g];
+              const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, Bv[4] = {B4.x, B4.y, B4.z, B4.w};
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                float y = acc[mt][t][v];
+                y = __builtin_fmaf(Av[v], P[v], y);
+                y = __builtin_fmaf(-Bv[v], sj, y);
+                acc[mt][t][v] = y;
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the planes and factors are read before the next round overwrites them
+  }
+  if constexpr (KW > 1) {  // the tile's K groups in wave order, through LDS (the planes are free now)
+    f32x4 *red = (f32x4 *)&xp[0][0][0][0];  // [KW - 1][RT][NM][TT][64]
+    if (kg > 0) {
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
-        for (int t = 0; t < TT; ++t) red[wave - 1][(i * NM + mt) * TT + t][lane] = acc[i][mt][t];
+        for (int t = 0; t < TT; ++t) red[(((kg - 1) * RT + tile) * NM + mt) * TT * 64 + t * 64 + lane] = acc[mt][t];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int q = 1; q < KW; ++q)
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+          for (int t = 0; t < TT; ++t) acc[mt][t] += red[(((q - 1) * RT + tile) * NM + mt) * TT * 64 + t * 64 + lane];
+    }
   }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < 3; ++w)
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[i][mt][t] += red[w][(i * NM + mt) * TT + t][lane];
-  // lane l holds rows 4*(l/16) + v of each row tile, token 16t + l % 16
+  // lane l of the tile's first wave: rows rbase + 4g + v, token 16t + l % 16
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
     const int tk = 16 * t + r16;
-    if (tk >= n) continue;
+    if (kg != 0 || tk >= n) continue;
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t rw = r0 + 16 * i + 4 * g + v;
-        if (rw >= rows) continue;
-        if constexpr (MODE == 0) {  // SwiGLU: g / (1 + exp(-g)) * u
-          const float gv = acc[i][0][t][v], uv = acc[i][1][t][v];
-          const float den = 1.0f + expf_cr(-gv);
-          const float qv = gv / den;
-          a.out[(p0 + tk) * rows + rw] = qv * uv;
-        } else {
-          a.out[(p0 + tk) * rows + rw] = acc[i][0][t][v];
-        }
+    for (int v = 0; v < 4; ++v) {
+      const int64_t rw = rbase + 4 * g + v;
+      if (rw >= rows) continue;
+      if constexpr (MODE == 0) {  // SwiGLU: g / (1 + exp(-g)) * u
+        const float gv = acc[0][t][v], uv = acc[1][t][v];
+        const float den = 1.0f + expf_cr(-gv);
+        const float qv = gv / den;
+        a.out[(p0 + tk) * rows + rw] = qv * uv;
+      } else {
+        a.out[(p0 + tk) * rows + rw] = acc[0][t][v];
       }
+    }
   }
 }
 
@@ -263,22 +308,33 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   // 16-row work-groups keep every CU busy when a single expert is on this
   // path). Measured, Qwen3 shape at 16 tokens (768 rows): gate/up 35 -> 27 µs
   // with one row tile, the step 105 -> 100 µs.
-#define KMOE_F32R(M, T, R)                                                                                 \
-  KMOE_LAUNCH((k_f32_rows<M, T, R>), dim3((unsigned)((rows + 16 * R - 1) / (16 * R)), (unsigned)max_active), \
+  // superblock groups per work-group: experts of at most 4096 rows split the
+  // superblocks over pairs of waves (32-row work-groups, so that enough run),
+  // wider ones give each wave its own 16 rows over all superblocks (64-row
+  // work-groups); four groups would need more LDS than leaves two work-groups
+  // per CU
+  const int kw = rows <= 4096 ? 2 : 1;
+#define KMOE_F32R(M, T, W)                                                                                     \
+  KMOE_LAUNCH((k_f32x3_rows<M, T, W>), dim3((unsigned)((rows + 64 / W - 1) / (64 / W)), (unsigned)max_active), \
               dim3(256), 0, st, a)
+#define KMOE_F32RW(M, T)       \
+  do {                         \
+    if (kw == 2) KMOE_F32R(M, T, 2); \
+    else KMOE_F32R(M, T, 1);   \
+  } while (0)
   a.min_rows = min_rows;
   a.max_rows = max_rows < 16 ? max_rows : 16;
   if (a.min_rows <= a.max_rows) {
-    if (mode == 0 && rows > 4096) KMOE_F32R(0, 1, 2);
-    else if (mode == 0) KMOE_F32R(0, 1, 1);
-    else KMOE_F32R(1, 1, 1);
+    if (mode == 0) KMOE_F32RW(0, 1);
+    else KMOE_F32RW(1, 1);
   }
   if (max_rows > 16) {
     a.min_rows = min_rows > 17 ? min_rows : 17;
     a.max_rows = max_rows;
-    if (mode == 0) KMOE_F32R(0, 2, 1);
-    else KMOE_F32R(1, 2, 1);
+    if (mode == 0) KMOE_F32RW(0, 2);
+    else KMOE_F32RW(1, 2);
   }
+#undef KMOE_F32RW
 #undef KMOE_F32R
   return hipGetLastError();
 }
