@@ -70,6 +70,26 @@ def check(r, tol=TOL):
     return e
 
 
+@pytest.mark.parametrize("E,K,d,F,S", [(8, 2, 2048, 1024, 16), (8, 2, 2048, 6144, 32), (16, 4, 2048, 768, 24),
+                                       (8, 2, 4096, 1024, 8)])
+def test_f32_regime_few_rows_is_fp32_accurate(ctx, orc, E, K, d, F, S):
+    """The exact regime's experts (every one on the f32 path, at most 32 rows
+    each) run the few-rows kernels, whose products use the bf16 matrix cores
+    on q and a three-piece split of x: still fp32 accuracy against the
+    oracle's f32 dequant-and-multiply, far inside the 1e-3 layer bound;
+    gate/up with 1024 rows (two waves per row tile over the superblocks) and
+    6144 rows (one wave per row tile), 16 and 17-32 token rows."""
+    spec = LayerSpec(E, K, d, F, Q4_K, seed=E + F)
+    ctx.profile_enable(True)
+    try:
+        r = run_layer(ctx, orc, spec, S, 2, seed=S)
+        assert ctx.profile_read("moe_gate_up_f32_rows")[1] == 1
+        assert ctx.profile_read("moe_down_f32_rows")[1] == 1
+    finally:
+        ctx.profile_enable(False)
+    assert check(r) < 3e-6
+
+
 @pytest.mark.parametrize("regime", [0, 1, 2])
 def test_c1_q8_0_moe_16_tokens(ctx, orc, regime):
     """Config 1: hidden 1024, FFN 512, 8 experts, top-2, Q8_0 from N(0, 0.02),
