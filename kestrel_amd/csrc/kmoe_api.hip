@@ -1599,11 +1599,11 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
                                                     w.xs, w.h, small_rows + 1, gd));
     }
   }
-  // The f32 regime's experts (quant.rs:242-260): in batches of at most 32
-  // tokens they stream their tiled Q4_K rows once through the few-rows
-  // kernels, gate and up in one launch; larger batches take the staged GEMM.
+  // The f32 regime's experts (quant.rs:242-260): tiled Q4_K rows stream
+  // through the bf16-split kernels (blocks of up to 64 token rows), gate and
+  // up in one launch; other row types take the staged GEMM.
   const int f32_lo = regime == KMOE_REGIME_EXACT ? 1 : 4;
-  const int f32_hi = S <= 32 ? (int)S : 0;
+  const int f32_hi = (int)S;
   if (any_f32) {
     int f32_done = 0;  // experts with f32_lo..f32_done rows are done
     if (gt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && f32_hi >= f32_lo) {

@@ -39,8 +39,8 @@ __device__ __forceinline__ bool rows_f32_regime(int regime, int n) {
 // result is the f32 regime's within a few fp32 roundings (the reference's
 // own sum runs in another order too).
 //
-// Work-group: 16 * (4 / KW) weight rows of one expert by up to 16 * TT of
-// its token rows; wave w takes row tile w / KW and, of every KW consecutive
+// Work-group: 16 * (4 / KW) weight rows of one expert by a block of up to
+// 16 * TT of its token rows (blockIdx.z); wave w takes row tile w / KW and, of every KW consecutive
 // superblocks, the (w % KW)-th (KW = 1 for wide experts; narrow ones split the
 // superblocks over the waves so that enough work-groups run). Per round of KW
 // superblocks the 256 threads split the tokens' x into LDS (three bf16 planes
@@ -76,7 +76,10 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   const int64_t p0 = a.rt.offsets[e];
   const int n = (int)(a.rt.offsets[e + 1] - p0);
   if (n < a.min_rows || n > a.max_rows || !rows_f32_regime(a.regime, n)) return;
-  const int ntt = (n + 15) / 16;  // token tiles of this expert (<= TT)
+  const int tok0 = (int)blockIdx.z * 16 * TT;  // this work-group's block of the expert's token rows
+  if (tok0 >= n) return;
+  const int nbt = n - tok0 < 16 * TT ? n - tok0 : 16 * TT;
+  const int ntt = (nbt + 15) / 16;  // token tiles of the block (<= TT)
   const int64_t cols = a.cols, nb = cols / 256, rows = a.rows, row_bytes = nb * 144;
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t rbase = (int64_t)blockIdx.x * (16 * RT) + 16 * tile;
@@ -92,7 +95,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   const float *xrow[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
-    const int tk = 16 * t + stok < n ? 16 * t + stok : n - 1;
+    const int tk = tok0 + (16 * t + stok < nbt ? 16 * t + stok : nbt - 1);
     const int64_t src = MODE == 0 ? (int64_t)(a.rt.perm[p0 + tk] / (uint32_t)a.rt.topk) : p0 + tk;
     xrow[t] = a.x + src * cols + 16 * sc16;
   }
@@ -266,8 +269,8 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   // lane l of the tile's first wave: rows rbase + 4g + v, token 16t + l % 16
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
-    const int tk = 16 * t + r16;
-    if (kg != 0 || tk >= n) continue;
+    const int tk = tok0 + 16 * t + r16;
+    if (kg != 0 || 16 * t + r16 >= nbt) continue;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int64_t rw = rbase + 4 * g + v;
@@ -293,7 +296,7 @@ bool f32_rows_supported(int type, int64_t rows, int64_t cols) {
 hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, int min_rows, int max_rows,
                            const float *x, float *out) {
-  if (!f32_rows_supported(type, rows, cols) || max_rows > 32) return hipErrorNotSupported;
+  if (!f32_rows_supported(type, rows, cols)) return hipErrorNotSupported;
   if (rows == 0 || max_active == 0 || max_rows < min_rows) return hipSuccess;
   F32RowsArgs a{};
   a.tier = tier;
@@ -303,24 +306,21 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   a.x = x;
   a.out = out;
   a.regime = regime;
-  // row tiles per work-group: gate/up 2 for one token tile over wide FFNs
-  // (Mixtral's 14336 rows), else 1; down 1 (its rows are few and long:
-  // 16-row work-groups keep every CU busy when a single expert is on this
-  // path). Measured, Qwen3 shape at 16 tokens (768 rows): gate/up 35 -> 27 µs
-  // with one row tile, the step 105 -> 100 µs.
-  // superblock groups per work-group: experts of at most 4096 rows split the
-  // superblocks over pairs of waves (32-row work-groups, so that enough run),
-  // wider ones give each wave its own 16 rows over all superblocks (64-row
-  // work-groups); four groups would need more LDS than leaves two work-groups
-  // per CU
+  // Experts of 4-16 rows take one token tile, 17-32 two, more blocks of four.
+  // Superblock groups per work-group: parts of at most 4096 rows split the
+  // superblocks over pairs of waves for one or two token tiles (32-row
+  // work-groups, so that enough run); wider parts, and four token tiles,
+  // give each wave its own 16 rows over all superblocks (64-row work-groups;
+  // more groups would need more LDS than leaves one or two work-groups per CU).
   const int kw = rows <= 4096 ? 2 : 1;
-#define KMOE_F32R(M, T, W)                                                                                     \
-  KMOE_LAUNCH((k_f32x3_rows<M, T, W>), dim3((unsigned)((rows + 64 / W - 1) / (64 / W)), (unsigned)max_active), \
-              dim3(256), 0, st, a)
-#define KMOE_F32RW(M, T)       \
-  do {                         \
-    if (kw == 2) KMOE_F32R(M, T, 2); \
-    else KMOE_F32R(M, T, 1);   \
+#define KMOE_F32R(M, T, W, Z)                                                                                   \
+  KMOE_LAUNCH((k_f32x3_rows<M, T, W>),                                                                         \
+              dim3((unsigned)((rows + 64 / W - 1) / (64 / W)), (unsigned)max_active, (unsigned)(Z)), dim3(256), 0, \
+              st, a)
+#define KMOE_F32RW(M, T)                 \
+  do {                                   \
+    if (kw == 2) KMOE_F32R(M, T, 2, 1);  \
+    else KMOE_F32R(M, T, 1, 1);          \
   } while (0)
   a.min_rows = min_rows;
   a.max_rows = max_rows < 16 ? max_rows : 16;
@@ -328,11 +328,18 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
     if (mode == 0) KMOE_F32RW(0, 1);
     else KMOE_F32RW(1, 1);
   }
-  if (max_rows > 16) {
-    a.min_rows = min_rows > 17 ? min_rows : 17;
-    a.max_rows = max_rows;
+  a.min_rows = min_rows > 17 ? min_rows : 17;
+  a.max_rows = max_rows < 32 ? max_rows : 32;
+  if (a.min_rows <= a.max_rows) {
     if (mode == 0) KMOE_F32RW(0, 2);
     else KMOE_F32RW(1, 2);
+  }
+  a.min_rows = min_rows > 33 ? min_rows : 33;
+  a.max_rows = max_rows;
+  if (a.min_rows <= a.max_rows) {
+    const int z = (max_rows + 63) / 64;
+    if (mode == 0) KMOE_F32R(0, 4, 1, z);
+    else KMOE_F32R(1, 4, 1, z);
   }
 #undef KMOE_F32RW
 #undef KMOE_F32R
