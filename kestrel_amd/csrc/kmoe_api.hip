@@ -1608,7 +1608,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     int f32_done = 0;  // experts with f32_lo..f32_done rows are done
     if (gt == KMOE_Q4_K && L->tiled[0] && L->tiled[1] && f32_hi >= f32_lo) {
       const hipError_t e = timed(c, "moe_gate_up_f32_rows", [&]() {
-        return launch_f32_rows(st, 0, gt, tier, F, d, rt, regime, max_active, f32_lo, f32_hi, h, w.h);
+        return launch_f32_rows(st, 0, gt, tier, F, d, rt, regime, max_active, slots, f32_lo, f32_hi, h, w.h);
       });
       if (e == hipSuccess) f32_done = f32_hi;
       else if (e != hipErrorNotSupported) HIP_OK(c, e);
@@ -1657,7 +1657,7 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
     int f32_done = 0;
     if (dt == KMOE_Q4_K && L->tiled[2] && f32_hi >= f32_lo) {
       const hipError_t e = timed(c, "moe_down_f32_rows", [&]() {
-        return launch_f32_rows(st, 1, dt, tier, d, F, rt, regime, max_active, f32_lo, f32_hi, w.h, w.y);
+        return launch_f32_rows(st, 1, dt, tier, d, F, rt, regime, max_active, slots, f32_lo, f32_hi, w.h, w.y);
       });
       if (e == hipSuccess) f32_done = f32_hi;
       else if (e != hipErrorNotSupported) HIP_OK(c, e);

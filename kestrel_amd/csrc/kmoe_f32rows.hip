@@ -20,6 +20,7 @@ struct F32RowsArgs {
   float *out;          // gate/up: h [slots, rows]; down: y [slots, rows]
   int regime;
   int min_rows, max_rows;  // experts with min_rows..max_rows rows on the f32 path
+  int ranked;              // blockIdx.y ranks the experts in that range, not the whole active list
 };
 
 __device__ __forceinline__ bool rows_f32_regime(int regime, int n) {
@@ -70,9 +71,37 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tile = wave / KW, kg = wave % KW;
-  const int i_act = blockIdx.y;
-  if (i_act >= *a.rt.n_active) return;
-  const int e = a.rt.active[i_act];
+  // blockIdx.y indexes the active list, or (ranked) ranks the experts this
+  // launch takes (row count in min_rows..max_rows, f32 regime) in the list's
+  // order: every wave finds the same one with ballots over the list.
+  int e = -1;
+  if (!a.ranked) {  // the grid covers the whole active list
+    if ((int)blockIdx.y < *a.rt.n_active) e = a.rt.active[blockIdx.y];
+  } else {
+    const int na = *a.rt.n_active;
+    int want = (int)blockIdx.y;
+    for (int base = 0; base < na; base += 64) {
+      const int i = base + lane;
+      int ei = 0;
+      bool in = false;
+      if (i < na) {
+        ei = a.rt.active[i];
+        const int ni = (int)(a.rt.offsets[ei + 1] - a.rt.offsets[ei]);
+        in = ni >= a.min_rows && ni <= a.max_rows && rows_f32_regime(a.regime, ni);
+      }
+      const uint64_t m = __ballot(in);
+      const int cnt = __popcll(m);
+      if (want < cnt) {
+        const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        const bool hit = in && below == want;
+        const uint64_t hm = __ballot(hit);
+        e = __builtin_amdgcn_readlane(ei, (int)__builtin_ctzll(hm));
+        break;
+      }
+      want -= cnt;
+    }
+  }
+  if (e < 0) return;
   const int64_t p0 = a.rt.offsets[e];
   const int n = (int)(a.rt.offsets[e + 1] - p0);
   if (n < a.min_rows || n > a.max_rows || !rows_f32_regime(a.regime, n)) return;
@@ -294,8 +323,8 @@ bool f32_rows_supported(int type, int64_t rows, int64_t cols) {
 }
 
 hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
-                           const Routing &rt, int regime, int max_active, int min_rows, int max_rows,
-                           const float *x, float *out) {
+                           const Routing &rt, int regime, int max_active, int64_t n_slots, int min_rows,
+                           int max_rows, const float *x, float *out) {
   if (!f32_rows_supported(type, rows, cols)) return hipErrorNotSupported;
   if (rows == 0 || max_active == 0 || max_rows < min_rows) return hipSuccess;
   F32RowsArgs a{};
@@ -313,10 +342,20 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   // give each wave its own 16 rows over all superblocks (64-row work-groups;
   // more groups would need more LDS than leaves one or two work-groups per CU).
   const int kw = rows <= 4096 ? 2 : 1;
-#define KMOE_F32R(M, T, W, Z)                                                                                   \
-  KMOE_LAUNCH((k_f32x3_rows<M, T, W>),                                                                         \
-              dim3((unsigned)((rows + 64 / W - 1) / (64 / W)), (unsigned)max_active, (unsigned)(Z)), dim3(256), 0, \
-              st, a)
+  // At most n_slots / min_rows experts hold min_rows or more rows: when that
+  // is fewer than the active experts, the grid's y ranks the experts in range
+  // instead of covering the active list.
+  auto ny = [&]() -> unsigned {
+    const int64_t m = n_slots / (a.min_rows > 1 ? a.min_rows : 1);
+    a.ranked = m < max_active;
+    return (unsigned)(m < max_active ? m : max_active);
+  };
+#define KMOE_F32R(M, T, W, Z)                                                                                 \
+  do {                                                                                                         \
+    if (ny() > 0)                                                                                              \
+      KMOE_LAUNCH((k_f32x3_rows<M, T, W>), dim3((unsigned)((rows + 64 / W - 1) / (64 / W)), ny(), (unsigned)(Z)), \
+                  dim3(256), 0, st, a);                                                                        \
+  } while (0)
 #define KMOE_F32RW(M, T)                 \
   do {                                   \
     if (kw == 2) KMOE_F32R(M, T, 2, 1);  \

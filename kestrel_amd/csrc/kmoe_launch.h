@@ -246,14 +246,14 @@ hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &
                           const Routing &rt, int regime, int max_active, int64_t max_rows_per_expert,
                           int64_t n_slots, const float *x, float *out, float *part, int64_t part_floats,
                           int min_rows = 0);
-// The f32 regime for experts with min_rows..max_rows (at most 32) rows over
-// tiled Q4_K rows (kmoe_f32rows.hip): mode 0 gate/up + SwiGLU into out [slots,
-// rows], mode 1 down into out [slots, rows]. hipErrorNotSupported for other
-// weight types or max_rows > 32.
+// The f32 regime for experts with min_rows..max_rows rows over tiled Q4_K
+// rows (kmoe_f32rows.hip): mode 0 gate/up + SwiGLU into out [slots, rows],
+// mode 1 down into out [slots, rows]. n_slots (S*k) bounds how many experts
+// can hold a given number of rows. hipErrorNotSupported for other weight types.
 bool f32_rows_supported(int type, int64_t rows, int64_t cols);
 hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
-                           const Routing &rt, int regime, int max_active, int min_rows, int max_rows,
-                           const float *x, float *out);
+                           const Routing &rt, int regime, int max_active, int64_t n_slots, int min_rows,
+                           int max_rows, const float *x, float *out);
 
 // ---- routing (kmoe_route.hip)
 // logits [S, E] = router [E, d] . x [S, d] in the reference's summation order
