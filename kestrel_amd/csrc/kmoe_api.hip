@@ -1445,7 +1445,11 @@ static int moe_ffn(kmoe_ctx *c, uint32_t layer, const float *h, int64_t S, float
       rc = run_norm();
       if (rc) return rc;
       select_in_gate_up = false;
-      LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits));
+      // the int8 rows of x come from extra work-groups of the router launch
+      const int qkind = regime == KMOE_REGIME_EXACT ? 0 : is_kq(gt) ? 1 : 2;
+      LAUNCH(c, "router_logits", launch_router_logits(st, L->router, (int32_t)E, d, h, S, w.logits, false, qkind,
+                                                      w.xq, w.xd, w.xs));
+      x_quantized = qkind != 0;
       LAUNCH(c, "route_topk", launch_route_topk(st, w.logits, S, (int32_t)E, (int32_t)k, D.norm_topk,
                                                 D.weights_scale, w.idx, w.wsel));
       LAUNCH(c, "dispatch", launch_dispatch(st, w.idx, slots, (int32_t)E, w.perm, w.offsets, w.inv, w.n_active,

@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   const int tok0 = (int)blockIdx.z * 16 * TT;  // this work-group's block of the expert's token rows
   if (tok0 >= n) return;
   const int nbt = n - tok0 < 16 * TT ? n - tok0 : 16 * TT;
-  const int ntt = (nbt + 15) / 16;  // token tiles of the block (<= TT)
+  const int ntt = (nbt + 15) / 16;  // token tiles of the block (<= TT; every tile is full below four)
   const int64_t cols = a.cols, nb = cols / 256, rows = a.rows, row_bytes = nb * 144;
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t rbase = (int64_t)blockIdx.x * (16 * RT) + 16 * tile;
@@ -119,6 +119,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
     const int64_t r = rbase + r16 < rows ? rbase + r16 : rows - 1;
     Wr[mt] = E + a.tier.off[MODE == 0 ? mt : 2] + r * row_bytes;
   }
+  const uint8_t *Wh = Wr[NM == 2 ? g >> 1 : 0];
   // the split: thread tid takes token tid / 16 (+16t) and columns 16*(tid % 16) .. +15 of each of the round's superblocks
   const int stok = tid >> 4, sc16 = tid & 15;
   const float *xrow[TT];
@@ -130,7 +131,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   }
   float4 xv[KW][TT][4];
   uint2 wq[NM][4];  // this wave's superblock: nibble bytes of the 4 quarters
-  u32x4v hd[NM];    // and its head (lanes with g == 0 use it)
+  u32x4v hd;        // and the head of this lane's row of matrix g / 2 (gate/up) or of down
   auto load_round = [&](int64_t b0) {
 #pragma unroll
     for (int q = 0; q < KW; ++q) {
@@ -145,8 +146,8 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
     for (int mt = 0; mt < NM; ++mt) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) wq[mt][k] = *(const uint2 *)(Wr[mt] + tq4_qs_off(nb, b, k, g >> 1) + 8 * (g & 1));
-      hd[mt] = *(const u32x4v *)(Wr[mt] + 16 * b);
     }
+    hd = *(const u32x4v *)(Wh + 16 * b);
   };
   f32x4 acc[NM][TT];
 #pragma unroll
@@ -197,21 +198,22 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
         }
         if ((sc16 & 1) == 0) xs[q][row][sc16 >> 1] = ss;
       }
-    // the rows' A_j = d*sc_j and B_j = dmin*m_j (dequant_row's factors) of this wave's superblock
-    if (g == 0) {
+    // the rows' A_j = d*sc_j and B_j = dmin*m_j (dequant_row's factors) of this wave's superblock:
+    // lane (row l % 16, group g) takes matrix g / 2 and quarters 2(g % 2), +1 of gate/up,
+    // quarter g of down
+    {
+      const u32x4v h = hd;
+      const int mt = NM == 2 ? g >> 1 : 0;
+      const float d = f16_bits_to_f32(h.x), dmin = f16_bits_to_f32(h.x >> 16);
 #pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        const u32x4v h = hd[mt];
-        const float d = f16_bits_to_f32(h.x), dmin = f16_bits_to_f32(h.x >> 16);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          int sA, mA, sB, mB;
-          q4k_scale_min_pair(h.y, h.z, h.w, k, sA, mA, sB, mB);
-          ab[wave][mt][0][2 * k][r16] = d * (float)sA;
-          ab[wave][mt][1][2 * k][r16] = dmin * (float)mA;
-          ab[wave][mt][0][2 * k + 1][r16] = d * (float)sB;
-          ab[wave][mt][1][2 * k + 1][r16] = dmin * (float)mB;
-        }
+      for (int kk = 0; kk < NM; ++kk) {
+        const int k = NM == 2 ? 2 * (g & 1) + kk : g;
+        int sA, mA, sB, mB;
+        q4k_scale_min_pair(h.y, h.z, h.w, k, sA, mA, sB, mB);
+        ab[wave][mt][0][2 * k][r16] = d * (float)sA;
+        ab[wave][mt][1][2 * k][r16] = dmin * (float)mA;
+        ab[wave][mt][0][2 * k + 1][r16] = d * (float)sB;
+        ab[wave][mt][1][2 * k + 1][r16] = dmin * (float)mB;
       }
     }
     uint2 wc[NM][4];
@@ -232,7 +234,10 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
 #pragma unroll
           for (int h = 0; h < 2; ++h) {  // each nibble q, exact in bf16 (the high half of (float)q)
             const uint32_t w = h ? wc[mt][k].y : wc[mt][k].x;
-            const uint32_t wl = w & 0x0f0f0f0fu, wh = (w >> 4) & 0x0f0f0f0fu;
+            uint32_t wl = w & 0x0f0f0f0fu, wh = (w >> 4) & 0x0f0f0f0fu;
+            // opaque, so each byte converts with one v_cvt_f32_ubyteN rather than a
+            // nibble extract and a conversion
+            asm("" : "+v"(wl), "+v"(wh));
             lo[2 * h] = bf16_pair(__float_as_uint((float)(wl & 0xffu)), __float_as_uint((float)((wl >> 8) & 0xffu)));
             lo[2 * h + 1] =
                 bf16_pair(__float_as_uint((float)((wl >> 16) & 0xffu)), __float_as_uint((float)(wl >> 24)));
@@ -245,7 +250,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
         }
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
-          if (t >= ntt) break;
+          if (TT > 2 && t >= ntt) break;  // with one or two tiles the phase stays one block
           const int tok = 16 * t + r16;
 #pragma unroll
           for (int sbh = 0; sbh < 2; ++sbh) {
@@ -341,7 +346,7 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   // work-groups, so that enough run); wider parts, and four token tiles,
   // give each wave its own 16 rows over all superblocks (64-row work-groups;
   // more groups would need more LDS than leaves one or two work-groups per CU).
-  const int kw = rows <= 4096 ? 2 : 1;
+  const int kw = rows <= 4096 && cols > 1024 ? 2 : 1;
   // At most n_slots / min_rows experts hold min_rows or more rows: when that
   // is fewer than the active experts, the grid's y ranks the experts in range
   // instead of covering the active list.

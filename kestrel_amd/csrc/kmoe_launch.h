@@ -258,8 +258,11 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
 // ---- routing (kmoe_route.hip)
 // logits [S, E] = router [E, d] . x [S, d] in the reference's summation order
 // for s_rows (quant::matmul), or always in quant::dot order when qdot is set.
+// qkind 1 / 2: the same launch also writes x's Q8_K / Q8 rows (xq, xd, xs as
+// launch_quant_q8k / launch_quant_q8 write them).
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
-                                int64_t s_rows, float *logits, bool qdot = false);
+                                int64_t s_rows, float *logits, bool qdot = false, int qkind = 0,
+                                int8_t *xq = nullptr, float *xd = nullptr, int32_t *xs = nullptr);
 hipError_t launch_route_topk(hipStream_t st, const float *logits, int64_t s_rows, int32_t n_expert, int32_t k,
                              int32_t norm_topk, float weights_scale, uint32_t *idx, float *w);
 // Decode routing (s_rows < 4): quant::dot-order logits (one work-group per

@@ -40,12 +40,28 @@ __device__ __forceinline__ float hsum8(const float *v) {
 // whole group of 8 (or 16) read global memory. Decode batches (S <= 8) take
 // one row and two tokens (many small work-groups); larger batches take 4 x 4
 // tiles, so a row is staged once per 4 tokens and a token once per 4 rows.
+// Work-groups from nlog on quantize the activation rows for the int8 path
+// instead (qkind 1: Q8_K, one wave per 256-block; 2: Q8, eight lanes per
+// 32-block), with k_quant_q8k's / k_quant_q8's arithmetic.
 template <int TE, int TT, int CH>
 __global__ void __launch_bounds__(256) k_router_logits(const float *__restrict__ W, int32_t E, int64_t d,
                                                        const float *__restrict__ X, int64_t S,
-                                                       float *__restrict__ logits, int qdot) {
+                                                       float *__restrict__ logits, int qdot, int32_t nlog, int qkind,
+                                                       int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                       int32_t *__restrict__ xs) {
   __shared__ __attribute__((aligned(16))) float Wc[TE][CH];
   __shared__ __attribute__((aligned(16))) float Xc[TT][CH];
+  if ((int32_t)blockIdx.x >= nlog) {  // no block barriers on this path
+    const int lane = threadIdx.x & 63;
+    const int64_t u = (int64_t)(blockIdx.x - nlog) * 4 + (threadIdx.x >> 6);
+    if (qkind == 1) {
+      if (u < S * (d / 256)) wave_quant_q8k_block(X + u * 256, xq + u * 256, xd + u, xs + u * 16, lane);
+    } else {
+      const int64_t blk = u * 8 + (lane >> 3);
+      if (blk < S * (d / 32)) group8_quant_q8_block(X + blk * 32, xq + blk * 32, xd + blk, xs + blk * 2, lane & 7);
+    }
+    return;
+  }
   const bool vec = d % 4 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
   const int tid = threadIdx.x;
   const int l16 = tid & 15, pair = tid >> 4;
@@ -697,18 +713,23 @@ __global__ void __launch_bounds__(256) k_route_dec(RouteDecArgs a) {
 }  // namespace
 
 hipError_t launch_router_logits(hipStream_t st, const float *router, int32_t n_expert, int64_t d, const float *x,
-                                int64_t s_rows, float *logits, bool qdot) {
+                                int64_t s_rows, float *logits, bool qdot, int qkind, int8_t *xq, float *xd,
+                                int32_t *xs) {
   if (s_rows * n_expert == 0) return hipSuccess;
+  int64_t qblocks = 0;  // work-groups of 4 waves for the int8 rows of x
+  if (qkind == 1) qblocks = (s_rows * (d / 256) + 3) / 4;
+  else if (qkind == 2) qblocks = ((s_rows * (d / 32) + 7) / 8 + 3) / 4;
   if (s_rows <= 8) {
     const int64_t blocks = (s_rows + 1) / 2 * n_expert;
-    KMOE_LAUNCH((k_router_logits<1, 2, 4096>), dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x,
-                s_rows, logits, qdot ? 1 : 0);
+    if (blocks + qblocks > (int64_t)INT32_MAX) return hipErrorInvalidValue;
+    KMOE_LAUNCH((k_router_logits<1, 2, 4096>), dim3((unsigned)(blocks + qblocks)), dim3(256), 0, st, router,
+                n_expert, d, x, s_rows, logits, qdot ? 1 : 0, (int32_t)blocks, qkind, xq, xd, xs);
     return hipGetLastError();
   }
   const int64_t blocks = (s_rows + 3) / 4 * ((n_expert + 3) / 4);
-  if (blocks > (int64_t)INT32_MAX) return hipErrorInvalidValue;
-  KMOE_LAUNCH((k_router_logits<4, 4, 1024>), dim3((unsigned)blocks), dim3(256), 0, st, router, n_expert, d, x, s_rows,
-              logits, qdot ? 1 : 0);
+  if (blocks + qblocks > (int64_t)INT32_MAX) return hipErrorInvalidValue;
+  KMOE_LAUNCH((k_router_logits<4, 4, 1024>), dim3((unsigned)(blocks + qblocks)), dim3(256), 0, st, router, n_expert,
+              d, x, s_rows, logits, qdot ? 1 : 0, (int32_t)blocks, qkind, xq, xd, xs);
   return hipGetLastError();
 }
 
