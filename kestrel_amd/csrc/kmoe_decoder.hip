@@ -715,21 +715,37 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ l, in
   __shared__ int64_t bi[16];
   float v = -INFINITY;
   int64_t idx = -1;
-  constexpr int U = 8;  // values loaded per thread before any is compared
-  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 1024 * U) {
-    float xs[U];
+  // each thread scans its values in ascending index order and keeps the first
+  // largest: 16-byte pieces j = tid + 1024u (values 4j..4j+3), U4 pieces
+  // loaded before any is compared, then the values past the last whole piece
+  constexpr int U4 = 16;
+  const int64_t n4 = (((uintptr_t)l & 15) == 0) ? n / 4 : 0;
+  for (int64_t j0 = threadIdx.x; j0 < n4; j0 += 1024 * U4) {
+    float4 xs[U4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + (int64_t)u * 1024;
-      xs[u] = i < n ? l[i] : __builtin_nanf("");
+    for (int u = 0; u < U4; ++u) {
+      const int64_t j = j0 + (int64_t)u * 1024;
+      const float q = __builtin_nanf("");
+      xs[u] = j < n4 ? ((const float4 *)l)[j] : make_float4(q, q, q, q);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {  // strided scan: ascending i, first max kept
-      const float x = xs[u];
-      if (!isnan(x) && (idx < 0 || x > v)) {
-        v = x;
-        idx = i0 + (int64_t)u * 1024;
+    for (int u = 0; u < U4; ++u) {
+      const float xv[4] = {xs[u].x, xs[u].y, xs[u].z, xs[u].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float x = xv[c];
+        if (!isnan(x) && (idx < 0 || x > v)) {
+          v = x;
+          idx = 4 * (j0 + (int64_t)u * 1024) + c;
+        }
       }
+    }
+  }
+  for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += 1024) {
+    const float x = l[i];
+    if (!isnan(x) && (idx < 0 || x > v)) {
+      v = x;
+      idx = i;
     }
   }
   // wave reduction: larger value wins, equal values keep the smaller index

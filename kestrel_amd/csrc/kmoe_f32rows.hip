@@ -224,30 +224,83 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
     const bool live = b0 + kg < nb;  // this wave has a superblock in the round
     __syncthreads();
     if (b0 + KW < nb) load_round(b0 + KW);
-    if (live) {
+    // quarter k's nibbles as the A operands: sub-blocks 2k (low nibbles), 2k+1 (high)
+    auto a_ops = [&](int k, bf16x8 (&aop)[NM][2]) {
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // each nibble q, exact in bf16 (the high half of (float)q)
+          const uint32_t w = h ? wc[mt][k].y : wc[mt][k].x;
+          uint32_t wl = w & 0x0f0f0f0fu, wh = (w >> 4) & 0x0f0f0f0fu;
+          // opaque, so each byte converts with one v_cvt_f32_ubyteN rather than a
+          // nibble extract and a conversion
+          asm("" : "+v"(wl), "+v"(wh));
+          lo[2 * h] = bf16_pair(__float_as_uint((float)(wl & 0xffu)), __float_as_uint((float)((wl >> 8) & 0xffu)));
+          lo[2 * h + 1] = bf16_pair(__float_as_uint((float)((wl >> 16) & 0xffu)), __float_as_uint((float)(wl >> 24)));
+          hi[2 * h] = bf16_pair(__float_as_uint((float)(wh & 0xffu)), __float_as_uint((float)((wh >> 8) & 0xffu)));
+          hi[2 * h + 1] = bf16_pair(__float_as_uint((float)((wh >> 16) & 0xffu)), __float_as_uint((float)(wh >> 24)));
+        }
+        aop[mt][0] = __builtin_bit_cast(bf16x8, u32x4v{lo[0], lo[1], lo[2], lo[3]});
+        aop[mt][1] = __builtin_bit_cast(bf16x8, u32x4v{hi[0], hi[1], hi[2], hi[3]});
+      }
+    };
+    if (live && TT == 1) {
+      // One token tile: quarter k + 1's LDS operands are read while quarter k
+      // multiplies (two sets), the sub-block sums once per round.
+      struct QOps {
+        bf16x8 b[2][3];    // x pieces of sub-blocks 2k, 2k+1
+        float4 A[NM][2], B[NM][2];  // rows 4g..4g+3's factors
+      };
+      auto ld = [&](int k, QOps &o) {
+#pragma unroll
+        for (int sbh = 0; sbh < 2; ++sbh) {
+          const int j = 2 * k + sbh, c0 = 32 * j + 8 * g;
+#pragma unroll
+          for (int pc = 0; pc < 3; ++pc) o.b[sbh][pc] = *(const bf16x8 *)&xp[kg][pc][r16][c0];
+#pragma unroll
+          for (int mt = 0; mt < NM; ++mt) {
+            o.A[mt][sbh] = *(const float4 *)&ab[wave][mt][0][j][4 * g];
+            o.B[mt][sbh] = *(const float4 *)&ab[wave][mt][1][j][4 * g];
+          }
+        }
+      };
+      const float4 s_lo = *(const float4 *)&xs[kg][r16][0], s_hi = *(const float4 *)&xs[kg][r16][4];
+      const float sjv[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+      QOps o[2];
+      ld(0, o[0]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        bf16x8 aop[NM][2];  // sub-blocks 2k (low nibbles), 2k+1 (high)
+        if (k < 3) ld(k + 1, o[(k + 1) & 1]);
+        bf16x8 aop[NM][2];
+        a_ops(k, aop);
+        const QOps &c = o[k & 1];
 #pragma unroll
-        for (int mt = 0; mt < NM; ++mt) {
-          uint32_t lo[4], hi[4];
+        for (int sbh = 0; sbh < 2; ++sbh) {
+          const float sj = sjv[2 * k + sbh];
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {  // each nibble q, exact in bf16 (the high half of (float)q)
-            const uint32_t w = h ? wc[mt][k].y : wc[mt][k].x;
-            uint32_t wl = w & 0x0f0f0f0fu, wh = (w >> 4) & 0x0f0f0f0fu;
-            // opaque, so each byte converts with one v_cvt_f32_ubyteN rather than a
-            // nibble extract and a conversion
-            asm("" : "+v"(wl), "+v"(wh));
-            lo[2 * h] = bf16_pair(__float_as_uint((float)(wl & 0xffu)), __float_as_uint((float)((wl >> 8) & 0xffu)));
-            lo[2 * h + 1] =
-                bf16_pair(__float_as_uint((float)((wl >> 16) & 0xffu)), __float_as_uint((float)(wl >> 24)));
-            hi[2 * h] = bf16_pair(__float_as_uint((float)(wh & 0xffu)), __float_as_uint((float)((wh >> 8) & 0xffu)));
-            hi[2 * h + 1] =
-                bf16_pair(__float_as_uint((float)((wh >> 16) & 0xffu)), __float_as_uint((float)(wh >> 24)));
+          for (int mt = 0; mt < NM; ++mt) {
+            f32x4 P = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], c.b[sbh][0], P, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], c.b[sbh][1], P, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt][sbh], c.b[sbh][2], P, 0, 0, 0);
+            const float Av[4] = {c.A[mt][sbh].x, c.A[mt][sbh].y, c.A[mt][sbh].z, c.A[mt][sbh].w};
+            const float Bv[4] = {c.B[mt][sbh].x, c.B[mt][sbh].y, c.B[mt][sbh].z, c.B[mt][sbh].w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              float y = acc[mt][0][v];
+              y = __builtin_fmaf(Av[v], P[v], y);
+              y = __builtin_fmaf(-Bv[v], sj, y);
+              acc[mt][0][v] = y;
+            }
           }
-          aop[mt][0] = __builtin_bit_cast(bf16x8, u32x4v{lo[0], lo[1], lo[2], lo[3]});
-          aop[mt][1] = __builtin_bit_cast(bf16x8, u32x4v{hi[0], hi[1], hi[2], hi[3]});
         }
+      }
+    } else if (live) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bf16x8 aop[NM][2];
+        a_ops(k, aop);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
           if (TT > 2 && t >= ntt) break;  // with one or two tiles the phase stays one block

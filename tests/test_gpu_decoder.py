@@ -269,6 +269,21 @@ def test_swiglu_add_rows_argmax(ctx, orc):
               np.array([np.nan, 1, 2], np.float32), rng.standard_normal(151936).astype(np.float32),
               np.full(70000, -1.0, np.float32)):
         assert int(host(ctx.argmax(dev(l)))[0]) == orc.argmax(l)
+    # the vocabulary's length and ragged ones: the largest value in the last
+    # whole 16-byte piece, in the values past it, tied across threads, NaN first
+    for n, at in ((102400, 102399), (102403, 102402), (102403, 102399), (70001, 3), (5, 4)):
+        l = rng.standard_normal(n).astype(np.float32)
+        l[at] = 9.0
+        assert int(host(ctx.argmax(dev(l)))[0]) == orc.argmax(l) == at
+    l = rng.standard_normal(102400).astype(np.float32)
+    l[[4097, 60000, 4096 * 3 + 1]] = 7.0
+    l[0] = np.nan
+    assert int(host(ctx.argmax(dev(l)))[0]) == orc.argmax(l) == 0
+    l[0] = 0.0
+    assert int(host(ctx.argmax(dev(l)))[0]) == orc.argmax(l) == 4097
+    # an unaligned start (a row of a larger buffer)
+    big = dev(rng.standard_normal(1 + 102400).astype(np.float32))
+    assert int(host(ctx.argmax(big[1:]))[0]) == orc.argmax(host(big[1:]))
 
 
 MODELS = {
