@@ -194,7 +194,7 @@ def cpu_baseline(ctx, torch, seconds: float, threads: int):
 
 # Kernel names the library's timing mode reports (kmoe_profile_read).
 PROFILE_NAMES = ("add_rows", "argmax", "attention", "attention_q8", "block_sums_q4k", "block_sums_q4k_mfma",
-                 "block_sums_q6k", "block_sums_q8_0", "combine", "dequant_x", "dispatch", "gemm_f32", "get_rows",
+                 "block_sums_q6k", "block_sums_q8_0", "combine", "dequant_x", "dispatch", "f32_rows_plain", "gemm_f32", "get_rows",
                  "kv_store", "matmul_f32_ordered", "matvec_q4k", "matvec_q4k_mfma", "matvec_q6k", "matvec_q8_0",
                  "matvec_qkv_rope", "matvec_unpacked", "moe_down_dec", "moe_down_f32", "moe_down_f32_rows", "moe_down_few",
                  "moe_down_int", "moe_down_shared", "moe_gate_up_few",

@@ -539,6 +539,15 @@ int matmul_core(kmoe_ctx *c, int t, const uint8_t *w, int64_t rows, int64_t cols
     return KMOE_OK;
   }
   if (!int_path(c->regime, s_rows)) {
+    // Q4_K rows: the bf16-split kernel (exact products on the bf16 matrix
+    // cores); other types, or unaligned buffers, the fp32 GEMM
+    if (t == KMOE_Q4_K) {
+      const hipError_t e = timed(c, "f32_rows_plain", [&]() {
+        return launch_f32_rows_plain(c->stream, t, w, rows, cols, x, s_rows, out);
+      });
+      if (e == hipSuccess) return KMOE_OK;
+      if (e != hipErrorNotSupported) HIP_OK(c, e);
+    }
     LAUNCH(c, "gemm_f32", launch_matmul_f32(c->stream, t, w, rows, cols, x, s_rows, out, qr.part, qr.part_floats));
     return KMOE_OK;
   }

@@ -21,6 +21,8 @@ struct F32RowsArgs {
   int regime;
   int min_rows, max_rows;  // experts with min_rows..max_rows rows on the f32 path
   int ranked;              // blockIdx.y ranks the experts in that range, not the whole active list
+  const uint8_t *pw;       // plain mode: GGUF rows [rows, cols] (16-byte aligned)
+  int64_t s_rows;          // plain mode: activation rows of x
 };
 
 __device__ __forceinline__ bool rows_f32_regime(int regime, int n) {
@@ -61,8 +63,12 @@ constexpr int kX3Pad = 264;           // bf16 per token row of a plane in LDS (2
 // Pairs of f32 whose low 16 bits are zero, as one dword of two bf16 (first low).
 __device__ __forceinline__ uint32_t bf16_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
+// MODE 0: grouped gate/up + SwiGLU, 1: grouped down (the expert tier's tiled
+// rows, routed token slots); 2: plain GGUF rows against s_rows activation rows
+// (quant::matmul's f32 regime, quant.rs:242-260).
 template <int MODE, int TT, int KW>
 __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32RowsArgs a) {
+  constexpr bool PLAIN = MODE == 2;
   constexpr int NM = MODE == 0 ? 2 : 1;
   constexpr int RT = 4 / KW;  // row tiles per work-group
   __shared__ __attribute__((aligned(16))) uint16_t xp[KW][3][TT * 16][kX3Pad];  // x pieces by token, column
@@ -75,7 +81,9 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   // launch takes (row count in min_rows..max_rows, f32 regime) in the list's
   // order: every wave finds the same one with ballots over the list.
   int e = -1;
-  if (!a.ranked) {  // the grid covers the whole active list
+  if (PLAIN) {
+    e = 0;
+  } else if (!a.ranked) {  // the grid covers the whole active list
     if ((int)blockIdx.y < *a.rt.n_active) e = a.rt.active[blockIdx.y];
   } else {
     const int na = *a.rt.n_active;
@@ -102,9 +110,9 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
     }
   }
   if (e < 0) return;
-  const int64_t p0 = a.rt.offsets[e];
-  const int n = (int)(a.rt.offsets[e + 1] - p0);
-  if (n < a.min_rows || n > a.max_rows || !rows_f32_regime(a.regime, n)) return;
+  const int64_t p0 = PLAIN ? 0 : a.rt.offsets[e];
+  const int n = PLAIN ? (int)a.s_rows : (int)(a.rt.offsets[e + 1] - p0);
+  if (!PLAIN && (n < a.min_rows || n > a.max_rows || !rows_f32_regime(a.regime, n))) return;
   const int tok0 = (int)blockIdx.z * 16 * TT;  // this work-group's block of the expert's token rows
   if (tok0 >= n) return;
   const int nbt = n - tok0 < 16 * TT ? n - tok0 : 16 * TT;
@@ -112,12 +120,12 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
   const int64_t cols = a.cols, nb = cols / 256, rows = a.rows, row_bytes = nb * 144;
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t rbase = (int64_t)blockIdx.x * (16 * RT) + 16 * tile;
-  const uint8_t *E = a.tier.base + (int64_t)e * a.tier.stride;
+  const uint8_t *E = PLAIN ? a.pw : a.tier.base + (int64_t)e * a.tier.stride;
   const uint8_t *Wr[NM];  // this lane's A-operand row
 #pragma unroll
   for (int mt = 0; mt < NM; ++mt) {
     const int64_t r = rbase + r16 < rows ? rbase + r16 : rows - 1;
-    Wr[mt] = E + a.tier.off[MODE == 0 ? mt : 2] + r * row_bytes;
+    Wr[mt] = E + (PLAIN ? 0 : a.tier.off[MODE == 0 ? mt : 2]) + r * row_bytes;
   }
   const uint8_t *Wh = Wr[NM == 2 ? g >> 1 : 0];
   // the split: thread tid takes token tid / 16 (+16t) and columns 16*(tid % 16) .. +15 of each of the round's superblocks
@@ -145,9 +153,11 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) wq[mt][k] = *(const uint2 *)(Wr[mt] + tq4_qs_off(nb, b, k, g >> 1) + 8 * (g & 1));
+      for (int k = 0; k < 4; ++k)  // bytes 8g .. 8g+7 of quarter k's 32 (GGUF: at 16 + 32k in the superblock)
+        wq[mt][k] = *(const uint2 *)(Wr[mt] + (PLAIN ? 144 * b + 16 + 32 * k + 8 * g
+                                                     : tq4_qs_off(nb, b, k, g >> 1) + 8 * (g & 1)));
     }
-    hd = *(const u32x4v *)(Wh + 16 * b);
+    hd = *(const u32x4v *)(Wh + (PLAIN ? 144 * b : 16 * b));
   };
   f32x4 acc[NM][TT];
 #pragma unroll
@@ -440,6 +450,39 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   }
 #undef KMOE_F32RW
 #undef KMOE_F32R
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                 const float *x, int64_t s_rows, float *out) {
+  if (!f32_rows_supported(type, rows, cols) || ((uintptr_t)w & 15u) || ((uintptr_t)x & 15u))
+    return hipErrorNotSupported;
+  if (s_rows <= 0) return hipSuccess;
+  F32RowsArgs a{};
+  a.rows = rows;
+  a.cols = cols;
+  a.x = x;
+  a.out = out;
+  a.pw = w;
+  a.s_rows = s_rows;
+  const int kw = rows <= 4096 && cols > 1024 ? 2 : 1;
+  const int64_t gx2 = (rows + 31) / 32, gx1 = (rows + 63) / 64;
+  // token blocks of 64, 32 or 16 rows: the largest that still gives at least
+  // two work-groups per CU (smaller blocks re-read the weights, from L2)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t z4 = (s_rows + 63) / 64, z2 = (s_rows + 31) / 32, z1 = (s_rows + 15) / 16;
+  const int64_t gx = kw == 2 ? gx2 : gx1;
+  if (z1 > 65535 || gx1 * 2 > (int64_t)UINT32_MAX) return hipErrorNotSupported;
+  if (s_rows > 32 && gx1 * z4 >= 2LL * cus) {
+    KMOE_LAUNCH((k_f32x3_rows<2, 4, 1>), dim3((unsigned)gx1, 1, (unsigned)z4), dim3(256), 0, st, a);
+  } else if (s_rows > 16 && gx * z2 >= 2LL * cus) {
+    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<2, 2, 2>), dim3((unsigned)gx2, 1, (unsigned)z2), dim3(256), 0, st, a);
+    else KMOE_LAUNCH((k_f32x3_rows<2, 2, 1>), dim3((unsigned)gx1, 1, (unsigned)z2), dim3(256), 0, st, a);
+  } else {
+    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<2, 1, 2>), dim3((unsigned)gx2, 1, (unsigned)z1), dim3(256), 0, st, a);
+    else KMOE_LAUNCH((k_f32x3_rows<2, 1, 1>), dim3((unsigned)gx1, 1, (unsigned)z1), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -251,6 +251,11 @@ hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &
 // mode 1 down into out [slots, rows]. n_slots (S*k) bounds how many experts
 // can hold a given number of rows. hipErrorNotSupported for other weight types.
 bool f32_rows_supported(int type, int64_t rows, int64_t cols);
+// The same kernel over plain GGUF Q4_K rows w [rows, cols] (16-byte aligned)
+// and x [s_rows, cols] (16-byte aligned): out [s_rows, rows], the f32 regime of
+// quant::matmul. hipErrorNotSupported for other types or alignments.
+hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                 const float *x, int64_t s_rows, float *out);
 hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, int64_t n_slots, int min_rows,
                            int max_rows, const float *x, float *out);
