@@ -196,6 +196,30 @@ def test_matmul_regimes_match_oracle(ctx, orc, t, S, regime):
     assert rel_l2(out, ref) < TOL, (S, regime, rel_l2(out, ref))
 
 
+@pytest.mark.parametrize("rows,cols,S,regime", [(2816, 2048, 128, 0), (300, 2048, 40, 0), (192, 1024, 70, 0),
+                                                (64, 4096, 33, 2), (100, 512, 5, 0), (77, 768, 2, 2)])
+def test_matmul_f32_regime_q4k_plain_rows(ctx, orc, rows, cols, S, regime):
+    """quant::matmul's f32 regime on GGUF Q4_K rows (the bf16-split kernel:
+    token blocks of 64, 32 and 16 rows, one and two K groups, ragged last
+    blocks): within a few fp32 roundings of the oracle's dequantize-and-multiply,
+    and the same through an unaligned activation buffer (the fp32 GEMM)."""
+    import torch
+
+    w = random_blocks(Q4_K, rows, cols, seed=rows * 7 + cols)
+    x = orc.normal(rows + S, S * cols).reshape(S, cols)
+    ctx.set_regime(regime)
+    try:
+        out = host(ctx.matmul(Q4_K, dev(w), rows, cols, dev(x)))
+        xb = torch.zeros(S * cols + 1, dtype=torch.float32, device="cuda")
+        xb[1:].copy_(torch.from_numpy(x.ravel()))
+        out_u = host(ctx.matmul(Q4_K, dev(w), rows, cols, xb[1:].view(S, cols)))
+    finally:
+        ctx.set_regime(0)
+    ref = orc.matmul(Q4_K, w, rows, cols, x, regime)
+    assert rel_l2(out, ref) < 3e-6, rel_l2(out, ref)
+    assert rel_l2(out_u, ref) < 3e-6, rel_l2(out_u, ref)
+
+
 @pytest.mark.parametrize("t,rows,cols,S,regime", [(Q4_K, 512, 4096, 1, 0), (Q4_K, 300, 2048, 5, 0),
                                                  (Q6_K, 64, 1024, 3, 0), (Q8_0, 100, 1024, 9, 1),
                                                  (Q4_K, 64, 1024, 12, 1), (F32, 8, 1024, 2, 0)])
