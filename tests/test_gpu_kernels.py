@@ -196,26 +196,31 @@ def test_matmul_regimes_match_oracle(ctx, orc, t, S, regime):
     assert rel_l2(out, ref) < TOL, (S, regime, rel_l2(out, ref))
 
 
-@pytest.mark.parametrize("rows,cols,S,regime", [(2816, 2048, 128, 0), (300, 2048, 40, 0), (192, 1024, 70, 0),
-                                                (64, 4096, 33, 2), (100, 512, 5, 0), (77, 768, 2, 2)])
-def test_matmul_f32_regime_q4k_plain_rows(ctx, orc, rows, cols, S, regime):
-    """quant::matmul's f32 regime on GGUF Q4_K rows (the bf16-split kernel:
-    token blocks of 64, 32 and 16 rows, one and two K groups, ragged last
-    blocks): within a few fp32 roundings of the oracle's dequantize-and-multiply,
-    and the same through an unaligned activation buffer (the fp32 GEMM)."""
+@pytest.mark.parametrize("t,rows,cols,S,regime", [(Q4_K, 2816, 2048, 128, 0), (Q4_K, 300, 2048, 40, 0),
+                                                  (Q4_K, 192, 1024, 70, 0), (Q4_K, 64, 4096, 33, 2),
+                                                  (Q4_K, 100, 512, 5, 0), (Q4_K, 77, 768, 2, 2),
+                                                  (Q8_0, 2048, 1408, 128, 0), (Q8_0, 300, 1088, 40, 0),
+                                                  (Q8_0, 64, 512, 5, 2), (Q8_0, 33, 4096, 20, 0)])
+def test_matmul_f32_regime_plain_rows(ctx, orc, t, rows, cols, S, regime):
+    """quant::matmul's f32 regime on GGUF rows: Q4_K through the bf16-split
+    kernel (token blocks of 64, 32 and 16 rows, one and two K groups, ragged
+    last blocks), Q8_0 through the fp32 GEMM (rows ending inside a 256-column
+    span included): within a few fp32 roundings of the oracle's
+    dequantize-and-multiply, and the same through an unaligned activation
+    buffer (the fp32 GEMM)."""
     import torch
 
-    w = random_blocks(Q4_K, rows, cols, seed=rows * 7 + cols)
+    w = random_blocks(t, rows, cols, seed=rows * 7 + cols)
     x = orc.normal(rows + S, S * cols).reshape(S, cols)
     ctx.set_regime(regime)
     try:
-        out = host(ctx.matmul(Q4_K, dev(w), rows, cols, dev(x)))
+        out = host(ctx.matmul(t, dev(w), rows, cols, dev(x)))
         xb = torch.zeros(S * cols + 1, dtype=torch.float32, device="cuda")
         xb[1:].copy_(torch.from_numpy(x.ravel()))
-        out_u = host(ctx.matmul(Q4_K, dev(w), rows, cols, xb[1:].view(S, cols)))
+        out_u = host(ctx.matmul(t, dev(w), rows, cols, xb[1:].view(S, cols)))
     finally:
         ctx.set_regime(0)
-    ref = orc.matmul(Q4_K, w, rows, cols, x, regime)
+    ref = orc.matmul(t, w, rows, cols, x, regime)
     assert rel_l2(out, ref) < 3e-6, rel_l2(out, ref)
     assert rel_l2(out_u, ref) < 3e-6, rel_l2(out_u, ref)
 
