@@ -201,7 +201,7 @@ PROFILE_NAMES = ("add_rows", "argmax", "attention", "attention_q8", "block_sums_
                  "moe_down_mfma", "moe_down_small", "moe_gate_f32", "moe_gate_up_dec", "moe_gate_up_f32_rows", "moe_gate_up_int",
                  "moe_gate_up_mfma", "moe_gate_up_small", "moe_up_f32", "pos_advance", "quant_q8", "quant_q8k",
                  "quant_slots_q8", "quant_slots_q8k", "quant_slots_shared", "rmsnorm", "rmsnorm_quant", "rope", "rope_kv",
-                 "route_decode", "route_topk", "router_logits", "shared_add", "shared_down_add", "shared_gate",
+                 "route_decode", "route_topk", "router_logits", "shared_add", "shared_down_add", "shared_gate", "shared_gate_up_f32",
                  "shared_swiglu", "shared_swiglu_quant", "swiglu")
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s

@@ -1728,10 +1728,20 @@ done:
       }
       goto shared_done;
     }
-    rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
-    if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
-    if (rc) return rc;
-    LAUNCH(c, "shared_swiglu", launch_swiglu(st, gs, us, S * Fs));
+    // f32 regime, Q4_K gate and up: both products and SwiGLU in one launch
+    hipError_t ef = hipErrorNotSupported;
+    if (!int_path(c->regime, S) && SH.type[0] == KMOE_Q4_K && SH.type[1] == KMOE_Q4_K)
+      ef = timed(c, "shared_gate_up_f32", [&]() {
+        return launch_f32_rows_plain(st, KMOE_Q4_K, SH.arena + SH.off[0], Fs, d, h, S, gs, SH.arena + SH.off[1]);
+      });
+    if (ef != hipErrorNotSupported) {
+      HIP_OK(c, ef);
+    } else {
+      rc = matmul_core(c, SH.type[0], SH.arena + SH.off[0], Fs, d, h, S, gs, qr);
+      if (!rc) rc = matmul_core(c, SH.type[1], SH.arena + SH.off[1], Fs, d, h, S, us, qr);
+      if (rc) return rc;
+      LAUNCH(c, "shared_swiglu", launch_swiglu(st, gs, us, S * Fs));
+    }
     rc = matmul_core(c, SH.type[2], SH.arena + SH.off[2], d, Fs, gs, S, ys, qr);
     if (rc) return rc;
     if (SH.gate_ok) LAUNCH(c, "shared_gate", launch_router_logits(st, SH.gate_inp, 1, d, h, S, gl, true));

@@ -21,7 +21,8 @@ struct F32RowsArgs {
   int regime;
   int min_rows, max_rows;  // experts with min_rows..max_rows rows on the f32 path
   int ranked;              // blockIdx.y ranks the experts in that range, not the whole active list
-  const uint8_t *pw;       // plain mode: GGUF rows [rows, cols] (16-byte aligned)
+  const uint8_t *pw;       // plain modes: GGUF rows [rows, cols] (16-byte aligned); mode 3: the gate rows
+  const uint8_t *pw2;      // mode 3: the up rows
   int64_t s_rows;          // plain mode: activation rows of x
 };
 
@@ -65,11 +66,12 @@ __device__ __forceinline__ uint32_t bf16_pair(uint32_t a, uint32_t b) { return _
 
 // MODE 0: grouped gate/up + SwiGLU, 1: grouped down (the expert tier's tiled
 // rows, routed token slots); 2: plain GGUF rows against s_rows activation rows
-// (quant::matmul's f32 regime, quant.rs:242-260).
+// (quant::matmul's f32 regime, quant.rs:242-260); 3: two plain GGUF matrices
+// (gate, up) and SwiGLU (a shared expert's front, transformer.rs:572-587).
 template <int MODE, int TT, int KW>
 __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32RowsArgs a) {
-  constexpr bool PLAIN = MODE == 2;
-  constexpr int NM = MODE == 0 ? 2 : 1;
+  constexpr bool PLAIN = MODE >= 2;
+  constexpr int NM = MODE == 0 || MODE == 3 ? 2 : 1;
   constexpr int RT = 4 / KW;  // row tiles per work-group
   __shared__ __attribute__((aligned(16))) uint16_t xp[KW][3][TT * 16][kX3Pad];  // x pieces by token, column
   __shared__ float xs[KW][TT * 16][8];                                          // sub-block sums of x by token
@@ -125,7 +127,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
 #pragma unroll
   for (int mt = 0; mt < NM; ++mt) {
     const int64_t r = rbase + r16 < rows ? rbase + r16 : rows - 1;
-    Wr[mt] = E + (PLAIN ? 0 : a.tier.off[MODE == 0 ? mt : 2]) + r * row_bytes;
+    Wr[mt] = (PLAIN && mt == 1 ? a.pw2 : E) + (PLAIN ? 0 : a.tier.off[MODE == 0 ? mt : 2]) + r * row_bytes;
   }
   const uint8_t *Wh = Wr[NM == 2 ? g >> 1 : 0];
   // the split: thread tid takes token tid / 16 (+16t) and columns 16*(tid % 16) .. +15 of each of the round's superblocks
@@ -372,7 +374,7 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
     for (int v = 0; v < 4; ++v) {
       const int64_t rw = rbase + 4 * g + v;
       if (rw >= rows) continue;
-      if constexpr (MODE == 0) {  // SwiGLU: g / (1 + exp(-g)) * u
+      if constexpr (NM == 2) {  // SwiGLU: g / (1 + exp(-g)) * u
         const float gv = acc[0][t][v], uv = acc[1][t][v];
         const float den = 1.0f + expf_cr(-gv);
         const float qv = gv / den;
@@ -453,18 +455,10 @@ hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier 
   return hipGetLastError();
 }
 
-hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
-                                 const float *x, int64_t s_rows, float *out) {
-  if (!f32_rows_supported(type, rows, cols) || ((uintptr_t)w & 15u) || ((uintptr_t)x & 15u))
-    return hipErrorNotSupported;
-  if (s_rows <= 0) return hipSuccess;
-  F32RowsArgs a{};
-  a.rows = rows;
-  a.cols = cols;
-  a.x = x;
-  a.out = out;
-  a.pw = w;
-  a.s_rows = s_rows;
+namespace {
+
+template <int M>
+hipError_t launch_plain_t(hipStream_t st, const F32RowsArgs &a, int64_t rows, int64_t cols, int64_t s_rows) {
   const int kw = rows <= 4096 && cols > 1024 ? 2 : 1;
   const int64_t gx2 = (rows + 31) / 32, gx1 = (rows + 63) / 64;
   // token blocks of 64, 32 or 16 rows: the largest that still gives at least
@@ -475,15 +469,35 @@ hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int
   const int64_t gx = kw == 2 ? gx2 : gx1;
   if (z1 > 65535 || gx1 * 2 > (int64_t)UINT32_MAX) return hipErrorNotSupported;
   if (s_rows > 32 && gx1 * z4 >= 2LL * cus) {
-    KMOE_LAUNCH((k_f32x3_rows<2, 4, 1>), dim3((unsigned)gx1, 1, (unsigned)z4), dim3(256), 0, st, a);
+    KMOE_LAUNCH((k_f32x3_rows<M, 4, 1>), dim3((unsigned)gx1, 1, (unsigned)z4), dim3(256), 0, st, a);
   } else if (s_rows > 16 && gx * z2 >= 2LL * cus) {
-    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<2, 2, 2>), dim3((unsigned)gx2, 1, (unsigned)z2), dim3(256), 0, st, a);
-    else KMOE_LAUNCH((k_f32x3_rows<2, 2, 1>), dim3((unsigned)gx1, 1, (unsigned)z2), dim3(256), 0, st, a);
+    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<M, 2, 2>), dim3((unsigned)gx2, 1, (unsigned)z2), dim3(256), 0, st, a);
+    else KMOE_LAUNCH((k_f32x3_rows<M, 2, 1>), dim3((unsigned)gx1, 1, (unsigned)z2), dim3(256), 0, st, a);
   } else {
-    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<2, 1, 2>), dim3((unsigned)gx2, 1, (unsigned)z1), dim3(256), 0, st, a);
-    else KMOE_LAUNCH((k_f32x3_rows<2, 1, 1>), dim3((unsigned)gx1, 1, (unsigned)z1), dim3(256), 0, st, a);
+    if (kw == 2) KMOE_LAUNCH((k_f32x3_rows<M, 1, 2>), dim3((unsigned)gx2, 1, (unsigned)z1), dim3(256), 0, st, a);
+    else KMOE_LAUNCH((k_f32x3_rows<M, 1, 1>), dim3((unsigned)gx1, 1, (unsigned)z1), dim3(256), 0, st, a);
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
+                                 const float *x, int64_t s_rows, float *out, const uint8_t *w_up) {
+  if (!f32_rows_supported(type, rows, cols) || ((uintptr_t)w & 15u) || ((uintptr_t)x & 15u) ||
+      ((uintptr_t)w_up & 15u))
+    return hipErrorNotSupported;
+  if (s_rows <= 0) return hipSuccess;
+  F32RowsArgs a{};
+  a.rows = rows;
+  a.cols = cols;
+  a.x = x;
+  a.out = out;
+  a.pw = w;
+  a.pw2 = w_up;
+  a.s_rows = s_rows;
+  if (w_up) return launch_plain_t<3>(st, a, rows, cols, s_rows);
+  return launch_plain_t<2>(st, a, rows, cols, s_rows);
 }
 
 }  // namespace kmoe

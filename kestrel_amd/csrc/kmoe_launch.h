@@ -253,9 +253,10 @@ hipError_t launch_moe_f32(hipStream_t st, int mode, int type, const ExpertTier &
 bool f32_rows_supported(int type, int64_t rows, int64_t cols);
 // The same kernel over plain GGUF Q4_K rows w [rows, cols] (16-byte aligned)
 // and x [s_rows, cols] (16-byte aligned): out [s_rows, rows], the f32 regime of
-// quant::matmul. hipErrorNotSupported for other types or alignments.
+// quant::matmul. With w_up (the same shape), w is the gate and out receives
+// SwiGLU(w . x, w_up . x). hipErrorNotSupported for other types or alignments.
 hipError_t launch_f32_rows_plain(hipStream_t st, int type, const uint8_t *w, int64_t rows, int64_t cols,
-                                 const float *x, int64_t s_rows, float *out);
+                                 const float *x, int64_t s_rows, float *out, const uint8_t *w_up = nullptr);
 hipError_t launch_f32_rows(hipStream_t st, int mode, int type, const ExpertTier &tier, int64_t rows, int64_t cols,
                            const Routing &rt, int regime, int max_active, int64_t n_slots, int min_rows,
                            int max_rows, const float *x, float *out);
