@@ -257,9 +257,12 @@ __global__ void __launch_bounds__(256, TT * KW > 2 ? 1 : 2) k_f32x3_rows(F32Rows
         aop[mt][1] = __builtin_bit_cast(bf16x8, u32x4v{hi[0], hi[1], hi[2], hi[3]});
       }
     };
-    if (live && TT == 1) {
-      // One token tile: quarter k + 1's LDS operands are read while quarter k
-      // multiplies (two sets), the sub-block sums once per round.
+    if (live && TT == 1 && KW == 2) {
+      // One token tile, two K groups: quarter k + 1's LDS operands are read
+      // while quarter k multiplies (two sets), the sub-block sums once per
+      // round. With one K group the second set would cost the kernel its four
+      // waves per SIMD (120 registers -> 183), which the 64-row work-groups
+      // need when many run.
       struct QOps {
         bf16x8 b[2][3];    // x pieces of sub-blocks 2k, 2k+1
         float4 A[NM][2], B[NM][2];  // rows 4g..4g+3's factors
