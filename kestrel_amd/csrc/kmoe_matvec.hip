@@ -1756,11 +1756,13 @@ hipError_t launch_matvec_qkv_rope(hipStream_t st, int type, const uint8_t *w, in
 // int path, in the active list's order (at most 256 experts). Slots past the
 // expert's rows repeat its last (loads unconditional, results dropped).
 // DBG: the per-block integers are added into a.dbg as the other int kernels do.
+// NR row groups per wave and item: the weights of NR rows are in flight
+// together, dotted with the one set of activation slices.
 constexpr int kFewMaxExperts = 256;
-template <int TYPE, int LPR, int NT, int MODE, bool DBG>
+template <int TYPE, int LPR, int NT, int MODE, bool DBG, int NR = 1>
 __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
   constexpr int RPW = 64 / LPR;
-  constexpr int RB = 4 * RPW;
+  constexpr int RB = 4 * RPW * NR;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row_in_wave = lane / LPR, lr = lane % LPR;
   const int64_t cols = a.cols, rows = a.rows;
@@ -1802,8 +1804,6 @@ __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
     const int e = qe[i];
     const int64_t p0 = a.rt.offsets[e];
     const int n = (int)(a.rt.offsets[e + 1] - (uint32_t)p0);
-    const int64_t r = rblk * RB + (int64_t)wave * RPW + row_in_wave;
-    const int64_t rc = r < rows ? r : rows - 1;
     ActSlice<TYPE> act[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -1812,9 +1812,18 @@ __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
       act_load<TYPE>(act[j], a.xq + src * cols, a.xd + src * nblk, a.xbs + src * xs_stride, t);
     }
     const uint8_t *eb = a.tier.base + (int64_t)e * a.tier.stride;
-    WTask<TYPE, true> w0, w1;
-    w_load<TYPE, true>(w0, eb + a.tier.off[MODE == 0 ? 0 : 2] + rc * row_bytes, t, nblk);
-    if constexpr (MODE == 0) w_load<TYPE, true>(w1, eb + a.tier.off[1] + rc * row_bytes, t, nblk);
+    WTask<TYPE, true> w0s[NR], w1s[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const int64_t r = rblk * RB + ((int64_t)wave * NR + q) * RPW + row_in_wave;
+      const int64_t rc = r < rows ? r : rows - 1;
+      w_load<TYPE, true>(w0s[q], eb + a.tier.off[MODE == 0 ? 0 : 2] + rc * row_bytes, t, nblk);
+      if constexpr (MODE == 0) w_load<TYPE, true>(w1s[q], eb + a.tier.off[1] + rc * row_bytes, t, nblk);
+    }
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+    const int64_t r = rblk * RB + ((int64_t)wave * NR + q) * RPW + row_in_wave;
+    const WTask<TYPE, true> &w0 = w0s[q], &w1 = w1s[q];
     float g[NT], u[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -1848,26 +1857,45 @@ __global__ void __launch_bounds__(256) k_few_int(MvArgs a) {
         }
       }
     }
+    }
   }
 }
+
+constexpr int kFewNR = 2;  // row groups per wave and item of k_few_int
 
 template <int TYPE, int MODE>
 static hipError_t launch_few_int_t(hipStream_t st, const MvArgs &a, int lpr, int max_active, bool dbg) {
   const int rpw = 64 / lpr;
-  const int64_t bpe = (a.rows + 4 * rpw - 1) / (4 * rpw);
+  const int64_t bpe = (a.rows + 4 * rpw * kFewNR - 1) / (4 * rpw * kFewNR);
   const int64_t items = (int64_t)max_active * bpe;
-  const int64_t cap = (int64_t)cu_count() * kGridMult;
-  const unsigned grid = (unsigned)(items < cap ? items : cap);
-#define KMOE_FEW(L)                                                                              \
-  do {                                                                                           \
-    if (dbg) KMOE_LAUNCH((k_few_int<TYPE, L, 3, MODE, true>), dim3(grid), dim3(256), 0, st, a);  \
-    else KMOE_LAUNCH((k_few_int<TYPE, L, 3, MODE, false>), dim3(grid), dim3(256), 0, st, a);     \
-    return hipGetLastError();                                                                    \
+  // as many work-groups per CU as are resident at once (the kernel's
+  // registers decide: 3 for the Q4_K gate/up, 4 or more for the others)
+  auto grid_for = [&](const void *k, int &occ) -> unsigned {
+    if (occ == 0) {
+      int o = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, k, 256, 0) != hipSuccess || o < 1) o = kGridMult;
+      occ = o < 8 ? o : 8;
+    }
+    const int64_t cap = (int64_t)cu_count() * occ;
+    return (unsigned)(items < cap ? items : cap);
+  };
+#define KMOE_FEW_D(L, DB)                                                                               \
+  do {                                                                                                  \
+    static int occ = 0;                                                                                 \
+    const unsigned grid = grid_for((const void *)k_few_int<TYPE, L, 3, MODE, DB, kFewNR>, occ);         \
+    KMOE_LAUNCH((k_few_int<TYPE, L, 3, MODE, DB, kFewNR>), dim3(grid), dim3(256), 0, st, a);            \
+  } while (0)
+#define KMOE_FEW(L)                  \
+  do {                               \
+    if (dbg) KMOE_FEW_D(L, true);    \
+    else KMOE_FEW_D(L, false);       \
+    return hipGetLastError();        \
   } while (0)
   if (lpr == 16) KMOE_FEW(16);
   if (lpr == 32) KMOE_FEW(32);
   if (lpr == 64) KMOE_FEW(64);
 #undef KMOE_FEW
+#undef KMOE_FEW_D
   return hipErrorNotSupported;
 }
 
