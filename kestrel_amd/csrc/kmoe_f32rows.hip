@@ -1,8 +1,10 @@
 // kmoe_f32rows.hip — the reference's f32 regime (quant.rs:242-260: weights
-// dequantized to f32, multiplied with f32 activations; avx2.rs:230-308) for
-// experts that hold a few token rows (decode batches), over the expert tier's
-// tiled Q4_K rows, streamed once: gate and up in one launch (SwiGLU,
-// transformer.rs:558, in the epilogue), down in another.
+// dequantized to f32, multiplied with f32 activations; avx2.rs:230-308) on
+// Q4_K rows: the expert tier's tiled rows of the experts in the regime
+// (blocks of up to 64 token rows per expert, each weight streamed once per
+// block; gate and up in one launch with SwiGLU, transformer.rs:558, in the
+// epilogue, down in another), and plain GGUF rows for quant::matmul itself and
+// a shared expert's gate/up.
 #include "kmoe_device.h"
 #include "kmoe_launch.h"
 
@@ -43,10 +45,11 @@ __device__ __forceinline__ bool rows_f32_regime(int regime, int n) {
 // result is the f32 regime's within a few fp32 roundings (the reference's
 // own sum runs in another order too).
 //
-// Work-group: 16 * (4 / KW) weight rows of one expert by a block of up to
-// 16 * TT of its token rows (blockIdx.z); wave w takes row tile w / KW and, of every KW consecutive
-// superblocks, the (w % KW)-th (KW = 1 for wide experts; narrow ones split the
-// superblocks over the waves so that enough work-groups run). Per round of KW
+// Work-group: 16 * (4 / KW) weight rows of one expert (or of the plain
+// matrix) by a block of up to 16 * TT of its token rows (blockIdx.z); wave w
+// takes row tile w / KW and, of every KW consecutive superblocks, the
+// (w % KW)-th (KW = 1 for wide parts; narrow ones split the superblocks over
+// the waves so that enough work-groups run). Per round of KW
 // superblocks the 256 threads split the tokens' x into LDS (three bf16 planes
 // per superblock, and the sub-block sums), each wave turns its rows' heads
 // into A_j, B_j in LDS, and for every quarter k a lane converts its 8 nibble
