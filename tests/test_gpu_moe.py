@@ -827,3 +827,61 @@ def test_norm_moe_ffn_matches_rmsnorm_then_moe(ctx, orc, wtype, d, ff, S, regime
     finally:
         ctx.set_regime(0)
         ctx.layer_destroy(lid)
+
+
+@pytest.mark.parametrize("shape", ["qwen3_small", "c5_small"])
+def test_decode_batches_graph_replays_equal_eager(ctx, orc, shape):
+    """Decode batches captured in one HIP graph: the router launch with its
+    quantizing work-groups, top-k, dispatch, the few-rows int kernels, the
+    f32 kernels (ranked grids, one, two and four token tiles; the shared
+    expert's plain-row gate/up) and the combine, at 6, 16, 24 and 40 tokens in
+    the AVX2 and int8 regimes. Every replay, with eager calls and
+    synchronizations between replays, equals the eager result bit for bit."""
+    import torch
+
+    sh = None
+    if shape == "qwen3_small":  # narrow rows (the few-rows int kernels), Zipf skew
+        spec = LayerSpec(32, 8, 2048, 768, Q4_K, seed=11, quantized=False, zipf=1.1)
+    else:  # 64 experts top-6, Q8_0 down, an ungated shared FFN (Q4_K gate/up, Q6_K down)
+        spec, sh = c5_spec()
+    lid = _layer_id[0]
+    _layer_id[0] += 1
+    spec.upload(ctx, lid)
+    try:
+        if sh is not None:
+            ctx.shared_expert(lid, C5_SHARED_FF, (Q4_K, Q4_K, Q6_K), sh[0], sh[1], sh[2], None)
+        for regime in (0, 1):
+            ctx.set_regime(regime)
+            xs = [torch.from_numpy(orc.normal(900 + S + 7 * regime, S * spec.d, 1.0, 1.0).reshape(S, spec.d)).cuda()
+                  for S in (6, 16, 24, 40)]
+            outs = [torch.empty_like(x) for x in xs]
+            eager = []
+            for x, o in zip(xs, outs):
+                ctx.moe_ffn(lid, x, o)
+                eager.append(o.clone())
+            torch.cuda.synchronize()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                ctx.set_stream(s)
+                with torch.cuda.graph(g, stream=s):
+                    for x, o in zip(xs, outs):
+                        ctx.moe_ffn(lid, x, o)
+            torch.cuda.current_stream().wait_stream(s)
+            ctx.set_stream(torch.cuda.current_stream())
+            for rep in range(3):
+                for o in outs:
+                    o.zero_()
+                g.replay()
+                torch.cuda.synchronize()
+                for i, (o, e) in enumerate(zip(outs, eager)):
+                    assert torch.equal(o, e), (shape, regime, rep, i)
+                # eager work between replays
+                ctx.moe_ffn(lid, xs[1], torch.empty_like(xs[1]))
+                torch.cuda.synchronize()
+            del g
+    finally:
+        ctx.set_regime(0)
+        ctx.set_stream(torch.cuda.current_stream())
+        ctx.layer_destroy(lid)
