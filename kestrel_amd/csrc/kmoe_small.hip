@@ -135,8 +135,15 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
   }
   const int kq = lane & 3;
 
-  for (int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU; r0 < rows; r0 += (int64_t)a.groups * 4 * RU) {
+  // One task per lane: two register sets, the next step's rows load while
+  // this step's are multiplied. Every load is unconditional (steps past the
+  // last row reload the last row, never stored), so the compiler's wait
+  // counts stay exact. Two tasks per lane keep one set (two would not leave
+  // two waves per SIMD).
+  struct WSet {
     u32x4 hg[RU][TPL], ag[RU][TPL], bg[RU][TPL], hu[RU][TPL], au[RU][TPL], bu[RU][TPL];
+  };
+  auto load = [&](int64_t r0, WSet &w) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int64_t r = r0 + u < rows ? r0 + u : rows - 1;
@@ -144,14 +151,16 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
       const uint8_t *ur = U + r * row_bytes;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
-        hg[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + oh[t]));
-        ag[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + oa[t]));
-        bg[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + ob[t]));
-        hu[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + oh[t]));
-        au[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + oa[t]));
-        bu[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + ob[t]));
+        w.hg[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + oh[t]));
+        w.ag[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + oa[t]));
+        w.bg[u][t] = __builtin_nontemporal_load((const u32x4 *)(gr + ob[t]));
+        w.hu[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + oh[t]));
+        w.au[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + oa[t]));
+        w.bu[u][t] = __builtin_nontemporal_load((const u32x4 *)(ur + ob[t]));
       }
     }
+  };
+  auto step = [&](int64_t r0, const WSet &w) {
     float gsum = 0.0f, usum = 0.0f;  // lane u*NT + j: row r0+u, token j
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
@@ -160,8 +169,8 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
       for (int j = 0; j < NT; ++j) gacc[j] = uacc[j] = 0.0f;
 #pragma unroll
       for (int t = 0; t < TPL; ++t) {
-        const TaskW wg = unpack_task(hg[u][t], ag[u][t], bg[u][t], kq);
-        const TaskW wu = unpack_task(hu[u][t], au[u][t], bu[u][t], kq);
+        const TaskW wg = unpack_task(w.hg[u][t], w.ag[u][t], w.bg[u][t], kq);
+        const TaskW wu = unpack_task(w.hu[u][t], w.au[u][t], w.bu[u][t], kq);
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
           if (j < n) {  // uniform: the expert's row count
@@ -194,6 +203,27 @@ __global__ void __launch_bounds__(256) k_small_gate_up(SmallArgs a) {
       const float den = 1.0f + expf_cr(-gsum);
       const float q = gsum / den;
       a.out[(p0 + j) * rows + r0 + u] = q * usum;
+    }
+  };
+  const int64_t stride = (int64_t)a.groups * 4 * RU;
+  int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RU;
+  if constexpr (TPL == 1) {
+    WSet w0, w1;
+    load(r0, w0);
+    while (r0 < rows) {
+      load(r0 + stride, w1);
+      step(r0, w0);
+      r0 += stride;
+      if (r0 >= rows) break;
+      load(r0 + stride, w0);
+      step(r0, w1);
+      r0 += stride;
+    }
+  } else {
+    for (; r0 < rows; r0 += stride) {
+      WSet w;
+      load(r0, w);
+      step(r0, w);
     }
   }
 }
