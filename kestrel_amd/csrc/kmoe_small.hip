@@ -262,19 +262,25 @@ __global__ void __launch_bounds__(256) k_small_down(SmallArgs a) {
 #pragma unroll
   for (int j = 0; j < NT; ++j) load_slice(s[j], a.xq, a.xd, a.xbs, cols, p0 + (j < n ? j : n - 1), sb, k);
 
-  for (int b0 = 0; b0 < nr; b0 += RU) {
+  // Two register sets: the next step's rows load while this step's are
+  // dotted (loads past the block's last row repeat it, never stored).
+  struct DSet {
     u32x4 hw[RU], aw[RU], bw[RU];
+  };
+  auto load = [&](int b0, DSet &d) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const int64_t r = r0 + (b0 + u < nr ? b0 + u : nr - 1);
       const uint8_t *row = W + r * row_bytes;
-      hw[u] = __builtin_nontemporal_load((const u32x4 *)(row + oh));
-      aw[u] = __builtin_nontemporal_load((const u32x4 *)(row + oa));
-      bw[u] = __builtin_nontemporal_load((const u32x4 *)(row + ob));
+      d.hw[u] = __builtin_nontemporal_load((const u32x4 *)(row + oh));
+      d.aw[u] = __builtin_nontemporal_load((const u32x4 *)(row + oa));
+      d.bw[u] = __builtin_nontemporal_load((const u32x4 *)(row + ob));
     }
+  };
+  auto step = [&](int b0, const DSet &d) {
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
-      const TaskW w = unpack_task(hw[u], aw[u], bw[u], k);
+      const TaskW w = unpack_task(d.hw[u], d.aw[u], d.bw[u], k);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if (j < n) {  // uniform: the expert's row count
@@ -291,6 +297,18 @@ __global__ void __launch_bounds__(256) k_small_down(SmallArgs a) {
         }
       }
     }
+  };
+  DSet d0, d1;
+  int b0 = 0;
+  load(0, d0);
+  while (b0 < nr) {
+    load(b0 + RU, d1);
+    step(b0, d0);
+    b0 += RU;
+    if (b0 >= nr) break;
+    load(b0 + RU, d0);
+    step(b0, d1);
+    b0 += RU;
   }
   __syncthreads();
   for (int q = threadIdx.x; q < nr * NT; q += 256) {
